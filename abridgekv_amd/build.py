@@ -1,0 +1,58 @@
+"""Build libabridgekv_amd.so in-tree with hipcc for gfx950.
+
+Usage: ``python -m abridgekv_amd.build`` (or ``__graft_entry__.build()``). Always recompiles.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libabridgekv_amd.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+DEVICE_SOURCES = ["decode_attn.hip", "kv_cache.hip", "prefill_attn.hip"]
+HOST_SOURCES = ["planner.cpp"]
+
+# -packed-fp32-ops off: hipcc would otherwise emit v_pk_{add,mul,fma}_f32 from scalar float code.
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]
+DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-munsafe-fp-atomics"]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(line for line in proc.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    objs = []
+    sources = [s for s in DEVICE_SOURCES if (CSRC / s).exists()]
+    for src in sources:
+        obj = objdir / (src + ".o")
+        _run([HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    for src in HOST_SOURCES:
+        obj = objdir / (src + ".o")
+        _run(["g++", *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

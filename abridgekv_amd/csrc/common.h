@@ -1,0 +1,42 @@
+// Shared device helpers for the abridged-KV kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace abkv {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Paged cache geometry of the served model (Qwen3-4B attention: 8 KV heads x 128, pages of 16 slots):
+// one page of one layer is [2 (K,V)][16 slots][8 heads][128 dims] bf16 = 64 KiB.
+constexpr int kPage = 16;
+constexpr int kHeadsKV = 8;
+constexpr int kHeadDim = 128;
+constexpr int kGroup = 4;                                  // query heads per KV head
+constexpr int kHeadsQ = kHeadsKV * kGroup;
+constexpr int kSlotElems = kHeadsKV * kHeadDim;            // 1024 elements = 2 KiB per slot per K or V
+constexpr int kHalfElems = kPage * kSlotElems;             // 16384 elements = 32 KiB (K half of a page)
+constexpr int kPageElems = 2 * kHalfElems;                 // 32768 elements = 64 KiB
+
+__device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8 a, const bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  // v_cvt_pk_bf16_f32: round-to-nearest-even of both halves
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace abkv

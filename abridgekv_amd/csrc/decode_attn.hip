@@ -1,0 +1,305 @@
+// Split-KV GQA decode attention over a per-group abridged paged KV cache (gfx950).
+//
+// Replaces the decode call the reference's vLLM overlay makes through the stock FlashInfer backend
+// (BatchDecodeWithPagedKVCache; metadata built in third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:
+// 1872-1887, 2184-2276) and the pure-torch consumer PackedKVSidecar._attend_decode_batched
+// (third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:564-616). Under physical per-layer quotas a
+// decode step needs no mask (gpu_model_runner.py:2042-2050): compaction already left each group's rows
+// contiguous as [prompt rows | q_l code rows per closed block | open block], so the kernel attends over physical
+// slots [0, seq_len) of the group's page table.
+//
+// Work decomposition: one workgroup of 8 waves per (sequence, split); wave w owns KV head w and its 4 query heads.
+// A split covers `split_pages` pages; the wave walks it 32 slots (two pages) at a time:
+//   S^T[32 slots x 16 cols] = K_tile . Q^T          two row tiles x 4 MFMA 16x16x32 (cols 0..3 = the 4 q heads)
+//   online softmax in fp32 (exp2 domain), per-head max shared across the 4 lane groups by two xor shuffles
+//   O^T[128 dims x 16 cols] += V^T . P^T            8 MFMA 16x16x32, V transposed in registers with v_perm
+// Operand layouts are chosen so that every global load is a 16-byte load straight into MFMA operand registers
+// (no LDS): for QK a lane loads 16 B of one slot's K row; for PV a lane loads 16 B (8 dims) of 8 slots' V rows and
+// an 8x8 bf16 transpose in registers produces the 8 V^T operands. The slot order inside the PV contraction is
+// picked so that the S^T accumulator registers of a lane are exactly its P^T operand (no cross-lane movement).
+//
+// Output: normalised bf16 out [B, 32, 128] and natural-log LSE [B, 32] directly when a sequence has one split;
+// otherwise un-normalised fp32 partials (o, m, l) per split and a merge kernel.
+#include "common.h"
+
+namespace abkv {
+
+struct DecodeArgs {
+  const __bf16* q;           // [B, 32, 128] (strides q_sb, q_sh in elements; dims contiguous)
+  long q_sb, q_sh;
+  const __bf16* kv;          // [num_pages, 2, 16, 8, 128]
+  const int32_t* block_table;  // [B, bt_stride]
+  long bt_stride;
+  const int32_t* seq_lens;   // [B]
+  int split_pages;           // pages per split (even)
+  int max_splits;
+  int max_pages;             // bound on pages per sequence (<= block-table width); longer sequences are clamped
+  int num_pages;             // pages in the cache; page ids are clamped into [0, num_pages)
+  float scale_log2;          // softmax scale * log2(e)
+  __bf16* out;               // [B, 32, 128] (strides o_sb, o_sh)
+  long o_sb, o_sh;
+  float* lse;                // [B, 32] or nullptr
+  float* part_o;             // [B, max_splits, 32, 128] fp32
+  float* part_ml;            // [B, max_splits, 32, 2] fp32 (m in log2 units, l)
+};
+
+__device__ __forceinline__ u32x4 ld16(const __bf16* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
+  const int b = blockIdx.y;
+  const int split = blockIdx.x;
+  const int kvh = threadIdx.x >> 6;           // wave index = KV head
+  const int lane = threadIdx.x & 63;
+  const int m16 = lane & 15;                  // MFMA row/col index of this lane
+  const int j = lane >> 4;                    // lane group (k-chunk index)
+
+  const int seq_len = min(a.seq_lens[b], a.max_pages * kPage);
+  const int n_pages = (seq_len + kPage - 1) / kPage;
+  const int pg_begin = split * a.split_pages;
+  if (pg_begin >= n_pages && !(split == 0 && seq_len <= 0)) return;
+  const int pg_end = min(n_pages, pg_begin + a.split_pages);
+  const int n_splits = max(1, (n_pages + a.split_pages - 1) / a.split_pages);
+  const int32_t* bt = a.block_table + (long)b * a.bt_stride;
+
+  // Q^T operand: lane supplies q[head m16][dims 8*(4i+j) .. +8] for MFMA i (zero for the 12 padding columns).
+  bf16x8 qop[4];
+  {
+    const __bf16* qh = a.q + (long)b * a.q_sb + (long)(kvh * kGroup + min(m16, kGroup - 1)) * a.q_sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 v = ld16(qh + 8 * (4 * i + j));
+      if (m16 >= kGroup) v = u32x4{0, 0, 0, 0};
+      qop[i] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  floatx4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;   // running max of this lane's head (log2 domain), identical across the lane group
+  float l_run = 0.f;         // partial row sum over this lane's slots
+
+  const __bf16* kv_h = a.kv + kvh * kHeadDim;
+  for (int pg = pg_begin; pg < pg_end; pg += 2) {
+    const int p0 = min(max(bt[pg], 0), a.num_pages - 1);
+    const int p1 = min(max(bt[min(pg + 1, n_pages - 1)], 0), a.num_pages - 1);
+    const __bf16* base0 = kv_h + (long)p0 * kPageElems;
+    const __bf16* base1 = kv_h + (long)p1 * kPageElems;
+
+    // K tiles: tile t row m16 = slot 16t + m16 of page p_t; lane loads dims 8*(4i+j)..+8 for MFMA i.
+    u32x4 kr[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kr[0][i] = ld16(base0 + m16 * kSlotElems + 8 * (4 * i + j));
+      kr[1][i] = ld16(base1 + m16 * kSlotElems + 8 * (4 * i + j));
+    }
+    // V rows: contraction index e<4 -> slot 4j+e of p0, e>=4 -> slot 4j+e-4 of p1; lane loads dims 8*m16..+8.
+    u32x4 vr[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vr[e] = ld16(base0 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
+      vr[4 + e] = ld16(base1 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
+    }
+
+    floatx4 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[t] = mfma16x16x32(__builtin_bit_cast(bf16x8, kr[t][i]), qop[i], s[t]);
+    }
+    // s[t][r] = score of slot pg*16 + 16t + 4j + r for head m16.
+    const bool tail = (pg + 2) * kPage > seq_len;
+    float sv[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = s[t][r] * a.scale_log2;
+        if (tail) {
+          const int slot = pg * kPage + 16 * t + 4 * j + r;
+          x = slot < seq_len ? x : -INFINITY;
+        }
+        sv[4 * t + r] = x;
+      }
+    if (tail) {
+      // Rows past seq_len may hold stale bytes: zero their V contribution (0 * NaN would poison the MFMA).
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int slot = pg * kPage + (e < 4 ? 0 : 16) + 4 * j + (e & 3);
+        if (slot >= seq_len) vr[e] = u32x4{0, 0, 0, 0};
+      }
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+    mx = fmaxf(mx, xor_shfl(mx, 16));
+    mx = fmaxf(mx, xor_shfl(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sv[e] = fast_exp2(sv[e] - m_new);
+      psum += sv[e];
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] *= alpha;
+
+    u32x4 pw;
+    pw[0] = pack_bf16x2(sv[0], sv[1]);
+    pw[1] = pack_bf16x2(sv[2], sv[3]);
+    pw[2] = pack_bf16x2(sv[4], sv[5]);
+    pw[3] = pack_bf16x2(sv[6], sv[7]);
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+
+    // 8x8 transpose: vt[i] dword k = (V[slot e=2k][dim 8*m16+i], V[slot e=2k+1][dim 8*m16+i]).
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lo[k] = __builtin_amdgcn_perm(vr[2 * k + 1][c], vr[2 * k][c], 0x05040100u);
+        hi[k] = __builtin_amdgcn_perm(vr[2 * k + 1][c], vr[2 * k][c], 0x07060302u);
+      }
+      o[2 * c] = mfma16x16x32(__builtin_bit_cast(bf16x8, lo), pop, o[2 * c]);
+      o[2 * c + 1] = mfma16x16x32(__builtin_bit_cast(bf16x8, hi), pop, o[2 * c + 1]);
+    }
+  }
+
+  // o[i][r] = un-normalised out[head m16][dim 32j + 8r + i]; l_run partial over this lane's slots.
+  float l_tot = l_run + xor_shfl(l_run, 16);
+  l_tot += xor_shfl(l_tot, 32);
+  if (m16 >= kGroup) return;
+  const int head = kvh * kGroup + m16;
+  if (n_splits == 1) {
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + 32 * j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      u32x4 w;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w[c] = pack_bf16x2(o[2 * c][r] * inv, o[2 * c + 1][r] * inv);
+      *reinterpret_cast<u32x4*>(oh + 8 * r) = w;
+    }
+    if (a.lse != nullptr && j == 0)
+      a.lse[(long)b * kHeadsQ + head] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+  } else {
+    float* po = a.part_o + (((long)b * a.max_splits + split) * kHeadsQ + head) * kHeadDim + 32 * j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatx4 w0 = {o[0][r], o[1][r], o[2][r], o[3][r]};
+      floatx4 w1 = {o[4][r], o[5][r], o[6][r], o[7][r]};
+      *reinterpret_cast<floatx4*>(po + 8 * r) = w0;
+      *reinterpret_cast<floatx4*>(po + 8 * r + 4) = w1;
+    }
+    if (j == 0) {
+      float* pml = a.part_ml + (((long)b * a.max_splits + split) * kHeadsQ + head) * 2;
+      pml[0] = m_run;
+      pml[1] = l_tot;
+    }
+  }
+}
+
+// Merge the split partials of every sequence with more than one split: one workgroup per sequence,
+// thread t handles head t/8, dims 16*(t%8) .. +16.
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int seq_len = min(a.seq_lens[b], a.max_pages * kPage);
+  const int n_pages = (seq_len + kPage - 1) / kPage;
+  const int n_splits = (n_pages + a.split_pages - 1) / a.split_pages;
+  if (n_splits <= 1) return;
+  const int head = threadIdx.x >> 3;
+  const int d0 = (threadIdx.x & 7) * 16;
+  const float* pml = a.part_ml + ((long)b * a.max_splits * kHeadsQ + head) * 2;
+  float M = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[(long)s * kHeadsQ * 2]);
+  float L = 0.f;
+  float acc[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  for (int s = 0; s < n_splits; ++s) {
+    const float w = fast_exp2(pml[(long)s * kHeadsQ * 2] - M);
+    L += w * pml[(long)s * kHeadsQ * 2 + 1];
+    const float* po = a.part_o + (((long)b * a.max_splits + s) * kHeadsQ + head) * kHeadDim + d0;
+#pragma unroll
+    for (int d = 0; d < 16; d += 4) {
+      floatx4 v = *reinterpret_cast<const floatx4*>(po + d);
+      acc[d] += w * v[0];
+      acc[d + 1] += w * v[1];
+      acc[d + 2] += w * v[2];
+      acc[d + 3] += w * v[3];
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + d0;
+#pragma unroll
+  for (int d = 0; d < 16; d += 8) {
+    u32x4 w;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = pack_bf16x2(acc[d + 2 * c] * inv, acc[d + 2 * c + 1] * inv);
+    *reinterpret_cast<u32x4*>(oh + d) = w;
+  }
+  if (a.lse != nullptr && (threadIdx.x & 7) == 0)
+    a.lse[(long)b * kHeadsQ + head] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : -INFINITY;
+}
+
+}  // namespace abkv
+
+extern "C" {
+
+// Workspace bytes needed by abkv_decode_attn for `num_seqs` sequences and `max_splits` splits per sequence.
+size_t abkv_decode_workspace_size(int num_seqs, int max_splits) {
+  const size_t per = (size_t)abkv::kHeadsQ * (abkv::kHeadDim + 2) * sizeof(float);
+  return (size_t)num_seqs * (size_t)max_splits * per;
+}
+
+int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
+                     const void* kv_cache, int num_pages, const int32_t* block_table, long block_table_stride,
+                     const int32_t* seq_lens, int num_seqs, int max_pages_per_seq, int split_pages,
+                     float scale, void* out, long out_stride_seq, long out_stride_head, float* lse,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  using namespace abkv;
+  if (num_seqs <= 0) return 0;
+  if (split_pages <= 0 || (split_pages & 1) || max_pages_per_seq <= 0 || num_pages <= 0 ||
+      block_table_stride < max_pages_per_seq)
+    return (int)hipErrorInvalidValue;
+  if (q == nullptr || kv_cache == nullptr || block_table == nullptr || seq_lens == nullptr || out == nullptr)
+    return (int)hipErrorInvalidValue;
+  const int max_splits = (max_pages_per_seq + split_pages - 1) / split_pages;
+  if (max_splits > 1 && (workspace == nullptr || workspace_bytes < abkv_decode_workspace_size(num_seqs, max_splits)))
+    return (int)hipErrorInvalidValue;
+  DecodeArgs a;
+  a.q = static_cast<const __bf16*>(q);
+  a.q_sb = q_stride_seq;
+  a.q_sh = q_stride_head;
+  a.kv = static_cast<const __bf16*>(kv_cache);
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.seq_lens = seq_lens;
+  a.split_pages = split_pages;
+  a.max_splits = max_splits;
+  a.max_pages = max_pages_per_seq;
+  a.num_pages = num_pages;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = static_cast<__bf16*>(out);
+  a.o_sb = out_stride_seq;
+  a.o_sh = out_stride_head;
+  a.lse = lse;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + (size_t)num_seqs * max_splits * kHeadsQ * kHeadDim;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(max_splits, num_seqs), dim3(512), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  if (max_splits > 1) {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs), dim3(256), 0, stream, a);
+    err = hipGetLastError();
+  }
+  return (int)err;
+}
+
+}  // extern "C"

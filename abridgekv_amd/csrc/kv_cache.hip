@@ -1,0 +1,240 @@
+// KV-cache row movement for block-boundary compaction, KV append and slot mapping (gfx950).
+//
+// Compaction executor: replaces GPUModelRunner._execute_kv_copy_operations / _execute_kv_copy_group
+// (third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1147-1224), which applies one ordered batch of
+// (src_block, src_off, dst_block, dst_off) ops per KV-cache group with gather-then-scatter semantics to every layer
+// tensor of the group. Here a launch takes a list of op *segments* (one per request batch) and applies each segment
+// to up to kMaxLayers layer tensors; grid = (segment, layer), 256 threads.
+//
+// Exactness without a staging buffer: a workgroup walks its segment in op order, kChunk ops at a time, loading
+// every source row of the chunk into registers, then (after a barrier) storing every destination row, then a
+// barrier. This equals gather-then-scatter whenever no op of the segment reads a slot that an EARLIER op of the same
+// segment writes -- true for compaction ops, which are emitted in increasing source order with dst < src
+// (single_type_kv_cache_manager.py:378-381). Segments must touch disjoint pages (different requests' pages are
+// disjoint; one request contributes one segment per batch). For op lists that violate the ordering precondition the
+// two-phase gather/scatter entry points below stage rows through a workspace instead.
+//
+// KV append: replaces the stock vLLM compiled op reshape_and_cache(_flash) that writes each new token's K and V
+// rows at slot_mapping[t] (slots from block_table.py:186-197); slot < 0 is skipped (padding).
+#include "common.h"
+
+namespace abkv {
+
+constexpr int kMaxLayers = 16;
+constexpr int kChunk = 16;        // ops per register chunk: 16 rows x 4 KiB = 64 KiB in flight per workgroup
+
+struct LayerPtrs {
+  char* p[kMaxLayers];
+};
+
+struct MoveArgs {
+  LayerPtrs layers;
+  const int32_t* ops;          // [n_ops, 4] (src_block, src_off, dst_block, dst_off)
+  const int32_t* seg_offsets;  // [n_seg + 1]
+  long page_bytes;             // bytes of one page of one layer (2 * block_size * slot_bytes)
+  long half_bytes;             // offset of the V half inside a page
+  int slot_bytes;              // bytes of one slot of K (or V), multiple of 16
+  int num_pages;               // pages per layer cache: ops outside [0, num_pages) x [0, block_size) are skipped
+  int block_size;
+};
+
+__device__ __forceinline__ bool op_ok(const int32_t* op, int num_pages, int block_size) {
+  return (unsigned)op[0] < (unsigned)num_pages && (unsigned)op[2] < (unsigned)num_pages &&
+         (unsigned)op[1] < (unsigned)block_size && (unsigned)op[3] < (unsigned)block_size;
+}
+
+// One "row" of an op = slot_bytes of K plus slot_bytes of V. 256 threads x 16 B cover 4096 B = one row of the
+// served geometry (2 KiB K + 2 KiB V); other geometries loop.
+__global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
+  const int seg = blockIdx.x;
+  char* base = a.layers.p[blockIdx.y];
+  const int s0 = a.seg_offsets[seg], s1 = a.seg_offsets[seg + 1];
+  const int row_vec = (2 * a.slot_bytes) / 16;          // 16-byte vectors per row
+  const int tid = threadIdx.x;
+  for (int c0 = s0; c0 < s1; c0 += kChunk) {
+    const int n = min(kChunk, s1 - c0);
+    for (int v0 = 0; v0 < row_vec; v0 += 256) {
+      const int v = v0 + tid;
+      const bool active = v < row_vec;
+      const int half = v >= row_vec / 2;                   // 0: K, 1: V
+      const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
+      u32x4 buf[kChunk];
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k) {
+        if (k < n && active) {
+          const int32_t* op = a.ops + 4L * (c0 + k);
+          if (!op_ok(op, a.num_pages, a.block_size)) continue;
+          const char* src = base + (long)op[0] * a.page_bytes + (long)op[1] * a.slot_bytes + inner;
+          buf[k] = *reinterpret_cast<const u32x4*>(src);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k) {
+        if (k < n && active) {
+          const int32_t* op = a.ops + 4L * (c0 + k);
+          if (!op_ok(op, a.num_pages, a.block_size)) continue;
+          char* dst = base + (long)op[2] * a.page_bytes + (long)op[3] * a.slot_bytes + inner;
+          *reinterpret_cast<u32x4*>(dst) = buf[k];
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Two-phase form for arbitrary op lists: gather every source row into `stage` [n_layers, n_ops, row], then scatter.
+__global__ __launch_bounds__(256) void kv_gather_kernel(MoveArgs a, char* stage, int n_ops) {
+  const int op_i = blockIdx.x;
+  const int layer = blockIdx.y;
+  const char* base = a.layers.p[layer];
+  const int row_vec = (2 * a.slot_bytes) / 16;
+  const int32_t* op = a.ops + 4L * op_i;
+  if (!op_ok(op, a.num_pages, a.block_size)) return;
+  char* out = stage + ((long)layer * n_ops + op_i) * (2L * a.slot_bytes);
+  for (int v = threadIdx.x; v < row_vec; v += 256) {
+    const int half = v >= row_vec / 2;
+    const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
+    *reinterpret_cast<u32x4*>(out + 16L * v) =
+        *reinterpret_cast<const u32x4*>(base + (long)op[0] * a.page_bytes + (long)op[1] * a.slot_bytes + inner);
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_scatter_kernel(MoveArgs a, const char* stage, int n_ops) {
+  const int op_i = blockIdx.x;
+  const int layer = blockIdx.y;
+  char* base = a.layers.p[layer];
+  const int row_vec = (2 * a.slot_bytes) / 16;
+  const int32_t* op = a.ops + 4L * op_i;
+  if (!op_ok(op, a.num_pages, a.block_size)) return;
+  const char* in = stage + ((long)layer * n_ops + op_i) * (2L * a.slot_bytes);
+  for (int v = threadIdx.x; v < row_vec; v += 256) {
+    const int half = v >= row_vec / 2;
+    const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
+    *reinterpret_cast<u32x4*>(base + (long)op[2] * a.page_bytes + (long)op[3] * a.slot_bytes + inner) =
+        *reinterpret_cast<const u32x4*>(in + 16L * v);
+  }
+}
+
+// KV append: one workgroup of 256 threads per token; thread moves 16 B of K or V.
+__global__ __launch_bounds__(256) void kv_append_kernel(const char* key, long k_stride, const char* value,
+                                                       long v_stride, const int64_t* slot_mapping, char* cache,
+                                                       long page_bytes, long half_bytes, int slot_bytes,
+                                                       int block_size, long num_pages) {
+  const int t = blockIdx.x;
+  const long slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_pages * block_size) return;
+  const long page = slot / block_size, off = slot % block_size;
+  const int vecs = slot_bytes / 16;
+  for (int v = threadIdx.x; v < 2 * vecs; v += 256) {
+    const int half = v >= vecs;
+    const int w = v - half * vecs;
+    const char* src = (half ? value + (long)t * v_stride : key + (long)t * k_stride) + 16L * w;
+    char* dst = cache + page * page_bytes + (long)half * half_bytes + off * slot_bytes + 16L * w;
+    *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+  }
+}
+
+// slot_mapping[t] = table[req[t]][pos[t] / block_size] * block_size + pos[t] % block_size; -1 for a negative
+// position or one past the table (pos >= width * block_size) or a request index outside [0, num_reqs).
+__global__ void slot_mapping_kernel(const int32_t* req_idx, const int64_t* positions, const int32_t* block_table,
+                                    int num_reqs, long bt_stride, int block_size, int64_t* slots, int n) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const long pos = positions[t];
+  const int r = req_idx[t];
+  if (pos < 0 || pos >= bt_stride * block_size || r < 0 || r >= num_reqs) {
+    slots[t] = -1;
+    return;
+  }
+  const long blk = block_table[(long)req_idx[t] * bt_stride + pos / block_size];
+  slots[t] = blk * block_size + pos % block_size;
+}
+
+static bool fill_layers(LayerPtrs& lp, void* const* layer_caches, int n_layers) {
+  if (n_layers <= 0 || n_layers > kMaxLayers) return false;
+  for (int i = 0; i < kMaxLayers; ++i) lp.p[i] = i < n_layers ? static_cast<char*>(layer_caches[i]) : nullptr;
+  for (int i = 0; i < n_layers; ++i)
+    if (lp.p[i] == nullptr) return false;
+  return true;
+}
+
+}  // namespace abkv
+
+extern "C" {
+
+int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                          long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments, hipStream_t stream) {
+  using namespace abkv;
+  if (n_segments <= 0) return 0;
+  if (ops == nullptr || seg_offsets == nullptr || slot_bytes <= 0 || slot_bytes % 16 != 0)
+    return (int)hipErrorInvalidValue;
+  MoveArgs a;
+  if (!fill_layers(a.layers, layer_caches, n_layers)) return (int)hipErrorInvalidValue;
+  a.ops = ops;
+  a.seg_offsets = seg_offsets;
+  a.page_bytes = page_bytes;
+  a.half_bytes = half_bytes;
+  a.slot_bytes = slot_bytes;
+  a.num_pages = num_pages;
+  a.block_size = block_size;
+  hipLaunchKernelGGL(kv_move_kernel, dim3(n_segments, n_layers), dim3(256), 0, stream, a);
+  return (int)hipGetLastError();
+}
+
+size_t abkv_kv_stage_bytes(int n_layers, int n_ops, int slot_bytes) {
+  return (size_t)n_layers * (size_t)n_ops * 2u * (size_t)slot_bytes;
+}
+
+int abkv_kv_copy_staged(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                        long half_bytes, int slot_bytes, const int32_t* ops, int n_ops, void* stage, size_t stage_bytes, hipStream_t stream) {
+  using namespace abkv;
+  if (n_ops <= 0) return 0;
+  if (ops == nullptr || slot_bytes <= 0 || slot_bytes % 16 != 0 ||
+      stage == nullptr || stage_bytes < abkv_kv_stage_bytes(n_layers, n_ops, slot_bytes))
+    return (int)hipErrorInvalidValue;
+  MoveArgs a;
+  if (!fill_layers(a.layers, layer_caches, n_layers)) return (int)hipErrorInvalidValue;
+  a.ops = ops;
+  a.seg_offsets = nullptr;
+  a.page_bytes = page_bytes;
+  a.half_bytes = half_bytes;
+  a.slot_bytes = slot_bytes;
+  a.num_pages = num_pages;
+  a.block_size = block_size;
+  hipLaunchKernelGGL(kv_gather_kernel, dim3(n_ops, n_layers), dim3(256), 0, stream, a, static_cast<char*>(stage),
+                     n_ops);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  hipLaunchKernelGGL(kv_scatter_kernel, dim3(n_ops, n_layers), dim3(256), 0, stream, a,
+                     static_cast<const char*>(stage), n_ops);
+  return (int)hipGetLastError();
+}
+
+int abkv_kv_append(const void* key, long key_stride, const void* value, long value_stride,
+                   const int64_t* slot_mapping, int num_tokens, void* kv_cache, int num_pages, long page_bytes,
+                   long half_bytes, int slot_bytes, int block_size, hipStream_t stream) {
+  using namespace abkv;
+  if (num_tokens <= 0) return 0;
+  if (key == nullptr || value == nullptr || slot_mapping == nullptr || kv_cache == nullptr || slot_bytes % 16 != 0 ||
+      block_size <= 0)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(num_tokens), dim3(256), 0, stream, static_cast<const char*>(key),
+                     key_stride, static_cast<const char*>(value), value_stride, slot_mapping,
+                     static_cast<char*>(kv_cache), page_bytes, half_bytes, slot_bytes, block_size, (long)num_pages);
+  return (int)hipGetLastError();
+}
+
+int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_tokens, const int32_t* block_table,
+                      int num_reqs, long block_table_stride, int block_size, int64_t* slot_mapping,
+                      hipStream_t stream) {
+  if (num_tokens <= 0) return 0;
+  if (req_idx == nullptr || positions == nullptr || block_table == nullptr || slot_mapping == nullptr ||
+      block_size <= 0)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(abkv::slot_mapping_kernel, dim3((num_tokens + 255) / 256), dim3(256), 0, stream, req_idx,
+                     positions, block_table, num_reqs, block_table_stride, block_size, slot_mapping, num_tokens);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,629 @@
+// Host-side compaction planner: page pool, per-group page lists, compacted-span maps and span removal.
+//
+// Bit-exact with the reference's scheduler/KV-manager bookkeeping (vLLM overlay):
+//   free-block FIFO ........ third_party/vllm_overlay/vllm/v1/core/kv_cache_utils.py:157-345
+//   page pool .............. third_party/vllm_overlay/vllm/v1/core/block_pool.py:160-176, 295-325, 385-399, 488-550
+//   per-group page lists ... third_party/vllm_overlay/vllm/v1/core/single_type_kv_cache_manager.py:66-145, 173-188,
+//                            358-452
+//   slot allocation ........ third_party/vllm_overlay/vllm/v1/core/kv_cache_manager.py:206-340 (no prefix caching,
+//                            no lookahead, no encoder tokens: CompressLM serving disables them)
+//   compacted spans ........ third_party/vllm_overlay/vllm/v1/compacted_spans.py:8-68, v1/request.py:263-321
+//   span removal ........... third_party/vllm_overlay/vllm/v1/core/sched/scheduler.py:2043-2204
+// Pure host code: no HIP call is made from this file.
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <deque>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+namespace abkv {
+
+struct SpanIndex {
+  std::vector<std::pair<int64_t, int64_t>> spans;
+  std::vector<int64_t> starts, cumulative, gap_physical, gap_logical;
+  int64_t total = 0;
+
+  void rebuild() {
+    starts.clear();
+    cumulative.clear();
+    gap_physical.assign(1, 0);
+    gap_logical.assign(1, 0);
+    total = 0;
+    for (auto& s : spans) {
+      starts.push_back(s.first);
+      total += s.second - s.first;
+      cumulative.push_back(total);
+      gap_physical.push_back(s.second - total);
+      gap_logical.push_back(s.second);
+    }
+  }
+  // bisect_right(starts, pos) - 1
+  long idx_le(int64_t pos) const {
+    return (long)(std::upper_bound(starts.begin(), starts.end(), pos) - starts.begin()) - 1;
+  }
+  bool is_active(int64_t pos) const {
+    if (starts.empty()) return true;
+    long i = idx_le(pos);
+    if (i < 0) return true;
+    return pos >= spans[i].second;
+  }
+  int64_t l2p(int64_t pos) const {
+    if (starts.empty()) return pos;
+    long i = idx_le(pos);
+    if (i < 0) return pos;
+    if (pos >= spans[i].second) return pos - cumulative[i];
+    int64_t prev = i > 0 ? cumulative[i - 1] : 0;
+    return pos - prev - (pos - starts[i]);
+  }
+  int64_t p2l(int64_t phys) const {
+    long i = (long)(std::upper_bound(gap_physical.begin(), gap_physical.end(), phys) - gap_physical.begin()) - 1;
+    return gap_logical[i] + (phys - gap_physical[i]);
+  }
+  // spans = merge(spans + [span])
+  void add_merged(std::pair<int64_t, int64_t> span) {
+    spans.push_back(span);
+    std::sort(spans.begin(), spans.end());
+    std::vector<std::pair<int64_t, int64_t>> merged;
+    for (auto& s : spans) {
+      if (!merged.empty() && s.first <= merged.back().second)
+        merged.back().second = std::max(merged.back().second, s.second);
+      else
+        merged.push_back(s);
+    }
+    spans.swap(merged);
+    rebuild();
+  }
+};
+
+struct Op {
+  int32_t src_block, src_off, dst_block, dst_off;
+};
+
+// One span removal applied to one group of one request during the current step (physical coordinates of the
+// layout the removal saw).
+struct Removal {
+  int64_t start, end, active;
+};
+
+struct GroupStep {
+  std::vector<std::vector<Op>> batches;   // reference-format ordered op batches
+  std::vector<int32_t> blocks_before;     // page list before the step's first removal
+  std::vector<Removal> removals;
+};
+
+struct Request {
+  int64_t num_computed = 0;
+  std::vector<SpanIndex> spans;           // per group
+  std::vector<std::vector<int32_t>> blocks;  // per group
+  std::vector<GroupStep> step;            // per group, cleared by take_step_outputs
+  bool has_trunc = false;
+  std::vector<int32_t> trunc;
+};
+
+struct Planner {
+  int num_blocks = 0, num_groups = 0, block_size = 16;
+  int64_t max_model_len = 0;
+  int32_t null_block = 0;
+  std::vector<int32_t> ref_cnt;
+  std::deque<int32_t> free_q;
+  std::unordered_map<int64_t, Request> reqs;
+  std::vector<int64_t> pending_order;     // rids with pending ops, first-insertion order
+  std::vector<int64_t> trunc_order;       // rids with a truncation record, first-insertion order
+  std::string last_error;
+
+  int64_t cdiv(int64_t a, int64_t b) const { return (a + b - 1) / b; }
+
+  bool get_new_blocks(int64_t n, std::vector<int32_t>& out) {
+    if (n > (int64_t)free_q.size()) {
+      last_error = "Cannot get " + std::to_string(n) + " free blocks from the pool";
+      return false;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+      int32_t b = free_q.front();
+      free_q.pop_front();
+      ref_cnt[b] += 1;
+      out.push_back(b);
+    }
+    return true;
+  }
+
+  void free_blocks(const std::vector<int32_t>& ordered) {
+    for (int32_t b : ordered) ref_cnt[b] -= 1;
+    for (int32_t b : ordered)
+      if (ref_cnt[b] == 0 && b != null_block) free_q.push_back(b);
+  }
+};
+
+static void note_order(std::vector<int64_t>& order, int64_t rid) {
+  if (std::find(order.begin(), order.end(), rid) == order.end()) order.push_back(rid);
+}
+
+}  // namespace abkv
+
+using abkv::Planner;
+using abkv::Request;
+
+extern "C" {
+
+// Error codes of the planner entry points.
+enum {
+  ABKV_OK = 0,
+  ABKV_ERR_ARG = -1,          // bad argument (null handle, out-of-range group, ...)
+  ABKV_ERR_NO_REQUEST = -2,   // unknown request id
+  ABKV_ERR_SPAN = -3,         // span rejected (the reference's SpanRemovalResult(success=False))
+  ABKV_ERR_POOL = -4,         // page pool exhausted inside an allocation that passed the total check
+  ABKV_ERR_CAPACITY = -5,     // output buffer too small
+};
+
+void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const int32_t* free_order,
+                          int64_t max_model_len) {
+  if (num_blocks < 2 || num_groups < 1 || block_size < 1) return nullptr;
+  Planner* p = new Planner();
+  p->num_blocks = num_blocks;
+  p->num_groups = num_groups;
+  p->block_size = block_size;
+  p->max_model_len = max_model_len > 0 ? max_model_len : ((int64_t)1 << 40);
+  p->ref_cnt.assign(num_blocks, 0);
+  p->null_block = 0;  // the queue starts in id order and its head (page 0) becomes the null block
+  if (free_order != nullptr) {
+    std::vector<char> seen(num_blocks, 0);
+    for (int i = 0; i < num_blocks - 1; ++i) {
+      int32_t b = free_order[i];
+      if (b < 1 || b >= num_blocks || seen[b]) {
+        delete p;
+        return nullptr;
+      }
+      seen[b] = 1;
+      p->free_q.push_back(b);
+    }
+  } else {
+    for (int32_t b = 1; b < num_blocks; ++b) p->free_q.push_back(b);
+  }
+  return p;
+}
+
+void abkv_planner_destroy(void* h) { delete static_cast<Planner*>(h); }
+
+const char* abkv_planner_last_error(void* h) { return h ? static_cast<Planner*>(h)->last_error.c_str() : ""; }
+
+int abkv_planner_add_request(void* h, int64_t rid) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  Request& r = p->reqs[rid];
+  r.num_computed = 0;
+  r.spans.assign(p->num_groups, abkv::SpanIndex());
+  for (auto& s : r.spans) s.rebuild();
+  r.blocks.assign(p->num_groups, {});
+  r.step.assign(p->num_groups, {});
+  r.has_trunc = false;
+  return ABKV_OK;
+}
+
+static Request* find_req(Planner* p, int64_t rid) {
+  auto it = p->reqs.find(rid);
+  return it == p->reqs.end() ? nullptr : &it->second;
+}
+
+// coordinator.free: every group frees its pages in reverse order (single_type_kv_cache_manager.py:173-188).
+int abkv_planner_free_request(void* h, int64_t rid) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  if (!r) return ABKV_ERR_NO_REQUEST;
+  for (int g = 0; g < p->num_groups; ++g) {
+    std::vector<int32_t> rev(r->blocks[g].rbegin(), r->blocks[g].rend());
+    p->free_blocks(rev);
+  }
+  p->reqs.erase(rid);
+  p->pending_order.erase(std::remove(p->pending_order.begin(), p->pending_order.end(), rid), p->pending_order.end());
+  p->trunc_order.erase(std::remove(p->trunc_order.begin(), p->trunc_order.end(), rid), p->trunc_order.end());
+  return ABKV_OK;
+}
+
+int abkv_planner_set_num_computed(void* h, int64_t rid, int64_t n) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  if (!r) return ABKV_ERR_NO_REQUEST;
+  r->num_computed = n;
+  return ABKV_OK;
+}
+
+int64_t abkv_planner_get_num_computed(void* h, int64_t rid) {
+  Planner* p = static_cast<Planner*>(h);
+  Request* r = p ? find_req(p, rid) : nullptr;
+  return r ? r->num_computed : -1;
+}
+
+// Returns 1 when pages were (or did not need to be) allocated, 0 when the pool cannot cover the request (the
+// reference returns None and allocates nothing), negative on error.
+int abkv_planner_allocate_slots(void* h, int64_t rid, int64_t num_new_tokens) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  if (!r) return ABKV_ERR_NO_REQUEST;
+  if (num_new_tokens == 0) {
+    p->last_error = "num_new_tokens must be greater than 0";
+    return ABKV_ERR_ARG;
+  }
+  const int64_t need = std::min(r->num_computed + num_new_tokens, p->max_model_len);
+  int64_t total = 0;
+  for (int g = 0; g < p->num_groups; ++g)
+    total += p->cdiv(need - r->spans[g].total, p->block_size) - (int64_t)r->blocks[g].size();
+  if (total > (int64_t)p->free_q.size()) return 0;
+  for (int g = 0; g < p->num_groups; ++g) {
+    const int64_t num_new = p->cdiv(need - r->spans[g].total, p->block_size) - (int64_t)r->blocks[g].size();
+    if (num_new <= 0) continue;
+    if (!p->get_new_blocks(num_new, r->blocks[g])) return ABKV_ERR_POOL;
+  }
+  return 1;
+}
+
+// Scheduler.mask_token_span. groups == nullptr (or n_groups < 0) targets every group. Returns ABKV_OK on success
+// (tokens_removed / blocks_freed filled), ABKV_ERR_SPAN with last_error holding the reference's error message.
+int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t end, const int32_t* groups,
+                                 int n_groups, int64_t* tokens_removed, int64_t* blocks_freed) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  if (tokens_removed) *tokens_removed = 0;
+  if (blocks_freed) *blocks_freed = 0;
+  Request* r = find_req(p, rid);
+  if (!r) {
+    p->last_error = "Request " + std::to_string(rid) + " not found";
+    return ABKV_ERR_SPAN;
+  }
+  if (start < 0 || end <= start) {
+    p->last_error = "Invalid span: must have 0 <= start < end";
+    return ABKV_ERR_SPAN;
+  }
+  if (end > r->num_computed) {
+    p->last_error = "end_position (" + std::to_string(end) + ") exceeds computed tokens (" +
+                    std::to_string(r->num_computed) + ")";
+    return ABKV_ERR_SPAN;
+  }
+  const int64_t masked = end - start;
+  const int G = p->num_groups;
+  std::vector<int> targets;
+  if (groups == nullptr || n_groups < 0) {
+    for (int g = 0; g < G; ++g) targets.push_back(g);
+  } else {
+    for (int i = 0; i < n_groups; ++i) targets.push_back(groups[i]);
+    std::sort(targets.begin(), targets.end());
+    targets.erase(std::unique(targets.begin(), targets.end()), targets.end());
+  }
+  struct Plan {
+    int g;
+    int64_t ps, pe, active;
+  };
+  std::vector<Plan> plans;
+  for (int g : targets) {
+    if (g < 0 || g >= G) {
+      p->last_error = "KV cache group " + std::to_string(g) + " out of range";
+      return ABKV_ERR_SPAN;
+    }
+    for (auto& s : r->spans[g].spans)
+      if (start < s.second && end > s.first) {
+        p->last_error = "Cannot compact an already-removed token span (group " + std::to_string(g) + ")";
+        return ABKV_ERR_SPAN;
+      }
+    const int64_t ps = r->spans[g].l2p(start), pe = r->spans[g].l2p(end);
+    if (pe - ps != masked) {
+      p->last_error = "Logical span does not map to one active physical span (group " + std::to_string(g) + ")";
+      return ABKV_ERR_SPAN;
+    }
+    const int64_t active = r->num_computed - r->spans[g].total;
+    if (active == masked) {
+      p->last_error = "Cannot compact: all tokens would be removed";
+      return ABKV_ERR_SPAN;
+    }
+    plans.push_back({g, ps, pe, active});
+  }
+  int64_t total_freed = 0;
+  const int bs = p->block_size;
+  for (auto& pl : plans) {
+    std::vector<int32_t>& blocks = r->blocks[pl.g];
+    abkv::GroupStep& st = r->step[pl.g];
+    if (!(0 <= pl.ps && pl.ps < pl.pe && pl.pe <= pl.active)) {
+      p->last_error = "Invalid physical compaction span";
+      return ABKV_ERR_SPAN;
+    }
+    if (!blocks.empty()) {
+      if (st.removals.empty()) st.blocks_before = blocks;
+      st.removals.push_back({pl.ps, pl.pe, pl.active});
+      const int64_t removed = pl.pe - pl.ps;
+      std::vector<abkv::Op> ops;
+      ops.reserve((size_t)(pl.active - pl.pe));
+      for (int64_t src = pl.pe; src < pl.active; ++src) {
+        const int64_t dst = src - removed;
+        ops.push_back({blocks[src / bs], (int32_t)(src % bs), blocks[dst / bs], (int32_t)(dst % bs)});
+      }
+      // _truncate_compacted_blocks
+      const int64_t needed = (pl.active - removed + bs - 1) / bs;
+      std::vector<int32_t> to_free;
+      for (int64_t i = needed; i < (int64_t)blocks.size(); ++i) {
+        if (blocks[i] != p->null_block) {
+          to_free.push_back(blocks[i]);
+          blocks[i] = p->null_block;
+          ++total_freed;
+        }
+      }
+      if ((int64_t)blocks.size() > needed) blocks.resize((size_t)needed);
+      if (!to_free.empty()) {
+        std::reverse(to_free.begin(), to_free.end());
+        p->free_blocks(to_free);
+      }
+      if (!ops.empty()) {
+        st.batches.push_back(std::move(ops));
+        abkv::note_order(p->pending_order, rid);
+      }
+    }
+    r->spans[pl.g].add_merged({start, end});
+  }
+  r->has_trunc = true;
+  r->trunc.resize(G);
+  for (int g = 0; g < G; ++g) r->trunc[g] = (int32_t)r->blocks[g].size();
+  abkv::note_order(p->trunc_order, rid);
+  if (tokens_removed) *tokens_removed = masked;
+  if (blocks_freed) *blocks_freed = total_freed;
+  return ABKV_OK;
+}
+
+// Sizes of the pending step outputs: reference-format op rows, truncation rows and fused move rows.
+int abkv_planner_pending_sizes(void* h, int64_t* n_op_rows, int64_t* n_trunc_rows, int64_t* n_fused_rows) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  int64_t ops = 0, fused = 0;
+  for (int64_t rid : p->pending_order) {
+    Request* r = find_req(p, rid);
+    for (auto& st : r->step)
+      for (auto& b : st.batches) ops += (int64_t)b.size();
+  }
+  for (auto& kv : p->reqs)
+    for (auto& st : kv.second.step)
+      if (!st.removals.empty()) {
+        const int64_t lo = std::min_element(st.removals.begin(), st.removals.end(),
+                                            [](const abkv::Removal& a, const abkv::Removal& b) {
+                                              return a.start < b.start;
+                                            })->start;
+        fused += st.removals.front().active - lo;   // upper bound
+      }
+  if (n_op_rows) *n_op_rows = ops;
+  if (n_trunc_rows) *n_trunc_rows = (int64_t)p->trunc_order.size();
+  if (n_fused_rows) *n_fused_rows = fused;
+  return ABKV_OK;
+}
+
+// Emit and clear the step outputs.
+//  op_rows    [n_op_rows, 7]  = (rid, group, batch, src_block, src_off, dst_block, dst_off), in the order the
+//             reference's SchedulerOutput.kv_copy_operations dict iterates (request first-insertion order, group,
+//             batch, op).
+//  trunc_rows [n_trunc_rows, 1 + G] = (rid, pages kept per group), pending_block_table_truncations order.
+//  fused_rows [n_fused, 6] = (rid, group, src_block, src_off, dst_block, dst_off): all of a step's removals of one
+//             (request, group) composed into one monotone move list (increasing source, dst < src), restricted to
+//             rows that survive the step; rows the reference moves and then truncates are not moved.
+// Any output pointer may be null to skip it. Returns ABKV_ERR_CAPACITY if a capacity is too small (nothing
+// cleared).
+int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, int64_t* n_ops, int64_t* trunc_rows,
+                                   int64_t trunc_cap, int64_t* n_trunc, int64_t* fused_rows, int64_t fused_cap,
+                                   int64_t* n_fused) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  int64_t need_ops = 0, need_trunc = 0, need_fused = 0;
+  abkv_planner_pending_sizes(h, &need_ops, &need_trunc, &need_fused);
+  if ((op_rows && need_ops > op_cap) || (trunc_rows && need_trunc > trunc_cap)) return ABKV_ERR_CAPACITY;
+  const int G = p->num_groups;
+  int64_t k = 0;
+  if (op_rows) {
+    for (int64_t rid : p->pending_order) {
+      Request* r = find_req(p, rid);
+      for (int g = 0; g < G; ++g) {
+        auto& st = r->step[g];
+        for (size_t b = 0; b < st.batches.size(); ++b)
+          for (auto& op : st.batches[b]) {
+            int64_t* row = op_rows + 7 * k++;
+            row[0] = rid;
+            row[1] = g;
+            row[2] = (int64_t)b;
+            row[3] = op.src_block;
+            row[4] = op.src_off;
+            row[5] = op.dst_block;
+            row[6] = op.dst_off;
+          }
+      }
+    }
+  }
+  if (n_ops) *n_ops = op_rows ? k : need_ops;
+  int64_t t = 0;
+  if (trunc_rows) {
+    for (int64_t rid : p->trunc_order) {
+      Request* r = find_req(p, rid);
+      int64_t* row = trunc_rows + (1 + G) * t++;
+      row[0] = rid;
+      for (int g = 0; g < G; ++g) row[1 + g] = r->trunc[g];
+    }
+  }
+  if (n_trunc) *n_trunc = trunc_rows ? t : need_trunc;
+  // Fused moves in request first-insertion order of the truncation records (every compacting request has one).
+  int64_t f = 0;
+  const int bs = p->block_size;
+  for (int64_t rid : p->trunc_order) {
+    Request* r = find_req(p, rid);
+    for (int g = 0; g < G; ++g) {
+      auto& st = r->step[g];
+      if (st.removals.empty()) continue;
+      int64_t lo = st.removals[0].start;
+      for (auto& rm : st.removals) lo = std::min(lo, rm.start);
+      const int64_t active0 = st.removals.front().active;
+      std::vector<int64_t> origin;
+      origin.reserve((size_t)(active0 - lo));
+      for (int64_t s = lo; s < active0; ++s) origin.push_back(s);
+      for (auto& rm : st.removals)
+        origin.erase(origin.begin() + (rm.start - lo), origin.begin() + (rm.end - lo));
+      for (size_t i = 0; i < origin.size(); ++i) {
+        const int64_t dst = lo + (int64_t)i, src = origin[i];
+        if (src == dst) continue;
+        if (fused_rows) {
+          if (f >= fused_cap) return ABKV_ERR_CAPACITY;
+          int64_t* row = fused_rows + 6 * f;
+          row[0] = rid;
+          row[1] = g;
+          row[2] = st.blocks_before[src / bs];
+          row[3] = src % bs;
+          row[4] = st.blocks_before[dst / bs];
+          row[5] = dst % bs;
+        }
+        ++f;
+      }
+    }
+  }
+  if (n_fused) *n_fused = f;
+  for (auto& kv : p->reqs) {
+    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    kv.second.has_trunc = false;
+  }
+  p->pending_order.clear();
+  p->trunc_order.clear();
+  return ABKV_OK;
+}
+
+int64_t abkv_planner_num_free(void* h) {
+  Planner* p = static_cast<Planner*>(h);
+  return p ? (int64_t)p->free_q.size() : -1;
+}
+
+int64_t abkv_planner_free_queue(void* h, int32_t* out, int64_t cap) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  if ((int64_t)p->free_q.size() > cap) return ABKV_ERR_CAPACITY;
+  int64_t i = 0;
+  for (int32_t b : p->free_q) out[i++] = b;
+  return i;
+}
+
+int64_t abkv_planner_block_ids(void* h, int64_t rid, int group, int32_t* out, int64_t cap) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  if (!r) return ABKV_ERR_NO_REQUEST;
+  auto& bl = r->blocks[group];
+  if ((int64_t)bl.size() > cap) return ABKV_ERR_CAPACITY;
+  for (size_t i = 0; i < bl.size(); ++i) out[i] = bl[i];
+  return (int64_t)bl.size();
+}
+
+// Write the page lists of `n` requests for one group into a [n, stride] int32 table (unused entries = pad).
+int abkv_planner_fill_block_table(void* h, const int64_t* rids, int n, int group, int32_t* table, int64_t stride,
+                                  int32_t pad) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  for (int i = 0; i < n; ++i) {
+    Request* r = find_req(p, rids[i]);
+    if (!r) return ABKV_ERR_NO_REQUEST;
+    auto& bl = r->blocks[group];
+    if ((int64_t)bl.size() > stride) return ABKV_ERR_CAPACITY;
+    int32_t* row = table + (int64_t)i * stride;
+    for (int64_t k = 0; k < stride; ++k) row[k] = k < (int64_t)bl.size() ? bl[k] : pad;
+  }
+  return ABKV_OK;
+}
+
+int64_t abkv_planner_compacted(void* h, int64_t rid, int group) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  return r ? r->spans[group].total : ABKV_ERR_NO_REQUEST;
+}
+
+int64_t abkv_planner_spans(void* h, int64_t rid, int group, int64_t* out, int64_t cap) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  if (!r) return ABKV_ERR_NO_REQUEST;
+  auto& sp = r->spans[group].spans;
+  if ((int64_t)sp.size() > cap) return ABKV_ERR_CAPACITY;
+  for (size_t i = 0; i < sp.size(); ++i) {
+    out[2 * i] = sp[i].first;
+    out[2 * i + 1] = sp[i].second;
+  }
+  return (int64_t)sp.size();
+}
+
+int64_t abkv_planner_logical_to_physical(void* h, int64_t rid, int group, int64_t pos) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  return r ? r->spans[group].l2p(pos) : ABKV_ERR_NO_REQUEST;
+}
+
+int64_t abkv_planner_physical_to_logical(void* h, int64_t rid, int group, int64_t pos) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  return r ? r->spans[group].p2l(pos) : ABKV_ERR_NO_REQUEST;
+}
+
+int abkv_planner_is_token_active(void* h, int64_t rid, int group, int64_t pos) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || group < 0 || group >= p->num_groups) return ABKV_ERR_ARG;
+  Request* r = find_req(p, rid);
+  return r ? (r->spans[group].is_active(pos) ? 1 : 0) : ABKV_ERR_NO_REQUEST;
+}
+
+// Apply a batch of scheduler events. Each event is 6 int64: (kind, rid, a, b, group_mask, 0) with
+//   kind 0: add request rid
+//   kind 1: schedule a tokens: allocate_slots(rid, a) then num_computed += a (must succeed)
+//   kind 2: mask_token_span(rid, a, b, groups = bits of group_mask, or all groups when group_mask < 0)
+//   kind 3: free request rid
+//   kind 4: take (and drop) the step outputs
+// Returns the number of events applied; on failure stops and returns -(index + 1) with last_error set.
+int64_t abkv_planner_apply_events(void* h, const int64_t* ev, int64_t n) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  std::vector<int32_t> gl;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t* e = ev + 6 * i;
+    int rc = ABKV_OK;
+    switch (e[0]) {
+      case 0:
+        rc = abkv_planner_add_request(h, e[1]);
+        break;
+      case 1: {
+        rc = abkv_planner_allocate_slots(h, e[1], e[2]);
+        if (rc == 0) {
+          p->last_error = "pool exhausted";
+          rc = ABKV_ERR_POOL;
+        } else if (rc == 1) {
+          rc = ABKV_OK;
+          find_req(p, e[1])->num_computed += e[2];
+        }
+        break;
+      }
+      case 2: {
+        gl.clear();
+        if (e[4] >= 0)
+          for (int g = 0; g < p->num_groups; ++g)
+            if ((e[4] >> g) & 1) gl.push_back(g);
+        rc = abkv_planner_mask_token_span(h, e[1], e[2], e[3], e[4] >= 0 ? gl.data() : nullptr,
+                                          e[4] >= 0 ? (int)gl.size() : -1, nullptr, nullptr);
+        break;
+      }
+      case 3:
+        rc = abkv_planner_free_request(h, e[1]);
+        break;
+      case 4:
+        rc = abkv_planner_take_step_outputs(h, nullptr, 0, nullptr, nullptr, 0, nullptr, nullptr, 0, nullptr);
+        break;
+      default:
+        p->last_error = "unknown event kind";
+        rc = ABKV_ERR_ARG;
+    }
+    if (rc != ABKV_OK) return -(i + 1);
+  }
+  return n;
+}
+
+}  // extern "C"

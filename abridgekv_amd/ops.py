@@ -1,0 +1,191 @@
+"""PyTorch-ROCm entry points of the abridged-KV kernels (thin wrappers over the C-ABI library).
+
+Every wrapper validates shapes, dtypes and devices on the host before a launch, runs on the caller's current HIP
+stream, never synchronises, and raises ``RuntimeError`` on a non-zero HIP error code. There is no CPU fallback:
+tensors must live on a GPU and the native library must be built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+
+from ._lib import check, lib
+
+PAGE = 16
+HEADS_KV = 8
+HEADS_Q = 32
+HEAD_DIM = 128
+SLOT_BYTES = HEADS_KV * HEAD_DIM * 2           # one slot of K (or V) of one layer, bf16
+HALF_BYTES = PAGE * SLOT_BYTES                 # K half of a page
+PAGE_BYTES = 2 * HALF_BYTES                    # one page of one layer
+DEFAULT_SPLIT_PAGES = 32                       # 512 slots per split
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def kv_cache_shape(num_pages: int) -> tuple[int, ...]:
+    """Layer cache shape [num_pages, 2, 16, 8, 128] (the reference's FlashInfer NHD layout,
+    third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1215-1217)."""
+    return (num_pages, 2, PAGE, HEADS_KV, HEAD_DIM)
+
+
+def _check_cache(kv_cache: torch.Tensor) -> None:
+    _require(kv_cache.is_cuda, "kv_cache must be on the GPU")
+    _require(kv_cache.dtype == torch.bfloat16, "kv_cache must be bfloat16")
+    _require(kv_cache.dim() == 5 and tuple(kv_cache.shape[1:]) == (2, PAGE, HEADS_KV, HEAD_DIM),
+             f"kv_cache must be [P, 2, {PAGE}, {HEADS_KV}, {HEAD_DIM}], got {tuple(kv_cache.shape)}")
+    _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+
+
+def decode_workspace(num_seqs: int, max_pages: int, split_pages: int = DEFAULT_SPLIT_PAGES,
+                     device=None) -> torch.Tensor | None:
+    """Workspace for :func:`decode_attention` (None when no sequence can need a second split)."""
+    max_splits = -(-max_pages // split_pages)
+    if max_splits <= 1:
+        return None
+    n = lib().abkv_decode_workspace_size(num_seqs, max_splits)
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     scale: float, max_pages: int | None = None, out: torch.Tensor | None = None,
+                     lse: torch.Tensor | None = None, split_pages: int = DEFAULT_SPLIT_PAGES,
+                     workspace: torch.Tensor | None = None):
+    """Decode attention of one layer over its group's paged cache.
+
+    q [B, 32, 128] bf16 (dims contiguous); kv_cache [P, 2, 16, 8, 128] bf16; block_table [B, W] int32;
+    seq_lens [B] int32 (physical rows); ``max_pages`` bounds ceil(seq_len / 16) (defaults to W).
+    Writes and returns (out [B, 32, 128] bf16, lse [B, 32] fp32 natural log or None).
+    """
+    _check_cache(kv_cache)
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM),
+             f"q must be cuda bf16 [B, {HEADS_Q}, {HEAD_DIM}]")
+    _require(q.stride(2) == 1, "q dims must be contiguous")
+    B = q.shape[0]
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] >= B and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() >= B
+             and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32 [B]")
+    _require(split_pages > 0 and split_pages % 2 == 0, "split_pages must be a positive even number")
+    W = block_table.shape[1]
+    max_pages = W if max_pages is None else int(max_pages)
+    _require(0 < max_pages <= W, "max_pages must be in [1, block_table width]")
+    if out is None:
+        out = torch.empty((B, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (B, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
+             "out must be bf16 [B, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= B * HEADS_Q,
+                 "lse must be contiguous fp32 [B, 32]")
+    max_splits = -(-max_pages // split_pages)
+    ws_bytes = 0
+    if max_splits > 1:
+        need = lib().abkv_decode_workspace_size(B, max_splits)
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        _require(workspace.numel() * workspace.element_size() >= need, "decode workspace too small")
+        ws_bytes = workspace.numel() * workspace.element_size()
+    rc = lib().abkv_decode_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                _ptr(block_table),
+                                block_table.stride(0), _ptr(seq_lens), B, max_pages, split_pages, float(scale),
+                                _ptr(out), out.stride(0), out.stride(1), _ptr(lse), _ptr(workspace), ws_bytes,
+                                C.c_void_p(_stream()))
+    check(rc, "abkv_decode_attn")
+    return out, lse
+
+
+def _layer_ptrs(layer_caches):
+    _require(0 < len(layer_caches) <= 16, "between 1 and 16 layer caches per launch")
+    for c in layer_caches:
+        _check_cache(c)
+    _require(len({c.shape[0] for c in layer_caches}) == 1, "layer caches of one launch must have equal page counts")
+    arr = (C.c_void_p * len(layer_caches))(*[c.data_ptr() for c in layer_caches])
+    return arr, layer_caches[0].shape[0]
+
+
+def kv_move_segments(layer_caches, ops: torch.Tensor, seg_offsets: torch.Tensor) -> None:
+    """Apply compaction copy ops (int32 [n, 4] on the GPU) to every layer cache, one workgroup per
+    (segment, layer). See abkv_kv_move_segments for the ordering precondition inside a segment."""
+    _require(ops.is_cuda and ops.dtype == torch.int32 and ops.dim() == 2 and ops.shape[1] == 4
+             and ops.is_contiguous(), "ops must be contiguous cuda int32 [n, 4]")
+    _require(seg_offsets.is_cuda and seg_offsets.dtype == torch.int32 and seg_offsets.is_contiguous(),
+             "seg_offsets must be contiguous cuda int32")
+    n_seg = seg_offsets.numel() - 1
+    if n_seg <= 0 or ops.shape[0] == 0:
+        return
+    arr, num_pages = _layer_ptrs(layer_caches)
+    rc = lib().abkv_kv_move_segments(arr, len(layer_caches), num_pages, PAGE, PAGE_BYTES, HALF_BYTES, SLOT_BYTES, _ptr(ops),
+                                     _ptr(seg_offsets), n_seg, C.c_void_p(_stream()))
+    check(rc, "abkv_kv_move_segments")
+
+
+def kv_copy_staged(layer_caches, ops: torch.Tensor, stage: torch.Tensor | None = None) -> None:
+    """Gather-then-scatter for an arbitrary op list, staged through a workspace."""
+    _require(ops.is_cuda and ops.dtype == torch.int32 and ops.dim() == 2 and ops.shape[1] == 4
+             and ops.is_contiguous(), "ops must be contiguous cuda int32 [n, 4]")
+    n = ops.shape[0]
+    if n == 0:
+        return
+    arr, num_pages = _layer_ptrs(layer_caches)
+    need = lib().abkv_kv_stage_bytes(len(layer_caches), n, SLOT_BYTES)
+    if stage is None:
+        stage = torch.empty(need, dtype=torch.uint8, device=ops.device)
+    nbytes = stage.numel() * stage.element_size()
+    _require(nbytes >= need, "stage buffer too small")
+    rc = lib().abkv_kv_copy_staged(arr, len(layer_caches), num_pages, PAGE, PAGE_BYTES, HALF_BYTES, SLOT_BYTES, _ptr(ops), n,
+                                   _ptr(stage), nbytes, C.c_void_p(_stream()))
+    check(rc, "abkv_kv_copy_staged")
+
+
+def kv_append(key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor, kv_cache: torch.Tensor) -> None:
+    """reshape_and_cache: write key/value [T, 8, 128] bf16 rows at slot_mapping [T] int64 (negative = skip)."""
+    _check_cache(kv_cache)
+    T = slot_mapping.numel()
+    for name, t in (("key", key), ("value", value)):
+        _require(t.is_cuda and t.dtype == torch.bfloat16 and t.shape[0] >= T
+                 and tuple(t.shape[1:]) == (HEADS_KV, HEAD_DIM) and t.stride(2) == 1 and t.stride(1) == HEAD_DIM,
+                 f"{name} must be cuda bf16 [T, {HEADS_KV}, {HEAD_DIM}] with contiguous rows")
+    _require(slot_mapping.is_cuda and slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous(),
+             "slot_mapping must be contiguous cuda int64")
+    if T == 0:
+        return
+    rc = lib().abkv_kv_append(_ptr(key), key.stride(0) * 2, _ptr(value), value.stride(0) * 2, _ptr(slot_mapping), T,
+                              _ptr(kv_cache), kv_cache.shape[0], PAGE_BYTES, HALF_BYTES, SLOT_BYTES, PAGE,
+                              C.c_void_p(_stream()))
+    check(rc, "abkv_kv_append")
+
+
+def slot_mapping(req_idx: torch.Tensor, positions: torch.Tensor, block_table: torch.Tensor,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Device slot mapping: table[req][pos // 16] * 16 + pos % 16 (negative positions -> -1)."""
+    _require(req_idx.is_cuda and req_idx.dtype == torch.int32 and req_idx.is_contiguous(), "req_idx: cuda int32")
+    _require(positions.is_cuda and positions.dtype == torch.int64 and positions.is_contiguous(),
+             "positions: cuda int64")
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.is_contiguous(),
+             "block_table: contiguous cuda int32 [B, W]")
+    n = positions.numel()
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64, device=positions.device)
+    _require(req_idx.numel() == n, "req_idx and positions must have the same length")
+    rc = lib().abkv_slot_mapping(_ptr(req_idx), _ptr(positions), n, _ptr(block_table), block_table.shape[0],
+                                 block_table.shape[1], PAGE,
+                                 _ptr(out), C.c_void_p(_stream()))
+    check(rc, "abkv_slot_mapping")
+    return out
+
+
+def default_scale() -> float:
+    return 1.0 / math.sqrt(HEAD_DIM)

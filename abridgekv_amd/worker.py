@@ -1,0 +1,110 @@
+"""Worker-side execution of compaction: copy ops, fused moves, block-table truncation, slot maps.
+
+Mirrors GPUModelRunner._execute_kv_copy_operations / _execute_kv_copy_group
+(third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1147-1224), the truncation step of _update_states
+(:935-950, block_table.py:132-137, :330-336) and the per-group slot maps (:1579-1661, block_table.py:186-197),
+executing on the HIP kernels of libabridgekv_amd.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+from .ops import PAGE
+
+
+def _validate_ops(all_ops: np.ndarray, num_pages: int) -> None:
+    if all_ops.size == 0:
+        return
+    if (all_ops[:, [0, 2]].min() < 0 or all_ops[:, [0, 2]].max() >= num_pages
+            or all_ops[:, [1, 3]].min() < 0 or all_ops[:, [1, 3]].max() >= PAGE):
+        raise ValueError("copy op names a page or offset outside the cache")
+
+
+def _reads_after_write(seg: np.ndarray) -> bool:
+    """True if some op of the segment reads a slot an earlier op of the segment wrote."""
+    dst = seg[:, 2].astype(np.int64) * PAGE + seg[:, 3]
+    src = seg[:, 0].astype(np.int64) * PAGE + seg[:, 1]
+    first_write = {}
+    for i, d in enumerate(dst.tolist()):
+        first_write.setdefault(d, i)
+    return any(first_write.get(s, len(dst)) < i for i, s in enumerate(src.tolist()))
+
+
+def execute_kv_copy_group(segments, layer_caches, check: bool = True) -> None:
+    """Apply one batch: ``segments`` is a list of per-request op lists [(src_block, src_off, dst_block, dst_off)];
+    every layer cache of the group receives the same moves with gather-then-scatter semantics."""
+    segs = [np.asarray(s, dtype=np.int32).reshape(-1, 4) for s in segments if len(s)]
+    if not segs:
+        return
+    all_ops = np.concatenate(segs)
+    device = layer_caches[0].device
+    num_pages = layer_caches[0].shape[0]
+    if check:
+        _validate_ops(all_ops, num_pages)
+    hazard = check and any(_reads_after_write(s) for s in segs)
+    ops_d = torch.from_numpy(all_ops).to(device, non_blocking=False)
+    for lo in range(0, len(layer_caches), 16):
+        caches = layer_caches[lo: lo + 16]
+        if hazard:
+            ops.kv_copy_staged(caches, ops_d)
+        else:
+            offs = np.zeros(len(segs) + 1, np.int32)
+            offs[1:] = np.cumsum([len(s) for s in segs])
+            ops.kv_move_segments(caches, ops_d, torch.from_numpy(offs).to(device))
+
+
+def execute_kv_copy_operations(kv_copy_operations: dict, layer_caches_by_group, check: bool = True) -> None:
+    """Per group, batch b of every request is applied together, batches in order (a later removal's ops assume the
+    earlier shift is done). ``kv_copy_operations``: request id -> per group -> ordered batches of ops."""
+    for gid, caches in enumerate(layer_caches_by_group):
+        batches = [per_group[gid] for per_group in kv_copy_operations.values() if gid < len(per_group)]
+        num_batches = max((len(b) for b in batches), default=0)
+        for b in range(num_batches):
+            segments = [req[b] for req in batches if b < len(req)]
+            execute_kv_copy_group(segments, caches, check=check)
+
+
+def execute_fused_moves(fused_moves: np.ndarray, layer_caches_by_group, check: bool = True) -> None:
+    """Apply a planner step's fused move rows (request, group, src_block, src_off, dst_block, dst_off): one launch
+    per group, one segment per request. Rows of one (request, group) are monotone (increasing source, dst < src), so
+    the in-register chunked copy is exact."""
+    if fused_moves.size == 0:
+        return
+    fm = np.asarray(fused_moves, dtype=np.int64)
+    for gid, caches in enumerate(layer_caches_by_group):
+        rows = fm[fm[:, 1] == gid]
+        if rows.size == 0:
+            continue
+        cut = np.flatnonzero(np.diff(rows[:, 0])) + 1
+        offs = np.concatenate([[0], cut, [rows.shape[0]]]).astype(np.int32)
+        ops_h = np.ascontiguousarray(rows[:, 2:6], dtype=np.int32)
+        if check:
+            _validate_ops(ops_h, caches[0].shape[0])
+        device = caches[0].device
+        ops_d = torch.from_numpy(ops_h).to(device)
+        offs_d = torch.from_numpy(offs).to(device)
+        for lo in range(0, len(caches), 16):
+            ops.kv_move_segments(caches[lo: lo + 16], ops_d, offs_d)
+
+
+def truncate_block_table(block_ids_by_group, keep):
+    """block_table.py:132-137 / gpu_model_runner.py:935-950: keep the first ``keep[g]`` pages of every group."""
+    if len(block_ids_by_group) != len(keep):
+        raise RuntimeError("KV cache group count changed during block-table compaction")
+    for ids, k in zip(block_ids_by_group, keep):
+        del ids[k:]
+
+
+def physical_positions(logical_positions, compacted_counts):
+    """gpu_model_runner.py:1585-1590: one physical position array per group, phys = logical - compacted[g]."""
+    lp = np.asarray(logical_positions, dtype=np.int64)
+    return [lp - c for c in compacted_counts]
+
+
+def slot_mapping_host(block_ids, positions):
+    """block_table.py:186-197 on the host (used when the metadata is built on the CPU)."""
+    pos = np.asarray(positions, dtype=np.int64)
+    table = np.asarray(block_ids, dtype=np.int64)
+    return table[pos // PAGE] * PAGE + pos % PAGE

@@ -1,0 +1,130 @@
+/* C-ABI of libabridgekv_amd.so: the MI355X (gfx950) abridged-KV hot path.
+ *
+ * Plain pointers and sizes only. Device pointers refer to HIP device memory of the current device; `stream` is a
+ * hipStream_t (0 = the null stream). Kernel entry points return 0 on success or a hipError_t code; they never
+ * synchronise. Planner entry points are pure host code and return the ABKV_* codes below.
+ *
+ * Cache geometry of the kernels (the served Qwen3-4B attention): a layer's paged KV cache is
+ * [num_pages, 2 (K,V), 16 slots, 8 KV heads, 128] bf16 -- the FlashInfer NHD layout the reference's worker allocates
+ * (third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1215-1217). 32 query heads (GQA 4).
+ */
+#ifndef ABRIDGEKV_AMD_H
+#define ABRIDGEKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* abkv_stream_t; /* == hipStream_t */
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Decode attention (kernel 1).
+ * Replaces the FlashInfer BatchDecodeWithPagedKVCache call of the stock vLLM backend that the reference's overlay
+ * drives with per-group metadata (third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1872-1887, 2184-2276;
+ * backend chosen at scripts/bench_decode.py:70) and the pure-torch consumer
+ * third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:564-616 (_attend_decode_batched).
+ * q [num_seqs, 32, 128] bf16 (strides in elements), block_table [num_seqs, block_table_stride] int32 (group's page
+ * table), seq_lens [num_seqs] int32 (physical rows of the group), out [num_seqs, 32, 128] bf16, lse [num_seqs, 32]
+ * fp32 natural log (may be NULL). num_pages: pages in kv_cache (page ids are clamped into range).
+ * split_pages: even number of pages per split. max_pages_per_seq (<= block_table_stride) bounds ceil(seq_len/16);
+ * longer sequences are truncated to max_pages_per_seq * 16 rows. workspace: >= abkv_decode_workspace_size(num_seqs, ceil(max_pages/split_pages))
+ * bytes when a sequence can need more than one split (may be NULL otherwise).
+ * ------------------------------------------------------------------------------------------------------------- */
+size_t abkv_decode_workspace_size(int num_seqs, int max_splits);
+int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache, int num_pages,
+                     const int32_t* block_table, long block_table_stride, const int32_t* seq_lens, int num_seqs,
+                     int max_pages_per_seq, int split_pages, float scale, void* out, long out_stride_seq,
+                     long out_stride_head, float* lse, void* workspace, size_t workspace_bytes,
+                     abkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * KV-cache row movement for compaction (kernel 2, device half).
+ * Replaces GPUModelRunner._execute_kv_copy_group (gpu_model_runner.py:1194-1224): ops [n, 4] int32 rows
+ * (src_block, src_off, dst_block, dst_off) applied to each of n_layers layer caches (<= 16) with gather-then-scatter
+ * semantics. abkv_kv_move_segments: ops are split into segments (seg_offsets [n_segments + 1] int32, device) touching
+ * disjoint pages; inside a segment no op may read a slot written by an earlier op of that segment (true for
+ * compaction ops: increasing source, dst < src, single_type_kv_cache_manager.py:378-381). abkv_kv_copy_staged: any op
+ * list, rows staged through `stage` (>= abkv_kv_stage_bytes). page_bytes / half_bytes / slot_bytes describe the cache
+ * (64 KiB / 32 KiB / 2 KiB for the served geometry); ops naming a page outside [0, num_pages) or an offset outside
+ * [0, block_size) are skipped.
+ * ------------------------------------------------------------------------------------------------------------- */
+int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                          long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments, abkv_stream_t stream);
+size_t abkv_kv_stage_bytes(int n_layers, int n_ops, int slot_bytes);
+int abkv_kv_copy_staged(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                        long half_bytes, int slot_bytes, const int32_t* ops, int n_ops, void* stage, size_t stage_bytes, abkv_stream_t stream);
+
+/* KV append: replaces the stock vLLM compiled op reshape_and_cache(_flash) fed by slot maps from
+ * third_party/vllm_overlay/vllm/v1/worker/block_table.py:186-197. key/value [num_tokens, slot_bytes] (row strides in
+ * bytes); slot_mapping [num_tokens] int64, negative or >= num_pages * block_size = skip. */
+int abkv_kv_append(const void* key, long key_stride, const void* value, long value_stride,
+                   const int64_t* slot_mapping, int num_tokens, void* kv_cache, int num_pages, long page_bytes,
+                   long half_bytes, int slot_bytes, int block_size, abkv_stream_t stream);
+
+/* Slot mapping on device: BlockTable.compute_slot_mapping (block_table.py:186-197, non-CP branch).
+ * slot = table[req_idx[t]][pos / block_size] * block_size + pos % block_size; -1 when pos < 0, pos is past the
+ * table row (block_table_stride pages) or req_idx[t] is outside [0, num_reqs). */
+int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_tokens, const int32_t* block_table,
+                      int num_reqs, long block_table_stride, int block_size, int64_t* slot_mapping,
+                      abkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager
+ * bookkeeping: Scheduler.mask_token_span (third_party/vllm_overlay/vllm/v1/core/sched/scheduler.py:2060-2204),
+ * SingleTypeKVCacheManager.compact_kv_cache_span/_truncate_compacted_blocks/allocate_new_blocks/free
+ * (v1/core/single_type_kv_cache_manager.py:122-145, 173-188, 358-452), BlockPool.get_new_blocks/free_blocks/
+ * copy_kv_slots (v1/core/block_pool.py:295-325, 385-399, 488-550), FreeKVCacheBlockQueue (v1/core/kv_cache_utils.py:
+ * 157-345), KVCacheManager.allocate_slots (v1/core/kv_cache_manager.py:206-340), CompactedSpanIndex
+ * (v1/compacted_spans.py:8-68). One planner = one page pool shared by num_groups KV-cache groups.
+ * ------------------------------------------------------------------------------------------------------------- */
+enum {
+  ABKV_OK = 0,
+  ABKV_ERR_ARG = -1,
+  ABKV_ERR_NO_REQUEST = -2,
+  ABKV_ERR_SPAN = -3,     /* the reference's SpanRemovalResult(success=False); message in abkv_planner_last_error */
+  ABKV_ERR_POOL = -4,
+  ABKV_ERR_CAPACITY = -5
+};
+
+/* free_order: NULL (pages 1..num_blocks-1 in id order, page 0 null -- the reference's construction) or a
+ * permutation of 1..num_blocks-1 giving the initial free-queue order. */
+void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const int32_t* free_order,
+                          int64_t max_model_len);
+void abkv_planner_destroy(void* planner);
+const char* abkv_planner_last_error(void* planner);
+int abkv_planner_add_request(void* planner, int64_t rid);
+int abkv_planner_free_request(void* planner, int64_t rid);
+int abkv_planner_set_num_computed(void* planner, int64_t rid, int64_t num_computed_tokens);
+int64_t abkv_planner_get_num_computed(void* planner, int64_t rid);
+/* 1 = allocated, 0 = pool cannot cover it (reference returns None), < 0 = error. */
+int abkv_planner_allocate_slots(void* planner, int64_t rid, int64_t num_new_tokens);
+int abkv_planner_mask_token_span(void* planner, int64_t rid, int64_t start, int64_t end, const int32_t* groups,
+                                 int n_groups, int64_t* tokens_removed, int64_t* blocks_freed);
+int abkv_planner_pending_sizes(void* planner, int64_t* n_op_rows, int64_t* n_trunc_rows, int64_t* n_fused_rows);
+/* op_rows [n,7] (rid, group, batch, src_block, src_off, dst_block, dst_off); trunc_rows [n, 1+G];
+ * fused_rows [n,6] (rid, group, src_block, src_off, dst_block, dst_off): the step's removals composed per
+ * (request, group), rows truncated later in the same step are not moved. */
+int abkv_planner_take_step_outputs(void* planner, int64_t* op_rows, int64_t op_cap, int64_t* n_ops,
+                                   int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc, int64_t* fused_rows,
+                                   int64_t fused_cap, int64_t* n_fused);
+int64_t abkv_planner_num_free(void* planner);
+int64_t abkv_planner_free_queue(void* planner, int32_t* out, int64_t cap);
+int64_t abkv_planner_block_ids(void* planner, int64_t rid, int group, int32_t* out, int64_t cap);
+int abkv_planner_fill_block_table(void* planner, const int64_t* rids, int n, int group, int32_t* table,
+                                  int64_t stride, int32_t pad);
+int64_t abkv_planner_compacted(void* planner, int64_t rid, int group);
+int64_t abkv_planner_spans(void* planner, int64_t rid, int group, int64_t* out, int64_t cap);
+int64_t abkv_planner_logical_to_physical(void* planner, int64_t rid, int group, int64_t pos);
+int64_t abkv_planner_physical_to_logical(void* planner, int64_t rid, int group, int64_t pos);
+int abkv_planner_is_token_active(void* planner, int64_t rid, int group, int64_t pos);
+/* events [n, 6] int64 (kind, rid, a, b, group_mask, 0): 0 add, 1 schedule a tokens, 2 mask [a, b) in the groups of
+ * group_mask (< 0: all), 3 free, 4 drop step outputs. Returns n, or -(failing index + 1). */
+int64_t abkv_planner_apply_events(void* planner, const int64_t* events, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ABRIDGEKV_AMD_H */

@@ -1,0 +1,112 @@
+"""Teacher-forced attention under the compression mask (oracle; test infrastructure only).
+
+Layout of one sequence: N blocks of [C content | K codes] (S0 = N * (C + K)), content tokens numbered block-major.
+Visibility (L=1, full code<->code attention, no replay / raw / retained tails, raw prompt of ``prompt_len`` content
+tokens, optional per-query-head code quota):
+  causal & (own-block content | earlier blocks' codes | raw-prompt content)  |  (code query & code key & same block)
+  and, with a quota, a code key is visible to head h only if its slot < quota[h].
+
+Two independent restatements of the reference are kept and cross-checked:
+* ``arith_mask``  -- closed-form integer arithmetic: abridgekv/compress_forward.py:695-727 (_arith_mask_mod) with
+                     the quota term of :725-726.
+* ``role_mask``   -- role/block/content-position gathers: abridgekv/gen_compress.py:1062-1140 (_dense_mask, the
+                     reference's own dense oracle) restricted to L=1 and no tails, plus the quota rule of
+                     abridgekv/compress_forward.py:230-236 (_quota_key_allowed).
+Pinning: the two agree element by element on every tested shape; brute-force per-element predicates written from
+the prose rule (tests/test_oracle_prefill.py); N=1 without codes reduces to the causal mask; masked_attention_fp64
+reduces to textbook causal attention under the causal mask and to per-row softmax identities (rows sum to one,
+single visible key -> that key's value).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def arith_mask(C, K, N, prompt_len=None, head_quota=None):
+    """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
+    per = C + K
+    S0 = N * per
+    q = np.arange(S0, dtype=np.int64).reshape(S0, 1)
+    kv = np.arange(S0, dtype=np.int64).reshape(1, S0)
+    qb, kb = q // per, kv // per
+    qw, kw = q - qb * per, kv - kb * per
+    k_content = kw < C
+    same_blk = kb == qb
+    vis = (k_content & same_blk) | ((~k_content) & (kb < qb))
+    if prompt_len is not None:
+        pl = np.asarray(prompt_len, dtype=np.int64).reshape(-1, 1, 1)
+        vis = vis[None] | (k_content & (kb * C + kw < pl))[...]
+    vis = (kv <= q) & vis
+    vis = vis | ((qw >= C) & (~k_content) & same_blk)
+    if head_quota is not None:
+        hq = np.asarray(head_quota, dtype=np.int64).reshape(-1, 1, 1)
+        quota_ok = k_content | ((kw - C) < hq)                    # [H, 1, S0]
+        if vis.ndim == 3:
+            vis = vis[:, None] & quota_ok[None]
+        else:
+            vis = vis[None] & quota_ok
+    return vis
+
+
+def role_mask(C, K, N, prompt_len=None, head_quota=None):
+    """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
+    per = C + K
+    S0 = N * per
+    idx = np.arange(S0)
+    within, blk = idx % per, idx // per
+    role = (within >= C).astype(np.int64)                           # 0 content, 1 code (L = 1)
+    content_abs = np.where(role == 0, blk * C + within, -1)
+    code_slot = np.where(role == 1, within - C, -1)
+    qr, kr = role.reshape(S0, 1), role.reshape(1, S0)
+    qb, kb = blk.reshape(S0, 1), blk.reshape(1, S0)
+    causal = idx.reshape(1, S0) <= idx.reshape(S0, 1)
+    content_vis = (kr == 0) & (kb == qb)
+    earlier_final = (kr == 1) & (kb < qb)
+    pause_q = qr == 1
+    samepass = pause_q & (kr == qr) & (kb == qb)
+    base = (causal & (content_vis | earlier_final)) | samepass
+    if prompt_len is not None:
+        pl = np.asarray(prompt_len).reshape(-1, 1, 1)
+        prompt_raw = (kr == 0)[None] & (content_abs.reshape(1, 1, S0) < pl) & (content_abs.reshape(1, 1, S0) >= 0)
+        base = base[None] | (causal[None] & prompt_raw)
+    if head_quota is not None:
+        hq = np.asarray(head_quota).reshape(-1, 1, 1)
+        slot = code_slot.reshape(1, 1, S0)
+        allowed = (slot < 0) | (slot < hq)                          # _quota_key_allowed
+        if base.ndim == 3:
+            base = base[:, None] & allowed[None]
+        else:
+            base = base[None] & allowed
+    return base
+
+
+def masked_attention_fp64(q, k, v, mask, scale):
+    """softmax(scale * q k^T, masked) v per head in float64, GQA by head // (Hq / Hkv).
+
+    q: [S, Hq, D]; k, v: [S, Hkv, D]; mask: [S, S] or [Hq, S, S] bool. Returns out [S, Hq, D], lse [S, Hq]
+    (natural log). Same arithmetic as the reference's dense path (gen_compress.py:1177-1179) in float64.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    out = np.zeros((S, Hq, D))
+    lse = np.zeros((S, Hq))
+    for h in range(Hq):
+        m = mask if mask.ndim == 2 else mask[h]
+        s = (q[:, h] @ k[:, h // g].T) * scale
+        s = np.where(m, s, -np.inf)
+        mx = s.max(axis=1, keepdims=True)
+        e = np.exp(s - mx)
+        z = e.sum(axis=1, keepdims=True)
+        out[:, h] = (e / z) @ v[:, h // g]
+        lse[:, h] = (mx + np.log(z))[:, 0]
+    return out, lse
+
+
+def visible_pairs(C, K, N, prompt_len=None):
+    """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
+    m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len])
+    return int(m.sum())

@@ -1,0 +1,215 @@
+"""Block state machine of one request: which tokens are scheduled when and which spans are compacted
+(oracle; test infrastructure only).
+
+Restates, for the served configuration of the per-layer arm (C=512 content tokens per block, K_max code rows,
+raw prompt, bitrev positions, no replay/retained tails, physical per-layer quotas), the role bookkeeping of
+third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:
+  prepare_request :42-105 (first prompt chunk), limit_num_new_tokens :123-151 (a CODE run is scheduled whole,
+  a CONTENT run up to its end), should_skip_sampling :153-168, update_after_step :170-257 (a full block stages
+  its K codes and holds the sampled token), _stage_codes :369-400, _finish_block :419-465 (compact, then open the
+  next block with the next prompt chunk or the held token), _compact_response_content :467-557 (response content
+  in every group, then code slots [q, K) per distinct quota q < K in ascending order).
+
+The machine is planner-agnostic: it emits the scheduler-visible events (allocate ``n`` new tokens, then compact
+spans) and is shared by the oracle planner and the product planner so that both see identical event streams.
+
+Pinning: tests/test_oracle_trace.py checks the reference's invariants (scripts/test_compresslm_physical_quotas.py:
+68-138): every compacted block keeps exactly codes[:q_g] and no response content in group g; removed rows per
+group differ from group 0 by (K - q_g) per compacted block; and the closed form of oracle.layout.rows_per_layer.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+CONTENT, CODE = 0, 1
+
+
+@dataclass
+class Block:
+    block_id: int
+    content_positions: list = field(default_factory=list)
+    prompt_positions: list = field(default_factory=list)
+    response_positions: list = field(default_factory=list)
+    code_span: tuple | None = None
+
+
+class RequestTrace:
+    """Logical token stream of one request and its block structure."""
+
+    def __init__(self, prompt_len, max_tokens, C, K, group_quotas):
+        if prompt_len <= 0:
+            raise ValueError("CompressLM decoding requires a non-empty prompt")
+        self.C, self.K = C, K
+        self.group_quotas = tuple(group_quotas)
+        self.prompt_len = prompt_len
+        self.max_tokens = max_tokens
+        self.roles: list[int] = []
+        self.kind: list[str] = []               # "prompt" | "response" | "code" per logical position
+        self.blocks = [Block(0)]
+        self.compacted_block_ids: set[int] = set()
+        self.num_computed_tokens = 0
+        self.pending_prompt = 0
+        self.held = False
+        self.visible = 0
+        self.finished = False
+        first = min(prompt_len, C)                # processor.py:90-104
+        self.pending_prompt = first
+        self._record_content(first, is_prompt=True)
+
+    @property
+    def num_tokens(self):
+        return len(self.roles)
+
+    @property
+    def current_block(self):
+        return self.blocks[-1]
+
+    def _record_content(self, n, is_prompt):       # processor.py:318-353 (no tails)
+        block = self.current_block
+        for _ in range(n):
+            pos = len(self.roles)
+            block.content_positions.append(pos)
+            (block.prompt_positions if is_prompt else block.response_positions).append(pos)
+            self.roles.append(CONTENT)
+            self.kind.append("prompt" if is_prompt else "response")
+
+    def next_chunk(self):
+        """Tokens the scheduler runs next for this request (limit_num_new_tokens with an unbounded budget)."""
+        start = self.num_computed_tokens
+        if self.finished or start >= self.num_tokens:
+            return 0
+        role = self.roles[start]
+        end = start + 1
+        while end < self.num_tokens and self.roles[end] == role:
+            end += 1
+        return end - start
+
+    def should_skip_sampling(self, n):             # processor.py:153-168
+        start = self.num_computed_tokens - n
+        end = self.num_computed_tokens
+        if self.roles[start] != CONTENT:
+            return True
+        if end < self.num_tokens:
+            return True
+        return self.pending_prompt < self.prompt_len
+
+    def after_step(self, n):
+        """update_after_step for a step that ran ``n`` tokens (num_computed_tokens already advanced).
+        Returns the compaction calls as (start, end, groups-or-None) in call order."""
+        end = self.num_computed_tokens
+        start = end - n
+        role = self.roles[start]
+        sampled = not self.should_skip_sampling(n)
+        calls = []
+        if sampled:
+            self.visible += 1
+            if self.visible >= self.max_tokens:        # _check_stop (processor.py:663-685), length cap
+                self.finished = True
+                return calls
+        block = self.blocks[self._block_of(start)]
+        role_end = end == self.num_tokens or self.roles[end] != role
+        if role == CONTENT:
+            if len(block.content_positions) == self.C and end == block.content_positions[-1] + 1:
+                if block.code_span is None:
+                    self.held = sampled
+                    cs = self.num_tokens                    # _stage_codes (processor.py:369-400)
+                    self.roles.extend([CODE] * self.K)
+                    self.kind.extend(["code"] * self.K)
+                    block.code_span = (cs, cs + self.K)
+            elif sampled:
+                self._record_content(1, is_prompt=False)
+        elif role == CODE and role_end:
+            calls = self._finish_block(block)
+        return calls
+
+    def _block_of(self, pos):
+        for b in self.blocks:
+            if b.content_positions and b.content_positions[0] <= pos:
+                last = b.code_span[1] if b.code_span else b.content_positions[-1] + 1
+                if pos < last:
+                    return b.block_id
+        raise RuntimeError(f"position {pos} outside every block")
+
+    def _finish_block(self, block):                # processor.py:419-465, :467-557
+        calls = []
+        if block.block_id not in self.compacted_block_ids:
+            pos = block.response_positions
+            if pos:
+                if pos != list(range(pos[0], pos[-1] + 1)):
+                    raise RuntimeError("CompressLM response content must be contiguous")
+                calls.append((pos[0], pos[-1] + 1, None))
+            cs, ce = block.code_span
+            for q in sorted(set(self.group_quotas)):
+                if q >= self.K:
+                    continue
+                calls.append((cs + q, ce, [g for g, gq in enumerate(self.group_quotas) if gq == q]))
+            self.compacted_block_ids.add(block.block_id)
+        nxt = Block(len(self.blocks))
+        self.blocks.append(nxt)
+        if self.pending_prompt < self.prompt_len:
+            chunk = min(self.C, self.prompt_len - self.pending_prompt)
+            self.pending_prompt += chunk
+            self._record_content(chunk, is_prompt=True)
+            return calls
+        if not self.held:
+            raise RuntimeError("CompressLM block completed without continuation token")
+        self.held = False
+        self._record_content(1, is_prompt=False)
+        return calls
+
+    def kept_positions(self, group):
+        """Brute-force physical stream of ``group``: every logical position not removed from that group."""
+        q = self.group_quotas[group]
+        keep = []
+        for b in self.blocks:
+            compacted = b.block_id in self.compacted_block_ids
+            for p in b.content_positions:
+                if p < self.num_computed_tokens and not (compacted and self.kind[p] == "response"):
+                    keep.append(p)
+            if b.code_span:
+                cs, ce = b.code_span
+                for p in range(cs, min(ce, self.num_computed_tokens)):
+                    if not (compacted and p - cs >= q):
+                        keep.append(p)
+        return sorted(keep)
+
+
+def build_schedule(prompt_lens, max_tokens, start_steps, num_steps, C, K, group_quotas):
+    """Planner-agnostic event stream of several requests served together.
+
+    Every step first schedules each running request in request order (allocate ``n`` new tokens), then, after the
+    model step, runs each request's update in request order (compaction calls), as the reference scheduler does
+    (schedule(): scheduler.py:300-1061, then update_from_output -> update_after_step: scheduler.py:1512-1532).
+    Returns (events, traces): events are ("alloc", rid, n) / ("mask", rid, start, end, groups) tuples grouped per
+    step as a list of lists; traces are the final RequestTrace objects.
+    """
+    traces = [RequestTrace(p, m, C, K, group_quotas) for p, m in zip(prompt_lens, max_tokens)]
+    steps = []
+    for step in range(num_steps):
+        events, ran = [], []
+        for rid, tr in enumerate(traces):
+            if step < start_steps[rid] or tr.finished:
+                continue
+            n = tr.next_chunk()
+            if n == 0:
+                continue
+            events.append(("alloc", rid, n))
+            tr.num_computed_tokens += n
+            ran.append((rid, n))
+        for rid, n in ran:
+            for s, e, g in traces[rid].after_step(n):
+                events.append(("mask", rid, s, e, g))
+        steps.append(events)
+    return steps, traces
+
+
+def steps_until_closed(prompt_len, num_closed, C, K, group_quotas):
+    """Number of steps a request needs, from its first prefill step, until ``num_closed`` blocks are compacted."""
+    tr = RequestTrace(prompt_len, 1 << 30, C, K, group_quotas)
+    steps = 0
+    while len(tr.compacted_block_ids) < num_closed:
+        n = tr.next_chunk()
+        tr.num_computed_tokens += n
+        tr.after_step(n)
+        steps += 1
+    return steps

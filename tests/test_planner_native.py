@@ -1,0 +1,95 @@
+"""The native compaction planner (host C++) is bit-exact with the oracle restatement of the reference's scheduler /
+KV-manager bookkeeping on seeded multi-request schedules: copy-op batches, truncations, page lists, free-queue
+order, span maps and error results. Host logic only (no GPU)."""
+import numpy as np
+import pytest
+
+from abridgekv_amd.planner import KVPlanner
+from oracle import compaction as oc
+from tests.planner_harness import compare_state, events_to_array, make_schedule, run_native_step, run_oracle_step
+
+SMALL = dict(C=8, K=4, quotas=(4, 2, 1, 2))          # the reference test's toy geometry (4 groups)
+SERVED = dict(C=512, K=256, quotas=(256, 64, 64, 128, 128, 128))
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("geom,block", [(SMALL, 2), (SERVED, 16)])
+def test_native_planner_matches_oracle(seed, geom, block):
+    C, K, quotas = geom["C"], geom["K"], geom["quotas"]
+    n_req = 6 if C == 8 else 4
+    steps, _ = make_schedule(seed, n_req, C, K, quotas, max_prompt=3 * C, max_closed=3)
+    num_blocks = 4000
+    perm = np.random.default_rng(100 + seed).permutation(np.arange(1, num_blocks)).astype(np.int32)
+    oracle = oc.Planner(num_blocks, len(quotas), block, free_order=perm)
+    native = KVPlanner(num_blocks, len(quotas), block, free_order=perm)
+    a_o, a_n = set(), set()
+    total_ops = 0
+    for events in steps:
+        ops_o, tr_o = run_oracle_step(oracle, events, a_o)
+        out_n = run_native_step(native, events, a_n)
+        assert ops_o == out_n.kv_copy_operations
+        assert list(ops_o) == list(out_n.kv_copy_operations), "request order of the op dict differs"
+        assert tr_o == out_n.block_table_truncations
+        assert list(tr_o) == list(out_n.block_table_truncations)
+        total_ops += sum(len(b) for v in ops_o.values() for g in v for b in g)
+        compare_state(oracle, native, sorted(a_o))
+    assert total_ops > 0
+
+
+def test_event_batch_api_matches_step_api():
+    steps, _ = make_schedule(3, 5, 8, 4, (4, 2, 1, 2), max_prompt=20, max_closed=4)
+    perm = np.random.default_rng(0).permutation(np.arange(1, 3000)).astype(np.int32)
+    a = KVPlanner(3000, 4, 2, free_order=perm)
+    b = KVPlanner(3000, 4, 2, free_order=perm)
+    added = set()
+    for events in steps:
+        run_native_step(a, events, added)
+    b.apply_events(events_to_array(steps, 4))
+    assert a.free_queue() == b.free_queue()
+    for rid in sorted(added):
+        assert a.get_blocks(rid) == b.get_blocks(rid)
+        assert a.compacted_counts(rid) == b.compacted_counts(rid)
+
+
+def test_span_errors_match_reference_messages():
+    o = oc.Planner(64, 2, 4)
+    n = KVPlanner(64, 2, 4)
+    for p in (o, n):
+        p.add_request(7)
+        assert p.allocate_slots(7, 10) is not None
+    o.requests[7].num_computed_tokens = 10
+    n.set_num_computed_tokens(7, 10)
+    cases = [(-1, 3, None), (4, 4, None), (2, 11, None), (0, 2, [5]), (0, 10, None)]
+    for s, e, g in cases:
+        ro, rn = o.mask_token_span(7, s, e, g), n.mask_token_span(7, s, e, g)
+        assert not ro.success and not rn.success
+        assert ro.error_message == rn.error_message, (s, e, g)
+    assert o.mask_token_span(7, 2, 5).success and n.mask_token_span(7, 2, 5).success
+    for s, e in [(4, 6), (1, 3)]:                       # overlaps an already-removed span
+        ro, rn = o.mask_token_span(7, s, e), n.mask_token_span(7, s, e)
+        assert not ro.success and ro.error_message == rn.error_message
+    ro, rn = o.mask_token_span(99, 0, 1), n.mask_token_span(99, 0, 1)
+    assert not rn.success and not ro.success
+
+
+def test_allocation_none_when_pool_exhausted():
+    o = oc.Planner(9, 2, 4)
+    n = KVPlanner(9, 2, 4)
+    for p in (o, n):
+        p.add_request(1)
+        assert p.allocate_slots(1, 16) is not None        # 4 pages x 2 groups = 8 = all free pages
+        assert p.allocate_slots(1, 17) is None
+    assert o.pool.free_queue.order() == n.free_queue() == []
+
+
+def test_free_request_returns_pages_in_reverse_group_order():
+    o = oc.Planner(40, 3, 4)
+    n = KVPlanner(40, 3, 4)
+    for p in (o, n):
+        p.add_request(1)
+        p.add_request(2)
+        p.allocate_slots(1, 9)
+        p.allocate_slots(2, 5)
+    o.free_request(1)
+    n.free(1)
+    assert o.pool.free_queue.order() == n.free_queue()
