@@ -1,0 +1,214 @@
+"""Synthetic serving states of the abridged cache, built through the compaction planner.
+
+A request with prompt length P that has produced content tokens up to T-1 (the decode query is content token T-1)
+went through this history (processor semantics, third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py):
+one prefill step per prompt chunk (a chunk ends at a block boundary), one decode step per response token, and after
+every full block of C=512 content tokens one code step of K_max=256 rows followed by compaction of that block
+(response rows in every group, code slots [q, K) per quota). The builder replays every request's history through the
+native planner as scheduler events -- all requests interleaved step by step, allocations of a step in request order
+before its compactions -- so page tables, free-queue order and compacted counts are exactly what the reference's
+scheduler would produce for that arrival pattern. Steps where no group needs a new page and nothing is compacted are
+folded into the next event (allocation depends only on the token totals), which keeps 256 x 32K-token histories
+cheap to replay.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from .planner import KVPlanner
+
+BLOCK_C = 512
+CODES_K_MAX = 256
+PAGE = 16
+
+# Per-layer code quotas of the per-layer arm (results/schedules/sched_trunc_perlayer_mean128.json, one quota per
+# layer: every head of a layer carries the same value).
+QWEN3_4B_LAYER_QUOTAS = (
+    256, 64, 64, 64, 64, 64, 64, 128, 64, 128, 64, 128, 128, 128, 128, 256, 128, 128,
+    256, 128, 256, 256, 128, 128, 256, 128, 128, 128, 128, 128, 64, 64, 64, 128, 128, 64,
+)
+
+
+def quota_groups(layer_quotas):
+    """KV-cache groups of a per-layer quota model: layers bucketed by quota in first-appearance order, each bucket
+    split into equal groups with layers[i::n] (third_party/vllm_overlay/vllm/v1/core/kv_cache_utils.py:1001-1052,
+    1216-1226). Returns (layers per group, quota per group)."""
+    buckets: dict[int, list[int]] = {}
+    for layer, q in enumerate(layer_quotas):
+        buckets.setdefault(int(q), []).append(layer)
+    sizes = [len(v) for v in buckets.values()]
+    group_size = max(sizes) if max(sizes) < min(sizes) * 1.25 else min(sizes)
+    groups, quotas = [], []
+    for q, layers in buckets.items():
+        n = -(-len(layers) // group_size)
+        for i in range(n):
+            groups.append(layers[i::n])
+            quotas.append(q)
+    return groups, quotas
+
+
+def rows_per_group(T, P, quota, C=BLOCK_C):
+    """Physical rows of a group at the decode query (content token T-1, counted): prompt rows, q rows per closed
+    block, the open block."""
+    nb = (T - 1) // C
+    return min(P, nb * C) + nb * quota + (T - nb * C)
+
+
+def request_history(T, P, group_quotas, C=BLOCK_C, K=CODES_K_MAX):
+    """Planner-relevant events of one request, in its own step numbering, up to (excluding) the decode step of
+    content token T-1. Returns (list of (step, kind, a, b, group_mask)), number of steps)."""
+    G = len(group_quotas)
+    compacted = [0] * G
+    computed = 0
+    pending = 0                      # tokens scheduled since the last emitted allocation
+    events = []
+    step = 0
+    c = 0                            # content tokens computed
+    target = T - 1
+    while c < target:
+        b = c // C
+        block_end = (b + 1) * C
+        if c < P:                    # one prefill step: the prompt chunk up to the block end
+            n = min(P, block_end, target) - c
+            events.append((step, "alloc", pending + n, 0, 0))
+            pending = 0
+            computed += n
+            c += n
+            step += 1
+        else:                        # decode steps of the response tokens of this block (folded)
+            n = min(block_end, target) - c
+            # steps i (0-based) where group g needs a new page: (computed + i - compacted_g) % 16 == 0
+            act0 = np.asarray([computed - compacted[g] for g in range(G)])
+            i = np.arange(n)
+            need = np.zeros(n, bool)
+            for g in range(G):
+                need |= (act0[g] + i) % PAGE == 0
+            for off in np.flatnonzero(need).tolist():
+                events.append((step + off, "alloc", pending + off + 1, 0, 0))
+                pending = -(off + 1)
+            pending += n
+            computed += n
+            c += n
+            step += n
+        if c == block_end and c <= target:
+            # code step: all K rows of the block's codes in one step, then compaction of the block
+            events.append((step, "alloc", pending + K, 0, 0))
+            pending = 0
+            code_start = computed
+            computed += K
+            resp_lo = max(P, b * C)
+            if resp_lo < block_end:  # response content of the block, logical [b*(C+K) + ..)
+                ls = b * (C + K) + (resp_lo - b * C)
+                le = b * (C + K) + C
+                events.append((step, "mask", ls, le, -1))
+                for g in range(G):
+                    compacted[g] += le - ls
+            for q in sorted(set(group_quotas)):
+                if q >= K:
+                    continue
+                mask = sum(1 << g for g, gq in enumerate(group_quotas) if gq == q)
+                events.append((step, "mask", code_start + q, code_start + K, mask))
+                for g, gq in enumerate(group_quotas):
+                    if gq == q:
+                        compacted[g] += K - q
+            step += 1
+    if pending:
+        events.append((step - 1, "tail", pending, 0, 0))
+    return events, step
+
+
+@dataclass
+class DecodeState:
+    """Per-group decode metadata of a batch at its next decode step (query = content token T-1 of every request)."""
+    T: np.ndarray                    # [B] content tokens incl. the query
+    P: np.ndarray                    # [B] prompt lengths
+    groups: list                     # layers per group
+    group_quotas: list               # quota per group
+    layer_group: np.ndarray          # [num_layers] group of each layer
+    layer_slot: np.ndarray           # [num_layers] index of the layer inside its group (= shared tensor index)
+    block_tables: list               # per group [B, W] int32
+    seq_lens: list                   # per group [B] int32 (rows incl. the query)
+    slots: list                      # per group [B] int64: slot of the query token
+    num_pages: int
+    planner: KVPlanner
+
+    @property
+    def num_layers(self):
+        return len(self.layer_group)
+
+    def rows(self, layer):
+        return self.seq_lens[self.layer_group[layer]]
+
+    def kv_bytes_per_step(self):
+        """Algorithmic K+V bytes one decode step streams over all layers (4096 B per row per layer)."""
+        return int(sum(int(self.rows(l).astype(np.int64).sum()) for l in range(self.num_layers)) * 4096)
+
+
+def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_pages=1024, C=BLOCK_C,
+                       K=CODES_K_MAX) -> DecodeState:
+    """Replay every request's history through a planner over a pool sized for the batch, then schedule the decode
+    step (one token per request). Requests arrive staggered so that all reach their query at the same step."""
+    T = np.asarray(T, np.int64)
+    P = np.minimum(np.asarray(P, np.int64), T - 1)
+    B = T.size
+    groups, gq = quota_groups(layer_quotas)
+    G = len(groups)
+    histories = [request_history(int(t), int(p), gq, C, K) for t, p in zip(T, P)]
+    S = max(h[1] for h in histories)
+    pages_needed = 0
+    for t, p in zip(T, P):
+        for q in gq:
+            # peak pages of a group: the open block's rows plus one code run before compaction
+            pages_needed += -(-(rows_per_group(int(t), int(p), q, C) + K) // PAGE) + 1
+    num_pages = pages_needed + slack_pages + 1
+    free_order = np.random.default_rng(seed).permutation(np.arange(1, num_pages)).astype(np.int32)
+    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
+    rows = []
+    for r, (evs, n_steps) in enumerate(histories):
+        start = S - n_steps
+        rows.append((start, -1, r, -1, (0, r, 0, 0, 0, 0)))            # the request arrives
+        for k, (st, kind, a, b, m) in enumerate(evs):
+            if kind == "mask":
+                rows.append((start + st, 1, r, k, (2, r, a, b, m, 0)))
+            else:                                                       # "alloc" or the folded "tail" tokens
+                rows.append((start + st, 0, r, k, (1, r, a, 0, 0, 0)))
+    rows.sort(key=lambda x: x[:4])                                      # step, allocations before compactions
+    planner.apply_events(np.asarray([x[4] for x in rows], np.int64))
+    # the decode step itself: one token per request
+    step_ev = np.array([(1, r, 1, 0, 0, 0) for r in range(B)], np.int64)
+    planner.apply_events(step_ev)
+    W = 0
+    seq_lens, tables, slots = [], [], []
+    for g in range(G):
+        sl = np.array([planner.num_computed_tokens(r) - planner.compacted_counts(r)[g] for r in range(B)], np.int32)
+        seq_lens.append(sl)
+    W = int(max(-(-s.max() // PAGE) for s in seq_lens))
+    for g in range(G):
+        tab = planner.fill_block_table(list(range(B)), g, W)
+        tables.append(tab)
+        pos = seq_lens[g].astype(np.int64) - 1
+        slots.append(tab[np.arange(B), pos // PAGE].astype(np.int64) * PAGE + pos % PAGE)
+    layer_group = np.zeros(len(layer_quotas), np.int64)
+    layer_slot = np.zeros(len(layer_quotas), np.int64)
+    for g, layers in enumerate(groups):
+        for i, l in enumerate(layers):
+            layer_group[l], layer_slot[l] = g, i
+    return DecodeState(T, P, groups, gq, layer_group, layer_slot, tables, seq_lens, slots, num_pages, planner)
+
+
+def saturated_decode_lengths(B=256, seed=0, t_range=(2048, 32768), p_range=(128, 1024)):
+    """Config of the saturated serving stress: total lengths T ~ U[2048, 32768] (32K cap), prompts ~ U[128, 1024]."""
+    rng = np.random.default_rng(seed)
+    T = rng.integers(t_range[0], t_range[1] + 1, B)
+    P = np.minimum(rng.integers(p_range[0], p_range[1] + 1, B), T - 1)
+    return T, P
+
+
+def full_model_decode_lengths(B=64, seed=0, prompt=512, closed_generated=32):
+    """Full-model decode: 512-token prompt, 32 generated closed blocks, open block of U[1, 511] tokens."""
+    rng = np.random.default_rng(seed)
+    L = rng.integers(1, 512, B)
+    T = prompt + closed_generated * BLOCK_C + L
+    return T, np.full(B, prompt)
