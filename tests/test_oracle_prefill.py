@@ -1,0 +1,124 @@
+"""Pins of oracle.prefill: the two reference mask forms agree, a per-element predicate written from the prose rule
+agrees, L=1 analogues of the reference's spot checks hold, and the fp64 attention reduces to textbook cases."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import scipy.special as sp
+
+from oracle import prefill as op
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def brute(C, K, N, prompt_len=None, quota=None):
+    """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
+    (code query & code key & same block); a code key with slot >= quota is hidden."""
+    per = C + K
+    S = N * per
+    m = np.zeros((S, S), bool)
+    for q in range(S):
+        qb, qw = divmod(q, per)
+        for k in range(S):
+            kb, kw = divmod(k, per)
+            k_content = kw < C
+            vis = (k_content and kb == qb) or ((not k_content) and kb < qb)
+            if prompt_len is not None and k_content and kb * C + kw < prompt_len:
+                vis = True
+            vis = vis and k <= q
+            if qw >= C and not k_content and kb == qb:
+                vis = True
+            if quota is not None and not k_content and kw - C >= quota:
+                vis = False
+            m[q, k] = vis
+    return m
+
+
+@pytest.mark.parametrize("C,K,N", [(4, 4, 3), (8, 2, 2), (4, 1, 4), (2, 4, 3)])
+def test_arith_equals_role_equals_brute(C, K, N):
+    a = op.arith_mask(C, K, N)
+    r = op.role_mask(C, K, N)
+    assert np.array_equal(a, r)
+    assert np.array_equal(a, brute(C, K, N))
+    pl = [0, 3, C + 1, N * C]
+    ap = op.arith_mask(C, K, N, prompt_len=pl)
+    assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl))
+    for b, p in enumerate(pl):
+        assert np.array_equal(ap[b], brute(C, K, N, prompt_len=p))
+
+
+def test_head_quotas_compose_with_base_mask():
+    """scripts/test_sft_head_code_quotas.py:175-197 rule (L=1): masked(h) == base & key_allowed(h), with per-query-head
+    quotas from the 2x2 fixture expanded over the GQA group (kv head quota repeated for its query heads)."""
+    quotas = json.loads((GOLDEN / "head_code_quotas_2x2.json").read_text())["head_code_quotas"]
+    C, K, N = 4, 4, 3
+    base = op.arith_mask(C, K, N)
+    for layer_q in quotas:
+        per_q_head = np.repeat(layer_q, 2)                          # 2 KV heads -> 4 query heads
+        got = op.arith_mask(C, K, N, head_quota=per_q_head)
+        assert np.array_equal(got, op.role_mask(C, K, N, head_quota=per_q_head))
+        for h, q in enumerate(per_q_head):
+            assert np.array_equal(got[h], brute(C, K, N, quota=q))
+            assert np.array_equal(got[h] & ~base, np.zeros_like(base))
+    pl = [5, 2]
+    got = op.arith_mask(C, K, N, prompt_len=pl, head_quota=[1, 1, 3, 3])
+    assert got.shape == (2, 4, N * (C + K), N * (C + K))
+    assert np.array_equal(got, op.role_mask(C, K, N, prompt_len=pl, head_quota=[1, 1, 3, 3]))
+
+
+def test_spot_checks_l1():
+    """L=1 analogues of the reference's point checks (scripts/test_sft_head_code_quotas.py:201-260)."""
+    C, K, N = 4, 4, 3
+    per = C + K
+    m = op.arith_mask(C, K, N, head_quota=[1, 1, 3, 3])[0]      # head 0, quota 1
+    assert m[per, C]                         # block-1 content sees block-0 code slot 0
+    assert not m[per, C + 1]                 # ... but not slot 1 (quota 1)
+    assert m[2 * per, C] and m[2 * per, per + C]
+    assert not m[2 * per, per + C + 1]
+    assert not m[C - 1, C]                   # content never sees its own block's codes
+    full = op.arith_mask(C, K, N)
+    assert full[C, C + 3]                    # codes attend to later codes of their block (bidirectional)
+    assert full[C + 3, 0]                    # codes see their own block's content
+    assert not full[per + C, 0]              # ... but not earlier blocks' content (no raw prompt)
+    assert op.arith_mask(C, K, N, prompt_len=[5])[0][per + C, 3]    # raw prompt is visible to everyone later
+
+
+def test_single_block_without_quota_is_causal_on_content():
+    m = op.arith_mask(6, 2, 1)
+    assert np.array_equal(m[:6, :6], np.tril(np.ones((6, 6), bool)))
+
+
+def test_masked_attention_textbook_cases():
+    rng = np.random.default_rng(0)
+    S, D = 12, 16
+    q = rng.standard_normal((S, 4, D))
+    k = rng.standard_normal((S, 2, D))
+    v = rng.standard_normal((S, 2, D))
+    causal = np.tril(np.ones((S, S), bool))
+    out, lse = op.masked_attention_fp64(q, k, v, causal, 0.25)
+    for h in range(4):
+        for i in range(S):
+            s = 0.25 * k[: i + 1, h // 2] @ q[i, h]
+            assert np.isclose(lse[i, h], sp.logsumexp(s))
+            assert np.allclose(out[i, h], sp.softmax(s) @ v[: i + 1, h // 2])
+    eye = np.eye(S, dtype=bool)                                     # one visible key -> its value
+    out, lse = op.masked_attention_fp64(q, k, v, eye, 0.25)
+    assert np.allclose(out[:, 1], v[:, 0]) and np.allclose(out[:, 3], v[:, 1])
+
+
+def closed_form_pairs(C, K, N):
+    """Visible pairs per head when block 0 is the raw prompt: block-b content queries see their block's content
+    causally, b*K earlier codes and (b > 0) the C prompt rows; block-b code queries see their block's C content and K
+    codes, b*K earlier codes and (b > 0) the prompt rows."""
+    n = 0
+    for b in range(N):
+        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0)
+        n += K * C + K * K + K * b * K + (K * C if b else 0)
+    return n
+
+
+@pytest.mark.parametrize("C,K,N", [(8, 4, 3), (16, 4, 5), (512, 128, 16)])
+def test_visible_pair_count(C, K, N):
+    """FLOP accounting of the masked prefill (config 4: N=16 blocks of [512 | 128], 512-token raw prompt)."""
+    assert op.visible_pairs(C, K, N, prompt_len=C) == closed_form_pairs(C, K, N)
