@@ -1,0 +1,329 @@
+// Block-masked teacher-forced attention (the compression mask) for gfx950.
+//
+// Replaces the FlexAttention call of CompressLM.forward (abridgekv/compress_forward.py:1134-1230) for the production
+// configuration (L=1, full code<->code attention, no replay / raw / retained tails), whose mask is the closed form
+// _arith_mask_mod (abridgekv/compress_forward.py:695-727) plus the per-query-head code quota (:725-726,
+// _quota_key_allowed :230-236). Sequence layout: N blocks of [C content | K codes], S0 = N * (C + K):
+//   visible(q, kv) = (kv <= q) & (own-block content | earlier blocks' codes | raw-prompt content)
+//                  | (code query & code key & same block),     and a code key needs slot < quota[head].
+//
+// Work decomposition: one workgroup of 4 waves per (sequence, KV head, 64-row query tile). Wave w owns query rows
+// q0 + 16w .. +16 for all 4 query heads of the KV head: 64 MFMA columns (column = head u x row), so one K operand
+// feeds 4 heads. Key tiles of 64 are staged in LDS (rows padded to 272 B: conflict-free 16-byte reads).
+// Each LDS tile is consumed in two halves of 32 keys (keeps the score accumulators at 32 VGPRs):
+//   S^T[32 keys x 64 cols]   = K . Q^T            2 key sub-tiles x 4 heads x 4 dim steps, MFMA 16x16x32 bf16
+//   online softmax (exp2 domain, lazy rescale: the running max moves only when a column max exceeds it by > 8)
+//   O^T[128 dims x 64 cols] += V^T . P^T          8 dim tiles x 4 heads; V^T by v_perm transposes in registers
+// Tiles are classified per workgroup from the mask arithmetic when C and K are multiples of 64: empty tiles are
+// skipped without loading, full tiles run unmasked, partial tiles evaluate the mask per element. Unaligned shapes run
+// every tile as partial (correct, slower).
+#include "common.h"
+
+namespace abkv {
+
+constexpr int kBM = 64;                  // query rows per workgroup
+constexpr int kBN = 64;                  // keys per tile
+constexpr int kLdsStride = kHeadDim + 8; // 136 bf16 = 272 B per LDS row
+
+struct PrefillArgs {
+  const __bf16* q;  long q_sb, q_ss, q_sh;   // [B, S0, 32, 128]
+  const __bf16* k;  long k_sb, k_ss, k_sh;   // [B, S0, 8, 128]
+  const __bf16* v;  long v_sb, v_ss, v_sh;
+  int B, S0, C, K, N;
+  const int32_t* prompt_len;                 // [B] raw-prompt content tokens (nullptr: none)
+  const int32_t* head_quota;                 // [32] code slots visible per query head (nullptr: all K)
+  float scale_log2;
+  __bf16* out;      long o_sb, o_ss, o_sh;   // [B, S0, 32, 128]
+  float* lse;                                // [B, 32, S0] natural log, or nullptr
+  int aligned;                               // C % 64 == 0 && K % 64 == 0
+  int num_q_tiles;
+};
+
+// Element visibility (the closed-form mask), used on partial tiles.
+__device__ __forceinline__ bool visible(int q, int kv, int C, int per, int plen, int quota) {
+  const int qb = q / per, kb = kv / per;
+  const int qw = q - qb * per, kw = kv - kb * per;
+  const bool kc = kw < C;
+  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen);
+  v = v && kv <= q;
+  v = v || (qw >= C && !kc && kb == qb);
+  return v && (kc || kw - C < quota);
+}
+
+// Tile class for an aligned layout: 0 empty, 1 full, 2 partial.
+__device__ __forceinline__ int classify(int q0, int k0, int C, int per, int plen, int qmin, int qmax) {
+  const int qb = q0 / per, kb = k0 / per;
+  const int qw0 = q0 - qb * per, kw0 = k0 - kb * per;
+  const bool q_code = qw0 >= C;
+  if (kw0 < C) {                                            // content keys
+    if (kb == qb) {
+      if (q_code) return 1;
+      if (k0 + kBN - 1 <= q0) return 1;
+      if (k0 > q0 + kBM - 1) return 0;
+      return 2;
+    }
+    if (kb < qb) {
+      const int a0 = kb * C + kw0;
+      if (a0 + kBN <= plen) return 1;
+      if (a0 >= plen) return 0;
+      return 2;
+    }
+    return 0;
+  }
+  const bool structural = kb < qb || (kb == qb && q_code);  // code keys
+  if (!structural) return 0;
+  const int slot0 = kw0 - C;
+  if (slot0 + kBN <= qmin) return 1;
+  if (slot0 >= qmax) return 0;
+  return 2;
+}
+
+__device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[kBN * kLdsStride];
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[kBN * kLdsStride];
+
+  // heavier (later) query tiles first
+  const int qt = a.num_q_tiles - 1 - blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int m16 = lane & 15;
+  const int j = lane >> 4;
+  const int per = a.C + a.K;
+  const int q0 = qt * kBM;
+  const int qrow = q0 + 16 * w + m16;                       // this lane's query row (MFMA column)
+  const int plen = a.prompt_len ? a.prompt_len[b] : 0;
+  int quota[4];
+  int qmin = 1 << 30, qmax = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    quota[u] = a.head_quota ? a.head_quota[kvh * kGroup + u] : a.K;
+    qmin = min(qmin, quota[u]);
+    qmax = max(qmax, quota[u]);
+  }
+
+  // Q^T operands: column (head u, row qrow), dims 8*(4i+j) .. +8 for dim step i.
+  bf16x8 qop[4][4];
+  {
+    const bool ok = qrow < a.S0;
+    const __bf16* qb = a.q + (long)b * a.q_sb + (long)min(qrow, a.S0 - 1) * a.q_ss;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x4 x = ld16g(qb + (long)(kvh * kGroup + u) * a.q_sh + 8 * (4 * i + j));
+        if (!ok) x = u32x4{0, 0, 0, 0};
+        qop[u][i] = __builtin_bit_cast(bf16x8, x);
+      }
+  }
+
+  floatx4 o[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[i][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    m_run[u] = -INFINITY;
+    l_run[u] = 0.f;
+  }
+
+  const long kbase = (long)b * a.k_sb + (long)kvh * a.k_sh;
+  const long vbase = (long)b * a.v_sb + (long)kvh * a.v_sh;
+  const int n_k_tiles = (a.S0 + kBN - 1) / kBN;
+  const int q_last = min(q0 + kBM, a.S0) - 1;
+  for (int kt = 0; kt < n_k_tiles; ++kt) {
+    const int k0 = kt * kBN;
+    int cls;
+    if (a.aligned) {
+      cls = classify(q0, k0, a.C, per, plen, qmin, qmax);
+    } else {
+      // unaligned: keys past the query tile's last row are visible only as same-block codes of a code query
+      const int qb_hi = q_last / per;
+      const int kb_lo = k0 / per;
+      cls = (k0 <= q_last || kb_lo <= qb_hi) ? 2 : 0;
+    }
+    if (cls == 0) continue;
+
+    // stage K and V tiles: 64 keys x 256 B each, 16 threads per key row
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int c = tid + 256 * x;
+      const int key = c >> 4, col = (c & 15) * 8;
+      const int kv = k0 + key;
+      u32x4 kk = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
+      if (kv < a.S0) {
+        kk = ld16g(a.k + kbase + (long)kv * a.k_ss + col);
+        vv = ld16g(a.v + vbase + (long)kv * a.v_ss + col);
+      }
+      *reinterpret_cast<u32x4*>(&Ks[key * kLdsStride + col]) = kk;
+      *reinterpret_cast<u32x4*>(&Vs[key * kLdsStride + col]) = vv;
+    }
+    __syncthreads();
+
+    // Two halves of 32 keys: key step kk covers tile keys 32kk + {16t' + 4j + r}, t' in {0, 1}.
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      // S^T = K . Q^T for 32 keys: s[t][u][r] is key k0 + 32kk + 16t + 4j + r, column (head u, row qrow)
+      floatx4 s[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const bf16x8 kop = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(&Ks[(32 * kk + 16 * t + m16) * kLdsStride + 8 * (4 * i + j)]));
+#pragma unroll
+          for (int u = 0; u < 4; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
+        }
+
+      float tmax[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = s[t][u][r] * a.scale_log2;
+            if (cls == 2) {
+              const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
+              const bool ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
+              x = ok ? x : -INFINITY;
+            }
+            s[t][u][r] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = fmaxf(mx, xor_shfl(mx, 16));
+        mx = fmaxf(mx, xor_shfl(mx, 32));
+        tmax[u] = mx;
+      }
+      // lazy rescale: move the running max only when a column's max grows by more than 8 (2^8 headroom in P)
+      bool need = false;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) need |= tmax[u] > m_run[u] + 8.f;
+      if (__any(need)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float m_new = fmaxf(m_run[u], tmax[u]);
+          const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+          m_run[u] = m_new;
+          l_run[u] *= alpha;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
+        }
+      }
+      bf16x8 pop[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
+        float ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = fast_exp2(s[t][u][r] - m_use);
+            s[t][u][r] = p;
+            ps += p;
+          }
+        l_run[u] += ps;
+        u32x4 pw;
+        pw[0] = pack_bf16x2(s[0][u][0], s[0][u][1]);
+        pw[1] = pack_bf16x2(s[0][u][2], s[0][u][3]);
+        pw[2] = pack_bf16x2(s[1][u][0], s[1][u][1]);
+        pw[3] = pack_bf16x2(s[1][u][2], s[1][u][3]);
+        pop[u] = __builtin_bit_cast(bf16x8, pw);
+      }
+
+      // O^T += V^T . P^T over the same 32 keys (P^T row e: e<4 -> key 32kk+4j+e, e>=4 -> key 32kk+16+4j+e-4)
+      u32x4 vr[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vr[e] = *reinterpret_cast<const u32x4*>(&Vs[(32 * kk + 4 * j + e) * kLdsStride + 8 * m16]);
+        vr[4 + e] = *reinterpret_cast<const u32x4*>(&Vs[(32 * kk + 16 + 4 * j + e) * kLdsStride + 8 * m16]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x05040100u);
+          hi[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x07060302u);
+        }
+        const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
+          o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
+        }
+      }
+    }
+  }
+
+  if (qrow >= a.S0) return;
+  // o[i][u][r] = un-normalised out[row qrow][head u][dim 32j + 8r + i]
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float l = l_run[u] + xor_shfl(l_run[u], 16);
+    l += xor_shfl(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int head = kvh * kGroup + u;
+    __bf16* oh = a.out + (long)b * a.o_sb + (long)qrow * a.o_ss + (long)head * a.o_sh + 32 * j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      u32x4 wv;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wv[c] = pack_bf16x2(o[2 * c][u][r] * inv, o[2 * c + 1][u][r] * inv);
+      *reinterpret_cast<u32x4*>(oh + 8 * r) = wv;
+    }
+    if (a.lse != nullptr && j == 0)
+      a.lse[((long)b * kHeadsQ + head) * a.S0 + qrow] =
+          l > 0.f ? (m_run[u] + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+  }
+}
+
+}  // namespace abkv
+
+extern "C" {
+
+int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
+                             long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
+                             long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
+                             int seq_len, const int32_t* prompt_len, const int32_t* head_quota, float scale,
+                             void* out, long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
+                             hipStream_t stream) {
+  using namespace abkv;
+  if (batch <= 0 || seq_len <= 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
+      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k))
+    return (int)hipErrorInvalidValue;
+  PrefillArgs a;
+  a.q = static_cast<const __bf16*>(q);
+  a.q_sb = q_stride_b; a.q_ss = q_stride_s; a.q_sh = q_stride_h;
+  a.k = static_cast<const __bf16*>(k);
+  a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.k_sh = k_stride_h;
+  a.v = static_cast<const __bf16*>(v);
+  a.v_sb = v_stride_b; a.v_ss = v_stride_s; a.v_sh = v_stride_h;
+  a.B = batch; a.S0 = seq_len; a.C = block_c; a.K = codes_k; a.N = num_blocks;
+  a.prompt_len = prompt_len;
+  a.head_quota = head_quota;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = static_cast<__bf16*>(out);
+  a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;
+  a.lse = lse;
+  a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
+  a.num_q_tiles = (seq_len + kBM - 1) / kBM;
+  hipLaunchKernelGGL(prefill_masked_kernel, dim3(a.num_q_tiles, kHeadsKV, batch), dim3(256), 0, stream, a);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

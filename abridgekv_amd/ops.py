@@ -187,5 +187,44 @@ def slot_mapping(req_idx: torch.Tensor, positions: torch.Tensor, block_table: to
     return out
 
 
+def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_c: int, codes_k: int,
+                             num_blocks: int, prompt_len: torch.Tensor | None = None,
+                             head_quota: torch.Tensor | None = None, scale: float | None = None,
+                             out: torch.Tensor | None = None, lse: torch.Tensor | None = None):
+    """Teacher-forced attention under the compression mask (N blocks of [C content | K codes]).
+
+    q [B, S0, 32, 128], k/v [B, S0, 8, 128] bf16 (any strides with contiguous dims, e.g. the [B, H, S, D]
+    transposed views HF attention receives, permuted back); prompt_len [B] int32 raw-prompt content tokens;
+    head_quota [32] int32 code slots visible per query head. Returns (out [B, S0, 32, 128] bf16,
+    lse [B, 32, S0] fp32 natural log or None).
+    """
+    B, S0 = q.shape[0], q.shape[1]
+    _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
+    for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
+        _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
+                 and t.stride(3) == 1, f"{name} must be cuda bf16 [B, S0, {h}, {HEAD_DIM}] with contiguous dims")
+    if prompt_len is not None:
+        _require(prompt_len.is_cuda and prompt_len.dtype == torch.int32 and prompt_len.numel() == B
+                 and prompt_len.is_contiguous(), "prompt_len must be contiguous cuda int32 [B]")
+    if head_quota is not None:
+        _require(head_quota.is_cuda and head_quota.dtype == torch.int32 and head_quota.numel() == HEADS_Q
+                 and head_quota.is_contiguous(), "head_quota must be contiguous cuda int32 [32]")
+    if out is None:
+        out = torch.empty((B, S0, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (B, S0, HEADS_Q, HEAD_DIM) and out.stride(3) == 1,
+             "out must be bf16 [B, S0, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, HEADS_Q, S0),
+                 "lse must be contiguous fp32 [B, 32, S0]")
+    scale = default_scale() if scale is None else float(scale)
+    rc = lib().abkv_prefill_masked_attn(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
+                                        k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2), B,
+                                        block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota), scale,
+                                        _ptr(out), out.stride(0), out.stride(1), out.stride(2), _ptr(lse),
+                                        C.c_void_p(_stream()))
+    check(rc, "abkv_prefill_masked_attn")
+    return out, lse
+
+
 def default_scale() -> float:
     return 1.0 / math.sqrt(HEAD_DIM)

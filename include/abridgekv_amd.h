@@ -72,6 +72,22 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
                       abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * Block-masked teacher-forced attention (kernel 3).
+ * Replaces the FlexAttention call of CompressLM.forward (abridgekv/compress_forward.py:1134-1230) with the mask of
+ * _arith_mask_mod (abridgekv/compress_forward.py:695-727) and the per-query-head code quota (:725-726, :230-236):
+ * layout N blocks of [block_c content | codes_k codes], seq_len = N * (block_c + codes_k).
+ * q [batch, seq_len, 32, 128], k/v [batch, seq_len, 8, 128], out [batch, seq_len, 32, 128] bf16 with element strides
+ * (dims contiguous); prompt_len [batch] int32 raw-prompt content tokens (NULL: none); head_quota [32] int32 code slots
+ * visible per query head (NULL: all); lse [batch, 32, seq_len] fp32 natural log (NULL: not written).
+ * ------------------------------------------------------------------------------------------------------------- */
+int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
+                             long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
+                             long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
+                             int seq_len, const int32_t* prompt_len, const int32_t* head_quota, float scale,
+                             void* out, long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
+                             abkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager
  * bookkeeping: Scheduler.mask_token_span (third_party/vllm_overlay/vllm/v1/core/sched/scheduler.py:2060-2204),
  * SingleTypeKVCacheManager.compact_kv_cache_span/_truncate_compacted_blocks/allocate_new_blocks/free

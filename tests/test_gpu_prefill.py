@@ -1,0 +1,87 @@
+"""Block-masked teacher-forced attention on the GPU vs the fp64 oracle under the arithmetic compression mask
+(tolerance: max-abs <= 2e-2 for bf16 outputs and LSE)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import prefill as op
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _bf16(x):
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
+
+
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None):
+    from abridgekv_amd import ops
+    S0 = N * (C + K)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    pl = None if prompt_len is None else torch.tensor(prompt_len, dtype=torch.int32, device=dev)
+    hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
+                                          lse=lse)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    worst = 0.0
+    for b in range(B):
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota)
+        if prompt_len is not None:
+            mask = mask[0]
+        sel = slice(None) if rows is None else rows
+        ref_o, ref_l = op.masked_attention_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(),
+                                                mask, 128 ** -0.5)
+        worst = max(worst, float(np.abs(out[b][sel] - ref_o[sel]).max()),
+                    float(np.abs(lse[b].T[sel] - ref_l[sel]).max()))
+    assert worst <= TOL, worst
+
+
+def test_aligned_tiles_no_prompt():
+    _check(C=128, K=64, N=3, B=1)
+
+
+def test_aligned_tiles_prompt_straddles_tiles():
+    _check(C=128, K=64, N=4, B=3, prompt_len=[0, 150, 320], seed=1)
+
+
+def test_aligned_tiles_head_quotas():
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()       # per KV head, expanded to its 4 q heads
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=2)
+
+
+def test_unaligned_small_blocks():
+    """C=8, K=4: every tile takes the per-element mask path; S0=60 leaves a partial query and key tile."""
+    quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+    _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=3)
+
+
+def test_config4_shape_sampled_rows():
+    """Config-4 block geometry (C=512, K=128) with 4 blocks; rows sampled across blocks and regions."""
+    rows = np.r_[0:70, 500:700, 1250:1300, 2400:2560]
+    _check(C=512, K=128, N=4, B=1, prompt_len=[512], rows=rows, seed=4)
+
+
+def test_strided_hf_layout():
+    """Inputs as HF hands them to an attention function: [B, H, S, D] views of [B, S, H, D] storage, passed back as
+    [B, S, H, D] permutations (non-contiguous strides)."""
+    from abridgekv_amd import ops
+    C, K, N, B = 64, 64, 2, 2
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q_bhsd = torch.randn((B, 32, S0, 128), generator=g, device=dev).to(torch.bfloat16)
+    k_bhsd = torch.randn((B, 8, S0, 128), generator=g, device=dev).to(torch.bfloat16)
+    v_bhsd = torch.randn((B, 8, S0, 128), generator=g, device=dev).to(torch.bfloat16)
+    out, _ = ops.prefill_masked_attention(q_bhsd.transpose(1, 2), k_bhsd.transpose(1, 2), v_bhsd.transpose(1, 2),
+                                          C, K, N)
+    ref, _ = ops.prefill_masked_attention(q_bhsd.transpose(1, 2).contiguous(), k_bhsd.transpose(1, 2).contiguous(),
+                                          v_bhsd.transpose(1, 2).contiguous(), C, K, N)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
