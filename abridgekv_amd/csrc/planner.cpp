@@ -93,6 +93,7 @@ struct GroupStep {
   std::vector<std::vector<Op>> batches;   // reference-format ordered op batches
   std::vector<int32_t> blocks_before;     // page list before the step's first removal
   std::vector<Removal> removals;
+  bool stale = false;                     // a removal followed an allocation that followed a removal (no take)
 };
 
 struct Request {
@@ -102,6 +103,7 @@ struct Request {
   std::vector<GroupStep> step;            // per group, cleared by take_step_outputs
   bool has_trunc = false;
   std::vector<int32_t> trunc;
+  bool alloc_after_removal = false;       // an allocation happened while removals were pending
 };
 
 struct Planner {
@@ -255,6 +257,8 @@ int abkv_planner_allocate_slots(void* h, int64_t rid, int64_t num_new_tokens) {
   for (int g = 0; g < p->num_groups; ++g)
     total += p->cdiv(need - r->spans[g].total, p->block_size) - (int64_t)r->blocks[g].size();
   if (total > (int64_t)p->free_q.size()) return 0;
+  for (auto& st : r->step)
+    if (!st.removals.empty()) r->alloc_after_removal = true;
   for (int g = 0; g < p->num_groups; ++g) {
     const int64_t num_new = p->cdiv(need - r->spans[g].total, p->block_size) - (int64_t)r->blocks[g].size();
     if (num_new <= 0) continue;
@@ -333,6 +337,7 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
     }
     if (!blocks.empty()) {
       if (st.removals.empty()) st.blocks_before = blocks;
+      else if (r->alloc_after_removal) st.stale = true;
       st.removals.push_back({pl.ps, pl.pe, pl.active});
       const int64_t removed = pl.pe - pl.ps;
       std::vector<abkv::Op> ops;
@@ -414,6 +419,13 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   if (!p) return ABKV_ERR_ARG;
   int64_t need_ops = 0, need_trunc = 0, need_fused = 0;
   abkv_planner_pending_sizes(h, &need_ops, &need_trunc, &need_fused);
+  for (int64_t rid : p->trunc_order)
+    for (auto& st : find_req(p, rid)->step)
+      if (st.stale) {
+        p->last_error = "span removals of one step were interleaved with an allocation: take the step outputs "
+                        "once per scheduler step";
+        return ABKV_ERR_ARG;
+      }
   if ((op_rows && need_ops > op_cap) || (trunc_rows && need_trunc > trunc_cap)) return ABKV_ERR_CAPACITY;
   const int G = p->num_groups;
   int64_t k = 0;
@@ -484,6 +496,7 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   for (auto& kv : p->reqs) {
     for (auto& st : kv.second.step) st = abkv::GroupStep();
     kv.second.has_trunc = false;
+    kv.second.alloc_after_removal = false;
   }
   p->pending_order.clear();
   p->trunc_order.clear();

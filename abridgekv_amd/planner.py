@@ -74,6 +74,7 @@ class KVPlanner:
         self.num_blocks, self.num_groups, self.block_size = num_blocks, num_groups, block_size
         self._ids: dict = {}
         self._names: dict = {}
+        self._bufs: dict = {}
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -195,19 +196,39 @@ class KVPlanner:
             return SpanRemovalResult(False, 0, 0, self._err())
         raise RuntimeError(f"mask_token_span failed ({rc}): {self._err()}")
 
-    def take_step_outputs(self) -> StepOutputs:
+    def _buffer(self, name: str, rows: int, cols: int) -> np.ndarray:
+        """Reusable, already-faulted output buffer (grown geometrically) so a step does not pay first-touch costs."""
+        buf = self._bufs.get(name)
+        if buf is None or buf.shape[0] < rows or buf.shape[1] != cols:
+            buf = np.zeros((max(rows, 1, 2 * (0 if buf is None else buf.shape[0])), cols), np.int64)
+            self._bufs[name] = buf
+        return buf
+
+    def reserve_outputs(self, n_ops: int, n_fused: int, n_trunc: int = 1024) -> None:
+        """Pre-size (and fault in) the step-output buffers, e.g. before a timed step."""
+        self._buffer("ops", n_ops, 7).fill(0)
+        self._buffer("fused", n_fused, 6).fill(0)
+        self._buffer("trunc", n_trunc, 1 + self.num_groups).fill(0)
+
+    def take_step_outputs(self, as_arrays: bool = False):
+        """The step's compaction outputs, then cleared. ``as_arrays=True`` returns the raw int64 rows
+        (op_rows [n, 7], trunc_rows [n, 1 + G], fused_moves [n, 6]) as views of reusable buffers, valid until the next
+        call, without building the dict form."""
         n_ops, n_tr, n_fu = C.c_int64(0), C.c_int64(0), C.c_int64(0)
         self._lib.abkv_planner_pending_sizes(self._h, C.byref(n_ops), C.byref(n_tr), C.byref(n_fu))
         G = self.num_groups
-        ops = np.zeros((max(n_ops.value, 1), 7), np.int64)
-        tr = np.zeros((max(n_tr.value, 1), 1 + G), np.int64)
-        fu = np.zeros((max(n_fu.value, 1), 6), np.int64)
+        ops = self._buffer("ops", n_ops.value, 7)
+        tr = self._buffer("trunc", n_tr.value, 1 + G)
+        fu = self._buffer("fused", n_fu.value, 6)
         o1, o2, o3 = C.c_int64(0), C.c_int64(0), C.c_int64(0)
         rc = self._lib.abkv_planner_take_step_outputs(self._h, _i64(ops), ops.shape[0], C.byref(o1), _i64(tr),
                                                       tr.shape[0], C.byref(o2), _i64(fu), fu.shape[0], C.byref(o3))
         if rc != ABKV_OK:
-            raise RuntimeError(f"take_step_outputs failed ({rc})")
+            raise RuntimeError(f"take_step_outputs failed ({rc}): {self._err()}")
         ops, tr, fu = ops[:o1.value], tr[:o2.value], fu[:o3.value]
+        if as_arrays:
+            return ops, tr, fu
+        ops, tr, fu = ops.copy(), tr.copy(), fu.copy()
         kv_ops: dict = {}
         for row in ops:
             rid = self.request_id(int(row[0]))

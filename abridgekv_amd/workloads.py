@@ -119,6 +119,20 @@ def request_history(T, P, group_quotas, C=BLOCK_C, K=CODES_K_MAX):
     return events, step
 
 
+def _schedule_rows(rows):
+    """Order (global step, phase, request, index, event) rows as the scheduler runs them: per step, arrivals and
+    allocations in request order, then the previous step's outputs are taken (they ride on this step's
+    SchedulerOutput), then the step's compactions in request order."""
+    rows = sorted(rows, key=lambda x: x[:4])
+    out, last_step = [], None
+    for step, phase, *_rest in rows:
+        if phase == 1 and step != last_step:
+            out.append((4, 0, 0, 0, 0, 0))
+            last_step = step
+        out.append(_rest[-1])
+    return np.asarray(out, np.int64)
+
+
 @dataclass
 class DecodeState:
     """Per-group decode metadata of a batch at its next decode step (query = content token T-1 of every request)."""
@@ -174,8 +188,7 @@ def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_p
                 rows.append((start + st, 1, r, k, (2, r, a, b, m, 0)))
             else:                                                       # "alloc" or the folded "tail" tokens
                 rows.append((start + st, 0, r, k, (1, r, a, 0, 0, 0)))
-    rows.sort(key=lambda x: x[:4])                                      # step, allocations before compactions
-    planner.apply_events(np.asarray([x[4] for x in rows], np.int64))
+    planner.apply_events(_schedule_rows(rows))
     # the decode step itself: one token per request
     step_ev = np.array([(1, r, 1, 0, 0, 0) for r in range(B)], np.int64)
     planner.apply_events(step_ev)
@@ -212,3 +225,67 @@ def full_model_decode_lengths(B=64, seed=0, prompt=512, closed_generated=32):
     L = rng.integers(1, 512, B)
     T = prompt + closed_generated * BLOCK_C + L
     return T, np.full(B, prompt)
+
+
+def visible_pairs_prompt_block(C, K, N):
+    """Visible (query, key) pairs per head of the teacher-forced mask when block 0 is the raw prompt: block-b content
+    queries see their block's content causally, b*K earlier codes and (b > 0) the C prompt rows; block-b code queries
+    see their block's C content and K codes, b*K earlier codes and (b > 0) the prompt rows."""
+    n = 0
+    for b in range(N):
+        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0)
+        n += K * C + K * K + K * b * K + (K * C if b else 0)
+    return n
+
+
+@dataclass
+class CompactionState:
+    """A batch whose requests all finished the code step of their current block and await its compaction."""
+    planner: KVPlanner
+    groups: list
+    group_quotas: list
+    num_pages: int
+    pending: np.ndarray              # the compaction calls of the step, abkv_planner_apply_events rows
+    prompt_lens: np.ndarray
+    closed_blocks: np.ndarray
+
+    def compact(self, as_arrays: bool = False):
+        """Run the step's span removals (processor order per request: response content in every group, then code
+        slots >= q per quota) and return the step outputs."""
+        self.planner.apply_events(self.pending)
+        return self.planner.take_step_outputs(as_arrays=as_arrays)
+
+
+def build_compaction_state(B=64, seed=0, layer_quotas=QWEN3_4B_LAYER_QUOTAS, C=BLOCK_C, K=CODES_K_MAX,
+                           max_prior_blocks=3, p_range=(128, 1024), slack_pages=1024) -> CompactionState:
+    """Config of the compaction benchmark: every request has closed ``nb`` earlier blocks (seeded in
+    [0, max_prior_blocks]) and has just computed the K code rows of block ``nb``; prompts P ~ U[p_range] (capped so the
+    closing block holds at least one response row)."""
+    rng = np.random.default_rng(seed)
+    nb = rng.integers(0, max_prior_blocks + 1, B)
+    P = rng.integers(p_range[0], p_range[1] + 1, B)
+    P = np.minimum(P, (nb + 1) * C - 1)
+    T = (nb + 1) * C + 1
+    groups, gq = quota_groups(layer_quotas)
+    G = len(groups)
+    histories = [request_history(int(t), int(p), gq, C, K) for t, p in zip(T, P)]
+    S = max(h[1] for h in histories)
+    pages_needed = sum(-(-(int(t) + K) // PAGE) + 1 for t in T) * G
+    num_pages = pages_needed + slack_pages + 1
+    free_order = rng.permutation(np.arange(1, num_pages)).astype(np.int32)
+    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
+    rows, pending = [], []
+    for r, (evs, n_steps) in enumerate(histories):
+        start = S - n_steps
+        rows.append((start, -1, r, -1, (0, r, 0, 0, 0, 0)))
+        for k, (st, kind, a, b, m) in enumerate(evs):
+            if kind == "mask":
+                if st == n_steps - 1:
+                    pending.append((2, r, a, b, m, 0))
+                else:
+                    rows.append((start + st, 1, r, k, (2, r, a, b, m, 0)))
+            else:
+                rows.append((start + st, 0, r, k, (1, r, a, 0, 0, 0)))
+    planner.apply_events(_schedule_rows(rows))
+    planner.take_step_outputs()                              # earlier steps' outputs were executed long ago
+    return CompactionState(planner, groups, gq, num_pages, np.asarray(pending, np.int64), P, nb)

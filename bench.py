@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=32)
-    ap.add_argument("--workload", choices=["saturated", "full_model"], default="saturated")
+    ap.add_argument("--workload", choices=["saturated", "full_model", "prefill", "compaction"], default="saturated")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     return ap.parse_args()
@@ -96,6 +96,106 @@ def cpu_baseline(torch, state, caches_gpu, qs, scale, n_seqs, target_s=12.0):
     return n_seqs / step_time, reps, el
 
 
+def bench_prefill(args, torch):
+    """Config 4: teacher-forced prefill under the compression mask, B=4, N=16 blocks of [512 content | 128 codes]
+    (S0 = 10240), 512-token raw prompt, 32 q / 8 kv heads, d128, bf16. FLOPs = 4 * D * visible pairs * heads * B."""
+    from abridgekv_amd import ops
+    from abridgekv_amd.workloads import visible_pairs_prompt_block
+
+    B, C, K, N, plen = 4, 512, 128, 16, 512
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    pl = torch.full((B,), plen, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    for _ in range(args.warmup):
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / args.steps
+    flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N) * 32 * B
+    tflops = flops / t / 1e12
+    return {
+        "metric": "masked teacher-forced prefill TFLOP/s (visible QK+PV flops); % of bf16 dense MFMA peak",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v from the seed",
+        "config": {"workload": f"masked prefill B={B}, N={N} blocks of [{C} content | {K} codes], S0={S0}, "
+                               f"raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": tflops / 2500.0, "traffic": None, "kernel": "prefill_masked_kernel",
+                     "alg_flops_per_launch": flops, "avg_launch_us": t * 1e6},
+    }
+
+
+def bench_compaction(args, torch):
+    """Config 2: 64 sequences each close one 512-token block (256 code rows computed) in one step; Qwen3-4B shape,
+    36 layers in 6 quota groups, page 16, seeded fragmented free list. Measures the planner (host) and the fused
+    device moves; algorithmic bytes = 2 x (kept code rows x 4096 B) summed over layers."""
+    from abridgekv_amd import ops, worker, workloads
+
+    B = 64
+    st = workloads.build_compaction_state(B, seed=args.seed)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    n_tensors = max(len(g) for g in st.groups)
+    caches = []
+    for _ in range(n_tensors):
+        c = torch.empty(ops.kv_cache_shape(st.num_pages), dtype=torch.bfloat16, device=dev)
+        c.normal_(generator=gen)
+        caches.append(c)
+    by_group = [[caches[i] for i in range(len(layers))] for layers in st.groups]
+    st.planner.reserve_outputs(B * len(st.groups) * 1024, B * len(st.groups) * 2048)
+    t0 = time.perf_counter()
+    op_rows, _, fused = st.compact(as_arrays=True)             # the planner step (host C++), reference semantics
+    plan_s = time.perf_counter() - t0
+    st_ref = workloads.build_compaction_state(B, seed=args.seed)
+    outs = st_ref.compact()                                    # same step, reference-format op dict for comparison
+    ref_rows = len(op_rows)
+    fused = fused.copy()
+    layers_per_group = len(st.groups[0])
+    alg_bytes = 2 * len(fused) * layers_per_group * 4096
+    for _ in range(args.warmup):
+        worker.execute_fused_moves(fused, by_group, check=False)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        worker.execute_fused_moves(fused, by_group, check=False)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / args.steps
+    s.record()
+    for _ in range(args.steps):
+        worker.execute_kv_copy_operations(outs.kv_copy_operations, by_group, check=False)
+    e.record()
+    torch.cuda.synchronize()
+    t_ref = s.elapsed_time(e) / 1e3 / args.steps
+    gbps = alg_bytes / t / 1e9
+    return {
+        "metric": "block-boundary compaction: sequences compacted per second (64 seqs x 36 layers)",
+        "value": B / (t + plan_s), "unit": "sequences/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": (t + plan_s) * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (row copies)", "data": "synthetic histories replayed through the planner",
+        "config": {"workload": "compaction: 64 sequences close a 512-token block (256 code rows), Qwen3-4B 36 layers "
+                               "/ 6 quota groups, page 16, seeded free list", "global_batch": B},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": None, "kernel": "kv_move_kernel (fused moves)",
+                     "alg_bytes_per_launch": alg_bytes / len(st.groups), "avg_launch_us": t / len(st.groups) * 1e6},
+        "planner_ms": plan_s * 1e3, "device_moves_ms": t * 1e3,
+        "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -103,6 +203,11 @@ def main():
               f"head with no exchange, so whole-job throughput at N GPUs is N x the one-GPU figure.", file=sys.stderr)
         return 2
     import torch
+
+    if args.workload in ("prefill", "compaction"):
+        res = (bench_prefill if args.workload == "prefill" else bench_compaction)(args, torch)
+        print(json.dumps(res), flush=True)
+        return 0
 
     from abridgekv_amd import ops, workloads
 
