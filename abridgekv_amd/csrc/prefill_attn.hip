@@ -9,7 +9,8 @@
 //
 // Work decomposition: one workgroup of 4 waves per (sequence, KV head, 64-row query tile). Wave w owns query rows
 // q0 + 16w .. +16 for all 4 query heads of the KV head: 64 MFMA columns (column = head u x row), so one K operand
-// feeds 4 heads. Key tiles of 64 are staged in LDS (rows padded to 272 B: conflict-free 16-byte reads).
+// feeds 4 heads. Key tiles of 64 are DMA'd into double-buffered, XOR-swizzled LDS one visible tile ahead
+// (global_load_lds_dwordx4: no VGPR staging), so loads overlap the previous tile's MFMA work.
 // Each LDS tile is consumed in two halves of 32 keys (keeps the score accumulators at 32 VGPRs):
 //   S^T[32 keys x 64 cols]   = K . Q^T            2 key sub-tiles x 4 heads x 4 dim steps, MFMA 16x16x32 bf16
 //   online softmax (exp2 domain, lazy rescale: the running max moves only when a column max exceeds it by > 8)
@@ -23,7 +24,7 @@ namespace abkv {
 
 constexpr int kBM = 64;                  // query rows per workgroup
 constexpr int kBN = 64;                  // keys per tile
-constexpr int kLdsStride = kHeadDim + 8; // 136 bf16 = 272 B per LDS row
+constexpr int kTileElems = kBN * kHeadDim;
 
 struct PrefillArgs {
   const __bf16* q;  long q_sb, q_ss, q_sh;   // [B, S0, 32, 128]
@@ -80,12 +81,181 @@ __device__ __forceinline__ int classify(int q0, int k0, int C, int per, int plen
 
 __device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-__global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) __bf16 Ks[kBN * kLdsStride];
-  __shared__ __attribute__((aligned(16))) __bf16 Vs[kBN * kLdsStride];
+#define ABKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-  // heavier (later) query tiles first
-  const int qt = a.num_q_tiles - 1 - blockIdx.x;
+// K/V tiles live in LDS as 64 rows x 256 B without padding; 16-byte chunk c of row r is stored at chunk c ^ (r % 16),
+// which makes both operand read patterns conflict-free (16 lanes hit 16 distinct chunks). Tiles are filled with
+// global_load_lds_dwordx4: a wave instruction writes 1 KiB contiguously (lane L -> bytes 16L), so each lane fetches
+// the global chunk that belongs at its swizzled position. Rows past the sequence end re-read the last row (finite data,
+// masked to probability 0).
+__device__ __forceinline__ void issue_tile(const __bf16* kg, long k_ss, const __bf16* vg, long v_ss, int k0, int S0,
+                                           __bf16* Kbuf, __bf16* Vbuf, int w, int lane) {
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int blk = 4 * w + n;                 // 1 KiB block of the 16 KiB tile
+    const int row = 4 * blk + (lane >> 4);
+    const int logical = (lane & 15) ^ (row & 15);
+    const int key = min(k0 + row, S0 - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(kg + (long)key * k_ss + 8 * logical), ABKV_LDS(Kbuf + 512 * blk),
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(vg + (long)key * v_ss + 8 * logical), ABKV_LDS(Vbuf + 512 * blk),
+                                     16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ u32x4 lds16(const __bf16* buf, int row, int chunk) {
+  return *reinterpret_cast<const u32x4*>(buf + row * kHeadDim + 8 * (chunk ^ (row & 15)));
+}
+
+struct TileMask {
+  int mode;        // 0 none, 1 key <= qrow (diagonal), 2 key < limit[u], 3 general (per-element arithmetic)
+  int limit[4];
+};
+
+// Attention of this wave's 64 columns against one 64-key tile held in (Kbuf, Vbuf).
+__device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* Vbuf, const bf16x8 (&qop)[4][4],
+                                             floatx4 (&o)[8][4], float (&m_run)[4], float (&l_run)[4], int k0,
+                                             const TileMask& tm, int qrow, const PrefillArgs& a, int per, int plen,
+                                             const int (&quota)[4], int m16, int j) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    // S^T = K . Q^T for 32 keys: s[t][u][r] = raw score of key k0 + 32kk + 16t + 4j + r, column (head u, qrow)
+    floatx4 s[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 kop = __builtin_bit_cast(bf16x8, lds16(Kbuf, 32 * kk + 16 * t + m16, 4 * i + j));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
+      }
+    if (tm.mode != 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
+            bool ok;
+            if (tm.mode == 1) ok = kv <= qrow;
+            else if (tm.mode == 2) ok = kv < tm.limit[u];
+            else ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
+            s[t][u][r] = ok ? s[t][u][r] : -INFINITY;
+          }
+    }
+    float tmax[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float mx = fmaxf(fmaxf(fmaxf(s[0][u][0], s[0][u][1]), fmaxf(s[0][u][2], s[0][u][3])),
+                       fmaxf(fmaxf(s[1][u][0], s[1][u][1]), fmaxf(s[1][u][2], s[1][u][3])));
+      mx = fmaxf(mx, xor_shfl(mx, 16));
+      mx = fmaxf(mx, xor_shfl(mx, 32));
+      tmax[u] = mx * a.scale_log2;                          // log2-domain max (scale > 0)
+    }
+    // lazy rescale: the running max moves only when a column max grows by more than 8 (2^8 headroom in P)
+    bool need = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) need |= tmax[u] > m_run[u] + 8.f;
+    if (__any(need)) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float m_new = fmaxf(m_run[u], tmax[u]);
+        const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+        m_run[u] = m_new;
+        l_run[u] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
+      }
+    }
+    bf16x8 pop[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(fmaf(s[t][u][r], a.scale_log2, neg_m));
+          s[t][u][r] = p;
+          ps += p;
+        }
+      l_run[u] += ps;
+      u32x4 pw;
+      pw[0] = pack_bf16x2(s[0][u][0], s[0][u][1]);
+      pw[1] = pack_bf16x2(s[0][u][2], s[0][u][3]);
+      pw[2] = pack_bf16x2(s[1][u][0], s[1][u][1]);
+      pw[3] = pack_bf16x2(s[1][u][2], s[1][u][3]);
+      pop[u] = __builtin_bit_cast(bf16x8, pw);
+    }
+    // O^T += V^T . P^T over the same 32 keys (P^T row e: e<4 -> key 32kk+4j+e, e>=4 -> key 32kk+16+4j+e-4)
+    u32x4 vr[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vr[e] = lds16(Vbuf, 32 * kk + 4 * j + e, m16);
+      vr[4 + e] = lds16(Vbuf, 32 * kk + 16 + 4 * j + e, m16);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x05040100u);
+        hi[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x07060302u);
+      }
+      const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
+        o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
+      }
+    }
+  }
+}
+
+// Class of key tile kt for this query tile: 0 skip, otherwise fills the mask mode.
+__device__ __forceinline__ int tile_class(const PrefillArgs& a, int kt, int q0, int q_last, int per, int plen,
+                                          int qmin, int qmax, const int (&quota)[4], TileMask& tm) {
+  const int k0 = kt * kBN;
+  if (!a.aligned) {
+    const int qb_hi = q_last / per;
+    tm.mode = 3;
+    return (k0 <= q_last || k0 / per <= qb_hi) ? 1 : 0;
+  }
+  const int cls = classify(q0, k0, a.C, per, plen, qmin, qmax);
+  if (cls != 2) {
+    tm.mode = 0;
+    return cls;
+  }
+  const int kb = k0 / per, kw0 = k0 - kb * per;
+  const int qb = q0 / per;
+  if (kw0 < a.C) {
+    if (kb == qb) {
+      tm.mode = 1;                                          // diagonal tile of the block's content
+    } else {
+      tm.mode = 2;                                          // raw-prompt boundary inside the tile
+      const int lim = kb * per + (plen - kb * a.C);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) tm.limit[u] = lim;
+    }
+  } else {
+    tm.mode = 2;                                            // quota boundary inside a code tile
+#pragma unroll
+    for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + a.C + quota[u];
+  }
+  return 1;
+}
+
+__global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) __bf16 Kb[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) __bf16 Vb[2 * kTileElems];
+
+  const int qt = a.num_q_tiles - 1 - blockIdx.x;            // heavier (later) query tiles first
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
@@ -106,7 +276,6 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
     qmax = max(qmax, quota[u]);
   }
 
-  // Q^T operands: column (head u, row qrow), dims 8*(4i+j) .. +8 for dim step i.
   bf16x8 qop[4][4];
   {
     const bool ok = qrow < a.S0;
@@ -120,7 +289,6 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
         qop[u][i] = __builtin_bit_cast(bf16x8, x);
       }
   }
-
   floatx4 o[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -133,140 +301,37 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
     l_run[u] = 0.f;
   }
 
-  const long kbase = (long)b * a.k_sb + (long)kvh * a.k_sh;
-  const long vbase = (long)b * a.v_sb + (long)kvh * a.v_sh;
+  const __bf16* kg = a.k + (long)b * a.k_sb + (long)kvh * a.k_sh;
+  const __bf16* vg = a.v + (long)b * a.v_sb + (long)kvh * a.v_sh;
   const int n_k_tiles = (a.S0 + kBN - 1) / kBN;
   const int q_last = min(q0 + kBM, a.S0) - 1;
-  for (int kt = 0; kt < n_k_tiles; ++kt) {
-    const int k0 = kt * kBN;
-    int cls;
-    if (a.aligned) {
-      cls = classify(q0, k0, a.C, per, plen, qmin, qmax);
+
+  // double-buffered walk over the visible key tiles
+  TileMask tm_cur, tm_nxt;
+  int cur = 0;
+  while (cur < n_k_tiles && !tile_class(a, cur, q0, q_last, per, plen, qmin, qmax, quota, tm_cur)) ++cur;
+  if (cur < n_k_tiles) issue_tile(kg, a.k_ss, vg, a.v_ss, cur * kBN, a.S0, Kb, Vb, w, lane);
+  int parity = 0;
+  while (cur < n_k_tiles) {
+    int nxt = cur + 1;
+    while (nxt < n_k_tiles && !tile_class(a, nxt, q0, q_last, per, plen, qmin, qmax, quota, tm_nxt)) ++nxt;
+    const int off_cur = parity * kTileElems, off_nxt = (parity ^ 1) * kTileElems;
+    // Plain s_barrier (no workgroup fence): a fence would wait for the prefetch just issued. Each wave waits for
+    // its own DMA of the current tile (vmcnt), the barrier then publishes every wave's part.
+    if (nxt < n_k_tiles) {
+      issue_tile(kg, a.k_ss, vg, a.v_ss, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
+      __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
     } else {
-      // unaligned: keys past the query tile's last row are visible only as same-block codes of a code query
-      const int qb_hi = q_last / per;
-      const int kb_lo = k0 / per;
-      cls = (k0 <= q_last || kb_lo <= qb_hi) ? 2 : 0;
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    if (cls == 0) continue;
-
-    // stage K and V tiles: 64 keys x 256 B each, 16 threads per key row
-    __syncthreads();
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int c = tid + 256 * x;
-      const int key = c >> 4, col = (c & 15) * 8;
-      const int kv = k0 + key;
-      u32x4 kk = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
-      if (kv < a.S0) {
-        kk = ld16g(a.k + kbase + (long)kv * a.k_ss + col);
-        vv = ld16g(a.v + vbase + (long)kv * a.v_ss + col);
-      }
-      *reinterpret_cast<u32x4*>(&Ks[key * kLdsStride + col]) = kk;
-      *reinterpret_cast<u32x4*>(&Vs[key * kLdsStride + col]) = vv;
-    }
-    __syncthreads();
-
-    // Two halves of 32 keys: key step kk covers tile keys 32kk + {16t' + 4j + r}, t' in {0, 1}.
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      // S^T = K . Q^T for 32 keys: s[t][u][r] is key k0 + 32kk + 16t + 4j + r, column (head u, row qrow)
-      floatx4 s[2][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const bf16x8 kop = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(&Ks[(32 * kk + 16 * t + m16) * kLdsStride + 8 * (4 * i + j)]));
-#pragma unroll
-          for (int u = 0; u < 4; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
-        }
-
-      float tmax[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = s[t][u][r] * a.scale_log2;
-            if (cls == 2) {
-              const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
-              const bool ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
-              x = ok ? x : -INFINITY;
-            }
-            s[t][u][r] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = fmaxf(mx, xor_shfl(mx, 16));
-        mx = fmaxf(mx, xor_shfl(mx, 32));
-        tmax[u] = mx;
-      }
-      // lazy rescale: move the running max only when a column's max grows by more than 8 (2^8 headroom in P)
-      bool need = false;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) need |= tmax[u] > m_run[u] + 8.f;
-      if (__any(need)) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float m_new = fmaxf(m_run[u], tmax[u]);
-          const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
-          m_run[u] = m_new;
-          l_run[u] *= alpha;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
-        }
-      }
-      bf16x8 pop[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
-        float ps = 0.f;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = fast_exp2(s[t][u][r] - m_use);
-            s[t][u][r] = p;
-            ps += p;
-          }
-        l_run[u] += ps;
-        u32x4 pw;
-        pw[0] = pack_bf16x2(s[0][u][0], s[0][u][1]);
-        pw[1] = pack_bf16x2(s[0][u][2], s[0][u][3]);
-        pw[2] = pack_bf16x2(s[1][u][0], s[1][u][1]);
-        pw[3] = pack_bf16x2(s[1][u][2], s[1][u][3]);
-        pop[u] = __builtin_bit_cast(bf16x8, pw);
-      }
-
-      // O^T += V^T . P^T over the same 32 keys (P^T row e: e<4 -> key 32kk+4j+e, e>=4 -> key 32kk+16+4j+e-4)
-      u32x4 vr[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vr[e] = *reinterpret_cast<const u32x4*>(&Vs[(32 * kk + 4 * j + e) * kLdsStride + 8 * m16]);
-        vr[4 + e] = *reinterpret_cast<const u32x4*>(&Vs[(32 * kk + 16 + 4 * j + e) * kLdsStride + 8 * m16]);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        u32x4 lo, hi;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lo[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x05040100u);
-          hi[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x07060302u);
-        }
-        const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
-          o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
-        }
-      }
-    }
+    __builtin_amdgcn_s_barrier();
+    tile_compute(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow, a, per, plen, quota, m16,
+                 j);
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are complete
+    __builtin_amdgcn_s_barrier();                           // the buffer just read is refilled next iteration
+    cur = nxt;
+    tm_cur = tm_nxt;
+    parity ^= 1;
   }
 
   if (qrow >= a.S0) return;
