@@ -135,8 +135,8 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
     float mx = sv[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
-    mx = fmaxf(mx, xor_shfl(mx, 16));
-    mx = fmaxf(mx, xor_shfl(mx, 32));
+    mx = max_xor16(mx);
+    mx = max_xor32(mx);
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
@@ -172,8 +172,7 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
   }
 
   // o[i][r] = un-normalised out[head m16][dim 32j + 8r + i]; l_run partial over this lane's slots.
-  float l_tot = l_run + xor_shfl(l_run, 16);
-  l_tot += xor_shfl(l_tot, 32);
+  const float l_tot = sum_xor32(sum_xor16(l_run));
   if (m16 >= kGroup) return;
   const int head = kvh * kGroup + m16;
   if (n_splits == 1) {

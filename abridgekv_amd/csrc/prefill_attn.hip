@@ -7,9 +7,9 @@
 //   visible(q, kv) = (kv <= q) & (own-block content | earlier blocks' codes | raw-prompt content)
 //                  | (code query & code key & same block),     and a code key needs slot < quota[head].
 //
-// Work decomposition: one workgroup of 4 waves per (sequence, KV head, 64-row query tile). Wave w owns query rows
-// q0 + 16w .. +16 for all 4 query heads of the KV head: 64 MFMA columns (column = head u x row), so one K operand
-// feeds 4 heads. Key tiles of 64 are DMA'd into double-buffered, XOR-swizzled LDS one visible tile ahead
+// Work decomposition: one workgroup of 8 waves per (sequence, KV head, 64-row query tile). A wave owns 16 query rows
+// for 2 of the 4 query heads of the KV head: 32 MFMA columns (column = head u x row), so one K operand feeds 2 heads
+// and the wave fits in 216 VGPRs (2 waves per SIMD). Key tiles of 64 are DMA'd into double-buffered, XOR-swizzled LDS one visible tile ahead
 // (global_load_lds_dwordx4: no VGPR staging), so loads overlap the previous tile's MFMA work.
 // Each LDS tile is consumed in two halves of 32 keys (keeps the score accumulators at 32 VGPRs):
 //   S^T[32 keys x 64 cols]   = K . Q^T            2 key sub-tiles x 4 heads x 4 dim steps, MFMA 16x16x32 bf16
@@ -88,11 +88,13 @@ __device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_ca
 // global_load_lds_dwordx4: a wave instruction writes 1 KiB contiguously (lane L -> bytes 16L), so each lane fetches
 // the global chunk that belongs at its swizzled position. Rows past the sequence end re-read the last row (finite data,
 // masked to probability 0).
+template <int kWaves>
 __device__ __forceinline__ void issue_tile(const __bf16* kg, long k_ss, const __bf16* vg, long v_ss, int k0, int S0,
                                            __bf16* Kbuf, __bf16* Vbuf, int w, int lane) {
+  constexpr int kPerWave = 16 / kWaves;        // 1 KiB blocks of the 16 KiB K (and V) tile per wave
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const int blk = 4 * w + n;                 // 1 KiB block of the 16 KiB tile
+  for (int n = 0; n < kPerWave; ++n) {
+    const int blk = kPerWave * w + n;
     const int row = 4 * blk + (lane >> 4);
     const int logical = (lane & 15) ^ (row & 15);
     const int key = min(k0 + row, S0 - 1);
@@ -113,57 +115,65 @@ struct TileMask {
 };
 
 // Attention of this wave's 64 columns against one 64-key tile held in (Kbuf, Vbuf).
-__device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* Vbuf, const bf16x8 (&qop)[4][4],
-                                             floatx4 (&o)[8][4], float (&m_run)[4], float (&l_run)[4], int k0,
+template <int H, bool kAligned>
+__device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* Vbuf, const bf16x8 (&qop)[H][4],
+                                             floatx4 (&o)[8][H], float (&m_run)[H], float (&l_run)[H], int k0,
                                              const TileMask& tm, int qrow, const PrefillArgs& a, int per, int plen,
-                                             const int (&quota)[4], int m16, int j) {
+                                             const int (&quota)[H], int hbase, int m16, int j) {
+  // aligned layouts: every partial tile is "key < lim[u]" with a per-column limit (uniform per head or qrow + 1)
+  int lim[H];
+#pragma unroll
+  for (int u = 0; u < H; ++u) lim[u] = tm.mode == 1 ? qrow + 1 : tm.limit[hbase + u];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     // S^T = K . Q^T for 32 keys: s[t][u][r] = raw score of key k0 + 32kk + 16t + 4j + r, column (head u, qrow)
-    floatx4 s[2][4];
+    floatx4 s[2][H];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < H; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const bf16x8 kop = __builtin_bit_cast(bf16x8, lds16(Kbuf, 32 * kk + 16 * t + m16, 4 * i + j));
 #pragma unroll
-        for (int u = 0; u < 4; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
+        for (int u = 0; u < H; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
       }
     if (tm.mode != 0) {
+      const int kb = k0 + 32 * kk + 4 * j;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < H; ++u)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
+            const int kv = kb + 16 * t + r;
             bool ok;
-            if (tm.mode == 1) ok = kv <= qrow;
-            else if (tm.mode == 2) ok = kv < tm.limit[u];
-            else ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
+            if constexpr (kAligned) {
+              ok = kv < lim[u];
+            } else {
+              ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
+            }
             s[t][u][r] = ok ? s[t][u][r] : -INFINITY;
           }
     }
-    float tmax[4];
+    float tmax[H];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < H; ++u) {
       float mx = fmaxf(fmaxf(fmaxf(s[0][u][0], s[0][u][1]), fmaxf(s[0][u][2], s[0][u][3])),
                        fmaxf(fmaxf(s[1][u][0], s[1][u][1]), fmaxf(s[1][u][2], s[1][u][3])));
-      mx = fmaxf(mx, xor_shfl(mx, 16));
-      mx = fmaxf(mx, xor_shfl(mx, 32));
+      mx = max_xor16(mx);
+      mx = max_xor32(mx);
       tmax[u] = mx * a.scale_log2;                          // log2-domain max (scale > 0)
     }
     // lazy rescale: the running max moves only when a column max grows by more than 8 (2^8 headroom in P)
     bool need = false;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) need |= tmax[u] > m_run[u] + 8.f;
+    for (int u = 0; u < H; ++u) need |= tmax[u] > m_run[u] + 8.f;
     if (__any(need)) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < H; ++u) {
         const float m_new = fmaxf(m_run[u], tmax[u]);
         const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
         m_run[u] = m_new;
@@ -172,9 +182,9 @@ __device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* V
         for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
       }
     }
-    bf16x8 pop[4];
+    bf16x8 pop[H];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < H; ++u) {
       const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
       float ps = 0.f;
 #pragma unroll
@@ -210,7 +220,7 @@ __device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* V
       }
       const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < H; ++u) {
         o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
         o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
       }
@@ -251,7 +261,9 @@ __device__ __forceinline__ int tile_class(const PrefillArgs& a, int kt, int q0, 
   return 1;
 }
 
-__global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
+template <int H, bool kAligned>
+__global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(PrefillArgs a) {
+  constexpr int kWaves = 4 * (4 / H);                       // 16 query rows x H heads per wave
   __shared__ __attribute__((aligned(16))) __bf16 Kb[2 * kTileElems];
   __shared__ __attribute__((aligned(16))) __bf16 Vb[2 * kTileElems];
 
@@ -263,40 +275,44 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
   const int lane = tid & 63;
   const int m16 = lane & 15;
   const int j = lane >> 4;
+  const int rg = w / (4 / H);                               // row group (16 rows)
+  const int hbase = H * (w % (4 / H));                      // first head of this wave inside the GQA group
   const int per = a.C + a.K;
   const int q0 = qt * kBM;
-  const int qrow = q0 + 16 * w + m16;                       // this lane's query row (MFMA column)
+  const int qrow = q0 + 16 * rg + m16;                      // this lane's query row (MFMA column)
   const int plen = a.prompt_len ? a.prompt_len[b] : 0;
-  int quota[4];
+  int quota_all[4], quota[H];
   int qmin = 1 << 30, qmax = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    quota[u] = a.head_quota ? a.head_quota[kvh * kGroup + u] : a.K;
-    qmin = min(qmin, quota[u]);
-    qmax = max(qmax, quota[u]);
+    quota_all[u] = a.head_quota ? a.head_quota[kvh * kGroup + u] : a.K;
+    qmin = min(qmin, quota_all[u]);
+    qmax = max(qmax, quota_all[u]);
   }
+#pragma unroll
+  for (int u = 0; u < H; ++u) quota[u] = quota_all[hbase + u];
 
-  bf16x8 qop[4][4];
+  bf16x8 qop[H][4];
   {
     const bool ok = qrow < a.S0;
     const __bf16* qb = a.q + (long)b * a.q_sb + (long)min(qrow, a.S0 - 1) * a.q_ss;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < H; ++u)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        u32x4 x = ld16g(qb + (long)(kvh * kGroup + u) * a.q_sh + 8 * (4 * i + j));
+        u32x4 x = ld16g(qb + (long)(kvh * kGroup + hbase + u) * a.q_sh + 8 * (4 * i + j));
         if (!ok) x = u32x4{0, 0, 0, 0};
         qop[u][i] = __builtin_bit_cast(bf16x8, x);
       }
   }
-  floatx4 o[8][4];
+  floatx4 o[8][H];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) o[i][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[4], l_run[4];
+    for (int u = 0; u < H; ++u) o[i][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run[H], l_run[H];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < H; ++u) {
     m_run[u] = -INFINITY;
     l_run[u] = 0.f;
   }
@@ -309,24 +325,25 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
   // double-buffered walk over the visible key tiles
   TileMask tm_cur, tm_nxt;
   int cur = 0;
-  while (cur < n_k_tiles && !tile_class(a, cur, q0, q_last, per, plen, qmin, qmax, quota, tm_cur)) ++cur;
-  if (cur < n_k_tiles) issue_tile(kg, a.k_ss, vg, a.v_ss, cur * kBN, a.S0, Kb, Vb, w, lane);
+  while (cur < n_k_tiles && !tile_class(a, cur, q0, q_last, per, plen, qmin, qmax, quota_all, tm_cur)) ++cur;
+  if (cur < n_k_tiles) issue_tile<kWaves>(kg, a.k_ss, vg, a.v_ss, cur * kBN, a.S0, Kb, Vb, w, lane);
   int parity = 0;
   while (cur < n_k_tiles) {
     int nxt = cur + 1;
-    while (nxt < n_k_tiles && !tile_class(a, nxt, q0, q_last, per, plen, qmin, qmax, quota, tm_nxt)) ++nxt;
+    while (nxt < n_k_tiles && !tile_class(a, nxt, q0, q_last, per, plen, qmin, qmax, quota_all, tm_nxt)) ++nxt;
     const int off_cur = parity * kTileElems, off_nxt = (parity ^ 1) * kTileElems;
     // Plain s_barrier (no workgroup fence): a fence would wait for the prefetch just issued. Each wave waits for
     // its own DMA of the current tile (vmcnt), the barrier then publishes every wave's part.
     if (nxt < n_k_tiles) {
-      issue_tile(kg, a.k_ss, vg, a.v_ss, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
-      __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      issue_tile<kWaves>(kg, a.k_ss, vg, a.v_ss, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
+      if constexpr (kWaves == 4) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
-    tile_compute(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow, a, per, plen, quota, m16,
-                 j);
+    tile_compute<H, kAligned>(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow, a, per,
+                              plen, quota, hbase, m16, j);
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are complete
     __builtin_amdgcn_s_barrier();                           // the buffer just read is refilled next iteration
     cur = nxt;
@@ -335,13 +352,12 @@ __global__ __launch_bounds__(256, 1) void prefill_masked_kernel(PrefillArgs a) {
   }
 
   if (qrow >= a.S0) return;
-  // o[i][u][r] = un-normalised out[row qrow][head u][dim 32j + 8r + i]
+  // o[i][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 8r + i]
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    float l = l_run[u] + xor_shfl(l_run[u], 16);
-    l += xor_shfl(l, 32);
+  for (int u = 0; u < H; ++u) {
+    const float l = sum_xor32(sum_xor16(l_run[u]));
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int head = kvh * kGroup + u;
+    const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)qrow * a.o_ss + (long)head * a.o_sh + 32 * j;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -387,7 +403,11 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.lse = lse;
   a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
-  hipLaunchKernelGGL(prefill_masked_kernel, dim3(a.num_q_tiles, kHeadsKV, batch), dim3(256), 0, stream, a);
+  // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
+  // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).
+  const dim3 grid(a.num_q_tiles, kHeadsKV, batch);
+  if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true>), grid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_masked_kernel<2, false>), grid, dim3(512), 0, stream, a);
   return (int)hipGetLastError();
 }
 

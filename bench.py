@@ -33,7 +33,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=32)
-    ap.add_argument("--workload", choices=["saturated", "full_model", "prefill", "compaction"], default="saturated")
+    ap.add_argument("--workload", choices=["saturated", "full_model", "prefill", "compaction", "copy"],
+                    default="saturated")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     return ap.parse_args()
@@ -196,6 +197,25 @@ def bench_compaction(args, torch):
     }
 
 
+def bench_copy(args, torch):
+    """Calibration kernel for the traffic counters: a plain device copy of 4 GiB (reads 4 GiB, writes 4 GiB)."""
+    n = 4 << 30
+    a = torch.ones(n // 2, dtype=torch.bfloat16, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / args.steps
+    return {"metric": "device copy bandwidth (read + write)", "value": 2 * n / t / 1e9, "unit": "GB/s",
+            "bytes_read_per_launch": n, "bytes_written_per_launch": n, "ms_per_step": t * 1e3, "steps": args.steps}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -204,8 +224,8 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("prefill", "compaction"):
-        res = (bench_prefill if args.workload == "prefill" else bench_compaction)(args, torch)
+    if args.workload in ("prefill", "compaction", "copy"):
+        res = {"prefill": bench_prefill, "compaction": bench_compaction, "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
