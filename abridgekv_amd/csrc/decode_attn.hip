@@ -204,46 +204,35 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
   }
 }
 
-// Merge the split partials of every sequence with more than one split: one workgroup per sequence,
-// thread t handles head t/8, dims 16*(t%8) .. +16.
+// Merge the split partials of every sequence with more than one split. Workgroup (sequence, group of 8 heads);
+// thread t handles head 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int b = blockIdx.x;
   const int seq_len = min(a.seq_lens[b], a.max_pages * kPage);
   const int n_pages = (seq_len + kPage - 1) / kPage;
   const int n_splits = (n_pages + a.split_pages - 1) / a.split_pages;
   if (n_splits <= 1) return;
-  const int head = threadIdx.x >> 3;
-  const int d0 = (threadIdx.x & 7) * 16;
+  const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
+  const int d0 = (threadIdx.x & 31) * 4;
   const float* pml = a.part_ml + ((long)b * a.max_splits * kHeadsQ + head) * 2;
   float M = -INFINITY;
   for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[(long)s * kHeadsQ * 2]);
   float L = 0.f;
-  float acc[16];
-#pragma unroll
-  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < n_splits; ++s) {
     const float w = fast_exp2(pml[(long)s * kHeadsQ * 2] - M);
     L += w * pml[(long)s * kHeadsQ * 2 + 1];
-    const float* po = a.part_o + (((long)b * a.max_splits + s) * kHeadsQ + head) * kHeadDim + d0;
-#pragma unroll
-    for (int d = 0; d < 16; d += 4) {
-      floatx4 v = *reinterpret_cast<const floatx4*>(po + d);
-      acc[d] += w * v[0];
-      acc[d + 1] += w * v[1];
-      acc[d + 2] += w * v[2];
-      acc[d + 3] += w * v[3];
-    }
+    const floatx4 v =
+        *reinterpret_cast<const floatx4*>(a.part_o + (((long)b * a.max_splits + s) * kHeadsQ + head) * kHeadDim + d0);
+    acc += w * v;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + d0;
-#pragma unroll
-  for (int d = 0; d < 16; d += 8) {
-    u32x4 w;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) w[c] = pack_bf16x2(acc[d + 2 * c] * inv, acc[d + 2 * c + 1] * inv);
-    *reinterpret_cast<u32x4*>(oh + d) = w;
-  }
-  if (a.lse != nullptr && (threadIdx.x & 7) == 0)
+  u32x2 wv;
+  wv[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  wv[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2*>(oh) = wv;
+  if (a.lse != nullptr && (threadIdx.x & 31) == 0)
     a.lse[(long)b * kHeadsQ + head] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : -INFINITY;
 }
 
@@ -295,7 +284,7 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   if (max_splits > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 8), dim3(256), 0, stream, a);
     err = hipGetLastError();
   }
   return (int)err;
