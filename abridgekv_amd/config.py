@@ -1,0 +1,193 @@
+"""Serving configuration of the abridged cache (API-compatible subset of the reference's CompressLMConfig).
+
+Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309 for the configuration this path serves: one pause
+pass, raw prompt, bitrev code positions, no replay / raw / retained tails, optional per-layer quotas with physical
+removal. Options of the reference that belong to other modes (replay tails, retained tails, packed per-head KV,
+selective full-history evaluation) are rejected with ValueError instead of being silently ignored.
+"""
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+def layer_index(layer_name: str) -> int | None:
+    """Index n of an attention layer named '...layers.n....' (None when not indexed)."""
+    marker = ".layers."
+    if marker not in layer_name:
+        return None
+    head = layer_name.split(marker, 1)[1].split(".", 1)[0]
+    return int(head) if head.isdigit() else None
+
+
+def bitrev_offsets(K: int, span: int) -> np.ndarray:
+    """Row k of a K-row code block -> floor(bitreverse_{log2 K}(k) * span / K) (int64)."""
+    if K <= 0 or K & (K - 1):
+        raise ValueError("num_code_tokens must be a power of two for bitrev positions")
+    if span < K:
+        raise ValueError(f"bitrev code span {span} < num_code_tokens {K}")
+    bits = K.bit_length() - 1
+    k = np.arange(K, dtype=np.int64)
+    rev = np.zeros_like(k)
+    for b in range(bits):
+        rev |= ((k >> b) & 1) << (bits - 1 - b)
+    return (rev * span) // K
+
+
+@dataclass
+class CompressLMConfig:
+    enable: bool = False
+    block_size: int = 512
+    num_code_tokens: int = 128
+    replay_tail: int = 0
+    retain_tail_kv: int = 0
+    retain_tail_policy: str = "rolling"
+    code_exclude_replay_tail: bool = False
+    raw_prompt: bool = True
+    num_passes: int = 1
+    pause_xattn: str = "full"
+    raw_tail: int = 0
+    code_token_format: str = "<|compress_code_{:03d}|>"
+    debug: bool = False
+    code_positions: str = "bitrev"
+    layer_code_quotas: tuple[int, ...] = ()
+    physical_layer_quotas: bool = False
+    retain_full_history_layers: tuple[int, ...] = ()
+    packed_kv: bool = False
+
+    _code_token_ids: list[int] = field(default_factory=list, repr=False)
+    _initialized: bool = field(default=False, repr=False)
+
+    def __post_init__(self) -> None:
+        self.layer_code_quotas = tuple(int(q) for q in self.layer_code_quotas)
+        self.retain_full_history_layers = tuple(sorted(set(self.retain_full_history_layers)))
+        if self.code_positions not in ("appended", "bitrev"):
+            raise ValueError("code_positions must be appended or bitrev")
+        if not self.enable:
+            return
+        C, K = self.block_size, self.num_code_tokens
+        if C <= 0:
+            raise ValueError("block_size must be positive")
+        if K <= 0:
+            raise ValueError("num_code_tokens must be positive")
+        if self.code_positions != "bitrev":
+            raise ValueError("this build serves code_positions='bitrev' only")
+        if (C & (C - 1)) or (K & (K - 1)):
+            raise ValueError("code_positions=bitrev needs power-of-two block_size and num_code_tokens")
+        if self.replay_tail or self.raw_tail or self.retain_tail_kv or self.code_exclude_replay_tail:
+            raise ValueError("this build serves no replay / raw / retained tails")
+        if self.num_passes != 1:
+            raise ValueError("CompressLM decoding supports num_passes=1 only")
+        if self.pause_xattn != "full":
+            raise ValueError("CompressLM decoding requires pause_xattn='full'")
+        if not self.raw_prompt:
+            raise ValueError("CompressLM decoding requires raw_prompt=True")
+        if self.packed_kv or self.retain_full_history_layers:
+            raise ValueError("packed per-head KV and selective full history are not served by this build")
+        for layer, q in enumerate(self.layer_code_quotas):
+            if not 0 < q <= K:
+                raise ValueError(f"layer_code_quotas[{layer}]={q} must be in [1, {K}]")
+        if self.physical_layer_quotas and not self.layer_code_quotas:
+            raise ValueError("physical_layer_quotas needs layer_code_quotas")
+
+    # -- positions ------------------------------------------------------------------------------------------------
+    @property
+    def code_excluded_tail(self) -> int:
+        return 0
+
+    def bitrev_code_offsets(self) -> np.ndarray:
+        """In-block RoPE offsets of the code rows (config/compresslm.py:192-206)."""
+        return bitrev_offsets(self.num_code_tokens, self.block_size - self.code_excluded_tail)
+
+    def bitrev_rope_positions(self, logical) -> np.ndarray:
+        """Logical positions (period C+K per block) -> bitrev RoPE positions (config/compresslm.py:208-216)."""
+        C, K = self.block_size, self.num_code_tokens
+        logical = np.asarray(logical, dtype=np.int64)
+        blk, within = logical // (C + K), logical % (C + K)
+        offs = self.bitrev_code_offsets()[np.clip(within - C, 0, K - 1)]
+        return blk * C + np.where(within >= C, offs, within)
+
+    # -- token ids ------------------------------------------------------------------------------------------------
+    def initialize_token_ids(self, tokenizer) -> "CompressLMConfig":
+        if self._initialized:
+            return self
+        if tokenizer is None:
+            raise ValueError("CompressLM decoding requires an initialized tokenizer")
+        ids = []
+        for token in self.code_tokens:
+            enc = tokenizer.encode(token, add_special_tokens=False)
+            if len(enc) != 1:
+                raise ValueError(f"CompressLM code token {token!r} must encode to one ID; got {enc}")
+            ids.append(enc[0])
+        if len(set(ids)) != len(ids):
+            raise ValueError("CompressLM code tokens must have distinct token IDs")
+        self._code_token_ids, self._initialized = ids, True
+        return self
+
+    def set_code_token_ids(self, ids: Sequence[int]) -> "CompressLMConfig":
+        """Install code-token ids directly (tokenizer-free use, tests)."""
+        ids = [int(i) for i in ids]
+        if len(ids) != self.num_code_tokens or len(set(ids)) != len(ids):
+            raise ValueError("need num_code_tokens distinct code token ids")
+        self._code_token_ids, self._initialized = ids, True
+        return self
+
+    @property
+    def code_token_ids(self) -> list[int]:
+        if not self._initialized:
+            raise RuntimeError("Call initialize_token_ids() before decoding")
+        return self._code_token_ids
+
+    @property
+    def code_tokens(self) -> list[str]:
+        return [self.code_token_format.format(i) for i in range(self.num_code_tokens)]
+
+    # -- quotas ---------------------------------------------------------------------------------------------------
+    @property
+    def uses_layer_quotas(self) -> bool:
+        return any(q < self.num_code_tokens for q in self.layer_code_quotas)
+
+    @property
+    def uses_physical_layer_quotas(self) -> bool:
+        return bool(self.physical_layer_quotas) and self.uses_layer_quotas
+
+    @property
+    def uses_selective_history(self) -> bool:
+        return False
+
+    @property
+    def uses_packed_kv(self) -> bool:
+        return False
+
+    def layer_quota(self, layer: int) -> int:
+        if 0 <= layer < len(self.layer_code_quotas):
+            return self.layer_code_quotas[layer]
+        return self.num_code_tokens
+
+    @property
+    def distinct_layer_quotas(self) -> tuple[int, ...]:
+        return tuple(sorted(set(self.layer_code_quotas)))
+
+    def kv_group_quotas(self, group_layer_names: Sequence[Sequence[str]]) -> tuple[int, ...]:
+        """Quota of every KV-cache group; a group must hold layers of one quota."""
+        out = []
+        for names in group_layer_names:
+            qs = set()
+            for name in names:
+                idx = layer_index(name)
+                if idx is None:
+                    raise ValueError(f"physical per-layer quotas need indexed attention layers; got {name!r}")
+                qs.add(self.layer_quota(idx))
+            if len(qs) != 1:
+                raise ValueError(f"KV cache group mixes code quotas {sorted(qs)}: {list(names)}")
+            out.append(qs.pop())
+        return tuple(out)
+
+    def kv_cache_groups(self, num_layers: int) -> tuple[list[list[int]], list[int]]:
+        """(layers per KV-cache group, quota per group) for a model of ``num_layers`` attention layers, grouped as the
+        reference's KV-cache config does (kv_cache_utils.py:1001-1052, 1216-1226)."""
+        from .workloads import quota_groups
+
+        return quota_groups([self.layer_quota(i) for i in range(num_layers)])

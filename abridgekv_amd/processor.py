@@ -1,0 +1,346 @@
+"""Scheduler-side block state machine: which tokens run when, and which spans are compacted.
+
+API-compatible with the reference's CompressLMProcessor (third_party/vllm_overlay/vllm/v1/core/compresslm/
+processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay / retained tails,
+physical per-layer quotas): prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121,
+limit_num_new_tokens :123-151, should_skip_sampling :153-168, update_after_step :170-257, reset_for_preemption
+:259-260, code_physical_spans :276-316, _stage_codes :369-400, _finish_block :419-465, _compact_response_content
+:467-557, _mask_or_raise :648-661, _check_stop :663-685. The compaction callback ``mask_span(request_id, start, end,
+groups=None)`` is KVPlanner.mask_token_span.
+"""
+from __future__ import annotations
+
+import enum
+from collections.abc import Callable, Sequence
+from dataclasses import dataclass, field
+
+from .config import CompressLMConfig
+
+CONTENT, CODE = 0, 1
+
+MaskSpan = Callable[..., object]
+
+
+class RequestStatus(enum.IntEnum):
+    RUNNING = 0
+    FINISHED_STOPPED = 1
+    FINISHED_LENGTH_CAPPED = 2
+
+
+@dataclass
+class SamplingSpec:
+    """The sampling fields the state machine reads."""
+    max_tokens: int = 1 << 30
+    ignore_eos: bool = False
+    stop_token_ids: tuple[int, ...] = ()
+    min_tokens: int = 0
+    bad_words_token_ids: list = field(default_factory=list)
+
+
+@dataclass
+class CompressLMBlock:
+    block_id: int
+    content_positions: list[int] = field(default_factory=list)
+    content_token_ids: list[int] = field(default_factory=list)
+    prompt_content_positions: list[int] = field(default_factory=list)
+    response_content_positions: list[int] = field(default_factory=list)
+    code_span: tuple[int, int] | None = None
+
+
+@dataclass
+class CompressLMState:
+    original_prompt_token_ids: list[int]
+    pending_prompt_index: int
+    blocks: list[CompressLMBlock]
+    roles: list[int] = field(default_factory=list)
+    position_to_block: list[int] = field(default_factory=list)
+    visible_output_token_ids: list[int] = field(default_factory=list)
+    held_sampled_token: int | None = None
+    compacted_block_ids: set[int] = field(default_factory=set)
+    current_block_id: int = 0
+    worker_token_ids_dirty: bool = False
+
+    @property
+    def current_block(self) -> CompressLMBlock:
+        return self.blocks[self.current_block_id]
+
+    def reset_compaction_progress(self) -> None:
+        self.compacted_block_ids.clear()
+
+
+class ServingRequest:
+    """Minimal request object with the fields the state machine and the planner read (vllm.v1.request.Request)."""
+
+    def __init__(self, request_id, prompt_token_ids, sampling: SamplingSpec | None = None, eos_token_id=None,
+                 planner=None):
+        self.request_id = request_id
+        self.prompt_token_ids = list(prompt_token_ids)
+        self.num_prompt_tokens = len(self.prompt_token_ids)
+        self._all_token_ids = list(self.prompt_token_ids)
+        self._output_token_ids: list[int] = []
+        self.num_computed_tokens = 0
+        self.sampling_params = sampling or SamplingSpec()
+        self.max_tokens = self.sampling_params.max_tokens
+        self.eos_token_id = eos_token_id
+        self.status = RequestStatus.RUNNING
+        self.stop_reason = None
+        self.compresslm_state: CompressLMState | None = None
+        self.planner = planner
+
+    @property
+    def num_tokens(self) -> int:
+        return len(self._all_token_ids)
+
+    @property
+    def all_token_ids(self) -> list[int]:
+        return self._all_token_ids
+
+    def append_output_token_ids(self, ids: Sequence[int]) -> None:
+        self._output_token_ids.extend(ids)
+        self._all_token_ids.extend(ids)
+
+    def logical_to_physical(self, pos: int, group: int = 0) -> int:
+        return pos if self.planner is None else self.planner.logical_to_physical(self.request_id, pos, group)
+
+
+class CompressLMProcessor:
+    def __init__(self, config: CompressLMConfig) -> None:
+        if not config._initialized:
+            raise ValueError("CompressLMConfig token IDs are not initialized")
+        self.config = config
+        self.group_quotas: tuple[int, ...] | None = None
+
+    def set_group_quotas(self, group_quotas: Sequence[int] | None) -> None:
+        if group_quotas is None:
+            self.group_quotas = None
+            return
+        K = self.config.num_code_tokens
+        for q in group_quotas:
+            if not 0 < q <= K:
+                raise ValueError(f"KV cache group quota {q} outside [1, {K}]")
+        self.group_quotas = tuple(int(q) for q in group_quotas)
+
+    # -- request set-up -------------------------------------------------------------------------------------------
+    def prepare_request(self, request) -> CompressLMState:
+        sampling = request.sampling_params
+        if sampling is None:
+            raise ValueError("CompressLM decoding requires sampling parameters")
+        if getattr(sampling, "min_tokens", 0) != 0:
+            raise ValueError("CompressLM decoding currently requires min_tokens=0")
+        banned = {ids[0] for ids in (getattr(sampling, "bad_words_token_ids", None) or []) if len(ids) == 1}
+        missing = set(self.config.code_token_ids) - banned
+        if missing:
+            raise ValueError("CompressLM code tokens must be passed as bad_words so internal IDs cannot be sampled; "
+                             f"missing {len(missing)} IDs")
+        prompt = list(request.prompt_token_ids)
+        if not prompt:
+            raise ValueError("CompressLM decoding requires a non-empty prompt")
+        first = prompt[: self.config.block_size]
+        state = CompressLMState(original_prompt_token_ids=prompt, pending_prompt_index=len(first),
+                                blocks=[CompressLMBlock(block_id=0)])
+        request.prompt_token_ids = first
+        request.num_prompt_tokens = len(first)
+        request._all_token_ids.clear()
+        request._all_token_ids.extend(first)
+        request._output_token_ids.clear()
+        self._record_content(state, 0, first, is_prompt=True)
+        return state
+
+    # -- scheduling queries ---------------------------------------------------------------------------------------
+    def is_code_ready(self, request) -> bool:
+        state = request.compresslm_state
+        if state is None or request.num_computed_tokens >= request.num_tokens:
+            return False
+        return state.roles[request.num_computed_tokens] == CODE
+
+    def num_code_rows_pending(self, request) -> int:
+        if not self.is_code_ready(request):
+            return 0
+        roles, start = request.compresslm_state.roles, request.num_computed_tokens
+        end = start + 1
+        while end < request.num_tokens and roles[end] == CODE:
+            end += 1
+        return end - start
+
+    def limit_num_new_tokens(self, request, proposed: int) -> int:
+        """A CODE run is scheduled whole (or not at all); a CONTENT run up to its end."""
+        state = request.compresslm_state
+        if state is None or proposed <= 0:
+            return proposed
+        start = request.num_computed_tokens
+        if start >= request.num_tokens:
+            return proposed
+        role = state.roles[start]
+        end = start + 1
+        while end < request.num_tokens and state.roles[end] == role:
+            end += 1
+        remaining = end - start
+        if role == CODE:
+            return remaining if proposed >= remaining else 0
+        return min(proposed, remaining)
+
+    def should_skip_sampling(self, request, num_scheduled_tokens: int) -> bool:
+        state = request.compresslm_state
+        if state is None:
+            return False
+        start = request.num_computed_tokens
+        end = start + num_scheduled_tokens
+        if state.roles[start] != CONTENT:
+            return True
+        if end < request.num_tokens:
+            return True
+        return state.pending_prompt_index < len(state.original_prompt_token_ids)
+
+    # -- after a model step ---------------------------------------------------------------------------------------
+    def update_after_step(self, request, num_scheduled_tokens: int, sampled_token_ids: list[int],
+                          mask_span: MaskSpan, max_model_len: int, pack_code_span=None) -> tuple[list[int], bool]:
+        """``request.num_computed_tokens`` already includes the step. Returns (visible sampled tokens, stopped)."""
+        state = request.compresslm_state
+        if state is None:
+            return sampled_token_ids, False
+        if len(sampled_token_ids) > 1:
+            raise RuntimeError("CompressLM decoding is incompatible with speculative multi-token output")
+        end = request.num_computed_tokens
+        start = end - num_scheduled_tokens
+        role = state.roles[start]
+        if any(state.roles[p] != role for p in range(start, end)):
+            raise RuntimeError("CompressLM scheduled a mixed-role model step")
+        sampled = sampled_token_ids[0] if sampled_token_ids else None
+        visible: list[int] = []
+        if sampled is not None:
+            state.visible_output_token_ids.append(sampled)
+            visible.append(sampled)
+            if self._check_stop(request, state, sampled, max_model_len):
+                return visible, True
+        block = state.blocks[state.position_to_block[start]]
+        role_end = end == request.num_tokens or state.roles[end] != role
+        if role == CONTENT:
+            if len(block.content_positions) == self.config.block_size and end == block.content_positions[-1] + 1:
+                if block.code_span is None:
+                    if end + self.config.num_code_tokens >= max_model_len:
+                        request.status = RequestStatus.FINISHED_LENGTH_CAPPED
+                        return visible, True
+                    state.held_sampled_token = sampled
+                    self._stage_codes(request, state, block)
+            elif sampled is not None:
+                self._append_content(request, state, [sampled], is_prompt=False)
+        elif role == CODE and role_end:
+            self._finish_block(request, state, block, mask_span)
+        return visible, False
+
+    def reset_for_preemption(self, state: CompressLMState) -> None:
+        state.reset_compaction_progress()
+
+    def code_physical_spans(self, request, group: int = 0, logical_limit: int | None = None):
+        """Physical [start, end) of every staged code span still holding all K rows in ``group``'s layout."""
+        state = request.compresslm_state
+        if state is None:
+            raise RuntimeError("CompressLM request has no state")
+        K = self.config.num_code_tokens
+        spans = []
+        for block in state.blocks:
+            if block.code_span is None:
+                continue
+            if self.group_quotas is not None and block.block_id in state.compacted_block_ids:
+                continue
+            start, end = block.code_span
+            if logical_limit is not None and end > logical_limit:
+                continue
+            ps = request.logical_to_physical(start, group)
+            pe = request.logical_to_physical(end - 1, group) + 1
+            if pe - ps != K:
+                raise RuntimeError("code span is not contiguous after KV compaction")
+            spans.append((ps, pe))
+        return spans
+
+    # -- internals ------------------------------------------------------------------------------------------------
+    def _record_content(self, state: CompressLMState, start: int, token_ids, is_prompt: bool) -> None:
+        block = state.current_block
+        for offset, tok in enumerate(token_ids):
+            pos = start + offset
+            block.content_positions.append(pos)
+            block.content_token_ids.append(tok)
+            (block.prompt_content_positions if is_prompt else block.response_content_positions).append(pos)
+            state.roles.append(CONTENT)
+            state.position_to_block.append(block.block_id)
+
+    def _append_content(self, request, state, token_ids, is_prompt: bool) -> None:
+        if not token_ids:
+            return
+        start = request.num_tokens
+        request.append_output_token_ids(token_ids)
+        self._record_content(state, start, token_ids, is_prompt)
+
+    def _stage_codes(self, request, state, block) -> None:
+        start = request.num_tokens
+        ids = self.config.code_token_ids
+        request.append_output_token_ids(ids)
+        block.code_span = (start, request.num_tokens)
+        state.roles.extend([CODE] * len(ids))
+        state.position_to_block.extend([block.block_id] * len(ids))
+        state.worker_token_ids_dirty = True
+
+    def _finish_block(self, request, state, block, mask_span) -> None:
+        self._compact_response_content(request, state, block, mask_span)
+        if block.code_span[1] < request.num_tokens:          # preemption replay: later tokens already exist
+            return
+        nxt = CompressLMBlock(block_id=len(state.blocks))
+        state.blocks.append(nxt)
+        state.current_block_id = nxt.block_id
+        if state.pending_prompt_index < len(state.original_prompt_token_ids):
+            chunk = state.original_prompt_token_ids[state.pending_prompt_index:][: self.config.block_size]
+            state.pending_prompt_index += len(chunk)
+            self._append_content(request, state, chunk, is_prompt=True)
+            state.worker_token_ids_dirty = True
+            return
+        if state.held_sampled_token is None:
+            raise RuntimeError("CompressLM block completed without continuation token")
+        held, state.held_sampled_token = state.held_sampled_token, None
+        self._append_content(request, state, [held], is_prompt=False)
+        state.worker_token_ids_dirty = True
+
+    def _compact_response_content(self, request, state, block, mask_span) -> None:
+        """Remove the block's response rows from every group, then (physical quotas) code slots [q, K) from the
+        groups of each quota q < K, ascending q, each on the layout the previous removal left."""
+        if block.block_id in state.compacted_block_ids:
+            return
+        pos = block.response_content_positions
+        if pos:
+            if pos != list(range(pos[0], pos[-1] + 1)):
+                raise RuntimeError("CompressLM response content must be contiguous")
+            self._mask_or_raise(mask_span, request.request_id, pos[0], pos[-1] + 1)
+        if self.group_quotas is not None:
+            if block.code_span is None:
+                raise RuntimeError("physical per-layer quotas need a completed code span")
+            cs, ce = block.code_span
+            K = self.config.num_code_tokens
+            for q in sorted(set(self.group_quotas)):
+                if q >= K:
+                    continue
+                groups = [g for g, gq in enumerate(self.group_quotas) if gq == q]
+                self._mask_or_raise(mask_span, request.request_id, cs + q, ce, groups=groups)
+        state.compacted_block_ids.add(block.block_id)
+
+    @staticmethod
+    def _mask_or_raise(mask_span, request_id, start, end, groups=None) -> None:
+        res = mask_span(request_id, start, end) if groups is None else mask_span(request_id, start, end, groups=groups)
+        if not res.success:
+            raise RuntimeError(f"CompressLM KV compaction failed for [{start}, {end}): {res.error_message}")
+
+    @staticmethod
+    def _check_stop(request, state, token_id, max_model_len) -> bool:
+        sampling = request.sampling_params
+        visible = len(state.visible_output_token_ids)
+        if visible < getattr(sampling, "min_tokens", 0):
+            return False
+        if not getattr(sampling, "ignore_eos", False) and token_id == request.eos_token_id:
+            request.status = RequestStatus.FINISHED_STOPPED
+            return True
+        if token_id in (getattr(sampling, "stop_token_ids", None) or ()):
+            request.status = RequestStatus.FINISHED_STOPPED
+            request.stop_reason = token_id
+            return True
+        if request.num_tokens >= max_model_len or visible >= request.max_tokens:
+            request.status = RequestStatus.FINISHED_LENGTH_CAPPED
+            return True
+        return False

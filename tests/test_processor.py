@@ -1,0 +1,176 @@
+"""The product state machine (abridgekv_amd.processor) and config against the oracle restatement and the reference's
+own CPU test scenarios (scripts/test_compresslm_physical_quotas.py:68-208)."""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from abridgekv_amd.config import CompressLMConfig, layer_index
+from abridgekv_amd.planner import KVPlanner
+from abridgekv_amd.processor import CODE, CompressLMProcessor, RequestStatus, SamplingSpec, ServingRequest
+from oracle import layout as ol
+from oracle import trace as ot
+
+CODES = [900, 901, 902, 903]
+
+
+def make(quotas=(4, 2, 1, 2), C=4, K=4):
+    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev",
+                           layer_code_quotas=quotas, physical_layer_quotas=True)
+    cfg.set_code_token_ids(CODES[:K] if K <= 4 else list(range(900, 900 + K)))
+    proc = CompressLMProcessor(cfg)
+    proc.set_group_quotas(quotas)
+    return cfg, proc
+
+
+def test_config_positions_match_oracle_and_validate():
+    cfg = CompressLMConfig(enable=True, block_size=512, num_code_tokens=256, layer_code_quotas=ol.PERLAYER_MEAN128_QUOTAS,
+                           physical_layer_quotas=True)
+    assert np.array_equal(cfg.bitrev_code_offsets(), ol.bitrev_code_offsets(256, 512))
+    logical = np.arange(5 * 768)
+    assert np.array_equal(cfg.bitrev_rope_positions(logical), ol.bitrev_rope_positions(logical, 512, 256))
+    groups, gq = cfg.kv_cache_groups(36)
+    assert (groups, gq) == ol.quota_groups(ol.PERLAYER_MEAN128_QUOTAS)
+    names = [[f"model.layers.{l}.self_attn.attn" for l in layers] for layers in groups]
+    assert cfg.kv_group_quotas(names) == tuple(gq)
+    assert layer_index("model.layers.12.self_attn.attn") == 12 and layer_index("lm_head") is None
+    with pytest.raises(ValueError):
+        cfg.kv_group_quotas([["model.layers.0.a", "model.layers.1.a"]])         # mixes quotas 256 and 64
+    for bad in (dict(layer_code_quotas=(300,)), dict(replay_tail=16), dict(num_passes=2), dict(raw_prompt=False),
+                dict(num_code_tokens=96), dict(physical_layer_quotas=True)):
+        with pytest.raises(ValueError):
+            CompressLMConfig(enable=True, block_size=512, num_code_tokens=bad.pop("num_code_tokens", 256), **bad)
+
+
+def run_reference_scenario(proc, request, mask_span, generated):
+    """The driving loop of scripts/test_compresslm_physical_quotas.py:100-121."""
+    state = request.compresslm_state
+    gi, code_steps = 0, 0
+    for _ in range(400):
+        if request.status != RequestStatus.RUNNING:
+            break
+        proposed = request.num_tokens - request.num_computed_tokens
+        count = proc.limit_num_new_tokens(request, proposed)
+        role = state.roles[request.num_computed_tokens]
+        if role == CODE:
+            code_steps += 1
+        skip = proc.should_skip_sampling(request, count)
+        yield count, role
+        request.num_computed_tokens += count
+        sampled = []
+        if not skip:
+            sampled = [generated[gi]]
+            gi += 1
+        proc.update_after_step(request, count, sampled, mask_span, max_model_len=256)
+    else:
+        raise AssertionError("did not terminate")
+    assert gi == len(generated) and code_steps >= 2
+
+
+def test_group_removals_keep_codes_prefix_recording_mask():
+    """Reference test scenario with the reference's recording mask_span: each compacted block keeps exactly codes[:q]
+    in group q and no response content; code_physical_spans exposes only the block being coded."""
+    quotas = (4, 2, 1, 2)
+    _, proc = make(quotas)
+    req = ServingRequest("r", [11, 12, 13, 14, 15, 16], SamplingSpec(max_tokens=13, bad_words_token_ids=[[c] for c in CODES]))
+    removed = [[] for _ in quotas]
+
+    def l2p(pos, group=0):
+        assert not any(s <= pos < e for s, e in removed[group])
+        return pos - sum(e - s for s, e in removed[group] if e <= pos)
+
+    req.logical_to_physical = l2p
+
+    def mask_span(_rid, start, end, groups=None):
+        for g in (range(len(quotas)) if groups is None else groups):
+            assert not any(s < end and start < e for s, e in removed[g])
+            removed[g].append((start, end))
+        return SimpleNamespace(success=True, error_message=None)
+
+    req.compresslm_state = proc.prepare_request(req)
+    generated = list(range(21, 34))
+    for count, role in run_reference_scenario(proc, req, mask_span, generated):
+        for g in range(len(quotas)):
+            phys = [t for i, t in enumerate(req.all_token_ids) if not any(s <= i < e for s, e in removed[g])]
+            spans = proc.code_physical_spans(req, g)
+            for ps, pe in spans:
+                assert pe - ps == 4 and phys[ps:pe] == CODES
+            if role == CODE:
+                assert len(spans) == 1
+    state = req.compresslm_state
+    for g, q in enumerate(quotas):
+        for block in state.blocks:
+            if block.block_id in state.compacted_block_ids and block.code_span:
+                cs, ce = block.code_span
+                kept = [req.all_token_ids[p] for p in range(cs, ce) if not any(s <= p < e for s, e in removed[g])]
+                assert kept == CODES[:q]
+                assert all(any(s <= p < e for s, e in removed[g]) for p in block.response_content_positions)
+    n = len(state.compacted_block_ids)
+    for g, q in enumerate(quotas):
+        assert sum(e - s for s, e in removed[g]) - sum(e - s for s, e in removed[0]) == n * (4 - q)
+
+
+@pytest.mark.parametrize("prompt_len,gen", [(6, 13), (1, 30), (9, 25), (16, 9)])
+def test_calls_match_oracle_trace_and_drive_the_planner(prompt_len, gen):
+    """The product machine issues the same compaction calls as the oracle trace, and driving the native planner with
+    them keeps its per-group layouts equal to the brute-force kept positions."""
+    quotas = (4, 2, 1, 2)
+    _, proc = make(quotas, C=8, K=4)
+    planner = KVPlanner(2048, len(quotas), 2)
+    req = ServingRequest(7, list(range(100, 100 + prompt_len)),
+                         SamplingSpec(max_tokens=gen, bad_words_token_ids=[[c] for c in CODES]), planner=planner)
+    planner.add_request(7)
+    req.compresslm_state = proc.prepare_request(req)
+    tr = ot.RequestTrace(prompt_len, gen, 8, 4, quotas)
+    calls_p, calls_o = [], []
+
+    def mask_span(rid, start, end, groups=None):
+        calls_p.append((start, end, None if groups is None else list(groups)))
+        return planner.mask_token_span(rid, start, end, groups)
+
+    for step in range(500):
+        if req.status != RequestStatus.RUNNING:
+            break
+        n = proc.limit_num_new_tokens(req, req.num_tokens - req.num_computed_tokens)
+        assert n == tr.next_chunk()
+        skip = proc.should_skip_sampling(req, n)
+        assert planner.allocate_slots(7, n) is not None
+        req.num_computed_tokens += n
+        planner.set_num_computed_tokens(7, req.num_computed_tokens)
+        tr.num_computed_tokens += n
+        proc.update_after_step(req, n, [] if skip else [500 + step], mask_span, max_model_len=10_000)
+        calls_o.extend(tr.after_step(n))
+        planner.take_step_outputs()
+        for g in range(len(quotas)):
+            active = req.num_computed_tokens - planner.compacted_counts(7)[g]
+            phys = [planner.physical_to_logical(7, x, g) for x in range(active)]
+            assert phys == tr.kept_positions(g)
+    assert calls_p == [(s, e, g) for s, e, g in calls_o]
+    assert tr.finished and req.status == RequestStatus.FINISHED_LENGTH_CAPPED
+
+
+def test_preemption_bounds_code_spans():
+    """scripts/test_compresslm_physical_quotas.py:170-208 restated: after a preemption the logical structure survives
+    but the KV does not; logical_limit admits exactly the blocks whose codes are back in the KV."""
+    _, proc = make((4, 2, 1, 2))
+    req = ServingRequest("r", [11, 12, 13, 14, 15, 16], SamplingSpec(max_tokens=13, bad_words_token_ids=[[c] for c in CODES]))
+    state = proc.prepare_request(req)
+    req.compresslm_state = state
+    state.blocks = [SimpleNamespace(block_id=i, code_span=(100 * i + 20, 100 * i + 24), response_content_positions=[])
+                    for i in range(4)]
+    proc.reset_for_preemption(state)
+    req.num_computed_tokens = 0
+    assert len(proc.code_physical_spans(req, 0)) == 4
+    for limit, expected in [(0, 0), (23, 0), (24, 1), (124, 2), (224, 3), (324, 4), (10_000, 4)]:
+        got = proc.code_physical_spans(req, 0, limit)
+        assert len(got) == expected and all(e <= limit for _, e in got)
+
+
+def test_request_validation():
+    _, proc = make()
+    with pytest.raises(ValueError):
+        proc.prepare_request(ServingRequest("a", [1, 2], SamplingSpec(bad_words_token_ids=[])))
+    with pytest.raises(ValueError):
+        proc.prepare_request(ServingRequest("a", [], SamplingSpec(bad_words_token_ids=[[c] for c in CODES])))
+    with pytest.raises(ValueError):
+        CompressLMProcessor(CompressLMConfig(enable=True, block_size=4, num_code_tokens=4))
