@@ -18,13 +18,9 @@
 // Tiles are classified per workgroup from the mask arithmetic when C and K are multiples of 64: empty tiles are
 // skipped without loading, full tiles run unmasked, partial tiles evaluate the mask per element. Unaligned shapes run
 // every tile as partial (correct, slower).
-#include "common.h"
+#include "attn_tile.h"
 
 namespace abkv {
-
-constexpr int kBM = 64;                  // query rows per workgroup
-constexpr int kBN = 64;                  // keys per tile
-constexpr int kTileElems = kBN * kHeadDim;
 
 struct PrefillArgs {
   const __bf16* q;  long q_sb, q_ss, q_sh;   // [B, S0, 32, 128]
@@ -39,17 +35,6 @@ struct PrefillArgs {
   int aligned;                               // C % 64 == 0 && K % 64 == 0
   int num_q_tiles;
 };
-
-// Element visibility (the closed-form mask), used on partial tiles.
-__device__ __forceinline__ bool visible(int q, int kv, int C, int per, int plen, int quota) {
-  const int qb = q / per, kb = kv / per;
-  const int qw = q - qb * per, kw = kv - kb * per;
-  const bool kc = kw < C;
-  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen);
-  v = v && kv <= q;
-  v = v || (qw >= C && !kc && kb == qb);
-  return v && (kc || kw - C < quota);
-}
 
 // Tile class for an aligned layout: 0 empty, 1 full, 2 partial.
 __device__ __forceinline__ int classify(int q0, int k0, int C, int per, int plen, int qmin, int qmax) {
@@ -77,155 +62,6 @@ __device__ __forceinline__ int classify(int q0, int k0, int C, int per, int plen
   if (slot0 + kBN <= qmin) return 1;
   if (slot0 >= qmax) return 0;
   return 2;
-}
-
-__device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
-
-#define ABKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// K/V tiles live in LDS as 64 rows x 256 B without padding; 16-byte chunk c of row r is stored at chunk c ^ (r % 16),
-// which makes both operand read patterns conflict-free (16 lanes hit 16 distinct chunks). Tiles are filled with
-// global_load_lds_dwordx4: a wave instruction writes 1 KiB contiguously (lane L -> bytes 16L), so each lane fetches
-// the global chunk that belongs at its swizzled position. Rows past the sequence end re-read the last row (finite data,
-// masked to probability 0).
-template <int kWaves>
-__device__ __forceinline__ void issue_tile(const __bf16* kg, long k_ss, const __bf16* vg, long v_ss, int k0, int S0,
-                                           __bf16* Kbuf, __bf16* Vbuf, int w, int lane) {
-  constexpr int kPerWave = 16 / kWaves;        // 1 KiB blocks of the 16 KiB K (and V) tile per wave
-#pragma unroll
-  for (int n = 0; n < kPerWave; ++n) {
-    const int blk = kPerWave * w + n;
-    const int row = 4 * blk + (lane >> 4);
-    const int logical = (lane & 15) ^ (row & 15);
-    const int key = min(k0 + row, S0 - 1);
-    __builtin_amdgcn_global_load_lds((const void*)(kg + (long)key * k_ss + 8 * logical), ABKV_LDS(Kbuf + 512 * blk),
-                                     16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(vg + (long)key * v_ss + 8 * logical), ABKV_LDS(Vbuf + 512 * blk),
-                                     16, 0, 0);
-  }
-}
-
-__device__ __forceinline__ u32x4 lds16(const __bf16* buf, int row, int chunk) {
-  return *reinterpret_cast<const u32x4*>(buf + row * kHeadDim + 8 * (chunk ^ (row & 15)));
-}
-
-struct TileMask {
-  int mode;        // 0 none, 1 key <= qrow (diagonal), 2 key < limit[u], 3 general (per-element arithmetic)
-  int limit[4];
-};
-
-// Attention of this wave's 64 columns against one 64-key tile held in (Kbuf, Vbuf).
-template <int H, bool kAligned>
-__device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* Vbuf, const bf16x8 (&qop)[H][4],
-                                             floatx4 (&o)[8][H], float (&m_run)[H], float (&l_run)[H], int k0,
-                                             const TileMask& tm, int qrow, const PrefillArgs& a, int per, int plen,
-                                             const int (&quota)[H], int hbase, int m16, int j) {
-  // aligned layouts: every partial tile is "key < lim[u]" with a per-column limit (uniform per head or qrow + 1)
-  int lim[H];
-#pragma unroll
-  for (int u = 0; u < H; ++u) lim[u] = tm.mode == 1 ? qrow + 1 : tm.limit[hbase + u];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    // S^T = K . Q^T for 32 keys: s[t][u][r] = raw score of key k0 + 32kk + 16t + 4j + r, column (head u, qrow)
-    floatx4 s[2][H];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int u = 0; u < H; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const bf16x8 kop = __builtin_bit_cast(bf16x8, lds16(Kbuf, 32 * kk + 16 * t + m16, 4 * i + j));
-#pragma unroll
-        for (int u = 0; u < H; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
-      }
-    if (tm.mode != 0) {
-      const int kb = k0 + 32 * kk + 4 * j;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int u = 0; u < H; ++u)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int kv = kb + 16 * t + r;
-            bool ok;
-            if constexpr (kAligned) {
-              ok = kv < lim[u];
-            } else {
-              ok = kv < a.S0 && qrow < a.S0 && visible(qrow, kv, a.C, per, plen, quota[u]);
-            }
-            s[t][u][r] = ok ? s[t][u][r] : -INFINITY;
-          }
-    }
-    float tmax[H];
-#pragma unroll
-    for (int u = 0; u < H; ++u) {
-      float mx = fmaxf(fmaxf(fmaxf(s[0][u][0], s[0][u][1]), fmaxf(s[0][u][2], s[0][u][3])),
-                       fmaxf(fmaxf(s[1][u][0], s[1][u][1]), fmaxf(s[1][u][2], s[1][u][3])));
-      mx = max_xor16(mx);
-      mx = max_xor32(mx);
-      tmax[u] = mx * a.scale_log2;                          // log2-domain max (scale > 0)
-    }
-    // lazy rescale: the running max moves only when a column max grows by more than 8 (2^8 headroom in P)
-    bool need = false;
-#pragma unroll
-    for (int u = 0; u < H; ++u) need |= tmax[u] > m_run[u] + 8.f;
-    if (__any(need)) {
-#pragma unroll
-      for (int u = 0; u < H; ++u) {
-        const float m_new = fmaxf(m_run[u], tmax[u]);
-        const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
-        m_run[u] = m_new;
-        l_run[u] *= alpha;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
-      }
-    }
-    bf16x8 pop[H];
-#pragma unroll
-    for (int u = 0; u < H; ++u) {
-      const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
-      float ps = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = fast_exp2(fmaf(s[t][u][r], a.scale_log2, neg_m));
-          s[t][u][r] = p;
-          ps += p;
-        }
-      l_run[u] += ps;
-      u32x4 pw;
-      pw[0] = pack_bf16x2(s[0][u][0], s[0][u][1]);
-      pw[1] = pack_bf16x2(s[0][u][2], s[0][u][3]);
-      pw[2] = pack_bf16x2(s[1][u][0], s[1][u][1]);
-      pw[3] = pack_bf16x2(s[1][u][2], s[1][u][3]);
-      pop[u] = __builtin_bit_cast(bf16x8, pw);
-    }
-    // O^T += V^T . P^T over the same 32 keys (P^T row e: e<4 -> key 32kk+4j+e, e>=4 -> key 32kk+16+4j+e-4)
-    u32x4 vr[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      vr[e] = lds16(Vbuf, 32 * kk + 4 * j + e, m16);
-      vr[4 + e] = lds16(Vbuf, 32 * kk + 16 + 4 * j + e, m16);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 lo, hi;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x05040100u);
-        hi[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x07060302u);
-      }
-      const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
-#pragma unroll
-      for (int u = 0; u < H; ++u) {
-        o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
-        o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
-      }
-    }
-  }
 }
 
 // Class of key tile kt for this query tile: 0 skip, otherwise fills the mask mode.
@@ -281,7 +117,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const int q0 = qt * kBM;
   const int qrow = q0 + 16 * rg + m16;                      // this lane's query row (MFMA column)
   const int plen = a.prompt_len ? a.prompt_len[b] : 0;
-  int quota_all[4], quota[H];
+  int quota_all[4];
   int qmin = 1 << 30, qmax = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -289,8 +125,6 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     qmin = min(qmin, quota_all[u]);
     qmax = max(qmax, quota_all[u]);
   }
-#pragma unroll
-  for (int u = 0; u < H; ++u) quota[u] = quota_all[hbase + u];
 
   bf16x8 qop[H][4];
   {
@@ -317,8 +151,9 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     l_run[u] = 0.f;
   }
 
-  const __bf16* kg = a.k + (long)b * a.k_sb + (long)kvh * a.k_sh;
-  const __bf16* vg = a.v + (long)b * a.v_sb + (long)kvh * a.v_sh;
+  const DenseRows rows{a.k + (long)b * a.k_sb + (long)kvh * a.k_sh, a.v + (long)b * a.v_sb + (long)kvh * a.v_sh,
+                       a.k_ss, a.v_ss};
+  const MaskGeom geo{qrow, a.S0, a.C, per, plen, quota_all};
   const int n_k_tiles = (a.S0 + kBN - 1) / kBN;
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
@@ -326,7 +161,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   TileMask tm_cur, tm_nxt;
   int cur = 0;
   while (cur < n_k_tiles && !tile_class(a, cur, q0, q_last, per, plen, qmin, qmax, quota_all, tm_cur)) ++cur;
-  if (cur < n_k_tiles) issue_tile<kWaves>(kg, a.k_ss, vg, a.v_ss, cur * kBN, a.S0, Kb, Vb, w, lane);
+  if (cur < n_k_tiles) issue_tile<kWaves>(rows, cur * kBN, a.S0, Kb, Vb, w, lane);
   int parity = 0;
   while (cur < n_k_tiles) {
     int nxt = cur + 1;
@@ -335,15 +170,15 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     // Plain s_barrier (no workgroup fence): a fence would wait for the prefetch just issued. Each wave waits for
     // its own DMA of the current tile (vmcnt), the barrier then publishes every wave's part.
     if (nxt < n_k_tiles) {
-      issue_tile<kWaves>(kg, a.k_ss, vg, a.v_ss, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
+      issue_tile<kWaves>(rows, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
       if constexpr (kWaves == 4) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
       else __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
-    tile_compute<H, kAligned>(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow, a, per,
-                              plen, quota, hbase, m16, j);
+    tile_compute<H, kAligned>(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow + 1,
+                              a.scale_log2, geo, hbase, m16, j);
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are complete
     __builtin_amdgcn_s_barrier();                           // the buffer just read is refilled next iteration
     cur = nxt;

@@ -226,5 +226,59 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     return out, lse
 
 
+def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start, kv_start,
+                            kv_limit, causal: bool, scale: float | None = None, out: torch.Tensor | None = None,
+                            lse: torch.Tensor | None = None):
+    """Multi-query attention over the paged cache (prompt chunks: causal; CompressLM code step: non-causal with
+    kv_limit = physical code start + quota).
+
+    q [T, 32, 128] bf16; block_table [B, W] int32 on the GPU; q_start [B+1], kv_start [B], kv_limit [B]: host
+    sequences (the metadata builder's CPU copies) -- request r's queries are tokens q_start[r]..q_start[r+1]-1 at
+    physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
+    Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None).
+    """
+    import numpy as np
+
+    _check_cache(kv_cache)
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1, "q must be cuda bf16 [T, 32, 128] with contiguous dims")
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    qs = np.asarray(q_start, dtype=np.int64)
+    ks = np.asarray(kv_start, dtype=np.int64)
+    kl = np.asarray(kv_limit, dtype=np.int64)
+    B = ks.size
+    W = block_table.shape[1]
+    _require(qs.size == B + 1 and kl.size == B and B <= block_table.shape[0], "q_start [B+1], kv_start/kv_limit [B]")
+    _require(qs[0] == 0 and np.all(np.diff(qs) >= 0) and qs[-1] <= q.shape[0], "q_start must be a prefix sum <= T")
+    _require(np.all(kl >= 0) and np.all(kl <= W * PAGE), "kv_limit must lie in [0, block_table width * 16]")
+    _require(np.all(ks >= 0), "kv_start must be non-negative")
+    T = q.shape[0]
+    if out is None:
+        out = torch.empty((T, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (T, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
+             "out must be bf16 [T, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (T, HEADS_Q),
+                 "lse must be contiguous fp32 [T, 32]")
+    nq = np.diff(qs)
+    tiles = [(r, q0) for r in range(B) for q0 in range(0, int(nq[r]), 64)]
+    if not tiles:
+        return out, lse
+    tr = np.asarray(tiles, dtype=np.int32)
+    dev = q.device
+    meta = torch.from_numpy(np.concatenate([qs, ks, kl]).astype(np.int32)).to(dev)
+    tl = torch.from_numpy(np.ascontiguousarray(tr.T)).to(dev)
+    q_start_d, kv_start_d, kv_limit_d = meta[: B + 1], meta[B + 1: 2 * B + 1], meta[2 * B + 1:]
+    scale = default_scale() if scale is None else float(scale)
+    rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                       _ptr(block_table), block_table.stride(0), W, _ptr(q_start_d),
+                                       _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
+                                       int(bool(causal)), scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+                                       C.c_void_p(_stream()))
+    check(rc, "abkv_paged_prefill_attn")
+    return out, lse
+
+
 def default_scale() -> float:
     return 1.0 / math.sqrt(HEAD_DIM)
