@@ -6,7 +6,7 @@
 // them and to the first q_g code rows of their own block (own-block slots >= q_g are hidden). In a group's physical
 // layout that is exactly "keys < code_start + q_g", so each request carries a key limit instead of a dense mask:
 //   query row i of request r sits at physical position kv_start[r] + i and sees keys k < kv_limit[r]
-//   (and k <= its own position when causal).
+//   (and k <= its own position when request r is causal; a batch may mix causal chunks and code steps).
 // Prompt chunks are the causal case with kv_limit = seq_len. Same tile machinery as the masked-prefill kernel
 // (attn_tile.h): 8 waves x (16 rows x 2 heads), 64-key tiles DMA'd from the page table into double-buffered LDS.
 #include "attn_tile.h"
@@ -22,7 +22,8 @@ struct PagedPrefillArgs {
   const int32_t* kv_limit;                     // [B] visible keys: physical slots [0, kv_limit)
   const int32_t* tile_req;                     // [n_tiles] request of each 64-row query tile
   const int32_t* tile_q0;                      // [n_tiles] first query row (within its request) of the tile
-  int causal;
+  const int32_t* causal;                       // [B] 1 = causal, 0 = non-causal (nullptr: causal_default)
+  int causal_default;
   float scale_log2;
   __bf16* out; long o_st, o_sh;                // [T, 32, 128]
   float* lse;                                  // [T, 32] natural log, or nullptr
@@ -47,10 +48,11 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const int nq = a.q_start[r + 1] - t0;
   const int kv0 = a.kv_start[r];
   const int limit = a.kv_limit[r];
+  const bool causal = a.causal ? a.causal[r] != 0 : a.causal_default != 0;
   const int qi = q0 + 16 * rg + m16;                        // query row within the request (MFMA column)
   const bool qvalid = qi < nq;
   const int pos = kv0 + qi;
-  const int lane_limit = a.causal ? min(limit, pos + 1) : limit;
+  const int lane_limit = causal ? min(limit, pos + 1) : limit;
 
   bf16x8 qop[H][4];
   {
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
 
   // key range of the tile: the largest lane limit bounds the walk, the smallest one marks the fully visible tiles
   const int q_hi = min(q0 + kBM, nq) - 1;
-  const int k_end = a.causal ? min(limit, kv0 + q_hi + 1) : limit;
-  const int k_full = a.causal ? min(limit, kv0 + q0 + 1) : limit;
+  const int k_end = causal ? min(limit, kv0 + q_hi + 1) : limit;
+  const int k_full = causal ? min(limit, kv0 + q0 + 1) : limit;
   const int n_k_tiles = (k_end + kBN - 1) / kBN;
   const PagedRows rows{a.kv + kvh * kHeadDim, a.block_table + (long)r * a.bt_stride, a.bt_width, a.num_pages};
   const MaskGeom geo{};
@@ -130,7 +132,8 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
                             const int32_t* block_table, long block_table_stride, int block_table_width,
                             const int32_t* q_start,
                             const int32_t* kv_start, const int32_t* kv_limit, const int32_t* tile_req,
-                            const int32_t* tile_q0, int num_tiles, int causal, float scale, void* out,
+                            const int32_t* tile_q0, int num_tiles, const int32_t* causal, int causal_default,
+                            float scale, void* out,
                             long out_stride_t, long out_stride_h, float* lse, hipStream_t stream) {
   using namespace abkv;
   if (num_tiles <= 0) return 0;
@@ -153,6 +156,7 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
   a.tile_req = tile_req;
   a.tile_q0 = tile_q0;
   a.causal = causal;
+  a.causal_default = causal_default;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out = static_cast<__bf16*>(out);
   a.o_st = out_stride_t;

@@ -227,7 +227,7 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
 
 
 def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start, kv_start,
-                            kv_limit, causal: bool, scale: float | None = None, out: torch.Tensor | None = None,
+                            kv_limit, causal, scale: float | None = None, out: torch.Tensor | None = None,
                             lse: torch.Tensor | None = None):
     """Multi-query attention over the paged cache (prompt chunks: causal; CompressLM code step: non-causal with
     kv_limit = physical code start + quota).
@@ -235,6 +235,7 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     q [T, 32, 128] bf16; block_table [B, W] int32 on the GPU; q_start [B+1], kv_start [B], kv_limit [B]: host
     sequences (the metadata builder's CPU copies) -- request r's queries are tokens q_start[r]..q_start[r+1]-1 at
     physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
+    ``causal``: a bool for the whole batch or one flag per request (code steps and prompt chunks may share a batch).
     Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None).
     """
     import numpy as np
@@ -267,14 +268,16 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
         return out, lse
     tr = np.asarray(tiles, dtype=np.int32)
     dev = q.device
-    meta = torch.from_numpy(np.concatenate([qs, ks, kl]).astype(np.int32)).to(dev)
+    cz = np.broadcast_to(np.asarray(causal, dtype=np.int64), (B,)).astype(np.int64)
+    meta = torch.from_numpy(np.concatenate([qs, ks, kl, cz]).astype(np.int32)).to(dev)
     tl = torch.from_numpy(np.ascontiguousarray(tr.T)).to(dev)
-    q_start_d, kv_start_d, kv_limit_d = meta[: B + 1], meta[B + 1: 2 * B + 1], meta[2 * B + 1:]
+    q_start_d, kv_start_d = meta[: B + 1], meta[B + 1: 2 * B + 1]
+    kv_limit_d, causal_d = meta[2 * B + 1: 3 * B + 1], meta[3 * B + 1:]
     scale = default_scale() if scale is None else float(scale)
     rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                        _ptr(block_table), block_table.stride(0), W, _ptr(q_start_d),
                                        _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
-                                       int(bool(causal)), scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+                                       _ptr(causal_d), 1, scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
                                        C.c_void_p(_stream()))
     check(rc, "abkv_paged_prefill_attn")
     return out, lse

@@ -94,14 +94,16 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
  * third_party/vllm_overlay/vllm/v1/worker/compresslm_masks.py:165-239 and gpu_model_runner.py:2042-2107): in a group's
  * physical layout the code step's mask is "keys < code_start + q_g", so each request carries a key limit.
  * q [T, 32, 128] (token stride, head stride), request r's queries are tokens [q_start[r], q_start[r+1]) at physical
- * positions kv_start[r] + i and see keys < kv_limit[r] (and <= their position when causal). tile_req / tile_q0
- * [num_tiles] list the 64-row query tiles (request, first row). All index arrays are device int32. lse [T, 32] or NULL.
+ * positions kv_start[r] + i and see keys < kv_limit[r] (and <= their position when request r is causal: causal[r] != 0,
+ * or causal_default when causal is NULL). tile_req / tile_q0 [num_tiles] list the 64-row query tiles (request, first
+ * row). All index arrays are device int32. lse [T, 32] or NULL.
  * ------------------------------------------------------------------------------------------------------------- */
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
                             const int32_t* block_table, long block_table_stride, int block_table_width,
                             const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
-                            const int32_t* tile_req, const int32_t* tile_q0, int num_tiles, int causal, float scale,
-                            void* out, long out_stride_t, long out_stride_h, float* lse, abkv_stream_t stream);
+                            const int32_t* tile_req, const int32_t* tile_q0, int num_tiles, const int32_t* causal,
+                            int causal_default, float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
+                            abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager

@@ -1,0 +1,137 @@
+"""Attention backend host logic (no GPU): the code-step mask restatement, its conversion into per-request key
+limits, and metadata validation."""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from abridgekv_amd import backend as bk
+from oracle import masks as om
+
+
+def test_oracle_causal_mask_is_shifted_tril():
+    for ql, sl in [(1, 1), (5, 5), (3, 9), (7, 40)]:
+        m = om.request_mask(ql, sl, [], None, 256, 256, causal=True)
+        assert np.array_equal(m, np.tril(np.ones((ql, sl), bool), k=sl - ql))
+
+
+@pytest.mark.parametrize("quota", [1, 2, 64, 128, 255, 256])
+def test_oracle_code_mask_is_prefix_below_code_start_plus_quota(quota):
+    """Physical quotas on the code step: queries = the block's K=256 code rows at the end; keys < start + q."""
+    K, resident = 256, 700
+    sl = resident + K
+    m = om.request_mask(K, sl, [(resident, sl)], None, quota, K, causal=False)
+    expect = np.broadcast_to(np.arange(sl) < resident + min(quota, K), (K, sl))
+    assert np.array_equal(m, expect)
+
+
+def test_oracle_mask_exclusion_and_several_spans_brute_force():
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        sl = int(rng.integers(20, 60))
+        ql = int(rng.integers(1, 8))
+        causal = bool(rng.integers(2))
+        cuts = np.sort(rng.choice(np.arange(sl - ql), 4, replace=False))
+        spans = [(int(cuts[0]), int(cuts[1])), (int(cuts[2]), int(cuts[3]))]
+        ex = (1, 3) if rng.integers(2) else None
+        q, K = int(rng.integers(0, 6)), 4
+        hidden = set()
+        if q < K:
+            for s, e in spans:
+                hidden |= set(range(s + q, e))
+        if ex is not None:
+            hidden |= set(range(*ex))
+        m = om.request_mask(ql, sl, spans, ex, q, K, causal)
+        for i in range(ql):
+            vis = {c for c in range(sl) if (c <= sl - ql + i or not causal)} - hidden
+            assert set(np.flatnonzero(m[i]).tolist()) == vis
+
+
+def _mixed_batch(rng):
+    """Requests (query_len, seq_len, code_span or None, causal) of one group in one step."""
+    reqs = []
+    for _ in range(int(rng.integers(1, 6))):
+        kind = int(rng.integers(3))
+        if kind == 0:                          # code step: 16 code rows after a resident prefix
+            res = int(rng.integers(0, 90))
+            reqs.append((16, res + 16, (res, res + 16), False))
+        elif kind == 1:                        # causal chunk after some context
+            ql = int(rng.integers(1, 30))
+            reqs.append((ql, ql + int(rng.integers(0, 50)), None, True))
+        else:                                  # decode
+            reqs.append((1, int(rng.integers(1, 80)), None, True))
+    return reqs
+
+
+@pytest.mark.parametrize("quota", [1, 5, 16, 40])
+def test_custom_mask_converts_to_code_step_limits(quota):
+    K = 16
+    rng = np.random.default_rng(quota)
+    for _ in range(10):
+        reqs = _mixed_batch(rng)
+        flat = np.concatenate([om.request_mask(ql, sl, [span] if span else [], None, quota, K, causal).reshape(-1)
+                               for ql, sl, span, causal in reqs])
+        qsl = np.concatenate([[0], np.cumsum([r[0] for r in reqs])])
+        sls = [r[1] for r in reqs]
+        limits, causal = bk.limits_from_custom_mask(torch.from_numpy(flat), qsl, sls)
+        expect = bk.code_step_key_limits(qsl, sls, [r[2] for r in reqs], quota, K)
+        for r, (ql, sl, span, c) in enumerate(reqs):
+            if span is not None:
+                assert limits[r] == expect[r] and not causal[r]
+            elif ql > 1:
+                assert causal[r] and limits[r] == sl
+            else:                              # one query row: the causal row is the full prefix
+                assert limits[r] == sl
+
+
+def test_custom_mask_rejects_non_prefix_masks():
+    m = np.ones((2, 5), bool)
+    m[0, 2] = False
+    with pytest.raises(RuntimeError):
+        bk.limits_from_custom_mask(torch.from_numpy(m.reshape(-1)), [0, 2], [5])
+    m = np.zeros((3, 5), bool)
+    m[0, :1], m[1, :3], m[2, :2] = True, True, True
+    with pytest.raises(RuntimeError):
+        bk.limits_from_custom_mask(torch.from_numpy(m.reshape(-1)), [0, 3], [5])
+    with pytest.raises(RuntimeError):
+        bk.limits_from_custom_mask(torch.ones(9, dtype=torch.bool), [0, 2], [5])
+
+
+def test_code_step_limits_validate_spans():
+    assert list(bk.code_step_key_limits([0, 1, 5], [9, 20], [None, (16, 20)], 2, 4)) == [bk.NOT_CODE, 18]
+    assert list(bk.code_step_key_limits([0, 4], [20], [(16, 20)], 256, 4)) == [20]
+    with pytest.raises(RuntimeError):
+        bk.code_step_key_limits([0, 4], [20], [(15, 19)], 2, 4)      # not the request's own query rows
+    with pytest.raises(RuntimeError):
+        bk.code_step_key_limits([0, 4], [20], [(18, 22)], 2, 4)
+
+
+def test_metadata_builder_validation():
+    b = bk.AbridgeMetadataBuilder(max_num_seqs=4, max_pages=8, device="cpu")
+    b._workspace = torch.empty(0)                      # keep the CPU test off the native library
+    bt = torch.zeros((4, 8), dtype=torch.int32)
+    sm = torch.zeros(8, dtype=torch.int64)
+    md = b.build([0, 1, 2, 6], [10, 30, 40], bt, sm, seq_lens_dev=torch.zeros(3, dtype=torch.int32))
+    assert (md.num_decodes, md.num_decode_tokens, md.num_actual_tokens, md.max_decode_pages) == (2, 2, 6, 2)
+    with pytest.raises(RuntimeError):                  # a decode after a chunk
+        b.build([0, 4, 5], [10, 30], bt, sm, seq_lens_dev=torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(RuntimeError):                  # past the table width
+        b.build([0, 1], [129], bt, sm, seq_lens_dev=torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(RuntimeError):                  # code limit outside the query rows
+        b.build([0, 4], [20], bt, sm, code_key_limit=[10], seq_lens_dev=torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(RuntimeError):
+        b.build([0] * 6, [1] * 5, bt, sm)
+    md = b.build([0, 4], [20], bt, sm, code_key_limit=[18], seq_lens_dev=torch.zeros(1, dtype=torch.int32))
+    assert md.num_decodes == 0 and md.workspace is None
+
+
+def test_backend_surface_and_hook_is_inert_without_impl():
+    assert bk.AbridgeAttentionBackend.get_kv_cache_shape(10) == (10, 2, 16, 8, 128)
+    with pytest.raises(NotImplementedError):
+        bk.AbridgeAttentionBackend.get_kv_cache_shape(10, block_size=32)
+    with pytest.raises(NotImplementedError):
+        bk.AbridgeAttentionImpl(num_heads=16)
+    out = torch.full((2, 32 * 128), 3.0)
+    bk.maybe_override_attention(SimpleNamespace(), torch.zeros(2, 32 * 128), torch.zeros(1), object(), out)
+    assert bool((out == 3.0).all())

@@ -93,3 +93,22 @@ def test_rejects_limits_past_the_table():
     with pytest.raises(ValueError):
         ops.paged_prefill_attention(torch.zeros((2, 32, 128), dtype=torch.bfloat16, device=dev), cache,
                                     torch.zeros((1, 2), dtype=torch.int32, device=dev), [0, 2], [0], [33], True)
+
+
+def test_mixed_code_and_prompt_chunk_batch():
+    """One launch mixing a non-causal code step (limit = code start + quota) with causal prompt chunks."""
+    nq = [256, 130, 1]
+    kv_start = [640, 0, 377]
+    limits = [640 + 128, 130, 378]
+    causal = [False, True, True]
+    cache, tables = _setup([max(s + n, l) for s, n, l in zip(kv_start, nq, limits)], 200, 4)
+    g = torch.Generator().manual_seed(5)
+    q_start = np.concatenate([[0], np.cumsum(nq)]).tolist()
+    q = torch.randn((q_start[-1], 32, 128), generator=g).to(torch.bfloat16)
+    out, lse = _run(cache, tables, q, q_start, kv_start, limits, causal)
+    cf = cache.float().numpy()
+    for r in range(len(nq)):
+        ro, rl = _oracle(q[q_start[r]: q_start[r + 1]].float().numpy(), cf, tables[r], kv_start[r], limits[r],
+                         causal[r])
+        assert np.abs(out[q_start[r]: q_start[r + 1]] - ro).max() <= TOL
+        assert np.abs(lse[q_start[r]: q_start[r + 1]] - rl).max() <= TOL
