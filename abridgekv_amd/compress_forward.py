@@ -1,0 +1,320 @@
+"""Teacher-forced CompressLM forward over the masked-prefill kernel (the training/evaluation entry point).
+
+Mirrors the served subset of abridgekv/compress_forward.py:240-1230 (``CompressLM``): one pause pass (L=1) with
+bidirectional code<->code attention in a block (``pause_xattn="full"``), optional raw prompt, optional fixed
+per-(layer, KV head) code quotas, ``active_code_rows`` and ``appended`` / ``bitrev`` code positions. The sequence
+layout, RoPE positions, loss positions and loss reductions follow the reference (compress_forward.py:20-88,
+1044-1071, 957-1042, 1134-1230); the attention of every decoder layer runs ``abkv_prefill_masked_attn`` through a
+HuggingFace attention function registered as ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask
+(``_arith_mask_mod`` / ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 695-727,
+815-894). The mask is never materialised: the kernel evaluates it from (C, K, N, prompt_len, head quota).
+
+Options of the reference that belong to other experiments (replay / raw / retained tails, learned or segment
+pooling, query residuals, copy and distillation losses, external block masks) raise NotImplementedError. The
+kernel has no backward: a backward pass through this forward raises RuntimeError.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+from .config import bitrev_offsets
+
+ATTN_IMPLEMENTATION = "abridgekv_hip"
+
+
+@dataclass(frozen=True)
+class CompressMask:
+    """What the kernel needs to evaluate the compression mask (the analogue of the reference's BlockMask):
+    N blocks of [C content | K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
+    ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K)."""
+    block_c: int
+    codes_k: int
+    num_blocks: int
+    prompt_len: torch.Tensor | None = None
+    head_quota: torch.Tensor | None = None
+
+
+class _MaskedPrefill(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, mask: CompressMask, layer_idx: int, scale: float):
+        hq = None if mask.head_quota is None else mask.head_quota[layer_idx]
+        out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
+                                              prompt_len=mask.prompt_len, head_quota=hq, scale=scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        raise RuntimeError("the masked-prefill kernel has no backward pass; run CompressLM.forward under "
+                           "torch.no_grad() or train with another attention implementation")
+
+
+def masked_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """HuggingFace attention function: query [B, 32, S0, 128], key/value [B, 8, S0, 128] bf16 ->
+    (out [B, S0, 32, 128], None). ``attention_mask`` must be a :class:`CompressMask`."""
+    if not isinstance(attention_mask, CompressMask):
+        raise TypeError(f"{ATTN_IMPLEMENTATION} attention needs a CompressMask, got {type(attention_mask).__name__}")
+    if dropout:
+        raise NotImplementedError("attention dropout is not supported")
+    if kwargs.get("sliding_window"):
+        raise NotImplementedError("sliding-window attention is not supported")
+    scale = ops.default_scale() if scaling is None else float(scaling)
+    out = _MaskedPrefill.apply(query.transpose(1, 2), key.transpose(1, 2), value.transpose(1, 2), attention_mask,
+                               int(module.layer_idx), scale)
+    return out, None
+
+
+def register_attention() -> None:
+    """Register ``"abridgekv_hip"`` with transformers' attention interface (idempotent)."""
+    from transformers import AttentionInterface
+    AttentionInterface.register(ATTN_IMPLEMENTATION, masked_attention_forward)
+
+
+def roles(C: int, N: int, K: int, device=None):
+    """(blk, role) per row of the L=1 layout: role 0 = content, 1 = code (compress_forward.py:20-31)."""
+    per = C + K
+    within = torch.arange(per, device=device).repeat(N)
+    blk = torch.arange(N, device=device).repeat_interleave(per)
+    return blk, (within >= C).long()
+
+
+def content_abs_pos(C: int, N: int, K: int, device=None) -> torch.Tensor:
+    """Absolute content index b*C + j of content rows; N*C for code rows (compress_forward.py:72-88, no replay)."""
+    per = C + K
+    within = torch.arange(per, device=device).repeat(N)
+    blk = torch.arange(N, device=device).repeat_interleave(per)
+    return torch.where(within < C, blk * C + within, torch.full_like(within, N * C))
+
+
+def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, device=None) -> torch.Tensor:
+    """(1, N*(C+K_act)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, L=1,
+    no replay tail, no copy rows)."""
+    per_full, per_act = C + K, C + K_act
+    idx = torch.arange(N * per_act, device=device)
+    within, blk = idx % per_act, idx // per_act
+    is_code = within >= C
+    p = (within - C).clamp_min(0)
+    if code_positions == "bitrev":
+        offs = torch.from_numpy(bitrev_offsets(K, C)).to(device)
+        pos = torch.where(is_code, blk * C + offs[p.clamp_max(K - 1)], blk * C + within)
+    else:
+        pos = torch.where(is_code, blk * per_full + C + p, blk * per_full + within)
+    return pos.view(1, -1)
+
+
+_UNSUPPORTED = ("pool_init", "query_residual", "code_q_heads", "code_kv_heads", "seg_pool", "gated_seg_pool",
+                "raw_tail", "replay_tail", "code_exclude_replay_tail", "retain_tail_kv")
+
+
+class CompressLM(nn.Module):
+    """API-compatible subset of the reference ``CompressLM(base_model, C, N, K, ...)``.
+
+    ``base_model`` is a HuggingFace causal LM with 32 query heads, 8 KV heads and head size 128 in bf16 (e.g.
+    Qwen3-4B or a random model of that attention shape); its attention implementation is switched to
+    ``"abridgekv_hip"``.
+    """
+
+    def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", head_code_quotas=None, active_code_rows=None,
+                 code_positions="appended", retain_tail_policy="rolling", **options):
+        super().__init__()
+        bad = sorted(name for name in options if name not in _UNSUPPORTED)
+        if bad:
+            raise TypeError(f"unexpected CompressLM options {bad}")
+        used = sorted(name for name, value in options.items() if value)
+        if used:
+            raise NotImplementedError(f"CompressLM options {used} are not supported by the native forward")
+        if L != 1:
+            raise NotImplementedError("only one pause pass (L=1) is supported")
+        if pause_xattn != "full":
+            raise NotImplementedError("only pause_xattn='full' (bidirectional codes) is supported")
+        if retain_tail_policy != "rolling":
+            raise ValueError(f"retain_tail_policy={retain_tail_policy!r} requires retain_tail_kv > 0")
+        if code_positions not in ("appended", "bitrev"):
+            raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
+        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1)):
+            raise ValueError("code_positions='bitrev' needs power-of-two C and K, L=1 and no tails")
+        cfg = base_model.config
+        heads, kv_heads = int(cfg.num_attention_heads), int(getattr(cfg, "num_key_value_heads", cfg.num_attention_heads))
+        head_dim = int(getattr(cfg, "head_dim", None) or cfg.hidden_size // heads)
+        if (heads, kv_heads, head_dim) != (ops.HEADS_Q, ops.HEADS_KV, ops.HEAD_DIM):
+            raise NotImplementedError(f"the kernels need {ops.HEADS_Q} query heads, {ops.HEADS_KV} KV heads and "
+                                      f"head size {ops.HEAD_DIM}; got {(heads, kv_heads, head_dim)}")
+        register_attention()
+        self.model = base_model
+        self.model.config._attn_implementation = ATTN_IMPLEMENTATION
+        self.C, self.N, self.K, self.L = int(C), int(N), int(K), 1
+        self.pause_xattn, self.code_positions = pause_xattn, code_positions
+        self.replay_tail = self.raw_tail = self.retain_tail_kv = self.code_excluded_tail = 0
+        self.K_act = int(active_code_rows) if active_code_rows else self.K
+        if not 1 <= self.K_act <= self.K:
+            raise ValueError(f"active_code_rows must be in [1, K={K}], got {active_code_rows}")
+        d = int(cfg.hidden_size)
+        std = getattr(cfg, "initializer_range", 0.02)
+        dev = next(base_model.parameters()).device
+        self.pause = nn.Parameter(torch.empty(self.K, d, device=dev).normal_(0, std))
+        self.num_layers = len(self.model.model.layers)
+        self.num_attention_heads, self.num_kv_heads = heads, kv_heads
+        self.num_key_value_groups = heads // kv_heads
+        self._set_layout(self.N)
+        self.set_head_code_quotas(head_code_quotas)
+
+    def _set_layout(self, N):
+        dev = self.pause.device
+        C, Ka = self.C, self.K_act
+        blk, role = roles(C, N, Ka, dev)
+        content = role == 0
+        pf = torch.tensor([k for k in range(N * C) if k % C != C - 1], device=dev, dtype=torch.long)
+        layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev),
+                  "loss_pos": content & torch.roll(content, -1), "content_pos": content.nonzero(as_tuple=True)[0],
+                  "predict_flat": pf, "predict_block": pf // C,
+                  "_pos_ids": rope_position_ids(C, N, self.K, Ka, self.code_positions, dev)}
+        for name, value in layout.items():
+            self.register_buffer(name, value, persistent=False)
+
+    def set_N(self, N):
+        """Rebuild the N-dependent layout for a new block count (compress_forward.py set_N)."""
+        self.N = int(N)
+        self._set_layout(self.N)
+
+    def set_head_code_quotas(self, head_code_quotas):
+        """Fixed per-(layer, KV head) code quotas in [1, K_act] (compress_forward.py:516-575); None clears them."""
+        dev = self.pause.device
+        if head_code_quotas is None:
+            self.register_buffer("head_code_quotas", torch.empty((0, 0), dtype=torch.long, device=dev), False)
+            self.register_buffer("query_head_code_quotas", torch.empty((0, 0), dtype=torch.long, device=dev), False)
+            self.register_buffer("_head_quota_i32", None, False)
+            return
+        try:
+            raw = torch.as_tensor(head_code_quotas, device=dev)
+        except (TypeError, ValueError, RuntimeError) as exc:
+            raise ValueError("head_code_quotas must be a rectangular 2D integer array") from exc
+        expected = (self.num_layers, self.num_kv_heads)
+        if tuple(raw.shape) != expected:
+            raise ValueError(f"head_code_quotas must have shape {expected}, got {tuple(raw.shape)}")
+        if raw.dtype == torch.bool or (raw.is_floating_point() and bool((raw != raw.round()).any())):
+            raise ValueError("head_code_quotas must contain integers")
+        physical = raw.to(torch.long)
+        if bool(((physical <= 0) | (physical > self.K)).any()):
+            raise ValueError(f"head_code_quotas must be in [1, {self.K}]")
+        if bool((physical > self.K_act).any()):
+            raise ValueError(f"head_code_quotas exceed active_code_rows={self.K_act}")
+        expanded = physical.repeat_interleave(self.num_key_value_groups, dim=1)
+        self.register_buffer("head_code_quotas", physical, False)
+        self.register_buffer("query_head_code_quotas", expanded, False)
+        self.register_buffer("_head_quota_i32", expanded.to(torch.int32).contiguous(), False)
+
+    @property
+    def has_head_code_quotas(self) -> bool:
+        return self.head_code_quotas.numel() > 0
+
+    def compress_mask(self, batch: int, prompt_len: torch.Tensor | None = None, N: int | None = None) -> CompressMask:
+        N = self.N if N is None else int(N)
+        if prompt_len is not None:
+            prompt_len = prompt_len.to(device=self.pause.device, dtype=torch.int32).contiguous()
+            if prompt_len.numel() != batch:
+                raise ValueError("prompt_len must hold one length per sequence")
+        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32)
+
+    def _lm_ce(self, hid, tgt, chunk):
+        if chunk <= 0:
+            return F.cross_entropy(self.model.lm_head(hid).float(), tgt)
+        tot = hid.new_zeros((), dtype=torch.float32)
+        for i in range(0, hid.size(0), chunk):
+            tot = tot + F.cross_entropy(self.model.lm_head(hid[i:i + chunk]).float(), tgt[i:i + chunk],
+                                        reduction="sum")
+        return tot / hid.size(0)
+
+    def _per_token_lm_ce(self, hid, tgt, chunk):
+        step = hid.size(0) if chunk <= 0 else chunk
+        return torch.cat([F.cross_entropy(self.model.lm_head(hid[i:i + step]).float(), tgt[i:i + step],
+                                          reduction="none") for i in range(0, hid.size(0), step)])
+
+    def _masked_lm_ce(self, hid, tgt, mask, chunk):
+        den = mask.sum().clamp_min(1.0)
+        return (self._per_token_lm_ce(hid, tgt, chunk) * mask).sum() / den
+
+    def _perblock_ce(self, hid, tgt, blk_idx, nblk, reps):
+        ce = F.cross_entropy(self.model.lm_head(hid).float(), tgt, reduction="none")
+        blk = blk_idx.repeat(reps)
+        s = ce.new_zeros(nblk).scatter_add_(0, blk, ce)
+        c = ce.new_zeros(nblk).scatter_add_(0, blk, torch.ones_like(ce))
+        return ce.mean(), s / c.clamp_min(1.0)
+
+    def hidden_states(self, content_ids, prompt_len=None):
+        """Final-normed hidden states [B, S0, d] of the compressed teacher-forced layout."""
+        B, N, C = content_ids.shape
+        if C != self.C:
+            raise ValueError(f"content_ids block size {C} != C={self.C}")
+        if N != self.N:
+            self.set_N(N)
+        K = self.K_act
+        tok_e = self.model.model.embed_tokens(content_ids)
+        d = tok_e.size(-1)
+        pause_e = self.pause[:K].to(tok_e.dtype).view(1, 1, K, d).expand(B, N, K, d)
+        x = torch.cat([tok_e, pause_e], dim=2).reshape(B, N * (C + K), d)
+        if torch.is_autocast_enabled(x.device.type):
+            x = x.to(torch.get_autocast_dtype(x.device.type))
+        mask = self.compress_mask(B, prompt_len, N)
+        out = self.model.model(inputs_embeds=x, attention_mask={"full_attention": mask},
+                               position_ids=self._pos_ids, use_cache=False)
+        return out.last_hidden_state
+
+    def forward(self, content_ids, distill_lambda=0.0, copy_lambda=0.0, distill_temp=1.0, ce_chunk=0, baseline=False,
+                ctx_blocks=0, teacher_logits=None, teacher_hidden=None, block_ce=False, resp_mask=None,
+                raw_prompt=False, blockmask=None, per_token=False, include_cross_block=False,
+                boundary_recovery_width=0, boundary_recovery_weight=1.0, teacher_rows=None, teacher_head=None):
+        """Losses of the compressed teacher-forced forward, same signature and return dicts as
+        compress_forward.py:1134-1230 for the supported arguments (the full-context baseline, distillation, copy
+        and representation losses and external block masks raise NotImplementedError)."""
+        unsupported = {"baseline": bool(baseline), "ctx_blocks": bool(ctx_blocks), "distill_lambda": distill_lambda > 0,
+                       "copy_lambda": copy_lambda > 0, "teacher_logits": teacher_logits is not None,
+                       "teacher_hidden": teacher_hidden is not None, "blockmask": blockmask is not None,
+                       "teacher_rows": teacher_rows is not None, "teacher_head": teacher_head is not None}
+        used = sorted(name for name, on in unsupported.items() if on)
+        if used:
+            raise NotImplementedError(f"CompressLM.forward arguments {used} are not supported by the native forward")
+        B, N, C = content_ids.shape
+        dev = content_ids.device
+        prompt_len = None
+        if raw_prompt and resp_mask is not None:
+            rmf = resp_mask.reshape(B, N * C)
+            prompt_len = (rmf.cumsum(1) == 0).sum(1).to(torch.int32)      # leading zeros = prompt length
+        out = self.hidden_states(content_ids, prompt_len)
+        d = out.size(-1)
+        S0 = N * (C + self.K_act)
+        if include_cross_block:
+            pred_flat = torch.arange(N * C - 1, device=dev)
+            hid = out[:, :S0, :][:, self.content_pos, :][:, :-1, :].reshape(-1, d)
+        else:
+            pred_flat = self.predict_flat
+            hid = out[:, :S0, :][:, self.loss_pos, :].reshape(-1, d)
+        tgt = content_ids.reshape(B, N * C)[:, pred_flat + 1].reshape(-1)
+        if block_ce:
+            m, bc = self._perblock_ce(hid, tgt, pred_flat // C, N, B)
+            return {"ce": m, "block_ce": bc}
+        if resp_mask is None:
+            return {"ce": self._lm_ce(hid, tgt, ce_chunk)}
+        tmask = resp_mask.reshape(B, N * C)[:, pred_flat + 1].reshape(-1).float()
+        target = pred_flat + 1
+        if per_token and include_cross_block:
+            return {"ce_pt": self._per_token_lm_ce(hid, tgt, ce_chunk), "tmask": tmask,
+                    "blk": (target // C).repeat(B), "pos": (target % C).repeat(B),
+                    "supervised": ((pred_flat % C) != C - 1).repeat(B)}
+        if boundary_recovery_width > 0 and boundary_recovery_weight != 1.0:
+            recovery = ((target // C > 0) & (target % C >= 1) & (target % C <= boundary_recovery_width)).repeat(B)
+            tmask = tmask * torch.where(recovery, tmask.new_tensor(boundary_recovery_weight), tmask.new_tensor(1.0))
+        if not per_token:
+            return {"ce": self._masked_lm_ce(hid, tgt, tmask, ce_chunk)}
+        return {"ce_pt": self._per_token_lm_ce(hid, tgt, 0), "tmask": tmask, "blk": self.predict_block.repeat(B),
+                "pos": (self.predict_flat % C).repeat(B)}
+
+    @torch.no_grad()
+    def loss_logits(self, content_ids, prompt_len=None):
+        """fp32 logits at the loss positions (block-major, within-block 0..C-2), as the reference's gate compares."""
+        out = self.hidden_states(content_ids, prompt_len)
+        hid = out[:, self.loss_pos, :].reshape(-1, out.size(-1))
+        return self.model.lm_head(hid).float()

@@ -1,0 +1,277 @@
+"""Incremental CompressLM generator over the paged abridged cache (the serving path for one sequence).
+
+Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``: ``feed_content``, ``compress``,
+``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, bidirectional codes,
+raw prompt, per-layer code quotas, no tails). The reference keeps a dense per-layer store and masks it; here
+every layer's rows live in paged caches, quotas are physical, and the block boundary is a compaction:
+
+* content chunks append K/V at the group's next physical slots (``abkv_kv_append``) and attend over every resident
+  row: one token -> ``abkv_decode_attn``, several -> causal ``abkv_paged_prefill_attn``. Resident rows are exactly
+  the reference's visible set (codes of earlier blocks, raw prompt, the current block's content;
+  gen_compress.py:667-707).
+* ``compress`` runs the K code rows of the block non-causally with the key limit ``code_start + q_layer`` (the
+  code visibility of gen_compress.py:328-358, 709-745), then removes the block's response content in every group and
+  code rows ``>= q`` in groups of quota ``q < K`` through the native planner (``mask_token_span``, the
+  ``_finish_block`` order of processor.py:467-557) and moves the surviving rows with the HIP mover.
+
+Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
+the serving worker shares them (kv_cache_utils.py:1110-1127). Per-head (non-uniform within a layer) quotas would
+need ragged per-head pages and raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import backend as bk
+from . import ops
+from .config import bitrev_offsets
+from .planner import KVPlanner
+from .worker import execute_fused_moves
+
+_UNSUPPORTED = ("capture_hidden", "capture_attention", "code_init_override", "raw_tail_override",
+                "oracle_full_history", "oracle_history_layers", "preserve_full_history", "retain_full_history_layers",
+                "history_replaces_codes_layers", "capture_content_attention", "content_attention_offsets",
+                "content_head_callback", "evict_policy", "keep_per_block", "evict_seed", "skip_unused_codes")
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def _layer_quotas(head_code_quotas, num_layers, num_kv_heads, K):
+    if head_code_quotas is None:
+        return [K] * num_layers
+    q = torch.as_tensor(head_code_quotas, dtype=torch.long).cpu()
+    if tuple(q.shape) != (num_layers, num_kv_heads):
+        raise ValueError(f"head_code_quotas must have shape [{num_layers}, {num_kv_heads}], got {tuple(q.shape)}")
+    if bool(((q <= 0) | (q > K)).any()):
+        raise ValueError(f"head_code_quotas must be in [1, {K}]")
+    if bool((q != q[:, :1]).any()):
+        raise NotImplementedError("per-head code quotas within a layer need per-head pages; rows must be uniform")
+    return [int(x) for x in q[:, 0]]
+
+
+class CompressGen:
+    """One sequence's incremental generator. ``clm`` is a :class:`abridgekv_amd.compress_forward.CompressLM` (or any
+    object with ``model``, ``C``, ``K``, ``pause``, ``code_positions``); ``max_tokens`` bounds the logical length the
+    page pool must hold."""
+
+    def __init__(self, clm, device, raw_prompt_len=0, head_code_quotas=None, code_attend_current_content=True,
+                 max_tokens: int = 1 << 15, **options):
+        bad = sorted(name for name in options if name not in _UNSUPPORTED)
+        if bad:
+            raise TypeError(f"unexpected CompressGen options {bad}")
+        used = sorted(name for name, value in options.items() if value)
+        if used:
+            raise NotImplementedError(f"CompressGen options {used} are not supported on the paged path")
+        if not code_attend_current_content:
+            raise NotImplementedError("code rows always attend the current block's content on the paged path")
+        if getattr(clm, "L", 1) != 1 or getattr(clm, "pause_xattn", "full") != "full":
+            raise NotImplementedError("the paged path serves L=1 with bidirectional code attention")
+        if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail", "retain_tail_kv")):
+            raise NotImplementedError("the paged path serves no replay / raw / retained tails")
+        self.clm = clm
+        self.inner = clm.model.model
+        self.layers = self.inner.layers
+        self.num_layers = len(self.layers)
+        self.lm_head = clm.model.lm_head
+        self.device = torch.device(device)
+        self.dtype = next(clm.model.parameters()).dtype
+        if self.dtype != torch.bfloat16:
+            raise NotImplementedError("the paged kernels run bf16 models")
+        self.C, self.K = int(clm.C), int(clm.K)
+        self.code_positions = getattr(clm, "code_positions", "appended")
+        self.raw_prompt_len = int(raw_prompt_len)
+        self.d = clm.model.config.hidden_size
+        cfg = clm.model.config
+        self.quotas = _layer_quotas(head_code_quotas, self.num_layers, int(cfg.num_key_value_heads), self.K)
+        self.head_code_quotas = None if head_code_quotas is None else torch.as_tensor(head_code_quotas)
+
+        # KV-cache groups: layers of equal quota, in order of first appearance; tensor i = i-th layer of each group
+        distinct = list(dict.fromkeys(self.quotas))
+        self.group_quotas = distinct
+        self.group_of = [distinct.index(q) for q in self.quotas]
+        self.tensor_of = [self.group_of[:li].count(self.group_of[li]) for li in range(self.num_layers)]
+        n_tensors = max(self.tensor_of) + 1
+        G = len(distinct)
+        pages_per_group = -(-int(max_tokens) // ops.PAGE) + 2
+        self.num_pages = G * pages_per_group + 1
+        self.caches = [torch.zeros(ops.kv_cache_shape(self.num_pages), dtype=torch.bfloat16, device=self.device)
+                       for _ in range(n_tensors)]
+        self.caches_by_group = [[self.caches[self.tensor_of[li]] for li in range(self.num_layers)
+                                 if self.group_of[li] == g] for g in range(G)]
+        self.planner = KVPlanner(self.num_pages, G, ops.PAGE)
+        self.rid = 0
+        self.planner.add_request(self.rid)
+        self.impl = bk.AbridgeAttentionImpl(scale=getattr(self.layers[0].self_attn, "scaling", None))
+        self.builder = bk.AbridgeMetadataBuilder(max_num_seqs=1, max_pages=pages_per_group, device=self.device)
+        self.b = 0                      # current block index
+        self.f = 0                      # content tokens committed in the current block
+        self.logical_len = 0            # tokens in the planner's logical sequence (content + code rows)
+        self._cur_ids: list[int] = []
+        self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C)).to(self.device)
+                              if self.code_positions == "bitrev" else None)
+
+    # -- positions ------------------------------------------------------------------------------------------------
+    def _content_pos(self, n):
+        """RoPE positions of the next n content tokens of block b (gen_compress.py:789-795)."""
+        base = self.b * self.C if self.code_positions == "bitrev" else self.b * (self.C + self.K)
+        return torch.arange(base + self.f, base + self.f + n, device=self.device)
+
+    def _code_pos(self):
+        """RoPE positions of the K code rows of block b (gen_compress.py:797-804)."""
+        if self.code_positions == "bitrev":
+            return self.b * self.C + self._code_offsets
+        base = self.b * (self.C + self.K)
+        return torch.arange(base + self.C, base + self.C + self.K, device=self.device)
+
+    # -- one step over all layers ---------------------------------------------------------------------------------
+    def _group_metadata(self, n, code_step):
+        """Per-group metadata for n new rows appended after each group's resident rows."""
+        blocks = self.planner.get_blocks(self.rid)
+        comp = self.planner.compacted_counts(self.rid)
+        out = []
+        for g, q in enumerate(self.group_quotas):
+            start = self.logical_len - comp[g]
+            seq_len = start + n
+            table = np.asarray(blocks[g], dtype=np.int32)
+            pos = np.arange(start, seq_len)
+            slots = table[pos // ops.PAGE].astype(np.int64) * ops.PAGE + pos % ops.PAGE
+            limit = [start + min(q, self.K)] if code_step else None
+            md = self.builder.build([0, n], [seq_len], torch.from_numpy(table).view(1, -1).to(self.device),
+                                    torch.from_numpy(slots).to(self.device), code_key_limit=limit)
+            out.append(md)
+        return out
+
+    @torch.no_grad()
+    def _forward_rows(self, hidden, positions, code_step):
+        """Run every decoder layer over hidden [1, n, d]; new K/V rows are committed to the caches."""
+        n = hidden.shape[1]
+        if self.planner.allocate_slots(self.rid, n) is None:
+            raise RuntimeError("page pool exhausted; raise max_tokens")
+        mds = self._group_metadata(n, code_step)
+        cos, sin = self.inner.rotary_emb(hidden, positions.view(1, -1))
+        cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)                      # [1, n, 1, D]
+        for li, layer in enumerate(self.layers):
+            attn = layer.self_attn
+            normed = layer.input_layernorm(hidden)
+            q = attn.q_proj(normed).view(1, n, -1, attn.head_dim)
+            k = attn.k_proj(normed).view(1, n, -1, attn.head_dim)
+            if getattr(attn, "q_norm", None) is not None:
+                q = attn.q_norm(q)
+            if getattr(attn, "k_norm", None) is not None:
+                k = attn.k_norm(k)
+            v = attn.v_proj(normed).view(1, n, -1, attn.head_dim)
+            q = (q * cos + _rotate_half(q) * sin).to(self.dtype)
+            k = (k * cos + _rotate_half(k) * sin).to(self.dtype)
+            o = torch.empty((n, ops.HEADS_Q * ops.HEAD_DIM), dtype=self.dtype, device=self.device)
+            self.impl.forward(layer, q[0].reshape(n, -1), k[0].contiguous(), v[0].contiguous(),
+                              self.caches[self.tensor_of[li]], mds[self.group_of[li]], o)
+            h = hidden + attn.o_proj(o.view(1, n, -1))
+            hidden = h + layer.mlp(layer.post_attention_layernorm(h))
+        self.logical_len += n
+        self.planner.set_num_computed_tokens(self.rid, self.logical_len)
+        return hidden
+
+    # -- reference surface ----------------------------------------------------------------------------------------
+    def feed_content(self, ids):
+        """Feed <= C - f content tokens as one chunk; returns the final-normed hidden states (n, d)."""
+        n = len(ids)
+        if n == 0 or self.f + n > self.C:
+            raise ValueError(f"chunk of {n} tokens does not fit the block ({self.f}/{self.C} used)")
+        hidden = self.inner.embed_tokens(torch.tensor([list(ids)], device=self.device))
+        hidden = self._forward_rows(hidden, self._content_pos(n), code_step=False)
+        self.f += n
+        self._cur_ids += [int(t) for t in ids]
+        return self.inner.norm(hidden)[0]
+
+    def compress(self):
+        """Code step of the full block, then compaction of its response content and of code rows >= quota."""
+        if self.f != self.C:
+            raise RuntimeError("compress() needs a full block")
+        K, C = self.K, self.C
+        hidden = self.clm.pause[:K].to(self.dtype).view(1, K, self.d)
+        code_start = self.logical_len
+        self._forward_rows(hidden, self._code_pos(), code_step=True)
+        block_start = code_start - C
+        resp_from = block_start + min(max(self.raw_prompt_len - self.b * C, 0), C)
+        calls = []
+        if resp_from < code_start:
+            calls.append((resp_from, code_start, None))
+        for q in sorted({q for q in self.group_quotas if q < K}):
+            calls.append((code_start + q, code_start + K, [g for g, gq in enumerate(self.group_quotas) if gq == q]))
+        for start, end, groups in calls:
+            res = self.planner.mask_token_span(self.rid, start, end, groups)
+            if not res.success:
+                raise RuntimeError(f"compaction failed: {res.error_message}")
+        _, _, fused = self.planner.take_step_outputs(as_arrays=True)
+        execute_fused_moves(fused.copy(), self.caches_by_group)
+        self.b += 1
+        self.f = 0
+        self._cur_ids = []
+
+    def step(self, token_id):
+        """Feed one content token (compressing when it completes the block); returns its next-token logits."""
+        h = self.feed_content([int(token_id)])
+        logits = self.lm_head(h[-1:]).float()[0]
+        if self.f == self.C:
+            self.compress()
+        return logits
+
+    def prefill(self, prompt_ids):
+        """Feed the prompt in block-aligned chunks (compressing full blocks); returns the last token's logits."""
+        ids = list(prompt_ids)
+        last, i = None, 0
+        while i < len(ids):
+            take = min(self.C - self.f, len(ids) - i)
+            h = self.feed_content(ids[i:i + take])
+            last = self.lm_head(h[-1:]).float()[0]
+            i += take
+            if self.f == self.C:
+                self.compress()
+        return last
+
+    @torch.no_grad()
+    def generate(self, prompt_ids, max_new_tokens, eos_id=None, temperature=0.0, top_p=1.0, top_k=0, gen=None):
+        logits = self.prefill(prompt_ids)
+        out = []
+        for _ in range(max_new_tokens):
+            nxt = sample(logits, temperature, top_p, top_k, gen)
+            out.append(nxt)
+            if eos_id is not None and nxt == eos_id:
+                break
+            logits = self.step(nxt)
+        return out
+
+    def resident_rows(self) -> list[int]:
+        """Physical rows held per layer (its group's length)."""
+        comp = self.planner.compacted_counts(self.rid)
+        return [self.logical_len - comp[g] for g in self.group_of]
+
+    def cache_kv_stats(self):
+        main = self.resident_rows()
+        total = sum(main)
+        return {"main_columns_by_layer": main, "history_columns_by_layer": [0] * self.num_layers,
+                "total_columns": total, "total_kv_elements": total * 2 * ops.HEADS_KV * ops.HEAD_DIM}
+
+
+def sample(logits, temperature, top_p, top_k, gen):
+    """Greedy for temperature <= 0, else temperature / top-k / top-p sampling (gen_compress.py:1035-1052)."""
+    if temperature is None or temperature <= 0:
+        return int(logits.argmax())
+    logits = logits / temperature
+    if top_k and top_k > 0:
+        kth = torch.topk(logits, min(top_k, logits.numel())).values[-1]
+        logits = logits.masked_fill(logits < kth, float("-inf"))
+    probs = F.softmax(logits, dim=-1)
+    if top_p and top_p < 1.0:
+        sp, si = torch.sort(probs, descending=True)
+        cut = torch.cumsum(sp, dim=-1) > top_p
+        cut[..., 1:] = cut[..., :-1].clone()
+        cut[..., 0] = False
+        probs = torch.zeros_like(probs).scatter_(-1, si, sp.masked_fill(cut, 0.0))
+        probs = probs / probs.sum()
+    return int(torch.multinomial(probs, 1, generator=gen))

@@ -42,6 +42,16 @@ def kv_cache_shape(num_pages: int) -> tuple[int, ...]:
     return (num_pages, 2, PAGE, HEADS_KV, HEAD_DIM)
 
 
+def _row_stride(block_table: torch.Tensor) -> int:
+    """Row stride of a [B, W] page table (a single row's stride is arbitrary in torch, e.g. 0 for a numpy
+    ``table[None]`` view, so it is reported as W)."""
+    W = block_table.shape[1]
+    if block_table.shape[0] <= 1:
+        return W
+    _require(block_table.stride(0) >= W, "block_table rows must not overlap")
+    return block_table.stride(0)
+
+
 def _check_cache(kv_cache: torch.Tensor) -> None:
     _require(kv_cache.is_cuda, "kv_cache must be on the GPU")
     _require(kv_cache.dtype == torch.bfloat16, "kv_cache must be bfloat16")
@@ -100,7 +110,7 @@ def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch
         ws_bytes = workspace.numel() * workspace.element_size()
     rc = lib().abkv_decode_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                 _ptr(block_table),
-                                block_table.stride(0), _ptr(seq_lens), B, max_pages, split_pages, float(scale),
+                                _row_stride(block_table), _ptr(seq_lens), B, max_pages, split_pages, float(scale),
                                 _ptr(out), out.stride(0), out.stride(1), _ptr(lse), _ptr(workspace), ws_bytes,
                                 C.c_void_p(_stream()))
     check(rc, "abkv_decode_attn")
@@ -275,7 +285,7 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     kv_limit_d, causal_d = meta[2 * B + 1: 3 * B + 1], meta[3 * B + 1:]
     scale = default_scale() if scale is None else float(scale)
     rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
-                                       _ptr(block_table), block_table.stride(0), W, _ptr(q_start_d),
+                                       _ptr(block_table), _row_stride(block_table), W, _ptr(q_start_d),
                                        _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
                                        _ptr(causal_d), 1, scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
                                        C.c_void_p(_stream()))

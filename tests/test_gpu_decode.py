@@ -148,6 +148,24 @@ def test_strided_q_and_out():
     assert torch.all(outbig[:, :4] == 0) and torch.all(outbig[:, 36:] == 0)
 
 
+def test_single_row_table_with_zero_row_stride():
+    """A one-row page table made as a numpy ``table[None]`` view has row stride 0 in torch; it must decode the same."""
+    rng = np.random.default_rng(4)
+    ks, vs = [rng.standard_normal((700, 8, 128))], [rng.standard_normal((700, 8, 128))]
+    q = rng.standard_normal((1, 32, 128)).astype(np.float32)
+    cache, tables, sl = _paged_cache(ks, vs, 80, rng)
+    row = np.ascontiguousarray(tables[0])
+    bt0 = torch.from_numpy(row[None])
+    assert bt0.stride(0) == 0
+    from abridgekv_amd import ops
+    dev = torch.device("cuda")
+    out, _ = ops.decode_attention(torch.from_numpy(q).to(dev, torch.bfloat16), torch.from_numpy(cache).to(dev, torch.bfloat16),
+                                  bt0.to(dev), torch.from_numpy(sl).to(dev), 128 ** -0.5, split_pages=8)
+    torch.cuda.synchronize()
+    ref_out, _ = _oracle(q, cache, tables, sl)
+    assert np.abs(out.float().cpu().numpy() - ref_out).max() <= TOL
+
+
 def test_shape_errors_raise_before_launch():
     from abridgekv_amd import ops
     dev = torch.device("cuda")

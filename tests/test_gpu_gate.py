@@ -1,0 +1,109 @@
+"""End-to-end gate on a random model with Qwen3-4B's attention shape (32 query heads, 8 KV heads, head size 128):
+the teacher-forced forward (masked-prefill kernel) and the incremental paged generator (decode / chunk / code-step
+kernels, planner compaction, row mover) must both reproduce the dense float64 teacher-forced forward, as the
+reference's gate requires of its generator (gen_compress.py:1189-1378).
+
+Tolerance: our bf16 paths may differ from the float64 oracle by at most 2x what the same model in plain PyTorch
+bf16 (dense masks, CPU) differs by, plus 2e-3 (logits here are O(0.3))."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+transformers = pytest.importorskip("transformers")
+
+CASES = [
+    # C, N, K, code positions, prompt lengths, per-layer quota (None: all K), token-by-token sequences
+    (64, 4, 16, "bitrev", [40, 100], [16, 4], [1]),
+    (32, 3, 8, "appended", None, None, [0]),
+    (64, 3, 32, "bitrev", [64, 0], [8, 32], [0, 1]),
+]
+
+
+def _model(seed):
+    torch.manual_seed(seed)
+    cfg = transformers.Qwen3Config(vocab_size=257, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                                   max_position_embeddings=4096,
+                                   rope_parameters={"rope_theta": 1e6, "rope_type": "default"})
+    cfg._attn_implementation = "eager"
+    return transformers.Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_generator_and_teacher_forced_match_dense_forward(case):
+    from abridgekv_amd.compress_forward import CompressLM
+    from abridgekv_amd.gen_compress import CompressGen
+
+    C, N, K, code_positions, prompt, quota, stepwise = CASES[case]
+    base = _model(case)
+    dev = torch.device("cuda")
+    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=code_positions,
+                     head_code_quotas=None if quota is None else [[q] * 8 for q in quota]).eval()
+    torch.manual_seed(100 + case)
+    with torch.no_grad():
+        clm.pause.normal_(0, 0.05)
+    ids = torch.randint(0, 257, (2, N, C))
+    lhq = None if quota is None else np.repeat(np.asarray(quota)[:, None], 32, axis=1)
+    pause = clm.pause.detach().cpu()
+
+    ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
+                               lhq)
+    eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq)
+    tol = 2 * (eager - ref).abs().max().item() + 2e-3
+
+    pl = None if prompt is None else torch.tensor(prompt, dtype=torch.int32, device=dev)
+    tf = clm.loss_logits(ids.to(dev), pl).double().cpu()
+    err_tf = (tf - ref).abs().max().item()
+    print(f"case {case}: eager-bf16 {(eager - ref).abs().max().item():.3e}  teacher-forced {err_tf:.3e}")
+    assert err_tf <= tol
+
+    rows_per_seq = N * (C - 1)
+    for bi in range(2):
+        p = 0 if prompt is None else prompt[bi]
+        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=None if quota is None else [[q] * 8 for q in quota],
+                        max_tokens=N * (C + K) + 16)
+        got = []
+        for blk in range(N):
+            toks = ids[bi, blk].tolist()
+            if bi in stepwise:
+                hs = torch.cat([g.feed_content([t]) for t in toks])
+            else:
+                hs = g.feed_content(toks)
+            got.append(clm.model.lm_head(hs).float()[: C - 1].double().cpu())
+            g.compress()
+            kept_prompt = min(p, (blk + 1) * C)
+            assert g.resident_rows() == [kept_prompt + (blk + 1) * (K if quota is None else q)
+                                         for q in (quota or [K, K])]
+        err = (torch.cat(got) - ref[bi * rows_per_seq: (bi + 1) * rows_per_seq]).abs().max().item()
+        print(f"case {case} seq {bi}: generator {err:.3e}")
+        assert err <= tol
+
+
+def test_forward_losses_match_dense_cross_entropy():
+    from abridgekv_amd.compress_forward import CompressLM
+
+    C, N, K = 64, 3, 16
+    base = _model(7)
+    dev = torch.device("cuda")
+    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions="bitrev").eval()
+    ids = torch.randint(0, 257, (2, N, C))
+    resp = torch.ones((2, N, C), dtype=torch.long)
+    resp.view(2, -1)[0, :70] = 0
+    resp.view(2, -1)[1, :5] = 0
+    pause = clm.pause.detach().cpu().double()
+    ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause, ids, C, N, K, "bitrev", [70, 5])
+    tgt = ids.view(2, -1)[:, torch.from_numpy(np.array([k for k in range(N * C) if k % C != C - 1])) + 1]
+    ce = torch.nn.functional.cross_entropy(ref, tgt.reshape(-1), reduction="none")
+    tm = resp.view(2, -1)[:, torch.from_numpy(np.array([k for k in range(N * C) if k % C != C - 1])) + 1]
+    tm = tm.reshape(-1).double()
+    want = (ce * tm).sum() / tm.sum()
+    with torch.no_grad():
+        got = clm(ids.to(dev), resp_mask=resp.to(dev), raw_prompt=True)["ce"].item()
+        blk = clm(ids.to(dev), resp_mask=resp.to(dev), raw_prompt=True, block_ce=True)
+    assert abs(got - want.item()) <= 1e-2
+    assert blk["block_ce"].shape == (N,)
