@@ -4,15 +4,17 @@
 // (third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1147-1224), which applies one ordered batch of
 // (src_block, src_off, dst_block, dst_off) ops per KV-cache group with gather-then-scatter semantics to every layer
 // tensor of the group. Here a launch takes a list of op *segments* (one per request batch) and applies each segment
-// to up to kMaxLayers layer tensors; grid = (segment, layer), 256 threads.
+// to up to kMaxLayers layer tensors; grid = (segment, layer, byte part), 256 threads.
 //
-// Exactness without a staging buffer: a workgroup walks its segment in op order, kChunk ops at a time, loading
+// Exactness without a staging buffer: a workgroup walks its segment in op order, kMoveRows ops at a time, loading
 // every source row of the chunk into registers, then (after a barrier) storing every destination row, then a
-// barrier. This equals gather-then-scatter whenever no op of the segment reads a slot that an EARLIER op of the same
-// segment writes -- true for compaction ops, which are emitted in increasing source order with dst < src
-// (single_type_kv_cache_manager.py:378-381). Segments must touch disjoint pages (different requests' pages are
-// disjoint; one request contributes one segment per batch). For op lists that violate the ordering precondition the
-// two-phase gather/scatter entry points below stage rows through a workspace instead.
+// barrier. This equals gather-then-scatter, for any chunk size, whenever no op of the segment reads a slot that an
+// EARLIER op of the same segment writes (a later op may overwrite a slot an earlier op read: that read has happened)
+// -- true for compaction ops, which are emitted in increasing source order with dst < src
+// (single_type_kv_cache_manager.py:378-381) -- and no two ops write one slot. Segments must touch disjoint pages
+// (different requests' pages are disjoint; one request contributes one segment per batch). For op lists that
+// violate the ordering precondition the two-phase gather/scatter entry points below stage rows through a workspace
+// instead.
 //
 // KV append: replaces the stock vLLM compiled op reshape_and_cache(_flash) that writes each new token's K and V
 // rows at slot_mapping[t] (slots from block_table.py:186-197); slot < 0 is skipped (padding).
@@ -21,7 +23,8 @@
 namespace abkv {
 
 constexpr int kMaxLayers = 16;
-constexpr int kChunk = 16;        // ops per register chunk: 16 rows x 4 KiB = 64 KiB in flight per workgroup
+constexpr int kMoveRows = 64;     // ops per chunk: 64 rows x 1 KiB (one byte part) in flight per workgroup
+constexpr int kMoveParts = 4;     // workgroups per (segment, layer), each moving one quarter of every row
 
 struct LayerPtrs {
   char* p[kMaxLayers];
@@ -43,41 +46,60 @@ __device__ __forceinline__ bool op_ok(const int32_t* op, int num_pages, int bloc
          (unsigned)op[1] < (unsigned)block_size && (unsigned)op[3] < (unsigned)block_size;
 }
 
-// One "row" of an op = slot_bytes of K plus slot_bytes of V. 256 threads x 16 B cover 4096 B = one row of the
-// served geometry (2 KiB K + 2 KiB V); other geometries loop.
+// One "row" of an op = slot_bytes of K plus slot_bytes of V (4 KiB in the served geometry). A workgroup owns one
+// byte part of the rows (grid.z parts; byte parts of a row never interact, so every part may run independently)
+// and walks its segment kMoveRows ops at a time: wave w of the workgroup moves rows w, w+4, ..., lane l the l-th
+// 16-byte vector of the part. Lane l of every wave fetches op c0 + l once per chunk; the row offsets are broadcast
+// with readlane (wave-uniform), so the 16 source loads of a thread issue back to back, land in registers before
+// the barrier, and the 16 stores follow it.
 __global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
   const int seg = blockIdx.x;
   char* base = a.layers.p[blockIdx.y];
   const int s0 = a.seg_offsets[seg], s1 = a.seg_offsets[seg + 1];
   const int row_vec = (2 * a.slot_bytes) / 16;          // 16-byte vectors per row
-  const int tid = threadIdx.x;
-  for (int c0 = s0; c0 < s1; c0 += kChunk) {
-    const int n = min(kChunk, s1 - c0);
-    for (int v0 = 0; v0 < row_vec; v0 += 256) {
-      const int v = v0 + tid;
-      const bool active = v < row_vec;
-      const int half = v >= row_vec / 2;                   // 0: K, 1: V
-      const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
-      u32x4 buf[kChunk];
+  const int vpp = (row_vec + (int)gridDim.z - 1) / (int)gridDim.z;   // vectors per part
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int c0 = s0; c0 < s1; c0 += kMoveRows) {
+    const int n = min(kMoveRows, s1 - c0);
+    int o0 = -1, o1 = -1, o2 = -1, o3 = -1;               // lane l: op c0 + l
+    if (lane < n) {
+      const int32_t* op = a.ops + 4L * (c0 + lane);
+      o0 = op[0];
+      o1 = op[1];
+      o2 = op[2];
+      o3 = op[3];
+    }
+    const bool ok_l = lane < n && (unsigned)o0 < (unsigned)a.num_pages && (unsigned)o2 < (unsigned)a.num_pages &&
+                      (unsigned)o1 < (unsigned)a.block_size && (unsigned)o3 < (unsigned)a.block_size;
+    const unsigned long long ok_mask = __ballot(ok_l);
+    // wave-uniform byte offsets of this wave's rows (invalid rows read slot 0 of page 0 and store nothing)
+    long soff[kMoveRows / 4], doff[kMoveRows / 4];
 #pragma unroll
-      for (int k = 0; k < kChunk; ++k) {
-        if (k < n && active) {
-          const int32_t* op = a.ops + 4L * (c0 + k);
-          if (!op_ok(op, a.num_pages, a.block_size)) continue;
-          const char* src = base + (long)op[0] * a.page_bytes + (long)op[1] * a.slot_bytes + inner;
-          buf[k] = *reinterpret_cast<const u32x4*>(src);
-        }
-      }
+    for (int k = 0; k < kMoveRows / 4; ++k) {
+      const int r = wave + 4 * k;                          // < 64: a lane of this wave
+      const bool ok = (ok_mask >> r) & 1ull;
+      soff[k] = ok ? (long)__builtin_amdgcn_readlane(o0, r) * a.page_bytes +
+                         (long)__builtin_amdgcn_readlane(o1, r) * a.slot_bytes : 0;
+      doff[k] = ok ? (long)__builtin_amdgcn_readlane(o2, r) * a.page_bytes +
+                         (long)__builtin_amdgcn_readlane(o3, r) * a.slot_bytes : -1;
+    }
+    for (int u0 = 0; u0 < vpp; u0 += 64) {
+      const int u = u0 + lane;
+      const int v = (int)blockIdx.z * vpp + u;
+      const bool active = u < vpp && v < row_vec;
+      const int half = v >= row_vec / 2;                   // 0: K, 1: V
+      const long inner = active ? (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16 : 0;
+      u32x4 buf[kMoveRows / 4];
+#pragma unroll
+      for (int k = 0; k < kMoveRows / 4; ++k) buf[k] = *reinterpret_cast<const u32x4*>(base + soff[k] + inner);
+      // every source row of the chunk is in registers before any wave stores (a store may hit a slot another wave
+      // of the chunk reads)
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
 #pragma unroll
-      for (int k = 0; k < kChunk; ++k) {
-        if (k < n && active) {
-          const int32_t* op = a.ops + 4L * (c0 + k);
-          if (!op_ok(op, a.num_pages, a.block_size)) continue;
-          char* dst = base + (long)op[2] * a.page_bytes + (long)op[3] * a.slot_bytes + inner;
-          *reinterpret_cast<u32x4*>(dst) = buf[k];
-        }
-      }
+      for (int k = 0; k < kMoveRows / 4; ++k)
+        if (doff[k] >= 0 && active) *reinterpret_cast<u32x4*>(base + doff[k] + inner) = buf[k];
       __syncthreads();
     }
   }
@@ -178,7 +200,7 @@ int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages
   a.slot_bytes = slot_bytes;
   a.num_pages = num_pages;
   a.block_size = block_size;
-  hipLaunchKernelGGL(kv_move_kernel, dim3(n_segments, n_layers), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(kv_move_kernel, dim3(n_segments, n_layers, kMoveParts), dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 

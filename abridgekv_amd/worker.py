@@ -66,27 +66,53 @@ def execute_kv_copy_operations(kv_copy_operations: dict, layer_caches_by_group, 
             execute_kv_copy_group(segments, caches, check=check)
 
 
+def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: bool = True):
+    """Host side of :func:`execute_fused_moves`: split a planner step's fused move rows (request, group, src_block,
+    src_off, dst_block, dst_off) by group into one op array and segment offsets (one segment per request), uploaded
+    in a single host-to-device copy. Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)]."""
+    if fused_moves.size == 0:
+        return []
+    fm = np.asarray(fused_moves, dtype=np.int64)
+    parts, meta = [], []
+    at = 0
+    for gid in np.unique(fm[:, 1]).tolist():
+        rows = fm[fm[:, 1] == gid]
+        cut = np.flatnonzero(np.diff(rows[:, 0])) + 1
+        offs = np.concatenate([[0], cut, [rows.shape[0]]]).astype(np.int32)
+        ops_h = np.ascontiguousarray(rows[:, 2:6], dtype=np.int32)
+        if check:
+            _validate_ops(ops_h, num_pages)
+        parts += [ops_h.reshape(-1), offs]
+        meta.append((gid, at, ops_h.size, at + ops_h.size, offs.size))
+        at += ops_h.size + offs.size
+    flat = torch.from_numpy(np.concatenate(parts)).to(device)
+    return [(gid, flat[o: o + n].view(-1, 4), flat[so: so + ns]) for gid, o, n, so, ns in meta]
+
+
+def launch_moves(prepared, layer_caches_by_group, events=None) -> None:
+    """Device side of :func:`execute_fused_moves`: one launch per group (and per 16 layer tensors). ``events``, if
+    given, is a list that receives (start, end) CUDA events recorded around every launch."""
+    for gid, ops_d, offs_d in prepared:
+        caches = layer_caches_by_group[gid]
+        for lo in range(0, len(caches), 16):
+            if events is not None:
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+            ops.kv_move_segments(caches[lo: lo + 16], ops_d, offs_d)
+            if events is not None:
+                e.record()
+                events.append((s, e))
+
+
 def execute_fused_moves(fused_moves: np.ndarray, layer_caches_by_group, check: bool = True) -> None:
     """Apply a planner step's fused move rows (request, group, src_block, src_off, dst_block, dst_off): one launch
     per group, one segment per request. Rows of one (request, group) are monotone (increasing source, dst < src), so
     the in-register chunked copy is exact."""
     if fused_moves.size == 0:
         return
-    fm = np.asarray(fused_moves, dtype=np.int64)
-    for gid, caches in enumerate(layer_caches_by_group):
-        rows = fm[fm[:, 1] == gid]
-        if rows.size == 0:
-            continue
-        cut = np.flatnonzero(np.diff(rows[:, 0])) + 1
-        offs = np.concatenate([[0], cut, [rows.shape[0]]]).astype(np.int32)
-        ops_h = np.ascontiguousarray(rows[:, 2:6], dtype=np.int32)
-        if check:
-            _validate_ops(ops_h, caches[0].shape[0])
-        device = caches[0].device
-        ops_d = torch.from_numpy(ops_h).to(device)
-        offs_d = torch.from_numpy(offs).to(device)
-        for lo in range(0, len(caches), 16):
-            ops.kv_move_segments(caches[lo: lo + 16], ops_d, offs_d)
+    num_pages = layer_caches_by_group[0][0].shape[0]
+    launch_moves(prepare_fused_moves(fused_moves, num_pages, layer_caches_by_group[0][0].device, check),
+                 layer_caches_by_group)
 
 
 def truncate_block_table(block_ids_by_group, keep):

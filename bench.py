@@ -165,16 +165,22 @@ def bench_compaction(args, torch):
     fused = fused.copy()
     layers_per_group = len(st.groups[0])
     alg_bytes = 2 * len(fused) * layers_per_group * 4096
+    worker.prepare_fused_moves(fused, st.num_pages, dev, check=False)      # first call pays one-off runtime setup
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    prepared = worker.prepare_fused_moves(fused, st.num_pages, dev, check=False)
+    torch.cuda.synchronize()
+    prep_s = time.perf_counter() - t0
     for _ in range(args.warmup):
-        worker.execute_fused_moves(fused, by_group, check=False)
+        worker.launch_moves(prepared, by_group)
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
+    events = []
     for _ in range(args.steps):
-        worker.execute_fused_moves(fused, by_group, check=False)
-    e.record()
+        worker.launch_moves(prepared, by_group, events)
     torch.cuda.synchronize()
-    t = s.elapsed_time(e) / 1e3 / args.steps
+    n_launch = len(events)
+    t = sum(s_.elapsed_time(e_) for s_, e_ in events) / 1e3 / args.steps
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):
         worker.execute_kv_copy_operations(outs.kv_copy_operations, by_group, check=False)
@@ -184,15 +190,16 @@ def bench_compaction(args, torch):
     gbps = alg_bytes / t / 1e9
     return {
         "metric": "block-boundary compaction: sequences compacted per second (64 seqs x 36 layers)",
-        "value": B / (t + plan_s), "unit": "sequences/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": (t + plan_s) * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": B / (t + plan_s + prep_s), "unit": "sequences/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": (t + plan_s + prep_s) * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 (row copies)", "data": "synthetic histories replayed through the planner",
         "config": {"workload": "compaction: 64 sequences close a 512-token block (256 code rows), Qwen3-4B 36 layers "
                                "/ 6 quota groups, page 16, seeded free list", "global_batch": B},
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": gbps / HBM_PEAK_GBPS, "traffic": None, "kernel": "kv_move_kernel (fused moves)",
-                     "alg_bytes_per_launch": alg_bytes / len(st.groups), "avg_launch_us": t / len(st.groups) * 1e6},
-        "planner_ms": plan_s * 1e3, "device_moves_ms": t * 1e3,
+                     "alg_bytes_per_launch": alg_bytes / (n_launch / args.steps),
+                     "avg_launch_us": t / (n_launch / args.steps) * 1e6},
+        "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
         "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
     }
 
