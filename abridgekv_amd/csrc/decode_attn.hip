@@ -215,10 +215,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
   const int d0 = (threadIdx.x & 31) * 4;
   const float* pml = a.part_ml + ((long)b * a.max_splits * kHeadsQ + head) * 2;
+  // unrolled so the per-split loads of a thread are in flight together (the loop is latency-bound otherwise)
   float M = -INFINITY;
+#pragma unroll 8
   for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[(long)s * kHeadsQ * 2]);
   float L = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
   for (int s = 0; s < n_splits; ++s) {
     const float w = fast_exp2(pml[(long)s * kHeadsQ * 2] - M);
     L += w * pml[(long)s * kHeadsQ * 2 + 1];

@@ -25,6 +25,22 @@ import numpy as np
 HBM_PEAK_GBPS = 8000.0
 
 
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch of a kernel on this workload, from the committed rocprofv3 PMC summary
+    profiles/<name> (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, calibrated on a plain 4 GiB copy); None if absent."""
+    try:
+        with open(os.path.join(PROFILES, name)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,7 +149,9 @@ def bench_prefill(args, torch):
         "config": {"workload": f"masked prefill B={B}, N={N} blocks of [{C} content | {K} codes], S0={S0}, "
                                f"raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": tflops / 2500.0, "traffic": None, "kernel": "prefill_masked_kernel",
+                     "frac": tflops / 2500.0,
+                     "traffic": profiled_traffic("prefill_masked_b4_s10240_pmc_traffic.md"),
+                     "traffic_source": "profiles/prefill_masked_b4_s10240_pmc_traffic.md", "kernel": "prefill_masked_kernel",
                      "alg_flops_per_launch": flops, "avg_launch_us": t * 1e6},
     }
 
@@ -196,7 +214,10 @@ def bench_compaction(args, torch):
         "config": {"workload": "compaction: 64 sequences close a 512-token block (256 code rows), Qwen3-4B 36 layers "
                                "/ 6 quota groups, page 16, seeded free list", "global_batch": B},
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": gbps / HBM_PEAK_GBPS, "traffic": None, "kernel": "kv_move_kernel (fused moves)",
+                     "frac": gbps / HBM_PEAK_GBPS,
+                     "traffic": profiled_traffic("kv_move_compaction_64seq_pmc_traffic.md"),
+                     "traffic_source": "profiles/kv_move_compaction_64seq_pmc_traffic.md",
+                     "kernel": "kv_move_kernel (fused moves)",
                      "alg_bytes_per_launch": alg_bytes / (n_launch / args.steps),
                      "avg_launch_us": t / (n_launch / args.steps) * 1e6},
         "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
@@ -327,7 +348,10 @@ def main():
         "config": {"workload": wl, "global_batch": B, "layers": L, "kv_groups": G,
                    "split_pages": args.split_pages, "seed": args.seed, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": (profiled_traffic("decode_attn_saturated_b256_pmc_traffic.md")
+                                 if args.workload == "saturated" and args.batch == 256 and args.seed == 0 else None),
+                     "traffic_source": "profiles/decode_attn_saturated_b256_pmc_traffic.md (decode_attn_kernel)",
                      "kernel": "decode_attn_kernel (+ decode_merge_kernel), per layer launch",
                      "alg_bytes_per_launch": alg_bytes / L, "avg_launch_us": attn_s_per_step / L * 1e6},
         "attn_tokens_per_s": B / attn_s_per_step,
