@@ -89,7 +89,7 @@ def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch
              and block_table.shape[0] >= B and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
     _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() >= B
              and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32 [B]")
-    _require(split_pages > 0 and split_pages % 2 == 0, "split_pages must be a positive even number")
+    _require(0 < split_pages <= 64 and split_pages % 2 == 0, "split_pages must be an even number in [2, 64]")
     W = block_table.shape[1]
     max_pages = W if max_pages is None else int(max_pages)
     _require(0 < max_pages <= W, "max_pages must be in [1, block_table width]")

@@ -293,6 +293,8 @@ def main():
     sls = [torch.from_numpy(s).to(dev) for s in st.seq_lens]
     slots = [torch.from_numpy(s).to(dev) for s in st.slots]
     W = st.block_tables[0].shape[1]
+    # per-group page bound (what a metadata builder passes: the batch's longest sequence in that group)
+    gmax = [max(1, int(-(-int(sl.max()) // 16))) for sl in st.seq_lens]
     ws = ops.decode_workspace(B, W, args.split_pages, device=dev)
     scale = ops.default_scale()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
@@ -304,7 +306,7 @@ def main():
             ops.kv_append(knew[l], vnew[l], slots[g], caches[i])
             if timed:
                 starts[l].record()
-            ops.decode_attention(qs[l], caches[i], bts[g], sls[g], scale, max_pages=W, out=outs[l], lse=lses[l],
+            ops.decode_attention(qs[l], caches[i], bts[g], sls[g], scale, max_pages=gmax[g], out=outs[l], lse=lses[l],
                                  split_pages=args.split_pages, workspace=ws)
             if timed:
                 ends[l].record()

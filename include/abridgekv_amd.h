@@ -29,7 +29,7 @@ typedef struct ihipStream_t* abkv_stream_t; /* == hipStream_t */
  * q [num_seqs, 32, 128] bf16 (strides in elements), block_table [num_seqs, block_table_stride] int32 (group's page
  * table), seq_lens [num_seqs] int32 (physical rows of the group), out [num_seqs, 32, 128] bf16, lse [num_seqs, 32]
  * fp32 natural log (may be NULL). num_pages: pages in kv_cache (page ids are clamped into range).
- * split_pages: even number of pages per split. max_pages_per_seq (<= block_table_stride) bounds ceil(seq_len/16);
+ * split_pages: even number of pages per split, at most 64. max_pages_per_seq (<= block_table_stride) bounds ceil(seq_len/16);
  * longer sequences are truncated to max_pages_per_seq * 16 rows. workspace: >= abkv_decode_workspace_size(num_seqs, ceil(max_pages/split_pages))
  * bytes when a sequence can need more than one split (may be NULL otherwise).
  * ------------------------------------------------------------------------------------------------------------- */
