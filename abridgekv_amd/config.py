@@ -7,8 +7,10 @@ selective full-history evaluation) are rejected with ValueError instead of being
 """
 from __future__ import annotations
 
+import json
 from collections.abc import Sequence
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, fields
+from pathlib import Path
 
 import numpy as np
 
@@ -34,6 +36,35 @@ def bitrev_offsets(K: int, span: int) -> np.ndarray:
     for b in range(bits):
         rev |= ((k >> b) & 1) << (bits - 1 - b)
     return (rev * span) // K
+
+
+def load_quota_rows(path) -> tuple[tuple[int, ...], ...]:
+    """(layer x KV head) quota rows of a schedule file: a 2D array, or an object with 'packed_kv_quotas' / 'quotas'
+    (scripts/compresslm_schedules.py:6-13)."""
+    payload = json.loads(Path(path).read_text())
+    if isinstance(payload, dict):
+        payload = payload.get("packed_kv_quotas", payload.get("quotas"))
+    if not isinstance(payload, list) or not payload:
+        raise ValueError(f"{path}: expected a non-empty 2D quota array or an object with 'quotas'")
+    return tuple(tuple(int(v) for v in row) for row in payload)
+
+
+def load_layer_quotas(path) -> tuple[int, ...]:
+    """Per-layer quotas for serving: every layer's row must be uniform across KV heads
+    (scripts/compresslm_schedules.py:16-25)."""
+    quotas = []
+    for layer, row in enumerate(load_quota_rows(path)):
+        if len(set(row)) != 1:
+            raise ValueError(f"{path}: layer {layer} has per-head quotas {sorted(set(row))}; per-layer serving needs "
+                             f"one quota per layer")
+        quotas.append(row[0])
+    return tuple(quotas)
+
+
+# the fields scripts/convert_compresslm_checkpoint_to_hf.py:189-206 writes into compresslm_config.json
+_EXPORT_FIELDS = ("enable", "block_size", "num_code_tokens", "num_passes", "pause_xattn", "raw_prompt", "raw_tail",
+                  "replay_tail", "code_positions", "retain_tail_kv", "retain_tail_policy", "code_exclude_replay_tail",
+                  "code_token_format")
 
 
 @dataclass
@@ -91,6 +122,50 @@ class CompressLMConfig:
                 raise ValueError(f"layer_code_quotas[{layer}]={q} must be in [1, {K}]")
         if self.physical_layer_quotas and not self.layer_code_quotas:
             raise ValueError("physical_layer_quotas needs layer_code_quotas")
+
+    # -- compresslm_config.json ------------------------------------------------------------------------------------
+    @classmethod
+    def from_metadata(cls, metadata: dict, layer_quotas_path=None, physical_layer_quotas: bool = False,
+                      **overrides) -> "CompressLMConfig":
+        """Config from an export's compresslm_config.json contents, as the serving entry points build it
+        (scripts/bench_decode.py:51-58, scripts/eval_math500_compresslm.py:273-285): provenance keys that are not
+        config fields are dropped; ``layer_quotas_path`` adds per-layer quotas from a schedule file; recorded
+        ``code_token_ids`` are installed."""
+        meta = dict(metadata)
+        ids = meta.pop("code_token_ids", None)
+        names = {f.name for f in fields(cls)}
+        meta = {k: v for k, v in meta.items() if k in names and not k.startswith("_")}
+        if layer_quotas_path is not None:
+            meta["layer_code_quotas"] = load_layer_quotas(layer_quotas_path)
+            meta["physical_layer_quotas"] = bool(physical_layer_quotas)
+        meta.update(overrides)
+        cfg = cls(**meta)
+        if ids is not None and cfg.enable:
+            cfg.set_code_token_ids(ids)
+        return cfg
+
+    @classmethod
+    def from_json(cls, path, **kwargs) -> "CompressLMConfig":
+        """Load ``<model_dir>/compresslm_config.json`` (or the file itself)."""
+        p = Path(path)
+        if p.is_dir():
+            p = p / "compresslm_config.json"
+        return cls.from_metadata(json.loads(p.read_text()), **kwargs)
+
+    def to_metadata(self) -> dict:
+        """The compresslm_config.json contents (scripts/convert_compresslm_checkpoint_to_hf.py:189-206, 244), plus
+        the code token ids when they are installed."""
+        meta = {name: getattr(self, name) for name in _EXPORT_FIELDS}
+        if self._initialized:
+            meta["code_token_ids"] = list(self._code_token_ids)
+        return meta
+
+    def write_json(self, path) -> Path:
+        p = Path(path)
+        if p.is_dir():
+            p = p / "compresslm_config.json"
+        p.write_text(json.dumps(self.to_metadata(), indent=2) + "\n")
+        return p
 
     # -- positions ------------------------------------------------------------------------------------------------
     @property

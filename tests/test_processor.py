@@ -174,3 +174,43 @@ def test_request_validation():
         proc.prepare_request(ServingRequest("a", [], SamplingSpec(bad_words_token_ids=[[c] for c in CODES])))
     with pytest.raises(ValueError):
         CompressLMProcessor(CompressLMConfig(enable=True, block_size=4, num_code_tokens=4))
+
+
+def test_config_json_round_trip_and_schedule_loading(tmp_path):
+    """compresslm_config.json written as the reference's exporter writes it, read back the way its serving entry
+    points read it, with per-layer quotas from the reference's schedule file (tests/golden)."""
+    import json
+    from pathlib import Path
+
+    from abridgekv_amd.config import load_layer_quotas, load_quota_rows
+    from abridgekv_amd.workloads import QWEN3_4B_LAYER_QUOTAS
+
+    sched = Path(__file__).parent / "golden" / "sched_trunc_perlayer_mean128.json"
+    rows = load_quota_rows(sched)
+    assert len(rows) == 36 and all(len(r) == 8 for r in rows)
+    assert load_layer_quotas(sched) == QWEN3_4B_LAYER_QUOTAS
+    assert sum(load_layer_quotas(sched)) == 4608
+
+    cfg = CompressLMConfig(enable=True, block_size=512, num_code_tokens=256)
+    cfg.set_code_token_ids(list(range(1000, 1256)))
+    path = cfg.write_json(tmp_path)
+    meta = json.loads(path.read_text())
+    assert meta["code_positions"] == "bitrev" and meta["code_token_ids"][:2] == [1000, 1001]
+    assert set(meta) == {"enable", "block_size", "num_code_tokens", "num_passes", "pause_xattn", "raw_prompt",
+                         "raw_tail", "replay_tail", "code_positions", "retain_tail_kv", "retain_tail_policy",
+                         "code_exclude_replay_tail", "code_token_format", "code_token_ids"}
+    meta["code_rows_of_k_max"] = 256                       # exporter provenance, not a config field
+    path.write_text(json.dumps(meta))
+    back = CompressLMConfig.from_json(tmp_path, layer_quotas_path=sched, physical_layer_quotas=True)
+    assert back.layer_code_quotas == QWEN3_4B_LAYER_QUOTAS and back.uses_physical_layer_quotas
+    assert back.code_token_ids == list(range(1000, 1256))
+    groups, gq = back.kv_cache_groups(36)
+    assert gq == [256, 64, 64, 128, 128, 128] and groups[0] == [0, 15, 18, 20, 21, 24]
+
+    bad = tmp_path / "bad.json"
+    bad.write_text(json.dumps([[64] * 7 + [128]]))
+    with pytest.raises(ValueError):
+        load_layer_quotas(bad)
+    bad.write_text(json.dumps({"other": 1}))
+    with pytest.raises(ValueError):
+        load_quota_rows(bad)
