@@ -25,6 +25,8 @@ SIGNATURES = {
                                       C.c_int, _vp, C.c_size_t, _vp]),
     "abkv_kv_append": (C.c_int, [_vp, C.c_long, _vp, C.c_long, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_long,
                                  C.c_int, C.c_int, _vp]),
+    "abkv_rope_kv_append": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_long, _vp, C.c_long, _vp, C.c_int, C.c_int,
+                                      C.c_int, _vp, C.c_long, _vp, _vp, C.c_int, _vp]),
     "abkv_slot_mapping": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_int, _vp, _vp]),
     "abkv_prefill_masked_attn": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
                                            _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,

@@ -157,6 +157,87 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const char* key, long k_
   }
 }
 
+// Fused rotary embedding + KV append for the served geometry (32 query / 8 KV heads, head size 128, NeoX halves):
+// q[t] rotated in place, key[t] rotated in place and, with value[t], written to the cache at slot_mapping[t].
+// Replaces the model-side rotary op plus reshape_and_cache of the overlay's attention path, and computes the RoPE
+// position of an abridged-layout token on the device when block_c > 0 (logical position of period block_c +
+// codes_k -> block * block_c + (offset < block_c ? offset : bitrev code offset), config/compresslm.py:192-216).
+struct RopeArgs {
+  __bf16* q; long q_st, q_sh;                  // [T, 32, 128]
+  __bf16* k; long k_st;                        // [T, 8, 128] (heads contiguous)
+  const __bf16* v; long v_st;                  // [T, 8, 128]
+  const int64_t* positions;                    // [T]
+  const float* cos_sin;                        // [max_pos, 128]: cos of the 64 frequencies, then sin
+  long max_pos;
+  int block_c, codes_k, log2_k;                // block_c == 0: positions are RoPE positions already
+  const int64_t* slot_mapping;                 // [T] or nullptr (rotate only); < 0 or past the cache = skip
+  __bf16* cache; long num_pages;
+};
+
+__device__ __forceinline__ long rope_position(const RopeArgs& a, long pos) {
+  if (pos < 0) pos = 0;
+  if (a.block_c > 0) {
+    const long per = a.block_c + a.codes_k;
+    const long blk = pos / per;
+    const int w = (int)(pos - blk * per);
+    long off = w;
+    if (w >= a.block_c) {
+      const unsigned k = (unsigned)(w - a.block_c);
+      const unsigned rev = a.log2_k > 0 ? (__brev(k) >> (32 - a.log2_k)) : 0u;
+      off = ((long)rev * a.block_c) / a.codes_k;
+    }
+    pos = blk * a.block_c + off;
+  }
+  return pos < a.max_pos ? pos : a.max_pos - 1;
+}
+
+// One workgroup per token: 512 q units + 128 k units of 4 rotation pairs (dims 4g..4g+3 with 64+4g..64+4g+3).
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
+  const int t = blockIdx.x;
+  const long pos = rope_position(a, a.positions[t]);
+  const float* cs = a.cos_sin + pos * kHeadDim;
+  long slot = a.slot_mapping ? a.slot_mapping[t] : -1;
+  if (slot >= a.num_pages * kPage) slot = -1;
+  __bf16* kv_slot = slot >= 0 ? a.cache + (slot / kPage) * kPageElems + (slot % kPage) * kSlotElems : nullptr;
+  for (int u = threadIdx.x; u < (kHeadsQ + kHeadsKV) * 16; u += 256) {
+    const bool isq = u < kHeadsQ * 16;
+    const int uu = isq ? u : u - kHeadsQ * 16;
+    const int h = uu >> 4, g = uu & 15;
+    __bf16* row = isq ? a.q + (long)t * a.q_st + (long)h * a.q_sh : a.k + (long)t * a.k_st + h * kHeadDim;
+    const u32x2 x1w = *reinterpret_cast<const u32x2*>(row + 4 * g);
+    const u32x2 x2w = *reinterpret_cast<const u32x2*>(row + 64 + 4 * g);
+    const floatx4 c = *reinterpret_cast<const floatx4*>(cs + 4 * g);
+    const floatx4 sn = *reinterpret_cast<const floatx4*>(cs + 64 + 4 * g);
+    float x1[4], x2[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      x1[2 * i] = __uint_as_float(x1w[i] << 16);
+      x1[2 * i + 1] = __uint_as_float(x1w[i] & 0xffff0000u);
+      x2[2 * i] = __uint_as_float(x2w[i] << 16);
+      x2[2 * i + 1] = __uint_as_float(x2w[i] & 0xffff0000u);
+    }
+    u32x2 o1, o2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      o1[i] = pack_bf16x2(x1[2 * i] * c[2 * i] - x2[2 * i] * sn[2 * i],
+                          x1[2 * i + 1] * c[2 * i + 1] - x2[2 * i + 1] * sn[2 * i + 1]);
+      o2[i] = pack_bf16x2(x2[2 * i] * c[2 * i] + x1[2 * i] * sn[2 * i],
+                          x2[2 * i + 1] * c[2 * i + 1] + x1[2 * i + 1] * sn[2 * i + 1]);
+    }
+    *reinterpret_cast<u32x2*>(row + 4 * g) = o1;
+    *reinterpret_cast<u32x2*>(row + 64 + 4 * g) = o2;
+    if (!isq && kv_slot != nullptr) {
+      *reinterpret_cast<u32x2*>(kv_slot + h * kHeadDim + 4 * g) = o1;
+      *reinterpret_cast<u32x2*>(kv_slot + h * kHeadDim + 64 + 4 * g) = o2;
+    }
+  }
+  if (kv_slot != nullptr && threadIdx.x < kSlotElems / 8) {      // V row: 128 x 16 B
+    const int i = threadIdx.x;
+    *reinterpret_cast<u32x4*>(kv_slot + kHalfElems + 8 * i) =
+        *reinterpret_cast<const u32x4*>(a.v + (long)t * a.v_st + 8 * i);
+  }
+}
+
 // slot_mapping[t] = table[req[t]][pos[t] / block_size] * block_size + pos[t] % block_size; -1 for a negative
 // position or one past the table (pos >= width * block_size) or a request index outside [0, num_reqs).
 __global__ void slot_mapping_kernel(const int32_t* req_idx, const int64_t* positions, const int32_t* block_table,
@@ -244,6 +325,42 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
   hipLaunchKernelGGL(kv_append_kernel, dim3(num_tokens), dim3(256), 0, stream, static_cast<const char*>(key),
                      key_stride, static_cast<const char*>(value), value_stride, slot_mapping,
                      static_cast<char*>(kv_cache), page_bytes, half_bytes, slot_bytes, block_size, (long)num_pages);
+  return (int)hipGetLastError();
+}
+
+int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, long key_stride_t, const void* value,
+                        long value_stride_t, const int64_t* positions, int num_tokens, int block_c, int codes_k,
+                        const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
+                        int num_pages, hipStream_t stream) {
+  using namespace abkv;
+  if (num_tokens <= 0) return 0;
+  if (q == nullptr || key == nullptr || value == nullptr || positions == nullptr || cos_sin == nullptr ||
+      max_pos <= 0 || block_c < 0 || (slot_mapping != nullptr && (kv_cache == nullptr || num_pages <= 0)))
+    return (int)hipErrorInvalidValue;
+  int log2_k = 0;
+  if (block_c > 0) {
+    if (codes_k <= 0 || (codes_k & (codes_k - 1)) || (block_c & (block_c - 1)) || codes_k > block_c)
+      return (int)hipErrorInvalidValue;
+    while ((1 << log2_k) < codes_k) ++log2_k;
+  }
+  RopeArgs a;
+  a.q = static_cast<__bf16*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.k = static_cast<__bf16*>(key);
+  a.k_st = key_stride_t;
+  a.v = static_cast<const __bf16*>(value);
+  a.v_st = value_stride_t;
+  a.positions = positions;
+  a.cos_sin = cos_sin;
+  a.max_pos = max_pos;
+  a.block_c = block_c;
+  a.codes_k = codes_k;
+  a.log2_k = log2_k;
+  a.slot_mapping = slot_mapping;
+  a.cache = static_cast<__bf16*>(kv_cache);
+  a.num_pages = num_pages;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(num_tokens), dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 

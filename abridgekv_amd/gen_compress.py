@@ -5,7 +5,8 @@ Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``
 raw prompt, per-layer code quotas, no tails). The reference keeps a dense per-layer store and masks it; here
 every layer's rows live in paged caches, quotas are physical, and the block boundary is a compaction:
 
-* content chunks append K/V at the group's next physical slots (``abkv_kv_append``) and attend over every resident
+* content chunks rotate q/k and append K/V at the group's next physical slots in one launch
+  (``abkv_rope_kv_append``) and attend over every resident
   row: one token -> ``abkv_decode_attn``, several -> causal ``abkv_paged_prefill_attn``. Resident rows are exactly
   the reference's visible set (codes of earlier blocks, raw prompt, the current block's content;
   gen_compress.py:667-707).
@@ -34,11 +35,6 @@ _UNSUPPORTED = ("capture_hidden", "capture_attention", "code_init_override", "ra
                 "oracle_full_history", "oracle_history_layers", "preserve_full_history", "retain_full_history_layers",
                 "history_replaces_codes_layers", "capture_content_attention", "content_attention_offsets",
                 "content_head_callback", "evict_policy", "keep_per_block", "evict_seed", "skip_unused_codes")
-
-
-def _rotate_half(x):
-    h = x.shape[-1] // 2
-    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
 
 
 def _layer_quotas(head_code_quotas, num_layers, num_kv_heads, K):
@@ -114,6 +110,9 @@ class CompressGen:
         self._cur_ids: list[int] = []
         self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C)).to(self.device)
                               if self.code_positions == "bitrev" else None)
+        # fp32 cos/sin of the model's rotary embedding for every position this sequence can reach (RoPE positions
+        # never exceed logical positions); the fused kernel rotates q/k and appends K/V in one launch per layer
+        self._cos_sin = ops.rotary_cos_sin_from_model(self.inner.rotary_emb, int(max_tokens) + 1, self.device)
 
     # -- positions ------------------------------------------------------------------------------------------------
     def _content_pos(self, n):
@@ -153,10 +152,11 @@ class CompressGen:
         if self.planner.allocate_slots(self.rid, n) is None:
             raise RuntimeError("page pool exhausted; raise max_tokens")
         mds = self._group_metadata(n, code_step)
-        cos, sin = self.inner.rotary_emb(hidden, positions.view(1, -1))
-        cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)                      # [1, n, 1, D]
+        positions = positions.to(torch.int64).contiguous()
         for li, layer in enumerate(self.layers):
             attn = layer.self_attn
+            md = mds[self.group_of[li]]
+            cache = self.caches[self.tensor_of[li]]
             normed = layer.input_layernorm(hidden)
             q = attn.q_proj(normed).view(1, n, -1, attn.head_dim)
             k = attn.k_proj(normed).view(1, n, -1, attn.head_dim)
@@ -164,12 +164,12 @@ class CompressGen:
                 q = attn.q_norm(q)
             if getattr(attn, "k_norm", None) is not None:
                 k = attn.k_norm(k)
-            v = attn.v_proj(normed).view(1, n, -1, attn.head_dim)
-            q = (q * cos + _rotate_half(q) * sin).to(self.dtype)
-            k = (k * cos + _rotate_half(k) * sin).to(self.dtype)
-            o = torch.empty((n, ops.HEADS_Q * ops.HEAD_DIM), dtype=self.dtype, device=self.device)
-            self.impl.forward(layer, q[0].reshape(n, -1), k[0].contiguous(), v[0].contiguous(),
-                              self.caches[self.tensor_of[li]], mds[self.group_of[li]], o)
+            q = q[0].to(self.dtype).contiguous()
+            k = k[0].to(self.dtype).contiguous()
+            v = attn.v_proj(normed).view(n, -1, attn.head_dim).contiguous()
+            ops.rope_kv_append(q, k, v, positions, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache)
+            o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
+            self.impl.attend(q, cache, md, o)
             h = hidden + attn.o_proj(o.view(1, n, -1))
             hidden = h + layer.mlp(layer.post_attention_layernorm(h))
         self.logical_len += n

@@ -178,6 +178,57 @@ def kv_append(key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor
     check(rc, "abkv_kv_append")
 
 
+def rope_cos_sin_cache(max_pos: int, theta: float = 1e6, device=None) -> torch.Tensor:
+    """[max_pos, 128] fp32 table of cos then sin of the 64 NeoX rotary frequencies, computed as HF's default
+    rotary embedding computes them (fp32 inverse frequencies theta^(-2i/128), fp32 products)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, HEAD_DIM, 2, dtype=torch.int64).float() / HEAD_DIM))
+    freqs = torch.arange(max_pos, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    return torch.cat([freqs.cos(), freqs.sin()], dim=1).contiguous().to(device)
+
+
+def rotary_cos_sin_from_model(rotary_emb, max_pos: int, device) -> torch.Tensor:
+    """The same table from a HuggingFace rotary-embedding module (whatever its scaling), in fp32."""
+    x = torch.zeros((1, 1, HEAD_DIM), dtype=torch.float32, device=device)
+    cos, sin = rotary_emb(x, torch.arange(max_pos, device=device).view(1, -1))
+    half = HEAD_DIM // 2
+    return torch.cat([cos[0, :, :half], sin[0, :, :half]], dim=1).float().contiguous()
+
+
+def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, positions: torch.Tensor,
+                   cos_sin: torch.Tensor, slot_mapping: torch.Tensor | None = None,
+                   kv_cache: torch.Tensor | None = None, block_c: int = 0, codes_k: int = 0) -> None:
+    """Rotate q [T, 32, 128] and key [T, 8, 128] in place (NeoX halves) and write rotated key and value rows at
+    slot_mapping (int64, < 0 = skip; None = rotate only). positions [T] int64: RoPE positions, or logical positions
+    of the abridged layout when block_c > 0 (mapped to bitrev RoPE positions on the device)."""
+    T = positions.numel()
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1 and q.shape[0] >= T, "q must be cuda bf16 [T, 32, 128] with contiguous dims")
+    for name, t in (("key", key), ("value", value)):
+        _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 3 and t.shape[0] >= T
+                 and tuple(t.shape[1:]) == (HEADS_KV, HEAD_DIM) and t.stride(2) == 1 and t.stride(1) == HEAD_DIM,
+                 f"{name} must be cuda bf16 [T, 8, 128] with contiguous rows")
+    _require(positions.is_cuda and positions.dtype == torch.int64 and positions.is_contiguous(),
+             "positions must be contiguous cuda int64")
+    _require(cos_sin.is_cuda and cos_sin.dtype == torch.float32 and cos_sin.dim() == 2
+             and cos_sin.shape[1] == HEAD_DIM and cos_sin.is_contiguous(), "cos_sin must be contiguous cuda fp32 [P, 128]")
+    if block_c:
+        _require(block_c > 0 and codes_k > 0 and block_c & (block_c - 1) == 0 and codes_k & (codes_k - 1) == 0
+                 and codes_k <= block_c, "block_c and codes_k must be powers of two with codes_k <= block_c")
+    num_pages = 0
+    if slot_mapping is not None:
+        _check_cache(kv_cache)
+        _require(slot_mapping.is_cuda and slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous()
+                 and slot_mapping.numel() >= T, "slot_mapping must be contiguous cuda int64 [T]")
+        num_pages = kv_cache.shape[0]
+    if T == 0:
+        return
+    rc = lib().abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(key), key.stride(0), _ptr(value),
+                                   value.stride(0), _ptr(positions), T, int(block_c), int(codes_k), _ptr(cos_sin),
+                                   cos_sin.shape[0], _ptr(slot_mapping), _ptr(kv_cache), num_pages,
+                                   C.c_void_p(_stream()))
+    check(rc, "abkv_rope_kv_append")
+
+
 def slot_mapping(req_idx: torch.Tensor, positions: torch.Tensor, block_table: torch.Tensor,
                  out: torch.Tensor | None = None) -> torch.Tensor:
     """Device slot mapping: table[req][pos // 16] * 16 + pos % 16 (negative positions -> -1)."""

@@ -64,6 +64,20 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
                    const int64_t* slot_mapping, int num_tokens, void* kv_cache, int num_pages, long page_bytes,
                    long half_bytes, int slot_bytes, int block_size, abkv_stream_t stream);
 
+/* Fused rotary embedding + KV append (served geometry: 32 query / 8 KV heads, head size 128, NeoX halves).
+ * Replaces the model's rotary op followed by reshape_and_cache on the overlay's attention path (positions from
+ * third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1593-1598 via config/compresslm.py:208-216; slots from
+ * block_table.py:186-197). q [T, 32, 128] (strides in elements, dims contiguous) and key [T, 8, 128] are rotated in
+ * place; rotated key and value rows are written at slot_mapping[t] (NULL: rotate only; < 0 or past the cache: skip).
+ * positions [T] int64: RoPE positions when block_c == 0; otherwise logical positions of the abridged layout (period
+ * block_c + codes_k, both powers of two) mapped on the device to block * block_c + (offset < block_c ? offset :
+ * floor(bitrev(offset - block_c) * block_c / codes_k)). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
+ * frequencies then their sin; positions are clamped into [0, max_pos). */
+int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, long key_stride_t, const void* value,
+                        long value_stride_t, const int64_t* positions, int num_tokens, int block_c, int codes_k,
+                        const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
+                        int num_pages, abkv_stream_t stream);
+
 /* Slot mapping on device: BlockTable.compute_slot_mapping (block_table.py:186-197, non-CP branch).
  * slot = table[req_idx[t]][pos / block_size] * block_size + pos % block_size; -1 when pos < 0, pos is past the
  * table row (block_table_stride pages) or req_idx[t] is outside [0, num_reqs). */

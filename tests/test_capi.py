@@ -4,6 +4,8 @@ import re
 import subprocess
 from pathlib import Path
 
+import pytest
+
 from abridgekv_amd import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -43,3 +45,22 @@ def test_host_only_entry_points_run_without_gpu():
     assert h
     assert lib.abkv_planner_num_free(h) == 7
     lib.abkv_planner_destroy(h)
+
+
+def test_rope_table_matches_hf_rotary():
+    """The fp32 cos/sin table equals HF's default rotary embedding values and is close to the float64 closed form."""
+    import math
+
+    import torch
+    transformers = pytest.importorskip("transformers")
+    from abridgekv_amd import ops
+
+    table = ops.rope_cos_sin_cache(4096, theta=1e6)
+    cfg = transformers.Qwen3Config(hidden_size=256, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                                   rope_parameters={"rope_theta": 1e6, "rope_type": "default"})
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
+    hf = ops.rotary_cos_sin_from_model(Qwen3RotaryEmbedding(cfg), 4096, "cpu")
+    assert torch.equal(table, hf)
+    pos, i = 1234, 5
+    want = math.cos(pos * 1e6 ** (-2 * i / 128))
+    assert abs(table[pos, i].item() - want) < 1e-4
