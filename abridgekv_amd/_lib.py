@@ -27,7 +27,16 @@ SIGNATURES = {
                                  C.c_int, C.c_int, _vp]),
     "abkv_rope_kv_append": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_long, _vp, C.c_long, _vp, C.c_int, C.c_int,
                                       C.c_int, _vp, C.c_long, _vp, _vp, C.c_int, _vp]),
-    "abkv_slot_mapping": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_int, _vp, _vp]),
+    "abkv_decode_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, _vp, C.c_int, C.c_int,
+                                       C.c_float, _vp, C.c_long, C.c_long, _vp, _vp]),
+    "abkv_paged_prefill_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp,
+                                              _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long,
+                                              C.c_long, _vp, _vp]),
+    "abkv_prefill_masked_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
+                                               _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               C.c_int, _vp, _vp, C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp,
+                                               _vp]),
+    "abkv_slot_mapping": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_int, _vp, _vp, _vp]),
     "abkv_prefill_masked_attn": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
                                            _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
                                            C.c_int, _vp, _vp, C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp,

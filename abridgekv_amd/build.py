@@ -14,7 +14,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libabridgekv_amd.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-DEVICE_SOURCES = ["decode_attn.hip", "kv_cache.hip", "prefill_attn.hip", "paged_prefill.hip"]
+DEVICE_SOURCES = ["decode_attn.hip", "kv_cache.hip", "prefill_attn.hip", "paged_prefill.hip", "attn_f32.hip"]
 HOST_SOURCES = ["planner.cpp"]
 
 # -packed-fp32-ops off: hipcc would otherwise emit v_pk_{add,mul,fma}_f32 from scalar float code.

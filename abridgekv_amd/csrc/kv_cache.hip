@@ -241,12 +241,17 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
 // slot_mapping[t] = table[req[t]][pos[t] / block_size] * block_size + pos[t] % block_size; -1 for a negative
 // position or one past the table (pos >= width * block_size) or a request index outside [0, num_reqs).
 __global__ void slot_mapping_kernel(const int32_t* req_idx, const int64_t* positions, const int32_t* block_table,
-                                    int num_reqs, long bt_stride, int block_size, int64_t* slots, int n) {
+                                    int num_reqs, long bt_stride, int block_size, const int32_t* compacted,
+                                    int64_t* slots, int n) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n) return;
-  const long pos = positions[t];
   const int r = req_idx[t];
-  if (pos < 0 || pos >= bt_stride * block_size || r < 0 || r >= num_reqs) {
+  if (r < 0 || r >= num_reqs) {
+    slots[t] = -1;
+    return;
+  }
+  const long pos = positions[t] - (compacted != nullptr ? compacted[r] : 0);   // logical -> physical in the group
+  if (pos < 0 || pos >= bt_stride * block_size) {
     slots[t] = -1;
     return;
   }
@@ -365,14 +370,15 @@ int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, lo
 }
 
 int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_tokens, const int32_t* block_table,
-                      int num_reqs, long block_table_stride, int block_size, int64_t* slot_mapping,
-                      hipStream_t stream) {
+                      int num_reqs, long block_table_stride, int block_size, const int32_t* compacted,
+                      int64_t* slot_mapping, hipStream_t stream) {
   if (num_tokens <= 0) return 0;
   if (req_idx == nullptr || positions == nullptr || block_table == nullptr || slot_mapping == nullptr ||
       block_size <= 0)
     return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(abkv::slot_mapping_kernel, dim3((num_tokens + 255) / 256), dim3(256), 0, stream, req_idx,
-                     positions, block_table, num_reqs, block_table_stride, block_size, slot_mapping, num_tokens);
+                     positions, block_table, num_reqs, block_table_stride, block_size, compacted, slot_mapping,
+                     num_tokens);
   return (int)hipGetLastError();
 }
 

@@ -52,9 +52,9 @@ def _row_stride(block_table: torch.Tensor) -> int:
     return block_table.stride(0)
 
 
-def _check_cache(kv_cache: torch.Tensor) -> None:
+def _check_cache(kv_cache: torch.Tensor, dtype=torch.bfloat16) -> None:
     _require(kv_cache.is_cuda, "kv_cache must be on the GPU")
-    _require(kv_cache.dtype == torch.bfloat16, "kv_cache must be bfloat16")
+    _require(kv_cache.dtype == dtype, f"kv_cache must be {dtype}")
     _require(kv_cache.dim() == 5 and tuple(kv_cache.shape[1:]) == (2, PAGE, HEADS_KV, HEAD_DIM),
              f"kv_cache must be [P, 2, {PAGE}, {HEADS_KV}, {HEAD_DIM}], got {tuple(kv_cache.shape)}")
     _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
@@ -79,7 +79,10 @@ def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch
     q [B, 32, 128] bf16 (dims contiguous); kv_cache [P, 2, 16, 8, 128] bf16; block_table [B, W] int32;
     seq_lens [B] int32 (physical rows); ``max_pages`` bounds ceil(seq_len / 16) (defaults to W).
     Writes and returns (out [B, 32, 128] bf16, lse [B, 32] fp32 natural log or None).
+    fp32 q and cache select the fp32 mode (out fp32; split_pages and workspace unused).
     """
+    if q.dtype == torch.float32:
+        return _decode_attention_f32(q, kv_cache, block_table, seq_lens, scale, max_pages, out, lse)
     _check_cache(kv_cache)
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM),
              f"q must be cuda bf16 [B, {HEADS_Q}, {HEAD_DIM}]")
@@ -114,6 +117,33 @@ def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch
                                 _ptr(out), out.stride(0), out.stride(1), _ptr(lse), _ptr(workspace), ws_bytes,
                                 C.c_void_p(_stream()))
     check(rc, "abkv_decode_attn")
+    return out, lse
+
+
+def _decode_attention_f32(q, kv_cache, block_table, seq_lens, scale, max_pages, out, lse):
+    _check_cache(kv_cache, torch.float32)
+    _require(q.is_cuda and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM) and q.stride(2) == 1,
+             "q must be cuda fp32 [B, 32, 128] with contiguous dims")
+    B = q.shape[0]
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] >= B and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() >= B
+             and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32 [B]")
+    W = block_table.shape[1]
+    max_pages = W if max_pages is None else int(max_pages)
+    _require(0 < max_pages <= W, "max_pages must be in [1, block_table width]")
+    if out is None:
+        out = torch.empty((B, HEADS_Q, HEAD_DIM), dtype=torch.float32, device=q.device)
+    _require(out.dtype == torch.float32 and tuple(out.shape) == (B, HEADS_Q, HEAD_DIM) and out.stride(2) == 1
+             and out.stride(1) % 2 == 0, "out must be fp32 [B, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= B * HEADS_Q,
+                 "lse must be contiguous fp32 [B, 32]")
+    rc = lib().abkv_decode_attn_f32(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                    _ptr(block_table), _row_stride(block_table), _ptr(seq_lens), B, max_pages,
+                                    float(scale), _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+                                    C.c_void_p(_stream()))
+    check(rc, "abkv_decode_attn_f32")
     return out, lse
 
 
@@ -230,20 +260,24 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
 
 
 def slot_mapping(req_idx: torch.Tensor, positions: torch.Tensor, block_table: torch.Tensor,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """Device slot mapping: table[req][pos // 16] * 16 + pos % 16 (negative positions -> -1)."""
+                 out: torch.Tensor | None = None, compacted: torch.Tensor | None = None) -> torch.Tensor:
+    """Device slot mapping of one KV-cache group: table[req][p // 16] * 16 + p % 16 with p = positions -
+    compacted[req] (``compacted`` [num_reqs] int32: tokens the group removed per request; None: positions are
+    physical). Positions before the table or past its width map to -1."""
     _require(req_idx.is_cuda and req_idx.dtype == torch.int32 and req_idx.is_contiguous(), "req_idx: cuda int32")
     _require(positions.is_cuda and positions.dtype == torch.int64 and positions.is_contiguous(),
              "positions: cuda int64")
     _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.is_contiguous(),
              "block_table: contiguous cuda int32 [B, W]")
+    if compacted is not None:
+        _require(compacted.is_cuda and compacted.dtype == torch.int32 and compacted.is_contiguous()
+                 and compacted.numel() >= block_table.shape[0], "compacted: contiguous cuda int32 [num_reqs]")
     n = positions.numel()
     if out is None:
         out = torch.empty(n, dtype=torch.int64, device=positions.device)
     _require(req_idx.numel() == n, "req_idx and positions must have the same length")
     rc = lib().abkv_slot_mapping(_ptr(req_idx), _ptr(positions), n, _ptr(block_table), block_table.shape[0],
-                                 block_table.shape[1], PAGE,
-                                 _ptr(out), C.c_void_p(_stream()))
+                                 block_table.shape[1], PAGE, _ptr(compacted), _ptr(out), C.c_void_p(_stream()))
     check(rc, "abkv_slot_mapping")
     return out
 
@@ -257,9 +291,11 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     q [B, S0, 32, 128], k/v [B, S0, 8, 128] bf16 (any strides with contiguous dims, e.g. the [B, H, S, D]
     transposed views HF attention receives, permuted back); prompt_len [B] int32 raw-prompt content tokens;
     head_quota [32] int32 code slots visible per query head. Returns (out [B, S0, 32, 128] bf16,
-    lse [B, 32, S0] fp32 natural log or None).
+    lse [B, 32, S0] fp32 natural log or None). fp32 q/k/v select the fp32 mode (out fp32).
     """
     B, S0 = q.shape[0], q.shape[1]
+    if q.dtype == torch.float32:
+        return _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse)
     _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
         _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
@@ -287,6 +323,36 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     return out, lse
 
 
+def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse):
+    B, S0 = q.shape[0], q.shape[1]
+    _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
+    for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
+        _require(t.is_cuda and t.dtype == torch.float32 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
+                 and t.stride(3) == 1 and all(x % 4 == 0 for x in t.stride()[:3]),
+                 f"{name} must be cuda fp32 [B, S0, {h}, {HEAD_DIM}] with contiguous, 16-byte aligned rows")
+    if prompt_len is not None:
+        _require(prompt_len.is_cuda and prompt_len.dtype == torch.int32 and prompt_len.numel() == B
+                 and prompt_len.is_contiguous(), "prompt_len must be contiguous cuda int32 [B]")
+    if head_quota is not None:
+        _require(head_quota.is_cuda and head_quota.dtype == torch.int32 and head_quota.numel() == HEADS_Q
+                 and head_quota.is_contiguous(), "head_quota must be contiguous cuda int32 [32]")
+    if out is None:
+        out = torch.empty((B, S0, HEADS_Q, HEAD_DIM), dtype=torch.float32, device=q.device)
+    _require(out.dtype == torch.float32 and tuple(out.shape) == (B, S0, HEADS_Q, HEAD_DIM) and out.stride(3) == 1
+             and all(x % 2 == 0 for x in out.stride()[:3]), "out must be fp32 [B, S0, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, HEADS_Q, S0),
+                 "lse must be contiguous fp32 [B, 32, S0]")
+    scale = default_scale() if scale is None else float(scale)
+    rc = lib().abkv_prefill_masked_attn_f32(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
+                                            k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+                                            B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota),
+                                            scale, _ptr(out), out.stride(0), out.stride(1), out.stride(2), _ptr(lse),
+                                            C.c_void_p(_stream()))
+    check(rc, "abkv_prefill_masked_attn_f32")
+    return out, lse
+
+
 def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start, kv_start,
                             kv_limit, causal, scale: float | None = None, out: torch.Tensor | None = None,
                             lse: torch.Tensor | None = None):
@@ -297,13 +363,15 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     sequences (the metadata builder's CPU copies) -- request r's queries are tokens q_start[r]..q_start[r+1]-1 at
     physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
     ``causal``: a bool for the whole batch or one flag per request (code steps and prompt chunks may share a batch).
-    Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None).
+    Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None). fp32 q and cache select the fp32 mode (out fp32).
     """
     import numpy as np
 
-    _check_cache(kv_cache)
-    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
-             and q.stride(2) == 1, "q must be cuda bf16 [T, 32, 128] with contiguous dims")
+    f32 = q.dtype == torch.float32
+    dt = torch.float32 if f32 else torch.bfloat16
+    _check_cache(kv_cache, dt)
+    _require(q.is_cuda and q.dtype == dt and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1, "q must be cuda [T, 32, 128] with contiguous dims")
     _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
              and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
     qs = np.asarray(q_start, dtype=np.int64)
@@ -317,13 +385,29 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     _require(np.all(ks >= 0), "kv_start must be non-negative")
     T = q.shape[0]
     if out is None:
-        out = torch.empty((T, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
-    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (T, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
-             "out must be bf16 [T, 32, 128] with contiguous dims")
+        out = torch.empty((T, HEADS_Q, HEAD_DIM), dtype=dt, device=q.device)
+    _require(out.dtype == dt and tuple(out.shape) == (T, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
+             "out must be [T, 32, 128] (dtype of q) with contiguous dims")
     if lse is not None:
         _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (T, HEADS_Q),
                  "lse must be contiguous fp32 [T, 32]")
     nq = np.diff(qs)
+    if f32:
+        if qs[-1] == 0:
+            return out, lse
+        dev = q.device
+        cz = np.broadcast_to(np.asarray(causal, dtype=np.int64), (B,)).astype(np.int64)
+        tok_req = np.repeat(np.arange(B), nq)
+        meta = torch.from_numpy(np.concatenate([qs, ks, kl, cz, tok_req]).astype(np.int32)).to(dev)
+        o1, o2, o3, o4 = B + 1, 2 * B + 1, 3 * B + 1, 4 * B + 1
+        scale = default_scale() if scale is None else float(scale)
+        rc = lib().abkv_paged_prefill_attn_f32(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                               _ptr(block_table), _row_stride(block_table), W, _ptr(meta[:o1]),
+                                               _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(meta[o4:]), int(qs[-1]),
+                                               _ptr(meta[o3:o4]), 1, scale, _ptr(out), out.stride(0), out.stride(1),
+                                               _ptr(lse), C.c_void_p(_stream()))
+        check(rc, "abkv_paged_prefill_attn_f32")
+        return out, lse
     tiles = [(r, q0) for r in range(B) for q0 in range(0, int(nq[r]), 64)]
     if not tiles:
         return out, lse

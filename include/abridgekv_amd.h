@@ -78,12 +78,14 @@ int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, lo
                         const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
                         int num_pages, abkv_stream_t stream);
 
-/* Slot mapping on device: BlockTable.compute_slot_mapping (block_table.py:186-197, non-CP branch).
- * slot = table[req_idx[t]][pos / block_size] * block_size + pos % block_size; -1 when pos < 0, pos is past the
- * table row (block_table_stride pages) or req_idx[t] is outside [0, num_reqs). */
+/* Slot mapping on device: BlockTable.compute_slot_mapping (block_table.py:186-197, non-CP branch) on the physical
+ * positions of one KV-cache group (gpu_model_runner.py:1579-1590: phys = logical - compacted[req, group]).
+ * slot = table[r][p / block_size] * block_size + p % block_size with r = req_idx[t], p = positions[t] -
+ * compacted[r] (compacted NULL: positions are physical); -1 when p < 0, p is past the table row
+ * (block_table_stride pages) or r is outside [0, num_reqs). */
 int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_tokens, const int32_t* block_table,
-                      int num_reqs, long block_table_stride, int block_size, int64_t* slot_mapping,
-                      abkv_stream_t stream);
+                      int num_reqs, long block_table_stride, int block_size, const int32_t* compacted,
+                      int64_t* slot_mapping, abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Block-masked teacher-forced attention (kernel 3).
@@ -118,6 +120,35 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
                             const int32_t* tile_req, const int32_t* tile_q0, int num_tiles, const int32_t* causal,
                             int causal_default, float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
                             abkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * fp32 mode of the three attention paths (same semantics as the bf16 entry points above, fp32 q / K / V / out,
+ * fp32 accumulation and accurate exp/log): the reference's PyTorch attention run in fp32
+ * (abridgekv/gen_compress.py:359-360, 555; compresslm_packed_kv.py:608-613; compress_forward.py:695-727).
+ * Caches are [num_pages, 2, 16, 8, 128] fp32. A correctness mode, not a tuned path.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* Decode over the group page table: out [B, 32, 128] fp32 (strides), lse [B, 32] or NULL. */
+int abkv_decode_attn_f32(const float* q, long q_stride_seq, long q_stride_head, const float* kv_cache, int num_pages,
+                         const int32_t* block_table, long block_table_stride, const int32_t* seq_lens, int num_seqs,
+                         int max_pages_per_seq, float scale, float* out, long out_stride_seq, long out_stride_head,
+                         float* lse, abkv_stream_t stream);
+
+/* Paged multi-query attention (prompt chunks, code steps): as abkv_paged_prefill_attn, with tok_req [num_tokens]
+ * (request of every query token) in place of the tile list. lse [T, 32] or NULL. */
+int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h, const float* kv_cache, int num_pages,
+                                const int32_t* block_table, long block_table_stride, int block_table_width,
+                                const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
+                                const int32_t* tok_req, int num_tokens, const int32_t* causal, int causal_default,
+                                float scale, float* out, long out_stride_t, long out_stride_h, float* lse,
+                                abkv_stream_t stream);
+
+/* Compression-masked teacher-forced attention: as abkv_prefill_masked_attn (strides in elements, head dims
+ * contiguous and 16-byte aligned rows). lse [B, 32, seq_len] or NULL. */
+int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh, const float* k, long k_sb,
+                                 long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
+                                 int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
+                                 const int32_t* head_quota, float scale, float* out, long o_sb, long o_ss, long o_sh,
+                                 float* lse, abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager
