@@ -41,9 +41,10 @@ SIGNATURES = {
                                            _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
                                            C.c_int, _vp, _vp, C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp,
                                            _vp]),
+    "abkv_paged_prefill_workspace_size": (C.c_size_t, [C.c_int, C.c_int]),
     "abkv_paged_prefill_attn": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp, _vp,
                                           _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long, C.c_long,
-                                          _vp, _vp]),
+                                          _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "abkv_planner_create": (_vp, [C.c_int, C.c_int, C.c_int, _i32p, C.c_int64]),
     "abkv_planner_destroy": (None, [_vp]),
     "abkv_planner_last_error": (C.c_char_p, [_vp]),

@@ -27,6 +27,10 @@ struct PagedPrefillArgs {
   float scale_log2;
   __bf16* out; long o_st, o_sh;                // [T, 32, 128]
   float* lse;                                  // [T, 32] natural log, or nullptr
+  int split_tiles;                             // > 0: key tiles per split (grid.z splits), partials to part_*
+  int num_tokens;
+  float* part_o;                               // [splits, T, 32, 128] un-normalised
+  float* part_ml;                              // [splits, T, 32, 2] (running max in log2 units, sum)
 };
 
 __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs a) {
@@ -88,10 +92,14 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   TileMask tm;
   tm.mode = 0;
 
-  if (n_k_tiles > 0) issue_tile<kWaves>(rows, 0, k_end, Kb, Vb, w, lane);
-  for (int kt = 0; kt < n_k_tiles; ++kt) {
-    const int off_cur = (kt & 1) * kTileElems, off_nxt = ((kt & 1) ^ 1) * kTileElems;
-    if (kt + 1 < n_k_tiles) {
+  // key tiles of this block: all of them, or split z's share when the launch is split along the keys
+  const int kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
+  const int kt_end = a.split_tiles > 0 ? min(n_k_tiles, kt_begin + a.split_tiles) : n_k_tiles;
+  if (kt_begin < kt_end) issue_tile<kWaves>(rows, kt_begin * kBN, k_end, Kb, Vb, w, lane);
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int par = (kt - kt_begin) & 1;
+    const int off_cur = par * kTileElems, off_nxt = (par ^ 1) * kTileElems;
+    if (kt + 1 < kt_end) {
       issue_tile<kWaves>(rows, (kt + 1) * kBN, k_end, Kb + off_nxt, Vb + off_nxt, w, lane);
       __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
@@ -106,6 +114,25 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   }
 
   if (!qvalid) return;
+  if (a.split_tiles > 0) {                                   // partials of this key split
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      const float l = sum_xor32(sum_xor16(l_run[u]));
+      const int head = kvh * kGroup + hbase + u;
+      const long row = ((long)blockIdx.z * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
+      float* po = a.part_o + row * kHeadDim + 32 * j;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        *reinterpret_cast<floatx4*>(po + 8 * rr) = floatx4{o[0][u][rr], o[1][u][rr], o[2][u][rr], o[3][u][rr]};
+        *reinterpret_cast<floatx4*>(po + 8 * rr + 4) = floatx4{o[4][u][rr], o[5][u][rr], o[6][u][rr], o[7][u][rr]};
+      }
+      if (j == 0) {
+        a.part_ml[row * 2] = m_run[u];
+        a.part_ml[row * 2 + 1] = l;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < H; ++u) {
     const float l = sum_xor32(sum_xor16(l_run[u]));
@@ -124,9 +151,45 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   }
 }
 
+// Combine the key-split partials of every query token: workgroup (token, group of 8 heads); thread t handles head
+// 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
+__global__ __launch_bounds__(256) void paged_merge_kernel(PagedPrefillArgs a, int n_splits) {
+  const long tok = blockIdx.x;
+  const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
+  const int d0 = (threadIdx.x & 31) * 4;
+  const long stride = (long)a.num_tokens * kHeadsQ;          // rows per split
+  const float* pml = a.part_ml + (tok * kHeadsQ + head) * 2;
+  float M = -INFINITY;
+#pragma unroll 8
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[s * stride * 2]);
+  float L = 0.f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (M != -INFINITY) {
+#pragma unroll 8
+    for (int s = 0; s < n_splits; ++s) {
+      const float w = fast_exp2(pml[s * stride * 2] - M);
+      L += w * pml[s * stride * 2 + 1];
+      acc += w * *reinterpret_cast<const floatx4*>(a.part_o + ((s * stride) + tok * kHeadsQ + head) * kHeadDim + d0);
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  __bf16* oh = a.out + tok * a.o_st + (long)head * a.o_sh + d0;
+  u32x2 wv;
+  wv[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  wv[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2*>(oh) = wv;
+  if (a.lse != nullptr && (threadIdx.x & 31) == 0)
+    a.lse[tok * kHeadsQ + head] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : -INFINITY;
+}
+
 }  // namespace abkv
 
 extern "C" {
+
+size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits) {
+  return (size_t)num_tokens * (size_t)num_splits * abkv::kHeadsQ * (abkv::kHeadDim + 2) * sizeof(float);
+}
+
 
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
                             const int32_t* block_table, long block_table_stride, int block_table_width,
@@ -134,7 +197,8 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
                             const int32_t* kv_start, const int32_t* kv_limit, const int32_t* tile_req,
                             const int32_t* tile_q0, int num_tiles, const int32_t* causal, int causal_default,
                             float scale, void* out,
-                            long out_stride_t, long out_stride_h, float* lse, hipStream_t stream) {
+                            long out_stride_t, long out_stride_h, float* lse, int num_tokens, int num_splits,
+                            int split_tiles, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   using namespace abkv;
   if (num_tiles <= 0) return 0;
   if (q == nullptr || kv_cache == nullptr || block_table == nullptr || q_start == nullptr || kv_start == nullptr ||
@@ -162,7 +226,22 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;
   a.lse = lse;
-  hipLaunchKernelGGL(paged_prefill_kernel, dim3(num_tiles, kHeadsKV), dim3(512), 0, stream, a);
+  a.num_tokens = num_tokens;
+  a.split_tiles = 0;
+  a.part_o = a.part_ml = nullptr;
+  if (num_splits > 1) {
+    if (split_tiles <= 0 || num_tokens <= 0 || workspace == nullptr ||
+        workspace_bytes < abkv_paged_prefill_workspace_size(num_tokens, num_splits))
+      return (int)hipErrorInvalidValue;
+    a.split_tiles = split_tiles;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + (size_t)num_splits * num_tokens * kHeadsQ * kHeadDim;
+  }
+  hipLaunchKernelGGL(paged_prefill_kernel, dim3(num_tiles, kHeadsKV, num_splits > 1 ? num_splits : 1), dim3(512), 0,
+                     stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || num_splits <= 1) return (int)err;
+  hipLaunchKernelGGL(paged_merge_kernel, dim3(num_tokens, kHeadsQ / 8), dim3(256), 0, stream, a, num_splits);
   return (int)hipGetLastError();
 }
 

@@ -353,9 +353,21 @@ def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_
     return out, lse
 
 
+def paged_split_plan(num_tiles: int, max_keys: int, target_blocks: int = 1024, min_split_tiles: int = 8):
+    """(num_splits, split_tiles) for a paged multi-query launch of num_tiles query tiles whose longest key range is
+    max_keys: split along the keys only when the 8 KV heads x num_tiles workgroups cannot fill the GPU."""
+    max_kt = -(-int(max_keys) // 64)
+    blocks = num_tiles * HEADS_KV
+    if blocks >= target_blocks // 2 or max_kt < 2 * min_split_tiles:
+        return 1, 0
+    n = min(-(-target_blocks // blocks), max_kt // min_split_tiles)
+    split_tiles = -(-max_kt // n)
+    return -(-max_kt // split_tiles), split_tiles
+
+
 def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start, kv_start,
                             kv_limit, causal, scale: float | None = None, out: torch.Tensor | None = None,
-                            lse: torch.Tensor | None = None):
+                            lse: torch.Tensor | None = None, split: int | None = None):
     """Multi-query attention over the paged cache (prompt chunks: causal; CompressLM code step: non-causal with
     kv_limit = physical code start + quota).
 
@@ -363,6 +375,7 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     sequences (the metadata builder's CPU copies) -- request r's queries are tokens q_start[r]..q_start[r+1]-1 at
     physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
     ``causal``: a bool for the whole batch or one flag per request (code steps and prompt chunks may share a batch).
+    ``split``: key splits (None: chosen by :func:`paged_split_plan`; 1: no split).
     Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None). fp32 q and cache select the fp32 mode (out fp32).
     """
     import numpy as np
@@ -419,11 +432,22 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     q_start_d, kv_start_d = meta[: B + 1], meta[B + 1: 2 * B + 1]
     kv_limit_d, causal_d = meta[2 * B + 1: 3 * B + 1], meta[3 * B + 1:]
     scale = default_scale() if scale is None else float(scale)
+    max_keys = int(kl.max()) if kl.size else 0
+    if split is None:
+        n_splits, split_tiles = paged_split_plan(len(tiles), max_keys)
+    else:
+        n_splits = max(1, int(split))
+        split_tiles = -(-(-(-max_keys // 64)) // n_splits) if n_splits > 1 else 0
+    ws, ws_bytes = None, 0
+    if n_splits > 1:
+        _require(n_splits * split_tiles * 64 >= max_keys, "key splits must cover every key")
+        ws_bytes = lib().abkv_paged_prefill_workspace_size(T, n_splits)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                        _ptr(block_table), _row_stride(block_table), W, _ptr(q_start_d),
                                        _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
                                        _ptr(causal_d), 1, scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
-                                       C.c_void_p(_stream()))
+                                       T, n_splits, split_tiles, _ptr(ws), ws_bytes, C.c_void_p(_stream()))
     check(rc, "abkv_paged_prefill_attn")
     return out, lse
 

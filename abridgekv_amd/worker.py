@@ -66,15 +66,14 @@ def execute_kv_copy_operations(kv_copy_operations: dict, layer_caches_by_group, 
             execute_kv_copy_group(segments, caches, check=check)
 
 
-def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: bool = True):
+def split_fused_moves(fused_moves: np.ndarray, num_pages: int, check: bool = True):
     """Host side of :func:`execute_fused_moves`: split a planner step's fused move rows (request, group, src_block,
-    src_off, dst_block, dst_off) by group into one op array and segment offsets (one segment per request), uploaded
-    in a single host-to-device copy. Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)]."""
+    src_off, dst_block, dst_off) by group into an op array and segment offsets (one segment per request).
+    Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)]."""
     if fused_moves.size == 0:
         return []
     fm = np.asarray(fused_moves, dtype=np.int64)
-    parts, meta = [], []
-    at = 0
+    out = []
     for gid in np.unique(fm[:, 1]).tolist():
         rows = fm[fm[:, 1] == gid]
         cut = np.flatnonzero(np.diff(rows[:, 0])) + 1
@@ -82,11 +81,23 @@ def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: 
         ops_h = np.ascontiguousarray(rows[:, 2:6], dtype=np.int32)
         if check:
             _validate_ops(ops_h, num_pages)
-        parts += [ops_h.reshape(-1), offs]
+        out.append((gid, ops_h, offs))
+    return out
+
+
+def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: bool = True):
+    """:func:`split_fused_moves` uploaded in a single host-to-device copy.
+    Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)] on the device."""
+    parts = split_fused_moves(fused_moves, num_pages, check)
+    if not parts:
+        return []
+    flat, meta, at = [], [], 0
+    for gid, ops_h, offs in parts:
+        flat += [ops_h.reshape(-1), offs]
         meta.append((gid, at, ops_h.size, at + ops_h.size, offs.size))
         at += ops_h.size + offs.size
-    flat = torch.from_numpy(np.concatenate(parts)).to(device)
-    return [(gid, flat[o: o + n].view(-1, 4), flat[so: so + ns]) for gid, o, n, so, ns in meta]
+    dev = torch.from_numpy(np.concatenate(flat)).to(device)
+    return [(gid, dev[o: o + n].view(-1, 4), dev[so: so + ns]) for gid, o, n, so, ns in meta]
 
 
 def launch_moves(prepared, layer_caches_by_group, events=None) -> None:

@@ -49,8 +49,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=32)
-    ap.add_argument("--workload", choices=["saturated", "full_model", "prefill", "compaction", "copy"],
-                    default="saturated")
+    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "compaction", "copy"],
+                    default="serving")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     return ap.parse_args()
@@ -225,6 +225,86 @@ def bench_compaction(args, torch):
     }
 
 
+def bench_serving(args, torch):
+    """The saturated serving stress with compaction interleaved: every request decodes one token per step; a request
+    whose open block fills runs its 256 code rows in the next step (code-step attention with per-group key limits)
+    and is then compacted (planner removals + fused row moves). value = decode tokens per second of wall time."""
+    from abridgekv_amd import ops
+    from abridgekv_amd.serving import ServingStress
+
+    T, P = workloads_lengths(args)
+    t0 = time.perf_counter()
+    s = ServingStress(T, P, seed=args.seed, split_pages=args.split_pages,
+                      growth_tokens=args.steps + args.warmup + 16)
+    build_s = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        s.step()
+    torch.cuda.synchronize()
+    before = dict(s.stats)
+    s.decode_events = []
+    alg = 0
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        alg += s.decode_bytes(s.step())
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t1
+    dec_s = sum(a.elapsed_time(b) for a, b in s.decode_events) / 1e3
+    n_launch = len(s.decode_events)
+    s.decode_events = None
+    stats = {k: s.stats[k] - before[k] for k in s.stats}
+    achieved = alg / dec_s / 1e9
+    B = len(T)
+    res = {
+        "metric": "abridged decode-attn tokens/s per GPU (B=256, 32K ctx); % HBM peak BW",
+        "value": stats["decode_tokens"] / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (N(0,1) K/V pages, queries and new rows from the seed; histories replayed through the "
+                "compaction planner)",
+        "config": {"workload": f"saturated serving stress with compaction, Qwen3-4B attention (36 layers, 6 quota "
+                               f"groups 256/128/64, 32q/8kv, d128, bf16, page 16), B={B}, T~U[2048,32768], "
+                               f"P~U[128,1024]; a request closing a 512-token block runs its 256 code rows next step "
+                               f"and is compacted", "global_batch": B, "layers": s.L, "kv_groups": s.G,
+                   "split_pages": args.split_pages, "seed": args.seed, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": profiled_traffic("decode_attn_serving_b256_pmc_traffic.md"),
+                     "traffic_source": "profiles/decode_attn_serving_b256_pmc_traffic.md (decode_attn_kernel)",
+                     "kernel": "decode_attn_kernel (+ decode_merge_kernel), per layer launch",
+                     "alg_bytes_per_launch": alg / n_launch, "avg_launch_us": dec_s / n_launch * 1e6},
+        "decode_attn_ms_per_step": dec_s / args.steps * 1e3,
+        "code_steps": stats["code_steps"], "compacted_rows_moved": stats["moved_rows"],
+        "state_build_s": build_s,
+    }
+    if not args.no_cpu_baseline:
+        n = min(args.cpu_seqs, B)
+        view = _CpuView(s)
+        tps, reps, el = cpu_baseline(torch, view, s.caches, [s.q_pool[:B]] * s.L, ops.default_scale(), n)
+        res["cpu_baseline"] = {"value": tps, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"first {n} requests of the batch at the end of the run, one layer per KV "
+                                         f"group (6 of 36, scaled x6), {reps} reps in {el:.1f} s; torch CPU "
+                                         f"restatement of the reference arithmetic (bf16 scores, fp32 softmax, bf16 "
+                                         f"probs)", "cpu": platform.processor() or platform.machine()}
+    return res
+
+
+class _CpuView:
+    """The attributes cpu_baseline reads, from a serving loop's current page tables and lengths."""
+
+    def __init__(self, s):
+        self.groups = s.st.groups
+        self.layer_group = s.st.layer_group
+        self.layer_slot = s.st.layer_slot
+        self.block_tables = list(s.tables)
+        self.seq_lens = [sl.astype(np.int32) for sl in s.seq_lens]
+        self.num_layers = s.L
+
+
+def workloads_lengths(args):
+    from abridgekv_amd import workloads
+    return workloads.saturated_decode_lengths(args.batch, seed=args.seed)
+
+
 def bench_copy(args, torch):
     """Calibration kernel for the traffic counters: a plain device copy of 4 GiB (reads 4 GiB, writes 4 GiB)."""
     n = 4 << 30
@@ -252,8 +332,9 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("prefill", "compaction", "copy"):
-        res = {"prefill": bench_prefill, "compaction": bench_compaction, "copy": bench_copy}[args.workload](args, torch)
+    if args.workload in ("serving", "prefill", "compaction", "copy"):
+        res = {"serving": bench_serving, "prefill": bench_prefill, "compaction": bench_compaction,
+               "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 

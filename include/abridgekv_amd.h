@@ -112,13 +112,19 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
  * q [T, 32, 128] (token stride, head stride), request r's queries are tokens [q_start[r], q_start[r+1]) at physical
  * positions kv_start[r] + i and see keys < kv_limit[r] (and <= their position when request r is causal: causal[r] != 0,
  * or causal_default when causal is NULL). tile_req / tile_q0 [num_tiles] list the 64-row query tiles (request, first
- * row). All index arrays are device int32. lse [T, 32] or NULL.
+ * row). All index arrays are device int32. lse [T, 32] or NULL. num_splits > 1 splits every tile's keys into
+ * num_splits ranges of split_tiles 64-key tiles (split z covers tiles [z * split_tiles, (z + 1) * split_tiles); the
+ * ranges must cover every request's keys) computed by separate workgroups and merged; the partials use workspace
+ * (>= abkv_paged_prefill_workspace_size(num_tokens, num_splits) bytes; num_tokens = T). num_splits <= 1: no split,
+ * no workspace.
  * ------------------------------------------------------------------------------------------------------------- */
+size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits);
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
                             const int32_t* block_table, long block_table_stride, int block_table_width,
                             const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
                             const int32_t* tile_req, const int32_t* tile_q0, int num_tiles, const int32_t* causal,
                             int causal_default, float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
+                            int num_tokens, int num_splits, int split_tiles, void* workspace, size_t workspace_bytes,
                             abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------

@@ -36,18 +36,20 @@ def _oracle(q_rows, cache, table, kv_start, limit, causal):
     return out, lse
 
 
-def _run(cache_bf, tables, q, q_start, kv_start, kv_limit, causal):
+def _run(cache_bf, tables, q, q_start, kv_start, kv_limit, causal, split=None):
     from abridgekv_amd import ops
     dev = torch.device("cuda")
     lse = torch.empty((q.shape[0], 32), dtype=torch.float32, device=dev)
     out, _ = ops.paged_prefill_attention(q.to(dev), cache_bf.to(dev), torch.from_numpy(tables).to(dev), q_start,
-                                         kv_start, kv_limit, causal, lse=lse)
+                                         kv_start, kv_limit, causal, lse=lse, split=split)
     torch.cuda.synchronize()
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
 
-def test_code_step_limits_per_group_quota():
-    """K=256 code queries per request at physical positions [R, R+256), visible keys < R + q (own slots >= q hidden)."""
+@pytest.mark.parametrize("split", [None, 1, 3, 7])
+def test_code_step_limits_per_group_quota(split):
+    """K=256 code queries per request at physical positions [R, R+256), visible keys < R + q (own slots >= q hidden);
+    with the keys split over several workgroups and merged, or not."""
     resident = [700, 1301, 45]
     quotas = [64, 256, 128]
     cache, tables = _setup([r + 256 for r in resident], 400, 0)
@@ -55,7 +57,7 @@ def test_code_step_limits_per_group_quota():
     q = torch.randn((3 * 256, 32, 128), generator=g).to(torch.bfloat16)
     q_start = [0, 256, 512, 768]
     kv_limit = [r + qq for r, qq in zip(resident, quotas)]
-    out, lse = _run(cache, tables, q, q_start, resident, kv_limit, causal=False)
+    out, lse = _run(cache, tables, q, q_start, resident, kv_limit, causal=False, split=split)
     cf = cache.float().numpy()
     for r in range(3):
         ro, rl = _oracle(q[q_start[r]: q_start[r + 1]].float().numpy(), cf, tables[r], resident[r], kv_limit[r],
@@ -73,7 +75,7 @@ def test_causal_prompt_chunks_ragged():
     g = torch.Generator().manual_seed(3)
     q_start = np.concatenate([[0], np.cumsum(nq)]).tolist()
     q = torch.randn((q_start[-1], 32, 128), generator=g).to(torch.bfloat16)
-    out, lse = _run(cache, tables, q, q_start, kv_start, lens, causal=True)
+    out, lse = _run(cache, tables, q, q_start, kv_start, lens, causal=True, split=4)
     cf = cache.float().numpy()
     for r in range(len(nq)):
         qr = q[q_start[r]: q_start[r + 1]].float().numpy()
