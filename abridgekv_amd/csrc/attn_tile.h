@@ -82,12 +82,45 @@ __device__ __forceinline__ u32x4 lds16(const __bf16* buf, int row, int chunk) {
   return *reinterpret_cast<const u32x4*>(buf + row * kHeadDim + 8 * (chunk ^ (row & 15)));
 }
 
+// Eight consecutive output dims (the four of accumulator lo, then the four of hi) times inv, as one 16-byte store.
+__device__ __forceinline__ void store_bf16x8(__bf16* dst, const floatx4& lo, const floatx4& hi, float inv) {
+  u32x4 wv;
+  wv[0] = pack_bf16x2(lo[0] * inv, lo[1] * inv);
+  wv[1] = pack_bf16x2(lo[2] * inv, lo[3] * inv);
+  wv[2] = pack_bf16x2(hi[0] * inv, hi[1] * inv);
+  wv[3] = pack_bf16x2(hi[2] * inv, hi[3] * inv);
+  *reinterpret_cast<u32x4*>(dst) = wv;
+}
+
 struct TileMask {
   int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[head], 3 general (per-element arithmetic)
   int limit[4];
 };
 
-// Attention of this wave's 64 columns against one 64-key tile held in (Kbuf, Vbuf).
+// V^T operand of one PV MFMA from the swizzled V tile with two ds_read_b64_tr_b16 (LDS transpose reads). Within a
+// 16-lane group, lane i of a transpose read receives element i % 4 of the 8-byte chunk addressed by lane
+// 4e + i / 4, for e = 0..3. The operand row m of dim slab t is dim 32 * (m / 4) + 4t + m % 4 and its k-index
+// 8g + e (g = lane group) is key kb + 4g + e for e < 4 and kb + 16 + 4g + e - 4 for e >= 4 (the contraction order the
+// P^T operand uses); so lane 4e + c of the group addresses row kb + 4g + e (then + 16), dims 32c + 4t .. +3.
+__device__ __forceinline__ bf16x8 vt_operand(const __bf16* Vbuf, int kb, int t, int lane) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const int g = lane >> 4, i = lane & 15;
+  const int e = i >> 2, c = i & 3;
+  const int dim = 32 * c + 4 * t;                   // 8-byte aligned, inside 16-byte chunk dim / 8
+  const int row0 = kb + 4 * g + e, row1 = row0 + 16;
+  const __bf16* p0 = Vbuf + row0 * kHeadDim + 8 * ((dim >> 3) ^ (row0 & 15)) + (dim & 7);
+  const __bf16* p1 = Vbuf + row1 * kHeadDim + 8 * ((dim >> 3) ^ (row1 & 15)) + (dim & 7);
+  const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0));
+  const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p1));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  const s8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Attention of this wave's 16H columns against one 64-key tile held in (Kbuf, Vbuf): S^T for all 64 keys first
+// (the MFMA results of the second half are not needed before the softmax of the first starts), one masked online
+// softmax step over the tile, then O^T += V^T . P^T per 32-key half. o[t][u][r] accumulates out dim
+// 32 * (lane >> 4) + 4t + r of column (head hbase + u, query row m16).
 template <int H, bool kAligned>
 __device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* Vbuf, const bf16x8 (&qop)[H][4],
                                              floatx4 (&o)[8][H], float (&m_run)[H], float (&l_run)[H], int k0,
@@ -97,109 +130,106 @@ __device__ __forceinline__ void tile_compute(const __bf16* Kbuf, const __bf16* V
   int lim[H];
 #pragma unroll
   for (int u = 0; u < H; ++u) lim[u] = tm.mode == 1 ? lane_limit : tm.limit[hbase + u];
+  // S^T = K . Q^T: s[kk][t][u][r] = raw score of key k0 + 32kk + 16t + 4j + r, column (head u, query row m16)
+  floatx4 s[2][2][H];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    // S^T = K . Q^T for 32 keys: s[t][u][r] = raw score of key k0 + 32kk + 16t + 4j + r, column (head u, qrow)
-    floatx4 s[2][H];
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int u = 0; u < H; ++u) s[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < H; ++u) s[kk][t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const bf16x8 kop = __builtin_bit_cast(bf16x8, lds16(Kbuf, 32 * kk + 16 * t + m16, 4 * i + j));
 #pragma unroll
-        for (int u = 0; u < H; ++u) s[t][u] = mfma16x16x32(kop, qop[u][i], s[t][u]);
+        for (int u = 0; u < H; ++u) s[kk][t][u] = mfma16x16x32(kop, qop[u][i], s[kk][t][u]);
       }
-    if (tm.mode != 0) {
-      const int kb = k0 + 32 * kk + 4 * j;
+  if (tm.mode != 0) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int u = 0; u < H; ++u)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int kv = kb + 16 * t + r;
+            const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
             bool ok;
             if constexpr (kAligned) {
               ok = kv < lim[u];
             } else {
               ok = geo.visible(kv, hbase + u);
             }
-            s[t][u][r] = ok ? s[t][u][r] : -INFINITY;
+            s[kk][t][u][r] = ok ? s[kk][t][u][r] : -INFINITY;
           }
-    }
-    float tmax[H];
+  }
+  float tmax[H];
+#pragma unroll
+  for (int u = 0; u < H; ++u) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        mx = fmaxf(mx, fmaxf(fmaxf(s[kk][t][u][0], s[kk][t][u][1]), fmaxf(s[kk][t][u][2], s[kk][t][u][3])));
+    mx = max_xor16(mx);
+    mx = max_xor32(mx);
+    tmax[u] = mx * scale_log2;                          // log2-domain max (scale > 0)
+  }
+  // lazy rescale: the running max moves only when a column max grows by more than 8 (2^8 headroom in P)
+  bool need = false;
+#pragma unroll
+  for (int u = 0; u < H; ++u) need |= tmax[u] > m_run[u] + 8.f;
+  if (__any(need)) {
 #pragma unroll
     for (int u = 0; u < H; ++u) {
-      float mx = fmaxf(fmaxf(fmaxf(s[0][u][0], s[0][u][1]), fmaxf(s[0][u][2], s[0][u][3])),
-                       fmaxf(fmaxf(s[1][u][0], s[1][u][1]), fmaxf(s[1][u][2], s[1][u][3])));
-      mx = max_xor16(mx);
-      mx = max_xor32(mx);
-      tmax[u] = mx * scale_log2;                          // log2-domain max (scale > 0)
+      const float m_new = fmaxf(m_run[u], tmax[u]);
+      const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+      m_run[u] = m_new;
+      l_run[u] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
     }
-    // lazy rescale: the running max moves only when a column max grows by more than 8 (2^8 headroom in P)
-    bool need = false;
+  }
+  bf16x8 pop[2][H];
 #pragma unroll
-    for (int u = 0; u < H; ++u) need |= tmax[u] > m_run[u] + 8.f;
-    if (__any(need)) {
+  for (int u = 0; u < H; ++u) {
+    const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
+    float ps = 0.f;
 #pragma unroll
-      for (int u = 0; u < H; ++u) {
-        const float m_new = fmaxf(m_run[u], tmax[u]);
-        const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
-        m_run[u] = m_new;
-        l_run[u] *= alpha;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
-      }
-    }
-    bf16x8 pop[H];
-#pragma unroll
-    for (int u = 0; u < H; ++u) {
-      const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
-      float ps = 0.f;
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = fast_exp2(fmaf(s[t][u][r], scale_log2, neg_m));
-          s[t][u][r] = p;
+          const float p = fast_exp2(fmaf(s[kk][t][u][r], scale_log2, neg_m));
+          s[kk][t][u][r] = p;
           ps += p;
         }
-      l_run[u] += ps;
+      // P^T operand of half kk: k-index e < 4 -> key 32kk + 4j + e, e >= 4 -> key 32kk + 16 + 4j + e - 4
       u32x4 pw;
-      pw[0] = pack_bf16x2(s[0][u][0], s[0][u][1]);
-      pw[1] = pack_bf16x2(s[0][u][2], s[0][u][3]);
-      pw[2] = pack_bf16x2(s[1][u][0], s[1][u][1]);
-      pw[3] = pack_bf16x2(s[1][u][2], s[1][u][3]);
-      pop[u] = __builtin_bit_cast(bf16x8, pw);
+      pw[0] = pack_bf16x2(s[kk][0][u][0], s[kk][0][u][1]);
+      pw[1] = pack_bf16x2(s[kk][0][u][2], s[kk][0][u][3]);
+      pw[2] = pack_bf16x2(s[kk][1][u][0], s[kk][1][u][1]);
+      pw[3] = pack_bf16x2(s[kk][1][u][2], s[kk][1][u][3]);
+      pop[kk][u] = __builtin_bit_cast(bf16x8, pw);
     }
-    // O^T += V^T . P^T over the same 32 keys (P^T row e: e<4 -> key 32kk+4j+e, e>=4 -> key 32kk+16+4j+e-4)
-    u32x4 vr[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      vr[e] = lds16(Vbuf, 32 * kk + 4 * j + e, m16);
-      vr[4 + e] = lds16(Vbuf, 32 * kk + 16 + 4 * j + e, m16);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 lo, hi;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x05040100u);
-        hi[e] = __builtin_amdgcn_perm(vr[2 * e + 1][c], vr[2 * e][c], 0x07060302u);
-      }
-      const bf16x8 lo8 = __builtin_bit_cast(bf16x8, lo), hi8 = __builtin_bit_cast(bf16x8, hi);
-#pragma unroll
-      for (int u = 0; u < H; ++u) {
-        o[2 * c][u] = mfma16x16x32(lo8, pop[u], o[2 * c][u]);
-        o[2 * c + 1][u] = mfma16x16x32(hi8, pop[u], o[2 * c + 1][u]);
-      }
-    }
+    l_run[u] += ps;
   }
+  // O^T += V^T . P^T, one 32-key half at a time, V^T straight from LDS with transpose reads
+  const int lane = 16 * j + m16;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const bf16x8 vop = vt_operand(Vbuf, 32 * kk, t, lane);
+#pragma unroll
+      for (int u = 0; u < H; ++u) o[t][u] = mfma16x16x32(vop, pop[kk][u], o[t][u]);
+    }
 }
-
 
 }  // namespace abkv

@@ -122,10 +122,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
       const long row = ((long)blockIdx.z * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
       float* po = a.part_o + row * kHeadDim + 32 * j;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        *reinterpret_cast<floatx4*>(po + 8 * rr) = floatx4{o[0][u][rr], o[1][u][rr], o[2][u][rr], o[3][u][rr]};
-        *reinterpret_cast<floatx4*>(po + 8 * rr + 4) = floatx4{o[4][u][rr], o[5][u][rr], o[6][u][rr], o[7][u][rr]};
-      }
+      for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * t) = o[t][u];
       if (j == 0) {
         a.part_ml[row * 2] = m_run[u];
         a.part_ml[row * 2 + 1] = l;
@@ -140,12 +137,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)(t0 + qi) * a.o_st + (long)head * a.o_sh + 32 * j;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      u32x4 wv;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) wv[c] = pack_bf16x2(o[2 * c][u][rr] * inv, o[2 * c + 1][u][rr] * inv);
-      *reinterpret_cast<u32x4*>(oh + 8 * rr) = wv;
-    }
+    for (int p = 0; p < 4; ++p) store_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], inv);
     if (a.lse != nullptr && j == 0)
       a.lse[(long)(t0 + qi) * kHeadsQ + head] = l > 0.f ? (m_run[u] + __log2f(l)) * 0.69314718055994531f : -INFINITY;
   }

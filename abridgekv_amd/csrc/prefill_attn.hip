@@ -187,7 +187,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   }
 
   if (qrow >= a.S0) return;
-  // o[i][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 8r + i]
+  // o[t][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 4t + r]
 #pragma unroll
   for (int u = 0; u < H; ++u) {
     const float l = sum_xor32(sum_xor16(l_run[u]));
@@ -195,12 +195,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)qrow * a.o_ss + (long)head * a.o_sh + 32 * j;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      u32x4 wv;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) wv[c] = pack_bf16x2(o[2 * c][u][r] * inv, o[2 * c + 1][u][r] * inv);
-      *reinterpret_cast<u32x4*>(oh + 8 * r) = wv;
-    }
+    for (int p = 0; p < 4; ++p) store_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], inv);
     if (a.lse != nullptr && j == 0)
       a.lse[((long)b * kHeadsQ + head) * a.S0 + qrow] =
           l > 0.f ? (m_run[u] + __log2f(l)) * 0.69314718055994531f : -INFINITY;
