@@ -9,15 +9,15 @@
 //
 // Work decomposition: one workgroup of 8 waves per (sequence, KV head, 64-row query tile). A wave owns 16 query rows
 // for 2 of the 4 query heads of the KV head: 32 MFMA columns (column = head u x row), so one K operand feeds 2 heads
-// and the wave fits in 216 VGPRs (2 waves per SIMD). Key tiles of 64 are DMA'd into double-buffered, XOR-swizzled LDS one visible tile ahead
-// (global_load_lds_dwordx4: no VGPR staging), so loads overlap the previous tile's MFMA work.
-// Each LDS tile is consumed in two halves of 32 keys (keeps the score accumulators at 32 VGPRs):
-//   S^T[32 keys x 64 cols]   = K . Q^T            2 key sub-tiles x 4 heads x 4 dim steps, MFMA 16x16x32 bf16
-//   online softmax (exp2 domain, lazy rescale: the running max moves only when a column max exceeds it by > 8)
-//   O^T[128 dims x 64 cols] += V^T . P^T          8 dim tiles x 4 heads; V^T by v_perm transposes in registers
-// Tiles are classified per workgroup from the mask arithmetic when C and K are multiples of 64: empty tiles are
-// skipped without loading, full tiles run unmasked, partial tiles evaluate the mask per element. Unaligned shapes run
-// every tile as partial (correct, slower).
+// and the wave fits in 2 waves per SIMD. Key tiles of 64 are DMA'd into double-buffered, XOR-swizzled LDS one visible
+// tile ahead (global_load_lds_dwordx4: no VGPR staging), so loads overlap the previous tile's MFMA work. Per tile:
+//   S^T[64 keys x 32 cols]   = K . Q^T            4 key sub-tiles x 2 heads x 4 dim steps, MFMA 16x16x32 bf16
+//   online softmax over the 64 keys (exp2 domain, lazy rescale: the running max moves only when a column max exceeds
+//   it by > 8)
+//   O^T[128 dims x 32 cols] += V^T . P^T          2 key halves x 8 dim tiles x 2 heads; V^T by LDS transpose reads
+// Aligned layouts (C and K multiples of 64) walk only the visible tiles, jumping over hidden segments, and tag each
+// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit). Unaligned shapes run every tile of
+// the visible prefix with the mask evaluated per element (correct, slower).
 #include "attn_tile.h"
 
 namespace abkv {
@@ -36,66 +36,77 @@ struct PrefillArgs {
   int num_q_tiles;
 };
 
-// Tile class for an aligned layout: 0 empty, 1 full, 2 partial.
-__device__ __forceinline__ int classify(int q0, int k0, int C, int per, int plen, int qmin, int qmax) {
-  const int qb = q0 / per, kb = k0 / per;
-  const int qw0 = q0 - qb * per, kw0 = k0 - kb * per;
-  const bool q_code = qw0 >= C;
-  if (kw0 < C) {                                            // content keys
-    if (kb == qb) {
-      if (q_code) return 1;
-      if (k0 + kBN - 1 <= q0) return 1;
-      if (k0 > q0 + kBM - 1) return 0;
-      return 2;
-    }
-    if (kb < qb) {
-      const int a0 = kb * C + kw0;
-      if (a0 + kBN <= plen) return 1;
-      if (a0 >= plen) return 0;
-      return 2;
-    }
-    return 0;
-  }
-  const bool structural = kb < qb || (kb == qb && q_code);  // code keys
-  if (!structural) return 0;
-  const int slot0 = kw0 - C;
-  if (slot0 + kBN <= qmin) return 1;
-  if (slot0 >= qmax) return 0;
-  return 2;
-}
+// Walk over the key tiles one query tile attends to, with the mask mode of each.
+// Aligned layouts (C and K multiples of 64): a key tile is named by (block kb, tile tw of the block's C + K rows).
+// Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
+// ends the segment and the walk jumps to the next one: no per-tile test of skipped tiles and no integer division.
+// Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
+struct TileWalk {
+  int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
+  bool q_code;
+  int kb, tw;
 
-// Class of key tile kt for this query tile: 0 skip, otherwise fills the mask mode.
-__device__ __forceinline__ int tile_class(const PrefillArgs& a, int kt, int q0, int q_last, int per, int plen,
-                                          int qmin, int qmax, const int (&quota)[4], TileMask& tm) {
-  const int k0 = kt * kBN;
-  if (!a.aligned) {
-    const int qb_hi = q_last / per;
-    tm.mode = 3;
-    return (k0 <= q_last || k0 / per <= qb_hi) ? 1 : 0;
+  __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_)
+      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0) {
+    qb = q0 / per;
+    q_code = q0 - qb * per >= C;
+    tpb = per / kBN;
+    ct = C / kBN;
+    n_tiles = (S0 + kBN - 1) / kBN;
   }
-  const int cls = classify(q0, k0, a.C, per, plen, qmin, qmax);
-  if (cls != 2) {
-    tm.mode = 0;
-    return cls;
-  }
-  const int kb = k0 / per, kw0 = k0 - kb * per;
-  const int qb = q0 / per;
-  if (kw0 < a.C) {
-    if (kb == qb) {
-      tm.mode = 1;                                          // diagonal tile of the block's content
-    } else {
-      tm.mode = 2;                                          // raw-prompt boundary inside the tile
-      const int lim = kb * per + (plen - kb * a.C);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) tm.limit[u] = lim;
+
+  // aligned: move (kb, tw) to the first visible tile at or after it; false when none is left
+  __device__ __forceinline__ bool seek() {
+    for (;;) {
+      if (kb > qb) return false;
+      if (tw < ct) {
+        const bool vis = kb == qb ? (q_code || kb * per + kBN * tw <= q_last) : (kb * C + kBN * tw < plen);
+        if (vis) return true;
+        tw = ct;                                            // the rest of this block's content is hidden too
+      }
+      if ((kb < qb || q_code) && tw < tpb && kBN * (tw - ct) < qmax) return true;
+      if (kb == qb) return false;                           // blocks after the query's own block are hidden
+      ++kb;
+      tw = 0;
     }
-  } else {
-    tm.mode = 2;                                            // quota boundary inside a code tile
-#pragma unroll
-    for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + a.C + quota[u];
   }
-  return 1;
-}
+
+  // aligned: mask mode of the visible tile (kb, tw)
+  __device__ __forceinline__ void mask(TileMask& tm, const int (&quota)[4]) const {
+    const int k0 = kb * per + kBN * tw;
+    tm.mode = 0;
+    if (tw < ct) {
+      if (kb == qb) {
+        if (!q_code && k0 + kBN - 1 > q0) tm.mode = 1;      // diagonal tile of the block's content
+      } else if (kb * C + kBN * tw + kBN > plen) {
+        tm.mode = 2;                                        // raw-prompt boundary inside the tile
+#pragma unroll
+        for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + (plen - kb * C);
+      }
+    } else if (kBN * (tw - ct) + kBN > qmin) {
+      tm.mode = 2;                                          // quota boundary inside a code tile
+#pragma unroll
+      for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + C + quota[u];
+    }
+  }
+
+  // next tile to attend (the first call gives the first); false when the walk is done
+  template <bool kAligned>
+  __device__ __forceinline__ bool next(int& kt, TileMask& tm, const int (&quota)[4], bool first) {
+    if constexpr (kAligned) {
+      if (!first) ++tw;
+      if (!seek()) return false;
+      kt = kb * tpb + tw;
+      mask(tm, quota);
+      return true;
+    } else {
+      kt = first ? 0 : kt + 1;
+      tm.mode = 3;
+      // keys up to the query tile's last row, or in a block up to its own (codes of the own block): a prefix
+      return kt < n_tiles && (kt * kBN <= q_last || (kt * kBN) / per <= q_last / per);
+    }
+  }
+};
 
 template <int H, bool kAligned>
 __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(PrefillArgs a) {
@@ -154,22 +165,22 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const DenseRows rows{a.k + (long)b * a.k_sb + (long)kvh * a.k_sh, a.v + (long)b * a.v_sb + (long)kvh * a.v_sh,
                        a.k_ss, a.v_ss};
   const MaskGeom geo{qrow, a.S0, a.C, per, plen, quota_all};
-  const int n_k_tiles = (a.S0 + kBN - 1) / kBN;
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
   // double-buffered walk over the visible key tiles
+  TileWalk walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax);
   TileMask tm_cur, tm_nxt;
-  int cur = 0;
-  while (cur < n_k_tiles && !tile_class(a, cur, q0, q_last, per, plen, qmin, qmax, quota_all, tm_cur)) ++cur;
-  if (cur < n_k_tiles) issue_tile<kWaves>(rows, cur * kBN, a.S0, Kb, Vb, w, lane);
+  int cur = 0, nxt = 0;
+  bool have = walk.next<kAligned>(cur, tm_cur, quota_all, true);
+  if (have) issue_tile<kWaves>(rows, cur * kBN, a.S0, Kb, Vb, w, lane);
   int parity = 0;
-  while (cur < n_k_tiles) {
-    int nxt = cur + 1;
-    while (nxt < n_k_tiles && !tile_class(a, nxt, q0, q_last, per, plen, qmin, qmax, quota_all, tm_nxt)) ++nxt;
+  while (have) {
+    nxt = cur;
+    const bool more = walk.next<kAligned>(nxt, tm_nxt, quota_all, false);
     const int off_cur = parity * kTileElems, off_nxt = (parity ^ 1) * kTileElems;
     // Plain s_barrier (no workgroup fence): a fence would wait for the prefetch just issued. Each wave waits for
     // its own DMA of the current tile (vmcnt), the barrier then publishes every wave's part.
-    if (nxt < n_k_tiles) {
+    if (more) {
       issue_tile<kWaves>(rows, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
       if constexpr (kWaves == 4) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
       else __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -181,6 +192,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
                               a.scale_log2, geo, hbase, m16, j);
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are complete
     __builtin_amdgcn_s_barrier();                           // the buffer just read is refilled next iteration
+    have = more;
     cur = nxt;
     tm_cur = tm_nxt;
     parity ^= 1;
