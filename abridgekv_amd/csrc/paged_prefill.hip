@@ -33,6 +33,16 @@ struct PagedPrefillArgs {
   float* part_ml;                              // [splits, T, 32, 2] (running max in log2 units, sum)
 };
 
+// Contiguous key tiles [kt_begin, kt_end); tiles past k_full (the smallest lane limit) are masked per lane.
+struct RangeWalk {
+  int kt_begin, kt_end, k_full;
+  __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
+    kt = first ? kt_begin : kt + 1;
+    tm.mode = (kt + 1) * kBN <= k_full ? 0 : 1;
+    return kt < kt_end;
+  }
+};
+
 __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs a) {
   constexpr int H = 2, kWaves = 8;
   __shared__ __attribute__((aligned(16))) __bf16 Kb[2 * kTileElems];
@@ -42,7 +52,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const int q0 = a.tile_q0[blockIdx.x];
   const int kvh = blockIdx.y;
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int lane = tid & 63;
   const int m16 = lane & 15;
   const int j = lane >> 4;
@@ -89,35 +99,19 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const int n_k_tiles = (k_end + kBN - 1) / kBN;
   const PagedRows rows{a.kv + kvh * kHeadDim, a.block_table + (long)r * a.bt_stride, a.bt_width, a.num_pages};
   const MaskGeom geo{};
-  TileMask tm;
-  tm.mode = 0;
-
   // key tiles of this block: all of them, or split z's share when the launch is split along the keys
-  const int kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
-  const int kt_end = a.split_tiles > 0 ? min(n_k_tiles, kt_begin + a.split_tiles) : n_k_tiles;
-  if (kt_begin < kt_end) issue_tile<kWaves>(rows, kt_begin * kBN, k_end, Kb, Vb, w, lane);
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int par = (kt - kt_begin) & 1;
-    const int off_cur = par * kTileElems, off_nxt = (par ^ 1) * kTileElems;
-    if (kt + 1 < kt_end) {
-      issue_tile<kWaves>(rows, (kt + 1) * kBN, k_end, Kb + off_nxt, Vb + off_nxt, w, lane);
-      __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __builtin_amdgcn_s_barrier();
-    tm.mode = (kt + 1) * kBN <= k_full ? 0 : 1;
-    tile_compute<H, true>(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, kt * kBN, tm, lane_limit, a.scale_log2,
-                          geo, hbase, m16, j);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-  }
+  RangeWalk walk;
+  walk.kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
+  walk.kt_end = a.split_tiles > 0 ? min(n_k_tiles, walk.kt_begin + a.split_tiles) : n_k_tiles;
+  walk.k_full = k_full;
+  attend_tiles<H, true, kWaves>(rows, walk, k_end, Kb, Vb, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo, hbase,
+                                w, lane);
 
   if (!qvalid) return;
   if (a.split_tiles > 0) {                                   // partials of this key split
 #pragma unroll
     for (int u = 0; u < H; ++u) {
-      const float l = sum_xor32(sum_xor16(l_run[u]));
+      const float l = l_run[u];
       const int head = kvh * kGroup + hbase + u;
       const long row = ((long)blockIdx.z * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
       float* po = a.part_o + row * kHeadDim + 32 * j;
@@ -132,7 +126,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   }
 #pragma unroll
   for (int u = 0; u < H; ++u) {
-    const float l = sum_xor32(sum_xor16(l_run[u]));
+    const float l = l_run[u];
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)(t0 + qi) * a.o_st + (long)head * a.o_sh + 32 * j;

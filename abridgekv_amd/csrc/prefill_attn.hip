@@ -41,13 +41,17 @@ struct PrefillArgs {
 // Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
 // ends the segment and the walk jumps to the next one: no per-tile test of skipped tiles and no integer division.
 // Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
+template <bool kAligned>
 struct TileWalk {
   int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
   bool q_code;
   int kb, tw;
+  const int (&quota)[4];
 
-  __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_)
-      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0) {
+  __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_,
+                                      const int (&quota_)[4])
+      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0),
+        quota(quota_) {
     qb = q0 / per;
     q_code = q0 - qb * per >= C;
     tpb = per / kBN;
@@ -72,7 +76,7 @@ struct TileWalk {
   }
 
   // aligned: mask mode of the visible tile (kb, tw)
-  __device__ __forceinline__ void mask(TileMask& tm, const int (&quota)[4]) const {
+  __device__ __forceinline__ void mask(TileMask& tm) const {
     const int k0 = kb * per + kBN * tw;
     tm.mode = 0;
     if (tw < ct) {
@@ -91,13 +95,12 @@ struct TileWalk {
   }
 
   // next tile to attend (the first call gives the first); false when the walk is done
-  template <bool kAligned>
-  __device__ __forceinline__ bool next(int& kt, TileMask& tm, const int (&quota)[4], bool first) {
+  __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
     if constexpr (kAligned) {
       if (!first) ++tw;
       if (!seek()) return false;
       kt = kb * tpb + tw;
-      mask(tm, quota);
+      mask(tm);
       return true;
     } else {
       kt = first ? 0 : kt + 1;
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int lane = tid & 63;
   const int m16 = lane & 15;
   const int j = lane >> 4;
@@ -167,42 +170,15 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const MaskGeom geo{qrow, a.S0, a.C, per, plen, quota_all};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
-  // double-buffered walk over the visible key tiles
-  TileWalk walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax);
-  TileMask tm_cur, tm_nxt;
-  int cur = 0, nxt = 0;
-  bool have = walk.next<kAligned>(cur, tm_cur, quota_all, true);
-  if (have) issue_tile<kWaves>(rows, cur * kBN, a.S0, Kb, Vb, w, lane);
-  int parity = 0;
-  while (have) {
-    nxt = cur;
-    const bool more = walk.next<kAligned>(nxt, tm_nxt, quota_all, false);
-    const int off_cur = parity * kTileElems, off_nxt = (parity ^ 1) * kTileElems;
-    // Plain s_barrier (no workgroup fence): a fence would wait for the prefetch just issued. Each wave waits for
-    // its own DMA of the current tile (vmcnt), the barrier then publishes every wave's part.
-    if (more) {
-      issue_tile<kWaves>(rows, nxt * kBN, a.S0, Kb + off_nxt, Vb + off_nxt, w, lane);
-      if constexpr (kWaves == 4) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __builtin_amdgcn_s_barrier();
-    tile_compute<H, kAligned>(Kb + off_cur, Vb + off_cur, qop, o, m_run, l_run, cur * kBN, tm_cur, qrow + 1,
-                              a.scale_log2, geo, hbase, m16, j);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are complete
-    __builtin_amdgcn_s_barrier();                           // the buffer just read is refilled next iteration
-    have = more;
-    cur = nxt;
-    tm_cur = tm_nxt;
-    parity ^= 1;
-  }
+  TileWalk<kAligned> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, quota_all);
+  attend_tiles<H, kAligned, kWaves>(rows, walk, a.S0, Kb, Vb, qop, o, m_run, l_run, qrow + 1, a.scale_log2, geo, hbase,
+                                    w, lane);
 
   if (qrow >= a.S0) return;
   // o[t][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 4t + r]
 #pragma unroll
   for (int u = 0; u < H; ++u) {
-    const float l = sum_xor32(sum_xor16(l_run[u]));
+    const float l = l_run[u];
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)qrow * a.o_ss + (long)head * a.o_sh + 32 * j;
