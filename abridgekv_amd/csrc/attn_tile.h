@@ -13,11 +13,11 @@ constexpr int kBN = 64;                  // keys per tile
 constexpr int kTileElems = kBN * kHeadDim;
 
 // Per-element visibility for layouts whose tiles cannot be classified (unaligned masked prefill); other kernels
-// never call it (their tiles are always aligned: kAligned = true).
+// never call it (their tiles are always aligned: kAligned = true). quota[u]: code slots visible to this wave's head u.
 struct MaskGeom {
   int qrow, S0, C, per, plen;
-  const int* quota;        // per head of the KV group
-  __device__ __forceinline__ bool visible(int kv, int head) const {
+  int quota[2];
+  __device__ __forceinline__ bool visible(int kv, int u) const {
     if (kv >= S0 || qrow >= S0) return false;
     const int qb = qrow / per, kb = kv / per;
     const int qw = qrow - qb * per, kw = kv - kb * per;
@@ -25,7 +25,7 @@ struct MaskGeom {
     bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen);
     v = v && kv <= qrow;
     v = v || (qw >= C && !kc && kb == qb);
-    return v && (kc || kw - C < quota[head]);
+    return v && (kc || kw - C < quota[u]);
   }
 };
 
@@ -38,76 +38,75 @@ __device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_ca
 // global_load_lds_dwordx4: a wave instruction writes 1 KiB contiguously (lane L -> bytes 16L), so each lane fetches
 // the global chunk that belongs at its swizzled position. Rows past the sequence end re-read the last row (finite data,
 // masked to probability 0).
-// Tile row sources for the DMA. tile_base<kV>(k0, blk) is the (wave-uniform) address that DMA block blk (rows
-// 4blk .. 4blk+3 of the tile at key k0) starts from and lane_off(row, chunk) the per-lane element offset from it, so
-// a full tile costs no per-tile vector address arithmetic. Rows at or past n_keys are never read (they may lie past
-// the tensor, or hold non-finite data that a zero weight would not cancel in P.V): the last tile of a walk takes the
-// per-row path, which re-reads row n_keys - 1 in their place (finite data, masked to zero weight).
+// Tile row sources for the DMA. src(k0, w) gathers, before the barrier that precedes the issue, the wave-uniform
+// facts one wave's DMA of the 64-key tile at k0 needs (its rows 4 * kPerWave * w .. +4 * kPerWave - 1 lie in one
+// page); addr<kV>(src, row, chunk, n_keys) is the per-lane source of LDS row `row`, chunk `chunk`. Rows at or past
+// n_keys are never read (they may lie past the tensor, or hold non-finite data that a zero weight would not cancel
+// in P.V): row n_keys - 1 is re-read in their place (finite data, masked to zero weight).
 // Contiguous [S, heads, 128] K/V pair (one KV head selected by the base pointers).
 struct DenseRows {
   const __bf16* k;
   const __bf16* v;
   long k_ss, v_ss;
+  struct Src {
+    int k0;
+  };
+  template <int kPerWave>
+  __device__ __forceinline__ Src src(int k0, int, int) const { return Src{k0}; }
   template <bool kV>
-  __device__ __forceinline__ const __bf16* tile_base(int k0, int) const {
-    return kV ? v + (long)k0 * v_ss : k + (long)k0 * k_ss;
-  }
-  template <bool kV>
-  __device__ __forceinline__ int lane_off(int row, int chunk) const {
-    return row * (int)(kV ? v_ss : k_ss) + 8 * chunk;
-  }
-  template <bool kV>
-  __device__ __forceinline__ const __bf16* row_ptr(int key) const {
-    return kV ? v + (long)key * v_ss : k + (long)key * k_ss;
+  __device__ __forceinline__ const __bf16* addr(const Src& t, int row, int chunk, int n_keys) const {
+    const __bf16* base = kV ? v : k;
+    const long ss = kV ? v_ss : k_ss;
+    if (t.k0 + kBN <= n_keys)                                   // uniform: a full tile
+      return base + (long)t.k0 * ss + (row * (int)ss + 8 * chunk);
+    return base + (long)min(t.k0 + row, n_keys - 1) * ss + 8 * chunk;
   }
 };
 
-// One sequence in the paged cache [pages, 2, 16, 8, 128] (one KV head): a DMA block's 4 rows lie in one page, whose
-// id is a wave-uniform load; page-table positions past the row and page ids out of range are clamped.
+// One sequence in the paged cache [pages, 2, 16, 8, 128] (one KV head). The page ids are scalar loads through the
+// constant address space (the table is not written while a kernel runs); table positions past the row and page ids
+// out of range are clamped.
 struct PagedRows {
   const __bf16* kv;        // cache base + kvh * 128
   const int32_t* table;    // the sequence's page-table row
   int width;               // entries in the row
   int num_pages;
-  template <bool kV>
-  __device__ __forceinline__ const __bf16* tile_base(int k0, int blk) const {
-    const int page = min(max(table[min((k0 >> 4) + (blk >> 2), width - 1)], 0), num_pages - 1);
-    return kv + (long)page * kPageElems + (kV ? kHalfElems : 0);
+  struct Src {
+    int k0, page, page_last;                                    // page of the wave's rows, page of row n_keys - 1
+  };
+  __device__ __forceinline__ int page_of(int idx) const {
+    const __attribute__((address_space(4))) int32_t* t = (const __attribute__((address_space(4))) int32_t*)table;
+    return min(max(t[min(max(idx, 0), width - 1)], 0), num_pages - 1);
+  }
+  template <int kPerWave>
+  __device__ __forceinline__ Src src(int k0, int w, int n_keys) const {
+    return Src{k0, page_of((k0 >> 4) + (4 * kPerWave * w >> 4)), page_of((n_keys - 1) >> 4)};
   }
   template <bool kV>
-  __device__ __forceinline__ int lane_off(int row, int chunk) const {
-    return (row & 15) * kSlotElems + 8 * chunk;
-  }
-  template <bool kV>
-  __device__ __forceinline__ const __bf16* row_ptr(int key) const {
-    return tile_base<kV>(key & ~15, 0) + (key & 15) * kSlotElems;
+  __device__ __forceinline__ const __bf16* addr(const Src& t, int row, int chunk, int n_keys) const {
+    const __bf16* base = kv + (kV ? kHalfElems : 0);
+    if (t.k0 + kBN <= n_keys)                                   // uniform: a full tile
+      return base + (long)t.page * kPageElems + ((row & 15) * kSlotElems + 8 * chunk);
+    const bool in = t.k0 + row < n_keys;
+    const int page = in ? t.page : t.page_last;
+    const int slot = in ? (row & 15) : ((n_keys - 1) & 15);
+    return base + (long)page * kPageElems + (slot * kSlotElems + 8 * chunk);
   }
 };
 
-// Fill the K (kV = false) or V (kV = true) tile of 64 keys at k0. Each wave issues 16 / kWaves DMA instructions (one
-// 1 KiB block of the 16 KiB tile each); w must be wave-uniform.
+// Fill the K (kV = false) or V (kV = true) tile described by src. Each wave issues 16 / kWaves DMA instructions (one
+// 1 KiB block = 4 rows of the 16 KiB tile each); w must be wave-uniform.
 template <int kWaves, bool kV, class Rows>
-__device__ __forceinline__ void issue_half(const Rows& rows, int k0, int n_keys, __bf16* buf, int w, int lane) {
+__device__ __forceinline__ void issue_half(const Rows& rows, const typename Rows::Src& src, int n_keys, __bf16* buf,
+                                           int w, int lane) {
   constexpr int kPerWave = 16 / kWaves;
-  if (k0 + kBN <= n_keys) {
 #pragma unroll
-    for (int n = 0; n < kPerWave; ++n) {
-      const int blk = kPerWave * w + n;
-      const int row = 4 * blk + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
-      const char* base = reinterpret_cast<const char*>(rows.template tile_base<kV>(k0, blk));
-      const unsigned off = 2u * (unsigned)rows.template lane_off<kV>(row, chunk);
-      __builtin_amdgcn_global_load_lds((const void*)(base + off), ABKV_LDS(buf + 512 * blk), 16, 0, 0);
-    }
-  } else {
-#pragma unroll
-    for (int n = 0; n < kPerWave; ++n) {
-      const int blk = kPerWave * w + n;
-      const int row = 4 * blk + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
-      const __bf16* src = rows.template row_ptr<kV>(min(k0 + row, n_keys - 1)) + 8 * chunk;
-      __builtin_amdgcn_global_load_lds((const void*)src, ABKV_LDS(buf + 512 * blk), 16, 0, 0);
-    }
+  for (int n = 0; n < kPerWave; ++n) {
+    const int blk = kPerWave * w + n;
+    const int row = 4 * blk + (lane >> 4);
+    const int chunk = (lane & 15) ^ (row & 15);
+    const __bf16* p = rows.template addr<kV>(src, row, chunk, n_keys);
+    __builtin_amdgcn_global_load_lds((const void*)p, ABKV_LDS(buf + 512 * blk), 16, 0, 0);
   }
 }
 
@@ -126,8 +125,8 @@ __device__ __forceinline__ void store_bf16x8(__bf16* dst, const floatx4& lo, con
 }
 
 struct TileMask {
-  int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[head], 3 general (per-element arithmetic)
-  int limit[4];
+  int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[u] (this wave's head u), 3 per-element mask
+  int limit[2];
 };
 
 // V^T operand of one PV MFMA from the swizzled V tile with two ds_read_b64_tr_b16 (LDS transpose reads). Within a
@@ -176,12 +175,13 @@ __device__ __forceinline__ void tile_scores(const __bf16* Kbuf, const bf16x8 (&q
 // Hidden keys of a partial tile get score -inf (tm.mode 0: nothing hidden).
 template <int H, bool kAligned>
 __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const TileMask& tm, int lane_limit,
-                                          const MaskGeom& geo, int hbase, int j) {
+                                          const MaskGeom& geo, int j) {
+  static_assert(H <= 2, "TileMask holds two per-head limits");
   if (tm.mode == 0) return;
   // every partial tile of an aligned layout is "key < lim[u]" with a per-column limit (per head or per lane)
   int lim[H];
 #pragma unroll
-  for (int u = 0; u < H; ++u) lim[u] = tm.mode == 1 ? lane_limit : tm.limit[hbase + u];
+  for (int u = 0; u < H; ++u) lim[u] = tm.mode == 1 ? lane_limit : tm.limit[u];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -195,7 +195,7 @@ __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const T
           if constexpr (kAligned) {
             ok = kv < lim[u];
           } else {
-            ok = geo.visible(kv, hbase + u);
+            ok = geo.visible(kv, u);
           }
           s[kk][t][u][r] = ok ? s[kk][t][u][r] : -INFINITY;
         }
@@ -283,64 +283,97 @@ __device__ __forceinline__ void tile_pv(const __bf16* Vbuf, const bf16x8 (&pop)[
   }
 }
 
-// Software-pipelined walk over a query tile's key tiles. Iteration n (tile n's scores already in s_cur):
-//   wait for this wave's DMA, barrier (publishes K(n+1), V(n); every wave is done reading K(n), V(n-1))
-//   DMA K(n+2) -> K buffer n % 2, V(n+1) -> V buffer (n+1) % 2
-//   mask + rescale of tile n; then the scores of tile n+1 (MFMA) interleaved with the probabilities of tile n (VALU),
-//   then O += V(n) . P(n).
+constexpr int kStages = 3;                 // K and V tile buffers each (LDS: 2 x 3 x 16 KiB)
+
+template <int N>
+struct Slot {
+  static constexpr int value = N;
+};
+
+// Software-pipelined walk over a query tile's key tiles; tile m lives in buffers K[m % 3], V[m % 3], six distinct LDS
+// arrays, so the compiler can tell a pending DMA into one slot from reads of another (a single array with computed
+// slot offsets makes it wait for every DMA in flight before each LDS read). Iteration n (tile n's scores in s_cur):
+//   wait for this wave's DMAs of iteration n-2 (K(n+1), V(n)), barrier (publishes them; every wave is done reading
+//   K(n) and V(n-1))
+//   DMA K(n+3) -> K[n % 3], V(n+2) -> V[(n+2) % 3]: two iterations of latency cover. Both are issued every
+//   iteration (past the last tile they re-load tile n into slots nobody reads again) so that each iteration has the
+//   same count of loads in flight: the waits below and the compiler's own then stay exact.
+//   mask + rescale of tile n; scores of tile n+1 (MFMA) with the probabilities of tile n (VALU); O += V(n) . P(n)
 // Walk::next(kt, tm, first) yields the tiles in order. Rows addresses key rows; keys >= n_keys are never read.
 // On return l_run[u] is the full weight sum of column (u, m16) in every lane of the column (o and m_run as above).
 template <int H, bool kAligned, int kWaves, class Rows, class Walk>
-__device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n_keys, __bf16* Kb, __bf16* Vb,
-                                             const bf16x8 (&qop)[H][4], floatx4 (&o)[8][H], float (&m_run)[H],
-                                             float (&l_run)[H], int lane_limit, float scale_log2,
-                                             const MaskGeom& geo, int hbase, int w, int lane) {
+__device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n_keys, __bf16* const (&K)[kStages],
+                                             __bf16* const (&V)[kStages], const bf16x8 (&qop)[H][4],
+                                             floatx4 (&o)[8][H], float (&m_run)[H], float (&l_run)[H],
+                                             int lane_limit, float scale_log2, const MaskGeom& geo, int w, int lane) {
+  constexpr int kPerWave = 16 / kWaves;
   const int m16 = lane & 15, j = lane >> 4;
-  int t_cur = 0, t_nxt = 0;
-  TileMask tm_cur, tm_nxt;
-  if (!walk.next(t_cur, tm_cur, true)) return;
-  t_nxt = t_cur;
-  bool has_nxt = walk.next(t_nxt, tm_nxt, false);
-  issue_half<kWaves, false>(rows, t_cur * kBN, n_keys, Kb, w, lane);
-  issue_half<kWaves, true>(rows, t_cur * kBN, n_keys, Vb, w, lane);
-  if (has_nxt) issue_half<kWaves, false>(rows, t_nxt * kBN, n_keys, Kb + kTileElems, w, lane);
+  int t0 = 0, t1 = 0, t2 = 0;                      // tiles n, n+1, n+2
+  TileMask m0, m1, m2;
+  if (!walk.next(t0, m0, true)) return;
+  t1 = t0;
+  bool h1 = walk.next(t1, m1, false);
+  t2 = t1;
+  bool h2 = h1 && walk.next(t2, m2, false);
+  {
+    const auto s0 = rows.template src<kPerWave>(t0 * kBN, w, n_keys);
+    issue_half<kWaves, false>(rows, s0, n_keys, K[0], w, lane);
+    issue_half<kWaves, true>(rows, s0, n_keys, V[0], w, lane);
+    if (h1) {
+      const auto s1 = rows.template src<kPerWave>(t1 * kBN, w, n_keys);
+      issue_half<kWaves, false>(rows, s1, n_keys, K[1], w, lane);
+      issue_half<kWaves, true>(rows, s1, n_keys, V[1], w, lane);
+    }
+    if (h2) issue_half<kWaves, false>(rows, rows.template src<kPerWave>(t2 * kBN, w, n_keys), n_keys, K[2], w, lane);
+  }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   floatx4 sa[2][2][H], sb[2][2][H], lsum[H];
 #pragma unroll
   for (int u = 0; u < H; ++u) lsum[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-  tile_scores<H>(Kb, qop, sa, m16, j);
+  tile_scores<H>(K[0], qop, sa, m16, j);
 
-  // one iteration; s_cur holds tile n's scores, s_nxt receives tile n+1's. p = n % 2. Returns false after the last.
-  auto step = [&](floatx4 (&s_cur)[2][2][H], floatx4 (&s_nxt)[2][2][H], int p) -> bool {
-    int t_nn = t_nxt;
-    TileMask tm_nn;
-    const bool has_nn = has_nxt && walk.next(t_nn, tm_nn, false);
-    // Plain s_barrier: each wave first waits for its own DMA (vmcnt) and its LDS reads (lgkmcnt).
-    __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  // one iteration, slot = n % 3; s_cur holds tile n's scores, s_nxt receives tile n+1's. False after the last tile.
+  auto step = [&](floatx4 (&s_cur)[2][2][H], floatx4 (&s_nxt)[2][2][H], auto slot_c) -> bool {
+    constexpr int slot = decltype(slot_c)::value;
+    constexpr int slot1 = (slot + 1) % kStages, slot2 = (slot + 2) % kStages;
+    int t3 = t2;
+    TileMask m3;
+    const bool h3 = h2 && walk.next(t3, m3, false);
+    const auto src_k = rows.template src<kPerWave>((h3 ? t3 : t0) * kBN, w, n_keys);
+    const auto src_v = rows.template src<kPerWave>((h2 ? t2 : t0) * kBN, w, n_keys);
+    // Plain s_barrier: each wave first waits for its own DMAs of two iterations back (vmcnt: the last iteration's
+    // 2 x 16 / kWaves stay in flight) and its LDS and scalar reads (lgkmcnt).
+    if constexpr (kWaves == 8) __asm__ volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (has_nn) issue_half<kWaves, false>(rows, t_nn * kBN, n_keys, Kb + p * kTileElems, w, lane);
-    if (has_nxt) issue_half<kWaves, true>(rows, t_nxt * kBN, n_keys, Vb + (p ^ 1) * kTileElems, w, lane);
-    tile_mask<H, kAligned>(s_cur, t_cur * kBN, tm_cur, lane_limit, geo, hbase, j);
+    issue_half<kWaves, false>(rows, src_k, n_keys, K[slot], w, lane);
+    issue_half<kWaves, true>(rows, src_v, n_keys, V[slot2], w, lane);
+    tile_mask<H, kAligned>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
     tile_rescale<H>(s_cur, o, m_run, lsum, scale_log2);
     bf16x8 pop[2][H];
-    // Branch-free so that both land in one scheduling region: after the last tile the scores are computed from the
-    // current K buffer (valid data) and discarded.
-    tile_scores<H>(Kb + (has_nxt ? p ^ 1 : p) * kTileElems, qop, s_nxt, m16, j);
+    // Unconditional so that both land in one scheduling region: after the last tile the scores are computed from
+    // whatever K[slot1] holds (finite data: a tile or its re-load) and discarded.
+    tile_scores<H>(K[slot1], qop, s_nxt, m16, j);
     tile_probs<H>(s_cur, m_run, scale_log2, pop);
-    tile_pv<H>(Vb + p * kTileElems, pop, o, lsum, lane);
-    if (!has_nxt) return false;
-    t_cur = t_nxt;
-    tm_cur = tm_nxt;
-    t_nxt = t_nn;
-    tm_nxt = tm_nn;
-    has_nxt = has_nn;
+    tile_pv<H>(V[slot], pop, o, lsum, lane);
+    if (!h1) return false;
+    t0 = t1; m0 = m1;
+    t1 = t2; m1 = m2; h1 = h2;
+    t2 = t3; m2 = m3; h2 = h3;
     return true;
   };
   for (;;) {
-    if (!step(sa, sb, 0)) break;
-    if (!step(sb, sa, 1)) break;
+    if (!step(sa, sb, Slot<0>{})) break;
+    if (!step(sb, sa, Slot<1>{})) break;
+    if (!step(sa, sb, Slot<2>{})) break;
+    if (!step(sb, sa, Slot<0>{})) break;
+    if (!step(sa, sb, Slot<1>{})) break;
+    if (!step(sb, sa, Slot<2>{})) break;
   }
+  // the re-loads issued by the last iterations land in LDS that this workgroup no longer reads, but they must finish
+  // before the workgroup ends and its LDS is handed to another
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
   for (int u = 0; u < H; ++u) l_run[u] = lsum[u][0];
 }

@@ -45,9 +45,10 @@ struct RangeWalk {
 
 __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs a) {
   constexpr int H = 2, kWaves = 8;
-  __shared__ __attribute__((aligned(16))) __bf16 Kb[2 * kTileElems];
-  __shared__ __attribute__((aligned(16))) __bf16 Vb[2 * kTileElems];
-
+  __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], K2[kTileElems];
+  __shared__ __attribute__((aligned(16))) __bf16 V0[kTileElems], V1[kTileElems], V2[kTileElems];
+  __bf16* const Kbuf[kStages] = {K0, K1, K2};
+  __bf16* const Vbuf[kStages] = {V0, V1, V2};
   const int r = a.tile_req[blockIdx.x];
   const int q0 = a.tile_q0[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -104,8 +105,8 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   walk.kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
   walk.kt_end = a.split_tiles > 0 ? min(n_k_tiles, walk.kt_begin + a.split_tiles) : n_k_tiles;
   walk.k_full = k_full;
-  attend_tiles<H, true, kWaves>(rows, walk, k_end, Kb, Vb, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo, hbase,
-                                w, lane);
+  attend_tiles<H, true, kWaves>(rows, walk, k_end, Kbuf, Vbuf, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo, w,
+                                lane);
 
   if (!qvalid) return;
   if (a.split_tiles > 0) {                                   // partials of this key split

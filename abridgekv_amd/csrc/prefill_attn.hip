@@ -46,12 +46,12 @@ struct TileWalk {
   int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
   bool q_code;
   int kb, tw;
-  const int (&quota)[4];
+  int wq0, wq1;                                             // code quotas of this wave's two heads
 
   __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_,
-                                      const int (&quota_)[4])
+                                      int wq0_, int wq1_)
       : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0),
-        quota(quota_) {
+        wq0(wq0_), wq1(wq1_) {
     qb = q0 / per;
     q_code = q0 - qb * per >= C;
     tpb = per / kBN;
@@ -84,13 +84,12 @@ struct TileWalk {
         if (!q_code && k0 + kBN - 1 > q0) tm.mode = 1;      // diagonal tile of the block's content
       } else if (kb * C + kBN * tw + kBN > plen) {
         tm.mode = 2;                                        // raw-prompt boundary inside the tile
-#pragma unroll
-        for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + (plen - kb * C);
+        tm.limit[0] = tm.limit[1] = kb * per + (plen - kb * C);
       }
     } else if (kBN * (tw - ct) + kBN > qmin) {
       tm.mode = 2;                                          // quota boundary inside a code tile
-#pragma unroll
-      for (int u = 0; u < 4; ++u) tm.limit[u] = kb * per + C + quota[u];
+      tm.limit[0] = kb * per + C + wq0;
+      tm.limit[1] = kb * per + C + wq1;
     }
   }
 
@@ -114,8 +113,10 @@ struct TileWalk {
 template <int H, bool kAligned>
 __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(PrefillArgs a) {
   constexpr int kWaves = 4 * (4 / H);                       // 16 query rows x H heads per wave
-  __shared__ __attribute__((aligned(16))) __bf16 Kb[2 * kTileElems];
-  __shared__ __attribute__((aligned(16))) __bf16 Vb[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], K2[kTileElems];
+  __shared__ __attribute__((aligned(16))) __bf16 V0[kTileElems], V1[kTileElems], V2[kTileElems];
+  __bf16* const Kbuf[kStages] = {K0, K1, K2};
+  __bf16* const Vbuf[kStages] = {V0, V1, V2};
 
   const int qt = a.num_q_tiles - 1 - blockIdx.x;            // heavier (later) query tiles first
   const int kvh = blockIdx.y;
@@ -167,12 +168,14 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
 
   const DenseRows rows{a.k + (long)b * a.k_sb + (long)kvh * a.k_sh, a.v + (long)b * a.v_sb + (long)kvh * a.v_sh,
                        a.k_ss, a.v_ss};
-  const MaskGeom geo{qrow, a.S0, a.C, per, plen, quota_all};
+  // this wave's heads hbase, hbase + 1 (hbase is 0 or 2): quotas by selection, not by a computed index
+  const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
+  const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
-  TileWalk<kAligned> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, quota_all);
-  attend_tiles<H, kAligned, kWaves>(rows, walk, a.S0, Kb, Vb, qop, o, m_run, l_run, qrow + 1, a.scale_log2, geo, hbase,
-                                    w, lane);
+  TileWalk<kAligned> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1);
+  attend_tiles<H, kAligned, kWaves>(rows, walk, a.S0, Kbuf, Vbuf, qop, o, m_run, l_run, qrow + 1, a.scale_log2, geo, w,
+                                    lane);
 
   if (qrow >= a.S0) return;
   // o[t][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 4t + r]
