@@ -38,12 +38,15 @@ __device__ __forceinline__ u32x4 ld16g(const __bf16* p) { return *reinterpret_ca
 // global_load_lds_dwordx4: a wave instruction writes 1 KiB contiguously (lane L -> bytes 16L), so each lane fetches
 // the global chunk that belongs at its swizzled position. Rows past the sequence end re-read the last row (finite data,
 // masked to probability 0).
-// Tile row sources for the DMA. src(k0, w) gathers, before the barrier that precedes the issue, the wave-uniform
-// facts one wave's DMA of the 64-key tile at k0 needs (its rows 4 * kPerWave * w .. +4 * kPerWave - 1 lie in one
-// page); addr<kV>(src, row, chunk, n_keys) is the per-lane source of LDS row `row`, chunk `chunk`. Rows at or past
-// n_keys are never read (they may lie past the tensor, or hold non-finite data that a zero weight would not cancel
-// in P.V): row n_keys - 1 is re-read in their place (finite data, masked to zero weight).
-// Contiguous [S, heads, 128] K/V pair (one KV head selected by the base pointers).
+// Tile row sources for the DMA. src(k0, w, n_keys) gathers, before the barrier that precedes the issue, the
+// wave-uniform facts one wave's DMA of the 64-key tile at k0 needs (its rows 4 * kPerWave * w .. +4 * kPerWave - 1 lie
+// in one page); addr<kV>(src, row, chunk, n_keys) is the per-lane source of LDS row `row`, chunk `chunk`. Rows at or
+// past n_keys are never read (they may lie past the tensor, or hold non-finite data that a zero weight would not
+// cancel in P.V): a valid row is re-read in their place (finite data, masked to zero weight). Both are branch-free
+// selects, so the compiler has no speculated slow path to hoist into every tile.
+// Contiguous [S, heads, 128] K/V pair (one KV head selected by the base pointers). kFull: every tile lies inside
+// [0, n_keys) (no row needs replacing).
+template <bool kFull>
 struct DenseRows {
   const __bf16* k;
   const __bf16* v;
@@ -57,9 +60,10 @@ struct DenseRows {
   __device__ __forceinline__ const __bf16* addr(const Src& t, int row, int chunk, int n_keys) const {
     const __bf16* base = kV ? v : k;
     const long ss = kV ? v_ss : k_ss;
-    if (t.k0 + kBN <= n_keys)                                   // uniform: a full tile
-      return base + (long)t.k0 * ss + (row * (int)ss + 8 * chunk);
-    return base + (long)min(t.k0 + row, n_keys - 1) * ss + 8 * chunk;
+    const int off = row * (int)ss + 8 * chunk;
+    if constexpr (kFull) return base + (long)t.k0 * ss + off;
+    // past the end: the tile's first row (key k0 < n_keys)
+    return base + (long)t.k0 * ss + (t.k0 + row < n_keys ? off : 8 * chunk);
   }
 };
 
@@ -72,7 +76,9 @@ struct PagedRows {
   int width;               // entries in the row
   int num_pages;
   struct Src {
-    int k0, page, page_last;                                    // page of the wave's rows, page of row n_keys - 1
+    int k0;
+    const __bf16* blk;     // page of the wave's rows
+    const __bf16* last;    // row n_keys - 1
   };
   __device__ __forceinline__ int page_of(int idx) const {
     const __attribute__((address_space(4))) int32_t* t = (const __attribute__((address_space(4))) int32_t*)table;
@@ -80,17 +86,15 @@ struct PagedRows {
   }
   template <int kPerWave>
   __device__ __forceinline__ Src src(int k0, int w, int n_keys) const {
-    return Src{k0, page_of((k0 >> 4) + (4 * kPerWave * w >> 4)), page_of((n_keys - 1) >> 4)};
+    const int last = n_keys - 1;
+    return Src{k0, kv + (long)page_of((k0 >> 4) + (4 * kPerWave * w >> 4)) * kPageElems,
+               kv + (long)page_of(last >> 4) * kPageElems + (last & 15) * kSlotElems};
   }
   template <bool kV>
   __device__ __forceinline__ const __bf16* addr(const Src& t, int row, int chunk, int n_keys) const {
-    const __bf16* base = kv + (kV ? kHalfElems : 0);
-    if (t.k0 + kBN <= n_keys)                                   // uniform: a full tile
-      return base + (long)t.page * kPageElems + ((row & 15) * kSlotElems + 8 * chunk);
     const bool in = t.k0 + row < n_keys;
-    const int page = in ? t.page : t.page_last;
-    const int slot = in ? (row & 15) : ((n_keys - 1) & 15);
-    return base + (long)page * kPageElems + (slot * kSlotElems + 8 * chunk);
+    const __bf16* base = in ? t.blk + (row & 15) * kSlotElems : t.last;
+    return base + ((kV ? kHalfElems : 0) + 8 * chunk);
   }
 };
 
@@ -201,65 +205,63 @@ __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const T
         }
 }
 
-// Online-softmax bookkeeping of one tile: column maxima (log2 domain) and the lazy rescale, which moves the running
-// max only when a column max grows by more than 8 (P stays below 2^8) and then rescales l and O.
+// Online softmax of one tile, in place: s becomes t = s * scale_log2 - m_run (log2 domain, relative to the running
+// max; an arithmetic result, so the maxima below need no NaN canonicalisation), then the P^T operands exp2(t) of the
+// two 32-key halves. Lazy rescale: the running max moves only when a column's max exceeds it by more than 8 (P stays
+// below 2^8); then O and the weight sums are rescaled and t shifted. P^T k-index e < 4 of half kk is key
+// 32kk + 4j + e, e >= 4 is key 32kk + 16 + 4j + e - 4 (the order vt_operand reads V in).
 template <int H>
-__device__ __forceinline__ void tile_rescale(const floatx4 (&s)[2][2][H], floatx4 (&o)[8][H], float (&m_run)[H],
-                                             floatx4 (&lsum)[H], float scale_log2) {
-  float tmax[H];
+__device__ __forceinline__ void tile_softmax(floatx4 (&s)[2][2][H], floatx4 (&o)[8][H], float (&m_run)[H],
+                                             floatx4 (&lsum)[H], float scale_log2, bf16x8 (&pop)[2][H]) {
+  float neg_m[H], tmax[H];
+  bool need = false;
 #pragma unroll
   for (int u = 0; u < H; ++u) {
-    float mx = fmaxf(fmaxf(s[0][0][u][0], s[0][0][u][1]), fmaxf(s[0][0][u][2], s[0][0][u][3]));
+    neg_m[u] = m_run[u] == -INFINITY ? 0.f : -m_run[u];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (kk == 0 && t == 0) continue;
-        mx = fmaxf(mx, fmaxf(fmaxf(s[kk][t][u][0], s[kk][t][u][1]), fmaxf(s[kk][t][u][2], s[kk][t][u][3])));
-      }
-    mx = max_xor16(mx);
-    mx = max_xor32(mx);
-    tmax[u] = mx * scale_log2;                          // log2-domain max (scale > 0)
-  }
-  bool need = false;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-  for (int u = 0; u < H; ++u) need |= tmax[u] > m_run[u] + 8.f;
+        for (int r = 0; r < 4; ++r) s[kk][t][u][r] = fmaf(s[kk][t][u][r], scale_log2, neg_m[u]);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        mx = fmaxf(mx, fmaxf(fmaxf(s[kk][t][u][0], s[kk][t][u][1]), fmaxf(s[kk][t][u][2], s[kk][t][u][3])));
+    mx = max_xor16(mx);
+    tmax[u] = max_xor32(mx);
+    need |= tmax[u] - neg_m[u] > m_run[u] + 8.f;       // absolute max (log2 units) beyond the headroom
+  }
   if (__any(need)) {
 #pragma unroll
     for (int u = 0; u < H; ++u) {
-      const float m_new = fmaxf(m_run[u], tmax[u]);
-      const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+      const float m_new = fmaxf(m_run[u], tmax[u] - neg_m[u]);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[u] - m_new);
+      const float d = m_new == -INFINITY ? 0.f : m_new + neg_m[u];    // new max minus the offset t was taken at
       m_run[u] = m_new;
       lsum[u] *= alpha;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i][u] *= alpha;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) s[kk][t][u] -= d;
     }
   }
-}
-
-// Probabilities of one tile as the P^T operands of its two 32-key halves. P^T k-index e < 4 of half kk is key
-// 32kk + 4j + e, e >= 4 is key 32kk + 16 + 4j + e - 4 (the order vt_operand reads V in).
-template <int H>
-__device__ __forceinline__ void tile_probs(const floatx4 (&s)[2][2][H], const float (&m_run)[H], float scale_log2,
-                                           bf16x8 (&pop)[2][H]) {
 #pragma unroll
-  for (int u = 0; u < H; ++u) {
-    const float neg_m = m_run[u] == -INFINITY ? 0.f : -m_run[u];
+  for (int u = 0; u < H; ++u)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      float p[2][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p[t][r] = fast_exp2(fmaf(s[kk][t][u][r], scale_log2, neg_m));
       u32x4 pw;
-      pw[0] = pack_bf16x2(p[0][0], p[0][1]);
-      pw[1] = pack_bf16x2(p[0][2], p[0][3]);
-      pw[2] = pack_bf16x2(p[1][0], p[1][1]);
-      pw[3] = pack_bf16x2(p[1][2], p[1][3]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        pw[2 * t] = pack_bf16x2(fast_exp2(s[kk][t][u][0]), fast_exp2(s[kk][t][u][1]));
+        pw[2 * t + 1] = pack_bf16x2(fast_exp2(s[kk][t][u][2]), fast_exp2(s[kk][t][u][3]));
+      }
       pop[kk][u] = __builtin_bit_cast(bf16x8, pw);
     }
-  }
 }
 
 // O^T += V^T . P^T over one tile: o[t][u][r] accumulates out dim 32 * (lane >> 4) + 4t + r of column (u, m16).
@@ -350,12 +352,11 @@ __device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n
     issue_half<kWaves, false>(rows, src_k, n_keys, K[slot], w, lane);
     issue_half<kWaves, true>(rows, src_v, n_keys, V[slot2], w, lane);
     tile_mask<H, kAligned>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
-    tile_rescale<H>(s_cur, o, m_run, lsum, scale_log2);
     bf16x8 pop[2][H];
-    // Unconditional so that both land in one scheduling region: after the last tile the scores are computed from
+    tile_softmax<H>(s_cur, o, m_run, lsum, scale_log2, pop);
+    // Unconditional so that the MFMAs can overlap the softmax work: after the last tile the scores are computed from
     // whatever K[slot1] holds (finite data: a tile or its re-load) and discarded.
     tile_scores<H>(K[slot1], qop, s_nxt, m16, j);
-    tile_probs<H>(s_cur, m_run, scale_log2, pop);
     tile_pv<H>(V[slot], pop, o, lsum, lane);
     if (!h1) return false;
     t0 = t1; m0 = m1;

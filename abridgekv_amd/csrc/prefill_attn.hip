@@ -166,7 +166,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     l_run[u] = 0.f;
   }
 
-  const DenseRows rows{a.k + (long)b * a.k_sb + (long)kvh * a.k_sh, a.v + (long)b * a.v_sb + (long)kvh * a.v_sh,
+  const DenseRows<kAligned> rows{a.k + (long)b * a.k_sb + (long)kvh * a.k_sh, a.v + (long)b * a.v_sb + (long)kvh * a.v_sh,
                        a.k_ss, a.v_ss};
   // this wave's heads hbase, hbase + 1 (hbase is 0 or 2): quotas by selection, not by a computed index
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
