@@ -45,6 +45,18 @@ SIGNATURES = {
     "abkv_paged_prefill_attn": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp, _vp,
                                           _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long, C.c_long,
                                           _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
+    "abkv_packed_capture": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_long, C.c_int, _vp,
+                                      _vp, C.c_int, _vp]),
+    "abkv_decode_side_split_rows": (C.c_int, [C.c_int]),
+    "abkv_decode_packed_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "abkv_decode_attn_packed": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, _vp, C.c_int, C.c_int,
+                                          C.c_int, _vp, C.c_int, C.c_int, _i32p, _vp, C.c_long, _vp, C.c_int, C.c_int,
+                                          C.c_float, _vp, C.c_long, C.c_long, _vp, _vp, C.c_size_t, _vp]),
+    "abkv_paged_prefill_attn_packed": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp,
+                                                 _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _vp, _vp, C.c_int,
+                                                 C.c_int, _i32p, _vp, C.c_long, _vp, C.c_int, C.c_float, _vp,
+                                                 C.c_long, C.c_long, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                                 C.c_int, _vp, C.c_size_t, _vp]),
     "abkv_planner_create": (_vp, [C.c_int, C.c_int, C.c_int, _i32p, C.c_int64]),
     "abkv_planner_destroy": (None, [_vp]),
     "abkv_planner_last_error": (C.c_char_p, [_vp]),

@@ -2,8 +2,9 @@
 
 Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309 for the configuration this path serves: one pause
 pass, raw prompt, bitrev code positions, no replay / raw / retained tails, optional per-layer quotas with physical
-removal. Options of the reference that belong to other modes (replay tails, retained tails, packed per-head KV,
-selective full-history evaluation) are rejected with ValueError instead of being silently ignored.
+removal, or per-head quotas in packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as at
+compresslm.py:145-190). Options of the reference that belong to other modes (replay tails, retained tails, selective
+full-history evaluation) are rejected with ValueError instead of being silently ignored.
 """
 from __future__ import annotations
 
@@ -87,12 +88,15 @@ class CompressLMConfig:
     physical_layer_quotas: bool = False
     retain_full_history_layers: tuple[int, ...] = ()
     packed_kv: bool = False
+    packed_kv_k_max: int = 2048
+    packed_kv_quotas: tuple[tuple[int, ...], ...] = ()
 
     _code_token_ids: list[int] = field(default_factory=list, repr=False)
     _initialized: bool = field(default=False, repr=False)
 
     def __post_init__(self) -> None:
         self.layer_code_quotas = tuple(int(q) for q in self.layer_code_quotas)
+        self.packed_kv_quotas = tuple(tuple(int(v) for v in row) for row in self.packed_kv_quotas)
         self.retain_full_history_layers = tuple(sorted(set(self.retain_full_history_layers)))
         if self.code_positions not in ("appended", "bitrev"):
             raise ValueError("code_positions must be appended or bitrev")
@@ -115,11 +119,24 @@ class CompressLMConfig:
             raise ValueError("CompressLM decoding requires pause_xattn='full'")
         if not self.raw_prompt:
             raise ValueError("CompressLM decoding requires raw_prompt=True")
-        if self.packed_kv or self.retain_full_history_layers:
-            raise ValueError("packed per-head KV and selective full history are not served by this build")
+        if self.retain_full_history_layers:
+            raise ValueError("selective full history is not served by this build")
         for layer, q in enumerate(self.layer_code_quotas):
             if not 0 < q <= K:
                 raise ValueError(f"layer_code_quotas[{layer}]={q} must be in [1, {K}]")
+        if self.packed_kv and any(q < K for q in self.layer_code_quotas):
+            raise ValueError("layer_code_quotas and packed KV are mutually exclusive")
+        if self.packed_kv:
+            if self.packed_kv_k_max != K:
+                raise ValueError("packed_kv_k_max must equal num_code_tokens so the dense code pass computes every "
+                                 "schedulable slot")
+            for layer, row in enumerate(self.packed_kv_quotas):
+                if not row:
+                    raise ValueError(f"packed_kv_quotas[{layer}] must not be empty")
+                for head, q in enumerate(row):
+                    if not 0 < q <= self.packed_kv_k_max:
+                        raise ValueError(f"packed_kv_quotas[{layer}][{head}]={q} must be in "
+                                         f"[1, {self.packed_kv_k_max}]")
         if self.physical_layer_quotas and not self.layer_code_quotas:
             raise ValueError("physical_layer_quotas needs layer_code_quotas")
 
@@ -234,7 +251,13 @@ class CompressLMConfig:
 
     @property
     def uses_packed_kv(self) -> bool:
-        return False
+        return bool(self.packed_kv)
+
+    def packed_layout(self, num_layers: int, num_kv_heads: int = 8):
+        """The PackedKVLayout of this config (uniform k_max rows when no schedule is given)."""
+        from .packed_kv import PackedKVLayout
+        return PackedKVLayout.from_schedule(self.packed_kv_quotas or None, num_layers=num_layers,
+                                            num_kv_heads=num_kv_heads, k_max=self.packed_kv_k_max)
 
     def layer_quota(self, layer: int) -> int:
         if 0 <= layer < len(self.layer_code_quotas):

@@ -39,8 +39,22 @@ struct DecodeArgs {
   __bf16* out;               // [B, 32, 128] (strides o_sb, o_sh)
   long o_sb, o_sh;
   float* lse;                // [B, 32] or nullptr
-  float* part_o;             // [B, max_splits, 32, 128] fp32
-  float* part_ml;            // [B, max_splits, 32, 2] fp32 (m in log2 units, l)
+  float* part_o;             // [B, part_stride, 32, 128] fp32
+  float* part_ml;            // [B, part_stride, 32, 2] fp32 (m in log2 units, l)
+  int part_stride;           // split slots per sequence in the partial buffers (max_splits, + side splits)
+  int force_partials;        // write partials even for one split (the side rows are merged in afterwards)
+  // Side rows (per-head packed code pages; unused when side_count is null): packed page p of a sequence holds, for
+  // KV head h, rows side_o[h] .. side_o[h] + side_q[h] - 1 of a [2][side_rows][128] page in side_kv.
+  const __bf16* side_kv;     // [side_pool_pages, 2, side_rows, 128]
+  int side_rows;
+  int side_pool_pages;
+  const int32_t* side_table; // [B, side_stride] packed page ids per sequence
+  long side_stride;
+  const int32_t* side_count; // [B] packed pages per sequence
+  int side_max_pages;        // bound on side_count
+  int side_split_rows;       // side rows per split and head (multiple of 32, <= 63 * min quota)
+  int side_qmax;
+  int side_q[kHeadsKV], side_o[kHeadsKV];
 };
 
 __device__ __forceinline__ u32x4 ld16(const __bf16* p) {
@@ -182,7 +196,7 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
   const float l_tot = sum_xor32(sum_xor16(l_run));
   if (m16 >= kGroup) return;
   const int head = kvh * kGroup + m16;
-  if (n_splits == 1) {
+  if (n_splits == 1 && !a.force_partials) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + 32 * j;
 #pragma unroll
@@ -195,7 +209,7 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
     if (a.lse != nullptr && j == 0)
       a.lse[(long)b * kHeadsQ + head] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
   } else {
-    float* po = a.part_o + (((long)b * a.max_splits + split) * kHeadsQ + head) * kHeadDim + 32 * j;
+    float* po = a.part_o + (((long)b * a.part_stride + split) * kHeadsQ + head) * kHeadDim + 32 * j;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       floatx4 w0 = {o[0][r], o[1][r], o[2][r], o[3][r]};
@@ -204,37 +218,51 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
       *reinterpret_cast<floatx4*>(po + 8 * r + 4) = w1;
     }
     if (j == 0) {
-      float* pml = a.part_ml + (((long)b * a.max_splits + split) * kHeadsQ + head) * 2;
+      float* pml = a.part_ml + (((long)b * a.part_stride + split) * kHeadsQ + head) * 2;
       pml[0] = m_run;
       pml[1] = l_tot;
     }
   }
 }
 
-// Merge the split partials of every sequence with more than one split. Workgroup (sequence, group of 8 heads);
-// thread t handles head 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
+// Side splits of sequence b (0 without side rows): its packed pages times the largest head quota, in split rows.
+__device__ __forceinline__ int side_splits(const DecodeArgs& a, int b) {
+  if (a.side_count == nullptr) return 0;
+  const int count = min(max(a.side_count[b], 0), a.side_max_pages);
+  return (count * a.side_qmax + a.side_split_rows - 1) / a.side_split_rows;
+}
+
+// Merge the split partials of every sequence with more than one split (main splits at slots [0, n_main), side splits
+// at [max_splits, max_splits + n_side)). Workgroup (sequence, group of 8 heads); thread t handles head
+// 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int b = blockIdx.x;
-  const int seq_len = min(a.seq_lens[b], a.max_pages * kPage);
+  const int seq_len = max(min(a.seq_lens[b], a.max_pages * kPage), 0);
   const int n_pages = (seq_len + kPage - 1) / kPage;
-  const int n_splits = (n_pages + a.split_pages - 1) / a.split_pages;
-  if (n_splits <= 1) return;
+  const int n_main = max(1, (n_pages + a.split_pages - 1) / a.split_pages);
+  const int n_side = side_splits(a, b);
+  if (!a.force_partials && n_main <= 1) return;
+  const int n_all = n_main + n_side;
   const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
   const int d0 = (threadIdx.x & 31) * 4;
-  const float* pml = a.part_ml + ((long)b * a.max_splits * kHeadsQ + head) * 2;
+  const float* pml = a.part_ml + ((long)b * a.part_stride * kHeadsQ + head) * 2;
+  const float* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
+  // split k of the n_all: main split k, or side split k - n_main at slot max_splits + (k - n_main)
+  auto slot = [&](int k) { return k < n_main ? k : a.max_splits + (k - n_main); };
   // unrolled so the per-split loads of a thread are in flight together (the loop is latency-bound otherwise)
   float M = -INFINITY;
 #pragma unroll 8
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[(long)s * kHeadsQ * 2]);
+  for (int k = 0; k < n_all; ++k) M = fmaxf(M, pml[(long)slot(k) * kHeadsQ * 2]);
   float L = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (M != -INFINITY) {
 #pragma unroll 8
-  for (int s = 0; s < n_splits; ++s) {
-    const float w = fast_exp2(pml[(long)s * kHeadsQ * 2] - M);
-    L += w * pml[(long)s * kHeadsQ * 2 + 1];
-    const floatx4 v =
-        *reinterpret_cast<const floatx4*>(a.part_o + (((long)b * a.max_splits + s) * kHeadsQ + head) * kHeadDim + d0);
-    acc += w * v;
+    for (int k = 0; k < n_all; ++k) {
+      const long s = slot(k);
+      const float w = fast_exp2(pml[s * kHeadsQ * 2] - M);
+      L += w * pml[s * kHeadsQ * 2 + 1];
+      acc += w * *reinterpret_cast<const floatx4*>(pob + s * kHeadsQ * kHeadDim);
+    }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + d0;
@@ -244,6 +272,138 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   *reinterpret_cast<u32x2*>(oh) = wv;
   if (a.lse != nullptr && (threadIdx.x & 31) == 0)
     a.lse[(long)b * kHeadsQ + head] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : -INFINITY;
+}
+
+// Attention of each sequence's 32 query heads over its side rows (per-head packed code pages; the reference keeps
+// them as PackedKVSidecar pages, third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:242-270, and
+// attends them ahead of the paged rows, :564-616). Grid (side splits, B), wave = KV head h: its rows are
+// r = 0 .. count * q_h - 1, row r being row side_o[h] + r % q_h of packed page r / q_h of the sequence. A split
+// covers side_split_rows rows of every head (heads with fewer rows finish early and write an empty partial), 32 rows
+// per step with the decode kernel's operand layout; partials go to slot max_splits + split.
+__global__ __launch_bounds__(512) void decode_side_kernel(DecodeArgs a) {
+  const int b = blockIdx.y;
+  const int split = blockIdx.x;
+  if (split >= side_splits(a, b)) return;
+  const int kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int m16 = lane & 15;
+  const int j = lane >> 4;
+  const int count = min(max(a.side_count[b], 0), a.side_max_pages);
+  const int qh = a.side_q[kvh], oh = a.side_o[kvh];
+  const int r_begin = split * a.side_split_rows;
+  const int r_end = min(count * qh, r_begin + a.side_split_rows);
+
+  bf16x8 qop[4];
+  {
+    const __bf16* qp = a.q + (long)b * a.q_sb + (long)(kvh * kGroup + min(m16, kGroup - 1)) * a.q_sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 v = ld16(qp + 8 * (4 * i + j));
+      if (m16 >= kGroup) v = u32x4{0, 0, 0, 0};
+      qop[i] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  floatx4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // Packed page ids of the split: lane l holds page p0 + l; the split's rows of this head lie in at most 64 pages
+  // (side_split_rows <= 63 * quota). Row r -> page r / q_h by a float reciprocal: exact while r < 2^21 (the distance
+  // of (r + 0.5) / q_h to an integer, 0.5 / q_h, exceeds the rounding error r / q_h * 2^-22).
+  const int p0 = r_begin / qh;
+  int pid_l = 0;
+  if (p0 + lane < count) pid_l = min(max(a.side_table[(long)b * a.side_stride + p0 + lane], 0), a.side_pool_pages - 1);
+  const float inv_q = 1.f / (float)qh;
+  const long page_elems = 2L * a.side_rows * kHeadDim;
+  const __bf16* base_h = a.side_kv + (long)oh * kHeadDim;
+  auto row_ptr = [&](int r) -> const __bf16* {
+    const int p = (int)(((float)r + 0.5f) * inv_q);
+    const int slot = r - p * qh;
+    const int pid = __shfl(pid_l, p - p0, 64);
+    return base_h + (long)pid * page_elems + slot * kHeadDim;
+  };
+  const long v_off = (long)a.side_rows * kHeadDim;
+
+  for (int c0 = r_begin; c0 < r_end; c0 += 32) {
+    // rows past r_end read row r_end - 1 instead (finite data; their weight is exactly 0)
+    u32x4 kr[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const __bf16* kp = row_ptr(min(c0 + 16 * t + m16, r_end - 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[t][i] = ld16(kp + 8 * (4 * i + j));
+    }
+    // V rows: contraction index e < 4 -> row c0 + 4j + e, e >= 4 -> row c0 + 16 + 4j + e - 4; dims 8*m16 .. +8
+    u32x4 vr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      vr[e] = ld16(row_ptr(min(c0 + (e < 4 ? 0 : 16) + 4 * j + (e & 3), r_end - 1)) + v_off + 8 * m16);
+
+    floatx4 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[t] = mfma16x16x32(__builtin_bit_cast(bf16x8, kr[t][i]), qop[i], s[t]);
+    }
+    float sv[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sv[4 * t + r] = c0 + 16 * t + 4 * j + r < r_end ? s[t][r] * a.scale_log2 : -INFINITY;
+    float mx = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+    mx = max_xor16(mx);
+    mx = max_xor32(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sv[e] = fast_exp2(sv[e] - m_new);
+      psum += sv[e];
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] *= alpha;
+    u32x4 pw;
+    pw[0] = pack_bf16x2(sv[0], sv[1]);
+    pw[1] = pack_bf16x2(sv[2], sv[3]);
+    pw[2] = pack_bf16x2(sv[4], sv[5]);
+    pw[3] = pack_bf16x2(sv[6], sv[7]);
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lo[k] = __builtin_amdgcn_perm(vr[2 * k + 1][c], vr[2 * k][c], 0x05040100u);
+        hi[k] = __builtin_amdgcn_perm(vr[2 * k + 1][c], vr[2 * k][c], 0x07060302u);
+      }
+      o[2 * c] = mfma16x16x32(__builtin_bit_cast(bf16x8, lo), pop, o[2 * c]);
+      o[2 * c + 1] = mfma16x16x32(__builtin_bit_cast(bf16x8, hi), pop, o[2 * c + 1]);
+    }
+  }
+
+  const float l_tot = sum_xor32(sum_xor16(l_run));
+  if (m16 >= kGroup) return;
+  const int head = kvh * kGroup + m16;
+  const long slot = (long)b * a.part_stride + a.max_splits + split;
+  float* po = a.part_o + (slot * kHeadsQ + head) * kHeadDim + 32 * j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    *reinterpret_cast<floatx4*>(po + 8 * r) = floatx4{o[0][r], o[1][r], o[2][r], o[3][r]};
+    *reinterpret_cast<floatx4*>(po + 8 * r + 4) = floatx4{o[4][r], o[5][r], o[6][r], o[7][r]};
+  }
+  if (j == 0) {
+    float* pml = a.part_ml + (slot * kHeadsQ + head) * 2;
+    pml[0] = m_run;
+    pml[1] = l_tot;
+  }
 }
 
 }  // namespace abkv
@@ -290,6 +450,9 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
   a.lse = lse;
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + (size_t)num_seqs * max_splits * kHeadsQ * kHeadDim;
+  a.part_stride = max_splits;
+  a.force_partials = 0;
+  a.side_count = nullptr;
   hipLaunchKernelGGL(decode_attn_kernel, dim3(max_splits, num_seqs), dim3(512), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
@@ -298,6 +461,101 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
     err = hipGetLastError();
   }
   return (int)err;
+}
+
+// Side rows per split and head for a packed layout whose smallest head quota is q_min (multiple of 32, at most
+// 63 * q_min so that a split's rows of any head lie in at most 64 packed pages, at most 512).
+int abkv_decode_side_split_rows(int q_min) {
+  if (q_min <= 0) return 0;
+  const int r = (63 * q_min / 32) * 32;
+  return r < 32 ? 32 : (r > 512 ? 512 : r);
+}
+
+// Workspace bytes for abkv_decode_attn_packed: partials of (main splits + side splits) per sequence.
+size_t abkv_decode_packed_workspace_size(int num_seqs, int max_pages_per_seq, int split_pages, int max_side_pages,
+                                         int side_q_max, int side_split_rows) {
+  if (num_seqs <= 0 || split_pages <= 0 || side_split_rows <= 0) return 0;
+  const int main_splits = (max_pages_per_seq + split_pages - 1) / split_pages;
+  const int side = (max_side_pages * side_q_max + side_split_rows - 1) / side_split_rows;
+  return abkv_decode_workspace_size(num_seqs, main_splits + side);
+}
+
+int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache, int num_pages,
+                            const int32_t* block_table, long block_table_stride, const int32_t* seq_lens,
+                            int num_seqs, int max_pages_per_seq, int split_pages, const void* packed_kv,
+                            int packed_pool_pages, int packed_rows, const int32_t* head_quota,
+                            const int32_t* packed_table, long packed_table_stride, const int32_t* packed_count,
+                            int max_packed_per_seq, int side_split_rows, float scale, void* out, long out_stride_seq,
+                            long out_stride_head, float* lse, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+  using namespace abkv;
+  if (num_seqs <= 0) return 0;
+  if (split_pages <= 0 || (split_pages & 1) || split_pages > 64 || max_pages_per_seq <= 0 || num_pages <= 0 ||
+      block_table_stride < max_pages_per_seq)
+    return (int)hipErrorInvalidValue;
+  if (q == nullptr || kv_cache == nullptr || block_table == nullptr || seq_lens == nullptr || out == nullptr ||
+      packed_kv == nullptr || packed_table == nullptr || packed_count == nullptr || head_quota == nullptr ||
+      packed_pool_pages <= 0 || max_packed_per_seq < 0 || packed_table_stride < max_packed_per_seq)
+    return (int)hipErrorInvalidValue;
+  // head quotas (host array): each in [1, 2048], rows = their sum
+  int qmin = 1 << 30, qmax = 0, rows = 0;
+  DecodeArgs a;
+  for (int h = 0; h < kHeadsKV; ++h) {
+    const int qh = head_quota[h];
+    if (qh <= 0 || qh > 2048) return (int)hipErrorInvalidValue;
+    a.side_q[h] = qh;
+    a.side_o[h] = rows;
+    rows += qh;
+    qmin = qh < qmin ? qh : qmin;
+    qmax = qh > qmax ? qh : qmax;
+  }
+  if (rows != packed_rows || side_split_rows <= 0 || (side_split_rows & 31) || side_split_rows > 63 * qmin ||
+      (long)max_packed_per_seq * qmax >= (1L << 21))
+    return (int)hipErrorInvalidValue;
+  const int max_splits = (max_pages_per_seq + split_pages - 1) / split_pages;
+  const int side_max = (max_packed_per_seq * qmax + side_split_rows - 1) / side_split_rows;
+  const int stride = max_splits + side_max;
+  if (workspace == nullptr || workspace_bytes < abkv_decode_workspace_size(num_seqs, stride))
+    return (int)hipErrorInvalidValue;
+  a.q = static_cast<const __bf16*>(q);
+  a.q_sb = q_stride_seq;
+  a.q_sh = q_stride_head;
+  a.kv = static_cast<const __bf16*>(kv_cache);
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.seq_lens = seq_lens;
+  a.split_pages = split_pages;
+  a.max_splits = max_splits;
+  a.max_pages = max_pages_per_seq;
+  a.num_pages = num_pages;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = static_cast<__bf16*>(out);
+  a.o_sb = out_stride_seq;
+  a.o_sh = out_stride_head;
+  a.lse = lse;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + (size_t)num_seqs * stride * kHeadsQ * kHeadDim;
+  a.part_stride = stride;
+  a.force_partials = 1;
+  a.side_kv = static_cast<const __bf16*>(packed_kv);
+  a.side_rows = packed_rows;
+  a.side_pool_pages = packed_pool_pages;
+  a.side_table = packed_table;
+  a.side_stride = packed_table_stride;
+  a.side_count = packed_count;
+  a.side_max_pages = max_packed_per_seq;
+  a.side_split_rows = side_split_rows;
+  a.side_qmax = qmax;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(max_splits, num_seqs), dim3(512), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  if (side_max > 0) {
+    hipLaunchKernelGGL(decode_side_kernel, dim3(side_max, num_seqs), dim3(512), 0, stream, a);
+    err = hipGetLastError();
+    if (err != hipSuccess) return (int)err;
+  }
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 8), dim3(256), 0, stream, a);
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

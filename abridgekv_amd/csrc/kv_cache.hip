@@ -267,6 +267,53 @@ static bool fill_layers(LayerPtrs& lp, void* const* layer_caches, int n_layers) 
   return true;
 }
 
+// Per-head packed code pages (reference: PackedKVLayout.pack_layer + PackedKVSidecar.capture,
+// third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:112-128, 259-284): the K_max code rows of a closed
+// block, read from the paged cache, are stored as one packed page per layer, [2][rows_l][128] with head h's first
+// q_lh code rows at rows off_lh .. off_lh + q_lh - 1 (off = running sum of the quotas over the heads).
+struct CaptureArgs {
+  const void* const* layer_kv;   // [L] paged caches [num_pages, 2, 16, 8, 128]
+  void* const* layer_pool;       // [L] packed pools [pool_pages, 2, rows_l, 128]
+  const int32_t* layer_rows;     // [L] rows_l = sum of the layer's head quotas
+  const int32_t* layer_quota;    // [L, 8]
+  const int32_t* block_table;    // [n, bt_stride] page table row of each capture's sequence
+  long bt_stride;
+  int bt_width;
+  const int32_t* code_start;     // [n] physical position of the block's first code row
+  const int32_t* dst_page;       // [n] packed page receiving the capture
+  int num_pages, pool_pages;
+};
+
+// Grid (capture, layer), 256 threads; thread t moves 16-byte chunk t % 32 (K chunks 0-15, V chunks 16-31) of packed
+// rows t / 32, t / 32 + 8, ...
+__global__ __launch_bounds__(256) void packed_capture_kernel(CaptureArgs a) {
+  const int c = blockIdx.x, l = blockIdx.y;
+  const int rows = a.layer_rows[l];
+  const int32_t* quota = a.layer_quota + l * kHeadsKV;
+  const __bf16* kv = static_cast<const __bf16*>(a.layer_kv[l]);
+  __bf16* pool = static_cast<__bf16*>(a.layer_pool[l]);
+  const int start = a.code_start[c];
+  const int dst = min(max(a.dst_page[c], 0), a.pool_pages - 1);
+  const int32_t* bt = a.block_table + (long)c * a.bt_stride;
+  const int part = threadIdx.x & 31, half = part >> 4, chunk = part & 15;
+  for (int row = threadIdx.x >> 5; row < rows; row += 8) {
+    int h = 0, off = 0;
+#pragma unroll
+    for (int k = 0; k < kHeadsKV - 1; ++k) {   // head of packed row `row`: off_h <= row < off_h + q_h
+      if (row >= off + quota[h]) {
+        off += quota[h];
+        ++h;
+      }
+    }
+    const int pos = start + (row - off);
+    const int page = min(max(bt[min(pos >> 4, a.bt_width - 1)], 0), a.num_pages - 1);
+    const __bf16* src = kv + (long)page * kPageElems + half * kHalfElems + (pos & 15) * kSlotElems + h * kHeadDim +
+                        8 * chunk;
+    __bf16* d = pool + ((long)dst * 2 + half) * rows * kHeadDim + (long)row * kHeadDim + 8 * chunk;
+    *reinterpret_cast<u32x4*>(d) = *reinterpret_cast<const u32x4*>(src);
+  }
+}
+
 }  // namespace abkv
 
 extern "C" {
@@ -379,6 +426,32 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
   hipLaunchKernelGGL(abkv::slot_mapping_kernel, dim3((num_tokens + 255) / 256), dim3(256), 0, stream, req_idx,
                      positions, block_table, num_reqs, block_table_stride, block_size, compacted, slot_mapping,
                      num_tokens);
+  return (int)hipGetLastError();
+}
+
+int abkv_packed_capture(const void* const* layer_kv, void* const* layer_pool, const int32_t* layer_rows,
+                        const int32_t* layer_quota, int num_layers, int num_pages, int pool_pages,
+                        const int32_t* block_table, long block_table_stride, int block_table_width,
+                        const int32_t* code_start, const int32_t* dst_page, int num_captures, hipStream_t stream) {
+  using namespace abkv;
+  if (num_captures <= 0 || num_layers <= 0) return 0;
+  if (layer_kv == nullptr || layer_pool == nullptr || layer_rows == nullptr || layer_quota == nullptr ||
+      block_table == nullptr || code_start == nullptr || dst_page == nullptr || num_pages <= 0 || pool_pages <= 0 ||
+      block_table_width <= 0 || block_table_stride < block_table_width)
+    return (int)hipErrorInvalidValue;
+  CaptureArgs a;
+  a.layer_kv = layer_kv;
+  a.layer_pool = layer_pool;
+  a.layer_rows = layer_rows;
+  a.layer_quota = layer_quota;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.bt_width = block_table_width;
+  a.code_start = code_start;
+  a.dst_page = dst_page;
+  a.num_pages = num_pages;
+  a.pool_pages = pool_pages;
+  hipLaunchKernelGGL(packed_capture_kernel, dim3(num_captures, num_layers), dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 

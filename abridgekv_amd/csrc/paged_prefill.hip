@@ -31,6 +31,37 @@ struct PagedPrefillArgs {
   int num_tokens;
   float* part_o;                               // [splits, T, 32, 128] un-normalised
   float* part_ml;                              // [splits, T, 32, 2] (running max in log2 units, sum)
+  int split_base;                              // first partial slot of this launch's splits
+  const int32_t* head_quota;                   // [8] or nullptr: a non-causal request sees keys < kv_start + q_h
+  // side rows (per-head packed code pages, attended by every query of the request); see PackedRows
+  const __bf16* side_kv; int side_rows; int side_pool_pages;
+  const int32_t* side_table; long side_stride; const int32_t* side_count; int side_max_pages;
+  int side_q[kHeadsKV], side_o[kHeadsKV];
+};
+
+constexpr int kMaxSideTable = 2048;             // packed pages per request the side launch stages in LDS
+
+// Side rows of one request for KV head h: row r is row side_o[h] + r % q_h of packed page table[r / q_h]
+// ([2][rows][128] pages). The request's packed page ids are staged in LDS once; r / q_h by a float reciprocal is
+// exact while r < 2^21 (0.5 / q_h exceeds the rounding error r / q_h * 2^-22).
+struct PackedRows {
+  const __bf16* base;      // pool + side_o[h] * 128
+  const int32_t* table;    // LDS copy of the request's page ids
+  int q;
+  float inv_q;
+  long page_elems, v_off;
+  struct Src {
+    int k0;
+  };
+  template <int kPerWave>
+  __device__ __forceinline__ Src src(int k0, int, int) const { return Src{k0}; }
+  template <bool kV>
+  __device__ __forceinline__ const __bf16* addr(const Src& t, int row, int chunk, int n_keys) const {
+    const int r = min(t.k0 + row, n_keys - 1);             // past the end: row n_keys - 1 (finite, weight 0)
+    const int p = (int)(((float)r + 0.5f) * inv_q);
+    const int slot = r - p * q;
+    return base + (long)table[p] * page_elems + slot * kHeadDim + (kV ? v_off : 0) + 8 * chunk;
+  }
 };
 
 // Contiguous key tiles [kt_begin, kt_end); tiles past k_full (the smallest lane limit) are masked per lane.
@@ -43,6 +74,8 @@ struct RangeWalk {
   }
 };
 
+// kSide = false: the paged rows of the request; true: its side rows (all visible to every query).
+template <bool kSide>
 __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs a) {
   constexpr int H = 2, kWaves = 8;
   __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], K2[kTileElems];
@@ -62,8 +95,15 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const int t0 = a.q_start[r];
   const int nq = a.q_start[r + 1] - t0;
   const int kv0 = a.kv_start[r];
-  const int limit = a.kv_limit[r];
-  const bool causal = a.causal ? a.causal[r] != 0 : a.causal_default != 0;
+  const bool causal = kSide ? false : (a.causal ? a.causal[r] != 0 : a.causal_default != 0);
+  int limit = a.kv_limit[r];
+  if (!kSide && !causal && a.head_quota != nullptr) limit = min(limit, kv0 + a.head_quota[kvh]);
+  int side_q = 0, side_n = 0;
+  if constexpr (kSide) {
+    side_q = a.side_q[kvh];
+    side_n = min(max(a.side_count[r], 0), a.side_max_pages);
+    limit = side_n * side_q;                                 // side rows of this head
+  }
   const int qi = q0 + 16 * rg + m16;                        // query row within the request (MFMA column)
   const bool qvalid = qi < nq;
   const int pos = kv0 + qi;
@@ -98,15 +138,26 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const int k_end = causal ? min(limit, kv0 + q_hi + 1) : limit;
   const int k_full = causal ? min(limit, kv0 + q0 + 1) : limit;
   const int n_k_tiles = (k_end + kBN - 1) / kBN;
-  const PagedRows rows{a.kv + kvh * kHeadDim, a.block_table + (long)r * a.bt_stride, a.bt_width, a.num_pages};
   const MaskGeom geo{};
   // key tiles of this block: all of them, or split z's share when the launch is split along the keys
   RangeWalk walk;
   walk.kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
   walk.kt_end = a.split_tiles > 0 ? min(n_k_tiles, walk.kt_begin + a.split_tiles) : n_k_tiles;
   walk.k_full = k_full;
-  attend_tiles<H, true, kWaves>(rows, walk, k_end, Kbuf, Vbuf, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo, w,
-                                lane);
+  if constexpr (kSide) {
+    __shared__ int32_t side_table[kMaxSideTable];
+    const int32_t* src = a.side_table + (long)r * a.side_stride;
+    for (int i = tid; i < side_n; i += 512) side_table[i] = min(max(src[i], 0), a.side_pool_pages - 1);
+    __syncthreads();
+    const PackedRows rows{a.side_kv + (long)a.side_o[kvh] * kHeadDim, side_table, side_q, 1.f / (float)side_q,
+                          2L * a.side_rows * kHeadDim, (long)a.side_rows * kHeadDim};
+    attend_tiles<H, true, kWaves>(rows, walk, k_end, Kbuf, Vbuf, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo,
+                                  w, lane);
+  } else {
+    const PagedRows rows{a.kv + kvh * kHeadDim, a.block_table + (long)r * a.bt_stride, a.bt_width, a.num_pages};
+    attend_tiles<H, true, kWaves>(rows, walk, k_end, Kbuf, Vbuf, qop, o, m_run, l_run, lane_limit, a.scale_log2, geo,
+                                  w, lane);
+  }
 
   if (!qvalid) return;
   if (a.split_tiles > 0) {                                   // partials of this key split
@@ -114,7 +165,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
     for (int u = 0; u < H; ++u) {
       const float l = l_run[u];
       const int head = kvh * kGroup + hbase + u;
-      const long row = ((long)blockIdx.z * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
+      const long row = ((long)(a.split_base + blockIdx.z) * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
       float* po = a.part_o + row * kHeadDim + 32 * j;
 #pragma unroll
       for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * t) = o[t][u];
@@ -216,6 +267,9 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
   a.num_tokens = num_tokens;
   a.split_tiles = 0;
   a.part_o = a.part_ml = nullptr;
+  a.split_base = 0;
+  a.head_quota = nullptr;
+  a.side_count = nullptr;
   if (num_splits > 1) {
     if (split_tiles <= 0 || num_tokens <= 0 || workspace == nullptr ||
         workspace_bytes < abkv_paged_prefill_workspace_size(num_tokens, num_splits))
@@ -224,11 +278,92 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + (size_t)num_splits * num_tokens * kHeadsQ * kHeadDim;
   }
-  hipLaunchKernelGGL(paged_prefill_kernel, dim3(num_tiles, kHeadsKV, num_splits > 1 ? num_splits : 1), dim3(512), 0,
-                     stream, a);
+  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(num_tiles, kHeadsKV, num_splits > 1 ? num_splits : 1),
+                     dim3(512), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || num_splits <= 1) return (int)err;
   hipLaunchKernelGGL(paged_merge_kernel, dim3(num_tokens, kHeadsQ / 8), dim3(256), 0, stream, a, num_splits);
+  return (int)hipGetLastError();
+}
+
+int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache,
+                                   int num_pages, const int32_t* block_table, long block_table_stride,
+                                   int block_table_width, const int32_t* q_start, const int32_t* kv_start,
+                                   const int32_t* kv_limit, const int32_t* tile_req, const int32_t* tile_q0,
+                                   int num_tiles, const int32_t* causal, int causal_default,
+                                   const int32_t* head_quota_dev, const void* packed_kv, int packed_pool_pages,
+                                   int packed_rows, const int32_t* head_quota, const int32_t* packed_table,
+                                   long packed_table_stride, const int32_t* packed_count, int max_packed_per_seq,
+                                   float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
+                                   int num_tokens, int num_splits, int split_tiles, int side_splits,
+                                   int side_split_tiles, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  using namespace abkv;
+  if (num_tiles <= 0) return 0;
+  if (q == nullptr || kv_cache == nullptr || block_table == nullptr || q_start == nullptr || kv_start == nullptr ||
+      kv_limit == nullptr || tile_req == nullptr || tile_q0 == nullptr || out == nullptr || num_pages <= 0 ||
+      block_table_width <= 0 || head_quota_dev == nullptr || packed_kv == nullptr || head_quota == nullptr ||
+      packed_table == nullptr || packed_count == nullptr || packed_pool_pages <= 0 || max_packed_per_seq < 0 ||
+      max_packed_per_seq > kMaxSideTable || packed_table_stride < max_packed_per_seq || num_splits < 1 ||
+      split_tiles <= 0 || side_splits < 1 || side_split_tiles <= 0 || num_tokens <= 0)
+    return (int)hipErrorInvalidValue;
+  PagedPrefillArgs a;
+  int rows = 0, qmax = 0;
+  for (int h = 0; h < kHeadsKV; ++h) {
+    if (head_quota[h] <= 0 || head_quota[h] > 2048) return (int)hipErrorInvalidValue;
+    a.side_q[h] = head_quota[h];
+    a.side_o[h] = rows;
+    rows += head_quota[h];
+    qmax = head_quota[h] > qmax ? head_quota[h] : qmax;
+  }
+  if (rows != packed_rows || (long)max_packed_per_seq * qmax >= (1L << 21) ||
+      (long)side_splits * side_split_tiles * kBN < (long)max_packed_per_seq * qmax)
+    return (int)hipErrorInvalidValue;
+  const int total = num_splits + side_splits;
+  if (workspace == nullptr || workspace_bytes < abkv_paged_prefill_workspace_size(num_tokens, total))
+    return (int)hipErrorInvalidValue;
+  a.q = static_cast<const __bf16*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.kv = static_cast<const __bf16*>(kv_cache);
+  a.num_pages = num_pages;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.bt_width = block_table_width;
+  a.q_start = q_start;
+  a.kv_start = kv_start;
+  a.kv_limit = kv_limit;
+  a.tile_req = tile_req;
+  a.tile_q0 = tile_q0;
+  a.causal = causal;
+  a.causal_default = causal_default;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = static_cast<__bf16*>(out);
+  a.o_st = out_stride_t;
+  a.o_sh = out_stride_h;
+  a.lse = lse;
+  a.num_tokens = num_tokens;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + (size_t)total * num_tokens * kHeadsQ * kHeadDim;
+  a.head_quota = head_quota_dev;
+  a.side_kv = static_cast<const __bf16*>(packed_kv);
+  a.side_rows = packed_rows;
+  a.side_pool_pages = packed_pool_pages;
+  a.side_table = packed_table;
+  a.side_stride = packed_table_stride;
+  a.side_count = packed_count;
+  a.side_max_pages = max_packed_per_seq;
+  a.split_tiles = split_tiles;
+  a.split_base = 0;
+  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(num_tiles, kHeadsKV, num_splits), dim3(512), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  a.split_tiles = side_split_tiles;
+  a.split_base = num_splits;
+  hipLaunchKernelGGL(paged_prefill_kernel<true>, dim3(num_tiles, kHeadsKV, side_splits), dim3(512), 0, stream, a);
+  err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  hipLaunchKernelGGL(paged_merge_kernel, dim3(num_tokens, kHeadsQ / 8), dim3(256), 0, stream, a, total);
   return (int)hipGetLastError();
 }
 

@@ -452,5 +452,195 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     return out, lse
 
 
+def _host_quota(head_quota):
+    hq = [int(x) for x in head_quota]
+    _require(len(hq) == HEADS_KV and all(1 <= x <= 2048 for x in hq), "head_quota must be 8 ints in [1, 2048]")
+    return hq, (C.c_int32 * HEADS_KV)(*hq)
+
+
+def _check_pool(pool: torch.Tensor, rows: int) -> None:
+    _require(pool.is_cuda and pool.dtype == torch.bfloat16 and pool.dim() == 4 and pool.shape[1] == 2
+             and pool.shape[2] == rows and pool.shape[3] == HEAD_DIM and pool.is_contiguous(),
+             f"packed pool must be contiguous cuda bf16 [pages, 2, {rows}, {HEAD_DIM}]")
+
+
+def _check_side_table(packed_table: torch.Tensor, packed_count: torch.Tensor, B: int) -> None:
+    _require(packed_table.is_cuda and packed_table.dtype == torch.int32 and packed_table.dim() == 2
+             and packed_table.shape[0] >= B and packed_table.stride(1) == 1,
+             "packed_table must be cuda int32 [B, S] with contiguous rows")
+    _require(packed_count.is_cuda and packed_count.dtype == torch.int32 and packed_count.numel() >= B
+             and packed_count.is_contiguous(), "packed_count must be contiguous cuda int32 [B]")
+
+
+def packed_capture(layer_caches, layer_pools, layer_rows: torch.Tensor, layer_quota: torch.Tensor,
+                   block_table: torch.Tensor, code_start: torch.Tensor, dst_page: torch.Tensor) -> None:
+    """Copy closed blocks' code rows into per-head packed pages, all layers in one launch.
+
+    layer_caches / layer_pools: per layer the paged cache [P, 2, 16, 8, 128] and the packed pool
+    [pool_pages, 2, rows_l, 128] (bf16); layer_rows [L] / layer_quota [L, 8]: cuda int32 (rows_l = sum of the row);
+    block_table [n, W] cuda int32: the page table row of each capture's sequence; code_start / dst_page [n] cuda int32.
+    """
+    L = len(layer_caches)
+    _require(L > 0 and len(layer_pools) == L, "one pool per layer cache")
+    for c in layer_caches:
+        _check_cache(c)
+    _require(len({c.shape[0] for c in layer_caches}) == 1, "layer caches must have equal page counts")
+    _require(len({p.shape[0] for p in layer_pools}) == 1, "layer pools must have equal page counts")
+    _require(layer_rows.is_cuda and layer_rows.dtype == torch.int32 and layer_rows.numel() == L
+             and layer_rows.is_contiguous(), "layer_rows must be contiguous cuda int32 [L]")
+    _require(layer_quota.is_cuda and layer_quota.dtype == torch.int32 and tuple(layer_quota.shape) == (L, HEADS_KV)
+             and layer_quota.is_contiguous(), "layer_quota must be contiguous cuda int32 [L, 8]")
+    rows_host = layer_rows.cpu().tolist()
+    for pool, rows in zip(layer_pools, rows_host):
+        _check_pool(pool, int(rows))
+    n = int(code_start.numel())
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] >= n and block_table.stride(1) == 1, "block_table must be cuda int32 [n, W]")
+    _require(code_start.is_cuda and code_start.dtype == torch.int32 and code_start.is_contiguous()
+             and dst_page.is_cuda and dst_page.dtype == torch.int32 and dst_page.numel() == n
+             and dst_page.is_contiguous(), "code_start / dst_page must be contiguous cuda int32 [n]")
+    if n == 0:
+        return
+    dev = code_start.device
+    ptrs = torch.tensor([c.data_ptr() for c in layer_caches] + [p.data_ptr() for p in layer_pools],
+                        dtype=torch.int64).to(dev)
+    rc = lib().abkv_packed_capture(_ptr(ptrs[:L]), _ptr(ptrs[L:]), _ptr(layer_rows), _ptr(layer_quota), L,
+                                   layer_caches[0].shape[0], layer_pools[0].shape[0], _ptr(block_table),
+                                   _row_stride(block_table), block_table.shape[1], _ptr(code_start), _ptr(dst_page),
+                                   n, C.c_void_p(_stream()))
+    check(rc, "abkv_packed_capture")
+
+
+def decode_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                            seq_lens: torch.Tensor, packed_pool: torch.Tensor, head_quota, packed_table: torch.Tensor,
+                            packed_count: torch.Tensor, scale: float, max_pages: int | None = None,
+                            max_packed: int | None = None, out: torch.Tensor | None = None,
+                            lse: torch.Tensor | None = None, split_pages: int = DEFAULT_SPLIT_PAGES,
+                            workspace: torch.Tensor | None = None):
+    """Decode attention of one layer over the paged rows plus each sequence's per-head packed code pages.
+
+    As :func:`decode_attention`, plus packed_pool [pool_pages, 2, rows, 128] bf16 (this layer), head_quota (8 ints,
+    this layer's quotas, rows = their sum), packed_table [B, S] / packed_count [B] cuda int32 (the sequences' packed
+    page ids); ``max_packed`` bounds packed_count (defaults to S). Returns (out, lse).
+    """
+    _check_cache(kv_cache)
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1, f"q must be cuda bf16 [B, {HEADS_Q}, {HEAD_DIM}] with contiguous dims")
+    B = q.shape[0]
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] >= B and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() >= B
+             and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32 [B]")
+    _require(0 < split_pages <= 64 and split_pages % 2 == 0, "split_pages must be an even number in [2, 64]")
+    hq, hq_c = _host_quota(head_quota)
+    rows = sum(hq)
+    _check_pool(packed_pool, rows)
+    _check_side_table(packed_table, packed_count, B)
+    W = block_table.shape[1]
+    max_pages = W if max_pages is None else int(max_pages)
+    _require(0 < max_pages <= W, "max_pages must be in [1, block_table width]")
+    S = packed_table.shape[1]
+    max_packed = S if max_packed is None else int(max_packed)
+    _require(0 <= max_packed <= S and max_packed * max(hq) < (1 << 21), "max_packed must be in [0, packed_table width]")
+    if out is None:
+        out = torch.empty((B, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (B, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
+             "out must be bf16 [B, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= B * HEADS_Q,
+                 "lse must be contiguous fp32 [B, 32]")
+    sr = lib().abkv_decode_side_split_rows(min(hq))
+    need = lib().abkv_decode_packed_workspace_size(B, max_pages, split_pages, max_packed, max(hq), sr)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    _require(ws_bytes >= need, "packed decode workspace too small")
+    rc = lib().abkv_decode_attn_packed(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                       _ptr(block_table), _row_stride(block_table), _ptr(seq_lens), B, max_pages,
+                                       split_pages, _ptr(packed_pool), packed_pool.shape[0], rows, hq_c,
+                                       _ptr(packed_table), _row_stride(packed_table), _ptr(packed_count), max_packed,
+                                       sr, float(scale), _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+                                       _ptr(workspace), ws_bytes, C.c_void_p(_stream()))
+    check(rc, "abkv_decode_attn_packed")
+    return out, lse
+
+
+def paged_prefill_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start,
+                                   kv_start, kv_limit, causal, packed_pool: torch.Tensor, head_quota,
+                                   packed_table: torch.Tensor, packed_count: torch.Tensor, max_packed: int,
+                                   scale: float | None = None, out: torch.Tensor | None = None,
+                                   lse: torch.Tensor | None = None, head_quota_dev: torch.Tensor | None = None):
+    """Multi-query attention over the paged rows plus each request's per-head packed code pages (visible to every
+    query). As :func:`paged_prefill_attention`; a non-causal request (code step) sees paged keys
+    ``< min(kv_limit, kv_start + q_h)`` for KV head h. ``max_packed`` bounds packed_count (<= 2048).
+    Returns (out, lse).
+    """
+    import numpy as np
+
+    _check_cache(kv_cache)
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1, "q must be cuda bf16 [T, 32, 128] with contiguous dims")
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    qs = np.asarray(q_start, dtype=np.int64)
+    ks = np.asarray(kv_start, dtype=np.int64)
+    kl = np.asarray(kv_limit, dtype=np.int64)
+    B = ks.size
+    W = block_table.shape[1]
+    _require(qs.size == B + 1 and kl.size == B and B <= block_table.shape[0], "q_start [B+1], kv_start/kv_limit [B]")
+    _require(qs[0] == 0 and np.all(np.diff(qs) >= 0) and qs[-1] <= q.shape[0], "q_start must be a prefix sum <= T")
+    _require(np.all(kl >= 0) and np.all(kl <= W * PAGE) and np.all(ks >= 0), "kv ranges out of the table")
+    hq, hq_c = _host_quota(head_quota)
+    rows = sum(hq)
+    _check_pool(packed_pool, rows)
+    _check_side_table(packed_table, packed_count, B)
+    max_packed = int(max_packed)
+    _require(0 <= max_packed <= min(2048, packed_table.shape[1]) and max_packed * max(hq) < (1 << 21),
+             "max_packed must be in [0, min(2048, packed_table width)]")
+    T = q.shape[0]
+    if out is None:
+        out = torch.empty((T, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (T, HEADS_Q, HEAD_DIM) and out.stride(2) == 1,
+             "out must be bf16 [T, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (T, HEADS_Q),
+                 "lse must be contiguous fp32 [T, 32]")
+    nq = np.diff(qs)
+    tiles = [(r, q0) for r in range(B) for q0 in range(0, int(nq[r]), 64)]
+    if not tiles:
+        return out, lse
+    dev = q.device
+    tr = np.asarray(tiles, dtype=np.int32)
+    cz = np.broadcast_to(np.asarray(causal, dtype=np.int64), (B,)).astype(np.int64)
+    meta = torch.from_numpy(np.concatenate([qs, ks, kl, cz, hq]).astype(np.int32)).to(dev)
+    tl = torch.from_numpy(np.ascontiguousarray(tr.T)).to(dev)
+    o1, o2, o3, o4 = B + 1, 2 * B + 1, 3 * B + 1, 4 * B + 1
+    if head_quota_dev is None:
+        head_quota_dev = meta[o4:]
+    _require(head_quota_dev.is_cuda and head_quota_dev.dtype == torch.int32 and head_quota_dev.numel() == HEADS_KV,
+             "head_quota_dev must be cuda int32 [8]")
+    scale = default_scale() if scale is None else float(scale)
+    max_keys = int(kl.max()) if kl.size else 0
+    n_splits, split_tiles = paged_split_plan(len(tiles), max_keys)
+    if n_splits <= 1:
+        n_splits, split_tiles = 1, max(1, -(-max_keys // 64))
+    side_rows = max(1, max_packed * max(hq))
+    side_tiles_all = -(-side_rows // 64)
+    side_splits, side_split_tiles = paged_split_plan(len(tiles), side_rows)
+    if side_splits <= 1:
+        side_splits, side_split_tiles = 1, side_tiles_all
+    ws_bytes = lib().abkv_paged_prefill_workspace_size(T, n_splits + side_splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    rc = lib().abkv_paged_prefill_attn_packed(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0], _ptr(block_table),
+        _row_stride(block_table), W, _ptr(meta[:o1]), _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(tl[0]), _ptr(tl[1]),
+        len(tiles), _ptr(meta[o3:o4]), 1, _ptr(head_quota_dev), _ptr(packed_pool), packed_pool.shape[0], rows, hq_c,
+        _ptr(packed_table), _row_stride(packed_table), _ptr(packed_count), max_packed, scale, _ptr(out),
+        out.stride(0), out.stride(1), _ptr(lse), T, n_splits, split_tiles, side_splits, side_split_tiles, _ptr(ws),
+        ws_bytes, C.c_void_p(_stream()))
+    check(rc, "abkv_paged_prefill_attn_packed")
+    return out, lse
+
+
 def default_scale() -> float:
     return 1.0 / math.sqrt(HEAD_DIM)

@@ -2,7 +2,7 @@
 
 API-compatible with the reference's CompressLMProcessor (third_party/vllm_overlay/vllm/v1/core/compresslm/
 processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay / retained tails,
-physical per-layer quotas): prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121,
+physical per-layer quotas or per-head packed KV pages): prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121,
 limit_num_new_tokens :123-151, should_skip_sampling :153-168, update_after_step :170-257, reset_for_preemption
 :259-260, code_physical_spans :276-316, _stage_codes :369-400, _finish_block :419-465, _compact_response_content
 :467-557, _mask_or_raise :648-661, _check_stop :663-685. The compaction callback ``mask_span(request_id, start, end,
@@ -225,7 +225,7 @@ class CompressLMProcessor:
             elif sampled is not None:
                 self._append_content(request, state, [sampled], is_prompt=False)
         elif role == CODE and role_end:
-            self._finish_block(request, state, block, mask_span)
+            self._finish_block(request, state, block, mask_span, pack_code_span)
         return visible, False
 
     def reset_for_preemption(self, state: CompressLMState) -> None:
@@ -241,7 +241,8 @@ class CompressLMProcessor:
         for block in state.blocks:
             if block.code_span is None:
                 continue
-            if self.group_quotas is not None and block.block_id in state.compacted_block_ids:
+            if (self.group_quotas is not None or self.config.uses_packed_kv) and \
+                    block.block_id in state.compacted_block_ids:
                 continue
             start, end = block.code_span
             if logical_limit is not None and end > logical_limit:
@@ -280,8 +281,8 @@ class CompressLMProcessor:
         state.position_to_block.extend([block.block_id] * len(ids))
         state.worker_token_ids_dirty = True
 
-    def _finish_block(self, request, state, block, mask_span) -> None:
-        self._compact_response_content(request, state, block, mask_span)
+    def _finish_block(self, request, state, block, mask_span, pack_code_span=None) -> None:
+        self._compact_response_content(request, state, block, mask_span, pack_code_span)
         if block.code_span[1] < request.num_tokens:          # preemption replay: later tokens already exist
             return
         nxt = CompressLMBlock(block_id=len(state.blocks))
@@ -299,12 +300,28 @@ class CompressLMProcessor:
         self._append_content(request, state, [held], is_prompt=False)
         state.worker_token_ids_dirty = True
 
-    def _compact_response_content(self, request, state, block, mask_span) -> None:
+    def _compact_response_content(self, request, state, block, mask_span, pack_code_span=None) -> None:
         """Remove the block's response rows from every group, then (physical quotas) code slots [q, K) from the
-        groups of each quota q < K, ascending q, each on the layout the previous removal left."""
+        groups of each quota q < K, ascending q, each on the layout the previous removal left. Packed KV: archive
+        the code span first (``pack_code_span(request_id, start, end)``), then remove the response content and the
+        codes as one span (compresslm/processor.py:484-520)."""
         if block.block_id in state.compacted_block_ids:
             return
         pos = block.response_content_positions
+        if self.config.uses_packed_kv:
+            if pack_code_span is None:
+                raise RuntimeError("packed KV decoding has no code capture callback")
+            if block.code_span is None:
+                raise RuntimeError("packed KV block has no completed code span")
+            cs, ce = block.code_span
+            pack_code_span(request.request_id, cs, ce)
+            if pos and pos != list(range(pos[0], pos[-1] + 1)):
+                raise RuntimeError("packed KV response content must be contiguous")
+            if pos and pos[-1] + 1 != cs:
+                raise RuntimeError("packed KV response content and code span are not contiguous")
+            self._mask_or_raise(mask_span, request.request_id, pos[0] if pos else cs, ce)
+            state.compacted_block_ids.add(block.block_id)
+            return
         if pos:
             if pos != list(range(pos[0], pos[-1] + 1)):
                 raise RuntimeError("CompressLM response content must be contiguous")

@@ -128,6 +128,59 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
                             abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * Per-head packed code pages (the reference's packed KV sidecar for per-head quota schedules:
+ * third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:12-155 PackedKVLayout, :214-284 PackedKVSidecar
+ * capture, :564-616 batched decode consumer, :648-741 per-request consumer). A packed page holds one closed block's
+ * code rows of one layer as [2 (K,V)][rows][128] bf16, KV head h's first q_h code rows at rows off_h .. off_h+q_h-1,
+ * off_h = q_0 + ... + q_{h-1}, rows = the sum of the layer's 8 head quotas (each in [1, 2048]). A layer's pool is
+ * [pool_pages, 2, rows, 128]; a sequence lists its packed page ids (one per captured block, the same id in every
+ * layer) in packed_table [num_seqs, packed_table_stride] with packed_count [num_seqs] entries (device int32).
+ *
+ * abkv_packed_capture: for capture c and layer l, copy the K_max code rows at physical positions code_start[c] ..
+ * (block_table row c) of layer_kv[l] into page dst_page[c] of layer_pool[l]. layer_kv / layer_pool: device arrays of
+ * num_layers device pointers; layer_rows [num_layers], layer_quota [num_layers, 8]: device int32.
+ *
+ * abkv_decode_attn_packed: decode attention over the paged rows [0, seq_len) (as abkv_decode_attn) plus, for KV
+ * head h, the sequence's side rows (q_h rows of each of its packed pages). head_quota: HOST int32 [8] (this layer's
+ * quotas; packed_rows must equal their sum). side_split_rows: abkv_decode_side_split_rows(min quota).
+ * max_packed_per_seq * max quota < 2^21. workspace >= abkv_decode_packed_workspace_size(...) bytes (always needed).
+ *
+ * abkv_paged_prefill_attn_packed: as abkv_paged_prefill_attn (always split: num_splits >= 1 ranges of split_tiles
+ * paged tiles) plus the side rows, visible to every query of the request, in side_splits ranges of side_split_tiles
+ * 64-row tiles (side_splits * side_split_tiles * 64 >= max_packed_per_seq * max quota); a non-causal request (code
+ * step) sees paged keys < min(kv_limit, kv_start + q_h) for KV head h (head_quota_dev: device int32 [8], the same
+ * quotas as the host head_quota). max_packed_per_seq <= 2048. workspace >=
+ * abkv_paged_prefill_workspace_size(num_tokens, num_splits + side_splits).
+ * ------------------------------------------------------------------------------------------------------------- */
+int abkv_packed_capture(const void* const* layer_kv, void* const* layer_pool, const int32_t* layer_rows,
+                        const int32_t* layer_quota, int num_layers, int num_pages, int pool_pages,
+                        const int32_t* block_table, long block_table_stride, int block_table_width,
+                        const int32_t* code_start, const int32_t* dst_page, int num_captures, abkv_stream_t stream);
+int abkv_decode_side_split_rows(int q_min);
+size_t abkv_decode_packed_workspace_size(int num_seqs, int max_pages_per_seq, int split_pages, int max_side_pages,
+                                         int side_q_max, int side_split_rows);
+int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache, int num_pages,
+                            const int32_t* block_table, long block_table_stride, const int32_t* seq_lens,
+                            int num_seqs, int max_pages_per_seq, int split_pages, const void* packed_kv,
+                            int packed_pool_pages, int packed_rows, const int32_t* head_quota,
+                            const int32_t* packed_table, long packed_table_stride, const int32_t* packed_count,
+                            int max_packed_per_seq, int side_split_rows, float scale, void* out, long out_stride_seq,
+                            long out_stride_head, float* lse, void* workspace, size_t workspace_bytes,
+                            abkv_stream_t stream);
+int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache,
+                                   int num_pages, const int32_t* block_table, long block_table_stride,
+                                   int block_table_width, const int32_t* q_start, const int32_t* kv_start,
+                                   const int32_t* kv_limit, const int32_t* tile_req, const int32_t* tile_q0,
+                                   int num_tiles, const int32_t* causal, int causal_default,
+                                   const int32_t* head_quota_dev, const void* packed_kv, int packed_pool_pages,
+                                   int packed_rows, const int32_t* head_quota, const int32_t* packed_table,
+                                   long packed_table_stride, const int32_t* packed_count, int max_packed_per_seq,
+                                   float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
+                                   int num_tokens, int num_splits, int split_tiles, int side_splits,
+                                   int side_split_tiles, void* workspace, size_t workspace_bytes,
+                                   abkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * fp32 mode of the three attention paths (same semantics as the bf16 entry points above, fp32 q / K / V / out,
  * fp32 accumulation and accurate exp/log): the reference's PyTorch attention run in fp32
  * (abridgekv/gen_compress.py:359-360, 555; compresslm_packed_kv.py:608-613; compress_forward.py:695-727).
