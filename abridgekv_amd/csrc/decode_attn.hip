@@ -53,7 +53,6 @@ struct DecodeArgs {
   const int32_t* side_count; // [B] packed pages per sequence
   int side_max_pages;        // bound on side_count
   int side_split_rows;       // side rows per split and head (multiple of 32, <= 63 * min quota)
-  int side_qmax;
   int side_q[kHeadsKV], side_o[kHeadsKV];
 };
 
@@ -225,11 +224,12 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(DecodeArgs a) {
   }
 }
 
-// Side splits of sequence b (0 without side rows): its packed pages times the largest head quota, in split rows.
-__device__ __forceinline__ int side_splits(const DecodeArgs& a, int b) {
+// Side splits of sequence b for KV head h (0 without side rows): its packed pages times the head's quota, in split
+// rows.
+__device__ __forceinline__ int side_splits(const DecodeArgs& a, int b, int h) {
   if (a.side_count == nullptr) return 0;
   const int count = min(max(a.side_count[b], 0), a.side_max_pages);
-  return (count * a.side_qmax + a.side_split_rows - 1) / a.side_split_rows;
+  return (count * a.side_q[h] + a.side_split_rows - 1) / a.side_split_rows;
 }
 
 // Merge the split partials of every sequence with more than one split (main splits at slots [0, n_main), side splits
@@ -240,10 +240,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int seq_len = max(min(a.seq_lens[b], a.max_pages * kPage), 0);
   const int n_pages = (seq_len + kPage - 1) / kPage;
   const int n_main = max(1, (n_pages + a.split_pages - 1) / a.split_pages);
-  const int n_side = side_splits(a, b);
   if (!a.force_partials && n_main <= 1) return;
-  const int n_all = n_main + n_side;
   const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
+  const int n_side = side_splits(a, b, head / kGroup);
+  const int n_all = n_main + n_side;
   const int d0 = (threadIdx.x & 31) * 4;
   const float* pml = a.part_ml + ((long)b * a.part_stride * kHeadsQ + head) * 2;
   const float* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
@@ -276,15 +276,15 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 // Attention of each sequence's 32 query heads over its side rows (per-head packed code pages; the reference keeps
 // them as PackedKVSidecar pages, third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:242-270, and
-// attends them ahead of the paged rows, :564-616). Grid (side splits, B), wave = KV head h: its rows are
-// r = 0 .. count * q_h - 1, row r being row side_o[h] + r % q_h of packed page r / q_h of the sequence. A split
-// covers side_split_rows rows of every head (heads with fewer rows finish early and write an empty partial), 32 rows
-// per step with the decode kernel's operand layout; partials go to slot max_splits + split.
-__global__ __launch_bounds__(512) void decode_side_kernel(DecodeArgs a) {
-  const int b = blockIdx.y;
+// attends them ahead of the paged rows, :564-616). Grid (side split, KV head h, B), one wave per workgroup (heads
+// hold different row counts, so waves of one workgroup would idle): head h's rows are r = 0 .. count * q_h - 1, row
+// r being row side_o[h] + r % q_h of packed page r / q_h of the sequence. A split covers side_split_rows rows, 32
+// rows per step with the decode kernel's operand layout; partials go to slot max_splits + split.
+__global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
+  const int b = blockIdx.z;
   const int split = blockIdx.x;
-  if (split >= side_splits(a, b)) return;
-  const int kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kvh = blockIdx.y;
+  if (split >= side_splits(a, b, kvh)) return;
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15;
   const int j = lane >> 4;
@@ -545,12 +545,11 @@ int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head
   a.side_count = packed_count;
   a.side_max_pages = max_packed_per_seq;
   a.side_split_rows = side_split_rows;
-  a.side_qmax = qmax;
   hipLaunchKernelGGL(decode_attn_kernel, dim3(max_splits, num_seqs), dim3(512), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   if (side_max > 0) {
-    hipLaunchKernelGGL(decode_side_kernel, dim3(side_max, num_seqs), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL(decode_side_kernel, dim3(side_max, kHeadsKV, num_seqs), dim3(64), 0, stream, a);
     err = hipGetLastError();
     if (err != hipSuccess) return (int)err;
   }

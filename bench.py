@@ -49,7 +49,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=32)
-    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "compaction", "copy"],
+    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "compaction", "packed",
+                                           "copy"],
                     default="serving")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
@@ -305,6 +306,75 @@ def workloads_lengths(args):
     return workloads.saturated_decode_lengths(args.batch, seed=args.seed)
 
 
+PACKED_HEAD_QUOTAS = (32, 64, 96, 128, 128, 160, 192, 224)    # a per-head schedule with mean 128 of K = 256
+
+
+def bench_packed(args, torch):
+    """Decode with per-head packed code pages, one layer: B=256 sequences of 32K logical context (42 closed blocks of
+    512 content + 256 codes archived as packed pages with the per-head quotas above, 1024 rows per page), paged rows =
+    512-token raw prompt + open block U[1, 511]. Algorithmic bytes = paged rows x 4096 B + packed rows x 512 B (K+V of
+    one head) + q/out. Times abkv_decode_attn_packed (paged splits + side splits + merge)."""
+    import numpy as np
+
+    from abridgekv_amd import ops
+
+    B, blocks, prompt = args.batch, 42, 512
+    rng = np.random.default_rng(args.seed)
+    rows_paged = prompt + rng.integers(1, 512, size=B)
+    pages_per = -(-rows_paged // 16)
+    W = int(pages_per.max())
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    cache = torch.empty(ops.kv_cache_shape(B * W), dtype=torch.bfloat16, device=dev)
+    cache.normal_(generator=gen)
+    bt = torch.from_numpy(np.arange(B * W, dtype=np.int32).reshape(B, W)).to(dev)
+    seq_lens = torch.from_numpy(rows_paged.astype(np.int32)).to(dev)
+    rows = sum(PACKED_HEAD_QUOTAS)
+    pool = torch.empty((B * blocks, 2, rows, 128), dtype=torch.bfloat16, device=dev)
+    pool.normal_(generator=gen)
+    ptab = torch.from_numpy(rng.permutation(B * blocks).astype(np.int32).reshape(B, blocks)).to(dev)
+    pcount = torch.full((B,), blocks, dtype=torch.int32, device=dev)
+    q = torch.randn((B, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, 32), dtype=torch.float32, device=dev)
+    scale = ops.default_scale()
+    sr = ops.lib().abkv_decode_side_split_rows(min(PACKED_HEAD_QUOTAS))
+    need = ops.lib().abkv_decode_packed_workspace_size(B, W, args.split_pages, blocks, max(PACKED_HEAD_QUOTAS), sr)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+
+    def launch():
+        ops.decode_attention_packed(q, cache, bt, seq_lens, pool, PACKED_HEAD_QUOTAS, ptab, pcount, scale,
+                                    max_pages=W, max_packed=blocks, out=out, lse=lse, split_pages=args.split_pages,
+                                    workspace=ws)
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        launch()
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / args.steps
+    alg = int(rows_paged.sum()) * 4096 + B * blocks * rows * 512 + B * 2 * 32 * 128 * 2
+    gbps = alg / t / 1e9
+    return {
+        "metric": "packed per-head decode GB/s (one layer launch, B=256, 32K ctx); % HBM peak BW",
+        "value": gbps, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) paged rows, packed pages and queries from the seed",
+        "config": {"workload": f"packed per-head decode, B={B}, {blocks} packed pages per sequence, head quotas "
+                               f"{list(PACKED_HEAD_QUOTAS)} ({rows} rows per page), paged rows 512 + U[1,511]",
+                   "global_batch": B},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "decode_side_kernel + decode_attn_kernel + decode_merge_kernel",
+                     "alg_bytes_per_launch": alg, "avg_launch_us": t * 1e6},
+        "tokens_per_s_one_layer": B / t,
+    }
+
+
 def bench_copy(args, torch):
     """Calibration kernel for the traffic counters: a plain device copy of 4 GiB (reads 4 GiB, writes 4 GiB)."""
     n = 4 << 30
@@ -332,9 +402,9 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "prefill", "compaction", "copy"):
+    if args.workload in ("serving", "prefill", "compaction", "packed", "copy"):
         res = {"serving": bench_serving, "prefill": bench_prefill, "compaction": bench_compaction,
-               "copy": bench_copy}[args.workload](args, torch)
+               "packed": bench_packed, "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
