@@ -108,11 +108,11 @@ class CompressLMConfig:
         if K <= 0:
             raise ValueError("num_code_tokens must be positive")
         if self.code_positions != "bitrev":
-            raise ValueError("this build serves code_positions='bitrev' only")
+            raise ValueError("only code_positions='bitrev' is served")
         if (C & (C - 1)) or (K & (K - 1)):
             raise ValueError("code_positions=bitrev needs power-of-two block_size and num_code_tokens")
         if self.replay_tail or self.raw_tail or self.retain_tail_kv or self.code_exclude_replay_tail:
-            raise ValueError("this build serves no replay / raw / retained tails")
+            raise ValueError("replay / raw / retained tails are not served")
         if self.num_passes != 1:
             raise ValueError("CompressLM decoding supports num_passes=1 only")
         if self.pause_xattn != "full":
@@ -120,7 +120,7 @@ class CompressLMConfig:
         if not self.raw_prompt:
             raise ValueError("CompressLM decoding requires raw_prompt=True")
         if self.retain_full_history_layers:
-            raise ValueError("selective full history is not served by this build")
+            raise ValueError("selective full history is not served")
         for layer, q in enumerate(self.layer_code_quotas):
             if not 0 < q <= K:
                 raise ValueError(f"layer_code_quotas[{layer}]={q} must be in [1, {K}]")
