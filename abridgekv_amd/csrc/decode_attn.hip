@@ -249,20 +249,22 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const float* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
   // split k of the n_all: main split k, or side split k - n_main at slot max_splits + (k - n_main)
   auto slot = [&](int k) { return k < n_main ? k : a.max_splits + (k - n_main); };
-  // unrolled so the per-split loads of a thread are in flight together (the loop is latency-bound otherwise)
-  float M = -INFINITY;
-#pragma unroll 8
-  for (int k = 0; k < n_all; ++k) M = fmaxf(M, pml[(long)slot(k) * kHeadsQ * 2]);
-  float L = 0.f;
+  // One pass with a running max (the loads of a split -- m, l and the four dims -- are needed together), unrolled so
+  // that several splits' loads are in flight together: the loop is latency-bound.
+  float M = -INFINITY, L = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (M != -INFINITY) {
 #pragma unroll 8
-    for (int k = 0; k < n_all; ++k) {
-      const long s = slot(k);
-      const float w = fast_exp2(pml[s * kHeadsQ * 2] - M);
-      L += w * pml[s * kHeadsQ * 2 + 1];
-      acc += w * *reinterpret_cast<const floatx4*>(pob + s * kHeadsQ * kHeadDim);
-    }
+  for (int k = 0; k < n_all; ++k) {
+    const long s = slot(k);
+    const float m = pml[s * kHeadsQ * 2];
+    const float l = pml[s * kHeadsQ * 2 + 1];
+    const floatx4 v = *reinterpret_cast<const floatx4*>(pob + s * kHeadsQ * kHeadDim);
+    const float mn = fmaxf(M, m);
+    const float alpha = mn == -INFINITY ? 1.f : fast_exp2(M - mn);
+    const float w = mn == -INFINITY ? 0.f : fast_exp2(m - mn);
+    L = L * alpha + l * w;
+    acc = acc * alpha + v * w;
+    M = mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + d0;
