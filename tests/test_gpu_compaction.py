@@ -140,3 +140,50 @@ def test_staged_copy_handles_overlapping_chains():
     src = np.array(ops_l)
     expect[src[:, 2], :, src[:, 3]] = before[src[:, 0], :, src[:, 1]]
     assert np.array_equal(cache.view(torch.int16).cpu().numpy(), expect)
+
+
+def test_full_size_compaction_moves_every_row_exactly():
+    """The served geometry at full size (64 sequences close a 512-token block with 256 code rows, 6 quota groups): the
+    fused moves of one planner step, applied by the mover to a cache whose every 4-byte word carries its own address,
+    leave each destination row equal, word for word, to the row that gather-then-scatter per (request, group)
+    assigns it, and leave a sample of untouched rows unchanged."""
+    from abridgekv_amd import workloads
+    st = workloads.build_compaction_state(64, seed=0)
+    _, _, fused = st.compact(as_arrays=True)
+    fused = np.asarray(fused, np.int64)
+    P = st.num_pages
+    dev = torch.device("cuda")
+    words = 2 * 16 * 512                                          # int32 words per page ([2][16 slots][512])
+    assert P * words < 2 ** 31
+    tag = torch.arange(P * words, dtype=torch.int32, device=dev)
+    cache = tag.view(torch.bfloat16).view(ops.kv_cache_shape(P))   # every word holds its own linear index
+    worker.execute_fused_moves(fused, [[cache] for _ in st.groups])
+    torch.cuda.synchronize()
+    # expected origin of every written row: gather-then-scatter per (request, group) segment, in order
+    origin = {}
+    for (r, g), rows in _segments(fused):
+        srcs = [origin.get((int(a), int(b)), (int(a), int(b))) for a, b in rows[:, 2:4]]
+        for (dp, ds), src in zip(rows[:, 4:6], srcs):
+            origin[(int(dp), int(ds))] = src
+    dst = np.array(list(origin.keys()), np.int64)
+    src = np.array([origin[k] for k in origin], np.int64)
+    got = tag.view(P, 2, 16, 512)[torch.from_numpy(dst[:, 0]).to(dev), :, torch.from_numpy(dst[:, 1]).to(dev)]
+    half = np.arange(2)[None, :, None]
+    word = np.arange(512)[None, None, :]
+    want = ((src[:, 0, None, None] * 2 + half) * 16 + src[:, 1, None, None]) * 512 + word
+    assert np.array_equal(got.cpu().numpy(), want)
+    rng = np.random.default_rng(1)
+    written = set(origin)
+    sample = [(int(p), int(s)) for p, s in zip(rng.integers(0, P, 4000), rng.integers(0, 16, 4000))
+              if (int(p), int(s)) not in written]
+    sp = np.array(sample, np.int64)
+    got = tag.view(P, 2, 16, 512)[torch.from_numpy(sp[:, 0]).to(dev), :, torch.from_numpy(sp[:, 1]).to(dev)]
+    want = ((sp[:, 0, None, None] * 2 + half) * 16 + sp[:, 1, None, None]) * 512 + word
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+def _segments(fused):
+    """(request, group) runs of a planner step's fused move rows, in order."""
+    cut = np.flatnonzero(np.any(np.diff(fused[:, :2], axis=0) != 0, axis=1)) + 1
+    for rows in np.split(fused, cut):
+        yield (int(rows[0, 0]), int(rows[0, 1])), rows
