@@ -16,8 +16,13 @@ every layer's rows live in paged caches, quotas are physical, and the block boun
   ``_finish_block`` order of processor.py:467-557) and moves the surviving rows with the HIP mover.
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
-the serving worker shares them (kv_cache_utils.py:1110-1127). Per-head (non-uniform within a layer) quotas would
-need ragged per-head pages and raise NotImplementedError.
+the serving worker shares them (kv_cache_utils.py:1110-1127).
+
+Per-head quotas (a layer whose KV heads keep different numbers of codes) use the per-head packed pages of the
+serving sidecar (compresslm_packed_kv.py): one KV-cache group; the code step hides paged code rows ``>= q_h`` per KV
+head (``abkv_paged_prefill_attn_packed``); ``compress`` then copies the block's code rows into one packed page per
+layer (``abkv_packed_capture``) and removes the response content and all K codes as one span; content steps attend
+over the packed pages plus the paged rows (``abkv_decode_attn_packed`` / ``abkv_paged_prefill_attn_packed``).
 """
 from __future__ import annotations
 
@@ -28,6 +33,7 @@ import torch.nn.functional as F
 from . import backend as bk
 from . import ops
 from .config import bitrev_offsets
+from .packed_kv import PackedKVLayout, PackedKVSidecar
 from .planner import KVPlanner
 from .worker import execute_fused_moves
 
@@ -45,9 +51,15 @@ def _layer_quotas(head_code_quotas, num_layers, num_kv_heads, K):
         raise ValueError(f"head_code_quotas must have shape [{num_layers}, {num_kv_heads}], got {tuple(q.shape)}")
     if bool(((q <= 0) | (q > K)).any()):
         raise ValueError(f"head_code_quotas must be in [1, {K}]")
-    if bool((q != q[:, :1]).any()):
-        raise NotImplementedError("per-head code quotas within a layer need per-head pages; rows must be uniform")
     return [int(x) for x in q[:, 0]]
+
+
+def _per_head(head_code_quotas) -> bool:
+    """Whether some layer's KV heads have different quotas (served through per-head packed pages)."""
+    if head_code_quotas is None:
+        return False
+    q = torch.as_tensor(head_code_quotas, dtype=torch.long)
+    return bool((q != q[:, :1]).any())
 
 
 class CompressGen:
@@ -85,6 +97,12 @@ class CompressGen:
         cfg = clm.model.config
         self.quotas = _layer_quotas(head_code_quotas, self.num_layers, int(cfg.num_key_value_heads), self.K)
         self.head_code_quotas = None if head_code_quotas is None else torch.as_tensor(head_code_quotas)
+        # Per-head quotas (rows not uniform): closed blocks' code rows move to per-head packed pages and leave the
+        # paged cache with the summarised content (one KV-cache group, every layer its own tensor); per-layer quotas:
+        # one group per distinct quota, code rows >= quota removed from the group's layout.
+        self.packed = _per_head(head_code_quotas)
+        if self.packed:
+            self.quotas = [self.K] * self.num_layers
 
         # KV-cache groups: layers of equal quota, in order of first appearance; tensor i = i-th layer of each group
         distinct = list(dict.fromkeys(self.quotas))
@@ -104,6 +122,13 @@ class CompressGen:
         self.planner.add_request(self.rid)
         self.impl = bk.AbridgeAttentionImpl(scale=getattr(self.layers[0].self_attn, "scaling", None))
         self.builder = bk.AbridgeMetadataBuilder(max_num_seqs=1, max_pages=pages_per_group, device=self.device)
+        self.sidecar = None
+        if self.packed:
+            layout = PackedKVLayout.from_schedule(self.head_code_quotas.tolist(), num_layers=self.num_layers,
+                                                  num_kv_heads=int(cfg.num_key_value_heads), k_max=self.K)
+            blocks = int(max_tokens) // self.C + 2
+            self.sidecar = PackedKVSidecar(layout, self.caches_by_group[0], pool_pages=blocks,
+                                           max_pages_per_request=min(blocks, 2048), device=self.device)
         self.b = 0                      # current block index
         self.f = 0                      # content tokens committed in the current block
         self.logical_len = 0            # tokens in the planner's logical sequence (content + code rows)
@@ -169,7 +194,13 @@ class CompressGen:
             v = attn.v_proj(normed).view(n, -1, attn.head_dim).contiguous()
             ops.rope_kv_append(q, k, v, positions, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache)
             o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
-            self.impl.attend(q, cache, md, o)
+            if self.sidecar is not None:
+                # paged rows + this layer's per-head packed pages; a code step's paged keys stop at the block's
+                # first q_h code rows for KV head h
+                self.sidecar.attend(li, q, cache, md.block_table, md.query_start_loc, md.seq_lens, not code_step, o,
+                                    request_ids=(self.rid,), seq_lens_dev=md.seq_lens_dev, scale=self.impl.scale)
+            else:
+                self.impl.attend(q, cache, md, o)
             h = hidden + attn.o_proj(o.view(1, n, -1))
             hidden = h + layer.mlp(layer.post_attention_layernorm(h))
         self.logical_len += n
@@ -199,10 +230,19 @@ class CompressGen:
         block_start = code_start - C
         resp_from = block_start + min(max(self.raw_prompt_len - self.b * C, 0), C)
         calls = []
-        if resp_from < code_start:
-            calls.append((resp_from, code_start, None))
-        for q in sorted({q for q in self.group_quotas if q < K}):
-            calls.append((code_start + q, code_start + K, [g for g, gq in enumerate(self.group_quotas) if gq == q]))
+        if self.sidecar is not None:
+            # archive the code rows into packed pages, then remove the response content and the codes as one span
+            # (compresslm/processor.py:484-520)
+            phys = code_start - self.planner.compacted_counts(self.rid)[0]
+            table = self.planner.get_blocks(self.rid)[0]
+            self.sidecar.capture(self.rid, physical_start=phys, physical_end=phys + K, block_ids=table)
+            calls.append((resp_from, code_start + K, None))
+        else:
+            if resp_from < code_start:
+                calls.append((resp_from, code_start, None))
+            for q in sorted({q for q in self.group_quotas if q < K}):
+                calls.append((code_start + q, code_start + K,
+                              [g for g, gq in enumerate(self.group_quotas) if gq == q]))
         for start, end, groups in calls:
             res = self.planner.mask_token_span(self.rid, start, end, groups)
             if not res.success:
@@ -247,15 +287,25 @@ class CompressGen:
         return out
 
     def resident_rows(self) -> list[int]:
-        """Physical rows held per layer (its group's length)."""
+        """Paged rows held per layer (its group's length)."""
         comp = self.planner.compacted_counts(self.rid)
         return [self.logical_len - comp[g] for g in self.group_of]
+
+    def packed_rows(self) -> list[int]:
+        """Rows held per layer in per-head packed pages (summed over the KV heads, so a row here is one head's
+        K/V; zero without per-head quotas)."""
+        if self.sidecar is None:
+            return [0] * self.num_layers
+        n = len(self.sidecar.request_pages(self.rid))
+        return [n * r for r in self.sidecar.layout.packed_slots_per_layer]
 
     def cache_kv_stats(self):
         main = self.resident_rows()
         total = sum(main)
+        elements = total * 2 * ops.HEADS_KV * ops.HEAD_DIM + sum(self.packed_rows()) * 2 * ops.HEAD_DIM
         return {"main_columns_by_layer": main, "history_columns_by_layer": [0] * self.num_layers,
-                "total_columns": total, "total_kv_elements": total * 2 * ops.HEADS_KV * ops.HEAD_DIM}
+                "packed_head_rows_by_layer": self.packed_rows(), "total_columns": total,
+                "total_kv_elements": elements}
 
 
 def sample(logits, temperature, top_p, top_k, gen):

@@ -17,10 +17,13 @@ pytestmark = pytest.mark.gpu
 transformers = pytest.importorskip("transformers")
 
 CASES = [
-    # C, N, K, code positions, prompt lengths, per-layer quota (None: all K), token-by-token sequences
+    # C, N, K, code positions, prompt lengths, quota per layer (an int, or 8 per KV head; None: all K),
+    # token-by-token sequences
     (64, 4, 16, "bitrev", [40, 100], [16, 4], [1]),
     (32, 3, 8, "appended", None, None, [0]),
     (64, 3, 32, "bitrev", [64, 0], [8, 32], [0, 1]),
+    # per-head quotas: closed blocks' codes live in per-head packed pages
+    (64, 3, 16, "bitrev", [40, 70], [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], [1]),
 ]
 
 
@@ -40,15 +43,17 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
     from abridgekv_amd.gen_compress import CompressGen
 
     C, N, K, code_positions, prompt, quota, stepwise = CASES[case]
+    hcq = None if quota is None else [list(q) if isinstance(q, list) else [q] * 8 for q in quota]
+    per_head = hcq is not None and any(len(set(row)) > 1 for row in hcq)
     base = _model(case)
     dev = torch.device("cuda")
     clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=code_positions,
-                     head_code_quotas=None if quota is None else [[q] * 8 for q in quota]).eval()
+                     head_code_quotas=hcq).eval()
     torch.manual_seed(100 + case)
     with torch.no_grad():
         clm.pause.normal_(0, 0.05)
     ids = torch.randint(0, 257, (2, N, C))
-    lhq = None if quota is None else np.repeat(np.asarray(quota)[:, None], 32, axis=1)
+    lhq = None if hcq is None else np.repeat(np.asarray(hcq), 4, axis=1)
     pause = clm.pause.detach().cpu()
 
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
@@ -65,8 +70,7 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
     rows_per_seq = N * (C - 1)
     for bi in range(2):
         p = 0 if prompt is None else prompt[bi]
-        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=None if quota is None else [[q] * 8 for q in quota],
-                        max_tokens=N * (C + K) + 16)
+        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=hcq, max_tokens=N * (C + K) + 16)
         got = []
         for blk in range(N):
             toks = ids[bi, blk].tolist()
@@ -77,8 +81,11 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
             got.append(clm.model.lm_head(hs).float()[: C - 1].double().cpu())
             g.compress()
             kept_prompt = min(p, (blk + 1) * C)
-            assert g.resident_rows() == [kept_prompt + (blk + 1) * (K if quota is None else q)
-                                         for q in (quota or [K, K])]
+            if per_head:
+                assert g.resident_rows() == [kept_prompt] * 2
+                assert g.packed_rows() == [(blk + 1) * sum(row) for row in hcq]
+            else:
+                assert g.resident_rows() == [kept_prompt + (blk + 1) * row[0] for row in (hcq or [[K], [K]])]
         err = (torch.cat(got) - ref[bi * rows_per_seq: (bi + 1) * rows_per_seq]).abs().max().item()
         print(f"case {case} seq {bi}: generator {err:.3e}")
         assert err <= tol
