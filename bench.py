@@ -41,6 +41,19 @@ def profiled_traffic(name: str):
     return None
 
 
+def profiled_mfma_util(name: str):
+    """rocprofv3 MfmaUtil of a kernel on this workload (fraction of SIMD cycles the matrix cores are busy), from the
+    committed PMC summary profiles/<name>; None if absent."""
+    try:
+        with open(os.path.join(PROFILES, name)) as f:
+            for line in f:
+                if line.startswith("mfma_util_rocprof:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,7 +166,9 @@ def bench_prefill(args, torch):
                      "frac": tflops / 2500.0,
                      "traffic": profiled_traffic("prefill_masked_b4_s10240_pmc_traffic.md"),
                      "traffic_source": "profiles/prefill_masked_b4_s10240_pmc_traffic.md", "kernel": "prefill_masked_kernel",
-                     "alg_flops_per_launch": flops, "avg_launch_us": t * 1e6},
+                     "alg_flops_per_launch": flops, "avg_launch_us": t * 1e6,
+                     "mfma_util_rocprof": profiled_mfma_util("prefill_masked_b4_s10240_pmc_mfma.md"),
+                     "mfma_util_source": "profiles/prefill_masked_b4_s10240_pmc_mfma.md (MfmaUtil)"},
     }
 
 
