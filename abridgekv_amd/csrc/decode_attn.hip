@@ -20,7 +20,8 @@
 // picked so that the S^T accumulator registers of a lane are exactly its P^T operand (no cross-lane movement).
 //
 // Output: normalised bf16 out [B, 32, 128] and natural-log LSE [B, 32] directly when a sequence has one split;
-// otherwise un-normalised fp32 partials (o, m, l) per split and a merge kernel.
+// otherwise per split a normalised fp16 partial output with an fp32 record (m, l, scale), and a merge kernel (fp16
+// partials move half the bytes of fp32 ones: 2.1 % of the saturated launch time).
 #include "common.h"
 
 namespace abkv {
@@ -40,8 +41,8 @@ struct DecodeArgs {
   __bf16* out;               // [B, 32, 128] (strides o_sb, o_sh)
   long o_sb, o_sh;
   float* lse;                // [B, 32] or nullptr
-  float* part_o;             // [B, part_stride, 32, 128] fp32
-  float* part_ml;            // [B, part_stride, 32, 2] fp32 (m in log2 units, l)
+  _Float16* part_o;          // [B, part_stride, 32, 128] fp16: split output / (l * scale)
+  float* part_ml;            // [B, part_stride, 32, 4] fp32: m (log2 units), l, scale, unused
   int part_stride;           // split slots per sequence in the partial buffers (max_splits, + side splits)
   int force_partials;        // write partials even for one split (the side rows are merged in afterwards)
   // Side rows (per-head packed code pages; unused when side_count is null): packed page p of a sequence holds, for
@@ -59,6 +60,43 @@ struct DecodeArgs {
 
 __device__ __forceinline__ u32x4 ld16(const __bf16* p) {
   return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const _Float16 x = (_Float16)lo, y = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+
+// Largest |o| over the 128 dims of this lane's column (the lane groups j hold dims 32j .. 32j + 31).
+__device__ __forceinline__ float column_absmax(const floatx4 (&o)[8]) {
+  float x = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x = fmaxf(x, fabsf(o[i][r]));
+  return max_xor32(max_xor16(x));
+}
+
+// Split partial of one query head: the split's output normalised by its weight sum l, stored in fp16 (11-bit
+// mantissa, half the bytes of fp32), divided by a scale that keeps every value within +-32768 (1 unless the split's
+// V rows exceed that), and the record (m, l, scale). o[i][r] = un-normalised out[dim 32j + 8r + i]; amax =
+// column_absmax(o).
+__device__ __forceinline__ void store_partial(const DecodeArgs& a, long slot, int head, int j, const floatx4 (&o)[8],
+                                              float amax, float m_run, float l_tot) {
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float an = amax * inv;
+  const float scale = an > 32768.f ? an * (1.f / 32768.f) : 1.f;
+  const float f = inv / scale;
+  _Float16* po = a.part_o + (slot * kHeadsQ + head) * kHeadDim + 32 * j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    u32x4 w;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = pack_f16x2(o[2 * c][r] * f, o[2 * c + 1][r] * f);
+    *reinterpret_cast<u32x4*>(po + 8 * r) = w;
+  }
+  if (j == 0)
+    *reinterpret_cast<floatx4*>(a.part_ml + (slot * kHeadsQ + head) * 4) = floatx4{m_run, l_tot, scale, 0.f};
 }
 
 template <int kW>
@@ -197,9 +235,11 @@ __global__ __launch_bounds__(64 * kW) void decode_attn_kernel(DecodeArgs a) {
 
   // o[i][r] = un-normalised out[head m16][dim 32j + 8r + i]; l_run partial over this lane's slots.
   const float l_tot = sum_xor32(sum_xor16(l_run));
+  const bool partial = n_splits > 1 || a.force_partials;
+  const float amax = partial ? column_absmax(o) : 0.f;    // (a uniform branch: all lanes take part in the shuffles)
   if (m16 >= kGroup) return;
   const int head = kvh * kGroup + m16;
-  if (n_splits == 1 && !a.force_partials) {
+  if (!partial) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + 32 * j;
 #pragma unroll
@@ -212,19 +252,7 @@ __global__ __launch_bounds__(64 * kW) void decode_attn_kernel(DecodeArgs a) {
     if (a.lse != nullptr && j == 0)
       a.lse[(long)b * kHeadsQ + head] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
   } else {
-    float* po = a.part_o + (((long)b * a.part_stride + split) * kHeadsQ + head) * kHeadDim + 32 * j;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      floatx4 w0 = {o[0][r], o[1][r], o[2][r], o[3][r]};
-      floatx4 w1 = {o[4][r], o[5][r], o[6][r], o[7][r]};
-      *reinterpret_cast<floatx4*>(po + 8 * r) = w0;
-      *reinterpret_cast<floatx4*>(po + 8 * r + 4) = w1;
-    }
-    if (j == 0) {
-      float* pml = a.part_ml + (((long)b * a.part_stride + split) * kHeadsQ + head) * 2;
-      pml[0] = m_run;
-      pml[1] = l_tot;
-    }
+    store_partial(a, (long)b * a.part_stride + split, head, j, o, amax, m_run, l_tot);
   }
 }
 
@@ -249,8 +277,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int n_side = side_splits(a, b, head / kGroup);
   const int n_all = n_main + n_side;
   const int d0 = (threadIdx.x & 31) * 4;
-  const float* pml = a.part_ml + ((long)b * a.part_stride * kHeadsQ + head) * 2;
-  const float* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
+  const float* pml = a.part_ml + ((long)b * a.part_stride * kHeadsQ + head) * 4;
+  const _Float16* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
   // split k of the n_all: main split k, or side split k - n_main at slot max_splits + (k - n_main)
   auto slot = [&](int k) { return k < n_main ? k : a.max_splits + (k - n_main); };
   // One pass with a running max (the loads of a split -- m, l and the four dims -- are needed together), unrolled so
@@ -259,15 +287,16 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
   for (int k = 0; k < n_all; ++k) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
     const long s = slot(k);
-    const float m = pml[s * kHeadsQ * 2];
-    const float l = pml[s * kHeadsQ * 2 + 1];
-    const floatx4 v = *reinterpret_cast<const floatx4*>(pob + s * kHeadsQ * kHeadDim);
-    const float mn = fmaxf(M, m);
+    const floatx4 rec = *reinterpret_cast<const floatx4*>(pml + s * kHeadsQ * 4);     // m, l, scale
+    const f16x4 h = *reinterpret_cast<const f16x4*>(pob + s * kHeadsQ * kHeadDim);
+    const floatx4 v = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    const float mn = fmaxf(M, rec[0]);
     const float alpha = mn == -INFINITY ? 1.f : fast_exp2(M - mn);
-    const float w = mn == -INFINITY ? 0.f : fast_exp2(m - mn);
-    L = L * alpha + l * w;
-    acc = acc * alpha + v * w;
+    const float w = mn == -INFINITY ? 0.f : fast_exp2(rec[0] - mn) * rec[1];    // the split's weight
+    L = L * alpha + w;
+    acc = acc * alpha + v * (w * rec[2]);
     M = mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -396,20 +425,9 @@ __global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
   }
 
   const float l_tot = sum_xor32(sum_xor16(l_run));
+  const float amax = column_absmax(o);
   if (m16 >= kGroup) return;
-  const int head = kvh * kGroup + m16;
-  const long slot = (long)b * a.part_stride + a.max_splits + split;
-  float* po = a.part_o + (slot * kHeadsQ + head) * kHeadDim + 32 * j;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    *reinterpret_cast<floatx4*>(po + 8 * r) = floatx4{o[0][r], o[1][r], o[2][r], o[3][r]};
-    *reinterpret_cast<floatx4*>(po + 8 * r + 4) = floatx4{o[4][r], o[5][r], o[6][r], o[7][r]};
-  }
-  if (j == 0) {
-    float* pml = a.part_ml + (slot * kHeadsQ + head) * 2;
-    pml[0] = m_run;
-    pml[1] = l_tot;
-  }
+  store_partial(a, (long)b * a.part_stride + a.max_splits + split, kvh * kGroup + m16, j, o, amax, m_run, l_tot);
 }
 
 // Four waves (KV heads 0-3 or 4-7) per workgroup: the two workgroups of a split are adjacent in dispatch order. Four
@@ -427,7 +445,7 @@ extern "C" {
 
 // Workspace bytes needed by abkv_decode_attn for `num_seqs` sequences and `max_splits` splits per sequence.
 size_t abkv_decode_workspace_size(int num_seqs, int max_splits) {
-  const size_t per = (size_t)abkv::kHeadsQ * (abkv::kHeadDim + 2) * sizeof(float);
+  const size_t per = (size_t)abkv::kHeadsQ * (abkv::kHeadDim * sizeof(_Float16) + 4 * sizeof(float));
   return (size_t)num_seqs * (size_t)max_splits * per;
 }
 
@@ -463,8 +481,8 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
   a.o_sb = out_stride_seq;
   a.o_sh = out_stride_head;
   a.lse = lse;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + (size_t)num_seqs * max_splits * kHeadsQ * kHeadDim;
+  a.part_o = static_cast<_Float16*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(a.part_o + (size_t)num_seqs * max_splits * kHeadsQ * kHeadDim);
   a.part_stride = max_splits;
   a.force_partials = 0;
   a.side_count = nullptr;
@@ -548,8 +566,8 @@ int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head
   a.o_sb = out_stride_seq;
   a.o_sh = out_stride_head;
   a.lse = lse;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + (size_t)num_seqs * stride * kHeadsQ * kHeadDim;
+  a.part_o = static_cast<_Float16*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(a.part_o + (size_t)num_seqs * stride * kHeadsQ * kHeadDim);
   a.part_stride = stride;
   a.force_partials = 1;
   a.side_kv = static_cast<const __bf16*>(packed_kv);

@@ -31,7 +31,8 @@ typedef struct ihipStream_t* abkv_stream_t; /* == hipStream_t */
  * fp32 natural log (may be NULL). num_pages: pages in kv_cache (page ids are clamped into range).
  * split_pages: even number of pages per split, at most 64. max_pages_per_seq (<= block_table_stride) bounds ceil(seq_len/16);
  * longer sequences are truncated to max_pages_per_seq * 16 rows. workspace: >= abkv_decode_workspace_size(num_seqs, ceil(max_pages/split_pages))
- * bytes when a sequence can need more than one split (may be NULL otherwise).
+ * bytes when a sequence can need more than one split (may be NULL otherwise); it holds each split's normalised
+ * output in fp16 and an fp32 (m, l, scale) record per query head.
  * ------------------------------------------------------------------------------------------------------------- */
 size_t abkv_decode_workspace_size(int num_seqs, int max_splits);
 int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache, int num_pages,

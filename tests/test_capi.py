@@ -39,7 +39,8 @@ def test_binding_table_matches_header():
 
 def test_host_only_entry_points_run_without_gpu():
     lib = _lib.lib()
-    assert lib.abkv_decode_workspace_size(256, 24) == 256 * 24 * 32 * 130 * 4
+    # per (sequence, split, query head): 128 fp16 partial values + an fp32 record (m, l, scale, unused)
+    assert lib.abkv_decode_workspace_size(256, 24) == 256 * 24 * 32 * (128 * 2 + 4 * 4)
     assert lib.abkv_kv_stage_bytes(6, 100, 2048) == 6 * 100 * 4096
     h = lib.abkv_planner_create(8, 2, 4, None, 0)
     assert h

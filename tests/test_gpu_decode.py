@@ -115,6 +115,26 @@ def test_peaked_scores_and_large_magnitudes():
     assert np.abs(lse - ref_lse).max() <= TOL * 4
 
 
+def test_values_beyond_fp16_range_in_split_partials():
+    """Split partials are stored in fp16 divided by a per-(split, head) scale; V rows of magnitude ~1e6 (beyond fp16's
+    65504, representable in bf16) must come out finite and as accurate, relative to that magnitude, as unit rows."""
+    rng = np.random.default_rng(11)
+    lens = [1500, 700, 64]
+    big = 1.0e6
+    ks = [rng.standard_normal((n, 8, 128)) for n in lens]
+    vs = [rng.standard_normal((n, 8, 128)) * big for n in lens]
+    vs[1][:, :4] /= big                         # KV heads 0-3 of the second sequence stay at unit scale
+    q = rng.standard_normal((3, 32, 128)).astype(np.float32)
+    cache, tables, sl = _paged_cache(ks, vs, 300, rng)
+    out, lse = _run(q, cache, tables, sl, split_pages=4)
+    ref_out, ref_lse = _oracle(q, cache, tables, sl)
+    assert np.isfinite(out).all()
+    err = np.abs(out - ref_out)
+    assert err[1, :16].max() <= TOL                       # the unit-scale heads (query heads 0-15)
+    assert err.max() <= TOL * big
+    assert np.abs(lse - ref_lse).max() <= TOL
+
+
 def test_zero_length_sequence_writes_zeros():
     rng = np.random.default_rng(2)
     ks = [rng.standard_normal((n, 8, 128)) for n in (0, 20)]
