@@ -23,7 +23,7 @@ CASES = [
     (32, 3, 8, "appended", None, None, [0]),
     (64, 3, 32, "bitrev", [64, 0], [8, 32], [0, 1]),
     # per-head quotas: closed blocks' codes live in per-head packed pages
-    (64, 3, 16, "bitrev", [40, 70], [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], [1]),
+    (64, 3, 16, "bitrev", [40, 100], [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], [1]),
 ]
 
 
