@@ -264,49 +264,96 @@ __device__ __forceinline__ int side_splits(const DecodeArgs& a, int b, int h) {
   return (count * a.side_q[h] + a.side_split_rows - 1) / a.side_split_rows;
 }
 
+// The two values of v held by lanes l and l ^ 16 (resp. l ^ 32), in an order fixed by the lane (the same for every
+// call, so pairing several variables through these keeps them matched).
+__device__ __forceinline__ void pair_xor16(float v, float& x, float& y) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair_xor32(float v, float& x, float& y) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
+
+// Online-softmax state of a merge lane: running max M (log2 units), weight sum L, weighted output dims acc.
+struct MergeState {
+  float M, L, acc[8];
+};
+
+// Combine the states of lane pairs {l, l ^ 16} (kXor32 = false) or {l, l ^ 32}: symmetric in the two states.
+template <bool kXor32>
+__device__ __forceinline__ void merge_pair(MergeState& st) {
+  auto pair = [](float v, float& x, float& y) {
+    if constexpr (kXor32) pair_xor32(v, x, y);
+    else pair_xor16(v, x, y);
+  };
+  float mx, my, lx, ly;
+  pair(st.M, mx, my);
+  pair(st.L, lx, ly);
+  const float mn = fmaxf(mx, my);
+  const float ax = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+  const float ay = my == -INFINITY ? 0.f : fast_exp2(my - mn);
+  st.M = mn;
+  st.L = lx * ax + ly * ay;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float x, y;
+    pair(st.acc[i], x, y);
+    st.acc[i] = x * ax + y * ay;
+  }
+}
+
 // Merge the split partials of every sequence with more than one split (main splits at slots [0, n_main), side splits
-// at [max_splits, max_splits + n_side)). Workgroup (sequence, group of 8 heads); thread t handles head
-// 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
+// at [max_splits, max_splits + n_side)). Workgroup (sequence, group of 4 heads), one wave per head; the wave's four
+// 16-lane groups g take the splits k = g, g + 4, ... (lane c of a group: dims 8c .. 8c + 7, one 16-byte load per
+// split), each keeping a running max, and the four states are combined with two cross-lane swaps.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int b = blockIdx.x;
   const int seq_len = max(min(a.seq_lens[b], a.max_pages * kPage), 0);
   const int n_pages = (seq_len + kPage - 1) / kPage;
   const int n_main = max(1, (n_pages + a.split_pages - 1) / a.split_pages);
   if (!a.force_partials && n_main <= 1) return;
-  const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
+  const int head = 4 * blockIdx.y + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
   const int n_side = side_splits(a, b, head / kGroup);
   const int n_all = n_main + n_side;
-  const int d0 = (threadIdx.x & 31) * 4;
   const float* pml = a.part_ml + ((long)b * a.part_stride * kHeadsQ + head) * 4;
-  const _Float16* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + d0;
+  const _Float16* pob = a.part_o + ((long)b * a.part_stride * kHeadsQ + head) * kHeadDim + 8 * c;
   // split k of the n_all: main split k, or side split k - n_main at slot max_splits + (k - n_main)
   auto slot = [&](int k) { return k < n_main ? k : a.max_splits + (k - n_main); };
-  // One pass with a running max (the loads of a split -- m, l and the four dims -- are needed together), unrolled so
-  // that several splits' loads are in flight together: the loop is latency-bound.
-  float M = -INFINITY, L = 0.f;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-  for (int k = 0; k < n_all; ++k) {
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  MergeState st;
+  st.M = -INFINITY;
+  st.L = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.acc[i] = 0.f;
+#pragma unroll 4
+  for (int k = g; k < n_all; k += 4) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
     const long s = slot(k);
     const floatx4 rec = *reinterpret_cast<const floatx4*>(pml + s * kHeadsQ * 4);     // m, l, scale
-    const f16x4 h = *reinterpret_cast<const f16x4*>(pob + s * kHeadsQ * kHeadDim);
-    const floatx4 v = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-    const float mn = fmaxf(M, rec[0]);
-    const float alpha = mn == -INFINITY ? 1.f : fast_exp2(M - mn);
+    const f16x8 h = *reinterpret_cast<const f16x8*>(pob + s * kHeadsQ * kHeadDim);
+    const float mn = fmaxf(st.M, rec[0]);
+    const float alpha = mn == -INFINITY ? 1.f : fast_exp2(st.M - mn);
     const float w = mn == -INFINITY ? 0.f : fast_exp2(rec[0] - mn) * rec[1];    // the split's weight
-    L = L * alpha + w;
-    acc = acc * alpha + v * (w * rec[2]);
-    M = mn;
+    const float ws = w * rec[2];
+    st.L = st.L * alpha + w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * alpha + (float)h[i] * ws;
+    st.M = mn;
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  __bf16* oh = a.out + (long)b * a.o_sb + (long)head * a.o_sh + d0;
-  u32x2 wv;
-  wv[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-  wv[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<u32x2*>(oh) = wv;
-  if (a.lse != nullptr && (threadIdx.x & 31) == 0)
-    a.lse[(long)b * kHeadsQ + head] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : -INFINITY;
+  merge_pair<false>(st);
+  merge_pair<true>(st);
+  if (g != 0) return;
+  const float inv = st.L > 0.f ? 1.f / st.L : 0.f;
+  u32x4 wv;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wv[i] = pack_bf16x2(st.acc[2 * i] * inv, st.acc[2 * i + 1] * inv);
+  *reinterpret_cast<u32x4*>(a.out + (long)b * a.o_sb + (long)head * a.o_sh + 8 * c) = wv;
+  if (a.lse != nullptr && c == 0)
+    a.lse[(long)b * kHeadsQ + head] = st.L > 0.f ? (st.M + __log2f(st.L)) * 0.69314718055994531f : -INFINITY;
 }
 
 // Attention of each sequence's 32 query heads over its side rows (per-head packed code pages; the reference keeps
@@ -490,7 +537,7 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   if (max_splits > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 8), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 4), dim3(256), 0, stream, a);
     err = hipGetLastError();
   }
   return (int)err;
@@ -586,7 +633,7 @@ int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head
     err = hipGetLastError();
     if (err != hipSuccess) return (int)err;
   }
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 8), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_seqs, kHeadsQ / 4), dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 
