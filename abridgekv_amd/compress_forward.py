@@ -10,8 +10,8 @@ HuggingFace attention function registered as ``"abridgekv_hip"`` in place of Fle
 815-894). The mask is never materialised: the kernel evaluates it from (C, K, N, prompt_len, head quota).
 
 Options of the reference that belong to other experiments (replay / raw / retained tails, learned or segment
-pooling, query residuals, copy and distillation losses, external block masks) raise NotImplementedError. The
-kernel has no backward: a backward pass through this forward raises RuntimeError.
+pooling, query residuals, copy and distillation losses, external block masks) raise NotImplementedError. Gradients
+flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module trains.
 """
 from __future__ import annotations
 
@@ -40,17 +40,34 @@ class CompressMask:
 
 
 class _MaskedPrefill(torch.autograd.Function):
+    """The masked-prefill kernel and its backward (abkv_prefill_masked_attn / _bwd), the FlexAttention
+    forward + backward the reference trains through (compress_forward.py:1134-1230, :1329)."""
+
     @staticmethod
     def forward(ctx, q, k, v, mask: CompressMask, layer_idx: int, scale: float):
         hq = None if mask.head_quota is None else mask.head_quota[layer_idx]
+        need_grad = any(ctx.needs_input_grad[:3])
+        lse = None
+        if need_grad:
+            if q.dtype != torch.bfloat16:
+                raise NotImplementedError("the masked-prefill backward runs bf16 inputs")
+            lse = torch.empty((q.shape[0], ops.HEADS_Q, q.shape[1]), dtype=torch.float32, device=q.device)
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
-                                              prompt_len=mask.prompt_len, head_quota=hq, scale=scale)
+                                              prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse)
+        if need_grad:
+            ctx.save_for_backward(q, k, v, out, lse)
+            ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        raise RuntimeError("the masked-prefill kernel has no backward pass; run CompressLM.forward under "
-                           "torch.no_grad() or train with another attention implementation")
+        q, k, v, out, lse = ctx.saved_tensors
+        m = ctx.mask
+        g = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
+        dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, g, m.block_c, m.codes_k, m.num_blocks,
+                                                           prompt_len=m.prompt_len, head_quota=ctx.hq,
+                                                           scale=ctx.scale)
+        return dq, dk, dv, None, None, None
 
 
 def masked_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):

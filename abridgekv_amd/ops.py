@@ -323,6 +323,42 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     return out, lse
 
 
+def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                                      lse: torch.Tensor, dout: torch.Tensor, block_c: int, codes_k: int,
+                                      num_blocks: int, prompt_len: torch.Tensor | None = None,
+                                      head_quota: torch.Tensor | None = None, scale: float | None = None):
+    """Gradients (dq [B, S0, 32, 128], dk, dv [B, S0, 8, 128], bf16) of sum(dout * out) for
+    :func:`prefill_masked_attention` under the same mask, from its out and lse (bf16 path only)."""
+    B, S0 = q.shape[0], q.shape[1]
+    _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
+    for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV), ("out", out, HEADS_Q),
+                       ("dout", dout, HEADS_Q)):
+        _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
+                 and t.stride(3) == 1, f"{name} must be cuda bf16 [B, S0, {h}, {HEAD_DIM}] with contiguous dims")
+    _require(lse.is_cuda and lse.dtype == torch.float32 and lse.is_contiguous()
+             and tuple(lse.shape) == (B, HEADS_Q, S0), "lse must be contiguous cuda fp32 [B, 32, S0]")
+    if prompt_len is not None:
+        _require(prompt_len.is_cuda and prompt_len.dtype == torch.int32 and prompt_len.numel() == B
+                 and prompt_len.is_contiguous(), "prompt_len must be contiguous cuda int32 [B]")
+    if head_quota is not None:
+        _require(head_quota.is_cuda and head_quota.dtype == torch.int32 and head_quota.numel() == HEADS_Q
+                 and head_quota.is_contiguous(), "head_quota must be contiguous cuda int32 [32]")
+    scale = default_scale() if scale is None else float(scale)
+    dq = torch.empty((B, S0, HEADS_Q, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    dk = torch.empty((B, S0, HEADS_KV, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    dv = torch.empty_like(dk)
+    ws = torch.empty(lib().abkv_prefill_masked_bwd_workspace_size(B, S0), dtype=torch.uint8, device=q.device)
+    args = []
+    for t in (q, k, v, out, dout):
+        args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+    args += [_ptr(lse), B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota), scale]
+    for t in (dq, dk, dv):
+        args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+    rc = lib().abkv_prefill_masked_attn_bwd(*args, _ptr(ws), ws.numel(), C.c_void_p(_stream()))
+    check(rc, "abkv_prefill_masked_attn_bwd")
+    return dq, dk, dv
+
+
 def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse):
     B, S0 = q.shape[0], q.shape[1]
     _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")

@@ -104,6 +104,23 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
                              void* out, long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
                              abkv_stream_t stream);
 
+/* Backward of abkv_prefill_masked_attn: the gradients dq [batch, seq_len, 32, 128] and dk, dv [batch, seq_len, 8,
+ * 128] (bf16, element strides, dims contiguous; written, not accumulated) of sum(dout * out) under the same mask,
+ * from the forward's out and lse (lse required). Replaces the FlexAttention backward the reference trains through
+ * (abridgekv/compress_forward.py:1134-1230 under autograd; its self-test calls backward at :1329).
+ * workspace >= abkv_prefill_masked_bwd_workspace_size(batch, seq_len) bytes. */
+size_t abkv_prefill_masked_bwd_workspace_size(int batch, int seq_len);
+int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
+                                 long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
+                                 long v_stride_s, long v_stride_h, const void* out, long out_stride_b,
+                                 long out_stride_s, long out_stride_h, const void* dout, long dout_stride_b,
+                                 long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
+                                 int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
+                                 const int32_t* head_quota, float scale, void* dq, long dq_stride_b,
+                                 long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b, long dk_stride_s,
+                                 long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s, long dv_stride_h,
+                                 void* workspace, size_t workspace_bytes, abkv_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Multi-query attention over the paged cache: prompt-chunk prefill (causal) and the CompressLM code step.
  * Replaces the FlashInfer paged-prefill call with a custom mask that the overlay routes code steps to

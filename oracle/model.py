@@ -43,7 +43,6 @@ def _rotate_half(x):
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
 
 
-@torch.no_grad()
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                  layer_head_quota=None):
     """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
@@ -93,7 +92,6 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     return inner.norm(h)
 
 
-@torch.no_grad()
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                       layer_head_quota=None):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""

@@ -110,3 +110,39 @@ def visible_pairs(C, K, N, prompt_len=None):
     """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
     m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len])
     return int(m.sum())
+
+
+def masked_attention_grads_fp64(q, k, v, mask, scale, dout):
+    """Gradients (dq, dk, dv) of sum(dout * masked_attention_fp64(q, k, v, mask, scale)[0]) in float64.
+
+    The softmax backward in closed form: P = softmax(scale * q k^T) over the visible keys, dP = dout v^T,
+    dS = P * (dP - rowsum(dP * P)), dq = scale * dS k, dk = scale * dS^T q, dv = P^T dout, dk / dv summed over the
+    query heads of each KV head. (The reference trains through FlexAttention's autograd of this attention,
+    abridgekv/compress_forward.py:1134-1230, :1329.) Rows with no visible key have P = 0 and contribute nothing.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    dout = np.asarray(dout, np.float64)
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    for h in range(Hq):
+        hk = h // g
+        m = mask if mask.ndim == 2 else mask[h]
+        s = np.where(m, (q[:, h] @ k[:, hk].T) * scale, -np.inf)
+        mx = s.max(axis=1, keepdims=True)
+        ok = np.isfinite(mx)
+        e = np.where(ok, np.exp(s - np.where(ok, mx, 0.0)), 0.0)
+        z = e.sum(axis=1, keepdims=True)
+        p = e / np.where(z > 0, z, 1.0)
+        dp = dout[:, h] @ v[:, hk].T
+        ds = p * (dp - (p * dp).sum(axis=1, keepdims=True))
+        dq[:, h] = scale * ds @ k[:, hk]
+        dk[:, hk] += scale * ds.T @ q[:, h]
+        dv[:, hk] += p.T @ dout[:, h]
+    return dq, dk, dv
+

@@ -1,0 +1,88 @@
+"""Backward of the block-masked teacher-forced attention on the GPU vs the fp64 closed-form gradients of the oracle
+(bf16 inputs; tolerance: max-abs error <= 2e-2 x the largest |gradient| of each tensor, plus 2e-3)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import prefill as op
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0):
+    from abridgekv_amd import ops
+    S0 = N * (C + K)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
+    dout = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    pl = None if prompt_len is None else torch.tensor(prompt_len, dtype=torch.int32, device=dev)
+    hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
+    qd, kd, vd, gd = (t.to(dev) for t in (q, k, v, dout))
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse)
+    dq, dk, dv = ops.prefill_masked_attention_backward(qd, kd, vd, out, lse, gd, C, K, N, prompt_len=pl,
+                                                       head_quota=hq)
+    torch.cuda.synchronize()
+    got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
+    worst = 0.0
+    for b in range(B):
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota)
+        if prompt_len is not None:
+            mask = mask[0]
+        ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
+                                             128 ** -0.5, dout[b].float().numpy())
+        for name, mine, r in zip("qkv", got, ref):
+            assert np.isfinite(mine[b]).all(), name
+            err = float(np.abs(mine[b] - r).max())
+            bound = 2e-2 * float(np.abs(r).max()) + 2e-3
+            print(f"d{name} b{b}: max err {err:.3e}, bound {bound:.3e}")
+            assert err <= bound, (name, b, err, bound)
+            worst = max(worst, err / bound)
+    return worst
+
+
+def test_aligned_no_prompt():
+    _check(C=128, K=64, N=3, B=1)
+
+
+def test_aligned_prompt_straddles_tiles():
+    _check(C=128, K=64, N=3, B=2, prompt_len=[150, 320], seed=1)
+
+
+def test_aligned_head_quotas():
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=2)
+
+
+def test_unaligned_small_blocks_partial_tiles():
+    """C=40, K=12: the per-element mask path; S0=208 leaves a partial query and key tile."""
+    quota = np.repeat([12, 3, 7, 12, 1, 5, 9, 12], 4).tolist()
+    _check(C=40, K=12, N=4, B=2, prompt_len=[50, 0], head_quota=quota, seed=3)
+
+
+def test_autograd_through_hf_attention_layout():
+    """The autograd function CompressLM's attention uses: [B, H, S, D] views in, gradients out in the same views."""
+    from abridgekv_amd import compress_forward as cf
+    from abridgekv_amd import ops
+    C, K, N, B = 64, 64, 2, 1
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn((B, 32, S0, 128), generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    k = torch.randn((B, 8, S0, 128), generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    v = torch.randn((B, 8, S0, 128), generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    mask = cf.CompressMask(block_c=C, codes_k=K, num_blocks=N)
+    module = type("M", (), {"layer_idx": 0})()
+    out, _ = cf.masked_attention_forward(module, q, k, v, mask, scaling=ops.default_scale())
+    dout = torch.randn(out.shape, generator=g, device=dev).to(torch.bfloat16)
+    (out.float() * dout.float()).sum().backward()
+    ref = op.masked_attention_grads_fp64(q.detach()[0].transpose(0, 1).float().cpu().numpy(),
+                                         k.detach()[0].transpose(0, 1).float().cpu().numpy(),
+                                         v.detach()[0].transpose(0, 1).float().cpu().numpy(),
+                                         op.arith_mask(C, K, N), ops.default_scale(), dout[0].float().cpu().numpy())
+    for t, r in zip((q, k, v), ref):
+        mine = t.grad[0].transpose(0, 1).float().cpu().numpy()
+        assert np.abs(mine - r).max() <= 2e-2 * np.abs(r).max() + 2e-3

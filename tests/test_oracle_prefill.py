@@ -122,3 +122,41 @@ def closed_form_pairs(C, K, N):
 def test_visible_pair_count(C, K, N):
     """FLOP accounting of the masked prefill (config 4: N=16 blocks of [512 | 128], 512-token raw prompt)."""
     assert op.visible_pairs(C, K, N, prompt_len=C) == closed_form_pairs(C, K, N)
+
+
+def test_masked_attention_grads_match_autograd_and_finite_differences():
+    """The closed-form softmax backward against torch autograd of the fp64 forward (an independent derivation) on the
+    compression mask with prompt and per-head quotas, and against central differences on a tiny case."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    C, K, N, Hq, Hkv, D = 6, 3, 3, 4, 2, 5
+    S = N * (C + K)
+    mask = op.arith_mask(C, K, N, [4], [3, 1, 2, 3])[0]           # [Hq, S, S]
+    q, k, v, dout = (rng.standard_normal(sh) for sh in ((S, Hq, D), (S, Hkv, D), (S, Hkv, D), (S, Hq, D)))
+    scale = 0.7
+    dq, dk, dv = op.masked_attention_grads_fp64(q, k, v, mask, scale, dout)
+
+    tq, tk, tv = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v))
+    outs = []
+    for h in range(Hq):
+        s = (tq[:, h] @ tk[:, h // 2].T) * scale
+        s = s.masked_fill(~torch.from_numpy(mask[h]), float("-inf"))
+        outs.append(torch.softmax(s, dim=1) @ tv[:, h // 2])
+    (torch.stack(outs, 1) * torch.from_numpy(dout)).sum().backward()
+    for mine, ref in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        np.testing.assert_allclose(mine, ref.numpy(), rtol=1e-10, atol=1e-12)
+
+    def loss(qq, kk, vv):
+        return float((op.masked_attention_fp64(qq, kk, vv, mask, scale)[0] * dout).sum())
+
+    eps = 1e-6
+    for arr, grad in ((q, dq), (k, dk), (v, dv)):
+        for idx in [(0, 0, 0), (S - 1, arr.shape[1] - 1, D - 1), (C + 1, 1, 2)]:
+            a1, a2 = arr.copy(), arr.copy()
+            a1[idx] += eps
+            a2[idx] -= eps
+            args1 = [a1 if arr is x else x for x in (q, k, v)]
+            args2 = [a2 if arr is x else x for x in (q, k, v)]
+            fd = (loss(*args1) - loss(*args2)) / (2 * eps)
+            assert abs(fd - grad[idx]) <= 1e-6 * max(1.0, abs(fd)), (idx, fd, grad[idx])
