@@ -62,8 +62,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=32)
-    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "compaction", "packed",
-                                           "copy"],
+    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "prefill_bwd",
+                                           "compaction", "packed", "copy"],
                     default="serving")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
@@ -169,6 +169,52 @@ def bench_prefill(args, torch):
                      "alg_flops_per_launch": flops, "avg_launch_us": t * 1e6,
                      "mfma_util_rocprof": profiled_mfma_util("prefill_masked_b4_s10240_pmc_mfma.md"),
                      "mfma_util_source": "profiles/prefill_masked_b4_s10240_pmc_mfma.md (MfmaUtil)"},
+    }
+
+
+def bench_prefill_bwd(args, torch):
+    """Backward of config 4 (gradients of q, k, v through the compression mask; what training CompressLM runs per
+    layer after the forward). FLOPs = 10 * D * visible pairs * heads * B: the five products of the attention backward
+    (S recomputed, dP, dV, dK, dQ) over the visible pairs, 2.5x the forward's; the kernels execute seven (the dQ and
+    the dK/dV kernels each recompute S and dP)."""
+    from abridgekv_amd import ops
+    from abridgekv_amd.workloads import visible_pairs_prompt_block
+
+    B, C, K, N, plen = 4, 512, 128, 16, 512
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    dout = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    pl = torch.full((B,), plen, dtype=torch.int32, device=dev)
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
+    for _ in range(args.warmup):
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / args.steps
+    flops = 10.0 * 128 * visible_pairs_prompt_block(C, K, N) * 32 * B
+    tflops = flops / t / 1e12
+    return {
+        "metric": "masked teacher-forced attention backward TFLOP/s (visible-pair flops, 2.5x forward); % of bf16 "
+                  "dense MFMA peak",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v/dout from the seed",
+        "config": {"workload": f"masked prefill backward B={B}, N={N} blocks of [{C} content | {K} codes], "
+                               f"S0={S0}, raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
+                     "traffic": None, "kernel": "prefill_bwd_prep_kernel + prefill_bwd_dq_kernel + "
+                                                "prefill_bwd_dkv_kernel", "alg_flops_per_launch": flops,
+                     "avg_launch_us": t * 1e6},
     }
 
 
@@ -417,9 +463,9 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "prefill", "compaction", "packed", "copy"):
-        res = {"serving": bench_serving, "prefill": bench_prefill, "compaction": bench_compaction,
-               "packed": bench_packed, "copy": bench_copy}[args.workload](args, torch)
+    if args.workload in ("serving", "prefill", "prefill_bwd", "compaction", "packed", "copy"):
+        res = {"serving": bench_serving, "prefill": bench_prefill, "prefill_bwd": bench_prefill_bwd,
+               "compaction": bench_compaction, "packed": bench_packed, "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
