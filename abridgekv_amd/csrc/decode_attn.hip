@@ -8,7 +8,7 @@
 // contiguous as [prompt rows | q_l code rows per closed block | open block], so the kernel attends over physical
 // slots [0, seq_len) of the group's page table.
 //
-// Work decomposition: two workgroups of 4 waves per (sequence, split), for KV heads 0-3 and 4-7; a wave owns one KV
+// Work decomposition: four workgroups of 2 waves per (sequence, split), each for two KV heads; a wave owns one KV
 // head and its 4 query heads.
 // A split covers `split_pages` pages; the wave walks it 32 slots (two pages) at a time:
 //   S^T[32 slots x 16 cols] = K_tile . Q^T          two row tiles x 4 MFMA 16x16x32 (cols 0..3 = the 4 q heads)
@@ -477,11 +477,11 @@ __global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
   store_partial(a, (long)b * a.part_stride + a.max_splits + split, kvh * kGroup + m16, j, o, amax, m_run, l_tot);
 }
 
-// Four waves (KV heads 0-3 or 4-7) per workgroup: the two workgroups of a split are adjacent in dispatch order. Four
-// waves measured 0.8 % faster than eight on the saturated and serving workloads (shorter workgroups, a shorter tail),
-// two waves the same as four, one wave 4 % slower.
+// Two waves (two KV heads) per workgroup: the four workgroups of a split are adjacent in dispatch order. Measured in
+// one process over the same pages: two waves 952.9 us per launch against four 959.1 and eight 990.5 on the saturated
+// B=256 workload, 241.5 against 245.1 and 254.7 on the B=64 full-model decode; one wave 4 % slower than four.
 inline void launch_decode(const DecodeArgs& a, int max_splits, int num_seqs, hipStream_t stream) {
-  constexpr int kW = 4;
+  constexpr int kW = 2;
   hipLaunchKernelGGL(decode_attn_kernel<kW>, dim3(max_splits * (kHeadsKV / kW), num_seqs), dim3(64 * kW), 0, stream,
                      a);
 }
