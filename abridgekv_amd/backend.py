@@ -136,13 +136,13 @@ class AbridgeMetadataBuilder:
     max_num_seqs: int
     max_pages: int
     device: torch.device | str = "cuda"
-    split_pages: int = ops.DEFAULT_SPLIT_PAGES
+    split_pages: int | None = None          # None: per step, ops.auto_split_pages of the decode requests' rows
     _workspace: torch.Tensor | None = field(default=None, init=False, repr=False)
 
     def workspace(self) -> torch.Tensor:
         if self._workspace is None:
-            self._workspace = ops.decode_workspace(self.max_num_seqs, self.max_pages, self.split_pages,
-                                                   device=self.device)
+            sp = min(self.split_pages or ops.DEFAULT_SPLIT_PAGES, ops.DEFAULT_SPLIT_PAGES)
+            self._workspace = ops.decode_workspace(self.max_num_seqs, self.max_pages, sp, device=self.device)
         return self._workspace
 
     def build(self, query_start_loc, seq_lens, block_table: torch.Tensor, slot_mapping: torch.Tensor,
@@ -177,7 +177,9 @@ class AbridgeMetadataBuilder:
         return AbridgeAttentionMetadata(query_start_loc=qsl, seq_lens=sl, block_table=block_table,
                                         slot_mapping=slot_mapping, seq_lens_dev=seq_lens_dev, num_decodes=nd,
                                         code_key_limit=limits, max_decode_pages=max(max_pages, 1),
-                                        workspace=self.workspace() if nd else None, split_pages=self.split_pages)
+                                        workspace=self.workspace() if nd else None,
+                                        split_pages=self.split_pages or (ops.auto_split_pages(sl[:nd]) if nd
+                                                                         else ops.DEFAULT_SPLIT_PAGES))
 
 
 class AbridgeAttentionImpl:

@@ -9,6 +9,7 @@ from __future__ import annotations
 import ctypes as C
 import math
 
+import numpy as np
 import torch
 
 from ._lib import check, lib
@@ -21,6 +22,7 @@ SLOT_BYTES = HEADS_KV * HEAD_DIM * 2           # one slot of K (or V) of one lay
 HALF_BYTES = PAGE * SLOT_BYTES                 # K half of a page
 PAGE_BYTES = 2 * HALF_BYTES                    # one page of one layer
 DEFAULT_SPLIT_PAGES = 32                       # 512 slots per split
+AUTO_SPLIT_CHOICES = (48, 40, 32)               # pages per split the host may pick (a workspace for 32 fits all)
 
 
 def _stream() -> int:
@@ -58,6 +60,30 @@ def _check_cache(kv_cache: torch.Tensor, dtype=torch.bfloat16) -> None:
     _require(kv_cache.dim() == 5 and tuple(kv_cache.shape[1:]) == (2, PAGE, HEADS_KV, HEAD_DIM),
              f"kv_cache must be [P, 2, {PAGE}, {HEADS_KV}, {HEAD_DIM}], got {tuple(kv_cache.shape)}")
     _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+
+
+_NUM_CUS = None
+
+
+def _num_cus() -> int:
+    global _NUM_CUS
+    if _NUM_CUS is None:
+        _NUM_CUS = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count \
+            if torch.cuda.is_available() else 256
+    return _NUM_CUS
+
+
+def auto_split_pages(seq_lens, num_cus: int | None = None) -> int:
+    """Pages per decode split for a batch of host row counts: the largest of 48, 40, 32 whose grid still fills the GPU
+    (four 2-wave workgroups per split, eight workgroups per CU). Longer splits write fewer partials; too few
+    workgroups leave CUs idle. Measured: 48 on the B=256 saturated workload (1.1 % faster than 32), 40 on the B=64
+    full-model decode (0.7 %), where 48 under-fills the GPU (1.7 % slower)."""
+    pages = -(-np.asarray(seq_lens, dtype=np.int64) // PAGE)
+    slots = 8 * (_num_cus() if num_cus is None else int(num_cus))
+    for sp in AUTO_SPLIT_CHOICES:
+        if 4 * int(np.maximum(1, -(-pages // sp)).sum()) >= slots:
+            return sp
+    return DEFAULT_SPLIT_PAGES
 
 
 def decode_workspace(num_seqs: int, max_pages: int, split_pages: int = DEFAULT_SPLIT_PAGES,

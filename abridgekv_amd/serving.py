@@ -87,6 +87,7 @@ class ServingPlan:
         tiles = np.array([(r, q0) for r in range(nc) for q0 in range(0, K, 64)], np.int64).reshape(-1, 2)
         dec_lens = self.seq_lens[:, dec]
         max_pages = [max(1, int(-(-dec_lens[g].max() // PAGE))) if nd else 1 for g in range(G)]
+        split = [ops.auto_split_pages(dec_lens[g]) if nd else ops.DEFAULT_SPLIT_PAGES for g in range(G)]
         rows = self.pending_rows
         self.pending_rows = np.zeros(0, np.int64)
         tok_req = np.concatenate([dec, np.repeat(cod, K)]).astype(np.int64)
@@ -94,7 +95,7 @@ class ServingPlan:
                                   ((self.logical[cod] - K)[:, None] + np.arange(K)[None, :]).reshape(-1)])
         return dict(dec=dec, cod=cod, nd=nd, nc=nc, n_tok=n_tok, slots=slots, dec_lens=dec_lens,
                     q_start=np.arange(nc + 1, dtype=np.int64) * K, kv_start=kv_start, limits=limits, tiles=tiles,
-                    max_pages=max_pages, upd_rows=rows, upd_tables=self.tables[:, rows], tok_req=tok_req,
+                    max_pages=max_pages, split=split, upd_rows=rows, upd_tables=self.tables[:, rows], tok_req=tok_req,
                     tok_pos=tok_pos)
 
     def advance(self, m) -> np.ndarray:
@@ -155,7 +156,7 @@ class ServingPlan:
 class ServingStress:
     """Device half: caches, synthetic q/k/v pools, and the per-step launches of a :class:`ServingPlan`."""
 
-    def __init__(self, T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, device="cuda", split_pages=32,
+    def __init__(self, T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, device="cuda", split_pages=None,
                  growth_tokens=2048, C=BLOCK_C, K=CODES_K_MAX, tag=False):
         plan = ServingPlan(T, P, layer_quotas, seed=seed, growth_tokens=growth_tokens, C=C, K=K)
         self.plan = plan
@@ -178,7 +179,9 @@ class ServingStress:
         self.v_pool = torch.randn((B * K, 8, 128), generator=gen, device=self.dev).to(torch.bfloat16)
         self.out = torch.empty((B * K, 32, 128), dtype=torch.bfloat16, device=self.dev)
         self.bt_dev = torch.from_numpy(plan.tables).to(self.dev)                       # [G, B, W]
-        self.ws = ops.decode_workspace(B, self.W, split_pages, device=self.dev)
+        # split_pages None: per step and group the plan's ops.auto_split_pages (never below 32, so this workspace fits)
+        self.ws = ops.decode_workspace(B, self.W, min(split_pages or ops.DEFAULT_SPLIT_PAGES, ops.DEFAULT_SPLIT_PAGES),
+                                       device=self.dev)
         self.ws_bytes = 0 if self.ws is None else self.ws.numel()
         # pinned staging ring for the per-step metadata
         self._pinned = [torch.empty(1 << 22, dtype=torch.int32, pin_memory=True) for _ in range(2)]
@@ -289,7 +292,8 @@ class ServingStress:
                     e0.record()
                 check(L.abkv_decode_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(cache), cache.shape[0],
                                          _ptr(dec_bt[g]), self.W, _ptr(v["dec_lens"][g]), nd, m["max_pages"][g],
-                                         self.split_pages, C.c_float(self.scale), _ptr(out), out.stride(0),
+                                         self.split_pages or m["split"][g], C.c_float(self.scale), _ptr(out),
+                                         out.stride(0),
                                          out.stride(1), None, None if self.ws is None else _ptr(self.ws),
                                          C.c_size_t(self.ws_bytes), stream), "abkv_decode_attn")
                 if self.decode_events is not None:

@@ -61,7 +61,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--split-pages", type=int, default=32)
+    ap.add_argument("--split-pages", type=int, default=None,
+                    help="pages per decode split (default: ops.auto_split_pages per launch: 48, 40 or 32)")
     ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "prefill_bwd",
                                            "compaction", "packed", "copy"],
                     default="serving")
@@ -327,7 +328,7 @@ def bench_serving(args, torch):
                                f"groups 256/128/64, 32q/8kv, d128, bf16, page 16), B={B}, T~U[2048,32768], "
                                f"P~U[128,1024]; a request closing a 512-token block runs its 256 code rows next step "
                                f"and is compacted", "global_batch": B, "layers": s.L, "kv_groups": s.G,
-                   "split_pages": args.split_pages, "seed": args.seed, "parallelism": "none (1 GPU)"},
+                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": profiled_traffic("decode_attn_serving_b256_pmc_traffic.md"),
@@ -400,12 +401,13 @@ def bench_packed(args, torch):
     lse = torch.empty((B, 32), dtype=torch.float32, device=dev)
     scale = ops.default_scale()
     sr = ops.lib().abkv_decode_side_split_rows(min(PACKED_HEAD_QUOTAS))
-    need = ops.lib().abkv_decode_packed_workspace_size(B, W, args.split_pages, blocks, max(PACKED_HEAD_QUOTAS), sr)
+    sp = args.split_pages or ops.DEFAULT_SPLIT_PAGES
+    need = ops.lib().abkv_decode_packed_workspace_size(B, W, sp, blocks, max(PACKED_HEAD_QUOTAS), sr)
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
 
     def launch():
         ops.decode_attention_packed(q, cache, bt, seq_lens, pool, PACKED_HEAD_QUOTAS, ptab, pcount, scale,
-                                    max_pages=W, max_packed=blocks, out=out, lse=lse, split_pages=args.split_pages,
+                                    max_pages=W, max_packed=blocks, out=out, lse=lse, split_pages=sp,
                                     workspace=ws)
 
     for _ in range(args.warmup):
@@ -507,7 +509,9 @@ def main():
     W = st.block_tables[0].shape[1]
     # per-group page bound (what a metadata builder passes: the batch's longest sequence in that group)
     gmax = [max(1, int(-(-int(sl.max()) // 16))) for sl in st.seq_lens]
-    ws = ops.decode_workspace(B, W, args.split_pages, device=dev)
+    ws = ops.decode_workspace(B, W, min(args.split_pages or ops.DEFAULT_SPLIT_PAGES, ops.DEFAULT_SPLIT_PAGES),
+                              device=dev)
+    gsplit = [args.split_pages or ops.auto_split_pages(sl) for sl in st.seq_lens]
     scale = ops.default_scale()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
@@ -519,7 +523,7 @@ def main():
             if timed:
                 starts[l].record()
             ops.decode_attention(qs[l], caches[i], bts[g], sls[g], scale, max_pages=gmax[g], out=outs[l], lse=lses[l],
-                                 split_pages=args.split_pages, workspace=ws)
+                                 split_pages=gsplit[g], workspace=ws)
             if timed:
                 ends[l].record()
 
@@ -560,7 +564,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (N(0,1) K/V pages and queries from the seed; page tables from the compaction planner)",
         "config": {"workload": wl, "global_batch": B, "layers": L, "kv_groups": G,
-                   "split_pages": args.split_pages, "seed": args.seed, "parallelism": "none (1 GPU)"},
+                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": (profiled_traffic("decode_attn_saturated_b256_pmc_traffic.md")

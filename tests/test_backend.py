@@ -135,3 +135,12 @@ def test_backend_surface_and_hook_is_inert_without_impl():
     out = torch.full((2, 32 * 128), 3.0)
     bk.maybe_override_attention(SimpleNamespace(), torch.zeros(2, 32 * 128), torch.zeros(1), object(), out)
     assert bool((out == 3.0).all())
+
+
+def test_auto_split_pages_fills_the_gpu_with_the_longest_split():
+    from abridgekv_amd import ops
+    rng = np.random.default_rng(0)
+    assert ops.auto_split_pages(rng.integers(2000, 17000, 256), num_cus=256) == 48       # saturated-like batch
+    assert ops.auto_split_pages(np.full(64, 5000), num_cus=256) == 40                    # 48 would leave CUs idle
+    assert ops.auto_split_pages([1068], num_cus=256) == ops.DEFAULT_SPLIT_PAGES          # tiny batch: the default
+    assert ops.auto_split_pages(np.full(64, 5000), num_cus=64) == 48
