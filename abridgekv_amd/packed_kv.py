@@ -262,7 +262,8 @@ class PackedKVSidecar:
             max_pages = max(1, int(-(-sl.max() // ops.PAGE)))
             ops.decode_attention_packed(query[:B], kv_cache, block_table, seq_lens_dev, pool, quotas, table, count,
                                         scale, max_pages=min(max_pages, block_table.shape[1]),
-                                        max_packed=max_packed, out=output[:B], lse=lse)
+                                        max_packed=max_packed, out=output[:B], lse=lse,
+                                        split_pages=ops.auto_split_pages(sl))
             return output
         kv_start = sl - nq
         ops.paged_prefill_attention_packed(query[:T], kv_cache, block_table, qsl, kv_start, sl, cz, pool, quotas,
