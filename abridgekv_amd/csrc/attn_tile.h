@@ -138,11 +138,28 @@ struct TileMask {
 // 4e + i / 4, for e = 0..3. The operand row m of dim slab t is dim 32 * (m / 4) + 4t + m % 4 and its k-index
 // 8g + e (g = lane group) is key kb + 4g + e for e < 4 and kb + 16 + 4g + e - 4 for e >= 4 (the contraction order the
 // P^T operand uses); so lane 4e + c of the group addresses row kb + 4g + e (then + 16), dims 32c + 4t .. +3.
+// Dim slab of accumulator tile t in lane group j: tile t of a PV-style product holds dims 32j + 4 * acc_tile(t, j)
+// .. + 3. Odd groups take the slabs in swapped pairs so that one transposed read's lanes use both 8-byte halves of
+// their 16-byte chunks, i.e. all LDS banks (with every lane on the same half, each bank was hit twice as often).
+__device__ __forceinline__ int acc_tile(int t, int j) { return t ^ (j & 1); }
+
+// Dims 8p .. 8p + 7 of an accumulator column (lane group j) times inv, as one 16-byte bf16 store.
+__device__ __forceinline__ void store_acc_bf16x8(__bf16* dst, const floatx4& a, const floatx4& b, int j, float inv) {
+  const bool odd = j & 1;
+  floatx4 lo, hi;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lo[r] = odd ? b[r] : a[r];
+    hi[r] = odd ? a[r] : b[r];
+  }
+  store_bf16x8(dst, lo, hi, inv);
+}
+
 __device__ __forceinline__ bf16x8 vt_operand(const __bf16* Vbuf, int kb, int t, int lane) {
   typedef short s4 __attribute__((ext_vector_type(4)));
   const int g = lane >> 4, i = lane & 15;
   const int e = i >> 2, c = i & 3;
-  const int dim = 32 * c + 4 * t;                   // 8-byte aligned, inside 16-byte chunk dim / 8
+  const int dim = 32 * c + 4 * acc_tile(t, c);       // 8-byte aligned, inside 16-byte chunk dim / 8
   const int row0 = kb + 4 * g + e, row1 = row0 + 16;
   const __bf16* p0 = Vbuf + row0 * kHeadDim + 8 * ((dim >> 3) ^ (row0 & 15)) + (dim & 7);
   const __bf16* p1 = Vbuf + row1 * kHeadDim + 8 * ((dim >> 3) ^ (row1 & 15)) + (dim & 7);
@@ -264,7 +281,8 @@ __device__ __forceinline__ void tile_softmax(floatx4 (&s)[2][2][H], floatx4 (&o)
     }
 }
 
-// O^T += V^T . P^T over one tile: o[t][u][r] accumulates out dim 32 * (lane >> 4) + 4t + r of column (u, m16).
+// O^T += V^T . P^T over one tile: o[t][u][r] accumulates out dim 32j + 4 * acc_tile(t, j) + r of column (u, m16),
+// j = lane >> 4.
 // The row sums ride on the MFMA too: lsum[u] += ones . P^T puts the column's sum of the (bf16) weights in every
 // entry, the same weights the output accumulates.
 template <int H>

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
       const long row = ((long)(a.split_base + blockIdx.z) * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
       float* po = a.part_o + row * kHeadDim + 32 * j;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * t) = o[t][u];
+      for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * acc_tile(t, j)) = o[t][u];
       if (j == 0) {
         a.part_ml[row * 2] = m_run[u];
         a.part_ml[row * 2 + 1] = l;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)(t0 + qi) * a.o_st + (long)head * a.o_sh + 32 * j;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) store_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], inv);
+    for (int p = 0; p < 4; ++p) store_acc_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], j, inv);
     if (a.lse != nullptr && j == 0)
       a.lse[(long)(t0 + qi) * kHeadsQ + head] = l > 0.f ? (m_run[u] + __log2f(l)) * 0.69314718055994531f : -INFINITY;
   }

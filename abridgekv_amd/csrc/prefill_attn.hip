@@ -178,7 +178,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
                                     lane);
 
   if (qrow >= a.S0) return;
-  // o[t][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 4t + r]
+  // o[t][u][r] = un-normalised out[row qrow][head hbase + u][dim 32j + 4 * acc_tile(t, j) + r]
 #pragma unroll
   for (int u = 0; u < H; ++u) {
     const float l = l_run[u];
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
     const int head = kvh * kGroup + hbase + u;
     __bf16* oh = a.out + (long)b * a.o_sb + (long)qrow * a.o_ss + (long)head * a.o_sh + 32 * j;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) store_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], inv);
+    for (int p = 0; p < 4; ++p) store_acc_bf16x8(oh + 8 * p, o[2 * p][u], o[2 * p + 1][u], j, inv);
     if (a.lse != nullptr && j == 0)
       a.lse[((long)b * kHeadsQ + head) * a.S0 + qrow] =
           l > 0.f ? (m_run[u] + __log2f(l)) * 0.69314718055994531f : -INFINITY;
@@ -242,8 +242,8 @@ __global__ __launch_bounds__(256) void prefill_bwd_prep_kernel(PrefillBwdArgs a)
 }
 
 // acc[t][u] += A^T . B^T over one 64-row tile: A^T operands by LDS transpose reads of the tile, B^T the packed bf16
-// operands (the forward's PV step without its row sums). acc[t][u][r] = dim 32 * (lane >> 4) + 4t + r of column (u,
-// m16).
+// operands (the forward's PV step without its row sums). acc[t][u][r] = dim 32j + 4 * acc_tile(t, j) + r of column
+// (u, m16), j = lane >> 4.
 template <int H>
 __device__ __forceinline__ void tile_acc(const __bf16* buf, const bf16x8 (&op)[2][H], floatx4 (&acc)[8][H], int lane) {
 #pragma unroll
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   for (int u = 0; u < H; ++u) {
     __bf16* dp = a.dq + (long)b * a.dq_sb + (long)qrow * a.dq_ss + (long)(kvh * kGroup + hbase + u) * a.dq_sh + 32 * j;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) store_bf16x8(dp + 8 * p, dq[2 * p][u], dq[2 * p + 1][u], a.scale);
+    for (int p = 0; p < 4; ++p) store_acc_bf16x8(dp + 8 * p, dq[2 * p][u], dq[2 * p + 1][u], j, a.scale);
   }
 }
 
@@ -565,8 +565,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   __bf16* vp = a.dv + (long)b * a.dv_sb + (long)key * a.dv_ss + (long)kvh * a.dv_sh + 32 * j;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    store_bf16x8(kp + 8 * p, dk[2 * p][0], dk[2 * p + 1][0], a.scale);
-    store_bf16x8(vp + 8 * p, dv[2 * p][0], dv[2 * p + 1][0], 1.f);
+    store_acc_bf16x8(kp + 8 * p, dk[2 * p][0], dk[2 * p + 1][0], j, a.scale);
+    store_acc_bf16x8(vp + 8 * p, dv[2 * p][0], dv[2 * p + 1][0], j, 1.f);
   }
 }
 
