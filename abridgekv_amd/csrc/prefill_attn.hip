@@ -441,6 +441,60 @@ __device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, 
   return 0;
 }
 
+// S = Q K^T and dP = dO V^T of a wave's 16 keys over one staged tile (32 ds_read_b128, 32 MFMAs). The two products
+// are interleaved and the reads run eight ahead of the MFMAs: at 2 waves per SIMD the other wave alone cannot cover
+// an LDS round trip per MFMA.
+__device__ __forceinline__ void dkv_scores(const __bf16* Qbuf, const __bf16* Gbuf, const bf16x8 (&kop)[4],
+                                           const bf16x8 (&vop)[4], floatx4 (&s)[2][2][1], floatx4 (&dp)[2][2][1],
+                                           int m16, int j) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) s[kk][t][0] = dp[kk][t][0] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 qa = __builtin_bit_cast(bf16x8, lds16(Qbuf, 32 * kk + 16 * t + m16, 4 * i + j));
+        const bf16x8 ga = __builtin_bit_cast(bf16x8, lds16(Gbuf, 32 * kk + 16 * t + m16, 4 * i + j));
+        s[kk][t][0] = mfma16x16x32(qa, kop[i], s[kk][t][0]);
+        dp[kk][t][0] = mfma16x16x32(ga, vop[i], dp[kk][t][0]);
+      }
+  // scheduling groups (mask 0x100 LDS reads, 0x008 MFMA): 8 reads, then one MFMA per read, then the last 8 MFMAs
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+  for (int n = 0; n < 24; ++n) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+}
+
+// dV^T += dO^T P and dK^T += Q^T dS over one staged tile (the forward's PV step twice, interleaved; 64 transposed
+// reads, 32 MFMAs), the reads running ahead of the MFMAs as in dkv_scores.
+__device__ __forceinline__ void dkv_acc(const __bf16* Qbuf, const __bf16* Gbuf, const bf16x8 (&pop)[2][1],
+                                        const bf16x8 (&dsop)[2][1], floatx4 (&dk)[8][1], floatx4 (&dv)[8][1],
+                                        int lane) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const bf16x8 ga = vt_operand(Gbuf, 32 * kk, t, lane);
+      const bf16x8 qa = vt_operand(Qbuf, 32 * kk, t, lane);
+      dv[t][0] = mfma16x16x32(ga, pop[kk][0], dv[t][0]);
+      dk[t][0] = mfma16x16x32(qa, dsop[kk][0], dk[t][0]);
+    }
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+  for (int n = 0; n < 28; ++n) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+}
+
 template <bool kAligned>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs a) {
   constexpr int kWaves = 4;
@@ -465,7 +519,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 #pragma unroll
   for (int u = 0; u < 4; ++u) quota_all[u] = f.head_quota ? f.head_quota[kvh * kGroup + u] : f.K;
 
-  bf16x8 kop[1][4], vop[1][4];
+  bf16x8 kop[4], vop[4];
   {
     const bool ok = key < f.S0;
     const int r = min(key, f.S0 - 1);
@@ -475,8 +529,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
     for (int i = 0; i < 4; ++i) {
       u32x4 x = ld16g(kp + 8 * (4 * i + j)), y = ld16g(vp + 8 * (4 * i + j));
       if (!ok) x = y = u32x4{0, 0, 0, 0};
-      kop[0][i] = __builtin_bit_cast(bf16x8, x);
-      vop[0][i] = __builtin_bit_cast(bf16x8, y);
+      kop[i] = __builtin_bit_cast(bf16x8, x);
+      vop[i] = __builtin_bit_cast(bf16x8, y);
     }
   }
   floatx4 dk[8][1], dv[8][1];
@@ -485,6 +539,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 
   // (query tile, head) pairs that can see this key tile, head fastest; queries start at the key's block
   const int qt_lo = (k0 / per) * per / kBN;
+  // aligned: a content tile outside the raw prompt is seen by its own block's rows only, so the walk ends there
+  int qt_end = f.num_q_tiles;
+  if (kAligned && k0 - (k0 / per) * per < f.C && (k0 / per) * f.C + (k0 - (k0 / per) * per) >= plen)
+    qt_end = min(qt_end, (k0 / per + 1) * per / kBN);
   int qt = qt_lo, h = -1, mode = 0, limit = 0;
   auto next_pair = [&]() -> bool {
     for (;;) {
@@ -492,7 +550,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
         h = 0;
         ++qt;
       }
-      if (qt >= f.num_q_tiles) return false;
+      if (qt >= qt_end) return false;
       if constexpr (kAligned) {
         const int qh = h == 0 ? quota_all[0] : h == 1 ? quota_all[1] : h == 2 ? quota_all[2] : quota_all[3];
         mode = pair_mode(qt, kt, qh, f.S0, f.C, per, plen, limit);
@@ -519,39 +577,52 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
     issue(qt, h, 0);
     auto step = [&](auto buf_c) -> bool {
       constexpr int sl = decltype(buf_c)::value;
-      const int cq = qt, ch = h, cmode = mode, climit = limit;
+      const int cq = qt, ch = h, cmode = mode;
       const bool hn = next_pair();
       __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       if (hn) issue(qt, h, 1 - sl);
       floatx4 s[2][2][1], dp[2][2][1];
-      tile_scores<1>(Qb[sl], kop, s, m16, j);
-      tile_scores<1>(Gb[sl], vop, dp, m16, j);
+      dkv_scores(Qb[sl], Gb[sl], kop, vop, s, dp, m16, j);
       const int qh = ch == 0 ? quota_all[0] : ch == 1 ? quota_all[1] : ch == 2 ? quota_all[2] : quota_all[3];
-      const bool col_hidden = cmode == 2 && key >= climit;
+      if (cmode == 0) {                                     // wave-uniform: every pair of the tile visible
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int r0 = 32 * kk + 16 * t + 4 * j;
-          const floatx4 l4 = *reinterpret_cast<const floatx4*>(Lb[sl] + r0);
-          const floatx4 e4 = *reinterpret_cast<const floatx4*>(Eb[sl] + r0);
+          for (int t = 0; t < 2; ++t) {
+            const int r0 = 32 * kk + 16 * t + 4 * j;
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(Lb[sl] + r0);
+            const floatx4 e4 = *reinterpret_cast<const floatx4*>(Eb[sl] + r0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int qrow = cq * kBN + r0 + r;
-            bool vis = !col_hidden;
-            if (cmode == 1) vis = key <= qrow;
-            if (cmode == 3) vis = elem_visible(qrow, key, f.S0, f.C, per, plen, qh);
-            const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
-            s[kk][t][0][r] = pr;
-            dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
+            for (int r = 0; r < 4; ++r) {
+              const float pr = fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r]));
+              s[kk][t][0][r] = pr;
+              dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
+            }
           }
-        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int r0 = 32 * kk + 16 * t + 4 * j;
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(Lb[sl] + r0);
+            const floatx4 e4 = *reinterpret_cast<const floatx4*>(Eb[sl] + r0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int qrow = cq * kBN + r0 + r;
+              // diagonal tiles: key <= row; bounded (mode 2) and unaligned tiles: the per-element predicate
+              const bool vis = cmode == 1 ? key <= qrow : elem_visible(qrow, key, f.S0, f.C, per, plen, qh);
+              const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
+              s[kk][t][0][r] = pr;
+              dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
+            }
+          }
+      }
       bf16x8 pop[2][1], dsop[2][1];
       pack_tile_op<1>(s, pop);
       pack_tile_op<1>(dp, dsop);
-      tile_acc<1>(Gb[sl], pop, dv, lane);
-      tile_acc<1>(Qb[sl], dsop, dk, lane);
+      dkv_acc(Qb[sl], Gb[sl], pop, dsop, dk, dv, lane);
       return hn;
     };
     for (;;) {
