@@ -36,6 +36,18 @@ struct PrefillArgs {
   int num_q_tiles;
 };
 
+// Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,
+// tile rank slowest. Workgroups go to the 8 XCDs round-robin by linear id, so every workgroup of one KV head runs on
+// one XCD and that XCD's L2 serves all re-reads of the head's rows; and each tile rank is issued for every (head,
+// sequence) before the next, so the costly tiles (which the callers rank first) do not trail at the end of the grid.
+struct GridPos {
+  int rank, kvh, b;
+};
+__device__ __forceinline__ GridPos grid_pos(int batch) {
+  const int l = blockIdx.x;
+  return {l / (kHeadsKV * batch), l % kHeadsKV, (l / kHeadsKV) % batch};
+}
+
 // Walk over the key tiles one query tile attends to, with the mask mode of each.
 // Aligned layouts (C and K multiples of 64): a key tile is named by (block kb, tile tw of the block's C + K rows).
 // Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
@@ -118,9 +130,10 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   __bf16* const Kbuf[kStages] = {K0, K1, K2};
   __bf16* const Vbuf[kStages] = {V0, V1, V2};
 
-  const int qt = a.num_q_tiles - 1 - blockIdx.x;            // heavier (later) query tiles first
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  const GridPos gp = grid_pos(a.B);
+  const int qt = a.num_q_tiles - 1 - gp.rank;               // heavier (later) query tiles first
+  const int kvh = gp.kvh;
+  const int b = gp.b;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int lane = tid & 63;
@@ -299,9 +312,10 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   __bf16* const Kb[2] = {K0, K1};
   __bf16* const Vb[2] = {V0, V1};
   const PrefillArgs& f = a.f;
-  const int qt = f.num_q_tiles - 1 - blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  const GridPos gp = grid_pos(f.B);
+  const int qt = f.num_q_tiles - 1 - gp.rank;               // heavier (later) query tiles first
+  const int kvh = gp.kvh;
+  const int b = gp.b;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
@@ -505,9 +519,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   float* const Lb[2] = {L0, L1};
   float* const Eb[2] = {E0, E1};
   const PrefillArgs& f = a.f;
-  const int kt = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  const GridPos gp = grid_pos(f.B);
+  const int kt = gp.rank;                                   // earlier key tiles are seen by more query tiles
+  const int kvh = gp.kvh;
+  const int b = gp.b;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
@@ -643,6 +658,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 
 }  // namespace abkv
 
+namespace {
+// Linear grid of the prefill kernels (grid_pos): num_q_tiles x 8 x batch workgroups; 0 when the launch's work-item
+// count would not fit the 32-bit grid size.
+unsigned prefill_grid(int num_q_tiles, int batch, int threads) {
+  const long n = (long)num_q_tiles * abkv::kHeadsKV * batch;
+  return n * threads > 0xFFFFFFFFL ? 0u : (unsigned)n;
+}
+}  // namespace
+
 extern "C" {
 
 int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
@@ -674,7 +698,8 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
   // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).
-  const dim3 grid(a.num_q_tiles, kHeadsKV, batch);
+  const unsigned grid = prefill_grid(a.num_q_tiles, batch, 512);
+  if (grid == 0) return (int)hipErrorInvalidValue;
   if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true>), grid, dim3(512), 0, stream, a);
   else hipLaunchKernelGGL((prefill_masked_kernel<2, false>), grid, dim3(512), 0, stream, a);
   return (int)hipGetLastError();
@@ -737,16 +762,17 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   a.dk_sb = dk_stride_b; a.dk_ss = dk_stride_s; a.dk_sh = dk_stride_h;
   a.dv = static_cast<__bf16*>(dv);
   a.dv_sb = dv_stride_b; a.dv_ss = dv_stride_s; a.dv_sh = dv_stride_h;
+  if (prefill_grid(f.num_q_tiles, batch, 512) == 0) return (int)hipErrorInvalidValue;
   const long rows = (long)batch * kHeadsQ * a.S0p;
   hipLaunchKernelGGL(prefill_bwd_prep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
-  const dim3 gq(f.num_q_tiles, kHeadsKV, batch);
+  const unsigned gq = prefill_grid(f.num_q_tiles, batch, 512);
   if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true>), gq, dim3(512), 0, stream, a);
   else hipLaunchKernelGGL((prefill_bwd_dq_kernel<false>), gq, dim3(512), 0, stream, a);
   err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
-  const dim3 gk(f.num_q_tiles, kHeadsKV, batch);
+  const unsigned gk = prefill_grid(f.num_q_tiles, batch, 256);
   if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true>), gk, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL((prefill_bwd_dkv_kernel<false>), gk, dim3(256), 0, stream, a);
   return (int)hipGetLastError();
