@@ -27,7 +27,8 @@ struct PagedPrefillArgs {
   float scale_log2;
   __bf16* out; long o_st, o_sh;                // [T, 32, 128]
   float* lse;                                  // [T, 32] natural log, or nullptr
-  int split_tiles;                             // > 0: key tiles per split (grid.z splits), partials to part_*
+  int num_tiles;                               // query tiles; the grid is 8 x num_tiles x splits (linear_block)
+  int split_tiles;                             // > 0: key tiles per split, partials to part_*
   int num_tokens;
   float* part_o;                               // [splits, T, 32, 128] un-normalised
   float* part_ml;                              // [splits, T, 32, 2] (running max in log2 units, sum)
@@ -82,9 +83,14 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   __shared__ __attribute__((aligned(16))) __bf16 V0[kTileElems], V1[kTileElems], V2[kTileElems];
   __bf16* const Kbuf[kStages] = {K0, K1, K2};
   __bf16* const Vbuf[kStages] = {V0, V1, V2};
-  const int r = a.tile_req[blockIdx.x];
-  const int q0 = a.tile_q0[blockIdx.x];
-  const int kvh = blockIdx.y;
+  // linear grid, KV head fastest, then query tile, then key split: workgroups go to the 8 XCDs round-robin by
+  // linear id, so the query tiles of one request that read the same K/V tiles (same head, same split) share an L2
+  const int l = blockIdx.x;
+  const int kvh = l % kHeadsKV;
+  const int tile = (l / kHeadsKV) % a.num_tiles;
+  const int split = l / (kHeadsKV * a.num_tiles);
+  const int r = a.tile_req[tile];
+  const int q0 = a.tile_q0[tile];
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int lane = tid & 63;
@@ -141,7 +147,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   const MaskGeom geo{};
   // key tiles of this block: all of them, or split z's share when the launch is split along the keys
   RangeWalk walk;
-  walk.kt_begin = a.split_tiles > 0 ? (int)blockIdx.z * a.split_tiles : 0;
+  walk.kt_begin = a.split_tiles > 0 ? split * a.split_tiles : 0;
   walk.kt_end = a.split_tiles > 0 ? min(n_k_tiles, walk.kt_begin + a.split_tiles) : n_k_tiles;
   walk.k_full = k_full;
   if constexpr (kSide) {
@@ -165,7 +171,7 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
     for (int u = 0; u < H; ++u) {
       const float l = l_run[u];
       const int head = kvh * kGroup + hbase + u;
-      const long row = ((long)(a.split_base + blockIdx.z) * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
+      const long row = ((long)(a.split_base + split) * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
       float* po = a.part_o + row * kHeadDim + 32 * j;
 #pragma unroll
       for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * acc_tile(t, j)) = o[t][u];
@@ -221,6 +227,15 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(PagedPrefillArgs a, in
 }
 
 }  // namespace abkv
+
+namespace {
+// Workgroups of a paged_prefill_kernel launch (8 x num_tiles x splits, 512 threads each); 0 when the work-item count
+// would not fit the 32-bit grid size.
+unsigned paged_grid(int num_tiles, int splits) {
+  const long n = (long)num_tiles * abkv::kHeadsKV * splits;
+  return n <= 0 || n * 512 > 0xFFFFFFFFL ? 0u : (unsigned)n;
+}
+}  // namespace
 
 extern "C" {
 
@@ -278,8 +293,10 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + (size_t)num_splits * num_tokens * kHeadsQ * kHeadDim;
   }
-  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(num_tiles, kHeadsKV, num_splits > 1 ? num_splits : 1),
-                     dim3(512), 0, stream, a);
+  const unsigned grid = paged_grid(num_tiles, num_splits > 1 ? num_splits : 1);
+  if (grid == 0) return (int)hipErrorInvalidValue;
+  a.num_tiles = num_tiles;
+  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(grid), dim3(512), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || num_splits <= 1) return (int)err;
   hipLaunchKernelGGL(paged_merge_kernel, dim3(num_tokens, kHeadsQ / 8), dim3(256), 0, stream, a, num_splits);
@@ -355,12 +372,15 @@ int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride
   a.side_max_pages = max_packed_per_seq;
   a.split_tiles = split_tiles;
   a.split_base = 0;
-  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(num_tiles, kHeadsKV, num_splits), dim3(512), 0, stream, a);
+  const unsigned grid_main = paged_grid(num_tiles, num_splits), grid_side = paged_grid(num_tiles, side_splits);
+  if (grid_main == 0 || grid_side == 0) return (int)hipErrorInvalidValue;
+  a.num_tiles = num_tiles;
+  hipLaunchKernelGGL(paged_prefill_kernel<false>, dim3(grid_main), dim3(512), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   a.split_tiles = side_split_tiles;
   a.split_base = num_splits;
-  hipLaunchKernelGGL(paged_prefill_kernel<true>, dim3(num_tiles, kHeadsKV, side_splits), dim3(512), 0, stream, a);
+  hipLaunchKernelGGL(paged_prefill_kernel<true>, dim3(grid_side), dim3(512), 0, stream, a);
   err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   hipLaunchKernelGGL(paged_merge_kernel, dim3(num_tokens, kHeadsQ / 8), dim3(256), 0, stream, a, total);
