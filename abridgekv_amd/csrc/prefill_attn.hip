@@ -233,24 +233,26 @@ struct PrefillBwdArgs {
 };
 
 __global__ __launch_bounds__(256) void prefill_bwd_prep_kernel(PrefillBwdArgs a) {
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (long)a.f.B * kHeadsQ * a.S0p) return;
+  // 16 lanes per (row, query head): lane c takes dims 8c .. 8c + 7 of O and dO (one 16-byte load each, so a wave reads
+  // four whole 256-byte rows), and the 16 partial dot products are summed by lane shuffles inside the group
+  const long idx = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const int c = threadIdx.x & 15;
+  if (idx >= (long)a.f.B * kHeadsQ * a.S0p) return;         // uniform over the 16 lanes of a row
   const int i = (int)(idx % a.S0p);
   const long bh = idx / a.S0p;
   const int h = (int)(bh % kHeadsQ), b = (int)(bh / kHeadsQ);
-  float l2 = INFINITY, d = 0.f;
+  float d = 0.f;
   if (i < a.f.S0) {
-    l2 = a.lse[bh * a.f.S0 + i] * 1.4426950408889634f;
     const __bf16* op = a.o + (long)b * a.o_sb + (long)i * a.o_ss + (long)h * a.o_sh;
     const __bf16* gp = a.dout + (long)b * a.g_sb + (long)i * a.g_ss + (long)h * a.g_sh;
-#pragma unroll 4
-    for (int c = 0; c < kHeadDim / 8; ++c) {
-      const u32x4 x = ld16g(op + 8 * c), y = ld16g(gp + 8 * c);
+    const u32x4 x = ld16g(op + 8 * c), y = ld16g(gp + 8 * c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) d += bf16_lo(x[e]) * bf16_lo(y[e]) + bf16_hi(x[e]) * bf16_hi(y[e]);
-    }
+    for (int e = 0; e < 4; ++e) d += bf16_lo(x[e]) * bf16_lo(y[e]) + bf16_hi(x[e]) * bf16_hi(y[e]);
   }
-  a.lse2[idx] = l2;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) d += __shfl_xor(d, m, 64);
+  if (c != 0) return;
+  a.lse2[idx] = i < a.f.S0 ? a.lse[bh * a.f.S0 + i] * 1.4426950408889634f : INFINITY;
   a.dvec[idx] = d;
 }
 
@@ -764,7 +766,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   a.dv_sb = dv_stride_b; a.dv_ss = dv_stride_s; a.dv_sh = dv_stride_h;
   if (prefill_grid(f.num_q_tiles, batch, 512) == 0) return (int)hipErrorInvalidValue;
   const long rows = (long)batch * kHeadsQ * a.S0p;
-  hipLaunchKernelGGL(prefill_bwd_prep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, a);
+  if (rows * 16 > 0xFFFFFFFFL) return (int)hipErrorInvalidValue;  // prep: 16 work-items per row and head
+  hipLaunchKernelGGL(prefill_bwd_prep_kernel, dim3((unsigned)((rows * 16 + 255) / 256)), dim3(256), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned gq = prefill_grid(f.num_q_tiles, batch, 512);
