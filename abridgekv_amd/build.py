@@ -18,7 +18,7 @@ DEVICE_SOURCES = ["decode_attn.hip", "kv_cache.hip", "prefill_attn.hip", "paged_
 HOST_SOURCES = ["planner.cpp"]
 
 # -packed-fp32-ops off: hipcc would otherwise emit v_pk_{add,mul,fma}_f32 from scalar float code.
-COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-I{PKG.parent / 'include'}"]
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                 "-munsafe-fp-atomics"]
 

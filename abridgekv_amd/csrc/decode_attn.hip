@@ -22,6 +22,7 @@
 // Output: normalised bf16 out [B, 32, 128] and natural-log LSE [B, 32] directly when a sequence has one split;
 // otherwise per split a normalised fp16 partial output with an fp32 record (m, l, scale), and a merge kernel (fp16
 // partials move half the bytes of fp32 ones: 2.1 % of the saturated launch time).
+#include "abridgekv_amd.h"
 #include "common.h"
 
 namespace abkv {

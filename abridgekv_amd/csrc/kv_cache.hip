@@ -391,7 +391,7 @@ int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, lo
     return (int)hipErrorInvalidValue;
   int log2_k = 0;
   if (block_c > 0) {
-    if (codes_k <= 0 || (codes_k & (codes_k - 1)) || (block_c & (block_c - 1)) || codes_k > block_c)
+    if (codes_k <= 0 || (codes_k & (codes_k - 1)) || codes_k > block_c)
       return (int)hipErrorInvalidValue;
     while ((1 << log2_k) < codes_k) ++log2_k;
   }

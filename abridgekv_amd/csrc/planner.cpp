@@ -10,6 +10,8 @@
 //   compacted spans ........ third_party/vllm_overlay/vllm/v1/compacted_spans.py:8-68, v1/request.py:263-321
 //   span removal ........... third_party/vllm_overlay/vllm/v1/core/sched/scheduler.py:2043-2204
 // Pure host code: no HIP call is made from this file.
+#include "abridgekv_amd.h"
+
 #include <stdint.h>
 #include <string.h>
 
@@ -152,14 +154,6 @@ using abkv::Request;
 extern "C" {
 
 // Error codes of the planner entry points.
-enum {
-  ABKV_OK = 0,
-  ABKV_ERR_ARG = -1,          // bad argument (null handle, out-of-range group, ...)
-  ABKV_ERR_NO_REQUEST = -2,   // unknown request id
-  ABKV_ERR_SPAN = -3,         // span rejected (the reference's SpanRemovalResult(success=False))
-  ABKV_ERR_POOL = -4,         // page pool exhausted inside an allocation that passed the total check
-  ABKV_ERR_CAPACITY = -5,     // output buffer too small
-};
 
 void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const int32_t* free_order,
                           int64_t max_model_len) {

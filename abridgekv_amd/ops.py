@@ -250,12 +250,25 @@ def rotary_cos_sin_from_model(rotary_emb, max_pos: int, device) -> torch.Tensor:
     return torch.cat([cos[0, :, :half], sin[0, :, :half]], dim=1).float().contiguous()
 
 
+def rope_bound(max_position: int, block_c: int = 0, codes_k: int = 0) -> int:
+    """Largest RoPE position of any token whose position (logical when block_c > 0) is <= max_position. In the
+    abridged layout block b's content rows map to b*C + offset and its code rows to b*C + (an offset < C), so a token
+    at logical (b, w) bounds every earlier token by b*C + min(w, C - 1)."""
+    if not block_c:
+        return int(max_position)
+    blk, w = divmod(int(max_position), block_c + codes_k)
+    return blk * block_c + min(w, block_c - 1)
+
+
 def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, positions: torch.Tensor,
                    cos_sin: torch.Tensor, slot_mapping: torch.Tensor | None = None,
-                   kv_cache: torch.Tensor | None = None, block_c: int = 0, codes_k: int = 0) -> None:
+                   kv_cache: torch.Tensor | None = None, block_c: int = 0, codes_k: int = 0,
+                   max_position: int | None = None) -> None:
     """Rotate q [T, 32, 128] and key [T, 8, 128] in place (NeoX halves) and write rotated key and value rows at
     slot_mapping (int64, < 0 = skip; None = rotate only). positions [T] int64: RoPE positions, or logical positions
-    of the abridged layout when block_c > 0 (mapped to bitrev RoPE positions on the device)."""
+    of the abridged layout when block_c > 0 (mapped to bitrev RoPE positions on the device; codes_k a power of two
+    <= block_c). ``max_position``: a host bound on ``positions`` (None: read back from the device, which
+    synchronises); the RoPE positions it implies must lie inside ``cos_sin`` (ValueError otherwise)."""
     T = positions.numel()
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
              and q.stride(2) == 1 and q.shape[0] >= T, "q must be cuda bf16 [T, 32, 128] with contiguous dims")
@@ -268,8 +281,8 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
     _require(cos_sin.is_cuda and cos_sin.dtype == torch.float32 and cos_sin.dim() == 2
              and cos_sin.shape[1] == HEAD_DIM and cos_sin.is_contiguous(), "cos_sin must be contiguous cuda fp32 [P, 128]")
     if block_c:
-        _require(block_c > 0 and codes_k > 0 and block_c & (block_c - 1) == 0 and codes_k & (codes_k - 1) == 0
-                 and codes_k <= block_c, "block_c and codes_k must be powers of two with codes_k <= block_c")
+        _require(block_c > 0 and codes_k > 0 and codes_k & (codes_k - 1) == 0 and codes_k <= block_c,
+                 "codes_k must be a power of two <= block_c")
     num_pages = 0
     if slot_mapping is not None:
         _check_cache(kv_cache)
@@ -278,6 +291,11 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
         num_pages = kv_cache.shape[0]
     if T == 0:
         return
+    if max_position is None:
+        max_position = int(positions.max())
+    _require(rope_bound(max_position, block_c, codes_k) < cos_sin.shape[0],
+             f"RoPE positions up to {rope_bound(max_position, block_c, codes_k)} exceed the cos/sin table "
+             f"({cos_sin.shape[0]} rows)")
     rc = lib().abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(key), key.stride(0), _ptr(value),
                                    value.stride(0), _ptr(positions), T, int(block_c), int(codes_k), _ptr(cos_sin),
                                    cos_sin.shape[0], _ptr(slot_mapping), _ptr(kv_cache), num_pages,
@@ -505,15 +523,16 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
         n_splits = max(1, int(split))
         split_tiles = -(-(-(-max_keys // 64)) // n_splits) if n_splits > 1 else 0
     ws, ws_bytes = None, 0
+    covered = int(qs[-1])                    # rows the launch writes; rows past q_start[-1] stay untouched
     if n_splits > 1:
         _require(n_splits * split_tiles * 64 >= max_keys, "key splits must cover every key")
-        ws_bytes = lib().abkv_paged_prefill_workspace_size(T, n_splits)
+        ws_bytes = lib().abkv_paged_prefill_workspace_size(covered, n_splits)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                        _ptr(block_table), _row_stride(block_table), W, _ptr(q_start_d),
                                        _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
                                        _ptr(causal_d), 1, scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
-                                       T, n_splits, split_tiles, _ptr(ws), ws_bytes, C.c_void_p(_stream()))
+                                       covered, n_splits, split_tiles, _ptr(ws), ws_bytes, C.c_void_p(_stream()))
     check(rc, "abkv_paged_prefill_attn")
     return out, lse
 
@@ -695,14 +714,15 @@ def paged_prefill_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, bloc
     side_splits, side_split_tiles = paged_split_plan(len(tiles), side_rows)
     if side_splits <= 1:
         side_splits, side_split_tiles = 1, side_tiles_all
-    ws_bytes = lib().abkv_paged_prefill_workspace_size(T, n_splits + side_splits)
+    covered = int(qs[-1])                    # rows the launch writes; rows past q_start[-1] stay untouched
+    ws_bytes = lib().abkv_paged_prefill_workspace_size(covered, n_splits + side_splits)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     rc = lib().abkv_paged_prefill_attn_packed(
         _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0], _ptr(block_table),
         _row_stride(block_table), W, _ptr(meta[:o1]), _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(tl[0]), _ptr(tl[1]),
         len(tiles), _ptr(meta[o3:o4]), 1, _ptr(head_quota_dev), _ptr(packed_pool), packed_pool.shape[0], rows, hq_c,
         _ptr(packed_table), _row_stride(packed_table), _ptr(packed_count), max_packed, scale, _ptr(out),
-        out.stride(0), out.stride(1), _ptr(lse), T, n_splits, split_tiles, side_splits, side_split_tiles, _ptr(ws),
+        out.stride(0), out.stride(1), _ptr(lse), covered, n_splits, split_tiles, side_splits, side_split_tiles, _ptr(ws),
         ws_bytes, C.c_void_p(_stream()))
     check(rc, "abkv_paged_prefill_attn_packed")
     return out, lse

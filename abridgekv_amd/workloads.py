@@ -248,6 +248,8 @@ class CompactionState:
     pending: np.ndarray              # the compaction calls of the step, abkv_planner_apply_events rows
     prompt_lens: np.ndarray
     closed_blocks: np.ndarray
+    history: np.ndarray              # the scheduler events replayed before the step (abkv_planner_apply_events rows)
+    free_order: np.ndarray           # the pool's initial free-queue order
 
     def compact(self, as_arrays: bool = False):
         """Run the step's span removals (processor order per request: response content in every group, then code
@@ -286,6 +288,7 @@ def build_compaction_state(B=64, seed=0, layer_quotas=QWEN3_4B_LAYER_QUOTAS, C=B
                     rows.append((start + st, 1, r, k, (2, r, a, b, m, 0)))
             else:
                 rows.append((start + st, 0, r, k, (1, r, a, 0, 0, 0)))
-    planner.apply_events(_schedule_rows(rows))
+    history = _schedule_rows(rows)
+    planner.apply_events(history)
     planner.take_step_outputs()                              # earlier steps' outputs were executed long ago
-    return CompactionState(planner, groups, gq, num_pages, np.asarray(pending, np.int64), P, nb)
+    return CompactionState(planner, groups, gq, num_pages, np.asarray(pending, np.int64), P, nb, history, free_order)

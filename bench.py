@@ -71,6 +71,29 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_threads(torch) -> dict:
+    """Give torch every host core this process may use and describe the host for the cpu_baseline record. The
+    count is the CPU affinity set (on a shared GPU host that is this job's share, not the machine), capped by
+    OMP_NUM_THREADS when the launcher sets it; nproc and the CPU model are recorded beside it."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    torch.set_num_threads(n)
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cores": torch.get_num_threads(), "nproc": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "omp_num_threads": omp or None, "cpu": model}
+
+
 def copy_bandwidth(torch, gb=8.0):
     """Measured device copy bandwidth (read + write bytes / time) of a large torch copy."""
     n = int(gb * 1e9) // 2
@@ -296,6 +319,7 @@ def bench_serving(args, torch):
     from abridgekv_amd.serving import ServingStress
 
     T, P = workloads_lengths(args)
+    copy_bw = copy_bandwidth(torch)                            # before the 212 GB of caches are allocated
     t0 = time.perf_counter()
     s = ServingStress(T, P, seed=args.seed, split_pages=args.split_pages,
                       growth_tokens=args.steps + args.warmup + 16)
@@ -337,17 +361,18 @@ def bench_serving(args, torch):
                      "alg_bytes_per_launch": alg / n_launch, "avg_launch_us": dec_s / n_launch * 1e6},
         "decode_attn_ms_per_step": dec_s / args.steps * 1e3,
         "code_steps": stats["code_steps"], "compacted_rows_moved": stats["moved_rows"],
-        "state_build_s": build_s,
+        "state_build_s": build_s, "copy_bw_gbps_measured": copy_bw,
     }
     if not args.no_cpu_baseline:
+        host = cpu_threads(torch)
         n = min(args.cpu_seqs, B)
         view = _CpuView(s)
         tps, reps, el = cpu_baseline(torch, view, s.caches, [s.q_pool[:B]] * s.L, ops.default_scale(), n)
-        res["cpu_baseline"] = {"value": tps, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        res["cpu_baseline"] = {"value": tps, "unit": "tokens/s", "kind": "port", **host,
                                "sample": f"first {n} requests of the batch at the end of the run, one layer per KV "
                                          f"group (6 of 36, scaled x6), {reps} reps in {el:.1f} s; torch CPU "
                                          f"restatement of the reference arithmetic (bf16 scores, fp32 softmax, bf16 "
-                                         f"probs)", "cpu": platform.processor() or platform.machine()}
+                                         f"probs)"}
     return res
 
 
@@ -582,13 +607,13 @@ def main():
     except RuntimeError as exc:                               # out of memory next to a 200 GB cache
         res["copy_bw_gbps_measured"] = f"skipped: {exc.__class__.__name__}"
     if not args.no_cpu_baseline:
+        host = cpu_threads(torch)
         n = min(args.cpu_seqs, B)
         tps, reps, el = cpu_baseline(torch, st, caches, qs, scale, n)
-        res["cpu_baseline"] = {"value": tps, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        res["cpu_baseline"] = {"value": tps, "unit": "tokens/s", "kind": "port", **host,
                                "sample": f"first {n} requests of the same batch, one layer per KV group (6 of 36, "
                                          f"scaled x6), {reps} reps in {el:.1f} s; torch CPU restatement of the "
-                                         f"reference arithmetic (bf16 scores, fp32 softmax, bf16 probs)",
-                               "cpu": platform.processor() or platform.machine()}
+                                         f"reference arithmetic (bf16 scores, fp32 softmax, bf16 probs)"}
     print(json.dumps(res), flush=True)
     return 0
 

@@ -20,6 +20,17 @@ extern "C" {
 
 typedef struct ihipStream_t* abkv_stream_t; /* == hipStream_t */
 
+/* Library error codes (negative; kernel entry points otherwise return 0 or a positive hipError_t code). */
+enum {
+  ABKV_OK = 0,
+  ABKV_ERR_ARG = -1,         /* bad argument (null handle, out-of-range group, ...) */
+  ABKV_ERR_NO_REQUEST = -2,  /* unknown request id */
+  ABKV_ERR_SPAN = -3,        /* the reference's SpanRemovalResult(success=False); message in abkv_planner_last_error */
+  ABKV_ERR_POOL = -4,        /* page pool exhausted inside an allocation that passed the total check */
+  ABKV_ERR_CAPACITY = -5,    /* output buffer too small */
+  ABKV_ERR_SCRATCH = -6      /* abkv_decode_attn_noalloc: the call needs more than the static scratch holds */
+};
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Decode attention (kernel 1).
  * Replaces the FlashInfer BatchDecodeWithPagedKVCache call of the stock vLLM backend that the reference's overlay
@@ -71,9 +82,10 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
  * block_table.py:186-197). q [T, 32, 128] (strides in elements, dims contiguous) and key [T, 8, 128] are rotated in
  * place; rotated key and value rows are written at slot_mapping[t] (NULL: rotate only; < 0 or past the cache: skip).
  * positions [T] int64: RoPE positions when block_c == 0; otherwise logical positions of the abridged layout (period
- * block_c + codes_k, both powers of two) mapped on the device to block * block_c + (offset < block_c ? offset :
- * floor(bitrev(offset - block_c) * block_c / codes_k)). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
- * frequencies then their sin; positions are clamped into [0, max_pos). */
+ * block_c + codes_k, codes_k a power of two <= block_c) mapped on the device to block * block_c + (offset < block_c ?
+ * offset : floor(bitrev(offset - block_c) * block_c / codes_k)). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
+ * frequencies then their sin. The caller guarantees every RoPE position is < max_pos (the Python wrapper checks it);
+ * the kernel clamps positions into [0, max_pos) only so that no read leaves the table. */
 int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, long key_stride_t, const void* value,
                         long value_stride_t, const int64_t* positions, int num_tokens, int block_c, int codes_k,
                         const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
@@ -133,8 +145,9 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
  * row). All index arrays are device int32. lse [T, 32] or NULL. num_splits > 1 splits every tile's keys into
  * num_splits ranges of split_tiles 64-key tiles (split z covers tiles [z * split_tiles, (z + 1) * split_tiles); the
  * ranges must cover every request's keys) computed by separate workgroups and merged; the partials use workspace
- * (>= abkv_paged_prefill_workspace_size(num_tokens, num_splits) bytes; num_tokens = T). num_splits <= 1: no split,
- * no workspace.
+ * (>= abkv_paged_prefill_workspace_size(num_tokens, num_splits) bytes). num_tokens = q_start[num_reqs], the rows
+ * the launch covers: the split merge writes exactly those rows, and rows of q / out past them are never touched.
+ * num_splits <= 1: no split, no workspace.
  * ------------------------------------------------------------------------------------------------------------- */
 size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits);
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
@@ -236,14 +249,6 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
  * 157-345), KVCacheManager.allocate_slots (v1/core/kv_cache_manager.py:206-340), CompactedSpanIndex
  * (v1/compacted_spans.py:8-68). One planner = one page pool shared by num_groups KV-cache groups.
  * ------------------------------------------------------------------------------------------------------------- */
-enum {
-  ABKV_OK = 0,
-  ABKV_ERR_ARG = -1,
-  ABKV_ERR_NO_REQUEST = -2,
-  ABKV_ERR_SPAN = -3,     /* the reference's SpanRemovalResult(success=False); message in abkv_planner_last_error */
-  ABKV_ERR_POOL = -4,
-  ABKV_ERR_CAPACITY = -5
-};
 
 /* free_order: NULL (pages 1..num_blocks-1 in id order, page 0 null -- the reference's construction) or a
  * permutation of 1..num_blocks-1 giving the initial free-queue order. */

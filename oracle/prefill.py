@@ -24,10 +24,16 @@ import numpy as np
 
 def arith_mask(C, K, N, prompt_len=None, head_quota=None):
     """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
+    S0 = N * (C + K)
+    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota)
+
+
+def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None):
+    """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
+    S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
     per = C + K
-    S0 = N * per
-    q = np.arange(S0, dtype=np.int64).reshape(S0, 1)
-    kv = np.arange(S0, dtype=np.int64).reshape(1, S0)
+    q = np.asarray(rows, dtype=np.int64).reshape(-1, 1)
+    kv = np.asarray(cols, dtype=np.int64).reshape(1, -1)
     qb, kb = q // per, kv // per
     qw, kw = q - qb * per, kv - kb * per
     k_content = kw < C
@@ -104,6 +110,99 @@ def masked_attention_fp64(q, k, v, mask, scale):
         out[:, h] = (e / z) @ v[:, h // g]
         lse[:, h] = (mx + np.log(z))[:, 0]
     return out, lse
+
+
+def masked_attention_rows_fp64(q, k, v, mask_rows, rows, scale):
+    """:func:`masked_attention_fp64` restricted to query ``rows`` (every key is still considered).
+
+    mask_rows: [len(rows), S] or [Hq, len(rows), S] (``arith_mask_block(.., rows, all keys, ..)``). Returns
+    out [R, Hq, D], lse [R, Hq]. Costs R x S per head instead of S x S, so full-length sequences can be sampled."""
+    rows = np.asarray(rows, dtype=np.int64)
+    return masked_attention_fp64_qk(np.asarray(q)[rows], k, v, mask_rows, scale)
+
+
+def masked_attention_fp64_qk(q_rows, k, v, mask_rows, scale):
+    """Attention of the given query rows [R, Hq, D] over all keys [S, Hkv, D] under mask_rows ([R, S] or
+    [Hq, R, S]); float64, GQA by head // (Hq / Hkv). Returns out [R, Hq, D], lse [R, Hq]."""
+    q = np.asarray(q_rows, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    R, Hq, D = q.shape
+    g = Hq // k.shape[1]
+    out = np.zeros((R, Hq, D))
+    lse = np.zeros((R, Hq))
+    for h in range(Hq):
+        m = mask_rows if mask_rows.ndim == 2 else mask_rows[h]
+        s = np.where(m, (q[:, h] @ k[:, h // g].T) * scale, -np.inf)
+        mx = s.max(axis=1, keepdims=True)
+        e = np.exp(s - mx)
+        z = e.sum(axis=1, keepdims=True)
+        out[:, h] = (e / z) @ v[:, h // g]
+        lse[:, h] = (mx + np.log(z))[:, 0]
+    return out, lse
+
+
+def masked_attention_query_grads_fp64(q, k, v, dout, mask_rows, rows, scale):
+    """dq of :func:`masked_attention_grads_fp64` for query ``rows`` only: row i's gradient needs only row i's own
+    softmax (dq_i = scale * sum_j P_ij (dP_ij - D_i) k_j with D_i = sum_j P_ij dP_ij). Returns dq [R, Hq, D]."""
+    rows = np.asarray(rows, dtype=np.int64)
+    qr = np.asarray(q, np.float64)[rows]
+    dr = np.asarray(dout, np.float64)[rows]
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    R, Hq, D = qr.shape
+    g = Hq // k.shape[1]
+    dq = np.zeros((R, Hq, D))
+    for h in range(Hq):
+        hk = h // g
+        m = mask_rows if mask_rows.ndim == 2 else mask_rows[h]
+        p = _softmax_rows(np.where(m, (qr[:, h] @ k[:, hk].T) * scale, -np.inf))
+        dp = dr[:, h] @ v[:, hk].T
+        ds = p * (dp - (p * dp).sum(axis=1, keepdims=True))
+        dq[:, h] = scale * ds @ k[:, hk]
+    return dq
+
+
+def masked_attention_key_grads_fp64(q, k, v, dout, mask_fn, keys, scale):
+    """dk, dv of :func:`masked_attention_grads_fp64` for the key rows ``keys`` only.
+
+    ``mask_fn(rows, cols)`` returns the mask block ([R, Cc] or [Hq, R, Cc]). Only the queries that see one of the keys
+    contribute; each of them needs its whole softmax row (for P and D_i), so the cost is (#such queries) x S per head:
+    cheap for keys late in the sequence. Returns dk, dv [len(keys), Hkv, D]."""
+    keys = np.asarray(keys, dtype=np.int64)
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    dout = np.asarray(dout, np.float64)
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    cols = mask_fn(np.arange(S), keys)
+    seen = cols.any(axis=-1) if cols.ndim == 2 else cols.any(axis=(0, 2))
+    qi = np.flatnonzero(seen)
+    dk = np.zeros((keys.size, Hkv, D))
+    dv = np.zeros((keys.size, Hkv, D))
+    if qi.size == 0:
+        return dk, dv
+    m_all = mask_fn(qi, np.arange(S))
+    for h in range(Hq):
+        hk = h // g
+        m = m_all if m_all.ndim == 2 else m_all[h]
+        p = _softmax_rows(np.where(m, (q[qi, h] @ k[:, hk].T) * scale, -np.inf))
+        dp = dout[qi, h] @ v[:, hk].T
+        ds = p * (dp - (p * dp).sum(axis=1, keepdims=True))
+        dk[:, hk] += scale * ds[:, keys].T @ q[qi, h]
+        dv[:, hk] += p[:, keys].T @ dout[qi, h]
+    return dk, dv
+
+
+def _softmax_rows(s):
+    """Row softmax of masked scores (-inf = hidden); an all-hidden row gives zeros."""
+    mx = s.max(axis=1, keepdims=True)
+    ok = np.isfinite(mx)
+    e = np.where(ok, np.exp(s - np.where(ok, mx, 0.0)), 0.0)
+    z = e.sum(axis=1, keepdims=True)
+    return e / np.where(z > 0, z, 1.0)
 
 
 def visible_pairs(C, K, N, prompt_len=None):

@@ -4,6 +4,7 @@ import re
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from abridgekv_amd import _lib
@@ -65,3 +66,15 @@ def test_rope_table_matches_hf_rotary():
     pos, i = 1234, 5
     want = math.cos(pos * 1e6 ** (-2 * i / 128))
     assert abs(table[pos, i].item() - want) < 1e-4
+
+
+@pytest.mark.parametrize("C,K", [(64, 16), (48, 16), (512, 256)])
+def test_rope_bound_is_the_running_maximum_of_the_bitrev_positions(C, K):
+    """ops.rope_bound(p) = max RoPE position over logical positions 0..p (brute force over the oracle's layout)."""
+    from abridgekv_amd import ops
+    from oracle import layout as ol
+    logical = np.arange(6 * (C + K))
+    running = np.maximum.accumulate(ol.bitrev_rope_positions(logical, C, K))
+    got = np.array([ops.rope_bound(int(p), C, K) for p in logical])
+    assert np.array_equal(got, running)
+    assert ops.rope_bound(1234) == 1234

@@ -114,3 +114,26 @@ def test_mixed_code_and_prompt_chunk_batch():
                          causal[r])
         assert np.abs(out[q_start[r]: q_start[r + 1]] - ro).max() <= TOL
         assert np.abs(lse[q_start[r]: q_start[r + 1]] - rl).max() <= TOL
+
+
+def test_rows_past_the_covered_queries_are_untouched_with_key_splits():
+    """q_start[-1] < T: the split merge writes only the rows the requests cover; the rest of out keeps its values."""
+    from abridgekv_amd import ops
+    resident = [900, 1500]
+    cache, tables = _setup([r + 64 for r in resident], 300, 5)
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(6)
+    T = 200
+    q = torch.randn((T, 32, 128), generator=g).to(torch.bfloat16).to(dev)
+    out = torch.full((T, 32, 128), 7.0, dtype=torch.bfloat16, device=dev)
+    q_start = [0, 64, 128]
+    kv_limit = [r + 32 for r in resident]
+    ops.paged_prefill_attention(q, cache.to(dev), torch.from_numpy(tables).to(dev), q_start, resident, kv_limit,
+                                False, out=out, split=3)
+    torch.cuda.synchronize()
+    assert bool((out[128:] == 7.0).all())
+    cf = cache.float().numpy()
+    for r in range(2):
+        ro, _ = _oracle(q[q_start[r]: q_start[r + 1]].float().cpu().numpy(), cf, tables[r], resident[r], kv_limit[r],
+                        causal=False)
+        assert np.abs(out[q_start[r]: q_start[r + 1]].float().cpu().numpy() - ro).max() <= TOL

@@ -85,3 +85,46 @@ def test_strided_hf_layout():
                                           v_bhsd.transpose(1, 2).contiguous(), C, K, N)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def config4_sample_rows(C, K, N, rng, extra=24):
+    """Query rows of the config-4 layout worth checking: the first and last tiles, tile-diagonal rows (first / last
+    row of a 64-row tile), the content / code boundary, code rows, in an early, a middle and the last block, plus
+    seeded random rows."""
+    per = C + K
+    picks = set()
+    for b in (0, 1, N // 2, N - 1):
+        base = b * per
+        picks.update(base + x for x in (0, 1, 62, 63, 64, 65, 255, 256, C - 1, C, C + 1, C + 63, C + 64, per - 1))
+    picks.update(rng.integers(0, N * per, extra).tolist())
+    return np.array(sorted(p for p in picks if p < N * per))
+
+
+def test_config4_full_size_sampled_rows():
+    """The benched launch itself: B=4, N=16 blocks of [512 content | 128 codes] (S0=10240, 160 query tiles per
+    sequence), 512-token raw prompt. Every output and LSE is finite; sampled rows of every sequence match the float64
+    oracle evaluated on those rows over all 10240 keys."""
+    from abridgekv_amd import ops
+    B, C, K, N = 4, 512, 128, 16
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(40)
+    q = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    pl = torch.full((B,), 512, dtype=torch.int32, device=dev)
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    rng = np.random.default_rng(4)
+    worst = 0.0
+    for b in range(B):
+        rows = config4_sample_rows(C, K, N, rng)
+        mask = op.arith_mask_block(C, K, N, rows, np.arange(S0), [512])[0]
+        qb, kb, vb = (t[b].float().cpu().numpy() for t in (q, k, v))
+        ref_o, ref_l = op.masked_attention_rows_fp64(qb, kb, vb, mask, rows, 128 ** -0.5)
+        got_o = out[b].float().cpu().numpy()[rows]
+        got_l = lse[b].cpu().numpy().T[rows]
+        worst = max(worst, float(np.abs(got_o - ref_o).max()), float(np.abs(got_l - ref_l).max()))
+    assert worst <= TOL, worst

@@ -86,3 +86,56 @@ def test_autograd_through_hf_attention_layout():
     for t, r in zip((q, k, v), ref):
         mine = t.grad[0].transpose(0, 1).float().cpu().numpy()
         assert np.abs(mine - r).max() <= 2e-2 * np.abs(r).max() + 2e-3
+
+
+def test_config4_geometry_full_oracle():
+    """C=512 / K=128 blocks (tiles of the benched geometry), N=4, two sequences with different raw prompts; every
+    gradient element against the full float64 oracle."""
+    _check(C=512, K=128, N=4, B=2, prompt_len=[512, 300], seed=5)
+
+
+def test_config4_full_size_sampled():
+    """The benched backward launch: B=4, N=16 blocks of [512 | 128] (S0=10240), 512-token raw prompt. dq, dk, dv are
+    finite everywhere; dq of sampled query rows (every sequence) and dk / dv of sampled keys of the last block (first
+    and last sequence) match the float64 oracle (tolerance 2e-2 x the largest |reference| + 2e-3 per tensor)."""
+    from abridgekv_amd import ops
+    from tests.test_gpu_prefill import config4_sample_rows
+    B, C, K, N = 4, 512, 128, 16
+    S0 = N * (C + K)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(41)
+    q = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    dout = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    pl = torch.full((B,), 512, dtype=torch.int32, device=dev)
+    lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
+    dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+    torch.cuda.synchronize()
+    for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert torch.isfinite(t).all(), name
+    rng = np.random.default_rng(5)
+    scale = 128 ** -0.5
+    last = (N - 1) * (C + K)
+    keys = np.array([last, last + 1, last + 63, last + 64, last + 300, last + C - 1, last + C, last + C + 1,
+                     last + C + 64, S0 - 1])
+
+    def close(name, got, ref):
+        err = float(np.abs(got - ref).max())
+        bound = 2e-2 * float(np.abs(ref).max()) + 2e-3
+        print(f"{name}: max err {err:.3e}, bound {bound:.3e}")
+        assert err <= bound, (name, err, bound)
+
+    for b in range(B):
+        qb, kb, vb, gb = (t[b].float().cpu().numpy() for t in (q, k, v, dout))
+        rows = config4_sample_rows(C, K, N, rng, extra=8)
+        mrows = op.arith_mask_block(C, K, N, rows, np.arange(S0), [512])[0]
+        close(f"dq b{b}", dq[b].float().cpu().numpy()[rows],
+              op.masked_attention_query_grads_fp64(qb, kb, vb, gb, mrows, rows, scale))
+        if b in (0, B - 1):
+            def mask_fn(r, c):
+                return op.arith_mask_block(C, K, N, r, c, [512])[0]
+            ref_k, ref_v = op.masked_attention_key_grads_fp64(qb, kb, vb, gb, mask_fn, keys, scale)
+            close(f"dk b{b}", dk[b].float().cpu().numpy()[keys], ref_k)
+            close(f"dv b{b}", dv[b].float().cpu().numpy()[keys], ref_v)

@@ -26,12 +26,14 @@ def _within_half_ulp(got, want):
     return bool(((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-6).all())
 
 
-@pytest.mark.parametrize("logical", [False, True])
-def test_rotation_and_cache_rows(logical):
+@pytest.mark.parametrize("logical,C,K", [(False, 64, 16), (True, 64, 16), (True, 48, 16)])
+def test_rotation_and_cache_rows(logical, C, K):
+    """Plain RoPE positions, and logical positions of the abridged layout mapped on the device (also with a block
+    size that is not a power of two: only the code count must be one)."""
     from abridgekv_amd import ops
     dev = torch.device("cuda")
     g = torch.Generator().manual_seed(11)
-    T, C, K, max_pos = 300, 64, 16, 8192
+    T, max_pos = 300, 8192
     q = torch.randn((T, 32, 128), generator=g).to(torch.bfloat16)
     k = (torch.randn((T, 8, 128), generator=g) * 3).to(torch.bfloat16)
     v = torch.randn((T, 8, 128), generator=g).to(torch.bfloat16)
@@ -62,3 +64,20 @@ def test_rotation_and_cache_rows(logical):
     flat_new = cc.permute(0, 2, 1, 3, 4).reshape(num_pages * 16, 2, 8, 128)
     flat_old = cache.permute(0, 2, 1, 3, 4).reshape(num_pages * 16, 2, 8, 128)
     assert torch.equal(flat_new[untouched], flat_old[untouched])
+
+
+def test_positions_past_the_table_are_rejected_on_the_host():
+    """A cos/sin table shorter than the largest RoPE position raises before any launch (no silent clamping)."""
+    from abridgekv_amd import ops
+    dev = torch.device("cuda")
+    q = torch.zeros((2, 32, 128), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((2, 8, 128), dtype=torch.bfloat16, device=dev)
+    table = ops.rope_cos_sin_cache(100).to(dev)
+    with pytest.raises(ValueError, match="cos/sin table"):
+        ops.rope_kv_append(q, k, k.clone(), torch.tensor([3, 100], device=dev), table)
+    with pytest.raises(ValueError, match="cos/sin table"):        # logical 260 = block 3, content row 20 -> 212
+        ops.rope_kv_append(q, k, k.clone(), torch.tensor([0, 260], device=dev), ops.rope_cos_sin_cache(212).to(dev),
+                           block_c=64, codes_k=16, max_position=260)
+    ops.rope_kv_append(q, k, k.clone(), torch.tensor([0, 260], device=dev), ops.rope_cos_sin_cache(213).to(dev),
+                       block_c=64, codes_k=16, max_position=260)
+    torch.cuda.synchronize()

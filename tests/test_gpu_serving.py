@@ -36,3 +36,37 @@ def test_serving_loop_layout_and_decode():
     torch.cuda.synchronize()
     ref, _ = od.decode_paged_fp64(q.float().numpy(), cache.float().cpu().numpy(), s.tables[g], lens, 128 ** -0.5)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+
+
+def test_serving_loop_served_geometry():
+    """Served geometry: C=512, K=256, the Qwen3-4B per-layer quotas (6 KV-cache groups, 36 layers), B=32 requests,
+    run until every request has closed at least two blocks (code step + compaction each). Every row written during the
+    run holds the logical position the planner maps it to; decode over the final state of the largest and the
+    smallest quota group matches the float64 oracle on sampled requests."""
+    from abridgekv_amd import ops
+    from abridgekv_amd.serving import ServingStress
+    rng = np.random.default_rng(7)
+    B = 32
+    T = rng.integers(2048, 6000, B)
+    P = rng.integers(128, 1025, B)
+    steps = 2 * 512 + 40
+    s = ServingStress(T, P, seed=7, growth_tokens=steps + 64, tag=True)
+    s.run(steps)
+    s.flush()
+    torch.cuda.synchronize()
+    assert s.stats["code_steps"] >= 2 * B, s.stats
+    assert s.check_layout() > B * steps
+    dev = torch.device("cuda")
+    for g in (0, s.G - 1):
+        cache = s.by_group[g][0]
+        lens = s.seq_lens[g].astype(np.int32)
+        q = torch.randn((B, 32, 128), generator=torch.Generator().manual_seed(g)).to(torch.bfloat16)
+        bt = torch.from_numpy(s.tables[g]).to(dev)
+        out, _ = ops.decode_attention(q.to(dev), cache, bt, torch.from_numpy(lens).to(dev), 128 ** -0.5)
+        torch.cuda.synchronize()
+        for b in sorted({int(np.argmin(lens)), int(np.argmax(lens)), 5}):
+            n = int(lens[b])
+            pos = torch.arange(n, device=dev)
+            rows = cache[bt[b].long()[pos // 16], :, pos % 16].float().cpu().numpy()
+            ref, _ = od.decode_fp64(q[b].float().numpy(), rows[:, 0], rows[:, 1], 128 ** -0.5)
+            assert np.abs(out[b].float().cpu().numpy() - ref).max() <= 2e-2, (g, b)

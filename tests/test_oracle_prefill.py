@@ -160,3 +160,48 @@ def test_masked_attention_grads_match_autograd_and_finite_differences():
             args2 = [a2 if arr is x else x for x in (q, k, v)]
             fd = (loss(*args1) - loss(*args2)) / (2 * eps)
             assert abs(fd - grad[idx]) <= 1e-6 * max(1.0, abs(fd)), (idx, fd, grad[idx])
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_mask_block_equals_role_mask_slices(seed):
+    """arith_mask_block (sampled rows x sampled keys) against the independent role/table restatement, with a raw
+    prompt and per-head quotas, on unsorted and repeated index sets."""
+    rng = np.random.default_rng(seed)
+    C, K, N = 8, 4, 4
+    S = N * (C + K)
+    rows = rng.integers(0, S, 17)
+    cols = rng.integers(0, S, 23)
+    pl, hq = [int(rng.integers(0, 2 * C))], rng.integers(1, K + 1, 4).tolist()
+    got = op.arith_mask_block(C, K, N, rows, cols, pl, hq)[0]
+    ref = op.role_mask(C, K, N, pl, hq)[0][:, rows][:, :, cols]
+    assert np.array_equal(got, ref)
+    assert np.array_equal(op.arith_mask_block(C, K, N, rows, cols), op.role_mask(C, K, N)[rows][:, cols])
+
+
+def test_row_and_key_restricted_attention_equal_the_full_forms():
+    """The sampled-row forward, the sampled-row dq and the sampled-key dk/dv equal the corresponding rows of the full
+    fp64 forms (which are pinned against autograd and central differences above)."""
+    rng = np.random.default_rng(11)
+    C, K, N, Hq, Hkv, D = 6, 3, 4, 4, 2, 5
+    S = N * (C + K)
+    pl, hq = [5], [3, 1, 2, 3]
+    mask = op.arith_mask(C, K, N, pl, hq)[0]
+    q, k, v, dout = (rng.standard_normal(sh) for sh in ((S, Hq, D), (S, Hkv, D), (S, Hkv, D), (S, Hq, D)))
+    scale = 0.6
+    out, lse = op.masked_attention_fp64(q, k, v, mask, scale)
+    dq, dk, dv = op.masked_attention_grads_fp64(q, k, v, mask, scale, dout)
+    rows = np.array([0, 3, C, C + K - 1, S - 1, 2 * (C + K) + 1])
+    mrows = op.arith_mask_block(C, K, N, rows, np.arange(S), pl, hq)[0]
+    o_r, l_r = op.masked_attention_rows_fp64(q, k, v, mrows, rows, scale)
+    np.testing.assert_allclose(o_r, out[rows], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(l_r, lse[rows], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(op.masked_attention_query_grads_fp64(q, k, v, dout, mrows, rows, scale), dq[rows],
+                               rtol=1e-10, atol=1e-12)
+    keys = np.array([0, 4, C, S - K - 1, S - 1, S - K])
+
+    def mask_fn(r, c):
+        return op.arith_mask_block(C, K, N, r, c, pl, hq)[0]
+
+    dk_r, dv_r = op.masked_attention_key_grads_fp64(q, k, v, dout, mask_fn, keys, scale)
+    np.testing.assert_allclose(dk_r, dk[keys], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dv_r, dv[keys], rtol=1e-10, atol=1e-12)

@@ -93,3 +93,37 @@ def test_free_request_returns_pages_in_reverse_group_order():
     o.free_request(1)
     n.free(1)
     assert o.pool.free_queue.order() == n.free_queue()
+
+
+def test_compaction_workload_64_sequences_matches_oracle():
+    """The compaction workload at its benched size: 64 sequences with seeded prompts and 0-3 earlier closed blocks,
+    a seeded fragmented free list, the served geometry (C=512, K=256, six Qwen3-4B quota groups). The whole replayed
+    history and then the compaction step itself go through the oracle planner; copy-op batches (per request, per
+    group, in order), truncations, free-queue order, page lists, compacted counts, span maps and the page tables the
+    worker would hold must all be identical."""
+    from abridgekv_amd import workloads
+    from tests.planner_harness import apply_events_oracle
+
+    st = workloads.build_compaction_state(64, seed=0)
+    G = len(st.groups)
+    oracle = oc.Planner(st.num_pages, G, 16, free_order=st.free_order)
+    apply_events_oracle(oracle, st.history)
+    oracle.take_step_outputs()
+    rids = list(range(64))
+    compare_state(oracle, st.planner, rids)
+    apply_events_oracle(oracle, st.pending)
+    ops_o, tr_o = oracle.take_step_outputs()
+    st.planner.apply_events(st.pending)
+    out = st.planner.take_step_outputs()
+    assert ops_o == out.kv_copy_operations
+    assert list(ops_o) == list(out.kv_copy_operations)
+    assert tr_o == out.block_table_truncations
+    assert sum(len(b) for v in ops_o.values() for g in v for b in g) > 64 * 256
+    compare_state(oracle, st.planner, rids)
+    for g in range(G):
+        W = max(len(oracle.block_ids(r)[g]) for r in rids)
+        ref = np.zeros((64, W), np.int32)
+        for r in rids:
+            ids = oracle.block_ids(r)[g]
+            ref[r, :len(ids)] = ids
+        assert np.array_equal(st.planner.fill_block_table(rids, g, W), ref), f"group {g}"
