@@ -10,13 +10,15 @@ One metadata object describes one KV-cache group on one step (each group has its
 table, gpu_model_runner.py:1672-1682). A step's batch is ordered decodes first (one query token each, the
 reorder FlashInfer applies with decode threshold 1) and then multi-token requests:
 
-* decode requests -> ``abkv_decode_attn`` (split-KV decode; graph-capturable, fixed workspace);
+* decode requests -> ``abkv_decode_attn`` (split-KV decode; graph-capturable, fixed workspace), called as the
+  custom op ``torch.ops.abridgekv.decode_attn`` so compiled callers keep it as one node;
 * prompt chunks -> ``abkv_paged_prefill_attn`` causal;
 * CompressLM code-step requests -> ``abkv_paged_prefill_attn`` non-causal with the key limit
   ``code_start + quota``: the physical-quota code mask of gpu_model_runner.py:2042-2107 (all resident rows, the
   block's own code slots ``>= quota`` hidden; compresslm_masks.py:165-239) expressed as a per-request limit.
 
-New K/V rows are written by ``abkv_kv_append`` before attention (``reshape_and_cache`` semantics: slot < 0 skips).
+New K/V rows are written by ``abkv_kv_append`` (``torch.ops.abridgekv.kv_append``) before attention
+(``reshape_and_cache`` semantics: slot < 0 skips).
 """
 from __future__ import annotations
 
@@ -26,6 +28,7 @@ import numpy as np
 import torch
 
 from . import ops
+from . import torch_ops  # noqa: F401  (torch.ops.abridgekv.*)
 
 NOT_CODE = -1
 
@@ -145,8 +148,13 @@ class AbridgeMetadataBuilder:
             self._workspace = ops.decode_workspace(self.max_num_seqs, self.max_pages, sp, device=self.device)
         return self._workspace
 
-    def build(self, query_start_loc, seq_lens, block_table: torch.Tensor, slot_mapping: torch.Tensor,
-              code_key_limit=None, seq_lens_dev: torch.Tensor | None = None) -> AbridgeAttentionMetadata:
+    def build(self, query_start_loc, seq_lens, block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
+              code_key_limit=None, seq_lens_dev: torch.Tensor | None = None, positions: torch.Tensor | None = None,
+              compacted: torch.Tensor | None = None) -> AbridgeAttentionMetadata:
+        """One group's metadata of a step. ``slot_mapping`` [T] int64 (device), or None to compute it on the device
+        from ``positions`` [T] int64 (the tokens' logical positions) and ``compacted`` [B] int32 (tokens the group
+        removed per request): slot = table[r][p // 16] * 16 + p % 16 with p = position - compacted[r]
+        (gpu_model_runner.py:1579-1661, block_table.py:186-197)."""
         qsl = np.asarray(query_start_loc, dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64)
         B = sl.size
@@ -174,6 +182,11 @@ class AbridgeMetadataBuilder:
             raise RuntimeError(f"decode needs {max_pages} pages > max_pages={self.max_pages}")
         if seq_lens_dev is None:
             seq_lens_dev = torch.from_numpy(sl.astype(np.int32)).to(block_table.device)
+        if slot_mapping is None:
+            if positions is None:
+                raise RuntimeError("build needs slot_mapping or the tokens' logical positions")
+            req_idx = torch.from_numpy(np.repeat(np.arange(B, dtype=np.int32), qlen)).to(block_table.device)
+            slot_mapping = ops.slot_mapping(req_idx, positions, block_table, compacted=compacted)
         return AbridgeAttentionMetadata(query_start_loc=qsl, seq_lens=sl, block_table=block_table,
                                         slot_mapping=slot_mapping, seq_lens_dev=seq_lens_dev, num_decodes=nd,
                                         code_key_limit=limits, max_decode_pages=max(max_pages, 1),
@@ -209,8 +222,9 @@ class AbridgeAttentionImpl:
         md = attn_metadata
         if key is not None:
             n = md.num_actual_tokens
-            ops.kv_append(key.view(-1, self.num_kv_heads, self.head_size)[:n],
-                          value.view(-1, self.num_kv_heads, self.head_size)[:n], md.slot_mapping[:n], kv_cache)
+            torch.ops.abridgekv.kv_append(key.view(-1, self.num_kv_heads, self.head_size)[:n],
+                                          value.view(-1, self.num_kv_heads, self.head_size)[:n], md.slot_mapping[:n],
+                                          kv_cache)
         self.attend(q, kv_cache, md, output.view(T, self.num_heads, self.head_size), output_lse)
         return output
 
@@ -219,10 +233,9 @@ class AbridgeAttentionImpl:
         """Attention only (the cache already holds this step's rows): decodes, then chunks and code steps."""
         nd, nd_tok, n_tok = md.num_decodes, md.num_decode_tokens, md.num_actual_tokens
         if nd:
-            ops.decode_attention(q[:nd_tok], kv_cache, md.block_table[:nd], md.seq_lens_dev[:nd], self.scale,
-                                 max_pages=md.max_decode_pages, out=out[:nd_tok],
-                                 lse=None if lse is None else lse[:nd_tok], split_pages=md.split_pages,
-                                 workspace=md.workspace)
+            torch.ops.abridgekv.decode_attn(q[:nd_tok], kv_cache, md.block_table[:nd], md.seq_lens_dev[:nd],
+                                            self.scale, md.max_decode_pages, md.split_pages, out[:nd_tok],
+                                            None if lse is None else lse[:nd_tok], md.workspace)
         if nd < md.num_reqs and n_tok > nd_tok:
             qsl = md.query_start_loc[nd:] - nd_tok
             sl = md.seq_lens[nd:]

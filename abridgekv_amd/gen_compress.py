@@ -6,14 +6,18 @@ raw prompt, per-layer code quotas, no tails). The reference keeps a dense per-la
 every layer's rows live in paged caches, quotas are physical, and the block boundary is a compaction:
 
 * content chunks rotate q/k and append K/V at the group's next physical slots in one launch
-  (``abkv_rope_kv_append``) and attend over every resident
-  row: one token -> ``abkv_decode_attn``, several -> causal ``abkv_paged_prefill_attn``. Resident rows are exactly
-  the reference's visible set (codes of earlier blocks, raw prompt, the current block's content;
-  gen_compress.py:667-707).
+  (``abkv_rope_kv_append``: the kernel maps the rows' logical positions to RoPE positions, and the slots come from
+  ``abkv_slot_mapping`` -- logical position minus the group's compacted count through its page table -- both on the
+  device) and attend over every resident row: one token -> ``abkv_decode_attn``, several -> causal
+  ``abkv_paged_prefill_attn``. Resident rows are exactly the reference's visible set (codes of earlier blocks, raw
+  prompt, the current block's content; gen_compress.py:667-707).
 * ``compress`` runs the K code rows of the block non-causally with the key limit ``code_start + q_layer`` (the
-  code visibility of gen_compress.py:328-358, 709-745), then removes the block's response content in every group and
-  code rows ``>= q`` in groups of quota ``q < K`` through the native planner (``mask_token_span``, the
-  ``_finish_block`` order of processor.py:467-557) and moves the surviving rows with the HIP mover.
+  code visibility of gen_compress.py:328-358, 709-745), then compacts the block with the removals the block state
+  machine prescribes (``CompressLMProcessor.block_removal_spans``: response content in every group, then code rows
+  ``>= q`` in groups of quota ``q < K``; processor.py:467-557) through the native planner (``mask_token_span``) and
+  moves the surviving rows with the HIP mover. The generator's API hands over the next token only after
+  ``compress()``, so it runs the processor's block compaction directly rather than through ``update_after_step``
+  (which needs that token to open the next block).
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
@@ -32,9 +36,10 @@ import torch.nn.functional as F
 
 from . import backend as bk
 from . import ops
-from .config import bitrev_offsets
+from .config import CompressLMConfig, bitrev_offsets
 from .packed_kv import PackedKVLayout, PackedKVSidecar
 from .planner import KVPlanner
+from .processor import CompressLMBlock, CompressLMProcessor
 from .worker import execute_fused_moves
 
 _UNSUPPORTED = ("capture_hidden", "capture_attention", "code_init_override", "raw_tail_override",
@@ -120,6 +125,14 @@ class CompressGen:
         self.planner = KVPlanner(self.num_pages, G, ops.PAGE)
         self.rid = 0
         self.planner.add_request(self.rid)
+        # the block state machine's compaction rule for these groups (the serving validation of an enabled config --
+        # bitrev positions, power-of-two sizes -- is the vLLM path's; the generator also runs appended positions)
+        pcfg = CompressLMConfig(block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
+                                packed_kv_k_max=self.K)
+        pcfg.set_code_token_ids(range(1 << 20, (1 << 20) + self.K))
+        self.proc = CompressLMProcessor(pcfg)
+        if not self.packed:
+            self.proc.set_group_quotas(self.group_quotas)
         self.impl = bk.AbridgeAttentionImpl(scale=getattr(self.layers[0].self_attn, "scaling", None))
         self.builder = bk.AbridgeMetadataBuilder(max_num_seqs=1, max_pages=pages_per_group, device=self.device)
         self.sidecar = None
@@ -153,31 +166,34 @@ class CompressGen:
         return torch.arange(base + self.C, base + self.C + self.K, device=self.device)
 
     # -- one step over all layers ---------------------------------------------------------------------------------
-    def _group_metadata(self, n, code_step):
-        """Per-group metadata for n new rows appended after each group's resident rows."""
+    def _group_metadata(self, n, code_step, logical):
+        """Per-group metadata for n new rows appended after each group's resident rows; the slots of the new rows are
+        computed on the device from their logical positions and the group's compacted count."""
         blocks = self.planner.get_blocks(self.rid)
         comp = self.planner.compacted_counts(self.rid)
+        comp_dev = torch.tensor(comp, dtype=torch.int32).to(self.device)
         out = []
         for g, q in enumerate(self.group_quotas):
             start = self.logical_len - comp[g]
             seq_len = start + n
-            table = np.asarray(blocks[g], dtype=np.int32)
-            pos = np.arange(start, seq_len)
-            slots = table[pos // ops.PAGE].astype(np.int64) * ops.PAGE + pos % ops.PAGE
+            table = torch.from_numpy(np.asarray(blocks[g], dtype=np.int32)).view(1, -1).to(self.device)
             limit = [start + min(q, self.K)] if code_step else None
-            md = self.builder.build([0, n], [seq_len], torch.from_numpy(table).view(1, -1).to(self.device),
-                                    torch.from_numpy(slots).to(self.device), code_key_limit=limit)
-            out.append(md)
+            out.append(self.builder.build([0, n], [seq_len], table, code_key_limit=limit, positions=logical,
+                                          compacted=comp_dev[g:g + 1]))
         return out
 
     @torch.no_grad()
-    def _forward_rows(self, hidden, positions, code_step):
-        """Run every decoder layer over hidden [1, n, d]; new K/V rows are committed to the caches."""
+    def _forward_rows(self, hidden, code_step):
+        """Run every decoder layer over hidden [1, n, d]; new K/V rows are committed to the caches. The rows take the
+        next n logical positions; the fused kernel maps them to RoPE positions on the device (bitrev layout:
+        block * C + in-block offset, config/compresslm.py:208-216; appended layout: the logical position itself)."""
         n = hidden.shape[1]
         if self.planner.allocate_slots(self.rid, n) is None:
             raise RuntimeError("page pool exhausted; raise max_tokens")
-        mds = self._group_metadata(n, code_step)
-        positions = positions.to(torch.int64).contiguous()
+        logical = torch.arange(self.logical_len, self.logical_len + n, dtype=torch.int64, device=self.device)
+        mds = self._group_metadata(n, code_step, logical)
+        bc, bk = (self.C, self.K) if self.code_positions == "bitrev" else (0, 0)
+        last = self.logical_len + n - 1
         for li, layer in enumerate(self.layers):
             attn = layer.self_attn
             md = mds[self.group_of[li]]
@@ -192,7 +208,8 @@ class CompressGen:
             q = q[0].to(self.dtype).contiguous()
             k = k[0].to(self.dtype).contiguous()
             v = attn.v_proj(normed).view(n, -1, attn.head_dim).contiguous()
-            ops.rope_kv_append(q, k, v, positions, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache)
+            ops.rope_kv_append(q, k, v, logical, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache,
+                               block_c=bc, codes_k=bk, max_position=last)
             o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
             if self.sidecar is not None:
                 # paged rows + this layer's per-head packed pages; a code step's paged keys stop at the block's
@@ -214,7 +231,7 @@ class CompressGen:
         if n == 0 or self.f + n > self.C:
             raise ValueError(f"chunk of {n} tokens does not fit the block ({self.f}/{self.C} used)")
         hidden = self.inner.embed_tokens(torch.tensor([list(ids)], device=self.device))
-        hidden = self._forward_rows(hidden, self._content_pos(n), code_step=False)
+        hidden = self._forward_rows(hidden, code_step=False)
         self.f += n
         self._cur_ids += [int(t) for t in ids]
         return self.inner.norm(hidden)[0]
@@ -226,27 +243,23 @@ class CompressGen:
         K, C = self.K, self.C
         hidden = self.clm.pause[:K].to(self.dtype).view(1, K, self.d)
         code_start = self.logical_len
-        self._forward_rows(hidden, self._code_pos(), code_step=True)
+        self._forward_rows(hidden, code_step=True)
         block_start = code_start - C
         resp_from = block_start + min(max(self.raw_prompt_len - self.b * C, 0), C)
-        calls = []
+        # the block as the state machine sees it; its removals (and their order) are the processor's
+        block = CompressLMBlock(self.b, content_positions=list(range(block_start, code_start)),
+                                prompt_content_positions=list(range(block_start, resp_from)),
+                                response_content_positions=list(range(resp_from, code_start)),
+                                code_span=(code_start, code_start + K))
+        spans = self.proc.block_removal_spans(block)
         if self.sidecar is not None:
-            # archive the code rows into packed pages, then remove the response content and the codes as one span
+            # archive the code rows into packed pages before the span that removes them runs
             # (compresslm/processor.py:484-520)
             phys = code_start - self.planner.compacted_counts(self.rid)[0]
             table = self.planner.get_blocks(self.rid)[0]
             self.sidecar.capture(self.rid, physical_start=phys, physical_end=phys + K, block_ids=table)
-            calls.append((resp_from, code_start + K, None))
-        else:
-            if resp_from < code_start:
-                calls.append((resp_from, code_start, None))
-            for q in sorted({q for q in self.group_quotas if q < K}):
-                calls.append((code_start + q, code_start + K,
-                              [g for g, gq in enumerate(self.group_quotas) if gq == q]))
-        for start, end, groups in calls:
-            res = self.planner.mask_token_span(self.rid, start, end, groups)
-            if not res.success:
-                raise RuntimeError(f"compaction failed: {res.error_message}")
+        for start, end, groups in spans:
+            CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end, groups)
         _, _, fused = self.planner.take_step_outputs(as_arrays=True)
         execute_fused_moves(fused.copy(), self.caches_by_group)
         self.b += 1

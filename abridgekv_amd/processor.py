@@ -103,22 +103,39 @@ class ServingRequest:
         return pos if self.planner is None else self.planner.logical_to_physical(self.request_id, pos, group)
 
 
+def _run_end(roles: list[int], start: int, stop: int) -> int:
+    """End of the run of equal roles that begins at ``start`` (scanning no further than ``stop``)."""
+    try:
+        return roles.index(CODE + CONTENT - roles[start], start + 1, stop)
+    except ValueError:
+        return max(stop, start + 1)
+
+
+def _no_mask(*_args, **_kwargs):
+    raise RuntimeError("a replayed decode step cannot compact a block")
+
+
 class CompressLMProcessor:
     def __init__(self, config: CompressLMConfig) -> None:
         if not config._initialized:
             raise ValueError("CompressLMConfig token IDs are not initialized")
         self.config = config
         self.group_quotas: tuple[int, ...] | None = None
+        self._code_removals: list[tuple[int, list[int]]] = []
 
     def set_group_quotas(self, group_quotas: Sequence[int] | None) -> None:
         if group_quotas is None:
             self.group_quotas = None
+            self._code_removals = []
             return
         K = self.config.num_code_tokens
         for q in group_quotas:
             if not 0 < q <= K:
                 raise ValueError(f"KV cache group quota {q} outside [1, {K}]")
         self.group_quotas = tuple(int(q) for q in group_quotas)
+        # code slots [q, K) leave the groups of quota q, for each quota q < K in ascending order
+        self._code_removals = [(q, [g for g, gq in enumerate(self.group_quotas) if gq == q])
+                               for q in sorted(set(self.group_quotas)) if q < K]
 
     # -- request set-up -------------------------------------------------------------------------------------------
     def prepare_request(self, request) -> CompressLMState:
@@ -156,11 +173,8 @@ class CompressLMProcessor:
     def num_code_rows_pending(self, request) -> int:
         if not self.is_code_ready(request):
             return 0
-        roles, start = request.compresslm_state.roles, request.num_computed_tokens
-        end = start + 1
-        while end < request.num_tokens and roles[end] == CODE:
-            end += 1
-        return end - start
+        start = request.num_computed_tokens
+        return _run_end(request.compresslm_state.roles, start, request.num_tokens) - start
 
     def limit_num_new_tokens(self, request, proposed: int) -> int:
         """A CODE run is scheduled whole (or not at all); a CONTENT run up to its end."""
@@ -171,10 +185,7 @@ class CompressLMProcessor:
         if start >= request.num_tokens:
             return proposed
         role = state.roles[start]
-        end = start + 1
-        while end < request.num_tokens and state.roles[end] == role:
-            end += 1
-        remaining = end - start
+        remaining = _run_end(state.roles, start, request.num_tokens) - start
         if role == CODE:
             return remaining if proposed >= remaining else 0
         return min(proposed, remaining)
@@ -203,7 +214,7 @@ class CompressLMProcessor:
         end = request.num_computed_tokens
         start = end - num_scheduled_tokens
         role = state.roles[start]
-        if any(state.roles[p] != role for p in range(start, end)):
+        if _run_end(state.roles, start, end) != end:
             raise RuntimeError("CompressLM scheduled a mixed-role model step")
         sampled = sampled_token_ids[0] if sampled_token_ids else None
         visible: list[int] = []
@@ -227,6 +238,41 @@ class CompressLMProcessor:
         elif role == CODE and role_end:
             self._finish_block(request, state, block, mask_span, pack_code_span)
         return visible, False
+
+    def update_after_decode_steps(self, request, sampled_token_ids: Sequence[int], max_model_len: int) -> None:
+        """``len(sampled_token_ids)`` consecutive one-token decode steps of one request at once, for replaying a known
+        history: the same state as calling :meth:`update_after_step` once per step with ``num_scheduled_tokens=1``
+        and the i-th sampled token, for a stretch in which no step computes the block's last content token (that step
+        stages the codes) and no sampled token stops the request. ``request.num_computed_tokens`` already includes
+        the steps. Anything else (a stretch reaching the block end, a possible stop) is stepped one by one."""
+        ids = list(sampled_token_ids)
+        m = len(ids)
+        state = request.compresslm_state
+        if m == 0:
+            return
+        end = request.num_computed_tokens
+        start = end - m
+        sampling = request.sampling_params
+        stops = set(getattr(sampling, "stop_token_ids", None) or ())
+        if not getattr(sampling, "ignore_eos", False) and request.eos_token_id is not None:
+            stops.add(request.eos_token_id)
+        block = state.blocks[state.position_to_block[start]] if start < len(state.position_to_block) else None
+        fast = (state is not None and block is not None and request.num_tokens == start + 1
+                and state.roles[start] == CONTENT and block is state.current_block
+                and len(block.content_positions) + m <= self.config.block_size
+                and block.content_positions[-1] == start and (not stops or stops.isdisjoint(ids))
+                and request.num_tokens + m < max_model_len
+                and len(state.visible_output_token_ids) + m < request.max_tokens)
+        if not fast:
+            request.num_computed_tokens = start
+            for tok in ids:
+                request.num_computed_tokens += 1
+                _, stopped = self.update_after_step(request, 1, [tok], _no_mask, max_model_len)
+                if stopped:
+                    raise RuntimeError("a replayed decode step stopped the request")
+            return
+        state.visible_output_token_ids.extend(ids)
+        self._append_content(request, state, ids, is_prompt=False)
 
     def reset_for_preemption(self, state: CompressLMState) -> None:
         state.reset_compaction_progress()
@@ -257,13 +303,13 @@ class CompressLMProcessor:
     # -- internals ------------------------------------------------------------------------------------------------
     def _record_content(self, state: CompressLMState, start: int, token_ids, is_prompt: bool) -> None:
         block = state.current_block
-        for offset, tok in enumerate(token_ids):
-            pos = start + offset
-            block.content_positions.append(pos)
-            block.content_token_ids.append(tok)
-            (block.prompt_content_positions if is_prompt else block.response_content_positions).append(pos)
-            state.roles.append(CONTENT)
-            state.position_to_block.append(block.block_id)
+        n = len(token_ids)
+        positions = range(start, start + n)
+        block.content_positions.extend(positions)
+        block.content_token_ids.extend(token_ids)
+        (block.prompt_content_positions if is_prompt else block.response_content_positions).extend(positions)
+        state.roles.extend([CONTENT] * n)
+        state.position_to_block.extend([block.block_id] * n)
 
     def _append_content(self, request, state, token_ids, is_prompt: bool) -> None:
         if not token_ids:
@@ -300,46 +346,52 @@ class CompressLMProcessor:
         self._append_content(request, state, [held], is_prompt=False)
         state.worker_token_ids_dirty = True
 
-    def _compact_response_content(self, request, state, block, mask_span, pack_code_span=None) -> None:
-        """Remove the block's response rows from every group, then (physical quotas) code slots [q, K) from the
-        groups of each quota q < K, ascending q, each on the layout the previous removal left. Packed KV: archive
-        the code span first (``pack_code_span(request_id, start, end)``), then remove the response content and the
-        codes as one span (compresslm/processor.py:484-520)."""
-        if block.block_id in state.compacted_block_ids:
-            return
+    def block_removal_spans(self, block: CompressLMBlock) -> list[tuple[int, int, list[int] | None]]:
+        """The span removals that compact a closed block, in the order they must run: ``(start, end, groups)`` with
+        ``groups`` None for every KV-cache group (compresslm/processor.py:467-557). Response content goes from every
+        group, then (physical quotas) code slots [q, K) from the groups of each quota q < K, ascending q, each on the
+        layout the previous removal left. Packed KV: the response content and the codes as one span (the codes are
+        archived into packed pages before it runs)."""
         pos = block.response_content_positions
+        if pos and pos[-1] - pos[0] + 1 != len(pos):
+            raise RuntimeError("packed KV response content must be contiguous" if self.config.uses_packed_kv
+                               else "CompressLM response content must be contiguous")
         if self.config.uses_packed_kv:
-            if pack_code_span is None:
-                raise RuntimeError("packed KV decoding has no code capture callback")
             if block.code_span is None:
                 raise RuntimeError("packed KV block has no completed code span")
             cs, ce = block.code_span
-            pack_code_span(request.request_id, cs, ce)
-            if pos and pos != list(range(pos[0], pos[-1] + 1)):
-                raise RuntimeError("packed KV response content must be contiguous")
             if pos and pos[-1] + 1 != cs:
                 raise RuntimeError("packed KV response content and code span are not contiguous")
-            self._mask_or_raise(mask_span, request.request_id, pos[0] if pos else cs, ce)
-            state.compacted_block_ids.add(block.block_id)
-            return
+            return [(pos[0] if pos else cs, ce, None)]
+        spans: list[tuple[int, int, list[int] | None]] = []
         if pos:
-            if pos != list(range(pos[0], pos[-1] + 1)):
-                raise RuntimeError("CompressLM response content must be contiguous")
-            self._mask_or_raise(mask_span, request.request_id, pos[0], pos[-1] + 1)
+            spans.append((pos[0], pos[-1] + 1, None))
         if self.group_quotas is not None:
             if block.code_span is None:
                 raise RuntimeError("physical per-layer quotas need a completed code span")
             cs, ce = block.code_span
-            K = self.config.num_code_tokens
-            for q in sorted(set(self.group_quotas)):
-                if q >= K:
-                    continue
-                groups = [g for g, gq in enumerate(self.group_quotas) if gq == q]
-                self._mask_or_raise(mask_span, request.request_id, cs + q, ce, groups=groups)
+            for q, groups in self._code_removals:
+                spans.append((cs + q, ce, list(groups)))
+        return spans
+
+    def _compact_response_content(self, request, state, block, mask_span, pack_code_span=None) -> None:
+        """Run :meth:`block_removal_spans` of the block through ``mask_span``. Packed KV: archive the code span first
+        (``pack_code_span(request_id, start, end)``), then remove the response content and the codes as one span
+        (compresslm/processor.py:484-520)."""
+        if block.block_id in state.compacted_block_ids:
+            return
+        spans = self.block_removal_spans(block)
+        if self.config.uses_packed_kv:
+            if pack_code_span is None:
+                raise RuntimeError("packed KV decoding has no code capture callback")
+            pack_code_span(request.request_id, *block.code_span)
+        for start, end, groups in spans:
+            self._mask_or_raise(mask_span, request.request_id, start, end, groups=groups)
         state.compacted_block_ids.add(block.block_id)
 
     @staticmethod
     def _mask_or_raise(mask_span, request_id, start, end, groups=None) -> None:
+        """Run one removal; a failed SpanRemovalResult becomes RuntimeError (processor.py:648-661)."""
         res = mask_span(request_id, start, end) if groups is None else mask_span(request_id, start, end, groups=groups)
         if not res.success:
             raise RuntimeError(f"CompressLM KV compaction failed for [{start}, {end}): {res.error_message}")

@@ -2,13 +2,20 @@
 interleaved, as the saturated serving workload runs (every request decodes one token per step; a request whose open
 block fills runs its K code rows in the next step, then its block is compacted).
 
-Per step, on one HIP stream: for every layer the new K/V rows are appended (``abkv_kv_append``), decoding requests
-attend with ``abkv_decode_attn`` over their group page table and coding requests with ``abkv_paged_prefill_attn``
-(non-causal, key limit ``code_start + quota`` per group); then the planner's removals of the finished blocks
-(``_finish_block`` order: response content in every group, code rows >= q in groups of quota q < K;
-third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:467-557) become fused row moves
-(``abkv_kv_move_segments``). The host planner work and metadata of step s+1 are prepared while step s runs: the
-metadata travels in one pinned, asynchronous host-to-device copy per step.
+Host side: the block state machine (``CompressLMProcessor``, the reference's
+third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py) decides every request's next run
+(``limit_num_new_tokens``, ``should_skip_sampling``), and after the step ``update_after_step`` settles it with
+``KVPlanner.mask_token_span`` as its ``mask_span`` callback: the compaction of a block whose code run ended is exactly
+the processor's ``_finish_block`` (processor.py:419-557), and the planner turns it into fused row moves.
+
+Device side, per step on one HIP stream: the previous step's compaction moves (``abkv_kv_move_segments``); the slot of
+every new row per KV-cache group (``abkv_slot_mapping``: logical position minus the group's compacted count through
+the group's page table, gpu_model_runner.py:1579-1661 + block_table.py:186-197); then for every layer the fused RoPE +
+KV append (``abkv_rope_kv_append``, bitrev RoPE positions of the abridged layout computed on the device,
+config/compresslm.py:208-216), decode attention for decoding requests (``abkv_decode_attn``) and code-step attention for
+coding requests (``abkv_paged_prefill_attn``, non-causal, key limit ``code_start + quota`` per group). The host work and
+metadata of step s+1 are prepared while step s runs: the metadata travels in one pinned, asynchronous host-to-device
+copy per step.
 
 Queries, keys and values are synthetic (N(0,1) bf16 pools from the seed): the loop measures the attention path,
 not a model.
@@ -22,8 +29,10 @@ import torch
 
 from . import ops
 from ._lib import check, lib
+from .backend import code_step_key_limits
 from .worker import launch_moves, split_fused_moves
-from .workloads import BLOCK_C, CODES_K_MAX, QWEN3_4B_LAYER_QUOTAS, build_decode_state
+from .workloads import (BLOCK_C, CODES_K_MAX, MAX_MODEL_LEN, QWEN3_4B_LAYER_QUOTAS, SAMPLED_TOKEN,
+                        build_decode_state)
 
 PAGE = ops.PAGE
 
@@ -33,7 +42,8 @@ def _ptr(t):
 
 
 class ServingPlan:
-    """Host half of the loop: the planner, every request's state, the page tables and the per-step metadata."""
+    """Host half of the loop: the state machine and request objects, the planner, the page tables and the per-step
+    metadata."""
 
     def __init__(self, T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, growth_tokens=2048, C=BLOCK_C,
                  K=CODES_K_MAX, max_coding=64):
@@ -45,110 +55,124 @@ class ServingPlan:
         st = build_decode_state(T, P, layer_quotas, seed=seed, slack_pages=slack, C=C, K=K)
         self.st = st
         self.planner = st.planner
+        self.proc = st.processor
+        self.reqs = st.requests
+        for req in self.reqs:                              # per-group logical -> physical maps of the planner
+            req.planner = self.planner
         # the replayed histories leave their last compaction's outputs pending; the synthetic cache already stands
         # for the compacted layout, so they are dropped rather than executed
         self.planner.take_step_outputs(as_arrays=True)
         self.B, self.L, self.G = len(T), st.num_layers, len(st.groups)
         self.gq = list(st.group_quotas)
         B, G = self.B, self.G
-        # request state: content tokens incl. the step's query, logical length, phase (0 decode, 1 code)
-        self.T = np.asarray(st.T, np.int64).copy()
-        self.P = np.asarray(st.P, np.int64).copy()
-        self.logical = np.array([self.planner.num_computed_tokens(r) for r in range(B)], np.int64)
-        self.phase = np.zeros(B, np.int64)
-        self.code_block = np.zeros(B, np.int64)          # block being coded (phase 1)
-        self.start_logical = self.logical.copy()
-        self.pending_rows = np.zeros(0, np.int64)         # page-table rows changed since the last prepare
-        self.seq_lens = np.stack([sl.astype(np.int64) for sl in st.seq_lens])         # [G, B] rows incl. the step
-        self.W = int(max(-(-(sl.max() + growth_tokens + 2 * K) // PAGE) for sl in self.seq_lens)) + 2
+        self.compacted = np.array([self.planner.compacted_counts(r) for r in range(B)], np.int64).T.copy()  # [G, B]
+        self.pending_rows = np.zeros(0, np.int64)         # page-table / compacted rows changed since the last prepare
+        self.W = int(max(-(-(sl.max() + growth_tokens + 2 * K) // PAGE) for sl in st.seq_lens)) + 2
         self.tables = np.stack([self.planner.fill_block_table(list(range(B)), g, self.W) for g in range(G)])
         self.stats = {"decode_tokens": 0, "code_steps": 0, "moved_rows": 0, "steps": 0}
+        # the query step is already allocated in the planner (build_decode_state scheduled it): only the state
+        # machine's side of scheduling runs for it
+        self._schedule(allocate=False)
+        self.start_logical = self.logical.copy()
+
+    # -- scheduler side ---------------------------------------------------------------------------------------
+    def _schedule(self, allocate=True) -> None:
+        """The state machine picks every request's next run (one decode token, or the K-row code run of a full
+        block); the planner allocates its slots (requests in batch order)."""
+        B, K = self.B, self.K
+        start = np.empty(B, np.int64)
+        n_new = np.empty(B, np.int64)
+        skip = np.empty(B, bool)
+        code = np.empty(B, bool)
+        proc = self.proc
+        for r, req in enumerate(self.reqs):
+            s0 = req.num_computed_tokens
+            n = proc.limit_num_new_tokens(req, req.num_tokens - s0)
+            code[r] = proc.is_code_ready(req)
+            if n != (K if code[r] else 1):
+                raise RuntimeError(f"request {r}: unexpected run of {n} tokens (code={bool(code[r])})")
+            skip[r] = proc.should_skip_sampling(req, n)
+            start[r], n_new[r] = s0, n
+            req.num_computed_tokens = s0 + n
+        if allocate:
+            ev = np.zeros((B, 6), np.int64)
+            ev[:, 0], ev[:, 1], ev[:, 2] = 1, np.arange(B), n_new
+            self.planner.apply_events(ev)
+        self.tok_start, self.n_new, self.skip, self.code = start, n_new, skip, code
+        self.logical = start + n_new
+        self.seq_lens = self.logical[None, :] - self.compacted            # [G, B] rows incl. the step's tokens
 
     def prepare(self) -> dict:
-        """Metadata (numpy) of the step about to run: tokens are the decodes (one each) then K code rows per coding
-        request; per-group slots, decode lengths, code-step starts / key limits / tiles, changed table rows."""
+        """Metadata (numpy) of the scheduled step: tokens are the decodes (one each) then K code rows per coding
+        request, each with its request and logical position (the device maps them to slots and RoPE positions);
+        decode lengths; code-step starts / key limits / tiles per group; changed table rows."""
         G, K = self.G, self.K
-        dec = np.flatnonzero(self.phase == 0)
-        cod = np.flatnonzero(self.phase == 1)
+        dec = np.flatnonzero(~self.code)
+        cod = np.flatnonzero(self.code)
         nd, nc = dec.size, cod.size
         n_tok = nd + nc * K
-        slots = np.empty((G, n_tok), np.int64)
-        for g in range(G):
-            sl, tab = self.seq_lens[g], self.tables[g]
-            pos_d = sl[dec] - 1
-            slots[g, :nd] = tab[dec, pos_d // PAGE].astype(np.int64) * PAGE + pos_d % PAGE
-            if nc:
-                pos_c = ((sl[cod] - K)[:, None] + np.arange(K)[None, :]).reshape(-1)
-                req_c = np.repeat(cod, K)
-                slots[g, nd:] = tab[req_c, pos_c // PAGE].astype(np.int64) * PAGE + pos_c % PAGE
-        kv_start = (np.stack([self.seq_lens[g][cod] - K for g in range(G)]) if nc
-                    else np.zeros((G, 0), np.int64))
-        limits = kv_start + np.minimum(np.asarray(self.gq)[:, None], K)
+        tok_req = np.concatenate([dec, np.repeat(cod, K)]).astype(np.int64)
+        tok_pos = np.concatenate([self.tok_start[dec],
+                                  (self.tok_start[cod][:, None] + np.arange(K)[None, :]).reshape(-1)])
+        q_start = np.arange(nc + 1, dtype=np.int64) * K
+        kv_start = np.zeros((G, nc), np.int64)
+        limits = np.zeros((G, nc), np.int64)
+        if nc:
+            for g in range(G):
+                # the staged code span of the block being closed, in the group's physical layout: the code step sees
+                # every row before it and the first min(q_g, K) rows of it (gpu_model_runner.py:2042-2107)
+                spans = [self.proc.code_physical_spans(self.reqs[r], g)[-1] for r in cod.tolist()]
+                kv_start[g] = [s for s, _ in spans]
+                limits[g] = code_step_key_limits(q_start, self.seq_lens[g][cod], spans, self.gq[g], K)
         tiles = np.array([(r, q0) for r in range(nc) for q0 in range(0, K, 64)], np.int64).reshape(-1, 2)
         dec_lens = self.seq_lens[:, dec]
         max_pages = [max(1, int(-(-dec_lens[g].max() // PAGE))) if nd else 1 for g in range(G)]
         split = [ops.auto_split_pages(dec_lens[g]) if nd else ops.DEFAULT_SPLIT_PAGES for g in range(G)]
         rows = self.pending_rows
         self.pending_rows = np.zeros(0, np.int64)
-        tok_req = np.concatenate([dec, np.repeat(cod, K)]).astype(np.int64)
-        tok_pos = np.concatenate([self.logical[dec] - 1,
-                                  ((self.logical[cod] - K)[:, None] + np.arange(K)[None, :]).reshape(-1)])
-        return dict(dec=dec, cod=cod, nd=nd, nc=nc, n_tok=n_tok, slots=slots, dec_lens=dec_lens,
-                    q_start=np.arange(nc + 1, dtype=np.int64) * K, kv_start=kv_start, limits=limits, tiles=tiles,
-                    max_pages=max_pages, split=split, upd_rows=rows, upd_tables=self.tables[:, rows], tok_req=tok_req,
-                    tok_pos=tok_pos)
+        return dict(dec=dec, cod=cod, nd=nd, nc=nc, n_tok=n_tok, dec_lens=dec_lens, q_start=q_start,
+                    kv_start=kv_start, limits=limits, tiles=tiles, max_pages=max_pages, split=split, upd_rows=rows,
+                    upd_tables=self.tables[:, rows], upd_compacted=self.compacted[:, rows], tok_req=tok_req,
+                    tok_pos=tok_pos, max_pos=int(tok_pos.max()) if n_tok else 0)
 
     def advance(self, m) -> np.ndarray:
-        """Account for the step described by ``m``: compact the blocks whose code step ran (the planner's removals),
-        move decoders on, schedule the next step's tokens. Returns the fused move rows to execute on the device
-        (after the step's attention, before the next step's appends)."""
-        B, G, K, Cb = self.B, self.G, self.K, self.C
-        dec, cod = m["dec"], m["cod"]
-        events = []
-        for r in cod.tolist():
-            code_start = int(self.logical[r]) - K
-            block_start = code_start - Cb
-            b = int(self.code_block[r])
-            resp_from = block_start + min(max(int(self.P[r]) - b * Cb, 0), Cb)
-            if resp_from < code_start:
-                events.append((2, r, resp_from, code_start, -1, 0))
-                self.seq_lens[:, r] -= code_start - resp_from
-            for qv in sorted({q for q in self.gq if q < K}):
-                mask = sum(1 << g for g, gq in enumerate(self.gq) if gq == qv)
-                events.append((2, r, code_start + qv, code_start + K, mask, 0))
-                for g, gq in enumerate(self.gq):
-                    if gq == qv:
-                        self.seq_lens[g, r] -= K - qv
-        changed = set(cod.tolist())
+        """Settle the step described by ``m`` in the state machine (compaction of the blocks whose code run ended, via
+        the planner), then schedule the next step. Returns the fused move rows to execute on the device (after the
+        step's attention, before the next step's appends)."""
+        B, G = self.B, self.G
+        touched: set[int] = set()
+        planner = self.planner
+
+        def mask_span(request_id, start, end, groups=None):
+            touched.add(request_id)
+            return planner.mask_token_span(request_id, start, end, groups)
+
+        for r, req in enumerate(self.reqs):
+            _, stopped = self.proc.update_after_step(req, int(self.n_new[r]),
+                                                     [] if self.skip[r] else [SAMPLED_TOKEN], mask_span,
+                                                     MAX_MODEL_LEN)
+            if stopped:
+                raise RuntimeError(f"request {r} stopped; the stress loop keeps every request decoding")
         fused = np.zeros((0, 6), np.int64)
-        if events:
-            self.planner.apply_events(np.asarray(events, np.int64))
-            _, _, fu = self.planner.take_step_outputs(as_arrays=True)
+        if touched:
+            _, _, fu = planner.take_step_outputs(as_arrays=True)
             fused = fu.copy()
             self.stats["moved_rows"] += int(fused.shape[0])
-        self.stats["decode_tokens"] += int(dec.size)
-        self.stats["code_steps"] += int(cod.size)
+            for r in touched:
+                self.compacted[:, r] = planner.compacted_counts(r)
+        self.stats["decode_tokens"] += int(m["nd"])
+        self.stats["code_steps"] += int(m["nc"])
         self.stats["steps"] += 1
-        finished = dec[(self.T[dec] % Cb) == 0]          # the decoded token closed its block: code it next step
-        self.code_block[finished] = (self.T[finished] - 1) // Cb
-        self.T[dec] += 1
-        self.phase[:] = 0
-        self.phase[finished] = 1
-        n_new = np.where(self.phase == 1, K, 1)
-        ev = np.zeros((B, 6), np.int64)
-        ev[:, 0], ev[:, 1], ev[:, 2] = 1, np.arange(B), n_new
         old_pages = -(-self.seq_lens // PAGE)
-        self.planner.apply_events(ev)
-        self.logical += n_new
-        self.seq_lens += n_new[None, :]
+        self._schedule()
         if int(self.seq_lens.max()) > self.W * PAGE:
             raise RuntimeError("page-table width exhausted; raise growth_tokens")
-        grew = np.flatnonzero((-(-self.seq_lens // PAGE) != old_pages).any(axis=0))
-        changed.update(grew.tolist())
+        changed = set(touched)
+        changed.update(np.flatnonzero((-(-self.seq_lens // PAGE) != old_pages).any(axis=0)).tolist())
         if changed:
             rows = np.asarray(sorted(changed), np.int64)
             for g in range(G):
-                self.tables[g][rows] = self.planner.fill_block_table(rows.tolist(), g, self.W)
+                self.tables[g][rows] = planner.fill_block_table(rows.tolist(), g, self.W)
             self.pending_rows = np.union1d(self.pending_rows, rows)
         return fused
 
@@ -178,7 +202,13 @@ class ServingStress:
         self.k_pool = torch.randn((B * K, 8, 128), generator=gen, device=self.dev).to(torch.bfloat16)
         self.v_pool = torch.randn((B * K, 8, 128), generator=gen, device=self.dev).to(torch.bfloat16)
         self.out = torch.empty((B * K, 32, 128), dtype=torch.bfloat16, device=self.dev)
+        self.slots = torch.empty((self.G, B * K), dtype=torch.int64, device=self.dev)
         self.bt_dev = torch.from_numpy(plan.tables).to(self.dev)                       # [G, B, W]
+        self.comp_dev = torch.from_numpy(plan.compacted.astype(np.int32)).to(self.dev)  # [G, B]
+        # RoPE table for every position the run can reach: in growth_tokens steps a request decodes at most
+        # growth_tokens tokens and runs at most growth_tokens // C + 2 code runs of K rows
+        max_logical = int(plan.logical.max()) + growth_tokens + (growth_tokens // C + 2) * K
+        self.cos_sin = ops.rope_cos_sin_cache(ops.rope_bound(max_logical, C, K) + 1, device=self.dev)
         # split_pages None: per step and group the plan's ops.auto_split_pages (never below 32, so this workspace fits)
         self.ws = ops.decode_workspace(B, self.W, min(split_pages or ops.DEFAULT_SPLIT_PAGES, ops.DEFAULT_SPLIT_PAGES),
                                        device=self.dev)
@@ -211,10 +241,14 @@ class ServingStress:
         G, W = self.G, self.W
         nd, nc, n_tok = m["nd"], m["nc"], m["n_tok"]
         rows = m["upd_rows"]
+        if ops.rope_bound(m["max_pos"], self.C, self.K) >= self.cos_sin.shape[0]:
+            raise RuntimeError("RoPE table exhausted; raise growth_tokens")
         parts = {
             "upd_rows": rows.astype(np.int32),
             "upd_tables": m["upd_tables"].astype(np.int32).reshape(-1),
-            "slots": m["slots"].view(np.int32).reshape(-1),
+            "upd_comp": m["upd_compacted"].astype(np.int32).reshape(-1),
+            "tok_req": m["tok_req"].astype(np.int32),
+            "tok_pos": m["tok_pos"].astype(np.int64).view(np.int32),
             "dec_lens": m["dec_lens"].astype(np.int32).reshape(-1),
             "dec_idx": m["dec"].astype(np.int32),
             "cod_idx": m["cod"].astype(np.int32),
@@ -249,11 +283,12 @@ class ServingStress:
         self._copy_done[i] = ev
         self._ring ^= 1
         v = {name: dev[o: o + n] for name, (o, n) in where.items()}
-        v["slots"] = v["slots"].view(torch.int64).view(G, n_tok)
+        v["tok_pos"] = v["tok_pos"].view(torch.int64)
         v["dec_lens"] = v["dec_lens"].view(G, nd)
         v["kv_start"] = v["kv_start"].view(G, nc)
         v["limits"] = v["limits"].view(G, nc)
         v["upd_tables"] = v["upd_tables"].view(G, rows.size, W)
+        v["upd_comp"] = v["upd_comp"].view(G, rows.size)
         if self.tag:
             v["tags"] = v["tags"].view(n_tok, 3)
         mv = [(gid, v[f"mv_ops{j}"].view(-1, 4), v[f"mv_offs{j}"]) for j, (gid, _, _) in enumerate(moves)]
@@ -275,17 +310,27 @@ class ServingStress:
         if m["moves"]:
             launch_moves(m["moves"], self.by_group)
         if m["n_upd"]:
-            self.bt_dev[:, v["upd_rows"].long()] = v["upd_tables"]
+            rows = v["upd_rows"].long()
+            self.bt_dev[:, rows] = v["upd_tables"]
+            self.comp_dev[:, rows] = v["upd_comp"]
         if self.tag:
-            k[:n_tok, 0, :3] = v["tags"].to(torch.bfloat16)
+            val[:n_tok, 0, :3] = v["tags"].to(torch.bfloat16)
+        # slots of the step's new rows per group: logical position - the group's compacted count -> page table
+        for g in range(self.G):
+            check(L.abkv_slot_mapping(_ptr(v["tok_req"]), _ptr(v["tok_pos"]), n_tok, _ptr(self.bt_dev[g]), self.B,
+                                      self.W, PAGE, _ptr(self.comp_dev[g]), _ptr(self.slots[g]), stream),
+                  "abkv_slot_mapping")
         dec_bt = [self.bt_dev[g].index_select(0, v["dec_idx"].long()) if nd else None for g in range(self.G)]
         cod_bt = [self.bt_dev[g].index_select(0, v["cod_idx"].long()) if nc else None for g in range(self.G)]
+        cs = self.cos_sin
         for layer in range(self.L):
             g = int(self.st.layer_group[layer])
             cache = self.caches[int(self.st.layer_slot[layer])]
-            check(L.abkv_kv_append(_ptr(k), k.stride(0) * 2, _ptr(val), val.stride(0) * 2, _ptr(v["slots"][g]), n_tok,
-                                   _ptr(cache), cache.shape[0], ops.PAGE_BYTES, ops.HALF_BYTES, ops.SLOT_BYTES, PAGE,
-                                   stream), "abkv_kv_append")
+            # RoPE of q and k at the bitrev positions of the abridged layout + KV append, one launch
+            check(L.abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), _ptr(val),
+                                        val.stride(0), _ptr(v["tok_pos"]), n_tok, self.C, self.K, _ptr(cs),
+                                        cs.shape[0], _ptr(self.slots[g]), _ptr(cache), cache.shape[0], stream),
+                  "abkv_rope_kv_append")
             if nd:
                 if self.decode_events is not None:
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -319,28 +364,29 @@ class ServingStress:
 
     def check_layout(self, requests=None):
         """With ``tag=True``: read every group's physical rows written during the run back from the cache and check
-        that row p of request r holds logical position planner.physical_to_logical(r, p, g) (rows of tokens
-        scheduled for the next step are not written yet and are skipped). Returns rows checked."""
+        that row p of request r holds logical position planner.physical_to_logical(r, p, g) (the tag is in the V
+        row, which RoPE leaves alone; rows of tokens scheduled for the next step are not written yet and are
+        skipped). Returns rows checked."""
         if not self.tag:
             raise RuntimeError("construct with tag=True")
         self.flush()
         torch.cuda.synchronize()
         checked = 0
+        plan = self.plan
         for g in range(self.G):
             cache = self.by_group[g][0]
             for r in (range(self.B) if requests is None else requests):
                 n = int(self.seq_lens[g, r])
                 pos = np.arange(n)
-                logical = np.array([self.plan.planner.physical_to_logical(r, int(p), g) for p in pos])
+                logical = np.array([plan.planner.physical_to_logical(r, int(p), g) for p in pos])
                 # rows written during the run; the tokens already scheduled for the next step are not written yet
-                pending = self.K if self.plan.phase[r] == 1 else 1
-                keep = (logical >= self.plan.start_logical[r] - 1) & (logical < self.plan.logical[r] - pending)
+                keep = (logical >= plan.start_logical[r] - 1) & (logical < plan.tok_start[r])
                 if not keep.any():
                     continue
                 pp = pos[keep]
                 pages = torch.from_numpy(self.tables[g][r, pp // PAGE].astype(np.int64)).to(self.dev)
                 offs = torch.from_numpy(pp % PAGE).to(self.dev)
-                tags = cache[pages, 0, offs, 0, :3].float().cpu().numpy().astype(np.int64)
+                tags = cache[pages, 1, offs, 0, :3].float().cpu().numpy().astype(np.int64)
                 if not (np.all(tags[:, 0] == r) and np.array_equal(tags[:, 1] * 256 + tags[:, 2], logical[keep])):
                     raise AssertionError(f"request {r} group {g}: rows do not hold their logical positions")
                 checked += int(keep.sum())
@@ -352,8 +398,8 @@ class ServingStress:
         return int(sum(per_group[int(self.st.layer_group[l])] for l in range(self.L)))
 
     def step(self):
-        """Launch the staged step; advance the plan; stage the next step (with this step's compaction moves, which
-        run first in the next launch: after this step's attention, before the next step's appends)."""
+        """Launch the staged step; settle it in the plan; stage the next step (with this step's compaction moves,
+        which run first in the next launch: after this step's attention, before the next step's appends)."""
         m = self._meta
         self._launch_step(m)
         moves = split_fused_moves(self.plan.advance(m), self.st.num_pages, check=False)

@@ -1,15 +1,16 @@
 """Synthetic serving states of the abridged cache, built through the compaction planner.
 
 A request with prompt length P that has produced content tokens up to T-1 (the decode query is content token T-1)
-went through this history (processor semantics, third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py):
-one prefill step per prompt chunk (a chunk ends at a block boundary), one decode step per response token, and after
-every full block of C=512 content tokens one code step of K_max=256 rows followed by compaction of that block
-(response rows in every group, code slots [q, K) per quota). The builder replays every request's history through the
-native planner as scheduler events -- all requests interleaved step by step, allocations of a step in request order
-before its compactions -- so page tables, free-queue order and compacted counts are exactly what the reference's
-scheduler would produce for that arrival pattern. Steps where no group needs a new page and nothing is compacted are
-folded into the next event (allocation depends only on the token totals), which keeps 256 x 32K-token histories
-cheap to replay.
+went through this history, every step decided by the block state machine (abridgekv_amd.processor, the reference's
+third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py): one prefill step per prompt chunk (a chunk ends at a
+block boundary), one decode step per response token, and after every full block of C=512 content tokens one code step
+of K_max=256 rows followed by the compaction the processor issues for that block. The builder replays every
+request's history through the native planner as scheduler events -- all requests interleaved step by step,
+allocations of a step in request order before its compactions -- so page tables, free-queue order and compacted
+counts are exactly what the reference's scheduler would produce for that arrival pattern, and the processor states
+are left at the query for the serving loop to continue. Steps where no group needs a new page and nothing is
+compacted are folded into the next event (allocation depends only on the token totals), which keeps 256 x 32K-token
+histories cheap to replay.
 """
 from __future__ import annotations
 
@@ -17,7 +18,9 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .planner import KVPlanner
+from .config import CompressLMConfig
+from .planner import KVPlanner, SpanRemovalResult
+from .processor import CODE, CompressLMProcessor, SamplingSpec, ServingRequest
 
 BLOCK_C = 512
 CODES_K_MAX = 256
@@ -56,67 +59,107 @@ def rows_per_group(T, P, quota, C=BLOCK_C):
     return min(P, nb * C) + nb * quota + (T - nb * C)
 
 
-def request_history(T, P, group_quotas, C=BLOCK_C, K=CODES_K_MAX):
-    """Planner-relevant events of one request, in its own step numbering, up to (excluding) the decode step of
-    content token T-1. Returns (list of (step, kind, a, b, group_mask)), number of steps)."""
-    G = len(group_quotas)
-    compacted = [0] * G
-    computed = 0
-    pending = 0                      # tokens scheduled since the last emitted allocation
+PROMPT_TOKEN = 3                  # synthetic token ids of the replayed histories
+SAMPLED_TOKEN = 11
+CODE_TOKEN_BASE = 1 << 20
+MAX_MODEL_LEN = 1 << 30
+
+
+def serving_processor(group_quotas, C=BLOCK_C, K=CODES_K_MAX) -> CompressLMProcessor:
+    """The block state machine of a served model with these per-group code quotas (synthetic code token ids)."""
+    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev")
+    cfg.set_code_token_ids(range(CODE_TOKEN_BASE, CODE_TOKEN_BASE + K))
+    proc = CompressLMProcessor(cfg)
+    proc.set_group_quotas(group_quotas)
+    return proc
+
+
+def new_request(proc: CompressLMProcessor, rid, P: int) -> ServingRequest:
+    """A request with a P-token synthetic prompt, prepared by the state machine (code tokens banned, no EOS)."""
+    ids = proc.config.code_token_ids
+    req = ServingRequest(rid, [PROMPT_TOKEN] * int(P), SamplingSpec(ignore_eos=True,
+                                                                   bad_words_token_ids=[[i] for i in ids]))
+    req.compresslm_state = proc.prepare_request(req)
+    return req
+
+
+def request_history(T, P, proc: CompressLMProcessor, rid=0, C=BLOCK_C, K=CODES_K_MAX):
+    """Scheduler events of one request up to (excluding) the decode step of content token T-1, in its own step
+    numbering, with the state machine deciding every step: one prefill step per prompt chunk, one decode step per
+    response token, a code step of K rows after each full block, and that block's compaction -- the removals are the
+    ones the processor issues through its ``mask_span`` callback, recorded here as events.
+
+    Returns (events [(step, kind, a, b, group_mask)], number of steps, the request with its processor state at the
+    query). Decode steps in which no group needs a new page are folded into the next allocation event (allocation
+    depends only on token totals), and a stretch of decode steps that does not reach the block end is replayed
+    through the processor at once (``update_after_decode_steps``)."""
+    req = new_request(proc, rid, P)
+    state = req.compresslm_state
+    G = len(proc.group_quotas)
+    compacted = [0] * G                  # tokens removed per group (the planner's tokens_removed of each span)
     events = []
+    pending = 0                          # tokens scheduled since the last emitted allocation
     step = 0
-    c = 0                            # content tokens computed
+    c = 0                                # content tokens computed
     target = T - 1
-    while c < target:
-        b = c // C
-        block_end = (b + 1) * C
-        if c < P:                    # one prefill step: the prompt chunk up to the block end
-            n = min(P, block_end, target) - c
+
+    def recorder(at):
+        def mask_span(request_id, start, end, groups=None):
+            for g in (range(G) if groups is None else groups):
+                compacted[g] += end - start
+            events.append((at, "mask", start, end, -1 if groups is None else sum(1 << g for g in groups)))
+            return SpanRemovalResult(True, end - start, 0)
+        return mask_span
+
+    while True:
+        start = req.num_computed_tokens
+        avail = req.num_tokens - start
+        if state.roles[start] == CODE:   # the code run of a full block, then its compaction
+            n = proc.limit_num_new_tokens(req, avail)
             events.append((step, "alloc", pending + n, 0, 0))
             pending = 0
-            computed += n
-            c += n
+            req.num_computed_tokens += n
+            proc.update_after_step(req, n, [], recorder(step), MAX_MODEL_LEN)
             step += 1
-        else:                        # decode steps of the response tokens of this block (folded)
-            n = min(block_end, target) - c
-            # steps i (0-based) where group g needs a new page: (computed + i - compacted_g) % 16 == 0
-            act0 = np.asarray([computed - compacted[g] for g in range(G)])
-            i = np.arange(n)
-            need = np.zeros(n, bool)
+            continue
+        if c >= target:
+            break
+        if avail > 1:                    # one prefill step: a prompt chunk (it ends at a block boundary)
+            n = proc.limit_num_new_tokens(req, min(avail, target - c))
+            skip = proc.should_skip_sampling(req, n)
+            events.append((step, "alloc", pending + n, 0, 0))
+            pending = 0
+            req.num_computed_tokens += n
+            c += n
+            proc.update_after_step(req, n, [] if skip else [SAMPLED_TOKEN], recorder(step), MAX_MODEL_LEN)
+            step += 1
+            continue
+        m = min(C - len(state.current_block.content_positions), target - c)
+        if m > 0:                        # decode steps that do not compute the block's last content token
+            # step i computes logical position start + i; group g needs a new page when its physical position
+            # start + i - compacted_g starts one
+            i = np.arange(m)
+            need = np.zeros(m, bool)
             for g in range(G):
-                need |= (act0[g] + i) % PAGE == 0
+                need |= (start + i - compacted[g]) % PAGE == 0
             for off in np.flatnonzero(need).tolist():
                 events.append((step + off, "alloc", pending + off + 1, 0, 0))
                 pending = -(off + 1)
-            pending += n
-            computed += n
-            c += n
-            step += n
-        if c == block_end and c <= target:
-            # code step: all K rows of the block's codes in one step, then compaction of the block
-            events.append((step, "alloc", pending + K, 0, 0))
+            pending += m
+            req.num_computed_tokens += m
+            c += m
+            proc.update_after_decode_steps(req, [SAMPLED_TOKEN] * m, MAX_MODEL_LEN)
+            step += m
+        else:                            # the step computing the block's last content token stages the codes
+            events.append((step, "alloc", pending + 1, 0, 0))
             pending = 0
-            code_start = computed
-            computed += K
-            resp_lo = max(P, b * C)
-            if resp_lo < block_end:  # response content of the block, logical [b*(C+K) + ..)
-                ls = b * (C + K) + (resp_lo - b * C)
-                le = b * (C + K) + C
-                events.append((step, "mask", ls, le, -1))
-                for g in range(G):
-                    compacted[g] += le - ls
-            for q in sorted(set(group_quotas)):
-                if q >= K:
-                    continue
-                mask = sum(1 << g for g, gq in enumerate(group_quotas) if gq == q)
-                events.append((step, "mask", code_start + q, code_start + K, mask))
-                for g, gq in enumerate(group_quotas):
-                    if gq == q:
-                        compacted[g] += K - q
+            req.num_computed_tokens += 1
+            c += 1
+            proc.update_after_step(req, 1, [SAMPLED_TOKEN], recorder(step), MAX_MODEL_LEN)
             step += 1
     if pending:
         events.append((step - 1, "tail", pending, 0, 0))
-    return events, step
+    return events, step, req
 
 
 def _schedule_rows(rows):
@@ -147,6 +190,8 @@ class DecodeState:
     slots: list                      # per group [B] int64: slot of the query token
     num_pages: int
     planner: KVPlanner
+    processor: CompressLMProcessor   # the block state machine the histories ran through
+    requests: list                   # its request objects (rid = batch index), at the decode query
 
     @property
     def num_layers(self):
@@ -169,7 +214,8 @@ def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_p
     B = T.size
     groups, gq = quota_groups(layer_quotas)
     G = len(groups)
-    histories = [request_history(int(t), int(p), gq, C, K) for t, p in zip(T, P)]
+    proc = serving_processor(gq, C, K)
+    histories = [request_history(int(t), int(p), proc, r, C, K) for r, (t, p) in enumerate(zip(T, P))]
     S = max(h[1] for h in histories)
     pages_needed = 0
     for t, p in zip(T, P):
@@ -180,7 +226,7 @@ def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_p
     free_order = np.random.default_rng(seed).permutation(np.arange(1, num_pages)).astype(np.int32)
     planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
     rows = []
-    for r, (evs, n_steps) in enumerate(histories):
+    for r, (evs, n_steps, _) in enumerate(histories):
         start = S - n_steps
         rows.append((start, -1, r, -1, (0, r, 0, 0, 0, 0)))            # the request arrives
         for k, (st, kind, a, b, m) in enumerate(evs):
@@ -208,7 +254,8 @@ def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_p
     for g, layers in enumerate(groups):
         for i, l in enumerate(layers):
             layer_group[l], layer_slot[l] = g, i
-    return DecodeState(T, P, groups, gq, layer_group, layer_slot, tables, seq_lens, slots, num_pages, planner)
+    return DecodeState(T, P, groups, gq, layer_group, layer_slot, tables, seq_lens, slots, num_pages, planner, proc,
+                       [h[2] for h in histories])
 
 
 def saturated_decode_lengths(B=256, seed=0, t_range=(2048, 32768), p_range=(128, 1024)):
@@ -270,14 +317,15 @@ def build_compaction_state(B=64, seed=0, layer_quotas=QWEN3_4B_LAYER_QUOTAS, C=B
     T = (nb + 1) * C + 1
     groups, gq = quota_groups(layer_quotas)
     G = len(groups)
-    histories = [request_history(int(t), int(p), gq, C, K) for t, p in zip(T, P)]
+    proc = serving_processor(gq, C, K)
+    histories = [request_history(int(t), int(p), proc, r, C, K) for r, (t, p) in enumerate(zip(T, P))]
     S = max(h[1] for h in histories)
     pages_needed = sum(-(-(int(t) + K) // PAGE) + 1 for t in T) * G
     num_pages = pages_needed + slack_pages + 1
     free_order = rng.permutation(np.arange(1, num_pages)).astype(np.int32)
     planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
     rows, pending = [], []
-    for r, (evs, n_steps) in enumerate(histories):
+    for r, (evs, n_steps, _) in enumerate(histories):
         start = S - n_steps
         rows.append((start, -1, r, -1, (0, r, 0, 0, 0, 0)))
         for k, (st, kind, a, b, m) in enumerate(evs):

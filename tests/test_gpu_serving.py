@@ -1,6 +1,7 @@
 """The serving stress loop on the GPU: decode steps with code steps and compaction interleaved. Every row written
 during the run must sit at the physical row the planner maps its logical position to (bit-exact tags), and decode
-over the final cache through the loop's page tables must match the float64 oracle (2e-2, bf16)."""
+over the final cache through the loop's page tables must match the float64 oracle (2e-2, bf16; see _close for the
+tagged dims)."""
 import numpy as np
 import pytest
 import torch
@@ -8,6 +9,15 @@ import torch
 from oracle import decode as od
 
 pytestmark = pytest.mark.gpu
+
+
+def _close(out, ref):
+    """|out - ref| <= 2e-2 everywhere, except where the layout tags sit: the loop writes integer tags (up to 255)
+    into dims 0..2 of KV head 0's V rows, so the outputs of query heads 0..3 in those dims are O(100) and carry the
+    bf16 rounding of the output itself (|ref| * 2^-8, doubled for slack) on top."""
+    bound = np.full(ref.shape, 2e-2)
+    bound[..., :4, :3] += 2.0 ** -7 * np.abs(ref[..., :4, :3])
+    return bool((np.abs(out - ref) <= bound).all()), float(np.abs(out - ref).max())
 
 
 def test_serving_loop_layout_and_decode():
@@ -35,7 +45,8 @@ def test_serving_loop_layout_and_decode():
                                   torch.from_numpy(lens).to(dev), 128 ** -0.5)
     torch.cuda.synchronize()
     ref, _ = od.decode_paged_fp64(q.float().numpy(), cache.float().cpu().numpy(), s.tables[g], lens, 128 ** -0.5)
-    assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+    ok, err = _close(out.float().cpu().numpy(), ref)
+    assert ok, err
 
 
 def test_serving_loop_served_geometry():
@@ -69,4 +80,5 @@ def test_serving_loop_served_geometry():
             pos = torch.arange(n, device=dev)
             rows = cache[bt[b].long()[pos // 16], :, pos % 16].float().cpu().numpy()
             ref, _ = od.decode_fp64(q[b].float().numpy(), rows[:, 0], rows[:, 1], 128 ** -0.5)
-            assert np.abs(out[b].float().cpu().numpy() - ref).max() <= 2e-2, (g, b)
+            ok, err = _close(out[b].float().cpu().numpy(), ref)
+            assert ok, (g, b, err)

@@ -214,3 +214,85 @@ def test_config_json_round_trip_and_schedule_loading(tmp_path):
     bad.write_text(json.dumps({"other": 1}))
     with pytest.raises(ValueError):
         load_quota_rows(bad)
+
+
+def _state_tuple(req):
+    st = req.compresslm_state
+    return (req.num_computed_tokens, list(req.all_token_ids), list(req._output_token_ids), req.status,
+            st.roles, st.position_to_block, st.visible_output_token_ids, st.held_sampled_token, st.current_block_id,
+            st.pending_prompt_index, sorted(st.compacted_block_ids), st.worker_token_ids_dirty,
+            [(b.block_id, b.content_positions, b.content_token_ids, b.prompt_content_positions,
+              b.response_content_positions, b.code_span) for b in st.blocks])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_bulk_decode_replay_equals_per_token_steps(seed):
+    """update_after_decode_steps (a stretch of one-token decode steps at once, as the history builder replays them)
+    leaves exactly the state of calling update_after_step once per step; stretches that reach the block end or hit a
+    stop token take the per-token path (and a stop raises)."""
+    rng = np.random.default_rng(seed)
+    C, K = 16, 4
+    _, proc = make(quotas=(4, 2, 1, 2), C=C, K=K)
+    sp = SamplingSpec(bad_words_token_ids=[[c] for c in CODES], stop_token_ids=(77,))
+    prompt = rng.integers(1, 50, int(rng.integers(1, 3 * C))).tolist()
+    reqs = [ServingRequest(i, prompt, sp, eos_token_id=99) for i in range(2)]
+    calls = [[], []]
+    for i, r in enumerate(reqs):
+        r.compresslm_state = proc.prepare_request(r)
+
+    def rec(i):
+        def mask(rid, s, e, groups=None):
+            calls[i].append((s, e, groups))
+            return SimpleNamespace(success=True, error_message=None)
+        return mask
+
+    for _ in range(60):
+        a, b = reqs
+        start = a.num_computed_tokens
+        pending = a.num_tokens - start
+        st = a.compresslm_state
+        if st.roles[start] == CODE or pending > 1:          # code run or prompt chunk: both step normally
+            n = proc.limit_num_new_tokens(a, pending)
+            skip = proc.should_skip_sampling(a, n)
+            tok = [] if skip else [int(rng.integers(1, 50))]
+            for i, r in enumerate(reqs):
+                r.num_computed_tokens += n
+                proc.update_after_step(r, n, tok, rec(i), 1 << 20)
+        else:
+            # at most up to the step that computes the block's last content token (it stages the codes)
+            m = int(rng.integers(1, C - len(st.current_block.content_positions) + 2))
+            ids = rng.integers(1, 50, m).tolist()
+            for tok in ids:
+                b.num_computed_tokens += 1
+                proc.update_after_step(b, 1, [tok], rec(1), 1 << 20)
+            a.num_computed_tokens += m
+            proc.update_after_decode_steps(a, ids, 1 << 20)
+        assert _state_tuple(a) == _state_tuple(b)
+        assert calls[0] == calls[1]
+    assert calls[0], "no block was compacted"
+    r = reqs[0]
+    while r.compresslm_state.roles[r.num_computed_tokens] == CODE or r.num_tokens - r.num_computed_tokens > 1:
+        n = proc.limit_num_new_tokens(r, r.num_tokens - r.num_computed_tokens)
+        skip = proc.should_skip_sampling(r, n)
+        r.num_computed_tokens += n
+        proc.update_after_step(r, n, [] if skip else [5], rec(0), 1 << 20)
+    if len(r.compresslm_state.current_block.content_positions) + 2 > C:     # keep the stop inside the block
+        return
+    r.num_computed_tokens += 2
+    with pytest.raises(RuntimeError, match="stopped"):
+        proc.update_after_decode_steps(r, [5, 77], 1 << 20)
+
+
+def test_block_removal_spans_order():
+    """The removals of a closed block: response content in every group, then code slots [q, K) per quota q < K in
+    ascending q; packed KV removes content and codes as one span."""
+    from abridgekv_amd.processor import CompressLMBlock
+    _, proc = make(quotas=(4, 2, 1, 2), C=8, K=4)
+    blk = CompressLMBlock(0, content_positions=list(range(8)), prompt_content_positions=[0, 1, 2],
+                          response_content_positions=list(range(3, 8)), code_span=(8, 12))
+    assert proc.block_removal_spans(blk) == [(3, 8, None), (9, 12, [2]), (10, 12, [1, 3])]
+    blk.response_content_positions = []
+    assert proc.block_removal_spans(blk) == [(9, 12, [2]), (10, 12, [1, 3])]
+    blk.response_content_positions = [3, 5]
+    with pytest.raises(RuntimeError, match="contiguous"):
+        proc.block_removal_spans(blk)
