@@ -18,6 +18,8 @@ SIGNATURES = {
     "abkv_decode_workspace_size": (C.c_size_t, [C.c_int, C.c_int]),
     "abkv_decode_attn": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, _vp, C.c_int, C.c_int, C.c_int,
                                    C.c_float, _vp, C.c_long, C.c_long, _vp, _vp, C.c_size_t, _vp]),
+    "abkv_decode_attn_noalloc": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, _vp, C.c_int,
+                                           C.c_int, C.c_int, C.c_float, _vp, C.c_long, C.c_long, _vp, _vp]),
     "abkv_kv_move_segments": (C.c_int, [C.POINTER(_vp), C.c_int, C.c_int, C.c_int, C.c_long, C.c_long, C.c_int,
                                         _vp, _vp, C.c_int, _vp]),
     "abkv_kv_stage_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),

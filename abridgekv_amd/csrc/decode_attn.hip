@@ -25,6 +25,8 @@
 #include "abridgekv_amd.h"
 #include "common.h"
 
+#include <mutex>
+
 namespace abkv {
 
 struct DecodeArgs {
@@ -487,6 +489,36 @@ inline void launch_decode(const DecodeArgs& a, int max_splits, int num_seqs, hip
                      a);
 }
 
+// Static split-partial scratch of abkv_decode_attn_noalloc: part of the library image, so every GPU the library runs
+// on holds its own copy from module load until the process ends, and no call allocates. Host code must never pass
+// the array's name to a kernel (on the host it is only a stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, fetched once per device with that device current.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (nullptr and *err set when the lookup fails).
+static void* scratch_ptr(hipError_t* err) {
+  int dev = -1;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace abkv
 
 extern "C" {
@@ -542,6 +574,31 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head,
     err = hipGetLastError();
   }
   return (int)err;
+}
+
+// abkv_decode_attn with the split partials in the library's static scratch (no workspace argument, no allocation).
+int abkv_decode_attn_noalloc(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache,
+                             int num_pages, const int32_t* block_table, long block_table_stride,
+                             const int32_t* seq_lens, int num_seqs, int max_pages_per_seq, int split_pages,
+                             float scale, void* out, long out_stride_seq, long out_stride_head, float* lse,
+                             hipStream_t stream) {
+  using namespace abkv;
+  if (num_seqs <= 0) return 0;
+  if (split_pages <= 0 || (split_pages & 1) || split_pages > 64 || max_pages_per_seq <= 0)
+    return (int)hipErrorInvalidValue;
+  const int max_splits = (max_pages_per_seq + split_pages - 1) / split_pages;
+  size_t need = 0;
+  void* ws = nullptr;
+  if (max_splits > 1) {
+    need = abkv_decode_workspace_size(num_seqs, max_splits);
+    if (need > kNoAllocScratchBytes) return ABKV_ERR_SCRATCH;
+    hipError_t err = hipSuccess;
+    ws = scratch_ptr(&err);
+    if (ws == nullptr) return (int)err;
+  }
+  return abkv_decode_attn(q, q_stride_seq, q_stride_head, kv_cache, num_pages, block_table, block_table_stride,
+                          seq_lens, num_seqs, max_pages_per_seq, split_pages, scale, out, out_stride_seq,
+                          out_stride_head, lse, ws, need, stream);
 }
 
 // Side rows per split and head for a packed layout whose smallest head quota is q_min (multiple of 32, at most

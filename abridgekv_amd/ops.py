@@ -146,6 +146,49 @@ def decode_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch
     return out, lse
 
 
+DECODE_NOALLOC_SCRATCH_BYTES = 64 << 20        # ABKV_DECODE_NOALLOC_SCRATCH_BYTES
+ABKV_ERR_SCRATCH = -6
+
+
+def decode_attention_noalloc(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                             seq_lens: torch.Tensor, scale: float, out: torch.Tensor, max_pages: int | None = None,
+                             lse: torch.Tensor | None = None, split_pages: int = DEFAULT_SPLIT_PAGES) -> None:
+    """:func:`decode_attention` for callers that cannot allocate (graph capture, tight serving loops): nothing is
+    allocated, the split partials use the library's static device scratch (64 MiB per GPU, shared by every call on
+    that GPU, so calls overlapping on one GPU race). ``out`` (and ``lse`` if wanted) must be given. A batch whose
+    partials exceed the scratch raises ValueError before any launch."""
+    _check_cache(kv_cache)
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
+             and q.stride(2) == 1, f"q must be cuda bf16 [B, {HEADS_Q}, {HEAD_DIM}] with contiguous dims")
+    B = q.shape[0]
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] >= B and block_table.stride(1) == 1, "block_table must be cuda int32 [B, W]")
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() >= B
+             and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32 [B]")
+    _require(0 < split_pages <= 64 and split_pages % 2 == 0, "split_pages must be an even number in [2, 64]")
+    W = block_table.shape[1]
+    max_pages = W if max_pages is None else int(max_pages)
+    _require(0 < max_pages <= W, "max_pages must be in [1, block_table width]")
+    _require(out is not None and out.dtype == torch.bfloat16 and tuple(out.shape) == (B, HEADS_Q, HEAD_DIM)
+             and out.stride(2) == 1, "out must be given: bf16 [B, 32, 128] with contiguous dims")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= B * HEADS_Q,
+                 "lse must be contiguous fp32 [B, 32]")
+    max_splits = -(-max_pages // split_pages)
+    if max_splits > 1:
+        need = lib().abkv_decode_workspace_size(B, max_splits)
+        _require(need <= DECODE_NOALLOC_SCRATCH_BYTES,
+                 f"{B} sequences x {max_splits} splits need {need} bytes of split partials, more than the "
+                 f"{DECODE_NOALLOC_SCRATCH_BYTES}-byte static scratch (use longer splits or decode_attention)")
+    rc = lib().abkv_decode_attn_noalloc(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
+                                        _ptr(block_table), _row_stride(block_table), _ptr(seq_lens), B, max_pages,
+                                        split_pages, float(scale), _ptr(out), out.stride(0), out.stride(1),
+                                        _ptr(lse), C.c_void_p(_stream()))
+    if rc == ABKV_ERR_SCRATCH:
+        raise ValueError("abkv_decode_attn_noalloc: the batch needs more than the static scratch")
+    check(rc, "abkv_decode_attn_noalloc")
+
+
 def _decode_attention_f32(q, kv_cache, block_table, seq_lens, scale, max_pages, out, lse):
     _check_cache(kv_cache, torch.float32)
     _require(q.is_cuda and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM) and q.stride(2) == 1,

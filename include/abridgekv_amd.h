@@ -52,6 +52,21 @@ int abkv_decode_attn(const void* q, long q_stride_seq, long q_stride_head, const
                      long out_stride_head, float* lse, void* workspace, size_t workspace_bytes,
                      abkv_stream_t stream);
 
+/* abkv_decode_attn without a workspace argument and without any allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The split partials live in a static device array of ABKV_DECODE_NOALLOC_SCRATCH_BYTES that the
+ * library image holds on every GPU it runs on until the process ends; a call whose partials need more
+ * (abkv_decode_workspace_size(num_seqs, ceil(max_pages_per_seq / split_pages)) bytes when that is > 1 split) returns
+ * ABKV_ERR_SCRATCH and launches nothing. Nothing in the scratch has to start at zero (every partial a launch reads
+ * was written by that launch). Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+#define ABKV_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int abkv_decode_attn_noalloc(const void* q, long q_stride_seq, long q_stride_head, const void* kv_cache,
+                             int num_pages, const int32_t* block_table, long block_table_stride,
+                             const int32_t* seq_lens, int num_seqs, int max_pages_per_seq, int split_pages,
+                             float scale, void* out, long out_stride_seq, long out_stride_head, float* lse,
+                             abkv_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * KV-cache row movement for compaction (kernel 2, device half).
  * Replaces GPUModelRunner._execute_kv_copy_group (gpu_model_runner.py:1194-1224): ops [n, 4] int32 rows
