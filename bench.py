@@ -59,16 +59,19 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--batch", type=int, default=None, help="default: 64 for full_model, 256 otherwise")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-pages", type=int, default=None,
                     help="pages per decode split (default: ops.auto_split_pages per launch: 48, 40 or 32)")
-    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "prefill", "prefill_bwd",
+    ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "config1", "prefill", "prefill_bwd",
                                            "compaction", "packed", "copy"],
                     default="serving")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.batch is None:
+        args.batch = 64 if args.workload == "full_model" else 256
+    return args
 
 
 def cpu_threads(torch) -> dict:
@@ -179,7 +182,9 @@ def bench_prefill(args, torch):
     t = s.elapsed_time(e) / 1e3 / args.steps
     flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N) * 32 * B
     tflops = flops / t / 1e12
+    cpu = None if args.no_cpu_baseline else prefill_cpu_baseline(torch, C, K, plen, flops, B, S0)
     return {
+        **({"cpu_baseline": cpu} if cpu else {}),
         "metric": "masked teacher-forced prefill TFLOP/s (visible QK+PV flops); % of bf16 dense MFMA peak",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
@@ -194,6 +199,35 @@ def bench_prefill(args, torch):
                      "mfma_util_rocprof": profiled_mfma_util("prefill_masked_b4_s10240_pmc_mfma.md"),
                      "mfma_util_source": "profiles/prefill_masked_b4_s10240_pmc_mfma.md (MfmaUtil)"},
     }
+
+
+def prefill_cpu_baseline(torch, C, K, plen, flops_full, B_full, S0_full, N_cpu=4, target_s=10.0):
+    """The reference's dense masked attention (oracle.prefill.dense_masked_attention_ref_torch: bf16 scores with an
+    additive mask, fp32 softmax, gen_compress.py:1176-1179) on the host cores, on one sequence of N_cpu blocks of the
+    same geometry. The dense path costs S0^2 per sequence and head whatever the mask, so the full workload's time is
+    the sample's x B x (S0_full / S0_cpu)^2; value = the full workload's visible-pair FLOPs / that time."""
+    from oracle import prefill as op
+
+    host = cpu_threads(torch)
+    S = N_cpu * (C + K)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 32, S, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 8, S, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, 8, S, 128), generator=g).to(torch.bfloat16)
+    mask = torch.from_numpy(op.arith_mask(C, K, N_cpu, [plen])[0])
+    op.dense_masked_attention_ref_torch(q, k, v, mask, 128 ** -0.5)          # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        op.dense_masked_attention_ref_torch(q, k, v, mask, 128 ** -0.5)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    t_full = el / reps * B_full * (S0_full / S) ** 2
+    return {"value": flops_full / t_full / 1e12, "unit": "TFLOP/s", "kind": "port", **host,
+            "sample": f"one sequence of {N_cpu} blocks [{C} | {K}] (S0={S}, raw prompt {plen}), {reps} reps in "
+                      f"{el:.1f} s ({el / reps * 1e3:.0f} ms each), scaled to B={B_full}, S0={S0_full} by the dense "
+                      f"path's B x S0^2 cost; torch CPU bf16 restatement of gen_compress.py:1176-1179"}
 
 
 def bench_prefill_bwd(args, torch):
@@ -292,7 +326,24 @@ def bench_compaction(args, torch):
     torch.cuda.synchronize()
     t_ref = s.elapsed_time(e) / 1e3 / args.steps
     gbps = alg_bytes / t / 1e9
+    # the copy ceiling for these bytes: a plain device copy of one launch's moved bytes (read + write each once)
+    n_copy = int(alg_bytes / (n_launch / args.steps)) // 2
+    src_buf = torch.ones(n_copy // 2, dtype=torch.bfloat16, device=dev)
+    dst_buf = torch.empty_like(src_buf)
+    for _ in range(args.warmup):
+        dst_buf.copy_(src_buf)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps * 6):
+        dst_buf.copy_(src_buf)
+    e.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * n_copy / (s.elapsed_time(e) / 1e3 / (args.steps * 6)) / 1e9
+    del src_buf, dst_buf
+    cpu = None if args.no_cpu_baseline else compaction_cpu_baseline(torch, B, args.seed, layers_per_group)
     return {
+        **({"cpu_baseline": cpu} if cpu else {}),
         "metric": "block-boundary compaction: sequences compacted per second (64 seqs x 36 layers)",
         "value": B / (t + plan_s + prep_s), "unit": "sequences/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": (t + plan_s + prep_s) * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -306,9 +357,145 @@ def bench_compaction(args, torch):
                      "kernel": "kv_move_kernel (fused moves)",
                      "alg_bytes_per_launch": alg_bytes / (n_launch / args.steps),
                      "avg_launch_us": t / (n_launch / args.steps) * 1e6},
+        "copy_ceiling": {"gbps": copy_gbps, "bytes_read": n_copy, "bytes_written": n_copy,
+                         "what": "torch device copy of one move launch's bytes (contiguous)",
+                         "mover_frac_of_copy": gbps / copy_gbps},
         "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
         "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
     }
+
+
+def compaction_cpu_baseline(torch, B, seed, layers_per_group):
+    """The reference's compaction path on the host: the sequential planner restatement (oracle.compaction.Planner:
+    scheduler.py:2060-2204 with the KV manager and block pool) plans the step, then the worker's gather-then-scatter
+    (oracle.compaction.execute_kv_copy_operations, gpu_model_runner.py:1194-1224) runs its op batches over 36 layer
+    caches (2-byte rows of the bf16 layout) holding the pages the ops touch. Both are single-threaded, as the
+    reference's scheduler is."""
+    from abridgekv_amd import workloads
+    from oracle import compaction as oc
+
+    st = workloads.build_compaction_state(B, seed=seed)
+    G = len(st.groups)
+    oracle = oc.Planner(st.num_pages, G, 16, free_order=st.free_order)
+    oracle.apply_events(st.history)
+    oracle.take_step_outputs()
+    t0 = time.perf_counter()
+    oracle.apply_events(st.pending)
+    kv_ops, _ = oracle.take_step_outputs()
+    plan_s = time.perf_counter() - t0
+    # compact host caches per group: only the pages the ops name, renumbered
+    remapped, caches = {}, []
+    for g in range(G):
+        pages = sorted({p for per in kv_ops.values() for b in per[g] for op_ in b for p in (op_[0], op_[2])})
+        idx = {p: i for i, p in enumerate(pages)}
+        caches.append([np.full((max(1, len(pages)), 2, 16, 8, 128), g + 1, dtype=np.uint16)])
+        for rid, per in kv_ops.items():
+            remapped.setdefault(rid, [[] for _ in range(G)])[g] = [
+                [(idx[a], o1, idx[c], o2) for a, o1, c, o2 in b] for b in per[g]]
+    oc.execute_kv_copy_operations(remapped, caches)            # warm-up (first touch of the gather buffers)
+    t0 = time.perf_counter()
+    oc.execute_kv_copy_operations(remapped, caches)            # one layer per group; every layer moves the same rows
+    move_s = (time.perf_counter() - t0) * layers_per_group
+    rows = sum(len(b) for per in kv_ops.values() for g in per for b in g)
+    return {"value": B / (plan_s + move_s), "unit": "sequences/s", "kind": "port", "cores": 1,
+            "cpu": cpu_threads(torch)["cpu"],
+            "sample": f"the whole step: {B} sequences, planner {plan_s * 1e3:.0f} ms + gather-then-scatter of "
+                      f"{rows} reference-format ops per layer, timed on one layer per group and scaled x"
+                      f"{layers_per_group} to {layers_per_group * G} layers: {move_s * 1e3:.0f} ms (numpy fancy "
+                      f"indexing, one thread)"}
+
+
+def bench_config1(args, torch):
+    """Config 1: single-layer abridged decode attention, B=1, quota K=128: 256 prompt rows at positions 0..255, 4 closed
+    blocks of C=512 starting at 256 compressed to 128 code rows at in-block bitrev positions, an open block of 300 rows
+    at 2304..2603 -> 1068 resident rows (812 without the prompt rows, the count the workload text gives; the reference
+    never evicts prompt rows, so both are run). K/V/Q N(0,1) from the seed; the fused RoPE + append kernel rotates
+    them at the stated positions (theta 1e6) while writing the rows to random pages. GPU: decode latency per launch;
+    CPU: the reference decode arithmetic (oracle.decode.decode_ref_torch) over the same rows."""
+    from abridgekv_amd import ops
+    from abridgekv_amd.config import bitrev_offsets
+    from oracle.decode import decode_ref_torch
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    rng = np.random.default_rng(args.seed)
+    scale = ops.default_scale()
+    cos_sin = ops.rope_cos_sin_cache(2604, device=dev)
+    variants, host = {}, None
+    for name, with_prompt in (("rows_1068", True), ("rows_812", False)):
+        pos = list(range(256)) if with_prompt else []
+        for b in range(4):
+            pos += (256 + 512 * b + bitrev_offsets(128, 512)).tolist()
+        pos += list(range(2304, 2604))
+        n = len(pos)
+        need = -(-n // 16)
+        num_pages = 256
+        cache = torch.empty(ops.kv_cache_shape(num_pages), dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+        table = torch.from_numpy(rng.permutation(np.arange(1, num_pages))[:need].astype(np.int32)).view(1, -1).to(dev)
+        k = torch.randn((n, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((n, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
+        qk = torch.empty((n, 32, 128), dtype=torch.bfloat16, device=dev)
+        slots = ops.slot_mapping(torch.zeros(n, dtype=torch.int32, device=dev), torch.arange(n, device=dev), table)
+        ops.rope_kv_append(qk, k, v, torch.tensor(pos, device=dev), cos_sin, slot_mapping=slots, kv_cache=cache,
+                           max_position=2603)
+        q = torch.randn((1, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+        ops.rope_kv_append(q, torch.zeros((1, 8, 128), dtype=torch.bfloat16, device=dev), v[:1],
+                           torch.tensor([2603], device=dev), cos_sin, max_position=2603)
+        sl = torch.tensor([n], dtype=torch.int32, device=dev)
+        out = torch.empty((1, 32, 128), dtype=torch.bfloat16, device=dev)
+        per_split = {}
+        for sp in (4, 8, 16, 32):
+            ws = ops.decode_workspace(1, need, sp, device=dev)
+            for _ in range(args.warmup + 20):
+                ops.decode_attention(q, cache, table, sl, scale, out=out, split_pages=sp, workspace=ws)
+            torch.cuda.synchronize()
+            reps = 200 * max(1, args.steps // 10)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                ops.decode_attention(q, cache, table, sl, scale, out=out, split_pages=sp, workspace=ws)
+            e1.record()
+            torch.cuda.synchronize()
+            per_split[sp] = e0.elapsed_time(e1) * 1e3 / reps
+        sp_best = min(per_split, key=per_split.get)
+        entry = {"rows": n, "us_per_launch": per_split[sp_best], "split_pages": sp_best,
+                 "us_per_launch_by_split_pages": per_split, "gbps": (n * 4096 + 16384) / per_split[sp_best] / 1e3}
+        if not args.no_cpu_baseline:
+            host = host or cpu_threads(torch)
+            used = table[0].long()
+            cpu_cache = cache[used].cpu()
+            cpu_tab = torch.arange(need, dtype=torch.int32).view(1, -1)
+            cpu_q, cpu_sl = q.cpu(), torch.tensor([n])
+            decode_ref_torch(cpu_q, cpu_cache, cpu_tab, cpu_sl, scale)
+            creps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 4.0:
+                decode_ref_torch(cpu_q, cpu_cache, cpu_tab, cpu_sl, scale)
+                creps += 1
+            entry["cpu_us_per_call"] = (time.perf_counter() - t0) / creps * 1e6
+            entry["cpu_reps"] = creps
+        variants[name] = entry
+    main = variants["rows_1068"]
+    us = main["us_per_launch"]
+    res = {
+        "metric": "single-layer abridged decode attention, B=1: tokens/s (1 / launch latency)",
+        "value": 1e6 / us, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q from the seed, RoPE theta 1e6 at the layout's positions",
+        "config": {"workload": "config 1: one layer, B=1, quota 128, prompt 256 + 4 closed blocks x 128 code rows + "
+                               "open block 300 (1068 rows; the 812-row variant without prompt rows alongside)",
+                   "global_batch": 1},
+        "roofline": {"bound": "hbm (latency-bound at B=1: 4.4 MB per launch)", "achieved": main["gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": main["gbps"] / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "decode_attn_kernel + decode_merge_kernel", "alg_bytes_per_launch": 1068 * 4096 + 16384,
+                     "avg_launch_us": us},
+        "variants": variants,
+    }
+    if "cpu_us_per_call" in main:
+        res["cpu_baseline"] = {"value": 1e6 / main["cpu_us_per_call"], "unit": "tokens/s", "kind": "port", **host,
+                               "sample": f"the same 1068 rows, {main['cpu_reps']} calls in 4 s (812 rows: "
+                                         f"{variants['rows_812']['cpu_us_per_call']:.0f} us per call); torch CPU "
+                                         f"restatement of the reference decode arithmetic"}
+    return res
 
 
 def bench_serving(args, torch):
@@ -490,9 +677,10 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "prefill", "prefill_bwd", "compaction", "packed", "copy"):
-        res = {"serving": bench_serving, "prefill": bench_prefill, "prefill_bwd": bench_prefill_bwd,
-               "compaction": bench_compaction, "packed": bench_packed, "copy": bench_copy}[args.workload](args, torch)
+    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "copy"):
+        res = {"serving": bench_serving, "config1": bench_config1, "prefill": bench_prefill,
+               "prefill_bwd": bench_prefill_bwd, "compaction": bench_compaction, "packed": bench_packed,
+               "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
@@ -570,13 +758,16 @@ def main():
     torch.cuda.synchronize()
     step_s = (time.perf_counter() - t1) / args.steps
 
+    traffic_profile = ("decode_attn_saturated_b256_pmc_traffic.md" if args.workload == "saturated"
+                       else "decode_attn_full_model_b64_pmc_traffic.md")
     kv_bytes = st.kv_bytes_per_step()
     qo_bytes = L * B * (32 * 128 * 2) * 2
     alg_bytes = kv_bytes + qo_bytes
     attn_s_per_step = attn_ms / 1e3 / args.steps
     achieved = alg_bytes / attn_s_per_step / 1e9
     res = {
-        "metric": "abridged decode-attn tokens/s per GPU (B=256, 32K ctx); % HBM peak BW",
+        "metric": ("abridged decode-attn tokens/s per GPU (B=256, 32K ctx); % HBM peak BW" if args.workload ==
+                   "saturated" else "abridged full-model decode-attn tokens/s per GPU (B=64, 17K ctx); % HBM peak BW"),
         "value": B / step_s,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -592,9 +783,9 @@ def main():
                    "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
-                     "traffic": (profiled_traffic("decode_attn_saturated_b256_pmc_traffic.md")
-                                 if args.workload == "saturated" and args.batch == 256 and args.seed == 0 else None),
-                     "traffic_source": "profiles/decode_attn_saturated_b256_pmc_traffic.md (decode_attn_kernel)",
+                     "traffic": (profiled_traffic(traffic_profile) if args.seed == 0 and
+                                 args.batch == (256 if args.workload == "saturated" else 64) else None),
+                     "traffic_source": f"profiles/{traffic_profile} (decode_attn_kernel)",
                      "kernel": "decode_attn_kernel (+ decode_merge_kernel), per layer launch",
                      "alg_bytes_per_launch": alg_bytes / L, "avg_launch_us": attn_s_per_step / L * 1e6},
         "attn_tokens_per_s": B / attn_s_per_step,

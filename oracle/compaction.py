@@ -336,6 +336,27 @@ class Planner:
         self.pending_block_table_truncations[rid] = tuple(len(m.blocks(rid)) for m in self.managers)
         return SpanRemovalResult(True, masked, total_freed)
 
+    def apply_events(self, rows) -> None:
+        """Scheduler events in the native planner's event-row format (kind, rid, a, b, group_mask, 0): 0 add,
+        1 schedule a tokens (allocate, then count them computed), 2 mask [a, b) in the groups of group_mask (< 0:
+        all), 3 free, 4 take (drop) the step outputs. A rejected allocation or span raises."""
+        for kind, rid, a, b, gm, _ in np.asarray(rows, np.int64).tolist():
+            if kind == 0:
+                self.add_request(rid)
+            elif kind == 1:
+                if self.allocate_slots(rid, a) is None:
+                    raise RuntimeError("oracle pool exhausted")
+                self.requests[rid].num_computed_tokens += a
+            elif kind == 2:
+                groups = None if gm < 0 else [g for g in range(self.num_groups) if (gm >> g) & 1]
+                res = self.mask_token_span(rid, a, b, groups)
+                if not res.success:
+                    raise RuntimeError(res.error_message)
+            elif kind == 3:
+                self.free_request(rid)
+            else:
+                self.take_step_outputs()
+
     def take_step_outputs(self):
         """What the next SchedulerOutput carries (output.py:221-225), then cleared."""
         ops, trunc = self.pending_kv_copy_operations, self.pending_block_table_truncations

@@ -205,6 +205,27 @@ def _softmax_rows(s):
     return e / np.where(z > 0, z, 1.0)
 
 
+def dense_masked_attention_ref_torch(q, k, v, mask, scale):
+    """The reference's dense teacher-forced attention on CPU torch (the timed CPU baseline of the masked prefill):
+    abridgekv/gen_compress.py:1158-1160, 1176-1179 -- an additive mask of finfo(dtype).min on hidden pairs, scores
+    ``q @ repeat_kv(k)^T * scale + add`` in the input dtype, softmax in float32 cast back, ``@ repeat_kv(v)``.
+
+    q [B, Hq, S, D], k / v [B, Hkv, S, D] torch tensors (bf16 as the reference's model runs); mask [S, S] or
+    [B, 1, S, S] bool. Returns out [B, Hq, S, D] in q's dtype."""
+    import torch
+
+    g = q.shape[1] // k.shape[1]
+    m = torch.as_tensor(mask)
+    if m.ndim == 2:
+        m = m[None, None]
+    add = torch.zeros(m.shape, dtype=q.dtype).masked_fill(~m, torch.finfo(q.dtype).min)
+    kk = k.repeat_interleave(g, dim=1)
+    vv = v.repeat_interleave(g, dim=1)
+    w = torch.matmul(q, kk.transpose(2, 3)) * scale + add
+    w = torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
+    return torch.matmul(w, vv)
+
+
 def visible_pairs(C, K, N, prompt_len=None):
     """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
     m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len])

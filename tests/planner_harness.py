@@ -76,21 +76,7 @@ def make_schedule(seed, n_req, C, K, quotas, max_prompt, max_closed, num_steps=N
     return ot.build_schedule(prompts, [1 << 30] * n_req, starts, total, C, K, quotas)
 
 
+
 def apply_events_oracle(planner: oc.Planner, rows) -> None:
-    """The oracle's reading of abkv_planner_apply_events rows (kind, rid, a, b, group_mask, 0): 0 add, 1 schedule a
-    tokens (allocate, then count them computed), 2 mask [a, b) in the groups of group_mask (< 0: all), 3 free,
-    4 take (drop) the step outputs."""
-    for kind, rid, a, b, gm, _ in np.asarray(rows, np.int64).tolist():
-        if kind == 0:
-            planner.add_request(rid)
-        elif kind == 1:
-            assert planner.allocate_slots(rid, a) is not None, "oracle pool exhausted"
-            planner.requests[rid].num_computed_tokens += a
-        elif kind == 2:
-            groups = None if gm < 0 else [g for g in range(planner.num_groups) if (gm >> g) & 1]
-            res = planner.mask_token_span(rid, a, b, groups)
-            assert res.success, res.error_message
-        elif kind == 3:
-            planner.free_request(rid)
-        else:
-            planner.take_step_outputs()
+    """abkv_planner_apply_events rows through the oracle planner."""
+    planner.apply_events(rows)

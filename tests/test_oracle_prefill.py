@@ -205,3 +205,27 @@ def test_row_and_key_restricted_attention_equal_the_full_forms():
     dk_r, dv_r = op.masked_attention_key_grads_fp64(q, k, v, dout, mask_fn, keys, scale)
     np.testing.assert_allclose(dk_r, dk[keys], rtol=1e-10, atol=1e-12)
     np.testing.assert_allclose(dv_r, dv[keys], rtol=1e-10, atol=1e-12)
+
+
+def test_dense_reference_torch_matches_fp64_within_bf16():
+    """The CPU baseline's dense bf16 attention (the reference's gen_compress.py arithmetic) against the fp64 oracle on
+    the same bf16 inputs: within 3e-2 (that arithmetic rounds scores and probabilities to bf16 itself), and a key
+    hidden from a row cannot move that row's output by a single bit."""
+    import torch
+
+    C, K, N = 16, 8, 3
+    S = N * (C + K)
+    rng = np.random.default_rng(2)
+    q, k, v = (rng.standard_normal(sh) for sh in ((S, 4, 32), (S, 2, 32), (S, 2, 32)))
+    t = [torch.from_numpy(x).permute(1, 0, 2)[None].to(torch.bfloat16) for x in (q, k, v)]
+    q, k, v = (x[0].permute(1, 0, 2).double().numpy() for x in t)
+    mask = op.arith_mask(C, K, N, [10])[0]
+    ref, _ = op.masked_attention_fp64(q, k, v, mask, 0.3)
+    got = op.dense_masked_attention_ref_torch(*t, torch.from_numpy(mask), 0.3)[0].permute(1, 0, 2).float().numpy()
+    assert np.abs(got - ref).max() <= 3e-2
+    t2 = [x.clone() for x in t]
+    t2[1][0, :, S - 1] = 100.0                 # the last key is visible only to the last block's code rows
+    got2 = op.dense_masked_attention_ref_torch(*t2, torch.from_numpy(mask), 0.3)[0].permute(1, 0, 2)
+    hidden_rows = ~mask[:, S - 1]
+    assert torch.equal(got2[torch.from_numpy(hidden_rows)], torch.from_numpy(got)[torch.from_numpy(hidden_rows)].to(
+        torch.bfloat16))
