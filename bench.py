@@ -326,20 +326,24 @@ def bench_compaction(args, torch):
     torch.cuda.synchronize()
     t_ref = s.elapsed_time(e) / 1e3 / args.steps
     gbps = alg_bytes / t / 1e9
-    # the copy ceiling for these bytes: a plain device copy of one launch's moved bytes (read + write each once)
+    # the copy ceiling for these bytes: plain device copies of one launch's moved bytes (read + write each once),
+    # each from the next of 16 slices of a buffer far larger than the 256 MB last-level cache, as the mover's pages are
     n_copy = int(alg_bytes / (n_launch / args.steps)) // 2
-    src_buf = torch.ones(n_copy // 2, dtype=torch.bfloat16, device=dev)
+    n_el = n_copy // 2
+    src_buf = torch.ones(16 * n_el, dtype=torch.bfloat16, device=dev)
     dst_buf = torch.empty_like(src_buf)
-    for _ in range(args.warmup):
-        dst_buf.copy_(src_buf)
+    for i in range(max(args.warmup, 1)):
+        dst_buf[i * n_el:(i + 1) * n_el].copy_(src_buf[i * n_el:(i + 1) * n_el])
     torch.cuda.synchronize()
+    reps = 16 * max(1, args.steps // 4)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(args.steps * 6):
-        dst_buf.copy_(src_buf)
+    for i in range(reps):
+        sl = slice((i % 16) * n_el, (i % 16 + 1) * n_el)
+        dst_buf[sl].copy_(src_buf[sl])
     e.record()
     torch.cuda.synchronize()
-    copy_gbps = 2 * n_copy / (s.elapsed_time(e) / 1e3 / (args.steps * 6)) / 1e9
+    copy_gbps = 2 * n_copy / (s.elapsed_time(e) / 1e3 / reps) / 1e9
     del src_buf, dst_buf
     cpu = None if args.no_cpu_baseline else compaction_cpu_baseline(torch, B, args.seed, layers_per_group)
     return {
@@ -358,7 +362,8 @@ def bench_compaction(args, torch):
                      "alg_bytes_per_launch": alg_bytes / (n_launch / args.steps),
                      "avg_launch_us": t / (n_launch / args.steps) * 1e6},
         "copy_ceiling": {"gbps": copy_gbps, "bytes_read": n_copy, "bytes_written": n_copy,
-                         "what": "torch device copy of one move launch's bytes (contiguous)",
+                         "what": "torch device copies of one move launch's bytes, contiguous, cycling through 16 "
+                                 "slices of a buffer larger than the last-level cache",
                          "mover_frac_of_copy": gbps / copy_gbps},
         "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
         "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
