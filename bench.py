@@ -270,8 +270,10 @@ def bench_prefill_bwd(args, torch):
         "config": {"workload": f"masked prefill backward B={B}, N={N} blocks of [{C} content | {K} codes], "
                                f"S0={S0}, raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
-                     "traffic": None, "kernel": "prefill_bwd_prep_kernel + prefill_bwd_dq_kernel + "
-                                                "prefill_bwd_dkv_kernel", "alg_flops_per_launch": flops,
+                     "traffic": profiled_traffic("prefill_masked_bwd_b4_s10240_pmc_traffic.md"),
+                     "traffic_source": "profiles/prefill_masked_bwd_b4_s10240_pmc_traffic.md (the three kernels)",
+                     "kernel": "prefill_bwd_prep_kernel + prefill_bwd_dq_kernel + prefill_bwd_dkv_kernel",
+                     "alg_flops_per_launch": flops,
                      "avg_launch_us": t * 1e6},
     }
 

@@ -19,7 +19,7 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_profile_readers_parse_committed_summaries():
     for name in ("decode_attn_serving_b256_pmc_traffic.md", "decode_attn_saturated_b256_pmc_traffic.md",
                  "prefill_masked_b4_s10240_pmc_traffic.md", "kv_move_compaction_64seq_pmc_traffic.md",
-                 "decode_attn_full_model_b64_pmc_traffic.md"):
+                 "decode_attn_full_model_b64_pmc_traffic.md", "prefill_masked_bwd_b4_s10240_pmc_traffic.md"):
         t = bench.profiled_traffic(name)
         assert t is not None and t > 1e8, name
     u = bench.profiled_mfma_util("prefill_masked_b4_s10240_pmc_mfma.md")
