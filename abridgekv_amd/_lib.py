@@ -22,6 +22,8 @@ SIGNATURES = {
                                            C.c_int, C.c_int, C.c_float, _vp, C.c_long, C.c_long, _vp, _vp]),
     "abkv_kv_move_segments": (C.c_int, [C.POINTER(_vp), C.c_int, C.c_int, C.c_int, C.c_long, C.c_long, C.c_int,
                                         _vp, _vp, C.c_int, _vp]),
+    "abkv_kv_move_mixed": (C.c_int, [C.POINTER(_vp), C.c_int, C.c_int, C.c_int, C.c_long, C.c_long, C.c_int,
+                                     _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
     "abkv_kv_stage_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "abkv_kv_copy_staged": (C.c_int, [C.POINTER(_vp), C.c_int, C.c_int, C.c_int, C.c_long, C.c_long, C.c_int, _vp,
                                       C.c_int, _vp, C.c_size_t, _vp]),
@@ -76,6 +78,7 @@ SIGNATURES = {
     "abkv_planner_pending_sizes": (C.c_int, [_vp, _i64p, _i64p, _i64p]),
     "abkv_planner_take_step_outputs": (C.c_int, [_vp, _i64p, C.c_int64, _i64p, _i64p, C.c_int64, _i64p, _i64p,
                                                  C.c_int64, _i64p]),
+    "abkv_moves_pack": (C.c_int64, [_i64p, C.c_int64, C.c_int, _i32p, C.c_int64, _i64p]),
     "abkv_planner_num_free": (C.c_int64, [_vp]),
     "abkv_planner_free_queue": (C.c_int64, [_vp, _i32p, C.c_int64]),
     "abkv_planner_block_ids": (C.c_int64, [_vp, C.c_int64, C.c_int, _i32p, C.c_int64]),

@@ -12,10 +12,12 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libabridgekv_amd.so"
+PROBE_LIB = PKG / "libabridgekv_probes.so"      # measurement probes, loaded by the benchmark only
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 DEVICE_SOURCES = ["decode_attn.hip", "kv_cache.hip", "prefill_attn.hip", "paged_prefill.hip", "attn_f32.hip"]
 HOST_SOURCES = ["planner.cpp"]
+PROBE_SOURCES = ["probes.hip"]
 
 # -packed-fp32-ops off: hipcc would otherwise emit v_pk_{add,mul,fma}_f32 from scalar float code.
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-I{PKG.parent / 'include'}"]
@@ -48,8 +50,16 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB)
+    probe_objs = []
+    for src in PROBE_SOURCES:
+        obj = objdir / (src + ".o")
+        _run([HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        probe_objs.append(obj)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, probe_objs), "-o", str(tmp)])
+    os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB.name}")
     return LIB
 
 

@@ -3,18 +3,20 @@
 // Compaction executor: replaces GPUModelRunner._execute_kv_copy_operations / _execute_kv_copy_group
 // (third_party/vllm_overlay/vllm/v1/worker/gpu_model_runner.py:1147-1224), which applies one ordered batch of
 // (src_block, src_off, dst_block, dst_off) ops per KV-cache group with gather-then-scatter semantics to every layer
-// tensor of the group. Here a launch takes a list of op *segments* (one per request batch) and applies each segment
-// to up to kMaxLayers layer tensors; grid = (segment, layer, byte part), 256 threads.
+// tensor of the group. Here one launch takes up to two op lists and applies them to up to kMaxLayers layer tensors:
+// ordered *segments* (one per request run whose ops depend on each other's order) and *independent* ops.
 //
-// Exactness without a staging buffer: a workgroup walks its segment in op order, kMoveRows ops at a time, loading
-// every source row of the chunk into registers, then (after a barrier) storing every destination row, then a
-// barrier. This equals gather-then-scatter, for any chunk size, whenever no op of the segment reads a slot that an
+// Exactness without a staging buffer: a workgroup walks an ordered segment in op order, kMoveRows ops at a time,
+// loading every source row of the chunk into registers, then (after a barrier) storing every destination row, then
+// a barrier. This equals gather-then-scatter, for any chunk size, whenever no op of the segment reads a slot that an
 // EARLIER op of the same segment writes (a later op may overwrite a slot an earlier op read: that read has happened)
 // -- true for compaction ops, which are emitted in increasing source order with dst < src
 // (single_type_kv_cache_manager.py:378-381) -- and no two ops write one slot. Segments must touch disjoint pages
-// (different requests' pages are disjoint; one request contributes one segment per batch). For op lists that
-// violate the ordering precondition the two-phase gather/scatter entry points below stage rows through a workspace
-// instead.
+// (different requests' pages are disjoint; one request contributes one segment per batch). Independent ops read and
+// write no slot that another op of the launch writes (a request run in which no op's destination is another op's
+// source: the planner's fused moves of a run whose shift is at least its length), so they run in any order and any
+// split. For op lists that violate the ordering precondition the two-phase gather/scatter entry points below stage
+// rows through a workspace instead.
 //
 // KV append: replaces the stock vLLM compiled op reshape_and_cache(_flash) that writes each new token's K and V
 // rows at slot_mapping[t] (slots from block_table.py:186-197); slot < 0 is skipped (padding).
@@ -23,8 +25,9 @@
 namespace abkv {
 
 constexpr int kMaxLayers = 16;
-constexpr int kMoveRows = 64;     // ops per chunk: 64 rows x 1 KiB (one byte part) in flight per workgroup
-constexpr int kMoveParts = 4;     // workgroups per (segment, layer), each moving one quarter of every row
+constexpr int kMoveRows = 64;     // ordered segments: ops per chunk, 64 rows x 1 KiB (one byte part) in flight
+constexpr int kMoveParts = 4;     // ordered segments: workgroups per (segment, layer), one quarter of every row each
+constexpr int kFreeRows = 4;      // independent ops: ops (whole rows) per workgroup
 
 struct LayerPtrs {
   char* p[kMaxLayers];
@@ -46,62 +49,125 @@ __device__ __forceinline__ bool op_ok(const int32_t* op, int num_pages, int bloc
          (unsigned)op[1] < (unsigned)block_size && (unsigned)op[3] < (unsigned)block_size;
 }
 
-// One "row" of an op = slot_bytes of K plus slot_bytes of V (4 KiB in the served geometry). A workgroup owns one
-// byte part of the rows (grid.z parts; byte parts of a row never interact, so every part may run independently)
-// and walks its segment kMoveRows ops at a time: wave w of the workgroup moves rows w, w+4, ..., lane l the l-th
-// 16-byte vector of the part. Lane l of every wave fetches op c0 + l once per chunk; the row offsets are broadcast
-// with readlane (wave-uniform), so the 16 source loads of a thread issue back to back, land in registers before
-// the barrier, and the 16 stores follow it.
-__global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
-  const int seg = blockIdx.x;
-  char* base = a.layers.p[blockIdx.y];
+// One "row" of an op = slot_bytes of K plus slot_bytes of V (4 KiB in the served geometry). One launch moves two
+// kinds of op lists, each workgroup taking one kind (blockIdx.x below n_ordered_wgs: ordered segments, first in
+// dispatch order since they are the longest; above: independent ops).
+//  Ordered segment (move_ordered): kMoveParts workgroups per (segment, layer), adjacent in dispatch order, each owning
+//    one byte part of the rows (byte parts of a row never interact). The workgroup walks its segment kMoveRows ops at
+//    a time: lane l of every wave fetches op c0 + l once per chunk, the row offsets are broadcast with readlane
+//    (wave-uniform), wave w moves rows w, w+4, ..., lane l the l-th 16-byte vector of the part; the 16 source loads
+//    of a thread issue back to back and land in registers before the barrier, the 16 stores follow it.
+//  Independent ops (move_free): no op reads or writes a slot another op of the list writes, so any split and order
+//    is exact; a workgroup moves kFreeRows consecutive ops as whole rows (consecutive ops are mostly consecutive slots
+//    of one page, so the workgroup reads and writes kFreeRows x 2 KiB contiguous runs of K and of V), thread t the
+//    t-th 16-byte vector of every row, kFreeRows loads back to back, then the stores.
+// Ordered segment, software-pipelined: the op fetch and source loads of chunk c + 1 are issued before the stores of
+// chunk c (a later op never reads a slot an earlier op writes, so those loads may run ahead of the stores), and the
+// stores of chunk c + 1 follow the barrier that closes its loads. One memory round trip per chunk on the critical
+// path instead of two.
+struct OrderedChunk {
+  long soff[kMoveRows / 4], doff[kMoveRows / 4];
+  u32x4 buf[kMoveRows / 4];
+};
+
+__device__ __forceinline__ void ordered_fetch(const MoveArgs& a, int c0, int s1, int wave, int lane, OrderedChunk& ch) {
+  const int n = min(kMoveRows, s1 - c0);
+  int o0 = -1, o1 = -1, o2 = -1, o3 = -1;                 // lane l: op c0 + l
+  if (lane < n) {
+    const int32_t* op = a.ops + 4L * (c0 + lane);
+    o0 = op[0];
+    o1 = op[1];
+    o2 = op[2];
+    o3 = op[3];
+  }
+  const bool ok_l = lane < n && (unsigned)o0 < (unsigned)a.num_pages && (unsigned)o2 < (unsigned)a.num_pages &&
+                    (unsigned)o1 < (unsigned)a.block_size && (unsigned)o3 < (unsigned)a.block_size;
+  const unsigned long long ok_mask = __ballot(ok_l);
+  // wave-uniform byte offsets of this wave's rows (invalid rows read slot 0 of page 0 and store nothing)
+#pragma unroll
+  for (int k = 0; k < kMoveRows / 4; ++k) {
+    const int r = wave + 4 * k;                            // < 64: a lane of this wave
+    const bool ok = (ok_mask >> r) & 1ull;
+    ch.soff[k] = ok ? (long)__builtin_amdgcn_readlane(o0, r) * a.page_bytes +
+                          (long)__builtin_amdgcn_readlane(o1, r) * a.slot_bytes : 0;
+    ch.doff[k] = ok ? (long)__builtin_amdgcn_readlane(o2, r) * a.page_bytes +
+                          (long)__builtin_amdgcn_readlane(o3, r) * a.slot_bytes : -1;
+  }
+}
+
+__device__ __forceinline__ void move_ordered(const MoveArgs& a, char* base, int seg, int part) {
   const int s0 = a.seg_offsets[seg], s1 = a.seg_offsets[seg + 1];
   const int row_vec = (2 * a.slot_bytes) / 16;          // 16-byte vectors per row
-  const int vpp = (row_vec + (int)gridDim.z - 1) / (int)gridDim.z;   // vectors per part
+  const int vpp = (row_vec + kMoveParts - 1) / kMoveParts;   // vectors per part
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int c0 = s0; c0 < s1; c0 += kMoveRows) {
-    const int n = min(kMoveRows, s1 - c0);
-    int o0 = -1, o1 = -1, o2 = -1, o3 = -1;               // lane l: op c0 + l
-    if (lane < n) {
-      const int32_t* op = a.ops + 4L * (c0 + lane);
-      o0 = op[0];
-      o1 = op[1];
-      o2 = op[2];
-      o3 = op[3];
-    }
-    const bool ok_l = lane < n && (unsigned)o0 < (unsigned)a.num_pages && (unsigned)o2 < (unsigned)a.num_pages &&
-                      (unsigned)o1 < (unsigned)a.block_size && (unsigned)o3 < (unsigned)a.block_size;
-    const unsigned long long ok_mask = __ballot(ok_l);
-    // wave-uniform byte offsets of this wave's rows (invalid rows read slot 0 of page 0 and store nothing)
-    long soff[kMoveRows / 4], doff[kMoveRows / 4];
+  if (s0 >= s1) return;
+  for (int u0 = 0; u0 < vpp; u0 += 64) {                  // one round in the served geometry (vpp = 64)
+    const int u = u0 + lane;
+    const int v = part * vpp + u;
+    const bool active = u < vpp && v < row_vec;
+    const int half = v >= row_vec / 2;                     // 0: K, 1: V
+    const long inner = active ? (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16 : 0;
+    OrderedChunk cur, nxt;
+    ordered_fetch(a, s0, s1, wave, lane, cur);
 #pragma unroll
-    for (int k = 0; k < kMoveRows / 4; ++k) {
-      const int r = wave + 4 * k;                          // < 64: a lane of this wave
-      const bool ok = (ok_mask >> r) & 1ull;
-      soff[k] = ok ? (long)__builtin_amdgcn_readlane(o0, r) * a.page_bytes +
-                         (long)__builtin_amdgcn_readlane(o1, r) * a.slot_bytes : 0;
-      doff[k] = ok ? (long)__builtin_amdgcn_readlane(o2, r) * a.page_bytes +
-                         (long)__builtin_amdgcn_readlane(o3, r) * a.slot_bytes : -1;
-    }
-    for (int u0 = 0; u0 < vpp; u0 += 64) {
-      const int u = u0 + lane;
-      const int v = (int)blockIdx.z * vpp + u;
-      const bool active = u < vpp && v < row_vec;
-      const int half = v >= row_vec / 2;                   // 0: K, 1: V
-      const long inner = active ? (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16 : 0;
-      u32x4 buf[kMoveRows / 4];
-#pragma unroll
-      for (int k = 0; k < kMoveRows / 4; ++k) buf[k] = *reinterpret_cast<const u32x4*>(base + soff[k] + inner);
-      // every source row of the chunk is in registers before any wave stores (a store may hit a slot another wave
-      // of the chunk reads)
+    for (int k = 0; k < kMoveRows / 4; ++k) cur.buf[k] = *reinterpret_cast<const u32x4*>(base + cur.soff[k] + inner);
+    for (int c0 = s0; c0 < s1; c0 += kMoveRows) {
+      const bool more = c0 + kMoveRows < s1;
+      if (more) ordered_fetch(a, c0 + kMoveRows, s1, wave, lane, nxt);
+      // every source row of chunk c is in registers before any wave stores it (a store may hit a slot another wave
+      // of the chunk reads); this also completes the op fetch of chunk c + 1
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if (more) {
+#pragma unroll
+        for (int k = 0; k < kMoveRows / 4; ++k)
+          nxt.buf[k] = *reinterpret_cast<const u32x4*>(base + nxt.soff[k] + inner);
+      }
 #pragma unroll
       for (int k = 0; k < kMoveRows / 4; ++k)
-        if (doff[k] >= 0 && active) *reinterpret_cast<u32x4*>(base + doff[k] + inner) = buf[k];
-      __syncthreads();
+        if (cur.doff[k] >= 0 && active) *reinterpret_cast<u32x4*>(base + cur.doff[k] + inner) = cur.buf[k];
+      cur = nxt;
     }
+  }
+}
+
+__device__ __forceinline__ void move_free(const MoveArgs& a, const int32_t* __restrict__ free_ops, char* base, int i0,
+                                          int i1) {
+  // the workgroup's ops, read once before any store (uniform addresses, nothing written before them: scalar loads)
+  long sb[kFreeRows], db[kFreeRows];
+#pragma unroll
+  for (int r = 0; r < kFreeRows; ++r) {
+    const int i = i0 + r;
+    const int32_t* op = free_ops + 4L * i;
+    const bool ok = i < i1 && op_ok(op, a.num_pages, a.block_size);
+    sb[r] = ok ? (long)op[0] * a.page_bytes + (long)op[1] * a.slot_bytes : 0;
+    db[r] = ok ? (long)op[2] * a.page_bytes + (long)op[3] * a.slot_bytes : -1;
+  }
+  const int row_vec = (2 * a.slot_bytes) / 16;
+  for (int v = threadIdx.x; v < row_vec; v += 256) {
+    const int half = v >= row_vec / 2;
+    const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
+    u32x4 buf[kFreeRows];
+#pragma unroll
+    for (int r = 0; r < kFreeRows; ++r) buf[r] = *reinterpret_cast<const u32x4*>(base + sb[r] + inner);
+#pragma unroll
+    for (int r = 0; r < kFreeRows; ++r)
+      if (db[r] >= 0) *reinterpret_cast<u32x4*>(base + db[r] + inner) = buf[r];
+  }
+}
+
+// free_ops is its own argument (not an offset read from seg_offsets): an independent-op workgroup lives for a few
+// memory round trips, and a dependent load before its op fetch would add one.
+__global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a, int n_ordered_wgs,
+                                                      const int32_t* __restrict__ free_ops, int n_free) {
+  char* base = a.layers.p[blockIdx.y];
+  const int x = blockIdx.x;
+  if (x < n_ordered_wgs) {
+    move_ordered(a, base, x / kMoveParts, x % kMoveParts);
+  } else {
+    const int i0 = (x - n_ordered_wgs) * kFreeRows;
+    move_free(a, free_ops, base, i0, min(i0 + kFreeRows, n_free));
   }
 }
 
@@ -318,12 +384,17 @@ __global__ __launch_bounds__(256) void packed_capture_kernel(CaptureArgs a) {
 
 extern "C" {
 
-int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
-                          long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments, hipStream_t stream) {
+int abkv_kv_move_mixed(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                       long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments,
+                       const int32_t* free_ops, int n_free, hipStream_t stream) {
   using namespace abkv;
-  if (n_segments <= 0) return 0;
-  if (ops == nullptr || seg_offsets == nullptr || slot_bytes <= 0 || slot_bytes % 16 != 0)
+  if (n_segments < 0 || n_free < 0) return (int)hipErrorInvalidValue;
+  if (n_segments == 0 && n_free == 0) return 0;
+  if ((n_segments > 0 && (ops == nullptr || seg_offsets == nullptr)) || (n_free > 0 && free_ops == nullptr) ||
+      slot_bytes <= 0 || slot_bytes % 16 != 0)
     return (int)hipErrorInvalidValue;
+  const long wgs = (long)n_segments * kMoveParts + (n_free + kFreeRows - 1) / kFreeRows;
+  if (wgs > 0x7FFFFFFFL) return (int)hipErrorInvalidValue;
   MoveArgs a;
   if (!fill_layers(a.layers, layer_caches, n_layers)) return (int)hipErrorInvalidValue;
   a.ops = ops;
@@ -333,8 +404,17 @@ int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages
   a.slot_bytes = slot_bytes;
   a.num_pages = num_pages;
   a.block_size = block_size;
-  hipLaunchKernelGGL(kv_move_kernel, dim3(n_segments, n_layers, kMoveParts), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(kv_move_kernel, dim3((unsigned)wgs, n_layers), dim3(256), 0, stream, a, n_segments * kMoveParts,
+                     free_ops, n_free);
   return (int)hipGetLastError();
+}
+
+int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                          long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets,
+                          int n_segments, hipStream_t stream) {
+  if (n_segments <= 0) return 0;
+  return abkv_kv_move_mixed(layer_caches, n_layers, num_pages, block_size, page_bytes, half_bytes, slot_bytes, ops,
+                            seg_offsets, n_segments, nullptr, 0, stream);
 }
 
 size_t abkv_kv_stage_bytes(int n_layers, int n_ops, int slot_bytes) {

@@ -497,6 +497,108 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   return ABKV_OK;
 }
 
+// Device-ready move lists of a step's fused rows (the fused_rows of abkv_planner_take_step_outputs; the rows of one
+// (request, group) contiguous and in emission order). Within a (request, group) run, op j *depends on* op i when
+// op j's destination is op i's source (j must store after i loads). Ops on such an edge are kept in one ordered
+// segment per run, in emission order (the walker's order matters there); every other op reads a slot no op writes
+// and writes a slot no op reads, so it is independent. Per group g < num_groups, in `out` back to back: the ops
+// [n_g, 4] int32 (src_block, src_off, dst_block, dst_off) -- the ordered segments first, then the independent ops --
+// followed by the segment offsets [n_segments + 1] relative to the group's first op (the last one is where the
+// independent ops start). index [num_groups, 5] = (ops_at, n_ops, offs_at, n_segments, n_free), positions in int32
+// elements of `out`; each group's section starts at a multiple of 4 elements (16 bytes). Returns the elements
+// written; ABKV_ERR_CAPACITY if out_cap < 5 * n + 4 * num_groups; ABKV_ERR_ARG for a group outside
+// [0, num_groups), a (request, group) run that appears twice, an offset outside [0, 65536), a slot read by two ops,
+// or an op that reads a slot an earlier op of its run writes.
+int64_t abkv_moves_pack(const int64_t* fused_rows, int64_t n, int num_groups, int32_t* out, int64_t out_cap,
+                        int64_t* index) {
+  if (n < 0 || num_groups <= 0 || (n > 0 && !fused_rows) || !out || !index) return ABKV_ERR_ARG;
+  if (out_cap < 5 * n + 4 * (int64_t)num_groups) return ABKV_ERR_CAPACITY;
+  const int G = num_groups;
+  struct Run {
+    int64_t lo, hi, n_chained;
+  };
+  std::vector<std::vector<Run>> runs((size_t)G);
+  std::vector<int64_t> n_ops((size_t)G, 0), n_chained((size_t)G, 0);
+  std::vector<uint8_t> chained((size_t)n, 0);
+  std::unordered_map<int64_t, int> seen;                 // (request, group) -> 1
+  std::vector<int64_t> tkey;
+  std::vector<int32_t> tidx;
+  auto slot_key = [](int64_t block, int64_t off) { return (block << 16) | off; };
+  auto slot_hash = [](int64_t k, size_t cap) {
+    return (size_t)((uint64_t)k * 0x9E3779B97F4A7C15ull >> 20) & (cap - 1);
+  };
+  for (int64_t lo = 0; lo < n;) {
+    const int64_t rid = fused_rows[6 * lo], g = fused_rows[6 * lo + 1];
+    if (g < 0 || g >= G) return ABKV_ERR_ARG;
+    int64_t hi = lo + 1;
+    while (hi < n && fused_rows[6 * hi] == rid && fused_rows[6 * hi + 1] == g) ++hi;
+    if (!seen.emplace(rid * G + g, 1).second) return ABKV_ERR_ARG;
+    // open-addressing table of the run's source slots -> op index
+    const int64_t m = hi - lo;
+    size_t cap = 16;
+    while ((int64_t)cap < 2 * m) cap <<= 1;
+    tkey.assign(cap, -1);
+    tidx.assign(cap, -1);
+    for (int64_t i = lo; i < hi; ++i) {
+      const int64_t* r = fused_rows + 6 * i;
+      if (r[3] < 0 || r[3] >= 65536 || r[5] < 0 || r[5] >= 65536 || r[2] < 0 || r[4] < 0) return ABKV_ERR_ARG;
+      const int64_t k = slot_key(r[2], r[3]);
+      size_t h = slot_hash(k, cap);
+      while (tkey[h] != -1) {
+        if (tkey[h] == k) return ABKV_ERR_ARG;           // one slot read by two ops
+        h = (h + 1) & (cap - 1);
+      }
+      tkey[h] = k;
+      tidx[h] = (int32_t)(i - lo);
+    }
+    int64_t nc = 0;
+    for (int64_t j = lo; j < hi; ++j) {
+      const int64_t* r = fused_rows + 6 * j;
+      const int64_t k = slot_key(r[4], r[5]);
+      size_t h = slot_hash(k, cap);
+      while (tkey[h] != -1 && tkey[h] != k) h = (h + 1) & (cap - 1);
+      if (tkey[h] == k) {
+        const int64_t i = lo + tidx[h];
+        if (i > j) return ABKV_ERR_ARG;                  // a later op would read what this one wrote
+        nc += !chained[(size_t)i];
+        chained[(size_t)i] = 1;
+        nc += !chained[(size_t)j];
+        chained[(size_t)j] = 1;
+      }
+    }
+    runs[(size_t)g].push_back({lo, hi, nc});
+    n_ops[(size_t)g] += m;
+    n_chained[(size_t)g] += nc;
+    lo = hi;
+  }
+  int64_t at = 0;
+  for (int g = 0; g < G; ++g) {
+    int32_t* ops = out + at;
+    int32_t* offs = ops + 4 * n_ops[(size_t)g];
+    int64_t k_ord = 0, k_free = n_chained[(size_t)g], n_seg = 0;
+    offs[0] = 0;
+    for (const Run& r : runs[(size_t)g]) {
+      for (int64_t i = r.lo; i < r.hi; ++i) {
+        const int64_t* f = fused_rows + 6 * i;
+        int32_t* d = ops + 4 * (chained[(size_t)i] ? k_ord++ : k_free++);
+        d[0] = (int32_t)f[2];
+        d[1] = (int32_t)f[3];
+        d[2] = (int32_t)f[4];
+        d[3] = (int32_t)f[5];
+      }
+      if (r.n_chained) offs[++n_seg] = (int32_t)k_ord;
+    }
+    int64_t* ix = index + 5 * g;
+    ix[0] = at;
+    ix[1] = n_ops[(size_t)g];
+    ix[2] = at + 4 * n_ops[(size_t)g];
+    ix[3] = n_seg;
+    ix[4] = n_ops[(size_t)g] - n_chained[(size_t)g];
+    at += 4 * n_ops[(size_t)g] + ((n_seg + 1 + 3) & ~(int64_t)3);
+  }
+  return at;
+}
+
 int64_t abkv_planner_num_free(void* h) {
   Planner* p = static_cast<Planner*>(h);
   return p ? (int64_t)p->free_q.size() : -1;

@@ -241,6 +241,26 @@ def kv_move_segments(layer_caches, ops: torch.Tensor, seg_offsets: torch.Tensor)
     check(rc, "abkv_kv_move_segments")
 
 
+def kv_move_mixed(layer_caches, ops: torch.Tensor, seg_offsets: torch.Tensor, free_ops: torch.Tensor) -> None:
+    """abkv_kv_move_mixed, one launch: the ordered segments of :func:`kv_move_segments` (``ops`` [n, 4] with
+    ``seg_offsets`` [n_seg + 1]; n_seg may be 0) and the independent ops ``free_ops`` [m, 4] -- ops that read or write
+    no slot another op of the call writes (:func:`abridgekv_amd.worker.pack_fused_moves` builds both)."""
+    for name, t in (("ops", ops), ("free_ops", free_ops)):
+        _require(t.is_cuda and t.dtype == torch.int32 and t.dim() == 2 and t.shape[1] == 4 and t.is_contiguous(),
+                 f"{name} must be contiguous cuda int32 [n, 4]")
+    _require(seg_offsets.is_cuda and seg_offsets.dtype == torch.int32 and seg_offsets.is_contiguous()
+             and seg_offsets.numel() >= 1, "seg_offsets must be contiguous cuda int32 with at least one entry")
+    n_seg = seg_offsets.numel() - 1 if ops.shape[0] else 0
+    n_free = free_ops.shape[0]
+    if n_seg == 0 and n_free == 0:
+        return
+    arr, num_pages = _layer_ptrs(layer_caches)
+    rc = lib().abkv_kv_move_mixed(arr, len(layer_caches), num_pages, PAGE, PAGE_BYTES, HALF_BYTES, SLOT_BYTES,
+                                  _ptr(ops) if n_seg else None, _ptr(seg_offsets) if n_seg else None, n_seg,
+                                  _ptr(free_ops) if n_free else None, n_free, C.c_void_p(_stream()))
+    check(rc, "abkv_kv_move_mixed")
+
+
 def kv_copy_staged(layer_caches, ops: torch.Tensor, stage: torch.Tensor | None = None) -> None:
     """Gather-then-scatter for an arbitrary op list, staged through a workspace."""
     _require(ops.is_cuda and ops.dtype == torch.int32 and ops.dim() == 2 and ops.shape[1] == 4

@@ -8,7 +8,7 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py) decides every req
 ``KVPlanner.mask_token_span`` as its ``mask_span`` callback: the compaction of a block whose code run ended is exactly
 the processor's ``_finish_block`` (processor.py:419-557), and the planner turns it into fused row moves.
 
-Device side, per step on one HIP stream: the previous step's compaction moves (``abkv_kv_move_segments``); the slot of
+Device side, per step on one HIP stream: the previous step's compaction moves (``abkv_kv_move_mixed``); the slot of
 every new row per KV-cache group (``abkv_slot_mapping``: logical position minus the group's compacted count through
 the group's page table, gpu_model_runner.py:1579-1661 + block_table.py:186-197); then for every layer the fused RoPE +
 KV append (``abkv_rope_kv_append``, bitrev RoPE positions of the abridged layout computed on the device,
@@ -30,7 +30,7 @@ import torch
 from . import ops
 from ._lib import check, lib
 from .backend import code_step_key_limits
-from .worker import launch_moves, split_fused_moves
+from .worker import device_move_lists, launch_moves, pack_fused_moves
 from .workloads import (BLOCK_C, CODES_K_MAX, MAX_MODEL_LEN, QWEN3_4B_LAYER_QUOTAS, SAMPLED_TOKEN,
                         build_decode_state)
 
@@ -235,7 +235,7 @@ class ServingStress:
     def tables(self):
         return self.plan.tables
 
-    def _stage(self, m, moves=()):
+    def _stage(self, m, moves=None):
         """Pack the step metadata (and the previous step's compaction moves) into one pinned buffer and start its
         asynchronous copy to the device."""
         G, W = self.G, self.W
@@ -258,9 +258,9 @@ class ServingStress:
             "tile_req": m["tiles"][:, 0].astype(np.int32).copy(),
             "tile_q0": m["tiles"][:, 1].astype(np.int32).copy(),
         }
-        for j, (gid, ops_h, offs) in enumerate(moves):
-            parts[f"mv_ops{j}"] = ops_h.reshape(-1)
-            parts[f"mv_offs{j}"] = offs
+        mv_buf, mv_parts = moves if moves else (None, [])
+        if mv_parts:
+            parts["moves"] = mv_buf                          # per-group sections, each 16-byte aligned
         if self.tag:                                       # (request, logical position) of every new row
             tp = m["tok_pos"]
             parts["tags"] = np.stack([m["tok_req"], tp // 256, tp % 256], axis=1).astype(np.int32).reshape(-1)
@@ -291,7 +291,7 @@ class ServingStress:
         v["upd_comp"] = v["upd_comp"].view(G, rows.size)
         if self.tag:
             v["tags"] = v["tags"].view(n_tok, 3)
-        mv = [(gid, v[f"mv_ops{j}"].view(-1, 4), v[f"mv_offs{j}"]) for j, (gid, _, _) in enumerate(moves)]
+        mv = device_move_lists(v["moves"], mv_parts) if mv_parts else []
         # key splits of the code step per group (its few query tiles cannot fill the GPU on their own)
         n_tiles = int(m["tiles"].shape[0])
         code_split = [ops.paged_split_plan(n_tiles, int(m["limits"][g].max())) if nc else (1, 0) for g in range(G)]
@@ -402,7 +402,7 @@ class ServingStress:
         which run first in the next launch: after this step's attention, before the next step's appends)."""
         m = self._meta
         self._launch_step(m)
-        moves = split_fused_moves(self.plan.advance(m), self.st.num_pages, check=False)
+        moves = pack_fused_moves(self.plan.advance(m), self.st.num_pages, check=False, num_groups=self.G)
         self._meta = self._stage(self.plan.prepare(), moves)
         return m
 

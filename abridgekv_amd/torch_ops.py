@@ -106,6 +106,19 @@ def _kv_move_segments_fake(layer_caches, ops, seg_offsets):
     _need(0 < len(layer_caches) <= 16, "between 1 and 16 layer caches per call")
 
 
+@torch.library.custom_op(f"{_NS}::kv_move_mixed", mutates_args=("layer_caches",))
+def kv_move_mixed(layer_caches: list[Tensor], ops: Tensor, seg_offsets: Tensor, free_ops: Tensor) -> None:
+    """abkv_kv_move_mixed: ordered segments and independent ops of a step's packed fused moves in one launch."""
+    _ops.kv_move_mixed(layer_caches, ops, seg_offsets, free_ops)
+
+
+@kv_move_mixed.register_fake
+def _kv_move_mixed_fake(layer_caches, ops, seg_offsets, free_ops):
+    _need(ops.dim() == 2 and ops.shape[1] == 4 and free_ops.dim() == 2 and free_ops.shape[1] == 4,
+          "ops and free_ops must be [n, 4]")
+    _need(0 < len(layer_caches) <= 16, "between 1 and 16 layer caches per call")
+
+
 # -- paged multi-query attention (prompt chunks, code steps) --------------------------------------------------------
 @torch.library.custom_op(f"{_NS}::paged_prefill_attn", mutates_args=("out", "lse", "workspace"))
 def paged_prefill_attn(q: Tensor, kv_cache: Tensor, block_table: Tensor, q_start: Tensor, kv_start: Tensor,
@@ -181,5 +194,5 @@ def _prefill_masked_attn_bwd_fake(q, k, v, out, lse, dout, block_c, codes_k, num
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
-OPS = ("decode_attn", "kv_append", "rope_kv_append", "slot_mapping", "kv_move_segments", "paged_prefill_attn",
-       "prefill_masked_attn", "prefill_masked_attn_bwd")
+OPS = ("decode_attn", "kv_append", "rope_kv_append", "slot_mapping", "kv_move_segments", "kv_move_mixed",
+       "paged_prefill_attn", "prefill_masked_attn", "prefill_masked_attn_bwd")

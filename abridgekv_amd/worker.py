@@ -7,10 +7,13 @@ executing on the HIP kernels of libabridgekv_amd.
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import torch
 
 from . import ops
+from ._lib import lib
 from .ops import PAGE
 
 
@@ -66,50 +69,60 @@ def execute_kv_copy_operations(kv_copy_operations: dict, layer_caches_by_group, 
             execute_kv_copy_group(segments, caches, check=check)
 
 
-def split_fused_moves(fused_moves: np.ndarray, num_pages: int, check: bool = True):
-    """Host side of :func:`execute_fused_moves`: split a planner step's fused move rows (request, group, src_block,
-    src_off, dst_block, dst_off) by group into an op array and segment offsets (one segment per request).
-    Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)]."""
+def pack_fused_moves(fused_moves: np.ndarray, num_pages: int, check: bool = True, num_groups: int | None = None):
+    """Host side of :func:`execute_fused_moves` (abkv_moves_pack): a planner step's fused move rows (request, group,
+    src_block, src_off, dst_block, dst_off) as per-group device-ready lists -- the runs in which some op's
+    destination is another op's source as ordered segments (op order kept), every other op as an independent op.
+    Returns (buffer int32, [(group, ops_at, n_ops, offs_at, n_segments, n_free)]) for the groups with ops; ops and
+    offsets are slices of the one buffer."""
     if fused_moves.size == 0:
-        return []
-    fm = np.asarray(fused_moves, dtype=np.int64)
-    out = []
-    for gid in np.unique(fm[:, 1]).tolist():
-        rows = fm[fm[:, 1] == gid]
-        cut = np.flatnonzero(np.diff(rows[:, 0])) + 1
-        offs = np.concatenate([[0], cut, [rows.shape[0]]]).astype(np.int32)
-        ops_h = np.ascontiguousarray(rows[:, 2:6], dtype=np.int32)
-        if check:
-            _validate_ops(ops_h, num_pages)
-        out.append((gid, ops_h, offs))
-    return out
+        return np.zeros(0, np.int32), []
+    fm = np.ascontiguousarray(fused_moves, dtype=np.int64)
+    if check:
+        _validate_ops(fm[:, 2:6], num_pages)
+    G = int(fm[:, 1].max()) + 1 if num_groups is None else num_groups
+    n = fm.shape[0]
+    out = np.empty(5 * n + 4 * G, np.int32)
+    index = np.zeros((G, 5), np.int64)
+    got = lib().abkv_moves_pack(fm.ctypes.data_as(C.POINTER(C.c_int64)), n, G,
+                                out.ctypes.data_as(C.POINTER(C.c_int32)), out.size,
+                                index.ctypes.data_as(C.POINTER(C.c_int64)))
+    if got < 0:
+        raise ValueError(f"abkv_moves_pack rejected the fused moves ({got}): rows of one (request, group) must be "
+                         "contiguous, and no op may read a slot an earlier op of its run writes")
+    return out[:got], [(g, *map(int, index[g])) for g in range(G) if index[g, 1] > 0]
 
 
 def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: bool = True):
-    """:func:`split_fused_moves` uploaded in a single host-to-device copy.
-    Returns [(group, ops [n, 4] int32, seg_offsets [n_seg + 1] int32)] on the device."""
-    parts = split_fused_moves(fused_moves, num_pages, check)
+    """:func:`pack_fused_moves` uploaded in a single host-to-device copy.
+    Returns [(group, ordered ops [n, 4] int32, seg_offsets [n_seg + 1] int32, independent ops [m, 4] int32)] on the
+    device."""
+    buf, parts = pack_fused_moves(fused_moves, num_pages, check)
     if not parts:
         return []
-    flat, meta, at = [], [], 0
-    for gid, ops_h, offs in parts:
-        flat += [ops_h.reshape(-1), offs]
-        meta.append((gid, at, ops_h.size, at + ops_h.size, offs.size))
-        at += ops_h.size + offs.size
-    dev = torch.from_numpy(np.concatenate(flat)).to(device)
-    return [(gid, dev[o: o + n].view(-1, 4), dev[so: so + ns]) for gid, o, n, so, ns in meta]
+    return device_move_lists(torch.from_numpy(buf).to(device), parts)
+
+
+def device_move_lists(dev_buf: torch.Tensor, parts):
+    """Views of an uploaded :func:`pack_fused_moves` buffer: [(group, ordered ops, seg_offsets, independent ops)]."""
+    out = []
+    for gid, o, n, so, ns, nf in parts:
+        n_ord = n - nf
+        out.append((gid, dev_buf[o: o + 4 * n_ord].view(-1, 4), dev_buf[so: so + ns + 1],
+                    dev_buf[o + 4 * n_ord: o + 4 * n].view(-1, 4)))
+    return out
 
 
 def launch_moves(prepared, layer_caches_by_group, events=None) -> None:
     """Device side of :func:`execute_fused_moves`: one launch per group (and per 16 layer tensors). ``events``, if
     given, is a list that receives (start, end) CUDA events recorded around every launch."""
-    for gid, ops_d, offs_d in prepared:
+    for gid, ops_d, offs_d, free_d in prepared:
         caches = layer_caches_by_group[gid]
         for lo in range(0, len(caches), 16):
             if events is not None:
                 s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 s.record()
-            ops.kv_move_segments(caches[lo: lo + 16], ops_d, offs_d)
+            ops.kv_move_mixed(caches[lo: lo + 16], ops_d, offs_d, free_d)
             if events is not None:
                 e.record()
                 events.append((s, e))
@@ -117,8 +130,8 @@ def launch_moves(prepared, layer_caches_by_group, events=None) -> None:
 
 def execute_fused_moves(fused_moves: np.ndarray, layer_caches_by_group, check: bool = True) -> None:
     """Apply a planner step's fused move rows (request, group, src_block, src_off, dst_block, dst_off): one launch
-    per group, one segment per request. Rows of one (request, group) are monotone (increasing source, dst < src), so
-    the in-register chunked copy is exact."""
+    per group. Rows of one (request, group) are monotone (increasing source, dst < src): a run whose ops depend on
+    each other's order is walked in order by the in-register chunked copy, every other op moves independently."""
     if fused_moves.size == 0:
         return
     num_pages = layer_caches_by_group[0][0].shape[0]

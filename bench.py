@@ -347,6 +347,8 @@ def bench_compaction(args, torch):
     torch.cuda.synchronize()
     copy_gbps = 2 * n_copy / (s.elapsed_time(e) / 1e3 / reps) / 1e9
     del src_buf, dst_buf
+    probe = same_pattern_probe(torch, prepared, by_group, st.num_pages, args)
+    probe["mover_frac_of_probe"] = gbps / probe["gbps"]
     cpu = None if args.no_cpu_baseline else compaction_cpu_baseline(torch, B, args.seed, layers_per_group)
     return {
         **({"cpu_baseline": cpu} if cpu else {}),
@@ -367,9 +369,71 @@ def bench_compaction(args, torch):
                          "what": "torch device copies of one move launch's bytes, contiguous, cycling through 16 "
                                  "slices of a buffer larger than the last-level cache",
                          "mover_frac_of_copy": gbps / copy_gbps},
+        "same_pattern_probe": probe,
         "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
         "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
     }
+
+
+def same_pattern_probe(torch, prepared, by_group, num_pages, args):
+    """Ceiling of the mover's access pattern: abkv_probe_row_copy (libabridgekv_probes.so) copies the same rows of the
+    same layers -- every (src page, slot) -> (dst page, slot) of each group launch, 4 KiB each -- into a second set of
+    caches, all ops in parallel (no segment order to keep). Swept over 4, 8 and 16 rows per workgroup; the best is
+    the ceiling. Returns its GB/s (read + write bytes / time of the same launches) and the sweep."""
+    import ctypes as C
+    from pathlib import Path
+
+    from abridgekv_amd import ops
+
+    path = Path(__file__).resolve().parent / "abridgekv_amd" / "libabridgekv_probes.so"
+    lib = C.CDLL(str(path))
+    fn = lib.abkv_probe_row_copy
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_long, C.c_long, C.c_int, C.c_int,
+                   C.c_int, C.c_int, C.c_void_p]
+    n_tensors = max(len(c) for c in by_group)
+    dst = [torch.empty_like(by_group[0][0]) for _ in range(n_tensors)]
+    launches, total_bytes = [], 0
+    for gid, ord_d, _, free_d in prepared:
+        ops_d = torch.cat([ord_d, free_d])
+        caches = by_group[gid]
+        for lo in range(0, len(caches), 16):
+            src_l = caches[lo: lo + 16]
+            srcs = (C.c_void_p * len(src_l))(*[c.data_ptr() for c in src_l])
+            dsts = (C.c_void_p * len(src_l))(*[d.data_ptr() for d in dst[:len(src_l)]])
+            launches.append((srcs, dsts, len(src_l), ops_d))
+            total_bytes += 2 * ops_d.shape[0] * len(src_l) * 2 * ops.SLOT_BYTES
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(rows, events=None):
+        for srcs, dsts, n_l, ops_d in launches:
+            if events is not None:
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+            rc = fn(srcs, dsts, n_l, C.c_void_p(ops_d.data_ptr()), int(ops_d.shape[0]), ops.PAGE_BYTES,
+                    ops.HALF_BYTES, ops.SLOT_BYTES, num_pages, ops.PAGE, rows, stream)
+            if rc != 0:
+                raise RuntimeError(f"abkv_probe_row_copy failed: {rc}")
+            if events is not None:
+                e.record()
+                events.append((s, e))
+
+    sweep = {}
+    for rows in (4, 8, 16):                                    # events around every launch, as for the mover
+        for _ in range(max(args.warmup, 1)):
+            run(rows)
+        torch.cuda.synchronize()
+        events = []
+        for _ in range(args.steps):
+            run(rows, events)
+        torch.cuda.synchronize()
+        t = sum(s_.elapsed_time(e_) for s_, e_ in events) / 1e3 / args.steps
+        sweep[rows] = total_bytes / t / 1e9
+    del dst
+    best = max(sweep, key=sweep.get)
+    return {"gbps": sweep[best], "rows_per_workgroup": best, "sweep_gbps": sweep, "bytes_per_step": total_bytes,
+            "what": "the same (layer, src slot, dst slot) rows copied into a second cache set, every op in parallel "
+                    "(abkv_probe_row_copy)"}
 
 
 def compaction_cpu_baseline(torch, B, seed, layers_per_group):

@@ -80,6 +80,13 @@ int abkv_decode_attn_noalloc(const void* q, long q_stride_seq, long q_stride_hea
  * ------------------------------------------------------------------------------------------------------------- */
 int abkv_kv_move_segments(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
                           long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments, abkv_stream_t stream);
+/* abkv_kv_move_mixed: one launch over the ordered segments of abkv_kv_move_segments (n_segments >= 0; ops /
+ * seg_offsets may be NULL when 0) and n_free independent ops free_ops [n_free, 4]: ops that read or write no slot
+ * another op of the launch writes, so they run in any order (the layout abkv_moves_pack builds from a planner step's
+ * fused moves; the same executor, gpu_model_runner.py:1194-1224). */
+int abkv_kv_move_mixed(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
+                       long half_bytes, int slot_bytes, const int32_t* ops, const int32_t* seg_offsets, int n_segments,
+                       const int32_t* free_ops, int n_free, abkv_stream_t stream);
 size_t abkv_kv_stage_bytes(int n_layers, int n_ops, int slot_bytes);
 int abkv_kv_copy_staged(void* const* layer_caches, int n_layers, int num_pages, int block_size, long page_bytes,
                         long half_bytes, int slot_bytes, const int32_t* ops, int n_ops, void* stage, size_t stage_bytes, abkv_stream_t stream);
@@ -286,6 +293,17 @@ int abkv_planner_pending_sizes(void* planner, int64_t* n_op_rows, int64_t* n_tru
 int abkv_planner_take_step_outputs(void* planner, int64_t* op_rows, int64_t op_cap, int64_t* n_ops,
                                    int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc, int64_t* fused_rows,
                                    int64_t fused_cap, int64_t* n_fused);
+/* Device-ready move lists from fused_rows [n, 6] (host; the host side of the executor above,
+ * gpu_model_runner.py:1194-1224, for the fused form): per group g < num_groups, back to back in `out` (capacity
+ * >= 5 n + 4 num_groups int32), the ops [n_g, 4] -- first the ordered segments, one per (request, group) run holding
+ * the run's ops that lie on a dependency (an op whose destination is another op's source, and that op), in emission
+ * order; then every other op, independent of all others -- and the segment offsets [n_segments + 1], each group's
+ * section 16-byte aligned. index [num_groups, 5] = (ops_at, n_ops, offs_at, n_segments, n_free) in int32 elements of
+ * `out`; feeds abkv_kv_move_mixed. Returns the elements written, ABKV_ERR_CAPACITY or ABKV_ERR_ARG (group out of
+ * range, a run split in two, an offset outside [0, 65536), a slot read twice, or an op that reads a slot an earlier
+ * op of its run writes). */
+int64_t abkv_moves_pack(const int64_t* fused_rows, int64_t n, int num_groups, int32_t* out, int64_t out_cap,
+                        int64_t* index);
 int64_t abkv_planner_num_free(void* planner);
 int64_t abkv_planner_free_queue(void* planner, int32_t* out, int64_t cap);
 int64_t abkv_planner_block_ids(void* planner, int64_t rid, int group, int32_t* out, int64_t cap);

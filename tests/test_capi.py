@@ -34,6 +34,16 @@ def test_library_exports_every_declared_symbol():
     assert exported <= declared_functions(), f"undeclared exports: {sorted(exported - declared_functions())}"
 
 
+def test_probe_library_loads_and_exports_only_the_probe():
+    """The benchmark's measurement probes live in their own library, outside the C-ABI boundary."""
+    import ctypes
+
+    path = _lib.LIB_PATH.parent / "libabridgekv_probes.so"
+    ctypes.CDLL(str(path))
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True).stdout
+    assert set(re.findall(r" T (abkv_[a-z0-9_]+)", out)) == {"abkv_probe_row_copy"}
+
+
 def test_binding_table_matches_header():
     assert set(_lib.SIGNATURES) == declared_functions()
 

@@ -45,6 +45,16 @@ def _inputs(seed=0):
     mv = np.stack([bt1[src // 16], src % 16, bt1[dst // 16], dst % 16], 1).astype(np.int32)
     d["mv"] = torch.from_numpy(mv).to(dev)
     d["offs"] = torch.tensor([0, 32], dtype=torch.int32, device=dev)
+    # a mixed move list: request 3 shifts rows 100..131 down by 16 (sources and destinations overlap: one ordered
+    # segment), request 4 shifts rows 200..231 down by 64 (no overlap: 32 independent ops)
+    def run(r, lo, shift):
+        s_ = np.arange(lo, lo + 32)
+        t_ = s_ - shift
+        b = pages[r].cpu().numpy()
+        return np.stack([b[s_ // 16], s_ % 16, b[t_ // 16], t_ % 16], 1)
+    d["mx"] = torch.from_numpy(run(3, 100, 16).astype(np.int32)).to(dev)
+    d["mx_free"] = torch.from_numpy(run(4, 200, 64).astype(np.int32)).to(dev)
+    d["mx_offs"] = torch.tensor([0, 32], dtype=torch.int32, device=dev)
     # masked prefill (C=64, K=16, N=3), 2 sequences, raw prompt 40 / 0
     S0 = 3 * 80
     d["pq"] = torch.randn((2, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
@@ -70,6 +80,7 @@ def _via_torch_ops(d, o):
     A.rope_kv_append(d["q"], d["key"], d["val"], d["pos"], d["cos_sin"], o["slots"], d["cache"], 0, 0,
                      d["bt"].shape[1] * 16 - 1)
     A.kv_move_segments([d["cache"]], d["mv"], d["offs"])
+    A.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
     A.decode_attn(d["q"], d["cache"], d["bt"], d["lens"], scale, d["bt"].shape[1], 8, o["out"], o["lse"], d["ws"])
     m = d["meta"]
     A.paged_prefill_attn(d["cq"], d["cache"], d["bt"], m[0:2], m[2:3], m[3:4], d["tiles"][0], d["tiles"][1], m[4:5],
@@ -84,6 +95,7 @@ def _via_ctypes(d, o):
     ops.rope_kv_append(d["q"], d["key"], d["val"], d["pos"], d["cos_sin"], slot_mapping=o["slots"],
                        kv_cache=d["cache"], max_position=d["bt"].shape[1] * 16 - 1)
     ops.kv_move_segments([d["cache"]], d["mv"], d["offs"])
+    ops.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
     ops.decode_attention(d["q"], d["cache"], d["bt"], d["lens"], scale, out=o["out"], lse=o["lse"], split_pages=8,
                          workspace=d["ws"])
     m = d["meta"].cpu().numpy()

@@ -13,6 +13,7 @@ MUTATES = {
     "rope_kv_append": {"q", "key", "kv_cache"},
     "slot_mapping": {"out"},
     "kv_move_segments": {"layer_caches"},
+    "kv_move_mixed": {"layer_caches"},
     "paged_prefill_attn": {"out", "lse", "workspace"},
     "prefill_masked_attn": {"out", "lse"},
     "prefill_masked_attn_bwd": set(),
@@ -38,6 +39,7 @@ def test_fake_tracing_keeps_each_op_as_one_node():
         torch.ops.abridgekv.paged_prefill_attn(q, cache, bt, meta[:3], meta[3:5], meta[5:7], tr, tq0, meta[7:9],
                                                0.088, 4, 2, 1, out, lse, ws)
         torch.ops.abridgekv.kv_move_segments([cache], mv_ops, offs)
+        torch.ops.abridgekv.kv_move_mixed([cache], mv_ops, offs, mv_ops)
         torch.ops.abridgekv.prefill_masked_attn(pq, pk, pv, 8, 4, 2, None, None, 0.088, pout, plse)
         dq, dk, dv = torch.ops.abridgekv.prefill_masked_attn_bwd(pq, pk, pv, pout, plse, pout, 8, 4, 2, None, None,
                                                                 0.088)
