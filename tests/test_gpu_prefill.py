@@ -100,10 +100,17 @@ def config4_sample_rows(C, K, N, rng, extra=24):
     return np.array(sorted(p for p in picks if p < N * per))
 
 
-def test_config4_full_size_sampled_rows():
+# per-KV-head code quotas (each KV head's 4 query heads share one), aligned and unaligned, for the full-size cases
+CONFIG4_QUOTAS = np.repeat([128, 64, 100, 32, 1, 47, 8, 16], 4).tolist()
+
+
+@pytest.mark.parametrize("prompts,quota", [([512] * 4, None), ([512, 300, 0, 640], CONFIG4_QUOTAS)],
+                         ids=["benched", "prompts_and_head_quotas"])
+def test_config4_full_size_sampled_rows(prompts, quota):
     """The benched launch itself: B=4, N=16 blocks of [512 content | 128 codes] (S0=10240, 160 query tiles per
-    sequence), 512-token raw prompt. Every output and LSE is finite; sampled rows of every sequence match the float64
-    oracle evaluated on those rows over all 10240 keys."""
+    sequence), 512-token raw prompts; and the same size with a different raw prompt per sequence and per-head code
+    quotas. Every output and LSE is finite; sampled rows of every sequence match the float64 oracle evaluated on those
+    rows over all 10240 keys."""
     from abridgekv_amd import ops
     B, C, K, N = 4, 512, 128, 16
     S0 = N * (C + K)
@@ -112,16 +119,17 @@ def test_config4_full_size_sampled_rows():
     q = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
-    pl = torch.full((B,), 512, dtype=torch.int32, device=dev)
+    pl = torch.tensor(prompts, dtype=torch.int32, device=dev)
+    hq = None if quota is None else torch.tensor(quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
-    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, head_quota=hq, lse=lse)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
     rng = np.random.default_rng(4)
     worst = 0.0
     for b in range(B):
         rows = config4_sample_rows(C, K, N, rng)
-        mask = op.arith_mask_block(C, K, N, rows, np.arange(S0), [512])[0]
+        mask = op.arith_mask_block(C, K, N, rows, np.arange(S0), [prompts[b]], quota)[0]
         qb, kb, vb = (t[b].float().cpu().numpy() for t in (q, k, v))
         ref_o, ref_l = op.masked_attention_rows_fp64(qb, kb, vb, mask, rows, 128 ** -0.5)
         got_o = out[b].float().cpu().numpy()[rows]

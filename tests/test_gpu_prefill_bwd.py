@@ -94,12 +94,15 @@ def test_config4_geometry_full_oracle():
     _check(C=512, K=128, N=4, B=2, prompt_len=[512, 300], seed=5)
 
 
-def test_config4_full_size_sampled():
-    """The benched backward launch: B=4, N=16 blocks of [512 | 128] (S0=10240), 512-token raw prompt. dq, dk, dv are
-    finite everywhere; dq of sampled query rows (every sequence) and dk / dv of sampled keys of the last block (first
-    and last sequence) match the float64 oracle (tolerance 2e-2 x the largest |reference| + 2e-3 per tensor)."""
+@pytest.mark.parametrize("case", ["benched", "prompts_and_head_quotas"])
+def test_config4_full_size_sampled(case):
+    """The benched backward launch: B=4, N=16 blocks of [512 | 128] (S0=10240), 512-token raw prompts; and the same
+    size with a different raw prompt per sequence and per-head code quotas. dq, dk, dv are finite everywhere; dq of
+    sampled query rows (every sequence) and dk / dv of sampled keys of the last block (first and last sequence) match
+    the float64 oracle (tolerance 2e-2 x the largest |reference| + 2e-3 per tensor)."""
     from abridgekv_amd import ops
-    from tests.test_gpu_prefill import config4_sample_rows
+    from tests.test_gpu_prefill import CONFIG4_QUOTAS, config4_sample_rows
+    prompts, quota = ([512] * 4, None) if case == "benched" else ([512, 300, 0, 640], CONFIG4_QUOTAS)
     B, C, K, N = 4, 512, 128, 16
     S0 = N * (C + K)
     dev = torch.device("cuda")
@@ -108,10 +111,12 @@ def test_config4_full_size_sampled():
     k = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn((B, S0, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     dout = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
-    pl = torch.full((B,), 512, dtype=torch.int32, device=dev)
+    pl = torch.tensor(prompts, dtype=torch.int32, device=dev)
+    hq = None if quota is None else torch.tensor(quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
-    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
-    dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, head_quota=hq, lse=lse)
+    dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl,
+                                                       head_quota=hq)
     torch.cuda.synchronize()
     for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
         assert torch.isfinite(t).all(), name
@@ -130,12 +135,12 @@ def test_config4_full_size_sampled():
     for b in range(B):
         qb, kb, vb, gb = (t[b].float().cpu().numpy() for t in (q, k, v, dout))
         rows = config4_sample_rows(C, K, N, rng, extra=8)
-        mrows = op.arith_mask_block(C, K, N, rows, np.arange(S0), [512])[0]
+        mrows = op.arith_mask_block(C, K, N, rows, np.arange(S0), [prompts[b]], quota)[0]
         close(f"dq b{b}", dq[b].float().cpu().numpy()[rows],
               op.masked_attention_query_grads_fp64(qb, kb, vb, gb, mrows, rows, scale))
         if b in (0, B - 1):
-            def mask_fn(r, c):
-                return op.arith_mask_block(C, K, N, r, c, [512])[0]
+            def mask_fn(r, c, b=b):
+                return op.arith_mask_block(C, K, N, r, c, [prompts[b]], quota)[0]
             ref_k, ref_v = op.masked_attention_key_grads_fp64(qb, kb, vb, gb, mask_fn, keys, scale)
             close(f"dk b{b}", dk[b].float().cpu().numpy()[keys], ref_k)
             close(f"dv b{b}", dv[b].float().cpu().numpy()[keys], ref_v)
