@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=None,
                     help="pages per decode split (default: ops.auto_split_pages per launch: 48, 40 or 32)")
     ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "config1", "prefill", "prefill_bwd",
-                                           "compaction", "packed", "copy"],
+                                           "compaction", "packed", "copy", "lds"],
                     default="serving")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
@@ -740,6 +740,42 @@ def bench_copy(args, torch):
             "bytes_read_per_launch": n, "bytes_written_per_launch": n, "ms_per_step": t * 1e3, "steps": args.steps}
 
 
+def bench_lds(args, torch):
+    """LDS read throughput per CU (abkv_probe_lds_read in libabridgekv_probes.so): ds_read_b128 and the transposed
+    ds_read_b64_tr_b16 with the masked-prefill kernels' operand addressing, at 1 and 2 workgroups of 4 waves per CU
+    (the prefill kernels run 8 waves per CU). B/clk from the probe's shader-clock cycle counts, GB/s from events."""
+    import ctypes as C
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "abridgekv_amd" / "libabridgekv_probes.so"
+    fn = C.CDLL(str(path)).abkv_probe_lds_read
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 20000
+    sink = torch.empty(2 * cus * 256, dtype=torch.int32, device="cuda")
+    cycles = torch.empty(2 * cus, dtype=torch.int64, device="cuda")
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for wpc in (1, 2):
+        for mode, name, bpi in ((0, "ds_read_b128", 1024), (1, "ds_read_b64_tr_b16", 512)):
+            n_wg = wpc * cus
+            for _ in range(max(args.warmup, 1)):
+                assert fn(mode, n_wg, iters, 37, C.c_void_p(sink.data_ptr()), C.c_void_p(cycles.data_ptr()), stream) == 0
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            assert fn(mode, n_wg, iters, 37, C.c_void_p(sink.data_ptr()), C.c_void_p(cycles.data_ptr()), stream) == 0
+            e.record()
+            torch.cuda.synchronize()
+            per_cu = wpc * 4 * iters * 8 * bpi
+            cyc = float(cycles[:n_wg].double().mean())
+            res[f"{name} {wpc} WG/CU"] = {"bytes_per_clk_per_cu": per_cu / cyc,
+                                          "gbps_per_cu": per_cu / (s.elapsed_time(e) / 1e3) / 1e9,
+                                          "clock_ghz": cyc / (s.elapsed_time(e) / 1e3) / 1e9}
+    return {"metric": "LDS read throughput per CU (probe)", "unit": "B/clk/CU", "cus": cus, "iters": iters,
+            "results": res}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -748,10 +784,10 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "copy"):
+    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "copy", "lds"):
         res = {"serving": bench_serving, "config1": bench_config1, "prefill": bench_prefill,
                "prefill_bwd": bench_prefill_bwd, "compaction": bench_compaction, "packed": bench_packed,
-               "copy": bench_copy}[args.workload](args, torch)
+               "copy": bench_copy, "lds": bench_lds}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
