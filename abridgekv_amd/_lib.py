@@ -67,6 +67,7 @@ SIGNATURES = {
                                                  C.c_int, _vp, C.c_size_t, _vp]),
     "abkv_planner_create": (_vp, [C.c_int, C.c_int, C.c_int, _i32p, C.c_int64]),
     "abkv_planner_destroy": (None, [_vp]),
+    "abkv_planner_set_op_rows": (C.c_int, [_vp, C.c_int]),
     "abkv_planner_last_error": (C.c_char_p, [_vp]),
     "abkv_planner_add_request": (C.c_int, [_vp, C.c_int64]),
     "abkv_planner_free_request": (C.c_int, [_vp, C.c_int64]),
@@ -79,6 +80,7 @@ SIGNATURES = {
     "abkv_planner_take_step_outputs": (C.c_int, [_vp, _i64p, C.c_int64, _i64p, _i64p, C.c_int64, _i64p, _i64p,
                                                  C.c_int64, _i64p]),
     "abkv_moves_pack": (C.c_int64, [_i64p, C.c_int64, C.c_int, _i32p, C.c_int64, _i64p]),
+    "abkv_planner_take_moves_packed": (C.c_int64, [_vp, _i64p, C.c_int64, _i64p, _i32p, C.c_int64, _i64p]),
     "abkv_planner_num_free": (C.c_int64, [_vp]),
     "abkv_planner_free_queue": (C.c_int64, [_vp, _i32p, C.c_int64]),
     "abkv_planner_block_ids": (C.c_int64, [_vp, C.c_int64, C.c_int, _i32p, C.c_int64]),

@@ -118,6 +118,17 @@ struct Planner {
   std::vector<int64_t> pending_order;     // rids with pending ops, first-insertion order
   std::vector<int64_t> trunc_order;       // rids with a truncation record, first-insertion order
   std::string last_error;
+  bool op_rows = true;                    // build the reference-format op batches (off: fused moves only)
+  // scratch of abkv_planner_take_moves_packed, kept between steps
+  std::vector<int64_t> mv_origin;
+  std::vector<uint8_t> mv_chained;
+  int bs_shift = -1;                      // log2(block_size) when it is a power of two
+
+  // slot position -> (page index, offset) without a division when the page size is a power of two
+  int64_t page_of(int64_t pos) const { return bs_shift >= 0 ? pos >> bs_shift : pos / block_size; }
+  int32_t off_of(int64_t pos) const {
+    return (int32_t)(bs_shift >= 0 ? pos & ((int64_t)block_size - 1) : pos % block_size);
+  }
 
   int64_t cdiv(int64_t a, int64_t b) const { return (a + b - 1) / b; }
 
@@ -162,6 +173,8 @@ void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const 
   p->num_blocks = num_blocks;
   p->num_groups = num_groups;
   p->block_size = block_size;
+  if ((block_size & (block_size - 1)) == 0)
+    while ((1 << (p->bs_shift + 1)) <= block_size) ++p->bs_shift;
   p->max_model_len = max_model_len > 0 ? max_model_len : ((int64_t)1 << 40);
   p->ref_cnt.assign(num_blocks, 0);
   p->null_block = 0;  // the queue starts in id order and its head (page 0) becomes the null block
@@ -183,6 +196,16 @@ void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const 
 }
 
 void abkv_planner_destroy(void* h) { delete static_cast<Planner*>(h); }
+
+// Build (1, the default) or skip (0) the reference-format op batches. With 0 the planner's bookkeeping (spans, page
+// lists, truncations, the free queue) is unchanged and the fused moves are still emitted; take_step_outputs then
+// returns no op rows. For callers that execute the fused moves only.
+int abkv_planner_set_op_rows(void* h, int enabled) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  p->op_rows = enabled != 0;
+  return ABKV_OK;
+}
 
 const char* abkv_planner_last_error(void* h) { return h ? static_cast<Planner*>(h)->last_error.c_str() : ""; }
 
@@ -335,10 +358,12 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
       st.removals.push_back({pl.ps, pl.pe, pl.active});
       const int64_t removed = pl.pe - pl.ps;
       std::vector<abkv::Op> ops;
-      ops.reserve((size_t)(pl.active - pl.pe));
-      for (int64_t src = pl.pe; src < pl.active; ++src) {
-        const int64_t dst = src - removed;
-        ops.push_back({blocks[src / bs], (int32_t)(src % bs), blocks[dst / bs], (int32_t)(dst % bs)});
+      if (p->op_rows) {
+        ops.reserve((size_t)(pl.active - pl.pe));
+        for (int64_t src = pl.pe; src < pl.active; ++src) {
+          const int64_t dst = src - removed;
+          ops.push_back({blocks[p->page_of(src)], p->off_of(src), blocks[p->page_of(dst)], p->off_of(dst)});
+        }
       }
       // _truncate_compacted_blocks
       const int64_t needed = (pl.active - removed + bs - 1) / bs;
@@ -455,7 +480,6 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   if (n_trunc) *n_trunc = trunc_rows ? t : need_trunc;
   // Fused moves in request first-insertion order of the truncation records (every compacting request has one).
   int64_t f = 0;
-  const int bs = p->block_size;
   for (int64_t rid : p->trunc_order) {
     Request* r = find_req(p, rid);
     for (int g = 0; g < G; ++g) {
@@ -477,10 +501,10 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
           int64_t* row = fused_rows + 6 * f;
           row[0] = rid;
           row[1] = g;
-          row[2] = st.blocks_before[src / bs];
-          row[3] = src % bs;
-          row[4] = st.blocks_before[dst / bs];
-          row[5] = dst % bs;
+          row[2] = st.blocks_before[p->page_of(src)];
+          row[3] = p->off_of(src);
+          row[4] = st.blocks_before[p->page_of(dst)];
+          row[5] = p->off_of(dst);
         }
         ++f;
       }
@@ -495,6 +519,155 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   p->pending_order.clear();
   p->trunc_order.clear();
   return ABKV_OK;
+}
+
+// The step's outputs for a caller that executes fused moves: the truncation rows of abkv_planner_take_step_outputs
+// and, instead of fused rows, the device move lists abkv_moves_pack would build from them, written directly (the
+// dependency of a run is found from physical positions: the run's destinations are exactly [lo, lo + n), so op i is
+// on an edge when origin[i] - lo names a moved op). The step is cleared as by take_step_outputs (op batches, if
+// built, are dropped). out_cap >= 5 * (the fused bound of abkv_planner_pending_sizes) + 4 * num_groups. Returns the
+// int32 elements written to `out` (index [num_groups, 5] as abkv_moves_pack), ABKV_ERR_CAPACITY or ABKV_ERR_ARG.
+int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc,
+                                       int32_t* out, int64_t out_cap, int64_t* index) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || !out || !index) return ABKV_ERR_ARG;
+  int64_t need_ops = 0, need_trunc = 0, need_fused = 0;
+  abkv_planner_pending_sizes(h, &need_ops, &need_trunc, &need_fused);
+  for (int64_t rid : p->trunc_order)
+    for (auto& st : find_req(p, rid)->step)
+      if (st.stale) {
+        p->last_error = "span removals of one step were interleaved with an allocation: take the step outputs "
+                        "once per scheduler step";
+        return ABKV_ERR_ARG;
+      }
+  const int G = p->num_groups;
+  if ((trunc_rows && need_trunc > trunc_cap) || out_cap < 5 * need_fused + 4 * (int64_t)G) return ABKV_ERR_CAPACITY;
+  int64_t t = 0;
+  if (trunc_rows) {
+    for (int64_t rid : p->trunc_order) {
+      Request* r = find_req(p, rid);
+      int64_t* row = trunc_rows + (1 + G) * t++;
+      row[0] = rid;
+      for (int g = 0; g < G; ++g) row[1 + g] = r->trunc[g];
+    }
+  }
+  if (n_trunc) *n_trunc = trunc_rows ? t : need_trunc;
+  // Pass 1: every run's surviving rows (origin) and which of them lie on a dependency edge, into flat scratch kept
+  // between steps; per group counts. Pass 2 writes each op once, at its final place in `out`.
+  struct RunInfo {
+    int g;
+    int64_t lo, n, at;                                    // at: the run's first row in the flat scratch
+    const int32_t* blocks;
+    bool any;
+  };
+  std::vector<RunInfo> runs;
+  std::vector<int64_t> n_ord_g((size_t)G, 0), n_free_g((size_t)G, 0), n_seg_g((size_t)G, 0);
+  std::vector<int64_t>& origin = p->mv_origin;
+  std::vector<uint8_t>& chained = p->mv_chained;
+  int64_t total = 0;
+  for (int64_t rid : p->trunc_order) {
+    Request* r = find_req(p, rid);
+    for (int g = 0; g < G; ++g) {
+      const auto& st = r->step[g];
+      if (st.removals.empty()) continue;
+      int64_t lo = st.removals[0].start, removed = 0;
+      for (auto& rm : st.removals) {
+        lo = std::min(lo, rm.start);
+        removed += rm.end - rm.start;
+      }
+      runs.push_back({g, lo, std::max<int64_t>(st.removals.front().active - lo - removed, 0), total,
+                      st.blocks_before.data(), false});
+      total += runs.back().n;
+    }
+  }
+  if ((int64_t)origin.size() < total) origin.resize((size_t)total);
+  if ((int64_t)chained.size() < total) chained.resize((size_t)total);
+  size_t ri = 0;
+  for (int64_t rid : p->trunc_order) {
+    Request* r = find_req(p, rid);
+    for (int g = 0; g < G; ++g) {
+      const auto& st = r->step[g];
+      if (st.removals.empty()) continue;
+      RunInfo& run = runs[ri++];
+      const int64_t lo = run.lo, n = run.n;
+      int64_t* org = origin.data() + run.at;
+      uint8_t* ch = chained.data() + run.at;
+      // final row i came from position lo + x, x found by undoing the removals last to first (each removal's span
+      // is in the coordinates the earlier ones left)
+      for (int64_t i = 0; i < n; ++i) {
+        int64_t x = i;
+        for (size_t k = st.removals.size(); k-- > 0;)
+          if (x >= st.removals[k].start - lo) x += st.removals[k].end - st.removals[k].start;
+        org[i] = lo + x;
+        ch[i] = 0;
+      }
+      // op i (row i, moved when org[i] != lo + i) reads org[i], the destination of op j = org[i] - lo when that row
+      // moves too: both lie on an edge
+      int64_t n_moved = 0, n_ch = 0;
+      for (int64_t i = 0; i < n; ++i) {
+        if (org[i] == lo + i) continue;
+        ++n_moved;
+        const int64_t j = org[i] - lo;
+        if (j < n && org[j] != lo + j) {
+          n_ch += !ch[i] + !ch[j];
+          ch[i] = ch[j] = 1;
+        }
+      }
+      run.any = n_ch > 0;
+      n_ord_g[(size_t)g] += n_ch;
+      n_free_g[(size_t)g] += n_moved - n_ch;
+      n_seg_g[(size_t)g] += run.any;
+    }
+  }
+  // layout, then pass 2
+  std::vector<int32_t*> ord_c((size_t)G), fre_c((size_t)G), seg_c((size_t)G);
+  int64_t at = 0;
+  for (int g = 0; g < G; ++g) {
+    const int64_t n_ord = n_ord_g[(size_t)g], n_free = n_free_g[(size_t)g], n_seg = n_seg_g[(size_t)g];
+    int32_t* ops = out + at;
+    int32_t* offs = ops + 4 * (n_ord + n_free);
+    ord_c[(size_t)g] = ops;
+    fre_c[(size_t)g] = ops + 4 * n_ord;
+    offs[0] = 0;
+    for (int64_t k2 = n_seg + 1; k2 < ((n_seg + 1 + 3) & ~(int64_t)3); ++k2) offs[k2] = 0;   // alignment padding
+    seg_c[(size_t)g] = offs + 1;
+    int64_t* ix = index + 5 * g;
+    ix[0] = at;
+    ix[1] = n_ord + n_free;
+    ix[2] = at + 4 * (n_ord + n_free);
+    ix[3] = n_seg;
+    ix[4] = n_free;
+    at += 4 * (n_ord + n_free) + ((n_seg + 1 + 3) & ~(int64_t)3);
+  }
+  for (const RunInfo& run : runs) {
+    const int g = run.g;
+    const int64_t* org = origin.data() + run.at;
+    const uint8_t* ch = chained.data() + run.at;
+    int32_t* vo = ord_c[(size_t)g];
+    int32_t* vf = fre_c[(size_t)g];
+    for (int64_t i = 0; i < run.n; ++i) {
+      const int64_t src = org[i], dst = run.lo + i;
+      if (src == dst) continue;
+      int32_t* d = ch[i] ? vo : vf;
+      d[0] = run.blocks[p->page_of(src)];
+      d[1] = p->off_of(src);
+      d[2] = run.blocks[p->page_of(dst)];
+      d[3] = p->off_of(dst);
+      if (ch[i]) vo += 4;
+      else vf += 4;
+    }
+    if (run.any) *seg_c[(size_t)g]++ = (int32_t)((vo - (out + index[5 * g])) / 4);
+    ord_c[(size_t)g] = vo;
+    fre_c[(size_t)g] = vf;
+  }
+  for (auto& kv : p->reqs) {
+    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    kv.second.has_trunc = false;
+    kv.second.alloc_after_removal = false;
+  }
+  p->pending_order.clear();
+  p->trunc_order.clear();
+  return at;
 }
 
 // Device-ready move lists of a step's fused rows (the fused_rows of abkv_planner_take_step_outputs; the rows of one
@@ -588,6 +761,7 @@ int64_t abkv_moves_pack(const int64_t* fused_rows, int64_t n, int num_groups, in
       }
       if (r.n_chained) offs[++n_seg] = (int32_t)k_ord;
     }
+    for (int64_t k2 = n_seg + 1; k2 < ((n_seg + 1 + 3) & ~(int64_t)3); ++k2) offs[k2] = 0;   // alignment padding
     int64_t* ix = index + 5 * g;
     ix[0] = at;
     ix[1] = n_ops[(size_t)g];

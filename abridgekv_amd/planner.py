@@ -60,7 +60,9 @@ class KVPlanner:
     """One page pool shared by ``num_groups`` KV-cache groups (pages of ``block_size`` slots, page 0 = null)."""
 
     def __init__(self, num_blocks: int, num_groups: int, block_size: int = 16, free_order=None,
-                 max_model_len: int | None = None):
+                 max_model_len: int | None = None, op_rows: bool = True):
+        """``op_rows=False``: skip the reference-format op batches (the bookkeeping and the fused moves are unchanged;
+        the step outputs then hold no ``kv_copy_operations``), for callers that execute the fused moves only."""
         self._lib = lib()
         fo = None
         if free_order is not None:
@@ -72,6 +74,9 @@ class KVPlanner:
         if not self._h:
             raise ValueError("invalid planner configuration (free_order must be a permutation of 1..num_blocks-1)")
         self.num_blocks, self.num_groups, self.block_size = num_blocks, num_groups, block_size
+        self.op_rows = bool(op_rows)
+        if not self.op_rows and self._lib.abkv_planner_set_op_rows(self._h, 0) != ABKV_OK:
+            raise RuntimeError("abkv_planner_set_op_rows failed")
         self._ids: dict = {}
         self._names: dict = {}
         self._bufs: dict = {}
@@ -221,11 +226,12 @@ class KVPlanner:
         tr = self._buffer("trunc", n_tr.value, 1 + G)
         fu = self._buffer("fused", n_fu.value, 6)
         o1, o2, o3 = C.c_int64(0), C.c_int64(0), C.c_int64(0)
-        rc = self._lib.abkv_planner_take_step_outputs(self._h, _i64(ops), ops.shape[0], C.byref(o1), _i64(tr),
-                                                      tr.shape[0], C.byref(o2), _i64(fu), fu.shape[0], C.byref(o3))
+        rc = self._lib.abkv_planner_take_step_outputs(self._h, _i64(ops) if self.op_rows else None, ops.shape[0],
+                                                      C.byref(o1), _i64(tr), tr.shape[0], C.byref(o2), _i64(fu),
+                                                      fu.shape[0], C.byref(o3))
         if rc != ABKV_OK:
             raise RuntimeError(f"take_step_outputs failed ({rc}): {self._err()}")
-        ops, tr, fu = ops[:o1.value], tr[:o2.value], fu[:o3.value]
+        ops, tr, fu = (ops[:o1.value] if self.op_rows else ops[:0]), tr[:o2.value], fu[:o3.value]
         if as_arrays:
             return ops, tr, fu
         ops, tr, fu = ops.copy(), tr.copy(), fu.copy()
@@ -239,6 +245,41 @@ class KVPlanner:
             batches[int(row[2])].append(tuple(int(x) for x in row[3:]))
         trunc = {self.request_id(int(row[0])): tuple(int(x) for x in row[1:]) for row in tr}
         return StepOutputs(kv_ops, trunc, fu)
+
+    def moves_capacity(self) -> int:
+        """int32 elements :meth:`take_step_moves` needs for the pending step."""
+        n_ops, n_tr, n_fu = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        self._lib.abkv_planner_pending_sizes(self._h, C.byref(n_ops), C.byref(n_tr), C.byref(n_fu))
+        return 5 * n_fu.value + 4 * self.num_groups
+
+    def take_step_moves(self, out: np.ndarray | None = None):
+        """The step's outputs for a caller that executes fused moves (abkv_planner_take_moves_packed), then cleared:
+        (trunc_rows [n, 1 + G] int64, buffer int32, parts) -- buffer and parts as :func:`worker.pack_fused_moves`
+        (per group the ordered segments, then the independent ops, then the segment offsets; parts lists (group,
+        ops_at, n_ops, offs_at, n_segments, n_free) for the groups with ops). ``out``: a contiguous int32 array of at
+        least :meth:`moves_capacity` elements to write into (e.g. pinned host memory); a reusable one otherwise. The
+        views are valid until the next call."""
+        n_ops, n_tr, n_fu = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        self._lib.abkv_planner_pending_sizes(self._h, C.byref(n_ops), C.byref(n_tr), C.byref(n_fu))
+        G = self.num_groups
+        need = 5 * n_fu.value + 4 * G
+        if out is None:
+            buf = self._bufs.get("moves")
+            if buf is None or buf.size < need:
+                buf = np.zeros(max(need, 2 * (0 if buf is None else buf.size)), np.int32)
+                self._bufs["moves"] = buf
+            out = buf
+        if out.dtype != np.int32 or not out.flags.c_contiguous or out.size < need:
+            raise ValueError(f"out must be a contiguous int32 array of at least {need} elements")
+        tr = self._buffer("trunc", n_tr.value, 1 + G)
+        index = np.zeros((G, 5), np.int64)
+        got_tr = C.c_int64(0)
+        rc = self._lib.abkv_planner_take_moves_packed(self._h, _i64(tr), tr.shape[0], C.byref(got_tr), _i32(out),
+                                                      out.size, _i64(index))
+        if rc < 0:
+            raise RuntimeError(f"take_moves_packed failed ({rc}): {self._err()}")
+        parts = [(g, *map(int, index[g])) for g in range(G) if index[g, 1] > 0]
+        return tr[:got_tr.value], out[:rc], parts
 
     def apply_events(self, events: np.ndarray) -> None:
         """Apply a batch of scheduler events (see abkv_planner_apply_events); raises on the first failure."""

@@ -30,7 +30,7 @@ import torch
 from . import ops
 from ._lib import check, lib
 from .backend import code_step_key_limits
-from .worker import device_move_lists, launch_moves, pack_fused_moves
+from .worker import device_move_lists, launch_moves
 from .workloads import (BLOCK_C, CODES_K_MAX, MAX_MODEL_LEN, QWEN3_4B_LAYER_QUOTAS, SAMPLED_TOKEN,
                         build_decode_state)
 
@@ -52,7 +52,7 @@ class ServingPlan:
         # pool slack for the run: every request's growth by growth_tokens rows per group, plus the code rows of up
         # to max_coding requests coding at once (compaction returns pages to the pool)
         slack = 1024 + len(T) * n_groups * (-(-growth_tokens // PAGE) + 2) + max_coding * n_groups * (K // PAGE + 2)
-        st = build_decode_state(T, P, layer_quotas, seed=seed, slack_pages=slack, C=C, K=K)
+        st = build_decode_state(T, P, layer_quotas, seed=seed, slack_pages=slack, C=C, K=K, op_rows=False)
         self.st = st
         self.planner = st.planner
         self.proc = st.processor
@@ -135,10 +135,11 @@ class ServingPlan:
                     upd_tables=self.tables[:, rows], upd_compacted=self.compacted[:, rows], tok_req=tok_req,
                     tok_pos=tok_pos, max_pos=int(tok_pos.max()) if n_tok else 0)
 
-    def advance(self, m) -> np.ndarray:
+    def advance(self, m):
         """Settle the step described by ``m`` in the state machine (compaction of the blocks whose code run ended, via
-        the planner), then schedule the next step. Returns the fused move rows to execute on the device (after the
-        step's attention, before the next step's appends)."""
+        the planner), then schedule the next step. Returns the step's fused moves as device move lists
+        (``KVPlanner.take_step_moves``: buffer, parts; valid until the next step) to execute on the device (after the
+        step's attention, before the next step's appends), or None."""
         B, G = self.B, self.G
         touched: set[int] = set()
         planner = self.planner
@@ -153,11 +154,11 @@ class ServingPlan:
                                                      MAX_MODEL_LEN)
             if stopped:
                 raise RuntimeError(f"request {r} stopped; the stress loop keeps every request decoding")
-        fused = np.zeros((0, 6), np.int64)
+        moves = None
         if touched:
-            _, _, fu = planner.take_step_outputs(as_arrays=True)
-            fused = fu.copy()
-            self.stats["moved_rows"] += int(fused.shape[0])
+            _, buf, parts = planner.take_step_moves()
+            moves = (buf, parts)
+            self.stats["moved_rows"] += sum(n for _, _, n, _, _, _ in parts)
             for r in touched:
                 self.compacted[:, r] = planner.compacted_counts(r)
         self.stats["decode_tokens"] += int(m["nd"])
@@ -174,7 +175,7 @@ class ServingPlan:
             for g in range(G):
                 self.tables[g][rows] = planner.fill_block_table(rows.tolist(), g, self.W)
             self.pending_rows = np.union1d(self.pending_rows, rows)
-        return fused
+        return moves
 
 
 class ServingStress:
@@ -402,7 +403,7 @@ class ServingStress:
         which run first in the next launch: after this step's attention, before the next step's appends)."""
         m = self._meta
         self._launch_step(m)
-        moves = pack_fused_moves(self.plan.advance(m), self.st.num_pages, check=False, num_groups=self.G)
+        moves = self.plan.advance(m)                       # staged (copied) before the planner's next step
         self._meta = self._stage(self.plan.prepare(), moves)
         return m
 

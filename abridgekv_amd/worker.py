@@ -103,6 +103,34 @@ def prepare_fused_moves(fused_moves: np.ndarray, num_pages: int, device, check: 
     return device_move_lists(torch.from_numpy(buf).to(device), parts)
 
 
+class MoveUploader:
+    """A planner step's move lists (KVPlanner.take_step_moves) written into pinned host memory and uploaded with one
+    asynchronous copy. The pinned buffer is reused: a call first waits for the copy that last read it."""
+
+    def __init__(self, device, capacity: int = 1 << 16):
+        self.device = device
+        self._pinned = torch.empty(capacity, dtype=torch.int32, pin_memory=True)
+        self._dev = torch.empty(capacity, dtype=torch.int32, device=device)
+        self._done = None
+
+    def take(self, planner):
+        """(trunc_rows, [(group, ordered ops, seg_offsets, independent ops)] on the device) of the pending step."""
+        need = planner.moves_capacity()
+        if self._done is not None:
+            self._done.synchronize()
+        if need > self._pinned.numel():
+            self._pinned = torch.empty(2 * need, dtype=torch.int32, pin_memory=True)
+            self._dev = torch.empty(2 * need, dtype=torch.int32, device=self.device)
+        trunc, buf, parts = planner.take_step_moves(self._pinned.numpy())
+        if not parts:
+            return trunc, []
+        n = buf.size
+        self._dev[:n].copy_(self._pinned[:n], non_blocking=True)
+        self._done = torch.cuda.Event()
+        self._done.record()
+        return trunc, device_move_lists(self._dev[:n], parts)
+
+
 def device_move_lists(dev_buf: torch.Tensor, parts):
     """Views of an uploaded :func:`pack_fused_moves` buffer: [(group, ordered ops, seg_offsets, independent ops)]."""
     out = []

@@ -206,9 +206,10 @@ class DecodeState:
 
 
 def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_pages=1024, C=BLOCK_C,
-                       K=CODES_K_MAX) -> DecodeState:
+                       K=CODES_K_MAX, op_rows: bool = True) -> DecodeState:
     """Replay every request's history through a planner over a pool sized for the batch, then schedule the decode
-    step (one token per request). Requests arrive staggered so that all reach their query at the same step."""
+    step (one token per request). Requests arrive staggered so that all reach their query at the same step.
+    ``op_rows=False``: a planner that emits the fused moves only."""
     T = np.asarray(T, np.int64)
     P = np.minimum(np.asarray(P, np.int64), T - 1)
     B = T.size
@@ -224,7 +225,7 @@ def build_decode_state(T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, slack_p
             pages_needed += -(-(rows_per_group(int(t), int(p), q, C) + K) // PAGE) + 1
     num_pages = pages_needed + slack_pages + 1
     free_order = np.random.default_rng(seed).permutation(np.arange(1, num_pages)).astype(np.int32)
-    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
+    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order, op_rows=op_rows)
     rows = []
     for r, (evs, n_steps, _) in enumerate(histories):
         start = S - n_steps
@@ -306,10 +307,11 @@ class CompactionState:
 
 
 def build_compaction_state(B=64, seed=0, layer_quotas=QWEN3_4B_LAYER_QUOTAS, C=BLOCK_C, K=CODES_K_MAX,
-                           max_prior_blocks=3, p_range=(128, 1024), slack_pages=1024) -> CompactionState:
+                           max_prior_blocks=3, p_range=(128, 1024), slack_pages=1024,
+                           op_rows: bool = True) -> CompactionState:
     """Config of the compaction benchmark: every request has closed ``nb`` earlier blocks (seeded in
     [0, max_prior_blocks]) and has just computed the K code rows of block ``nb``; prompts P ~ U[p_range] (capped so the
-    closing block holds at least one response row)."""
+    closing block holds at least one response row). ``op_rows=False``: a planner that emits the fused moves only."""
     rng = np.random.default_rng(seed)
     nb = rng.integers(0, max_prior_blocks + 1, B)
     P = rng.integers(p_range[0], p_range[1] + 1, B)
@@ -323,7 +325,7 @@ def build_compaction_state(B=64, seed=0, layer_quotas=QWEN3_4B_LAYER_QUOTAS, C=B
     pages_needed = sum(-(-(int(t) + K) // PAGE) + 1 for t in T) * G
     num_pages = pages_needed + slack_pages + 1
     free_order = rng.permutation(np.arange(1, num_pages)).astype(np.int32)
-    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order)
+    planner = KVPlanner(num_pages, G, PAGE, free_order=free_order, op_rows=op_rows)
     rows, pending = [], []
     for r, (evs, n_steps, _) in enumerate(histories):
         start = S - n_steps

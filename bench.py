@@ -280,12 +280,15 @@ def bench_prefill_bwd(args, torch):
 
 def bench_compaction(args, torch):
     """Config 2: 64 sequences each close one 512-token block (256 code rows computed) in one step; Qwen3-4B shape,
-    36 layers in 6 quota groups, page 16, seeded fragmented free list. Measures the planner (host) and the fused
-    device moves; algorithmic bytes = 2 x (kept code rows x 4096 B) summed over layers."""
+    36 layers in 6 quota groups, page 16, seeded fragmented free list. Timed: the planner step (the span removals with
+    the reference's bookkeeping -- spans, page lists, truncations, free queue -- without the reference-format op
+    rows the fused path does not execute), the op upload (the planner writes the packed move lists into pinned memory,
+    one copy to the device) and the fused device moves; algorithmic bytes = 2 x (kept code rows x 4096 B) summed over
+    layers."""
     from abridgekv_amd import ops, worker, workloads
 
     B = 64
-    st = workloads.build_compaction_state(B, seed=args.seed)
+    st = workloads.build_compaction_state(B, seed=args.seed, op_rows=False)      # the fused path needs no op rows
     dev = torch.device("cuda")
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     n_tensors = max(len(g) for g in st.groups)
@@ -295,22 +298,26 @@ def bench_compaction(args, torch):
         c.normal_(generator=gen)
         caches.append(c)
     by_group = [[caches[i] for i in range(len(layers))] for layers in st.groups]
-    st.planner.reserve_outputs(B * len(st.groups) * 1024, B * len(st.groups) * 2048)
-    t0 = time.perf_counter()
-    op_rows, _, fused = st.compact(as_arrays=True)             # the planner step (host C++), reference semantics
-    plan_s = time.perf_counter() - t0
-    st_ref = workloads.build_compaction_state(B, seed=args.seed)
-    outs = st_ref.compact()                                    # same step, reference-format op dict for comparison
-    ref_rows = len(op_rows)
-    fused = fused.copy()
-    layers_per_group = len(st.groups[0])
-    alg_bytes = 2 * len(fused) * layers_per_group * 4096
-    worker.prepare_fused_moves(fused, st.num_pages, dev, check=False)      # first call pays one-off runtime setup
+    st.planner.reserve_outputs(0, 0, B)
+    uploader = worker.MoveUploader(dev, capacity=8 << 20)     # pinned staging, sized once (8 Mi int32)
+    warm = workloads.build_compaction_state(B, seed=args.seed + 1, op_rows=False)
+    warm.planner.apply_events(warm.pending)
+    uploader.take(warm.planner)                                # first use pays one-off runtime setup
     torch.cuda.synchronize()
+    del warm
     t0 = time.perf_counter()
-    prepared = worker.prepare_fused_moves(fused, st.num_pages, dev, check=False)
+    st.planner.apply_events(st.pending)                        # the planner step (host C++), reference semantics
+    plan_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    _, prepared = uploader.take(st.planner)                    # move lists written into pinned memory, one upload
     torch.cuda.synchronize()
     prep_s = time.perf_counter() - t0
+    n_fused = sum(int(o.shape[0]) + int(f.shape[0]) for _, o, _, f in prepared)
+    st_ref = workloads.build_compaction_state(B, seed=args.seed)
+    outs = st_ref.compact()                                    # same step, reference-format op dict for comparison
+    ref_rows = sum(len(b) for v in outs.kv_copy_operations.values() for g in v for b in g)
+    layers_per_group = len(st.groups[0])
+    alg_bytes = 2 * n_fused * layers_per_group * 4096
     for _ in range(args.warmup):
         worker.launch_moves(prepared, by_group)
     torch.cuda.synchronize()
@@ -371,7 +378,7 @@ def bench_compaction(args, torch):
                          "mover_frac_of_copy": gbps / copy_gbps},
         "same_pattern_probe": probe,
         "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
-        "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": int(len(fused)),
+        "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": n_fused,
     }
 
 

@@ -277,6 +277,10 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
 void* abkv_planner_create(int num_blocks, int num_groups, int block_size, const int32_t* free_order,
                           int64_t max_model_len);
 void abkv_planner_destroy(void* planner);
+/* 1 (default): build the reference-format op batches; 0: skip them (the bookkeeping and the fused moves are unchanged;
+ * take_step_outputs then returns no op rows). The reference always builds them (single_type_kv_cache_manager.py:
+ * 378-381, consumed by gpu_model_runner.py:1194-1224); a caller that executes the fused moves only turns them off. */
+int abkv_planner_set_op_rows(void* planner, int enabled);
 const char* abkv_planner_last_error(void* planner);
 int abkv_planner_add_request(void* planner, int64_t rid);
 int abkv_planner_free_request(void* planner, int64_t rid);
@@ -304,6 +308,13 @@ int abkv_planner_take_step_outputs(void* planner, int64_t* op_rows, int64_t op_c
  * op of its run writes). */
 int64_t abkv_moves_pack(const int64_t* fused_rows, int64_t n, int num_groups, int32_t* out, int64_t out_cap,
                         int64_t* index);
+/* The step outputs for a caller that executes fused moves: trunc_rows as abkv_planner_take_step_outputs, and the
+ * device move lists of abkv_moves_pack written directly into `out` (capacity >= 5 x the fused bound of
+ * abkv_planner_pending_sizes + 4 num_groups int32; index [num_groups, 5] as abkv_moves_pack). Clears the step.
+ * Returns the int32 elements written, ABKV_ERR_CAPACITY or ABKV_ERR_ARG. (The reference's scheduler output,
+ * scheduler.py:2060-2204 and sched/output.py:221-225, in the fused form.) */
+int64_t abkv_planner_take_moves_packed(void* planner, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc,
+                                       int32_t* out, int64_t out_cap, int64_t* index);
 int64_t abkv_planner_num_free(void* planner);
 int64_t abkv_planner_free_queue(void* planner, int32_t* out, int64_t cap);
 int64_t abkv_planner_block_ids(void* planner, int64_t rid, int group, int32_t* out, int64_t cap);

@@ -24,6 +24,12 @@ def run_oracle_step(planner: oc.Planner, events, added: set):
 
 
 def run_native_step(planner, events, added: set):
+    run_events(planner, events, added)
+    return planner.take_step_outputs()
+
+
+def run_events(planner, events, added: set) -> None:
+    """A step's allocations and span removals on the native planner (outputs left pending)."""
     for ev in events:
         if ev[0] == "alloc":
             _, rid, n = ev
@@ -36,7 +42,6 @@ def run_native_step(planner, events, added: set):
             _, rid, s, e, g = ev
             res = planner.mask_token_span(rid, s, e, g)
             assert res.success, res.error_message
-    return planner.take_step_outputs()
 
 
 def events_to_array(steps, num_groups):

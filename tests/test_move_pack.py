@@ -170,3 +170,36 @@ def test_pack_rejects_inputs_the_launch_cannot_run():
     twice = np.array([[1, 0, 5, 3, 5, 0], [1, 0, 5, 3, 5, 1]], np.int64)                    # one slot read twice
     with pytest.raises(ValueError):
         worker.pack_fused_moves(twice, 16)
+
+
+@pytest.mark.parametrize("op_rows", [True, False])
+def test_planner_writes_the_same_move_lists_directly(op_rows):
+    """KVPlanner.take_step_moves (the planner writing the packed lists itself, dependencies from physical positions)
+    equals take_step_outputs followed by pack_fused_moves, element for element, with the same truncation rows: on the
+    64-sequence step and on served multi-step schedules."""
+    a = workloads.build_compaction_state(64, seed=0, op_rows=op_rows)
+    b = workloads.build_compaction_state(64, seed=0, op_rows=op_rows)
+    _, tr_a, fu_a = a.compact(as_arrays=True)
+    buf_a, parts_a = worker.pack_fused_moves(fu_a, a.num_pages)
+    b.planner.apply_events(b.pending)
+    tr_b, buf_b, parts_b = b.planner.take_step_moves()
+    assert np.array_equal(tr_a, tr_b) and parts_a == parts_b and np.array_equal(buf_a, buf_b)
+    assert b.planner.free_queue() == a.planner.free_queue()
+    quotas = (256, 64, 64, 128, 128, 128)
+    for seed in range(3):
+        steps, _ = make_schedule(seed, 4, 512, 256, quotas, max_prompt=3 * 512, max_closed=3)
+        perm = np.random.default_rng(100 + seed).permutation(np.arange(1, 4000)).astype(np.int32)
+        pa = KVPlanner(4000, len(quotas), PAGE, free_order=perm, op_rows=op_rows)
+        pb = KVPlanner(4000, len(quotas), PAGE, free_order=perm, op_rows=op_rows)
+        seen_a, seen_b = set(), set()
+        from tests.planner_harness import run_events
+        for events in steps:
+            out = run_native_step(pa, events, seen_a)
+            run_events(pb, events, seen_b)
+            tr, buf, parts = pb.take_step_moves()
+            fm = np.asarray(out.fused_moves, dtype=np.int64)
+            ref_buf, ref_parts = worker.pack_fused_moves(fm, 4000, num_groups=len(quotas)) if fm.size else (None, [])
+            assert parts == ref_parts
+            if parts:
+                assert np.array_equal(buf, ref_buf)
+            assert {pb.request_id(int(r[0])): tuple(int(x) for x in r[1:]) for r in tr} == out.block_table_truncations

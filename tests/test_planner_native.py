@@ -127,3 +127,39 @@ def test_compaction_workload_64_sequences_matches_oracle():
             ids = oracle.block_ids(r)[g]
             ref[r, :len(ids)] = ids
         assert np.array_equal(st.planner.fill_block_table(rids, g, W), ref), f"group {g}"
+
+
+def test_fused_only_planner_keeps_the_bookkeeping_and_the_fused_moves():
+    """op_rows=False skips the reference-format op batches only: on the 64-sequence compaction step and on served
+    multi-step schedules, page lists, spans, truncations, the free queue and the fused moves equal those of the planner
+    that builds the op batches, and no op rows are emitted."""
+    from abridgekv_amd import workloads
+
+    a = workloads.build_compaction_state(64, seed=0)
+    b = workloads.build_compaction_state(64, seed=0, op_rows=False)
+    ops_a, tr_a, fu_a = a.compact(as_arrays=True)
+    ops_b, tr_b, fu_b = b.compact(as_arrays=True)
+    assert len(ops_a) > 64 * 256 and len(ops_b) == 0
+    assert np.array_equal(tr_a, tr_b) and np.array_equal(fu_a, fu_b)
+    assert a.planner.free_queue() == b.planner.free_queue()
+    for r in range(64):
+        assert a.planner.get_blocks(r) == b.planner.get_blocks(r)
+        assert a.planner.compacted_counts(r) == b.planner.compacted_counts(r)
+    quotas = SERVED["quotas"]
+    for seed in range(3):
+        steps, _ = make_schedule(seed, 4, SERVED["C"], SERVED["K"], quotas, max_prompt=3 * SERVED["C"], max_closed=3)
+        perm = np.random.default_rng(100 + seed).permutation(np.arange(1, 4000)).astype(np.int32)
+        full = KVPlanner(4000, len(quotas), 16, free_order=perm)
+        fused = KVPlanner(4000, len(quotas), 16, free_order=perm, op_rows=False)
+        seen_a, seen_b = set(), set()
+        for events in steps:
+            out_a = run_native_step(full, events, seen_a)
+            out_b = run_native_step(fused, events, seen_b)
+            assert out_b.kv_copy_operations == {}
+            assert out_a.block_table_truncations == out_b.block_table_truncations
+            assert np.array_equal(out_a.fused_moves, out_b.fused_moves)
+        assert full.free_queue() == fused.free_queue()
+        for r in sorted(seen_a):
+            assert full.get_blocks(r) == fused.get_blocks(r)
+            for g in range(len(quotas)):
+                assert full.group_compacted_spans(r, g) == fused.group_compacted_spans(r, g)
