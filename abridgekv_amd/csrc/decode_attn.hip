@@ -412,11 +412,23 @@ __global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
   const long v_off = (long)a.side_rows * kHeadDim;
 
   for (int c0 = r_begin; c0 < r_end; c0 += 32) {
+    // With q_h >= 32 the chunk's 32 rows lie in pages pa and pa + 1: both ids by readlane (scalar) and a select per
+    // row; smaller quotas look each row's page up across lanes.
+    const int pa = (int)(((float)c0 + 0.5f) * inv_q);
+    const int pid_a = __builtin_amdgcn_readlane(pid_l, min(pa - p0, 63));
+    const int pid_b = __builtin_amdgcn_readlane(pid_l, min(pa + 1 - p0, 63));
+    const int bound = (pa + 1) * qh;
+    auto chunk_row_ptr = [&](int r) -> const __bf16* {
+      if (qh < 32) return row_ptr(r);
+      const bool second = r >= bound;
+      const int slot = r - (second ? bound : pa * qh);
+      return base_h + (long)(second ? pid_b : pid_a) * page_elems + slot * kHeadDim;
+    };
     // rows past r_end read row r_end - 1 instead (finite data; their weight is exactly 0)
     u32x4 kr[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const __bf16* kp = row_ptr(min(c0 + 16 * t + m16, r_end - 1));
+      const __bf16* kp = chunk_row_ptr(min(c0 + 16 * t + m16, r_end - 1));
 #pragma unroll
       for (int i = 0; i < 4; ++i) kr[t][i] = ld16(kp + 8 * (4 * i + j));
     }
@@ -424,7 +436,7 @@ __global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
     u32x4 vr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      vr[e] = ld16(row_ptr(min(c0 + (e < 4 ? 0 : 16) + 4 * j + (e & 3), r_end - 1)) + v_off + 8 * m16);
+      vr[e] = ld16(chunk_row_ptr(min(c0 + (e < 4 ? 0 : 16) + 4 * j + (e & 3), r_end - 1)) + v_off + 8 * m16);
 
     floatx4 s[2];
 #pragma unroll

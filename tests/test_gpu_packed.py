@@ -183,3 +183,43 @@ def test_sidecar_capture_then_decode():
             assert np.abs(_f64(out[i]) - ro[0]).max() <= TOL, f"layer {layer} request {r}"
     side.free("a")
     assert side.request_pages("a") == [] and len(side._free) == 32 - 1
+
+
+def test_decode_packed_wide_quotas_matches_oracle():
+    """Head quotas of 32 and more, some not multiples of 32 (the side kernel then takes a 32-row chunk's two packed
+    pages by readlane, and chunks straddle page boundaries), up to 40 packed pages per sequence so that splits span
+    many pages; packed pools filled at random."""
+    from abridgekv_amd import ops
+    row = (32, 48, 64, 100, 128, 160, 200, 256)
+    rng = np.random.default_rng(31)
+    g = torch.Generator().manual_seed(31)
+    cache = torch.randn((400, 2, 16, 8, 128), generator=g).to(torch.bfloat16)
+    lens = [1, 17, 300, 1100, 37, 520]
+    counts = [3, 0, 1, 7, 40, 12]
+    pool_pages = 70
+    pool = torch.randn((pool_pages, 2, sum(row), 128), generator=g).to(torch.bfloat16)
+    free = list(rng.permutation(pool_pages))
+    pages = [[int(free.pop()) for _ in range(n)] for n in counts]
+    need = [-(-n // 16) for n in lens]
+    perm = rng.permutation(np.arange(1, 400))
+    bt = np.zeros((len(lens), max(need)), dtype=np.int32)
+    at = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = perm[at: at + n]
+        at += n
+    q = torch.randn((len(lens), 32, 128), generator=g).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    table, count = _table(pages)
+    lse = torch.empty((len(lens), 32), dtype=torch.float32, device=dev)
+    out, _ = ops.decode_attention_packed(q.to(dev), cache.to(dev), torch.from_numpy(bt).to(dev),
+                                         torch.tensor(lens, dtype=torch.int32, device=dev), pool.to(dev), row,
+                                         torch.from_numpy(table).to(dev), torch.from_numpy(count).to(dev),
+                                         128 ** -0.5, lse=lse)
+    torch.cuda.synchronize()
+    cf, pf = cache.float().numpy(), pool.float().numpy()
+    for i in range(len(lens)):
+        ro, rl = opk.packed_attention_fp64(_f64(q[i:i + 1]), [pf[p] for p in pages[i]], row, cf, bt[i], lens[i], 1,
+                                           True, 256, 128 ** -0.5)
+        go, gl = _f64(out[i]), lse[i].cpu().numpy()
+        assert np.abs(go - ro[0]).max() <= TOL, f"seq {i}"
+        assert np.abs(gl - rl[0]).max() <= TOL
