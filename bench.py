@@ -64,8 +64,10 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=None,
                     help="pages per decode split (default: ops.auto_split_pages per launch: 48, 40 or 32)")
     ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "config1", "prefill", "prefill_bwd",
-                                           "compaction", "packed", "copy", "lds"],
+                                           "compaction", "packed", "code_step", "copy", "lds"],
                     default="serving")
+    ap.add_argument("--code-requests", type=int, default=1,
+                    help="code_step: requests coding in one launch (the serving stress averages ~0.5 per step)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     args = ap.parse_args()
@@ -483,6 +485,145 @@ def compaction_cpu_baseline(torch, B, seed, layers_per_group):
                       f"indexing, one thread)"}
 
 
+def bench_code_step(args, torch):
+    """The code step of the saturated serving stress: a request whose 512-token block just filled attends its K=256
+    code rows (32 q heads) to every row it holds before them (raw prompt, earlier blocks' codes), the block's 512
+    content rows and the first q of its own code rows (non-causal, key limit code_start + q per group), one launch per
+    layer over the 36 layers (6 groups, quotas 256/64/64/128/128/128), keys split over workgroups and merged
+    (ops.paged_split_plan). Requests: the first R of the saturated workload's (T, P) draws, each at its last closed
+    block b = T // 512 - 1. value = visible QK+PV FLOPs (4 * D * 256 * limit * 32 heads per request and layer) over the
+    launches' event time (kernel + merge)."""
+    import ctypes as C_
+
+    from abridgekv_amd import ops, workloads
+    from abridgekv_amd._lib import check, lib
+
+    R, C, K = args.code_requests, workloads.BLOCK_C, workloads.CODES_K_MAX
+    T, P = workloads.saturated_decode_lengths(256, seed=args.seed)
+    T, P = [int(t) for t in T[:R]], [int(p) for p in P[:R]]
+    groups, gq = workloads.quota_groups(workloads.QWEN3_4B_LAYER_QUOTAS)
+    layer_quota = {l: gq[g] for g, ls in enumerate(groups) for l in ls}
+    L = len(workloads.QWEN3_4B_LAYER_QUOTAS)
+    blocks = [t // C - 1 for t in T]
+    # physical rows before block b's code rows = the group's rows once the block's last content token is computed
+    starts = [[workloads.rows_per_group((b + 1) * C, p, layer_quota[l], C) for b, p in zip(blocks, P)] for l in range(L)]
+    limits = [[s + min(layer_quota[l], K) for s in starts[l]] for l in range(L)]
+    need = [[-(-(s + K) // 16) for s in starts[l]] for l in range(L)]
+    n_pages = sum(sum(x) for x in need) + 1
+    W = max(max(x) for x in need)
+    rng = np.random.default_rng(args.seed)
+    perm = rng.permutation(np.arange(1, n_pages)).astype(np.int32)
+    tables, at = [], 0
+    for l in range(L):
+        tab = np.zeros((R, W), np.int32)
+        for r in range(R):
+            tab[r, : need[l][r]] = perm[at: at + need[l][r]]
+            at += need[l][r]
+        tables.append(tab)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    cache = torch.empty(ops.kv_cache_shape(n_pages), dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+    q = torch.randn((R * K, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    tiles = np.array([(r, q0) for r in range(R) for q0 in range(0, K, 64)], np.int32)
+    n_tiles = tiles.shape[0]
+    tl = torch.from_numpy(np.ascontiguousarray(tiles.T)).to(dev)
+    q_start = torch.from_numpy(np.arange(R + 1, dtype=np.int32) * K).to(dev)
+    meta = [(torch.from_numpy(tables[l]).to(dev), torch.tensor(starts[l], dtype=torch.int32, device=dev),
+             torch.tensor(limits[l], dtype=torch.int32, device=dev), ops.paged_split_plan(n_tiles, max(limits[l])))
+            for l in range(L)]
+    ws_bytes = max((lib().abkv_paged_prefill_workspace_size(R * K, m[3][0]) for m in meta if m[3][0] > 1), default=0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    scale = ops.default_scale()
+    stream = C_.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ptr = lambda t: C_.c_void_p(t.data_ptr())
+
+    def launch(l):
+        bt, ks, kl, (n_sp, sp_tiles) = meta[l]
+        check(lib().abkv_paged_prefill_attn(ptr(q), q.stride(0), q.stride(1), ptr(cache), n_pages, ptr(bt), W, W,
+                                            ptr(q_start), ptr(ks), ptr(kl), ptr(tl[0]), ptr(tl[1]), n_tiles, None, 0,
+                                            C_.c_float(scale), ptr(out), out.stride(0), out.stride(1), None, R * K,
+                                            n_sp, sp_tiles, ptr(ws) if n_sp > 1 else None,
+                                            C_.c_size_t(ws_bytes if n_sp > 1 else 0), stream),
+              "abkv_paged_prefill_attn")
+
+    for _ in range(args.warmup):
+        for l in range(L):
+            launch(l)
+    torch.cuda.synchronize()
+    evs = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for l in range(L):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch(l)
+            e1.record()
+            evs.append((e0, e1))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_launch = sum(a.elapsed_time(b) for a, b in evs) / 1e3 / len(evs)
+    flops_step = sum(4.0 * 128 * K * sum(limits[l]) * 32 for l in range(L))
+    flops_launch = flops_step / L
+    kv_bytes_launch = sum(4096.0 * sum(limits[l]) for l in range(L)) / L
+    tflops = flops_launch / t_launch / 1e12
+    res = {
+        "metric": "serving code-step attention TFLOP/s (visible QK+PV flops); % of bf16 dense MFMA peak",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic N(0,1) K/V pages and code-row queries from the seed",
+        "config": {"workload": f"code step of the saturated serving stress: {R} request(s) (T={T}, P={P}) attend "
+                               f"their {K} code rows to the rows before them + the block's {C} content rows + the "
+                               f"first q own code rows, 36 layers (quotas 256/64/64/128/128/128), 32q/8kv, d128, "
+                               f"page 16", "global_batch": R, "layers": L,
+                   "key_limits_per_group": [limits[groups[g][0]] for g in range(len(groups))],
+                   "splits_per_group": [meta[groups[g][0]][3][0] for g in range(len(groups))]},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
+                     "traffic": None, "kernel": "paged_prefill_kernel (+ paged_merge_kernel), per layer launch",
+                     "alg_flops_per_launch": flops_launch, "avg_launch_us": t_launch * 1e6,
+                     "kv_bytes_per_launch": kv_bytes_launch,
+                     "kv_stream_gbps": kv_bytes_launch / t_launch / 1e9},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = code_step_cpu_baseline(torch, cache, q, tables, starts, limits, groups, K, scale)
+    return res
+
+
+def code_step_cpu_baseline(torch, cache, q, tables, starts, limits, groups, K, scale, target_s=10.0):
+    """The reference's per-request multi-query arithmetic (oracle.decode.request_ref_torch, restating
+    compresslm_packed_kv.py:648-745: bf16 scores, fp32 softmax, bf16 weights) on the host cores, over the same code
+    steps: every request, one layer per group (the other layers of a group have the same key counts). value = the
+    sample's visible FLOPs over its time."""
+    from oracle.decode import request_ref_torch
+
+    host = cpu_threads(torch)
+    samples, flops = [], 0.0
+    for g in range(len(groups)):
+        l = groups[g][0]
+        for r in range(len(starts[l])):
+            n = starts[l][r] + K
+            rows = torch.arange(n)
+            pages = torch.from_numpy(tables[l][r].astype(np.int64)).cuda()[rows.cuda() // 16]
+            kv = cache[pages, :, (rows % 16).cuda()].cpu()                     # [n, 2, 8, 128]
+            key = kv[:, 0].permute(1, 0, 2).contiguous()
+            value = kv[:, 1].permute(1, 0, 2).contiguous()
+            samples.append((q[r * K: (r + 1) * K].cpu(), key, value, limits[l][r]))
+            flops += 4.0 * 128 * K * limits[l][r] * 32
+    for qq, k, v, lim in samples:                                            # warm-up
+        request_ref_torch(qq, k, v, scale, lim)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for qq, k, v, lim in samples:
+            request_ref_torch(qq, k, v, scale, lim)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    return {"value": flops * reps / el / 1e12, "unit": "TFLOP/s", "kind": "port", **host,
+            "sample": f"the same code steps, one layer per KV group ({len(samples)} request-layers), {reps} reps in "
+                      f"{el:.1f} s; torch CPU restatement of compresslm_packed_kv.py:648-745"}
+
+
 def bench_config1(args, torch):
     """Config 1: single-layer abridged decode attention, B=1, quota K=128: 256 prompt rows at positions 0..255, 4 closed
     blocks of C=512 starting at 256 compressed to 128 code rows at in-block bitrev positions, an open block of 300 rows
@@ -791,10 +932,11 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "copy", "lds"):
+    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "code_step", "copy",
+                         "lds"):
         res = {"serving": bench_serving, "config1": bench_config1, "prefill": bench_prefill,
                "prefill_bwd": bench_prefill_bwd, "compaction": bench_compaction, "packed": bench_packed,
-               "copy": bench_copy, "lds": bench_lds}[args.workload](args, torch)
+               "code_step": bench_code_step, "copy": bench_copy, "lds": bench_lds}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 

@@ -8,6 +8,9 @@ Pinning:
                             invariance of rows, and agreement with scipy.special.logsumexp / softmax.
 * ``decode_ref_torch``   -- the reference's own arithmetic on CPU torch; pinned against decode_fp64 within the bf16
                             bound (it is a measurement baseline, not a parity target).
+* ``request_ref_torch``  -- the reference's per-request multi-query arithmetic (code step / prompt chunk) on CPU
+                            torch; pinned against decode_fp64 row by row within the bf16 bound, with a planted value
+                            row just past each query's visible range that would break the bound if it were read.
 """
 from __future__ import annotations
 
@@ -98,3 +101,27 @@ def decode_ref_torch(q, kv_cache, block_table, seq_lens, scale, page: int = PAGE
     weights = torch.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
     attended = torch.einsum("rhgt,rhtd->rhgd", weights, value)
     return attended.reshape(B, Hq, D)
+
+
+def request_ref_torch(q, key, value, scale, limit: int, causal: bool = False, prefix_len: int = 0):
+    """The reference's multi-query attention of one request on CPU torch, used as the timed CPU baseline of the code
+    step: third_party/vllm_overlay/vllm/v1/worker/compresslm_packed_kv.py:648-745 (_attend_request_vectorized: one
+    einsum over all KV heads, hidden keys -> -inf, softmax(dtype=float32).to(q.dtype), einsum), main rows only.
+
+    q [n, Hq, D]; key / value [Hkv, S, D] (the request's physical rows); query i sees keys < limit, and when causal
+    also keys <= prefix_len + i (the code step is non-causal with limit = code start + quota). Returns [n, Hq, D].
+    """
+    import torch
+
+    n, Hq, D = q.shape
+    Hkv, S = key.shape[0], key.shape[1]
+    g = Hq // Hkv
+    qq = q.reshape(n, Hkv, g, D)
+    scores = torch.einsum("qhgd,htd->qhgt", qq, key) * scale
+    pos = torch.arange(S)
+    hidden = (pos >= limit).unsqueeze(0).expand(n, S)
+    if causal:
+        hidden = hidden | (pos.unsqueeze(0) >= (prefix_len + torch.arange(1, n + 1)).unsqueeze(1))
+    scores.masked_fill_(hidden.view(n, 1, 1, S), -torch.inf)
+    weights = torch.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
+    return torch.einsum("qhgt,htd->qhgd", weights, value).reshape(n, Hq, D)

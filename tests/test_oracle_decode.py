@@ -85,3 +85,30 @@ def test_reference_arithmetic_within_bf16_bound():
                               128 ** -0.5).float().numpy()
     ref, _ = od.decode_paged_fp64(q.float().numpy(), cache.float().numpy(), table, lens, 128 ** -0.5)
     assert np.abs(got - ref).max() <= 2e-2
+
+
+def test_request_arithmetic_within_bf16_bound_and_limit_exact():
+    """The reference's per-request multi-query arithmetic (code step: non-causal, keys < limit; prompt chunk: causal
+    after a prefix) row by row against the fp64 closed form. The key row just past each query's visible range carries
+    values of 100: reading it would move that query's output far beyond the 2e-2 bound."""
+    g = torch.Generator().manual_seed(3)
+    S, n = 90, 12
+    key = torch.randn((8, S, 128), generator=g).to(torch.bfloat16)
+    value = torch.randn((8, S, 128), generator=g).to(torch.bfloat16)
+    q = torch.randn((n, 32, 128), generator=g).to(torch.bfloat16)
+    kf, vf, qf = (t.float().numpy() for t in (key, value, q))
+    # non-causal, keys < 70: row 70 planted
+    v_pl = value.clone()
+    v_pl[:, 70] = 100.0
+    got = od.request_ref_torch(q, key, v_pl, 128 ** -0.5, limit=70).float().numpy()
+    for i in range(n):
+        ref, _ = od.decode_fp64(qf[i], kf[:, :70].transpose(1, 0, 2), vf[:, :70].transpose(1, 0, 2), 128 ** -0.5)
+        assert np.abs(got[i] - ref).max() <= 2e-2
+    # causal after a prefix of 60: query i sees keys <= 60 + i; the planted row is the first one it must not see
+    for i in (0, 5, 11):
+        v_pl = value.clone()
+        v_pl[:, 61 + i] = 100.0
+        got = od.request_ref_torch(q, key, v_pl, 128 ** -0.5, limit=S, causal=True, prefix_len=60).float().numpy()
+        m = 61 + i
+        ref, _ = od.decode_fp64(qf[i], kf[:, :m].transpose(1, 0, 2), vf[:, :m].transpose(1, 0, 2), 128 ** -0.5)
+        assert np.abs(got[i] - ref).max() <= 2e-2
