@@ -1,9 +1,11 @@
 """Serving configuration of the abridged cache (API-compatible subset of the reference's CompressLMConfig).
 
 Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309 for the configuration this path serves: one pause
-pass, raw prompt, bitrev code positions, no replay / raw / retained tails, optional per-layer quotas with physical
-removal, or per-head quotas in packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as at
-compresslm.py:145-190). Options of the reference that belong to other modes (replay tails, retained tails, selective
+pass, raw prompt, bitrev code positions, an optional STATIC retained tail (retain_tail_kv = T with
+retain_tail_policy="static": the last T content rows of every block stay resident and the codes summarize only the
+first C - T, compresslm.py:22-25, 192-206), optional per-layer quotas with physical removal, or per-head quotas in
+packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as at compresslm.py:145-190). Options of the
+reference that belong to other modes (replay / raw tails, the rolling and sticky window tails, selective
 full-history evaluation) are rejected with ValueError instead of being silently ignored.
 """
 from __future__ import annotations
@@ -98,6 +100,8 @@ class CompressLMConfig:
         self.layer_code_quotas = tuple(int(q) for q in self.layer_code_quotas)
         self.packed_kv_quotas = tuple(tuple(int(v) for v in row) for row in self.packed_kv_quotas)
         self.retain_full_history_layers = tuple(sorted(set(self.retain_full_history_layers)))
+        if self.retain_tail_policy not in ("rolling", "sticky", "static"):
+            raise ValueError("retain_tail_policy must be one of: rolling, sticky, static")
         if self.code_positions not in ("appended", "bitrev"):
             raise ValueError("code_positions must be appended or bitrev")
         if not self.enable:
@@ -111,8 +115,17 @@ class CompressLMConfig:
             raise ValueError("only code_positions='bitrev' is served")
         if (C & (C - 1)) or (K & (K - 1)):
             raise ValueError("code_positions=bitrev needs power-of-two block_size and num_code_tokens")
-        if self.replay_tail or self.raw_tail or self.retain_tail_kv or self.code_exclude_replay_tail:
-            raise ValueError("replay / raw / retained tails are not served")
+        if self.replay_tail or self.raw_tail or self.code_exclude_replay_tail:
+            raise ValueError("replay / raw tails are not served")
+        if not 0 <= self.retain_tail_kv < C:
+            raise ValueError("retain_tail_kv must be in [0, block_size)")
+        if self.retain_tail_policy == "sticky" and not self.retain_tail_kv:
+            raise ValueError("retain_tail_policy='sticky' requires retain_tail_kv > 0")
+        if self.retain_tail_kv and self.retain_tail_policy != "static":
+            raise ValueError("only the static retained tail is served (retain_tail_policy='static'); the rolling / "
+                             "sticky window tails are not")
+        if C - self.retain_tail_kv < K:
+            raise ValueError(f"bitrev code span {C - self.retain_tail_kv} < num_code_tokens {K}")
         if self.num_passes != 1:
             raise ValueError("CompressLM decoding supports num_passes=1 only")
         if self.pause_xattn != "full":
@@ -187,7 +200,9 @@ class CompressLMConfig:
     # -- positions ------------------------------------------------------------------------------------------------
     @property
     def code_excluded_tail(self) -> int:
-        return 0
+        """Content rows at the end of each block that the block's own codes never see and do not summarize (the
+        static retained tail: compresslm.py:254-257 with no replay tail)."""
+        return self.retain_tail_kv
 
     def bitrev_code_offsets(self) -> np.ndarray:
         """In-block RoPE offsets of the code rows (config/compresslm.py:192-206)."""

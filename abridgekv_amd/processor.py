@@ -1,12 +1,13 @@
 """Scheduler-side block state machine: which tokens run when, and which spans are compacted.
 
 API-compatible with the reference's CompressLMProcessor (third_party/vllm_overlay/vllm/v1/core/compresslm/
-processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay / retained tails,
-physical per-layer quotas or per-head packed KV pages): prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121,
-limit_num_new_tokens :123-151, should_skip_sampling :153-168, update_after_step :170-257, reset_for_preemption
-:259-260, code_physical_spans :276-316, _stage_codes :369-400, _finish_block :419-465, _compact_response_content
-:467-557, _mask_or_raise :648-661, _check_stop :663-685. The compaction callback ``mask_span(request_id, start, end,
-groups=None)`` is KVPlanner.mask_token_span.
+processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay tail, an optional
+static retained tail, physical per-layer quotas or per-head packed KV pages): prepare_request :42-105, is_code_ready /
+num_code_rows_pending :106-121, limit_num_new_tokens :123-151, should_skip_sampling :153-168, update_after_step
+:170-257, reset_for_preemption :259-260, code_excluded_logical_range :262-274, code_physical_spans :276-316,
+_stage_codes :369-400, _finish_block :419-465, _compact_response_content :467-557, _mask_or_raise :648-661,
+_check_stop :663-685; the physical exclusion ranges of a code step restate sched/scheduler.py:979-991. The compaction
+callback ``mask_span(request_id, start, end, groups=None)`` is KVPlanner.mask_token_span.
 """
 from __future__ import annotations
 
@@ -45,6 +46,8 @@ class CompressLMBlock:
     prompt_content_positions: list[int] = field(default_factory=list)
     response_content_positions: list[int] = field(default_factory=list)
     code_span: tuple[int, int] | None = None
+    retained_tail_positions: list[int] = field(default_factory=list)
+    code_excluded_content_span: tuple[int, int] | None = None
 
 
 @dataclass
@@ -277,6 +280,35 @@ class CompressLMProcessor:
     def reset_for_preemption(self, state: CompressLMState) -> None:
         state.reset_compaction_progress()
 
+    def code_excluded_logical_range(self, request) -> tuple[int, int] | None:
+        """Logical [start, end) of the current block's content rows its own codes must not see (the static tail),
+        or None without a tail."""
+        if not self.config.code_excluded_tail:
+            return None
+        state = request.compresslm_state
+        if state is None:
+            raise RuntimeError("CompressLM request has no state")
+        block = state.current_block
+        if block.code_excluded_content_span is None:
+            raise RuntimeError("tail-exclusive code block has no source span")
+        return block.code_excluded_content_span
+
+    def code_excluded_physical_ranges(self, request, num_groups: int) -> list[tuple[int, int]] | None:
+        """Physical [start, end) of the excluded range in each KV-cache group's layout during the block's code step
+        (sched/scheduler.py:979-991), or None without a tail."""
+        logical = self.code_excluded_logical_range(request)
+        if logical is None:
+            return None
+        ls, le = logical
+        ranges = []
+        for g in range(num_groups):
+            ps = request.logical_to_physical(ls, g)
+            pe = request.logical_to_physical(le - 1, g) + 1
+            if pe - ps != self.config.code_excluded_tail:
+                raise RuntimeError("exact tail source is not contiguous after KV compaction")
+            ranges.append((ps, pe))
+        return ranges
+
     def code_physical_spans(self, request, group: int = 0, logical_limit: int | None = None):
         """Physical [start, end) of every staged code span still holding all K rows in ``group``'s layout."""
         state = request.compresslm_state
@@ -323,6 +355,13 @@ class CompressLMProcessor:
         ids = self.config.code_token_ids
         request.append_output_token_ids(ids)
         block.code_span = (start, request.num_tokens)
+        T = self.config.retain_tail_kv
+        if T:
+            block.retained_tail_positions = block.content_positions[-T:]
+            tail = block.content_positions[-self.config.code_excluded_tail:]
+            if tail != list(range(tail[0], tail[-1] + 1)):
+                raise RuntimeError("exact tail source positions must be contiguous")
+            block.code_excluded_content_span = (tail[0], tail[-1] + 1)
         state.roles.extend([CODE] * len(ids))
         state.position_to_block.extend([block.block_id] * len(ids))
         state.worker_token_ids_dirty = True
@@ -351,8 +390,12 @@ class CompressLMProcessor:
         ``groups`` None for every KV-cache group (compresslm/processor.py:467-557). Response content goes from every
         group, then (physical quotas) code slots [q, K) from the groups of each quota q < K, ascending q, each on the
         layout the previous removal left. Packed KV: the response content and the codes as one span (the codes are
-        archived into packed pages before it runs)."""
+        archived into packed pages before it runs). A static retained tail (the block's last T content rows) is never
+        removed: the response content before it goes, and with packed KV the codes go as a span of their own."""
         pos = block.response_content_positions
+        if self.config.retain_tail_kv:
+            kept = set(block.retained_tail_positions)
+            pos = [p for p in pos if p not in kept]
         if pos and pos[-1] - pos[0] + 1 != len(pos):
             raise RuntimeError("packed KV response content must be contiguous" if self.config.uses_packed_kv
                                else "CompressLM response content must be contiguous")
@@ -360,6 +403,8 @@ class CompressLMProcessor:
             if block.code_span is None:
                 raise RuntimeError("packed KV block has no completed code span")
             cs, ce = block.code_span
+            if self.config.retain_tail_kv:
+                return ([(pos[0], pos[-1] + 1, None)] if pos else []) + [(cs, ce, None)]
             if pos and pos[-1] + 1 != cs:
                 raise RuntimeError("packed KV response content and code span are not contiguous")
             return [(pos[0] if pos else cs, ce, None)]

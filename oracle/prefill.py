@@ -6,12 +6,17 @@ tokens, optional per-query-head code quota):
   causal & (own-block content | earlier blocks' codes | raw-prompt content)  |  (code query & code key & same block)
   and, with a quota, a code key is visible to head h only if its slot < quota[h].
 
+With a static retained tail of T rows (retain_tail_kv = T, policy "static"): the last T content rows of every earlier
+block are visible to every later query (causal), and a block's codes never see its own last T content rows.
+
 Two independent restatements of the reference are kept and cross-checked:
 * ``arith_mask``  -- closed-form integer arithmetic: abridgekv/compress_forward.py:695-727 (_arith_mask_mod) with
-                     the quota term of :725-726.
+                     the quota term of :725-726 and the static-tail terms of :714-715, :721-722.
 * ``role_mask``   -- role/block/content-position gathers: abridgekv/gen_compress.py:1062-1140 (_dense_mask, the
-                     reference's own dense oracle) restricted to L=1 and no tails, plus the quota rule of
-                     abridgekv/compress_forward.py:230-236 (_quota_key_allowed).
+                     reference's own dense oracle) restricted to L=1, no replay / raw tail, with its static
+                     ``retained_tail`` term (:1088-1094) and the own-tail exclusion of compress_forward.py:139-155
+                     (_code_content_tail_excluded), plus the quota rule of abridgekv/compress_forward.py:230-236
+                     (_quota_key_allowed).
 Pinning: the two agree element by element on every tested shape; brute-force per-element predicates written from
 the prose rule (tests/test_oracle_prefill.py); N=1 without codes reduces to the causal mask; masked_attention_fp64
 reduces to textbook causal attention under the causal mask and to per-row softmax identities (rows sum to one,
@@ -22,13 +27,13 @@ from __future__ import annotations
 import numpy as np
 
 
-def arith_mask(C, K, N, prompt_len=None, head_quota=None):
+def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0):
     """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
     S0 = N * (C + K)
-    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota)
+    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail)
 
 
-def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None):
+def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
     per = C + K
@@ -38,12 +43,17 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None):
     qw, kw = q - qb * per, kv - kb * per
     k_content = kw < C
     same_blk = kb == qb
+    T = int(retain_tail)
     vis = (k_content & same_blk) | ((~k_content) & (kb < qb))
+    if T:
+        vis = vis | (k_content & (kb < qb) & (kw >= C - T))                 # earlier blocks' static tails
     if prompt_len is not None:
         pl = np.asarray(prompt_len, dtype=np.int64).reshape(-1, 1, 1)
         vis = vis[None] | (k_content & (kb * C + kw < pl))[...]
     vis = (kv <= q) & vis
     vis = vis | ((qw >= C) & (~k_content) & same_blk)
+    if T:
+        vis = vis & ~((qw >= C) & same_blk & k_content & (kw >= C - T))    # codes never see their own tail
     if head_quota is not None:
         hq = np.asarray(head_quota, dtype=np.int64).reshape(-1, 1, 1)
         quota_ok = k_content | ((kw - C) < hq)                    # [H, 1, S0]
@@ -54,7 +64,7 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None):
     return vis
 
 
-def role_mask(C, K, N, prompt_len=None, head_quota=None):
+def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0):
     """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
     per = C + K
     S0 = N * per
@@ -70,11 +80,16 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None):
     earlier_final = (kr == 1) & (kb < qb)
     pause_q = qr == 1
     samepass = pause_q & (kr == qr) & (kb == qb)
-    base = (causal & (content_vis | earlier_final)) | samepass
+    T = int(retain_tail)
+    retained = (kr == 0) & (kb < qb) & (content_abs.reshape(1, S0) % C >= C - T) & (T > 0)
+    base = (causal & (content_vis | earlier_final | retained)) | samepass
     if prompt_len is not None:
         pl = np.asarray(prompt_len).reshape(-1, 1, 1)
         prompt_raw = (kr == 0)[None] & (content_abs.reshape(1, 1, S0) < pl) & (content_abs.reshape(1, 1, S0) >= 0)
         base = base[None] | (causal[None] & prompt_raw)
+    if T:
+        own_tail = pause_q & (kr == 0) & (kb == qb) & (content_abs.reshape(1, S0) % C >= C - T)
+        base = base & ~own_tail
     if head_quota is not None:
         hq = np.asarray(head_quota).reshape(-1, 1, 1)
         slot = code_slot.reshape(1, 1, S0)

@@ -8,7 +8,9 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:
   a CONTENT run up to its end), should_skip_sampling :153-168, update_after_step :170-257 (a full block stages
   its K codes and holds the sampled token), _stage_codes :369-400, _finish_block :419-465 (compact, then open the
   next block with the next prompt chunk or the held token), _compact_response_content :467-557 (response content
-  in every group, then code slots [q, K) per distinct quota q < K in ascending order).
+  in every group, then code slots [q, K) per distinct quota q < K in ascending order). With a static retained tail
+  (``retain_tail`` = T, compresslm.py:22-25) the block's last T content rows are never removed (:480-482): the
+  response content before them goes.
 
 The machine is planner-agnostic: it emits the scheduler-visible events (allocate ``n`` new tokens, then compact
 spans) and is shared by the oracle planner and the product planner so that both see identical event streams.
@@ -16,6 +18,9 @@ spans) and is shared by the oracle planner and the product planner so that both 
 Pinning: tests/test_oracle_trace.py checks the reference's invariants (scripts/test_compresslm_physical_quotas.py:
 68-138): every compacted block keeps exactly codes[:q_g] and no response content in group g; removed rows per
 group differ from group 0 by (K - q_g) per compacted block; and the closed form of oracle.layout.rows_per_layer.
+The static tail: tests/test_static_tail.py checks the kept rows against their closed form (prompt content, the last T
+content rows and q codes per closed block) and the reference's own static-tail scenarios through the product machine,
+which must issue this trace's calls.
 """
 from __future__ import annotations
 
@@ -36,10 +41,11 @@ class Block:
 class RequestTrace:
     """Logical token stream of one request and its block structure."""
 
-    def __init__(self, prompt_len, max_tokens, C, K, group_quotas):
+    def __init__(self, prompt_len, max_tokens, C, K, group_quotas, retain_tail=0):
         if prompt_len <= 0:
             raise ValueError("CompressLM decoding requires a non-empty prompt")
         self.C, self.K = C, K
+        self.T = retain_tail
         self.group_quotas = tuple(group_quotas)
         self.prompt_len = prompt_len
         self.max_tokens = max_tokens
@@ -133,7 +139,8 @@ class RequestTrace:
     def _finish_block(self, block):                # processor.py:419-465, :467-557
         calls = []
         if block.block_id not in self.compacted_block_ids:
-            pos = block.response_positions
+            tail = set(block.content_positions[-self.T:]) if self.T else set()
+            pos = [p for p in block.response_positions if p not in tail]
             if pos:
                 if pos != list(range(pos[0], pos[-1] + 1)):
                     raise RuntimeError("CompressLM response content must be contiguous")
@@ -163,8 +170,9 @@ class RequestTrace:
         keep = []
         for b in self.blocks:
             compacted = b.block_id in self.compacted_block_ids
+            tail = set(b.content_positions[-self.T:]) if self.T else set()
             for p in b.content_positions:
-                if p < self.num_computed_tokens and not (compacted and self.kind[p] == "response"):
+                if p < self.num_computed_tokens and not (compacted and self.kind[p] == "response" and p not in tail):
                     keep.append(p)
             if b.code_span:
                 cs, ce = b.code_span

@@ -12,9 +12,11 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
-    (code query & code key & same block); a code key with slot >= quota is hidden."""
+    (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
+    prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
+    all later queries (content and code rows), and the codes summarize only the first block_size - T tokens"."""
     per = C + K
     S = N * per
     m = np.zeros((S, S), bool)
@@ -26,9 +28,13 @@ def brute(C, K, N, prompt_len=None, quota=None):
             vis = (k_content and kb == qb) or ((not k_content) and kb < qb)
             if prompt_len is not None and k_content and kb * C + kw < prompt_len:
                 vis = True
+            if tail and k_content and kb < qb and kw >= C - tail:
+                vis = True                       # an earlier block's tail row: resident, seen by every later query
             vis = vis and k <= q
             if qw >= C and not k_content and kb == qb:
                 vis = True
+            if tail and qw >= C and k_content and kb == qb and kw >= C - tail:
+                vis = False                      # a code row does not summarize its own block's tail
             if quota is not None and not k_content and kw - C >= quota:
                 vis = False
             m[q, k] = vis
@@ -46,6 +52,35 @@ def test_arith_equals_role_equals_brute(C, K, N):
     assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl))
     for b, p in enumerate(pl):
         assert np.array_equal(ap[b], brute(C, K, N, prompt_len=p))
+
+
+@pytest.mark.parametrize("C,K,N,T", [(4, 2, 3, 2), (8, 4, 3, 3), (8, 2, 4, 1), (6, 4, 3, 2)])
+def test_static_tail_arith_equals_role_equals_brute(C, K, N, T):
+    a = op.arith_mask(C, K, N, retain_tail=T)
+    assert np.array_equal(a, op.role_mask(C, K, N, retain_tail=T))
+    assert np.array_equal(a, brute(C, K, N, tail=T))
+    assert not np.array_equal(a, op.arith_mask(C, K, N))                    # the tail changes the mask
+    pl = [0, 3, C + 1, N * C]
+    hq = [1, K, 2, K]
+    ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, retain_tail=T)
+    assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, retain_tail=T))
+    for b, p in enumerate(pl):
+        for h, q in enumerate(hq):
+            assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T))
+
+
+def test_static_tail_spot_checks():
+    """Block 1's content sees block 0's last T rows but not the rows before them; block 0's codes do not see its own
+    tail; a tail row inside the raw prompt is still hidden from its own block's codes."""
+    C, K, N, T = 8, 4, 3, 3
+    per = C + K
+    m = op.arith_mask(C, K, N, retain_tail=T)
+    assert m[per, C - T] and m[per, C - 1] and not m[per, C - T - 1]
+    assert m[2 * per + C, C - 1]                        # codes of a later block see earlier tails
+    assert m[C, 0] and m[C, C - T - 1] and not m[C, C - T] and not m[C, C - 1]
+    assert m[C - 1, C - T]                              # content sees its own block causally, tail included
+    mp = op.arith_mask(C, K, N, prompt_len=[2 * C], retain_tail=T)[0]
+    assert mp[per, 0] and not mp[C, C - 1] and not mp[per + C, per + C - 1]
 
 
 def test_head_quotas_compose_with_base_mask():
