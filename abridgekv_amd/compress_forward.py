@@ -2,15 +2,18 @@
 
 Mirrors the served subset of abridgekv/compress_forward.py:240-1230 (``CompressLM``): one pause pass (L=1) with
 bidirectional code<->code attention in a block (``pause_xattn="full"``), optional raw prompt, optional fixed
-per-(layer, KV head) code quotas, ``active_code_rows`` and ``appended`` / ``bitrev`` code positions. The sequence
+per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` / ``bitrev`` code positions and the static
+retained tail (``retain_tail_kv`` = T with ``retain_tail_policy="static"``: every earlier block's last T content rows
+stay visible, a block's codes do not see or summarize its own; bitrev codes spread over the first C - T). The sequence
 layout, RoPE positions, loss positions and loss reductions follow the reference (compress_forward.py:20-88,
 1044-1071, 957-1042, 1134-1230); the attention of every decoder layer runs ``abkv_prefill_masked_attn`` through a
 HuggingFace attention function registered as ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask
 (``_arith_mask_mod`` / ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 695-727,
 815-894). The mask is never materialised: the kernel evaluates it from (C, K, N, prompt_len, head quota).
 
-Options of the reference that belong to other experiments (replay / raw / retained tails, learned or segment
-pooling, query residuals, copy and distillation losses, external block masks) raise NotImplementedError. Gradients
+Options of the reference that belong to other experiments (replay / raw tails, the rolling / sticky window tails,
+learned or segment pooling, query residuals, copy and distillation losses, external block masks) raise
+NotImplementedError. Gradients
 flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module trains.
 """
 from __future__ import annotations
@@ -31,12 +34,14 @@ ATTN_IMPLEMENTATION = "abridgekv_hip"
 class CompressMask:
     """What the kernel needs to evaluate the compression mask (the analogue of the reference's BlockMask):
     N blocks of [C content | K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
-    ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K)."""
+    ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a static
+    retained tail (0: none)."""
     block_c: int
     codes_k: int
     num_blocks: int
     prompt_len: torch.Tensor | None = None
     head_quota: torch.Tensor | None = None
+    retain_tail: int = 0
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -53,7 +58,8 @@ class _MaskedPrefill(torch.autograd.Function):
                 raise NotImplementedError("the masked-prefill backward runs bf16 inputs")
             lse = torch.empty((q.shape[0], ops.HEADS_Q, q.shape[1]), dtype=torch.float32, device=q.device)
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
-                                              prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse)
+                                              prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
+                                              retain_tail=mask.retain_tail)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -66,7 +72,7 @@ class _MaskedPrefill(torch.autograd.Function):
         g = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
         dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, g, m.block_c, m.codes_k, m.num_blocks,
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
-                                                           scale=ctx.scale)
+                                                           scale=ctx.scale, retain_tail=m.retain_tail)
         return dq, dk, dv, None, None, None
 
 
@@ -107,16 +113,17 @@ def content_abs_pos(C: int, N: int, K: int, device=None) -> torch.Tensor:
     return torch.where(within < C, blk * C + within, torch.full_like(within, N * C))
 
 
-def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, device=None) -> torch.Tensor:
+def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, device=None,
+                      code_excluded_tail: int = 0) -> torch.Tensor:
     """(1, N*(C+K_act)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, L=1,
-    no replay tail, no copy rows)."""
+    no replay tail, no copy rows); bitrev code rows spread over the first C - code_excluded_tail in-block offsets."""
     per_full, per_act = C + K, C + K_act
     idx = torch.arange(N * per_act, device=device)
     within, blk = idx % per_act, idx // per_act
     is_code = within >= C
     p = (within - C).clamp_min(0)
     if code_positions == "bitrev":
-        offs = torch.from_numpy(bitrev_offsets(K, C)).to(device)
+        offs = torch.from_numpy(bitrev_offsets(K, C - code_excluded_tail)).to(device)
         pos = torch.where(is_code, blk * C + offs[p.clamp_max(K - 1)], blk * C + within)
     else:
         pos = torch.where(is_code, blk * per_full + C + p, blk * per_full + within)
@@ -124,7 +131,7 @@ def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, d
 
 
 _UNSUPPORTED = ("pool_init", "query_residual", "code_q_heads", "code_kv_heads", "seg_pool", "gated_seg_pool",
-                "raw_tail", "replay_tail", "code_exclude_replay_tail", "retain_tail_kv")
+                "raw_tail", "replay_tail", "code_exclude_replay_tail")
 
 
 class CompressLM(nn.Module):
@@ -136,7 +143,7 @@ class CompressLM(nn.Module):
     """
 
     def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", head_code_quotas=None, active_code_rows=None,
-                 code_positions="appended", retain_tail_policy="rolling", **options):
+                 code_positions="appended", retain_tail_kv=0, retain_tail_policy="rolling", **options):
         super().__init__()
         bad = sorted(name for name in options if name not in _UNSUPPORTED)
         if bad:
@@ -148,8 +155,14 @@ class CompressLM(nn.Module):
             raise NotImplementedError("only one pause pass (L=1) is supported")
         if pause_xattn != "full":
             raise NotImplementedError("only pause_xattn='full' (bidirectional codes) is supported")
-        if retain_tail_policy != "rolling":
+        if not 0 <= retain_tail_kv < C:
+            raise ValueError(f"retain_tail_kv must be in [0, C={C}), got {retain_tail_kv}")
+        if retain_tail_policy not in ("rolling", "sticky", "static"):
+            raise ValueError(f"retain_tail_policy must be 'rolling', 'sticky' or 'static', got {retain_tail_policy!r}")
+        if retain_tail_policy != "rolling" and not retain_tail_kv:
             raise ValueError(f"retain_tail_policy={retain_tail_policy!r} requires retain_tail_kv > 0")
+        if retain_tail_kv and retain_tail_policy != "static":
+            raise NotImplementedError("only the static retained tail is supported by the native forward")
         if code_positions not in ("appended", "bitrev"):
             raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
         if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1)):
@@ -165,7 +178,11 @@ class CompressLM(nn.Module):
         self.model.config._attn_implementation = ATTN_IMPLEMENTATION
         self.C, self.N, self.K, self.L = int(C), int(N), int(K), 1
         self.pause_xattn, self.code_positions = pause_xattn, code_positions
-        self.replay_tail = self.raw_tail = self.retain_tail_kv = self.code_excluded_tail = 0
+        self.replay_tail = self.raw_tail = 0
+        self.retain_tail_kv = self.code_excluded_tail = int(retain_tail_kv)
+        self.retain_tail_policy = retain_tail_policy
+        if code_positions == "bitrev" and C - self.code_excluded_tail < K:
+            raise ValueError(f"bitrev code span {C - self.code_excluded_tail} < num_code_tokens {K}")
         self.K_act = int(active_code_rows) if active_code_rows else self.K
         if not 1 <= self.K_act <= self.K:
             raise ValueError(f"active_code_rows must be in [1, K={K}], got {active_code_rows}")
@@ -188,7 +205,8 @@ class CompressLM(nn.Module):
         layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev),
                   "loss_pos": content & torch.roll(content, -1), "content_pos": content.nonzero(as_tuple=True)[0],
                   "predict_flat": pf, "predict_block": pf // C,
-                  "_pos_ids": rope_position_ids(C, N, self.K, Ka, self.code_positions, dev)}
+                  "_pos_ids": rope_position_ids(C, N, self.K, Ka, self.code_positions, dev,
+                                                self.code_excluded_tail)}
         for name, value in layout.items():
             self.register_buffer(name, value, persistent=False)
 
@@ -234,7 +252,7 @@ class CompressLM(nn.Module):
             prompt_len = prompt_len.to(device=self.pause.device, dtype=torch.int32).contiguous()
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
-        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32)
+        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv)
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:

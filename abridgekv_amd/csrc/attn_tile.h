@@ -12,19 +12,24 @@ constexpr int kBM = 64;                  // query rows per workgroup
 constexpr int kBN = 64;                  // keys per tile
 constexpr int kTileElems = kBN * kHeadDim;
 
-// Per-element visibility for layouts whose tiles cannot be classified (unaligned masked prefill); other kernels
-// never call it (their tiles are always aligned: kAligned = true). quota[u]: code slots visible to this wave's head u.
+// Per-element visibility for layouts whose tiles cannot be classified (unaligned masked prefill, or any layout with a
+// static retained tail); other kernels never call it (their tiles are always aligned: kAligned = true). quota[u]:
+// code slots visible to this wave's head u; tail: the static retained tail T (the last T content rows of an earlier
+// block are visible to every later row; a block's codes never see its own last T content rows).
 struct MaskGeom {
   int qrow, S0, C, per, plen;
   int quota[2];
+  int tail;
   __device__ __forceinline__ bool visible(int kv, int u) const {
     if (kv >= S0 || qrow >= S0) return false;
     const int qb = qrow / per, kb = kv / per;
     const int qw = qrow - qb * per, kw = kv - kb * per;
     const bool kc = kw < C;
-    bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen);
+    const bool in_tail = kc && kw >= C - tail;
+    bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) || (in_tail && kb < qb);
     v = v && kv <= qrow;
     v = v || (qw >= C && !kc && kb == qb);
+    v = v && !(qw >= C && kb == qb && in_tail);
     return v && (kc || kw - C < quota[u]);
   }
 };

@@ -1,11 +1,13 @@
 // Block-masked teacher-forced attention (the compression mask) for gfx950.
 //
 // Replaces the FlexAttention call of CompressLM.forward (abridgekv/compress_forward.py:1134-1230) for the production
-// configuration (L=1, full code<->code attention, no replay / raw / retained tails), whose mask is the closed form
-// _arith_mask_mod (abridgekv/compress_forward.py:695-727) plus the per-query-head code quota (:725-726,
-// _quota_key_allowed :230-236). Sequence layout: N blocks of [C content | K codes], S0 = N * (C + K):
-//   visible(q, kv) = (kv <= q) & (own-block content | earlier blocks' codes | raw-prompt content)
-//                  | (code query & code key & same block),     and a code key needs slot < quota[head].
+// configuration (L=1, full code<->code attention, no replay / raw tail, an optional static retained tail), whose
+// mask is the closed form _arith_mask_mod (abridgekv/compress_forward.py:695-727) plus the per-query-head code quota
+// (:725-726, _quota_key_allowed :230-236). Sequence layout: N blocks of [C content | K codes], S0 = N * (C + K):
+//   visible(q, kv) = (kv <= q) & (own-block content | earlier blocks' codes | raw-prompt content
+//                                 | earlier blocks' last T content rows)
+//                  | (code query & code key & same block),     and a code key needs slot < quota[head];
+//   a code query never sees its own block's last T content rows (static retained tail T, :714-715, :721-722).
 //
 // Work decomposition: one workgroup of 8 waves per (sequence, KV head, 64-row query tile). A wave owns 16 query rows
 // for 2 of the 4 query heads of the KV head: 32 MFMA columns (column = head u x row), so one K operand feeds 2 heads
@@ -16,8 +18,8 @@
 //   it by > 8)
 //   O^T[128 dims x 32 cols] += V^T . P^T          2 key halves x 8 dim tiles x 2 heads; V^T by LDS transpose reads
 // Aligned layouts (C and K multiples of 64) walk only the visible tiles, jumping over hidden segments, and tag each
-// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit). Unaligned shapes run every tile of
-// the visible prefix with the mask evaluated per element (correct, slower).
+// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit). Unaligned shapes and layouts with a
+// retained tail run every tile of the visible prefix with the mask evaluated per element (correct, slower).
 #include "attn_tile.h"
 
 namespace abkv {
@@ -32,8 +34,9 @@ struct PrefillArgs {
   float scale_log2;
   __bf16* out;      long o_sb, o_ss, o_sh;   // [B, S0, 32, 128]
   float* lse;                                // [B, 32, S0] natural log, or nullptr
-  int aligned;                               // C % 64 == 0 && K % 64 == 0
+  int aligned;                               // C % 64 == 0 && K % 64 == 0 and no retained tail
   int num_q_tiles;
+  int tail;                                  // static retained tail T (0: none)
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
                        a.k_ss, a.v_ss};
   // this wave's heads hbase, hbase + 1 (hbase is 0 or 2): quotas by selection, not by a computed index
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
-  const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}};
+  const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}, a.tail};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
   TileWalk<kAligned> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1);
@@ -290,15 +293,17 @@ __device__ __forceinline__ void pack_tile_op(const floatx4 (&x)[2][2][H], bf16x8
 }
 
 // Visibility of key kv to query row q under the compression mask (the per-element predicate of MaskGeom::visible
-// with the query as an argument), for unaligned layouts.
-__device__ __forceinline__ bool elem_visible(int q, int kv, int S0, int C, int per, int plen, int quota) {
+// with the query as an argument), for unaligned layouts and layouts with a static retained tail.
+__device__ __forceinline__ bool elem_visible(int q, int kv, int S0, int C, int per, int plen, int quota, int tail) {
   if (kv >= S0 || q >= S0) return false;
   const int qb = q / per, kb = kv / per;
   const int qw = q - qb * per, kw = kv - kb * per;
   const bool kc = kw < C;
-  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen);
+  const bool in_tail = kc && kw >= C - tail;
+  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) || (in_tail && kb < qb);
   v = v && kv <= q;
   v = v || (qw >= C && !kc && kb == qb);
+  v = v && !(qw >= C && kb == qb && in_tail);
   return v && (kc || kw - C < quota);
 }
 
@@ -365,7 +370,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const DenseRows<kAligned> rows{f.k + (long)b * f.k_sb + (long)kvh * f.k_sh, f.v + (long)b * f.v_sb + (long)kvh * f.v_sh,
                                  f.k_ss, f.v_ss};
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
-  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}};
+  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail};
   const int q_last = min(q0 + kBM, f.S0) - 1;
   TileWalk<kAligned> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1);
 
@@ -629,7 +634,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
             for (int r = 0; r < 4; ++r) {
               const int qrow = cq * kBN + r0 + r;
               // diagonal tiles: key <= row; bounded (mode 2) and unaligned tiles: the per-element predicate
-              const bool vis = cmode == 1 ? key <= qrow : elem_visible(qrow, key, f.S0, f.C, per, plen, qh);
+              const bool vis = cmode == 1 ? key <= qrow : elem_visible(qrow, key, f.S0, f.C, per, plen, qh, f.tail);
               const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
               s[kk][t][0][r] = pr;
               dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
@@ -674,13 +679,13 @@ extern "C" {
 int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
-                             int seq_len, const int32_t* prompt_len, const int32_t* head_quota, float scale,
-                             void* out, long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
-                             hipStream_t stream) {
+                             int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
+                             float scale, void* out, long out_stride_b, long out_stride_s, long out_stride_h,
+                             float* lse, hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
-      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k))
+      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c)
     return (int)hipErrorInvalidValue;
   PrefillArgs a;
   a.q = static_cast<const __bf16*>(q);
@@ -696,7 +701,8 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.out = static_cast<__bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;
   a.lse = lse;
-  a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
+  a.tail = retain_tail;
+  a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && retain_tail == 0;
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
   // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).
@@ -721,7 +727,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long out_stride_s, long out_stride_h, const void* dout, long dout_stride_b,
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, float scale, void* dq, long dq_stride_b,
+                                 const int32_t* head_quota, int retain_tail, float scale, void* dq, long dq_stride_b,
                                  long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b, long dk_stride_s,
                                  long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s, long dv_stride_h,
                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -729,7 +735,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || dout == nullptr || lse == nullptr ||
       dq == nullptr || dk == nullptr || dv == nullptr || block_c <= 0 || codes_k <= 0 || num_blocks <= 0 ||
-      seq_len != num_blocks * (block_c + codes_k))
+      seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c)
     return (int)hipErrorInvalidValue;
   if (workspace == nullptr || workspace_bytes < abkv_prefill_masked_bwd_workspace_size(batch, seq_len))
     return (int)hipErrorInvalidValue;
@@ -747,7 +753,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.scale_log2 = scale * 1.4426950408889634f;
   f.out = nullptr; f.o_sb = f.o_ss = f.o_sh = 0;
   f.lse = nullptr;
-  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
+  f.tail = retain_tail;
+  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && retain_tail == 0;
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;

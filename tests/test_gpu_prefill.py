@@ -14,7 +14,7 @@ def _bf16(x):
     return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0):
     from abridgekv_amd import ops
     S0 = N * (C + K)
     g = torch.Generator().manual_seed(seed)
@@ -26,13 +26,13 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None):
     hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
-                                          lse=lse)
+                                          lse=lse, retain_tail=tail)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota)
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -66,6 +66,25 @@ def test_config4_shape_sampled_rows():
     """Config-4 block geometry (C=512, K=128) with 4 blocks; rows sampled across blocks and regions."""
     rows = np.r_[0:70, 500:700, 1250:1300, 2400:2560]
     _check(C=512, K=128, N=4, B=1, prompt_len=[512], rows=rows, seed=4)
+
+
+def test_static_tail_aligned_blocks():
+    """Static retained tail T=32 on 64-aligned blocks (the tail forces the per-element mask path): earlier blocks'
+    last 32 content rows visible to every later row, hidden from their own block's codes; raw prompt and quotas."""
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=4, B=2, prompt_len=[100, 0], head_quota=quota, seed=6, tail=32)
+
+
+def test_static_tail_unaligned_blocks():
+    """C=8, K=4, T=3 with a partial last tile; a raw prompt that covers a tail."""
+    quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+    _check(C=8, K=4, N=5, B=2, prompt_len=[8, 13], head_quota=quota, seed=7, tail=3)
+
+
+def test_static_tail_served_block_geometry():
+    """C=512, K=128, T=64 (span 448 for the codes) with 4 blocks; rows sampled across blocks and regions."""
+    rows = np.r_[0:70, 440:520, 600:700, 1250:1300, 2400:2560]
+    _check(C=512, K=128, N=4, B=1, prompt_len=[512], rows=rows, seed=8, tail=64)
 
 
 def test_strided_hf_layout():

@@ -9,7 +9,7 @@ from oracle import prefill as op
 pytestmark = pytest.mark.gpu
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0):
     from abridgekv_amd import ops
     S0 = N * (C + K)
     g = torch.Generator().manual_seed(seed)
@@ -22,14 +22,15 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0):
     hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
     qd, kd, vd, gd = (t.to(dev) for t in (q, k, v, dout))
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
-    out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse)
+    out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse,
+                                          retain_tail=tail)
     dq, dk, dv = ops.prefill_masked_attention_backward(qd, kd, vd, out, lse, gd, C, K, N, prompt_len=pl,
-                                                       head_quota=hq)
+                                                       head_quota=hq, retain_tail=tail)
     torch.cuda.synchronize()
     got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
     worst = 0.0
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota)
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail)
         if prompt_len is not None:
             mask = mask[0]
         ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
@@ -61,6 +62,18 @@ def test_unaligned_small_blocks_partial_tiles():
     """C=40, K=12: the per-element mask path; S0=208 leaves a partial query and key tile."""
     quota = np.repeat([12, 3, 7, 12, 1, 5, 9, 12], 4).tolist()
     _check(C=40, K=12, N=4, B=2, prompt_len=[50, 0], head_quota=quota, seed=3)
+
+
+def test_static_tail_aligned_blocks():
+    """Static retained tail T=32 on 64-aligned blocks: the dK/dV pair walk must reach every later query tile of an
+    earlier block's tail keys, and a block's codes must give its own tail keys no gradient."""
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=5, tail=32)
+
+
+def test_static_tail_unaligned_blocks():
+    quota = np.repeat([12, 3, 7, 12, 1, 5, 9, 12], 4).tolist()
+    _check(C=40, K=12, N=4, B=1, prompt_len=[45], head_quota=quota, seed=6, tail=7)
 
 
 def test_autograd_through_hf_attention_layout():
