@@ -30,11 +30,11 @@ SIGNATURES = {
     "abkv_kv_append": (C.c_int, [_vp, C.c_long, _vp, C.c_long, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_long,
                                  C.c_int, C.c_int, _vp]),
     "abkv_rope_kv_append": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_long, _vp, C.c_long, _vp, C.c_int, C.c_int,
-                                      C.c_int, _vp, C.c_long, _vp, _vp, C.c_int, _vp]),
+                                      C.c_int, C.c_int, _vp, C.c_long, _vp, _vp, C.c_int, _vp]),
     "abkv_decode_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, _vp, C.c_int, C.c_int,
                                        C.c_float, _vp, C.c_long, C.c_long, _vp, _vp]),
     "abkv_paged_prefill_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp,
-                                              _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long,
+                                              _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long,
                                               C.c_long, _vp, _vp]),
     "abkv_prefill_masked_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
                                                _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -52,8 +52,8 @@ SIGNATURES = {
                                      + [_vp, C.c_long, C.c_long, C.c_long] * 3 + [_vp, C.c_size_t, _vp]),
     "abkv_paged_prefill_workspace_size": (C.c_size_t, [C.c_int, C.c_int]),
     "abkv_paged_prefill_attn": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp, _vp,
-                                          _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long, C.c_long,
-                                          _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
+                                          _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_float, _vp, C.c_long,
+                                          C.c_long, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp]),
     "abkv_packed_capture": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_long, C.c_int, _vp,
                                       _vp, C.c_int, _vp]),
     "abkv_decode_side_split_rows": (C.c_int, [C.c_int]),
@@ -62,7 +62,7 @@ SIGNATURES = {
                                           C.c_int, _vp, C.c_int, C.c_int, _i32p, _vp, C.c_long, _vp, C.c_int, C.c_int,
                                           C.c_float, _vp, C.c_long, C.c_long, _vp, _vp, C.c_size_t, _vp]),
     "abkv_paged_prefill_attn_packed": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp,
-                                                 _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _vp, _vp, C.c_int,
+                                                 _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _vp, _vp, C.c_int,
                                                  C.c_int, _i32p, _vp, C.c_long, _vp, C.c_int, C.c_float, _vp,
                                                  C.c_long, C.c_long, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
                                                  C.c_int, _vp, C.c_size_t, _vp]),

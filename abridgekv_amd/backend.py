@@ -15,7 +15,8 @@ reorder FlashInfer applies with decode threshold 1) and then multi-token request
 * prompt chunks -> ``abkv_paged_prefill_attn`` causal;
 * CompressLM code-step requests -> ``abkv_paged_prefill_attn`` non-causal with the key limit
   ``code_start + quota``: the physical-quota code mask of gpu_model_runner.py:2042-2107 (all resident rows, the
-  block's own code slots ``>= quota`` hidden; compresslm_masks.py:165-239) expressed as a per-request limit.
+  block's own code slots ``>= quota`` hidden; compresslm_masks.py:165-239) expressed as a per-request limit, and with
+  a static retained tail the block's own tail rows hidden as a per-request excluded range (:2086-2094).
 
 New K/V rows are written by ``abkv_kv_append`` (``torch.ops.abridgekv.kv_append``) before attention
 (``reshape_and_cache`` semantics: slot < 0 skips).
@@ -40,7 +41,9 @@ class AbridgeAttentionMetadata:
     ``query_start_loc`` [B+1] and ``seq_lens`` [B] (physical rows of the group after this step's tokens) are host
     int arrays; ``block_table`` [B, W] int32, ``slot_mapping`` [T] int64 and ``seq_lens_dev`` [B] int32 live on the
     GPU. ``code_key_limit`` [B] holds, for a code-step request, the physical key limit (code start + the group's
-    quota) and ``NOT_CODE`` for every other request. ``num_decodes`` leading requests have one query token.
+    quota) and ``NOT_CODE`` for every other request; ``code_excluded`` [B, 2] the physical rows a code-step request
+    must not see (its block's static tail; an empty range otherwise), or None. ``num_decodes`` leading requests have
+    one query token.
     """
     query_start_loc: np.ndarray
     seq_lens: np.ndarray
@@ -53,6 +56,7 @@ class AbridgeAttentionMetadata:
     workspace: torch.Tensor | None = None
     causal: bool = True
     split_pages: int = ops.DEFAULT_SPLIT_PAGES
+    code_excluded: np.ndarray | None = None
 
     @property
     def num_reqs(self) -> int:
@@ -92,13 +96,37 @@ def code_step_key_limits(query_start_loc, seq_lens, code_spans, group_quota: int
     return out
 
 
-def limits_from_custom_mask(mask: torch.Tensor, query_start_loc, seq_lens) -> tuple[np.ndarray, np.ndarray]:
-    """Turn a flat custom mask of the reference's format (row-major per-request ``q_len x seq_len`` blocks,
-    compresslm_masks.py:165-239) into per-request ``(key_limit, causal)``.
+def code_step_excluded_ranges(code_spans, excluded_ranges, query_start_loc, seq_lens) -> np.ndarray | None:
+    """Per-request excluded key ranges [B, 2] of a code step in one group (the block's own static retained tail,
+    ``CompressLMProcessor.code_excluded_physical_ranges`` of the group), checked as the worker checks them
+    (gpu_model_runner.py:2086-2091: ``0 <= start < end <= seq_len - query_len``); None when no request has one."""
+    qsl = np.asarray(query_start_loc, dtype=np.int64)
+    sl = np.asarray(seq_lens, dtype=np.int64)
+    out = np.zeros((sl.size, 2), dtype=np.int64)
+    any_range = False
+    for r, ex in enumerate(excluded_ranges):
+        if ex is None:
+            continue
+        if code_spans[r] is None:
+            raise RuntimeError(f"request {r} has an excluded range but is not coding")
+        start, end = int(ex[0]), int(ex[1])
+        if not 0 <= start < end <= sl[r] - (qsl[r + 1] - qsl[r]):
+            raise RuntimeError(f"invalid CompressLM code exclusion range {(start, end)} for "
+                               f"query_len={int(qsl[r + 1] - qsl[r])}, seq_len={int(sl[r])}")
+        out[r] = (start, end)
+        any_range = True
+    return out if any_range else None
 
-    Accepts exactly the masks this backend can run: per request, either every query row sees a prefix ``[0, L)``
-    with the same L (a code step) or row i sees ``[0, seq_len - q_len + i]`` (a causal chunk). Any other mask raises
-    ``RuntimeError``: the kernels keep no dense mask.
+
+def key_ranges_from_custom_mask(mask: torch.Tensor, query_start_loc, seq_lens):
+    """Turn a flat custom mask of the reference's format (row-major per-request ``q_len x seq_len`` blocks,
+    compresslm_masks.py:165-239) into per-request ``(key_limit, causal, excluded)``.
+
+    Accepts exactly the masks this backend can run: per request, either every query row sees the same set
+    ``[0, L)`` minus at most one contiguous range ``[a, b)`` inside it (a code step; the range is its block's static
+    tail) or row i sees ``[0, seq_len - q_len + i]`` (a causal chunk). ``excluded`` is None when no request hides a
+    range, else [B, 2] (an empty range for the others). Any other mask raises ``RuntimeError``: the kernels keep no
+    dense mask.
     """
     m = mask.detach().to("cpu", torch.bool).numpy().reshape(-1)
     qsl = np.asarray(query_start_loc, dtype=np.int64)
@@ -106,6 +134,7 @@ def limits_from_custom_mask(mask: torch.Tensor, query_start_loc, seq_lens) -> tu
     B = sl.size
     limits = np.zeros(B, dtype=np.int64)
     causal = np.zeros(B, dtype=bool)
+    excluded = np.zeros((B, 2), dtype=np.int64)
     at = 0
     for r in range(B):
         q_len, s_len = int(qsl[r + 1] - qsl[r]), int(sl[r])
@@ -117,18 +146,36 @@ def limits_from_custom_mask(mask: torch.Tensor, query_start_loc, seq_lens) -> tu
             limits[r] = s_len
             continue
         block = block.reshape(q_len, s_len)
-        counts = block.sum(axis=1)
         col = np.arange(s_len)
+        if np.all(block == block[0]):
+            row = block[0]
+            lim = int(np.flatnonzero(row)[-1]) + 1 if row.any() else 0
+            gap = np.flatnonzero(~row[:lim])
+            if gap.size and gap[-1] - gap[0] + 1 != gap.size:
+                raise RuntimeError(f"custom mask of request {r} hides more than one key range")
+            limits[r] = lim
+            if gap.size:
+                excluded[r] = (gap[0], gap[-1] + 1)
+            continue
+        counts = block.sum(axis=1)
         if not np.array_equal(block, col[None, :] < counts[:, None]):
             raise RuntimeError(f"custom mask of request {r} is not a per-row key prefix")
-        if np.all(counts == counts[0]):
-            limits[r] = counts[0]
-        elif np.array_equal(counts, s_len - q_len + 1 + np.arange(q_len)):
+        if np.array_equal(counts, s_len - q_len + 1 + np.arange(q_len)):
             limits[r], causal[r] = s_len, True
         else:
             raise RuntimeError(f"custom mask of request {r} is neither a shared key limit nor causal")
     if at != m.size:
         raise RuntimeError("custom mask is longer than sum(q_len * seq_len)")
+    return limits, causal, (excluded if excluded[:, 1].any() else None)
+
+
+def limits_from_custom_mask(mask: torch.Tensor, query_start_loc, seq_lens) -> tuple[np.ndarray, np.ndarray]:
+    """:func:`key_ranges_from_custom_mask` for masks without an excluded range: per-request ``(key_limit, causal)``;
+    a mask that hides a range inside a request's keys raises ``RuntimeError``."""
+    limits, causal, excluded = key_ranges_from_custom_mask(mask, query_start_loc, seq_lens)
+    if excluded is not None:
+        r = int(np.flatnonzero(excluded[:, 1])[0])
+        raise RuntimeError(f"custom mask of request {r} is not a per-row key prefix")
     return limits, causal
 
 
@@ -150,11 +197,12 @@ class AbridgeMetadataBuilder:
 
     def build(self, query_start_loc, seq_lens, block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
               code_key_limit=None, seq_lens_dev: torch.Tensor | None = None, positions: torch.Tensor | None = None,
-              compacted: torch.Tensor | None = None) -> AbridgeAttentionMetadata:
+              compacted: torch.Tensor | None = None, code_excluded=None) -> AbridgeAttentionMetadata:
         """One group's metadata of a step. ``slot_mapping`` [T] int64 (device), or None to compute it on the device
         from ``positions`` [T] int64 (the tokens' logical positions) and ``compacted`` [B] int32 (tokens the group
         removed per request): slot = table[r][p // 16] * 16 + p % 16 with p = position - compacted[r]
-        (gpu_model_runner.py:1579-1661, block_table.py:186-197)."""
+        (gpu_model_runner.py:1579-1661, block_table.py:186-197). ``code_excluded``: None, or [B, 2] physical key
+        ranges the code-step requests must not see (:func:`code_step_excluded_ranges`)."""
         qsl = np.asarray(query_start_loc, dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64)
         B = sl.size
@@ -177,6 +225,15 @@ class AbridgeMetadataBuilder:
         code = limits != NOT_CODE
         if np.any(code & ((limits < sl - qlen) | (limits > sl))):
             raise RuntimeError("code key limit must lie within the request's own query rows")
+        if code_excluded is not None:
+            code_excluded = np.asarray(code_excluded, dtype=np.int64).reshape(B, 2)
+            has = code_excluded[:, 1] > code_excluded[:, 0]
+            if np.any(has & ~code):
+                raise RuntimeError("only code-step requests may carry an excluded key range")
+            if np.any(has & ((code_excluded[:, 0] < 0) | (code_excluded[:, 1] > sl - qlen))):
+                raise RuntimeError("an excluded key range must lie before the request's own query rows")
+            if not has.any():
+                code_excluded = None
         max_pages = int(-(-sl[:nd].max() // ops.PAGE)) if nd else 0
         if max_pages > self.max_pages:
             raise RuntimeError(f"decode needs {max_pages} pages > max_pages={self.max_pages}")
@@ -189,7 +246,8 @@ class AbridgeMetadataBuilder:
             slot_mapping = ops.slot_mapping(req_idx, positions, block_table, compacted=compacted)
         return AbridgeAttentionMetadata(query_start_loc=qsl, seq_lens=sl, block_table=block_table,
                                         slot_mapping=slot_mapping, seq_lens_dev=seq_lens_dev, num_decodes=nd,
-                                        code_key_limit=limits, max_decode_pages=max(max_pages, 1),
+                                        code_key_limit=limits, code_excluded=code_excluded,
+                                        max_decode_pages=max(max_pages, 1),
                                         workspace=self.workspace() if nd else None,
                                         split_pages=self.split_pages or (ops.auto_split_pages(sl[:nd]) if nd
                                                                          else ops.DEFAULT_SPLIT_PAGES))
@@ -242,9 +300,12 @@ class AbridgeAttentionImpl:
             qlen = np.diff(qsl)
             lim = md.code_key_limit[nd:]
             code = lim != NOT_CODE
+            ex = None if md.code_excluded is None else [tuple(e) if e[1] > e[0] else None
+                                                         for e in md.code_excluded[nd:]]
             ops.paged_prefill_attention(q[nd_tok:n_tok], kv_cache, md.block_table[nd:], qsl, sl - qlen,
                                         np.where(code, lim, sl), md.causal & ~code, self.scale,
-                                        out=out[nd_tok:n_tok], lse=None if lse is None else lse[nd_tok:n_tok])
+                                        out=out[nd_tok:n_tok], lse=None if lse is None else lse[nd_tok:n_tok],
+                                        excluded=ex)
 
 
 class AbridgeAttentionBackend:

@@ -31,6 +31,7 @@ struct F32Args {
   const int32_t* q_start;      // [B + 1]
   const int32_t* kv_start;     // [B]
   const int32_t* kv_limit;     // [B]
+  const int32_t* kv_excluded;  // [B][2] physical [start, end) hidden from the request, or nullptr
   const int32_t* causal;       // [B] or nullptr (causal_default)
   int causal_default;
   // mode 2
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
   if (t >= a.num_tokens) return;                      // whole wave exits together; no block barrier below
 
   // Which keys, and how a key row is addressed.
-  int b = 0, qrow = 0, n_keys = 0, lim_lane = 0, plen = 0;
+  int b = 0, qrow = 0, n_keys = 0, lim_lane = 0, plen = 0, ex_lo = 0, ex_hi = 0;
   const int32_t* table = nullptr;
   int quota[kGroup] = {1 << 30, 1 << 30, 1 << 30, 1 << 30};
   if (a.mode == 1) {
@@ -105,6 +106,10 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
     const bool causal = a.causal ? a.causal[b] != 0 : a.causal_default != 0;
     n_keys = min(causal ? min(limit, pos + 1) : limit, a.bt_width * kPage);
     table = a.block_table + (long)b * a.bt_stride;
+    if (a.kv_excluded != nullptr) {
+      ex_lo = a.kv_excluded[2 * b];
+      ex_hi = a.kv_excluded[2 * b + 1];
+    }
   } else {
     b = t;
     n_keys = max(min(a.seq_lens[b], a.max_pages * kPage), 0);
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
     bool vis[kGroup];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
-      vis[u] = j < lim_lane && (a.mode != 1 || f32_visible(a, qrow, j, plen, quota[u]));
+      vis[u] = j < lim_lane && (j < ex_lo || j >= ex_hi) && (a.mode != 1 || f32_visible(a, qrow, j, plen, quota[u]));
       s[u] = -INFINITY;
     }
     if (vis[0] || vis[1] || vis[2] || vis[3]) {
@@ -262,9 +267,9 @@ int abkv_decode_attn_f32(const float* q, long q_stride_seq, long q_stride_head, 
 int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h, const float* kv_cache, int num_pages,
                                 const int32_t* block_table, long block_table_stride, int block_table_width,
                                 const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
-                                const int32_t* tok_req, int num_tokens, const int32_t* causal, int causal_default,
-                                float scale, float* out, long out_stride_t, long out_stride_h, float* lse,
-                                hipStream_t stream) {
+                                const int32_t* kv_excluded, const int32_t* tok_req, int num_tokens,
+                                const int32_t* causal, int causal_default, float scale, float* out, long out_stride_t,
+                                long out_stride_h, float* lse, hipStream_t stream) {
   using namespace abkv;
   if (num_tokens <= 0) return 0;
   if (q == nullptr || kv_cache == nullptr || block_table == nullptr || q_start == nullptr || kv_start == nullptr ||
@@ -283,6 +288,7 @@ int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h
   a.q_start = q_start;
   a.kv_start = kv_start;
   a.kv_limit = kv_limit;
+  a.kv_excluded = kv_excluded;
   a.tok_req = tok_req;
   a.causal = causal;
   a.causal_default = causal_default;

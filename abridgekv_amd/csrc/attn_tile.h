@@ -134,7 +134,8 @@ __device__ __forceinline__ void store_bf16x8(__bf16* dst, const floatx4& lo, con
 }
 
 struct TileMask {
-  int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[u] (this wave's head u), 3 per-element mask
+  int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[u] (this wave's head u), 3 per-element mask,
+                   // 4 key < this lane's limit and outside the excluded range [limit[0], limit[1])
   int limit[2];
 };
 
@@ -199,11 +200,27 @@ __device__ __forceinline__ void tile_scores(const __bf16* Kbuf, const bf16x8 (&q
 }
 
 // Hidden keys of a partial tile get score -inf (tm.mode 0: nothing hidden).
-template <int H, bool kAligned>
+template <int H, bool kAligned, bool kHole = false>
 __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const TileMask& tm, int lane_limit,
                                           const MaskGeom& geo, int j) {
   static_assert(H <= 2, "TileMask holds two per-head limits");
   if (tm.mode == 0) return;
+  if constexpr (kHole) {
+    if (tm.mode == 4) {                                  // a walk with an excluded key range (code step, static tail)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
+            const bool ok = kv < lane_limit && (kv < tm.limit[0] || kv >= tm.limit[1]);
+#pragma unroll
+            for (int u = 0; u < H; ++u) s[kk][t][u][r] = ok ? s[kk][t][u][r] : -INFINITY;
+          }
+      return;
+    }
+  }
   // every partial tile of an aligned layout is "key < lim[u]" with a per-column limit (per head or per lane)
   int lim[H];
 #pragma unroll
@@ -374,7 +391,7 @@ __device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n
     __builtin_amdgcn_s_barrier();
     issue_half<kWaves, false>(rows, src_k, n_keys, K[slot], w, lane);
     issue_half<kWaves, true>(rows, src_v, n_keys, V[slot2], w, lane);
-    tile_mask<H, kAligned>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
+    tile_mask<H, kAligned, Walk::kHole>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
     bf16x8 pop[2][H];
     tile_softmax<H>(s_cur, o, m_run, lsum, scale_log2, pop);
     // Unconditional so that the MFMAs can overlap the softmax work: after the last tile the scores are computed from

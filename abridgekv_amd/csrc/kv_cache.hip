@@ -227,7 +227,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const char* key, long k_
 // q[t] rotated in place, key[t] rotated in place and, with value[t], written to the cache at slot_mapping[t].
 // Replaces the model-side rotary op plus reshape_and_cache of the overlay's attention path, and computes the RoPE
 // position of an abridged-layout token on the device when block_c > 0 (logical position of period block_c +
-// codes_k -> block * block_c + (offset < block_c ? offset : bitrev code offset), config/compresslm.py:192-216).
+// codes_k -> block * block_c + (offset < block_c ? offset : bitrev code offset over the code span, block_c minus a
+// static retained tail), config/compresslm.py:192-216).
 struct RopeArgs {
   __bf16* q; long q_st, q_sh;                  // [T, 32, 128]
   __bf16* k; long k_st;                        // [T, 8, 128] (heads contiguous)
@@ -236,6 +237,7 @@ struct RopeArgs {
   const float* cos_sin;                        // [max_pos, 128]: cos of the 64 frequencies, then sin
   long max_pos;
   int block_c, codes_k, log2_k;                // block_c == 0: positions are RoPE positions already
+  int code_span;                               // code rows spread over in-block offsets [0, code_span)
   const int64_t* slot_mapping;                 // [T] or nullptr (rotate only); < 0 or past the cache = skip
   __bf16* cache; long num_pages;
 };
@@ -250,7 +252,7 @@ __device__ __forceinline__ long rope_position(const RopeArgs& a, long pos) {
     if (w >= a.block_c) {
       const unsigned k = (unsigned)(w - a.block_c);
       const unsigned rev = a.log2_k > 0 ? (__brev(k) >> (32 - a.log2_k)) : 0u;
-      off = ((long)rev * a.block_c) / a.codes_k;
+      off = ((long)rev * a.code_span) / a.codes_k;
     }
     pos = blk * a.block_c + off;
   }
@@ -462,16 +464,18 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
 
 int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, long key_stride_t, const void* value,
                         long value_stride_t, const int64_t* positions, int num_tokens, int block_c, int codes_k,
-                        const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
-                        int num_pages, hipStream_t stream) {
+                        int code_span, const float* cos_sin, long max_pos, const int64_t* slot_mapping,
+                        void* kv_cache, int num_pages, hipStream_t stream) {
   using namespace abkv;
   if (num_tokens <= 0) return 0;
   if (q == nullptr || key == nullptr || value == nullptr || positions == nullptr || cos_sin == nullptr ||
       max_pos <= 0 || block_c < 0 || (slot_mapping != nullptr && (kv_cache == nullptr || num_pages <= 0)))
     return (int)hipErrorInvalidValue;
   int log2_k = 0;
+  if (code_span == 0) code_span = block_c;
   if (block_c > 0) {
-    if (codes_k <= 0 || (codes_k & (codes_k - 1)) || codes_k > block_c)
+    if (codes_k <= 0 || (codes_k & (codes_k - 1)) || codes_k > block_c || code_span < codes_k ||
+        code_span > block_c)
       return (int)hipErrorInvalidValue;
     while ((1 << log2_k) < codes_k) ++log2_k;
   }
@@ -489,6 +493,7 @@ int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, lo
   a.block_c = block_c;
   a.codes_k = codes_k;
   a.log2_k = log2_k;
+  a.code_span = code_span;
   a.slot_mapping = slot_mapping;
   a.cache = static_cast<__bf16*>(kv_cache);
   a.num_pages = num_pages;

@@ -20,6 +20,7 @@ struct PagedPrefillArgs {
   const int32_t* q_start;                      // [B + 1] first query token of each request
   const int32_t* kv_start;                     // [B] physical position of each request's first query token
   const int32_t* kv_limit;                     // [B] visible keys: physical slots [0, kv_limit)
+  const int32_t* kv_excluded;                  // [B][2] physical [start, end) hidden from the request, or nullptr
   const int32_t* tile_req;                     // [n_tiles] request of each 64-row query tile
   const int32_t* tile_q0;                      // [n_tiles] first query row (within its request) of the tile
   const int32_t* causal;                       // [B] 1 = causal, 0 = non-causal (nullptr: causal_default)
@@ -65,12 +66,19 @@ struct PackedRows {
   }
 };
 
-// Contiguous key tiles [kt_begin, kt_end); tiles past k_full (the smallest lane limit) are masked per lane.
+// Contiguous key tiles [kt_begin, kt_end); tiles past k_full (the smallest lane limit) are masked per lane, and tiles
+// that meet the excluded key range [ex_lo, ex_hi) (empty when ex_lo >= ex_hi) mask it as well.
 struct RangeWalk {
-  int kt_begin, kt_end, k_full;
+  static constexpr bool kHole = true;
+  int kt_begin, kt_end, k_full, ex_lo, ex_hi;
   __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
     kt = first ? kt_begin : kt + 1;
     tm.mode = (kt + 1) * kBN <= k_full ? 0 : 1;
+    if (kt * kBN < ex_hi && (kt + 1) * kBN > ex_lo) {
+      tm.mode = 4;
+      tm.limit[0] = ex_lo;
+      tm.limit[1] = ex_hi;
+    }
     return kt < kt_end;
   }
 };
@@ -150,6 +158,11 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
   walk.kt_begin = a.split_tiles > 0 ? split * a.split_tiles : 0;
   walk.kt_end = a.split_tiles > 0 ? min(n_k_tiles, walk.kt_begin + a.split_tiles) : n_k_tiles;
   walk.k_full = k_full;
+  walk.ex_lo = walk.ex_hi = 0;
+  if (!kSide && a.kv_excluded != nullptr) {
+    walk.ex_lo = a.kv_excluded[2 * r];
+    walk.ex_hi = a.kv_excluded[2 * r + 1];
+  }
   if constexpr (kSide) {
     __shared__ int32_t side_table[kMaxSideTable];
     const int32_t* src = a.side_table + (long)r * a.side_stride;
@@ -247,7 +260,8 @@ size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits) {
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
                             const int32_t* block_table, long block_table_stride, int block_table_width,
                             const int32_t* q_start,
-                            const int32_t* kv_start, const int32_t* kv_limit, const int32_t* tile_req,
+                            const int32_t* kv_start, const int32_t* kv_limit, const int32_t* kv_excluded,
+                            const int32_t* tile_req,
                             const int32_t* tile_q0, int num_tiles, const int32_t* causal, int causal_default,
                             float scale, void* out,
                             long out_stride_t, long out_stride_h, float* lse, int num_tokens, int num_splits,
@@ -270,6 +284,7 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
   a.q_start = q_start;
   a.kv_start = kv_start;
   a.kv_limit = kv_limit;
+  a.kv_excluded = kv_excluded;
   a.tile_req = tile_req;
   a.tile_q0 = tile_q0;
   a.causal = causal;
@@ -306,7 +321,8 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
 int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache,
                                    int num_pages, const int32_t* block_table, long block_table_stride,
                                    int block_table_width, const int32_t* q_start, const int32_t* kv_start,
-                                   const int32_t* kv_limit, const int32_t* tile_req, const int32_t* tile_q0,
+                                   const int32_t* kv_limit, const int32_t* kv_excluded, const int32_t* tile_req,
+                                   const int32_t* tile_q0,
                                    int num_tiles, const int32_t* causal, int causal_default,
                                    const int32_t* head_quota_dev, const void* packed_kv, int packed_pool_pages,
                                    int packed_rows, const int32_t* head_quota, const int32_t* packed_table,
@@ -350,6 +366,7 @@ int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride
   a.q_start = q_start;
   a.kv_start = kv_start;
   a.kv_limit = kv_limit;
+  a.kv_excluded = kv_excluded;
   a.tile_req = tile_req;
   a.tile_q0 = tile_q0;
   a.causal = causal;

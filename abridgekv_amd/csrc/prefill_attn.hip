@@ -58,6 +58,7 @@ __device__ __forceinline__ GridPos grid_pos(int batch) {
 // Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
 template <bool kAligned>
 struct TileWalk {
+  static constexpr bool kHole = false;                      // never yields an excluded key range (mode 4)
   int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
   bool q_code;
   int kb, tw;

@@ -2,8 +2,9 @@
 
 Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``: ``feed_content``, ``compress``,
 ``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, bidirectional codes,
-raw prompt, per-layer code quotas, no tails). The reference keeps a dense per-layer store and masks it; here
-every layer's rows live in paged caches, quotas are physical, and the block boundary is a compaction:
+raw prompt, per-layer code quotas, no replay / raw tail, an optional static retained tail). The reference keeps a
+dense per-layer store and masks it; here every layer's rows live in paged caches, quotas are physical, and the block
+boundary is a compaction:
 
 * content chunks rotate q/k and append K/V at the group's next physical slots in one launch
   (``abkv_rope_kv_append``: the kernel maps the rows' logical positions to RoPE positions, and the slots come from
@@ -18,6 +19,9 @@ every layer's rows live in paged caches, quotas are physical, and the block boun
   moves the surviving rows with the HIP mover. The generator's API hands over the next token only after
   ``compress()``, so it runs the processor's block compaction directly rather than through ``update_after_step``
   (which needs that token to open the next block).
+* a static retained tail of T rows (``retain_tail_kv`` with ``retain_tail_policy="static"``): the block's last T
+  content rows are never removed, so every later row sees them as resident rows; the code step hides them from the
+  block's own codes (an excluded key range) and the bitrev code positions spread over the first C - T offsets.
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
@@ -84,8 +88,11 @@ class CompressGen:
             raise NotImplementedError("code rows always attend the current block's content on the paged path")
         if getattr(clm, "L", 1) != 1 or getattr(clm, "pause_xattn", "full") != "full":
             raise NotImplementedError("the paged path serves L=1 with bidirectional code attention")
-        if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail", "retain_tail_kv")):
-            raise NotImplementedError("the paged path serves no replay / raw / retained tails")
+        if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail")):
+            raise NotImplementedError("the paged path serves no replay / raw tails")
+        self.T = int(getattr(clm, "retain_tail_kv", 0) or 0)
+        if self.T and getattr(clm, "retain_tail_policy", "rolling") != "static":
+            raise NotImplementedError("the paged path serves the static retained tail only")
         self.clm = clm
         self.inner = clm.model.model
         self.layers = self.inner.layers
@@ -128,7 +135,8 @@ class CompressGen:
         # the block state machine's compaction rule for these groups (the serving validation of an enabled config --
         # bitrev positions, power-of-two sizes -- is the vLLM path's; the generator also runs appended positions)
         pcfg = CompressLMConfig(block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
-                                packed_kv_k_max=self.K)
+                                packed_kv_k_max=self.K, retain_tail_kv=self.T,
+                                retain_tail_policy="static" if self.T else "rolling")
         pcfg.set_code_token_ids(range(1 << 20, (1 << 20) + self.K))
         self.proc = CompressLMProcessor(pcfg)
         if not self.packed:
@@ -146,7 +154,7 @@ class CompressGen:
         self.f = 0                      # content tokens committed in the current block
         self.logical_len = 0            # tokens in the planner's logical sequence (content + code rows)
         self._cur_ids: list[int] = []
-        self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C)).to(self.device)
+        self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C - self.T)).to(self.device)
                               if self.code_positions == "bitrev" else None)
         # fp32 cos/sin of the model's rotary embedding for every position this sequence can reach (RoPE positions
         # never exceed logical positions); the fused kernel rotates q/k and appends K/V in one launch per layer
@@ -178,8 +186,10 @@ class CompressGen:
             seq_len = start + n
             table = torch.from_numpy(np.asarray(blocks[g], dtype=np.int32)).view(1, -1).to(self.device)
             limit = [start + min(q, self.K)] if code_step else None
+            # the block's own static tail: its last T content rows, just before the code rows in every group
+            excluded = [[start - self.T, start]] if code_step and self.T else None
             out.append(self.builder.build([0, n], [seq_len], table, code_key_limit=limit, positions=logical,
-                                          compacted=comp_dev[g:g + 1]))
+                                          compacted=comp_dev[g:g + 1], code_excluded=excluded))
         return out
 
     @torch.no_grad()
@@ -209,13 +219,15 @@ class CompressGen:
             k = k[0].to(self.dtype).contiguous()
             v = attn.v_proj(normed).view(n, -1, attn.head_dim).contiguous()
             ops.rope_kv_append(q, k, v, logical, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache,
-                               block_c=bc, codes_k=bk, max_position=last)
+                               block_c=bc, codes_k=bk, max_position=last, code_span=bc - self.T if bc else 0)
             o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
             if self.sidecar is not None:
                 # paged rows + this layer's per-head packed pages; a code step's paged keys stop at the block's
                 # first q_h code rows for KV head h
+                ex = None if md.code_excluded is None else [tuple(md.code_excluded[0])]
                 self.sidecar.attend(li, q, cache, md.block_table, md.query_start_loc, md.seq_lens, not code_step, o,
-                                    request_ids=(self.rid,), seq_lens_dev=md.seq_lens_dev, scale=self.impl.scale)
+                                    request_ids=(self.rid,), seq_lens_dev=md.seq_lens_dev, scale=self.impl.scale,
+                                    excluded=ex)
             else:
                 self.impl.attend(q, cache, md, o)
             h = hidden + attn.o_proj(o.view(1, n, -1))
@@ -250,7 +262,8 @@ class CompressGen:
         block = CompressLMBlock(self.b, content_positions=list(range(block_start, code_start)),
                                 prompt_content_positions=list(range(block_start, resp_from)),
                                 response_content_positions=list(range(resp_from, code_start)),
-                                code_span=(code_start, code_start + K))
+                                code_span=(code_start, code_start + K),
+                                retained_tail_positions=list(range(code_start - self.T, code_start)) if self.T else [])
         spans = self.proc.block_removal_spans(block)
         if self.sidecar is not None:
             # archive the code rows into packed pages before the span that removes them runs

@@ -326,11 +326,12 @@ def rope_bound(max_position: int, block_c: int = 0, codes_k: int = 0) -> int:
 def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, positions: torch.Tensor,
                    cos_sin: torch.Tensor, slot_mapping: torch.Tensor | None = None,
                    kv_cache: torch.Tensor | None = None, block_c: int = 0, codes_k: int = 0,
-                   max_position: int | None = None) -> None:
+                   max_position: int | None = None, code_span: int = 0) -> None:
     """Rotate q [T, 32, 128] and key [T, 8, 128] in place (NeoX halves) and write rotated key and value rows at
     slot_mapping (int64, < 0 = skip; None = rotate only). positions [T] int64: RoPE positions, or logical positions
     of the abridged layout when block_c > 0 (mapped to bitrev RoPE positions on the device; codes_k a power of two
-    <= block_c). ``max_position``: a host bound on ``positions`` (None: read back from the device, which
+    <= block_c; the code rows spread over in-block offsets [0, code_span), 0 meaning block_c, block_c - T with a
+    static retained tail). ``max_position``: a host bound on ``positions`` (None: read back from the device, which
     synchronises); the RoPE positions it implies must lie inside ``cos_sin`` (ValueError otherwise)."""
     T = positions.numel()
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
@@ -346,6 +347,7 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
     if block_c:
         _require(block_c > 0 and codes_k > 0 and codes_k & (codes_k - 1) == 0 and codes_k <= block_c,
                  "codes_k must be a power of two <= block_c")
+        _require(code_span == 0 or codes_k <= code_span <= block_c, "code_span must be 0 or in [codes_k, block_c]")
     num_pages = 0
     if slot_mapping is not None:
         _check_cache(kv_cache)
@@ -360,9 +362,9 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
              f"RoPE positions up to {rope_bound(max_position, block_c, codes_k)} exceed the cos/sin table "
              f"({cos_sin.shape[0]} rows)")
     rc = lib().abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(key), key.stride(0), _ptr(value),
-                                   value.stride(0), _ptr(positions), T, int(block_c), int(codes_k), _ptr(cos_sin),
-                                   cos_sin.shape[0], _ptr(slot_mapping), _ptr(kv_cache), num_pages,
-                                   C.c_void_p(_stream()))
+                                   value.stride(0), _ptr(positions), T, int(block_c), int(codes_k),
+                                   int(code_span), _ptr(cos_sin), cos_sin.shape[0], _ptr(slot_mapping),
+                                   _ptr(kv_cache), num_pages, C.c_void_p(_stream()))
     check(rc, "abkv_rope_kv_append")
 
 
@@ -518,9 +520,26 @@ def paged_split_plan(num_tiles: int, max_keys: int, target_blocks: int | None = 
     return -(-max_kt // split_tiles), split_tiles
 
 
+def _excluded_pairs(excluded, B):
+    """Per-request excluded key ranges as int32 [B, 2] (an empty range for None entries), or None for none at all."""
+    import numpy as np
+
+    if excluded is None:
+        return None
+    ex = list(excluded)
+    _require(len(ex) == B, "excluded: one (start, end) or None per request")
+    pairs = np.zeros((B, 2), dtype=np.int64)
+    for r, e in enumerate(ex):
+        if e is not None:
+            s, t = int(e[0]), int(e[1])
+            _require(0 <= s <= t, "excluded ranges must satisfy 0 <= start <= end")
+            pairs[r] = (s, t)
+    return pairs if pairs[:, 1].max(initial=0) > 0 else None
+
+
 def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, q_start, kv_start,
                             kv_limit, causal, scale: float | None = None, out: torch.Tensor | None = None,
-                            lse: torch.Tensor | None = None, split: int | None = None):
+                            lse: torch.Tensor | None = None, split: int | None = None, excluded=None):
     """Multi-query attention over the paged cache (prompt chunks: causal; CompressLM code step: non-causal with
     kv_limit = physical code start + quota).
 
@@ -528,7 +547,8 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     sequences (the metadata builder's CPU copies) -- request r's queries are tokens q_start[r]..q_start[r+1]-1 at
     physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
     ``causal``: a bool for the whole batch or one flag per request (code steps and prompt chunks may share a batch).
-    ``split``: key splits (None: chosen by :func:`paged_split_plan`; 1: no split).
+    ``excluded``: None, or per request a physical (start, end) its queries must not see (None: nothing), e.g. the
+    code step's own-block static tail. ``split``: key splits (None: chosen by :func:`paged_split_plan`; 1: no split).
     Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None). fp32 q and cache select the fp32 mode (out fp32).
     """
     import numpy as np
@@ -558,6 +578,8 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
         _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (T, HEADS_Q),
                  "lse must be contiguous fp32 [T, 32]")
     nq = np.diff(qs)
+    exd = _excluded_pairs(excluded, B)
+    ex_t = None if exd is None else torch.from_numpy(exd.astype(np.int32).reshape(-1)).to(q.device)
     if f32:
         if qs[-1] == 0:
             return out, lse
@@ -569,9 +591,9 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
         scale = default_scale() if scale is None else float(scale)
         rc = lib().abkv_paged_prefill_attn_f32(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                                _ptr(block_table), _row_stride(block_table), W, _ptr(meta[:o1]),
-                                               _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(meta[o4:]), int(qs[-1]),
-                                               _ptr(meta[o3:o4]), 1, scale, _ptr(out), out.stride(0), out.stride(1),
-                                               _ptr(lse), C.c_void_p(_stream()))
+                                               _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(ex_t), _ptr(meta[o4:]),
+                                               int(qs[-1]), _ptr(meta[o3:o4]), 1, scale, _ptr(out), out.stride(0),
+                                               out.stride(1), _ptr(lse), C.c_void_p(_stream()))
         check(rc, "abkv_paged_prefill_attn_f32")
         return out, lse
     tiles = [(r, q0) for r in range(B) for q0 in range(0, int(nq[r]), 64)]
@@ -599,7 +621,8 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     rc = lib().abkv_paged_prefill_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0],
                                        _ptr(block_table), _row_stride(block_table), W, _ptr(q_start_d),
-                                       _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(tl[0]), _ptr(tl[1]), len(tiles),
+                                       _ptr(kv_start_d), _ptr(kv_limit_d), _ptr(ex_t), _ptr(tl[0]), _ptr(tl[1]),
+                                       len(tiles),
                                        _ptr(causal_d), 1, scale, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
                                        covered, n_splits, split_tiles, _ptr(ws), ws_bytes, C.c_void_p(_stream()))
     check(rc, "abkv_paged_prefill_attn")
@@ -723,11 +746,12 @@ def paged_prefill_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, bloc
                                    kv_start, kv_limit, causal, packed_pool: torch.Tensor, head_quota,
                                    packed_table: torch.Tensor, packed_count: torch.Tensor, max_packed: int,
                                    scale: float | None = None, out: torch.Tensor | None = None,
-                                   lse: torch.Tensor | None = None, head_quota_dev: torch.Tensor | None = None):
+                                   lse: torch.Tensor | None = None, head_quota_dev: torch.Tensor | None = None,
+                                   excluded=None):
     """Multi-query attention over the paged rows plus each request's per-head packed code pages (visible to every
     query). As :func:`paged_prefill_attention`; a non-causal request (code step) sees paged keys
-    ``< min(kv_limit, kv_start + q_h)`` for KV head h. ``max_packed`` bounds packed_count (<= 2048).
-    Returns (out, lse).
+    ``< min(kv_limit, kv_start + q_h)`` for KV head h, except its ``excluded`` range. ``max_packed`` bounds
+    packed_count (<= 2048). Returns (out, lse).
     """
     import numpy as np
 
@@ -767,6 +791,8 @@ def paged_prefill_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, bloc
     tr = np.asarray(tiles, dtype=np.int32)
     cz = np.broadcast_to(np.asarray(causal, dtype=np.int64), (B,)).astype(np.int64)
     meta = torch.from_numpy(np.concatenate([qs, ks, kl, cz, hq]).astype(np.int32)).to(dev)
+    exd = _excluded_pairs(excluded, B)
+    ex_t = None if exd is None else torch.from_numpy(exd.astype(np.int32).reshape(-1)).to(dev)
     tl = torch.from_numpy(np.ascontiguousarray(tr.T)).to(dev)
     o1, o2, o3, o4 = B + 1, 2 * B + 1, 3 * B + 1, 4 * B + 1
     if head_quota_dev is None:
@@ -788,8 +814,8 @@ def paged_prefill_attention_packed(q: torch.Tensor, kv_cache: torch.Tensor, bloc
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     rc = lib().abkv_paged_prefill_attn_packed(
         _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.shape[0], _ptr(block_table),
-        _row_stride(block_table), W, _ptr(meta[:o1]), _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(tl[0]), _ptr(tl[1]),
-        len(tiles), _ptr(meta[o3:o4]), 1, _ptr(head_quota_dev), _ptr(packed_pool), packed_pool.shape[0], rows, hq_c,
+        _row_stride(block_table), W, _ptr(meta[:o1]), _ptr(meta[o1:o2]), _ptr(meta[o2:o3]), _ptr(ex_t), _ptr(tl[0]),
+        _ptr(tl[1]), len(tiles), _ptr(meta[o3:o4]), 1, _ptr(head_quota_dev), _ptr(packed_pool), packed_pool.shape[0], rows, hq_c,
         _ptr(packed_table), _row_stride(packed_table), _ptr(packed_count), max_packed, scale, _ptr(out),
         out.stride(0), out.stride(1), _ptr(lse), covered, n_splits, split_tiles, side_splits, side_split_tiles, _ptr(ws),
         ws_bytes, C.c_void_p(_stream()))

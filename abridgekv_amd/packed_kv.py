@@ -233,10 +233,13 @@ class PackedKVSidecar:
 
     def attend(self, layer_index: int, query: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
                query_start_loc, seq_lens, causal, output: torch.Tensor, request_ids=None,
-               seq_lens_dev: torch.Tensor | None = None, scale: float | None = None, lse=None) -> torch.Tensor:
+               seq_lens_dev: torch.Tensor | None = None, scale: float | None = None, lse=None,
+               excluded=None) -> torch.Tensor:
         """Attention of one layer for a batch of requests: paged rows (``block_table``, ``seq_lens`` physical rows
         after this step's tokens, host ``query_start_loc``) plus each request's packed side rows. ``causal``: one
-        flag for the batch or one per request (a non-causal request is a code step of exactly k_max queries)."""
+        flag for the batch or one per request (a non-causal request is a code step of exactly k_max queries).
+        ``excluded``: None or per request the physical paged rows a code step must not see (its block's static
+        tail, compresslm_packed_kv.py:725-729)."""
         rids = tuple(self.active_request_ids if request_ids is None else request_ids)
         qsl = np.asarray(query_start_loc, dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64)
@@ -268,7 +271,7 @@ class PackedKVSidecar:
         kv_start = sl - nq
         ops.paged_prefill_attention_packed(query[:T], kv_cache, block_table, qsl, kv_start, sl, cz, pool, quotas,
                                            table, count, max_packed, scale=scale, out=output[:T], lse=lse,
-                                           head_quota_dev=self._quota_dev[layer_index])
+                                           head_quota_dev=self._quota_dev[layer_index], excluded=excluded)
         return output
 
     def override_attention(self, *, layer_index: int, layer, query: torch.Tensor, kv_cache: torch.Tensor,

@@ -329,7 +329,7 @@ class ServingStress:
             cache = self.caches[int(self.st.layer_slot[layer])]
             # RoPE of q and k at the bitrev positions of the abridged layout + KV append, one launch
             check(L.abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), _ptr(val),
-                                        val.stride(0), _ptr(v["tok_pos"]), n_tok, self.C, self.K, _ptr(cs),
+                                        val.stride(0), _ptr(v["tok_pos"]), n_tok, self.C, self.K, 0, _ptr(cs),
                                         cs.shape[0], _ptr(self.slots[g]), _ptr(cache), cache.shape[0], stream),
                   "abkv_rope_kv_append")
             if nd:
@@ -350,7 +350,7 @@ class ServingStress:
                 n_sp, sp_tiles = m["code_split"][g]
                 check(L.abkv_paged_prefill_attn(_ptr(qc), qc.stride(0), qc.stride(1), _ptr(cache), cache.shape[0],
                                                 _ptr(cod_bt[g]), self.W, self.W, _ptr(v["q_start"]),
-                                                _ptr(v["kv_start"][g]), _ptr(v["limits"][g]), _ptr(v["tile_req"]),
+                                                _ptr(v["kv_start"][g]), _ptr(v["limits"][g]), None, _ptr(v["tile_req"]),
                                                 _ptr(v["tile_q0"]), m["n_tiles"], None, 0, C.c_float(self.scale),
                                                 _ptr(oc), oc.stride(0), oc.stride(1), None, nc * self.K, n_sp,
                                                 sp_tiles, _ptr(self._code_ws) if n_sp > 1 else None,

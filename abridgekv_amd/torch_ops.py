@@ -68,16 +68,18 @@ def _kv_append_fake(key, value, slot_mapping, kv_cache):
 @torch.library.custom_op(f"{_NS}::rope_kv_append", mutates_args=("q", "key", "kv_cache"))
 def rope_kv_append(q: Tensor, key: Tensor, value: Tensor, positions: Tensor, cos_sin: Tensor,
                    slot_mapping: Optional[Tensor], kv_cache: Optional[Tensor], block_c: int, codes_k: int,
-                   max_position: int) -> None:
+                   max_position: int, code_span: int = 0) -> None:
     """abkv_rope_kv_append: q and key rotated in place at the RoPE positions of ``positions`` (logical positions of
-    the abridged layout when block_c > 0), rotated key and value appended at slot_mapping. ``max_position``: host
-    bound on the positions (checked against the cos/sin table without reading the device)."""
+    the abridged layout when block_c > 0; code rows over offsets [0, code_span), 0 = block_c), rotated key and value
+    appended at slot_mapping. ``max_position``: host bound on the positions (checked against the cos/sin table
+    without reading the device)."""
     _ops.rope_kv_append(q, key, value, positions, cos_sin, slot_mapping=slot_mapping, kv_cache=kv_cache,
-                        block_c=block_c, codes_k=codes_k, max_position=max_position)
+                        block_c=block_c, codes_k=codes_k, max_position=max_position, code_span=code_span)
 
 
 @rope_kv_append.register_fake
-def _rope_kv_append_fake(q, key, value, positions, cos_sin, slot_mapping, kv_cache, block_c, codes_k, max_position):
+def _rope_kv_append_fake(q, key, value, positions, cos_sin, slot_mapping, kv_cache, block_c, codes_k, max_position,
+                         code_span=0):
     _need(q.shape[0] >= positions.shape[0] and key.shape[0] >= positions.shape[0], "q / key must cover the positions")
 
 
@@ -124,10 +126,10 @@ def _kv_move_mixed_fake(layer_caches, ops, seg_offsets, free_ops):
 def paged_prefill_attn(q: Tensor, kv_cache: Tensor, block_table: Tensor, q_start: Tensor, kv_start: Tensor,
                        kv_limit: Tensor, tile_req: Tensor, tile_q0: Tensor, causal: Tensor, scale: float,
                        num_tokens: int, num_splits: int, split_tiles: int, out: Tensor, lse: Optional[Tensor],
-                       workspace: Optional[Tensor]) -> None:
+                       workspace: Optional[Tensor], kv_excluded: Optional[Tensor] = None) -> None:
     """abkv_paged_prefill_attn with device metadata (int32: q_start [B+1], kv_start / kv_limit / causal [B], the
-    64-row query tiles tile_req / tile_q0) and a caller workspace when num_splits > 1; ``num_tokens`` is
-    q_start[B] (the rows the launch writes)."""
+    64-row query tiles tile_req / tile_q0, optional kv_excluded [B, 2] key ranges hidden per request) and a caller
+    workspace when num_splits > 1; ``num_tokens`` is q_start[B] (the rows the launch writes)."""
     _need(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: cuda bf16 [T, 32, 128]")
     _ops._check_cache(kv_cache)
     for name, t in (("block_table", block_table), ("q_start", q_start), ("kv_start", kv_start),
@@ -145,12 +147,16 @@ def paged_prefill_attn(q: Tensor, kv_cache: Tensor, block_table: Tensor, q_start
     if lse is not None:
         _need(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= q.shape[0] * _ops.HEADS_Q,
               "lse must be contiguous fp32 [T, 32]")
+    if kv_excluded is not None:
+        _need(kv_excluded.is_cuda and kv_excluded.dtype == torch.int32 and kv_excluded.is_contiguous()
+              and kv_excluded.numel() == 2 * kv_start.numel(), "kv_excluded must be contiguous cuda int32 [B, 2]")
     if tile_req.numel() == 0:
         return
     rc = lib().abkv_paged_prefill_attn(
         _ops._ptr(q), q.stride(0), q.stride(1), _ops._ptr(kv_cache), kv_cache.shape[0], _ops._ptr(block_table),
         _ops._row_stride(block_table), block_table.shape[1], _ops._ptr(q_start), _ops._ptr(kv_start),
-        _ops._ptr(kv_limit), _ops._ptr(tile_req), _ops._ptr(tile_q0), tile_req.numel(), _ops._ptr(causal), 1,
+        _ops._ptr(kv_limit), _ops._ptr(kv_excluded), _ops._ptr(tile_req), _ops._ptr(tile_q0), tile_req.numel(),
+        _ops._ptr(causal), 1,
         float(scale), _ops._ptr(out), out.stride(0), out.stride(1), _ops._ptr(lse), num_tokens, num_splits,
         split_tiles, _ops._ptr(workspace) if num_splits > 1 else None, ws_bytes, C.c_void_p(_ops._stream()))
     check(rc, "abkv_paged_prefill_attn")
@@ -158,7 +164,7 @@ def paged_prefill_attn(q: Tensor, kv_cache: Tensor, block_table: Tensor, q_start
 
 @paged_prefill_attn.register_fake
 def _paged_prefill_attn_fake(q, kv_cache, block_table, q_start, kv_start, kv_limit, tile_req, tile_q0, causal, scale,
-                             num_tokens, num_splits, split_tiles, out, lse, workspace):
+                             num_tokens, num_splits, split_tiles, out, lse, workspace, kv_excluded=None):
     _need(tuple(out.shape) == tuple(q.shape), "out must be [T, 32, 128]")
 
 

@@ -541,7 +541,7 @@ def bench_code_step(args, torch):
     def launch(l):
         bt, ks, kl, (n_sp, sp_tiles) = meta[l]
         check(lib().abkv_paged_prefill_attn(ptr(q), q.stride(0), q.stride(1), ptr(cache), n_pages, ptr(bt), W, W,
-                                            ptr(q_start), ptr(ks), ptr(kl), ptr(tl[0]), ptr(tl[1]), n_tiles, None, 0,
+                                            ptr(q_start), ptr(ks), ptr(kl), None, ptr(tl[0]), ptr(tl[1]), n_tiles, None, 0,
                                             C_.c_float(scale), ptr(out), out.stride(0), out.stride(1), None, R * K,
                                             n_sp, sp_tiles, ptr(ws) if n_sp > 1 else None,
                                             C_.c_size_t(ws_bytes if n_sp > 1 else 0), stream),

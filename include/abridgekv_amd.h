@@ -105,13 +105,15 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
  * place; rotated key and value rows are written at slot_mapping[t] (NULL: rotate only; < 0 or past the cache: skip).
  * positions [T] int64: RoPE positions when block_c == 0; otherwise logical positions of the abridged layout (period
  * block_c + codes_k, codes_k a power of two <= block_c) mapped on the device to block * block_c + (offset < block_c ?
- * offset : floor(bitrev(offset - block_c) * block_c / codes_k)). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
+ * offset : floor(bitrev(offset - block_c) * span / codes_k)) with span = code_span, the in-block range the codes
+ * summarize (0: block_c; block_c - T with a static retained tail of T rows, config/compresslm.py:192-206; codes_k <=
+ * span <= block_c). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
  * frequencies then their sin. The caller guarantees every RoPE position is < max_pos (the Python wrapper checks it);
  * the kernel clamps positions into [0, max_pos) only so that no read leaves the table. */
 int abkv_rope_kv_append(void* q, long q_stride_t, long q_stride_h, void* key, long key_stride_t, const void* value,
                         long value_stride_t, const int64_t* positions, int num_tokens, int block_c, int codes_k,
-                        const float* cos_sin, long max_pos, const int64_t* slot_mapping, void* kv_cache,
-                        int num_pages, abkv_stream_t stream);
+                        int code_span, const float* cos_sin, long max_pos, const int64_t* slot_mapping,
+                        void* kv_cache, int num_pages, abkv_stream_t stream);
 
 /* Slot mapping on device: BlockTable.compute_slot_mapping (block_table.py:186-197, non-CP branch) on the physical
  * positions of one KV-cache group (gpu_model_runner.py:1579-1590: phys = logical - compacted[req, group]).
@@ -166,7 +168,9 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
  * physical layout the code step's mask is "keys < code_start + q_g", so each request carries a key limit.
  * q [T, 32, 128] (token stride, head stride), request r's queries are tokens [q_start[r], q_start[r+1]) at physical
  * positions kv_start[r] + i and see keys < kv_limit[r] (and <= their position when request r is causal: causal[r] != 0,
- * or causal_default when causal is NULL). tile_req / tile_q0 [num_tiles] list the 64-row query tiles (request, first
+ * or causal_default when causal is NULL), except the keys of kv_excluded[r] = [start, end) (NULL: none; the code
+ * step's own-block static retained tail, gpu_model_runner.py:2086-2094 "excluded" ranges, compresslm_masks.py:206-213;
+ * start >= end: none). tile_req / tile_q0 [num_tiles] list the 64-row query tiles (request, first
  * row). All index arrays are device int32. lse [T, 32] or NULL. num_splits > 1 splits every tile's keys into
  * num_splits ranges of split_tiles 64-key tiles (split z covers tiles [z * split_tiles, (z + 1) * split_tiles); the
  * ranges must cover every request's keys) computed by separate workgroups and merged; the partials use workspace
@@ -178,7 +182,8 @@ size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits);
 int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache, int num_pages,
                             const int32_t* block_table, long block_table_stride, int block_table_width,
                             const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
-                            const int32_t* tile_req, const int32_t* tile_q0, int num_tiles, const int32_t* causal,
+                            const int32_t* kv_excluded, const int32_t* tile_req, const int32_t* tile_q0, int num_tiles,
+                            const int32_t* causal,
                             int causal_default, float scale, void* out, long out_stride_t, long out_stride_h, float* lse,
                             int num_tokens, int num_splits, int split_tiles, void* workspace, size_t workspace_bytes,
                             abkv_stream_t stream);
@@ -226,8 +231,8 @@ int abkv_decode_attn_packed(const void* q, long q_stride_seq, long q_stride_head
 int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride_h, const void* kv_cache,
                                    int num_pages, const int32_t* block_table, long block_table_stride,
                                    int block_table_width, const int32_t* q_start, const int32_t* kv_start,
-                                   const int32_t* kv_limit, const int32_t* tile_req, const int32_t* tile_q0,
-                                   int num_tiles, const int32_t* causal, int causal_default,
+                                   const int32_t* kv_limit, const int32_t* kv_excluded, const int32_t* tile_req,
+                                   const int32_t* tile_q0, int num_tiles, const int32_t* causal, int causal_default,
                                    const int32_t* head_quota_dev, const void* packed_kv, int packed_pool_pages,
                                    int packed_rows, const int32_t* head_quota, const int32_t* packed_table,
                                    long packed_table_stride, const int32_t* packed_count, int max_packed_per_seq,
@@ -253,9 +258,9 @@ int abkv_decode_attn_f32(const float* q, long q_stride_seq, long q_stride_head, 
 int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h, const float* kv_cache, int num_pages,
                                 const int32_t* block_table, long block_table_stride, int block_table_width,
                                 const int32_t* q_start, const int32_t* kv_start, const int32_t* kv_limit,
-                                const int32_t* tok_req, int num_tokens, const int32_t* causal, int causal_default,
-                                float scale, float* out, long out_stride_t, long out_stride_h, float* lse,
-                                abkv_stream_t stream);
+                                const int32_t* kv_excluded, const int32_t* tok_req, int num_tokens,
+                                const int32_t* causal, int causal_default, float scale, float* out, long out_stride_t,
+                                long out_stride_h, float* lse, abkv_stream_t stream);
 
 /* Compression-masked teacher-forced attention: as abkv_prefill_masked_attn (strides in elements, head dims
  * contiguous and 16-byte aligned rows). lse [B, 32, seq_len] or NULL. */

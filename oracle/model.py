@@ -6,9 +6,12 @@ decoder layer manual attention under the dense boolean mask of ``oracle.prefill.
 ``_dense_mask`` / ``_arith_mask_mod``), with the per-layer query-head quota of compress_forward.py:230-236. Runs the
 HuggingFace layer modules of ``model`` in whatever dtype the model is in (float64 on the CPU for a tight bound).
 
+With a static retained tail of T rows the mask is ``arith_mask(..., retain_tail=T)`` and the bitrev code rows spread
+over the first C - T in-block offsets (compress_forward.py:1059).
+
 Pinning: tests/test_oracle_model.py checks that with one block the content logits equal the model's own causal
 forward (code rows come after the content and are invisible to it), that all-K quotas equal no quotas, and that
-``rope_positions`` matches the closed-form bitrev / appended layout.
+``rope_positions`` matches the closed-form bitrev / appended layout (with and without a code span).
 """
 from __future__ import annotations
 
@@ -20,10 +23,11 @@ from . import layout as ol
 from . import prefill as op
 
 
-def rope_positions(C, N, K, code_positions):
-    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071, L=1, no tails)."""
+def rope_positions(C, N, K, code_positions, span=None):
+    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071, L=1, no replay tail); bitrev
+    code rows spread over in-block offsets [0, span) (span None: C)."""
     pos = np.zeros(N * (C + K), dtype=np.int64)
-    offs = ol.bitrev_code_offsets(K, C) if code_positions == "bitrev" else None
+    offs = ol.bitrev_code_offsets(K, C, span) if code_positions == "bitrev" else None
     for b in range(N):
         for j in range(C + K):
             if code_positions == "bitrev":
@@ -44,9 +48,10 @@ def _rotate_half(x):
 
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                 layer_head_quota=None):
+                 layer_head_quota=None, retain_tail=0):
     """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
-    (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt)."""
+    (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
+    static retained tail."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
@@ -54,7 +59,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     d = tok_e.shape[-1]
     x = torch.cat([tok_e, pause.to(dt).view(1, 1, K, d).expand(B, N, K, d)], dim=2).reshape(B, N * (C + K), d)
     S0 = x.shape[1]
-    pos = torch.from_numpy(rope_positions(C, N, K, code_positions)).view(1, -1)
+    pos = torch.from_numpy(rope_positions(C, N, K, code_positions, C - retain_tail)).view(1, -1)
     cos, sin = inner.rotary_emb(x, pos)
     cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
     pl = None if prompt_len is None else np.asarray(prompt_len, dtype=np.int64)
@@ -62,7 +67,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq)                  # [B?, H?, S0, S0]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail)     # [B?, H?, S0, S0]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -93,8 +98,8 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                      layer_head_quota=None):
+                      layer_head_quota=None, retain_tail=0):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
-    h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota)
+    h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail)
     rows = torch.from_numpy(loss_rows(C, N, K))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

@@ -11,7 +11,9 @@ Pinning:
 * ``packed_attention_fp64`` -- with equal quotas q in every head it must equal the plain paged attention
   (oracle.decode.decode_fp64 / oracle.masks.masked_paged_attention_fp64, pinned by closed forms) over the rows
   [q code rows of every captured block | paged rows]; each KV head's output depends only on its own quota (the
-  output of head h under a mixed schedule equals the output under the uniform schedule q_h).
+  output of head h under a mixed schedule equals the output under the uniform schedule q_h); with no captured
+  block a code step equals the code-step mask of oracle.masks, also with an excluded range (the block's static tail,
+  :725-729).
 """
 from __future__ import annotations
 
@@ -46,11 +48,13 @@ def capture(kv_cache, block_table, start, k_max, quota_row):
     return pack(quota_row, dense)
 
 
-def packed_attention_fp64(q_rows, pages, quota_row, kv_cache, block_table, seq_len, query_len, causal, k_max, scale):
+def packed_attention_fp64(q_rows, pages, quota_row, kv_cache, block_table, seq_len, query_len, causal, k_max, scale,
+                          excluded=None):
     """One request's attention with side rows (the per-head loop of override_attention, :422-484).
 
     q_rows [query_len, Hq, D]; pages: the request's packed pages [2, sum q, D] in capture order; the queries are the
-    last query_len of the seq_len paged rows. Returns (out [query_len, Hq, D], lse [query_len, Hq]) in float64.
+    last query_len of the seq_len paged rows; ``excluded``: physical paged rows [start, end) a code step hides (its
+    block's static tail, :725-729). Returns (out [query_len, Hq, D], lse [query_len, Hq]) in float64.
     """
     q_rows = np.asarray(q_rows, dtype=np.float64)
     mk, mv = paged_rows(kv_cache, block_table, seq_len)
@@ -74,6 +78,8 @@ def packed_attention_fp64(q_rows, pages, quota_row, kv_cache, block_table, seq_l
             if query_len != k_max:
                 raise RuntimeError("noncausal step must contain exactly k_max code queries")
             hidden[:, side:] = (main_pos >= prefix + quota_row[h])[None, :]
+            if excluded is not None:
+                hidden[:, side + excluded[0]: side + excluded[1]] = True
         for gi in range(g):
             hq = h * g + gi
             s = scale * q_rows[:, hq] @ key.T

@@ -85,6 +85,44 @@ def test_custom_mask_converts_to_code_step_limits(quota):
                 assert limits[r] == sl
 
 
+@pytest.mark.parametrize("quota", [1, 5, 16])
+def test_custom_mask_with_static_tail_converts_to_limits_and_excluded_ranges(quota):
+    """The reference's code-step mask with a static retained tail (compresslm_masks.py:206-213: the block's own tail
+    rows hidden from its codes) converts to the same key limit plus an excluded range, and code_step_excluded_ranges
+    accepts exactly the ranges the worker accepts (gpu_model_runner.py:2086-2091)."""
+    K, T = 16, 6
+    rng = np.random.default_rng(10 + quota)
+    for _ in range(10):
+        reqs = _mixed_batch(rng)
+        ex = [(span[0] - T, span[0]) if span is not None and span[0] >= T + 2 else None
+              for _, _, span, _ in reqs]
+        flat = np.concatenate([om.request_mask(ql, sl, [span] if span else [], e, quota, K, causal).reshape(-1)
+                               for (ql, sl, span, causal), e in zip(reqs, ex)])
+        qsl = np.concatenate([[0], np.cumsum([r[0] for r in reqs])])
+        sls = [r[1] for r in reqs]
+        limits, causal, excluded = bk.key_ranges_from_custom_mask(torch.from_numpy(flat), qsl, sls)
+        expect = bk.code_step_key_limits(qsl, sls, [r[2] for r in reqs], quota, K)
+        expect_ex = bk.code_step_excluded_ranges([r[2] for r in reqs], ex, qsl, sls)
+        for r, (ql, sl, span, c) in enumerate(reqs):
+            if span is not None:
+                assert limits[r] == expect[r] and not causal[r]
+                got = None if excluded is None or excluded[r, 1] == 0 else tuple(excluded[r])
+                assert got == ex[r]
+                if ex[r] is not None:
+                    assert tuple(expect_ex[r]) == ex[r]
+        if any(e is not None for e in ex):
+            with pytest.raises(RuntimeError, match="prefix"):
+                bk.limits_from_custom_mask(torch.from_numpy(flat), qsl, sls)
+    with pytest.raises(RuntimeError, match="exclusion"):           # must end before the query rows
+        bk.code_step_excluded_ranges([(16, 20)], [(14, 17)], [0, 4], [20])
+    with pytest.raises(RuntimeError, match="not coding"):
+        bk.code_step_excluded_ranges([None], [(2, 4)], [0, 1], [9])
+    m = np.ones((2, 9), bool)
+    m[:, 1] = m[:, 4] = False                                        # two hidden ranges: not runnable
+    with pytest.raises(RuntimeError, match="more than one"):
+        bk.key_ranges_from_custom_mask(torch.from_numpy(m.reshape(-1)), [0, 2], [9])
+
+
 def test_custom_mask_rejects_non_prefix_masks():
     m = np.ones((2, 5), bool)
     m[0, 2] = False
@@ -123,7 +161,15 @@ def test_metadata_builder_validation():
     with pytest.raises(RuntimeError):
         b.build([0] * 6, [1] * 5, bt, sm)
     md = b.build([0, 4], [20], bt, sm, code_key_limit=[18], seq_lens_dev=torch.zeros(1, dtype=torch.int32))
-    assert md.num_decodes == 0 and md.workspace is None
+    assert md.num_decodes == 0 and md.workspace is None and md.code_excluded is None
+    md = b.build([0, 4], [20], bt, sm, code_key_limit=[18], seq_lens_dev=torch.zeros(1, dtype=torch.int32),
+                 code_excluded=[[10, 16]])
+    assert md.code_excluded.tolist() == [[10, 16]]
+    with pytest.raises(RuntimeError):                  # the excluded range reaches into the query rows
+        b.build([0, 4], [20], bt, sm, code_key_limit=[18], seq_lens_dev=torch.zeros(1, dtype=torch.int32),
+                code_excluded=[[10, 17]])
+    with pytest.raises(RuntimeError):                  # only code-step requests carry one
+        b.build([0, 4], [20], bt, sm, seq_lens_dev=torch.zeros(1, dtype=torch.int32), code_excluded=[[10, 12]])
 
 
 def test_backend_surface_and_hook_is_inert_without_impl():

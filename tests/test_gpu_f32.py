@@ -45,10 +45,14 @@ def test_decode_f32_matches_fp64():
     assert np.all(np.isneginf(got_l[~live])) and np.all(got_o[~live] == 0)
 
 
-def test_paged_multi_query_f32_code_step_and_chunks():
+@pytest.mark.parametrize("tail", [0, 40])
+def test_paged_multi_query_f32_code_step_and_chunks(tail):
+    """fp32 code step (key limit code start + quota; with a static tail, the block's last rows before the codes
+    excluded: the reference's mask with its excluded range, compresslm_masks.py:206-213) and causal chunks."""
     from abridgekv_amd import ops
     quota, K = 64, 128
     reqs = [(K, 500 + K, (500, 500 + K)), (90, 90 + 200, None), (1, 777, None)]
+    excluded = [(500 - tail, 500) if tail and span else None for _, _, span in reqs]
     cache, tables = _paged([sl for _, sl, _ in reqs], 300, 2)
     qsl = np.concatenate([[0], np.cumsum([r[0] for r in reqs])])
     g = torch.Generator().manual_seed(3)
@@ -60,12 +64,12 @@ def test_paged_multi_query_f32_code_step_and_chunks():
     dev = torch.device("cuda")
     lse = torch.empty((int(qsl[-1]), 32), dtype=torch.float32, device=dev)
     out, _ = ops.paged_prefill_attention(q.to(dev), cache.to(dev), torch.from_numpy(tables).to(dev), qsl, kv_start,
-                                         limits, causal, lse=lse)
+                                         limits, causal, lse=lse, excluded=excluded if tail else None)
     torch.cuda.synchronize()
     got_o, got_l = out.cpu().numpy(), lse.cpu().numpy()
     cf = cache.numpy()
     for r, (ql, sl, span) in enumerate(reqs):
-        m = om.request_mask(ql, sl, [span] if span else [], None, quota, K, causal=span is None)
+        m = om.request_mask(ql, sl, [span] if span else [], excluded[r], quota, K, causal=span is None)
         ro, rl = om.masked_paged_attention_fp64(q[qsl[r]: qsl[r + 1]].numpy(), cf, tables[r], sl, m, 128 ** -0.5)
         assert np.abs(got_o[qsl[r]: qsl[r + 1]] - ro).max() <= TOL, f"request {r}"
         assert np.abs(got_l[qsl[r]: qsl[r + 1]] - rl).max() <= TOL, f"request {r}"

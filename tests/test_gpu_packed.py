@@ -115,9 +115,11 @@ def test_decode_packed_matches_oracle(layer):
         assert np.all(np.isneginf(gl[~live])) and np.all(go[~live] == 0)
 
 
-def test_multi_query_packed_matches_oracle():
-    """A causal prompt chunk, a code step (K queries, non-causal, paged keys < prefix + q_h per head) and a chunk of
-    a request with no packed pages in one launch."""
+@pytest.mark.parametrize("tail", [0, 23])
+def test_multi_query_packed_matches_oracle(tail):
+    """A causal prompt chunk, a code step (K queries, non-causal, paged keys < prefix + q_h per head; with a static
+    tail, the block's last rows before the codes hidden) and a chunk of a request with no packed pages in one
+    launch."""
     from abridgekv_amd import ops
     rng, caches = _setup(20)
     layer = 0
@@ -140,15 +142,17 @@ def test_multi_query_packed_matches_oracle():
     sls = np.asarray([r[1] for r in reqs])
     ql = np.asarray([r[0] for r in reqs])
     lse = torch.empty((int(qsl[-1]), 32), dtype=torch.float32, device=dev)
+    excluded = [(sl - n - tail, sl - n) if tail and not causal else None for n, sl, causal in reqs]
     out, _ = ops.paged_prefill_attention_packed(q.to(dev), caches[layer].to(dev), torch.from_numpy(bt).to(dev), qsl,
                                                 sls - ql, sls, [r[2] for r in reqs], _bf(pools[layer]).to(dev), row,
                                                 torch.from_numpy(table).to(dev), torch.from_numpy(count).to(dev),
-                                                int(count.max()), scale=128 ** -0.5, lse=lse)
+                                                int(count.max()), scale=128 ** -0.5, lse=lse,
+                                                excluded=excluded if tail else None)
     torch.cuda.synchronize()
     cf = caches[layer].float().numpy()
     for i, (n, sl, causal) in enumerate(reqs):
         ro, rl = opk.packed_attention_fp64(_f64(q[qsl[i]: qsl[i + 1]]), [pools[layer][p] for p in pages[i]], row, cf,
-                                           bt[i], sl, n, causal, K, 128 ** -0.5)
+                                           bt[i], sl, n, causal, K, 128 ** -0.5, excluded=excluded[i])
         assert np.abs(_f64(out[qsl[i]: qsl[i + 1]]) - ro).max() <= TOL, f"request {i}"
         assert np.abs(lse[qsl[i]: qsl[i + 1]].cpu().numpy() - rl).max() <= TOL, f"request {i}"
 

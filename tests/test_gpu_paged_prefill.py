@@ -25,23 +25,27 @@ def _setup(n_rows, n_pages, seed):
     return cache, tables
 
 
-def _oracle(q_rows, cache, table, kv_start, limit, causal):
-    """fp64 attention of query rows q_rows [n, 32, 128] at positions kv_start + i over physical keys < limit."""
+def _oracle(q_rows, cache, table, kv_start, limit, causal, excluded=None):
+    """fp64 attention of query rows q_rows [n, 32, 128] at positions kv_start + i over physical keys < limit (minus
+    the excluded range)."""
     out = np.zeros((len(q_rows), 32, 128))
     lse = np.zeros((len(q_rows), 32))
     k, v = od.paged_rows(cache, table, limit)
     for i in range(len(q_rows)):
         n = min(limit, kv_start + i + 1) if causal else limit
-        out[i], lse[i] = od.decode_fp64(q_rows[i], k[:n], v[:n], 128 ** -0.5)
+        keep = np.arange(n)
+        if excluded is not None:
+            keep = keep[(keep < excluded[0]) | (keep >= excluded[1])]
+        out[i], lse[i] = od.decode_fp64(q_rows[i], k[keep], v[keep], 128 ** -0.5)
     return out, lse
 
 
-def _run(cache_bf, tables, q, q_start, kv_start, kv_limit, causal, split=None):
+def _run(cache_bf, tables, q, q_start, kv_start, kv_limit, causal, split=None, excluded=None):
     from abridgekv_amd import ops
     dev = torch.device("cuda")
     lse = torch.empty((q.shape[0], 32), dtype=torch.float32, device=dev)
     out, _ = ops.paged_prefill_attention(q.to(dev), cache_bf.to(dev), torch.from_numpy(tables).to(dev), q_start,
-                                         kv_start, kv_limit, causal, lse=lse, split=split)
+                                         kv_start, kv_limit, causal, lse=lse, split=split, excluded=excluded)
     torch.cuda.synchronize()
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
@@ -64,6 +68,29 @@ def test_code_step_limits_per_group_quota(split):
                          causal=False)
         assert np.abs(out[q_start[r]: q_start[r + 1]] - ro).max() <= TOL
         assert np.abs(lse[q_start[r]: q_start[r + 1]] - rl).max() <= TOL
+
+
+@pytest.mark.parametrize("split", [None, 1, 5])
+def test_code_step_static_tail_excluded(split):
+    """Code steps whose block's last T content rows (just before the code rows) are hidden from the codes: T = 64
+    aligned to a tile, T = 37 across a tile boundary, T = 200 spanning whole tiles (one of them entirely hidden), and
+    a request without a range in the same launch."""
+    resident = [700, 1301, 460, 900]
+    quotas = [64, 256, 128, 32]
+    tails = [64, 37, 200, None]
+    cache, tables = _setup([r + 256 for r in resident], 400, 7)
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn((4 * 256, 32, 128), generator=g).to(torch.bfloat16)
+    q_start = [0, 256, 512, 768, 1024]
+    kv_limit = [r + qq for r, qq in zip(resident, quotas)]
+    excluded = [None if t is None else (r - t, r) for r, t in zip(resident, tails)]
+    out, lse = _run(cache, tables, q, q_start, resident, kv_limit, causal=False, split=split, excluded=excluded)
+    cf = cache.float().numpy()
+    for r in range(4):
+        ro, rl = _oracle(q[q_start[r]: q_start[r + 1]].float().numpy(), cf, tables[r], resident[r], kv_limit[r],
+                         causal=False, excluded=excluded[r])
+        assert np.abs(out[q_start[r]: q_start[r + 1]] - ro).max() <= TOL, r
+        assert np.abs(lse[q_start[r]: q_start[r + 1]] - rl).max() <= TOL, r
 
 
 def test_causal_prompt_chunks_ragged():

@@ -26,10 +26,12 @@ def _within_half_ulp(got, want):
     return bool(((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-6).all())
 
 
-@pytest.mark.parametrize("logical,C,K", [(False, 64, 16), (True, 64, 16), (True, 48, 16)])
-def test_rotation_and_cache_rows(logical, C, K):
+@pytest.mark.parametrize("logical,C,K,span", [(False, 64, 16, 0), (True, 64, 16, 0), (True, 48, 16, 0),
+                                              (True, 64, 16, 52)])
+def test_rotation_and_cache_rows(logical, C, K, span):
     """Plain RoPE positions, and logical positions of the abridged layout mapped on the device (also with a block
-    size that is not a power of two: only the code count must be one)."""
+    size that is not a power of two: only the code count must be one; and with the code rows spread over the first
+    span offsets, a static retained tail of C - span rows)."""
     from abridgekv_amd import ops
     dev = torch.device("cuda")
     g = torch.Generator().manual_seed(11)
@@ -39,7 +41,7 @@ def test_rotation_and_cache_rows(logical, C, K):
     v = torch.randn((T, 8, 128), generator=g).to(torch.bfloat16)
     if logical:
         lpos = torch.randint(0, 90 * (C + K), (T,), generator=g)
-        rpos = torch.from_numpy(ol.bitrev_rope_positions(lpos.numpy(), C, K))
+        rpos = torch.from_numpy(ol.bitrev_rope_positions(lpos.numpy(), C, K, span or None))
     else:
         lpos = rpos = torch.randint(0, max_pos, (T,), generator=g)
     table = ops.rope_cos_sin_cache(max_pos)
@@ -50,7 +52,7 @@ def test_rotation_and_cache_rows(logical, C, K):
     cache = torch.randn((num_pages, 2, 16, 8, 128), generator=g).to(torch.bfloat16)
     qd, kd, vd, cd = q.to(dev), k.to(dev), v.to(dev), cache.to(dev)
     ops.rope_kv_append(qd, kd, vd, lpos.to(dev), table.to(dev), slot_mapping=slots.to(dev), kv_cache=cd,
-                       block_c=C if logical else 0, codes_k=K if logical else 0)
+                       block_c=C if logical else 0, codes_k=K if logical else 0, code_span=span)
     torch.cuda.synchronize()
     assert _within_half_ulp(qd.cpu(), _rotate_fp64(q, rpos, table))
     assert _within_half_ulp(kd.cpu(), _rotate_fp64(k, rpos, table))

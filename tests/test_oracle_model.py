@@ -27,6 +27,11 @@ def test_rope_positions_closed_form():
         assert list(bitrev[b * (C + K): b * (C + K) + C]) == list(range(b * C, b * C + C))
         assert list(bitrev[b * (C + K) + C: (b + 1) * (C + K)]) == list(b * C + offs)
     assert list(om.rope_positions(C, N, K, "appended")) == list(range(N * (C + K)))
+    # a static tail of 5: code rows spread over [0, 11) -- the reference's own check (test_compresslm_vllm_state.py:
+    # 349-352, C=8, K=4, T=2: offsets < 6, distinct, the first 0)
+    tail = om.rope_positions(C, N, K, "bitrev", span=C - 5)[C: C + K] - 0
+    assert tail.max() < C - 5 and len(set(tail.tolist())) == K and tail[0] == 0
+    assert list(ol.bitrev_code_offsets(4, 8, 6)) == [0, 3, 1, 4]
 
 
 @pytest.mark.parametrize("code_positions", ["appended", "bitrev"])

@@ -143,6 +143,13 @@ def test_oracle_code_step_without_pages_is_the_code_mask():
     m = om.request_mask(K, seq_len, [(seq_len - K, seq_len)], None, q, K, causal=False)
     ref, ref_l = om.masked_paged_attention_fp64(qr, cache, table, seq_len, m, 0.3)
     assert np.allclose(got, ref, atol=1e-12) and np.allclose(got_l, ref_l, atol=1e-12)
+    ex = (seq_len - K - 7, seq_len - K)                    # the block's static tail, just before its codes
+    got, got_l = opk.packed_attention_fp64(qr, [], (q,) * 8, cache, table, seq_len, K, False, K, 0.3, excluded=ex)
+    m = om.request_mask(K, seq_len, [(seq_len - K, seq_len)], ex, q, K, causal=False)
+    ref, ref_l = om.masked_paged_attention_fp64(qr, cache, table, seq_len, m, 0.3)
+    assert np.allclose(got, ref, atol=1e-12) and np.allclose(got_l, ref_l, atol=1e-12)
+    assert not np.allclose(got, opk.packed_attention_fp64(qr, [], (q,) * 8, cache, table, seq_len, K, False, K,
+                                                          0.3)[0])
 
 
 def test_packed_config_validation():
