@@ -64,6 +64,13 @@ struct DecodeArgs {
 __device__ __forceinline__ u32x4 ld16(const __bf16* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// K/V rows: every byte is read by exactly one wave of one launch and a decode step streams far more rows than any
+// cache holds, so the loads are non-temporal (no allocation in L2 / the last-level cache). Same-process A/B over the
+// same pages, outputs bit-identical: saturated B=256 1723.8 -> 1687.4 us; full-model B=64 groups q64 143.5 -> 141.0,
+// q128 236.4 -> 224.8, q256 426.3 -> 412.1 us.
+__device__ __forceinline__ u32x4 ld16_stream(const __bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   const _Float16 x = (_Float16)lo, y = (_Float16)hi;
@@ -157,15 +164,15 @@ __global__ __launch_bounds__(64 * kW) void decode_attn_kernel(DecodeArgs a) {
     u32x4 kr[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kr[0][i] = ld16(base0 + m16 * kSlotElems + 8 * (4 * i + j));
-      kr[1][i] = ld16(base1 + m16 * kSlotElems + 8 * (4 * i + j));
+      kr[0][i] = ld16_stream(base0 + m16 * kSlotElems + 8 * (4 * i + j));
+      kr[1][i] = ld16_stream(base1 + m16 * kSlotElems + 8 * (4 * i + j));
     }
     // V rows: contraction index e<4 -> slot 4j+e of p0, e>=4 -> slot 4j+e-4 of p1; lane loads dims 8*m16..+8.
     u32x4 vr[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vr[e] = ld16(base0 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
-      vr[4 + e] = ld16(base1 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
+      vr[e] = ld16_stream(base0 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
+      vr[4 + e] = ld16_stream(base1 + kHalfElems + (4 * j + e) * kSlotElems + 8 * m16);
     }
 
     floatx4 s[2];
@@ -430,13 +437,13 @@ __global__ __launch_bounds__(64) void decode_side_kernel(DecodeArgs a) {
     for (int t = 0; t < 2; ++t) {
       const __bf16* kp = chunk_row_ptr(min(c0 + 16 * t + m16, r_end - 1));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[t][i] = ld16(kp + 8 * (4 * i + j));
+      for (int i = 0; i < 4; ++i) kr[t][i] = ld16_stream(kp + 8 * (4 * i + j));
     }
     // V rows: contraction index e < 4 -> row c0 + 4j + e, e >= 4 -> row c0 + 16 + 4j + e - 4; dims 8*m16 .. +8
     u32x4 vr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      vr[e] = ld16(chunk_row_ptr(min(c0 + (e < 4 ? 0 : 16) + 4 * j + (e & 3), r_end - 1)) + v_off + 8 * m16);
+      vr[e] = ld16_stream(chunk_row_ptr(min(c0 + (e < 4 ? 0 : 16) + 4 * j + (e & 3), r_end - 1)) + v_off + 8 * m16);
 
     floatx4 s[2];
 #pragma unroll

@@ -33,6 +33,19 @@ struct LayerPtrs {
   char* p[kMaxLayers];
 };
 
+// Row moves read every moved byte once and write it once, far more bytes per step than any cache holds: streaming
+// (non-temporal) loads and stores, which leave L2 and the last-level cache alone. Same-process A/B of the 64-sequence
+// step (six group launches), bytes bit-identical: 490.7 -> 446.9 us (4.92 -> 5.41 TB/s). The hint changes where lines
+// are kept, not the order of the accesses: every load and store is issued where it was, and the launch's ordering
+// argument (no op reads a slot that an earlier op of its segment writes; independent ops touch no slot another op
+// writes) does not depend on caching.
+__device__ __forceinline__ u32x4 ld16_stream(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st16_stream(char* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 struct MoveArgs {
   LayerPtrs layers;
   const int32_t* ops;          // [n_ops, 4] (src_block, src_off, dst_block, dst_off)
@@ -111,7 +124,7 @@ __device__ __forceinline__ void move_ordered(const MoveArgs& a, char* base, int 
     OrderedChunk cur, nxt;
     ordered_fetch(a, s0, s1, wave, lane, cur);
 #pragma unroll
-    for (int k = 0; k < kMoveRows / 4; ++k) cur.buf[k] = *reinterpret_cast<const u32x4*>(base + cur.soff[k] + inner);
+    for (int k = 0; k < kMoveRows / 4; ++k) cur.buf[k] = ld16_stream(base + cur.soff[k] + inner);
     for (int c0 = s0; c0 < s1; c0 += kMoveRows) {
       const bool more = c0 + kMoveRows < s1;
       if (more) ordered_fetch(a, c0 + kMoveRows, s1, wave, lane, nxt);
@@ -122,11 +135,11 @@ __device__ __forceinline__ void move_ordered(const MoveArgs& a, char* base, int 
       if (more) {
 #pragma unroll
         for (int k = 0; k < kMoveRows / 4; ++k)
-          nxt.buf[k] = *reinterpret_cast<const u32x4*>(base + nxt.soff[k] + inner);
+          nxt.buf[k] = ld16_stream(base + nxt.soff[k] + inner);
       }
 #pragma unroll
       for (int k = 0; k < kMoveRows / 4; ++k)
-        if (cur.doff[k] >= 0 && active) *reinterpret_cast<u32x4*>(base + cur.doff[k] + inner) = cur.buf[k];
+        if (cur.doff[k] >= 0 && active) st16_stream(base + cur.doff[k] + inner, cur.buf[k]);
       cur = nxt;
     }
   }
@@ -150,10 +163,10 @@ __device__ __forceinline__ void move_free(const MoveArgs& a, const int32_t* __re
     const long inner = (long)half * a.half_bytes + (long)(v - half * (row_vec / 2)) * 16;
     u32x4 buf[kFreeRows];
 #pragma unroll
-    for (int r = 0; r < kFreeRows; ++r) buf[r] = *reinterpret_cast<const u32x4*>(base + sb[r] + inner);
+    for (int r = 0; r < kFreeRows; ++r) buf[r] = ld16_stream(base + sb[r] + inner);
 #pragma unroll
     for (int r = 0; r < kFreeRows; ++r)
-      if (db[r] >= 0) *reinterpret_cast<u32x4*>(base + db[r] + inner) = buf[r];
+      if (db[r] >= 0) st16_stream(base + db[r] + inner, buf[r]);
   }
 }
 

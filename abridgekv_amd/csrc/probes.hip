@@ -19,7 +19,8 @@ using u32x4 = __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t;
 // Row copy with a compaction launch's addresses and none of its ordering: op i of layer l copies the row at
 // (src_block, src_off) of src[l] to (dst_block, dst_off) of dst[l], a different tensor, so every op is independent.
 // Workgroup = kRows ops of one layer, thread t = the t-th 16-byte vector of a row (K half, then V half); each thread
-// issues its kRows loads back to back, then its kRows stores. Ops outside the cache are skipped.
+// issues its kRows loads back to back, then its kRows stores, streaming (non-temporal) as the mover does. Ops outside
+// the cache are skipped.
 template <int kRows>
 __global__ __launch_bounds__(256) void probe_row_copy_kernel(ProbeLayers L, const int32_t* __restrict__ ops, int n_ops,
                                                              long page_bytes, long half_bytes, int slot_bytes,
@@ -50,10 +51,11 @@ __global__ __launch_bounds__(256) void probe_row_copy_kernel(ProbeLayers L, cons
     u32x4 buf[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
-      buf[r] = soff[r] >= 0 ? *reinterpret_cast<const u32x4*>(src + soff[r]) : u32x4{0, 0, 0, 0};
+      buf[r] = soff[r] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + soff[r]))
+                            : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
-      if (doff[r] >= 0) *reinterpret_cast<u32x4*>(dst + doff[r]) = buf[r];
+      if (doff[r] >= 0) __builtin_nontemporal_store(buf[r], reinterpret_cast<u32x4*>(dst + doff[r]));
   }
 }
 
