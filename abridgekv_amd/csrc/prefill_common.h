@@ -1,0 +1,118 @@
+// Shared pieces of the masked-prefill forward (prefill_attn.hip) and backward (prefill_bwd.hip): the kernel
+// arguments, the workgroup -> (query tile, KV head, sequence) grid order and the tile walk over the visible key tiles
+// of the compression mask (abridgekv/compress_forward.py:695-727).
+#pragma once
+#include "attn_tile.h"
+
+namespace abkv {
+
+struct PrefillArgs {
+  const __bf16* q;  long q_sb, q_ss, q_sh;   // [B, S0, 32, 128]
+  const __bf16* k;  long k_sb, k_ss, k_sh;   // [B, S0, 8, 128]
+  const __bf16* v;  long v_sb, v_ss, v_sh;
+  int B, S0, C, K, N;
+  const int32_t* prompt_len;                 // [B] raw-prompt content tokens (nullptr: none)
+  const int32_t* head_quota;                 // [32] code slots visible per query head (nullptr: all K)
+  float scale_log2;
+  __bf16* out;      long o_sb, o_ss, o_sh;   // [B, S0, 32, 128]
+  float* lse;                                // [B, 32, S0] natural log, or nullptr
+  int aligned;                               // C % 64 == 0 && K % 64 == 0 and no retained tail
+  int num_q_tiles;
+  int tail;                                  // static retained tail T (0: none)
+};
+
+// Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,
+// tile rank slowest. Workgroups go to the 8 XCDs round-robin by linear id, so every workgroup of one KV head runs on
+// one XCD and that XCD's L2 serves all re-reads of the head's rows; and each tile rank is issued for every (head,
+// sequence) before the next, so the costly tiles (which the callers rank first) do not trail at the end of the grid.
+struct GridPos {
+  int rank, kvh, b;
+};
+__device__ __forceinline__ GridPos grid_pos(int batch) {
+  const int l = blockIdx.x;
+  return {l / (kHeadsKV * batch), l % kHeadsKV, (l / kHeadsKV) % batch};
+}
+
+// Walk over the key tiles one query tile attends to, with the mask mode of each.
+// Aligned layouts (C and K multiples of 64): a key tile is named by (block kb, tile tw of the block's C + K rows).
+// Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
+// ends the segment and the walk jumps to the next one: no per-tile test of skipped tiles and no integer division.
+// Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
+template <bool kAligned>
+struct TileWalk {
+  static constexpr bool kHole = false;                      // never yields an excluded key range (mode 4)
+  int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
+  bool q_code;
+  int kb, tw;
+  int wq0, wq1;                                             // code quotas of this wave's two heads
+
+  __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_,
+                                      int wq0_, int wq1_)
+      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0),
+        wq0(wq0_), wq1(wq1_) {
+    qb = q0 / per;
+    q_code = q0 - qb * per >= C;
+    tpb = per / kBN;
+    ct = C / kBN;
+    n_tiles = (S0 + kBN - 1) / kBN;
+  }
+
+  // aligned: move (kb, tw) to the first visible tile at or after it; false when none is left
+  __device__ __forceinline__ bool seek() {
+    for (;;) {
+      if (kb > qb) return false;
+      if (tw < ct) {
+        const bool vis = kb == qb ? (q_code || kb * per + kBN * tw <= q_last) : (kb * C + kBN * tw < plen);
+        if (vis) return true;
+        tw = ct;                                            // the rest of this block's content is hidden too
+      }
+      if ((kb < qb || q_code) && tw < tpb && kBN * (tw - ct) < qmax) return true;
+      if (kb == qb) return false;                           // blocks after the query's own block are hidden
+      ++kb;
+      tw = 0;
+    }
+  }
+
+  // aligned: mask mode of the visible tile (kb, tw)
+  __device__ __forceinline__ void mask(TileMask& tm) const {
+    const int k0 = kb * per + kBN * tw;
+    tm.mode = 0;
+    if (tw < ct) {
+      if (kb == qb) {
+        if (!q_code && k0 + kBN - 1 > q0) tm.mode = 1;      // diagonal tile of the block's content
+      } else if (kb * C + kBN * tw + kBN > plen) {
+        tm.mode = 2;                                        // raw-prompt boundary inside the tile
+        tm.limit[0] = tm.limit[1] = kb * per + (plen - kb * C);
+      }
+    } else if (kBN * (tw - ct) + kBN > qmin) {
+      tm.mode = 2;                                          // quota boundary inside a code tile
+      tm.limit[0] = kb * per + C + wq0;
+      tm.limit[1] = kb * per + C + wq1;
+    }
+  }
+
+  // next tile to attend (the first call gives the first); false when the walk is done
+  __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
+    if constexpr (kAligned) {
+      if (!first) ++tw;
+      if (!seek()) return false;
+      kt = kb * tpb + tw;
+      mask(tm);
+      return true;
+    } else {
+      kt = first ? 0 : kt + 1;
+      tm.mode = 3;
+      // keys up to the query tile's last row, or in a block up to its own (codes of the own block): a prefix
+      return kt < n_tiles && (kt * kBN <= q_last || (kt * kBN) / per <= q_last / per);
+    }
+  }
+};
+
+// Linear grid of the prefill kernels (grid_pos): num_q_tiles x 8 x batch workgroups; 0 when the launch's work-item
+// count would not fit the 32-bit grid size.
+inline unsigned prefill_grid(int num_q_tiles, int batch, int threads) {
+  const long n = (long)num_q_tiles * kHeadsKV * batch;
+  return n * threads > 0xFFFFFFFFL ? 0u : (unsigned)n;
+}
+
+}  // namespace abkv

@@ -57,7 +57,9 @@ def profiled_mfma_util(name: str):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 300 for serving, about 11 s of GPU work, so that a sampler of the "
+                         "GPU's busy state running beside the bench sees the timed region; 10 otherwise)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=None, help="default: 64 for full_model, 256 otherwise")
     ap.add_argument("--seed", type=int, default=0)
@@ -73,6 +75,8 @@ def parse():
     args = ap.parse_args()
     if args.batch is None:
         args.batch = 64 if args.workload == "full_model" else 256
+    if args.steps is None:
+        args.steps = 300 if args.workload == "serving" else 10
     return args
 
 
