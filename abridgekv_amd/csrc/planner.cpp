@@ -670,6 +670,257 @@ int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t tru
   return at;
 }
 
+namespace {
+
+// Run descriptor of abkv_planner_take_move_runs (int32 fields; layout shared with moves_expand_kernel).
+constexpr int kRunRemovalsMax = 8;
+constexpr int kRunFields = 14 + 2 * kRunRemovalsMax;
+
+// The row map of one (request, group) run in closed form. Final row i (relative to lo) came from lo + f(i): undoing
+// the removals last to first adds removal k's length exactly from the first final row whose partially undone
+// position reaches the removal's start, so f(i) = i + c[J(i)] with tau sorted ascending, c the running sums of the
+// lengths in that order and J(i) the number of thresholds <= i.
+struct RowMap {
+  int m = 0;
+  int64_t tau[kRunRemovalsMax], c[kRunRemovalsMax];
+  int64_t f(int64_t x) const {
+    int64_t add = 0;
+    for (int j = 0; j < m; ++j) add = x >= tau[j] ? c[j] : add;
+    return x + add;
+  }
+  // smallest x >= 0 with f(x) >= y
+  int64_t inv(int64_t y) const {
+    for (int j = 0; j <= m; ++j) {
+      const int64_t lo = j == 0 ? 0 : tau[j - 1], add = j == 0 ? 0 : c[j - 1];
+      const int64_t x = std::max(lo, y - add);
+      if (j == m || x < tau[j]) return x;
+    }
+    return y;
+  }
+};
+
+// Thresholds of the removals of one run (start, len in the coordinates the earlier removals left, relative to lo):
+// false when there are more than kRunRemovalsMax non-empty removals.
+bool build_row_map(const std::vector<abkv::Removal>& rm, int64_t lo, RowMap& out) {
+  int64_t tau[kRunRemovalsMax], len[kRunRemovalsMax];
+  int m = 0;
+  for (size_t k = rm.size(); k-- > 0;) {               // last removal first: its threshold is its own start
+    const int64_t L = rm[k].end - rm[k].start;
+    if (L <= 0) continue;
+    if (m == kRunRemovalsMax) return false;
+    // smallest x with x + (lengths of the later removals whose thresholds are <= x) >= start - lo
+    RowMap later;
+    later.m = m;
+    int order[kRunRemovalsMax];
+    for (int j = 0; j < m; ++j) order[j] = j;
+    std::sort(order, order + m, [&](int a, int b) { return tau[a] < tau[b]; });
+    int64_t run = 0;
+    for (int j = 0; j < m; ++j) {
+      later.tau[j] = tau[order[j]];
+      run += len[order[j]];
+      later.c[j] = run;
+    }
+    tau[m] = later.inv(rm[k].start - lo);
+    len[m] = L;
+    ++m;
+  }
+  int order[kRunRemovalsMax];
+  for (int j = 0; j < m; ++j) order[j] = j;
+  std::stable_sort(order, order + m, [&](int a, int b) { return tau[a] < tau[b]; });
+  out.m = m;
+  int64_t run = 0;
+  for (int j = 0; j < m; ++j) {
+    out.tau[j] = tau[order[j]];
+    run += len[order[j]];
+    out.c[j] = run;
+  }
+  return true;
+}
+
+}  // namespace
+
+// Sizes of abkv_planner_take_move_runs for the pending step: runs (records) and pages (int32) it will write.
+int abkv_planner_pending_run_sizes(void* h, int64_t* n_runs, int64_t* n_pages) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p) return ABKV_ERR_ARG;
+  int64_t runs = 0, pages = 0;
+  for (int64_t rid : p->trunc_order) {
+    Request* r = find_req(p, rid);
+    for (auto& st : r->step) {
+      if (st.removals.empty()) continue;
+      ++runs;
+      int64_t lo = st.removals[0].start;
+      for (auto& rm : st.removals) lo = std::min(lo, rm.start);
+      pages += p->page_of(std::max<int64_t>(st.removals.front().active - 1, lo)) - p->page_of(lo) + 1;
+    }
+  }
+  if (n_runs) *n_runs = runs;
+  if (n_pages) *n_pages = pages;
+  return ABKV_OK;
+}
+
+// The step's fused moves as run descriptors that abkv_moves_expand turns into exactly the move lists
+// abkv_planner_take_moves_packed writes (same index, same element order), so the host does O(runs + pages) work and
+// the device the O(rows) part. Per (request, group) run with moved rows, one record of kRunFields int32:
+//   0 n (rows of the run), 1 lo_w (the run's first row within its page window), 2 pages_at, 3 ord_at and 4 free_at
+//   (int32 element positions in `out` of the run's first ordered / independent op), 5 n_chained, 6 n_free,
+//   7 seg_at (-1: the run has no ordered op) and 8 its segment offset, 9 m, 10 t_star (first moved row),
+//   11 a_end (rows [t_star, a_end) read a row the run also writes), 12 pages in the window, 13 unused, 14.. tau[m],
+//   then c[m] at 14 + kRunRemovalsMax
+// pages: each run's page window (the pages of rows lo .. the run's last source row). groups [num_groups, 4] =
+// (offs_at, n_segments, end of the section's padding, 0) for the offsets' first entry and padding. index as
+// abkv_planner_take_moves_packed. sizes = (records written, pages written, int32 elements of `out`). Clears the step as
+// take_moves_packed does. ABKV_ERR_CAPACITY (nothing cleared) or ABKV_ERR_ARG (page size not a power of two, more
+// than kRunRemovalsMax removals in one run, or a step interleaved with an allocation).
+int abkv_planner_take_move_runs(void* h, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc, int32_t* runs,
+                                int64_t runs_cap, int32_t* pages, int64_t pages_cap, int32_t* groups, int64_t* index,
+                                int64_t* sizes) {
+  Planner* p = static_cast<Planner*>(h);
+  if (!p || !runs || !pages || !groups || !index || !sizes) return ABKV_ERR_ARG;
+  if (p->bs_shift < 0) {
+    p->last_error = "move runs need a power-of-two page size";
+    return ABKV_ERR_ARG;
+  }
+  for (int64_t rid : p->trunc_order)
+    for (auto& st : find_req(p, rid)->step)
+      if (st.stale) {
+        p->last_error = "span removals of one step were interleaved with an allocation: take the step outputs "
+                        "once per scheduler step";
+        return ABKV_ERR_ARG;
+      }
+  int64_t need_runs = 0, need_pages = 0, need_trunc = (int64_t)p->trunc_order.size();
+  abkv_planner_pending_run_sizes(h, &need_runs, &need_pages);
+  if ((trunc_rows && need_trunc > trunc_cap) || need_runs > runs_cap || need_pages > pages_cap)
+    return ABKV_ERR_CAPACITY;
+  const int G = p->num_groups;
+  struct RunInfo {
+    int g;
+    int64_t lo, n, n_ch, n_moved, t_star, a_end;
+    RowMap map;
+    const std::vector<int32_t>* blocks;
+    int64_t win_lo, win_n;
+  };
+  std::vector<RunInfo> infos;
+  infos.reserve((size_t)need_runs);
+  std::vector<int64_t> n_ord_g((size_t)G, 0), n_free_g((size_t)G, 0), n_seg_g((size_t)G, 0);
+  for (int64_t rid : p->trunc_order) {
+    Request* r = find_req(p, rid);
+    for (int g = 0; g < G; ++g) {
+      const auto& st = r->step[g];
+      if (st.removals.empty()) continue;
+      RunInfo ri;
+      ri.g = g;
+      int64_t lo = st.removals[0].start, removed = 0;
+      for (auto& rm : st.removals) {
+        lo = std::min(lo, rm.start);
+        removed += rm.end - rm.start;
+      }
+      ri.lo = lo;
+      ri.n = std::max<int64_t>(st.removals.front().active - lo - removed, 0);
+      if (!build_row_map(st.removals, lo, ri.map)) {
+        p->last_error = "more than " + std::to_string(kRunRemovalsMax) + " span removals of one request and group "
+                        "in one step";
+        return ABKV_ERR_ARG;
+      }
+      // moved rows [t_star, n); A = moved rows whose source is a row of the run, [t_star, a_end); B = f(A); the
+      // ordered ops are A u B (|B| = |A|, |A n B| = rows of A whose source lies in A)
+      ri.t_star = ri.map.m ? std::min(ri.map.tau[0], ri.n) : ri.n;
+      ri.n_moved = ri.n - ri.t_star;
+      ri.a_end = std::max(std::min(ri.map.inv(ri.n), ri.n), ri.t_star);
+      const int64_t nA = ri.a_end - ri.t_star;
+      const int64_t nAB = std::max<int64_t>(std::min(ri.a_end, ri.map.inv(ri.a_end)) - ri.t_star, 0);
+      ri.n_ch = 2 * nA - nAB;
+      ri.blocks = &st.blocks_before;
+      ri.win_lo = p->page_of(lo);
+      ri.win_n = p->page_of(std::max<int64_t>(st.removals.front().active - 1, lo)) - ri.win_lo + 1;
+      if (ri.win_lo + ri.win_n > (int64_t)st.blocks_before.size()) {
+        p->last_error = "a run's rows lie past its page list";
+        return ABKV_ERR_ARG;
+      }
+      n_ord_g[(size_t)g] += ri.n_ch;
+      n_free_g[(size_t)g] += ri.n_moved - ri.n_ch;
+      n_seg_g[(size_t)g] += ri.n_ch > 0;
+      infos.push_back(ri);
+    }
+  }
+  // the layout of abkv_planner_take_moves_packed
+  std::vector<int64_t> ops_at((size_t)G), offs_at((size_t)G), ord_cur((size_t)G, 0), free_cur((size_t)G, 0),
+      seg_cur((size_t)G, 0);
+  int64_t at = 0;
+  for (int g = 0; g < G; ++g) {
+    const int64_t n_ord = n_ord_g[(size_t)g], n_free = n_free_g[(size_t)g], n_seg = n_seg_g[(size_t)g];
+    const int64_t pad = (n_seg + 1 + 3) & ~(int64_t)3;
+    ops_at[(size_t)g] = at;
+    offs_at[(size_t)g] = at + 4 * (n_ord + n_free);
+    int64_t* ix = index + 5 * g;
+    ix[0] = at;
+    ix[1] = n_ord + n_free;
+    ix[2] = offs_at[(size_t)g];
+    ix[3] = n_seg;
+    ix[4] = n_free;
+    groups[4 * g + 0] = (int32_t)offs_at[(size_t)g];
+    groups[4 * g + 1] = (int32_t)n_seg;
+    groups[4 * g + 2] = (int32_t)(offs_at[(size_t)g] + pad);
+    groups[4 * g + 3] = 0;
+    at += 4 * (n_ord + n_free) + pad;
+  }
+  if (at > INT32_MAX) {
+    p->last_error = "move lists exceed 2^31 int32 elements";
+    return ABKV_ERR_ARG;
+  }
+  int64_t nr = 0, np = 0;
+  for (const RunInfo& ri : infos) {
+    const size_t g = (size_t)ri.g;
+    const int64_t ord_base = ord_cur[g], free_base = free_cur[g];
+    ord_cur[g] += ri.n_ch;
+    free_cur[g] += ri.n_moved - ri.n_ch;
+    int64_t seg_at = -1;
+    if (ri.n_ch > 0) seg_at = offs_at[g] + 1 + seg_cur[g]++;
+    if (ri.n_moved == 0) continue;
+    int32_t* rec = runs + kRunFields * nr++;
+    rec[0] = (int32_t)ri.n;
+    rec[1] = (int32_t)(ri.lo - ri.win_lo * p->block_size);
+    rec[2] = (int32_t)np;
+    rec[3] = (int32_t)(ops_at[g] + 4 * ord_base);
+    rec[4] = (int32_t)(ops_at[g] + 4 * (n_ord_g[g] + free_base));
+    rec[5] = (int32_t)ri.n_ch;
+    rec[6] = (int32_t)(ri.n_moved - ri.n_ch);
+    rec[7] = (int32_t)seg_at;
+    rec[8] = (int32_t)ord_cur[g];
+    rec[9] = ri.map.m;
+    rec[10] = (int32_t)ri.t_star;
+    rec[11] = (int32_t)ri.a_end;
+    rec[12] = (int32_t)ri.win_n;
+    rec[13] = 0;
+    for (int j = 0; j < kRunRemovalsMax; ++j) {
+      rec[14 + j] = j < ri.map.m ? (int32_t)ri.map.tau[j] : 0;
+      rec[14 + kRunRemovalsMax + j] = j < ri.map.m ? (int32_t)ri.map.c[j] : 0;
+    }
+    for (int64_t k = 0; k < ri.win_n; ++k) pages[np++] = (*ri.blocks)[(size_t)(ri.win_lo + k)];
+  }
+  int64_t t = 0;
+  if (trunc_rows) {
+    for (int64_t rid : p->trunc_order) {
+      Request* r = find_req(p, rid);
+      int64_t* row = trunc_rows + (1 + G) * t++;
+      row[0] = rid;
+      for (int g = 0; g < G; ++g) row[1 + g] = r->trunc[g];
+    }
+  }
+  if (n_trunc) *n_trunc = trunc_rows ? t : need_trunc;
+  sizes[0] = nr;
+  sizes[1] = np;
+  sizes[2] = at;
+  for (auto& kv : p->reqs) {
+    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    kv.second.has_trunc = false;
+    kv.second.alloc_after_removal = false;
+  }
+  p->pending_order.clear();
+  p->trunc_order.clear();
+  return ABKV_OK;
+}
+
 // Device-ready move lists of a step's fused rows (the fused_rows of abkv_planner_take_step_outputs; the rows of one
 // (request, group) contiguous and in emission order). Within a (request, group) run, op j *depends on* op i when
 // op j's destination is op i's source (j must store after i loads). Ops on such an edge are kept in one ordered

@@ -281,6 +281,55 @@ class KVPlanner:
         parts = [(g, *map(int, index[g])) for g in range(G) if index[g, 1] > 0]
         return tr[:got_tr.value], out[:rc], parts
 
+    RUN_FIELDS = 30                                        # int32 per record of abkv_planner_take_move_runs
+
+    def move_runs_capacity(self) -> int:
+        """int32 elements :meth:`take_step_move_runs` needs for the pending step (records, page windows, group table
+        and section alignment)."""
+        n_runs, n_pages = C.c_int64(0), C.c_int64(0)
+        self._lib.abkv_planner_pending_run_sizes(self._h, C.byref(n_runs), C.byref(n_pages))
+        return self.RUN_FIELDS * n_runs.value + n_pages.value + 4 * self.num_groups + 12
+
+    def take_step_move_runs(self, out: np.ndarray | None = None):
+        """The step's fused moves as run descriptors (abkv_planner_take_move_runs), then cleared: (trunc_rows,
+        buffer int32, layout, parts, n_elems). ``buffer`` holds three 16-byte aligned sections -- the records
+        [n_runs, RUN_FIELDS], the page windows, the group table [num_groups, 4] -- at ``layout`` = (runs_at, n_runs,
+        pages_at, groups_at); ``parts`` as :meth:`take_step_moves`; ``n_elems`` = int32 elements of the move lists
+        abkv_moves_expand writes from them (the buffer :meth:`take_step_moves` would return, element for element).
+        ``out``: a contiguous int32 array of at least :meth:`move_runs_capacity` elements (e.g. pinned memory)."""
+        n_runs, n_pages = C.c_int64(0), C.c_int64(0)
+        self._lib.abkv_planner_pending_run_sizes(self._h, C.byref(n_runs), C.byref(n_pages))
+        G = self.num_groups
+        r_cap, p_cap = n_runs.value, n_pages.value
+        runs_at = 0
+        pages_at = (runs_at + self.RUN_FIELDS * r_cap + 3) & ~3
+        groups_at = (pages_at + p_cap + 3) & ~3
+        need = groups_at + 4 * G
+        if out is None:
+            buf = self._bufs.get("runs")
+            if buf is None or buf.size < need:
+                buf = np.zeros(max(need, 2 * (0 if buf is None else buf.size)), np.int32)
+                self._bufs["runs"] = buf
+            out = buf
+        if out.dtype != np.int32 or not out.flags.c_contiguous or out.size < need:
+            raise ValueError(f"out must be a contiguous int32 array of at least {need} elements")
+        n_ops, n_tr, n_fu = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        self._lib.abkv_planner_pending_sizes(self._h, C.byref(n_ops), C.byref(n_tr), C.byref(n_fu))
+        tr = self._buffer("trunc", n_tr.value, 1 + G)
+        index = np.zeros((G, 5), np.int64)
+        sizes = np.zeros(3, np.int64)
+        got_tr = C.c_int64(0)
+        base = out.ctypes.data
+        rc = self._lib.abkv_planner_take_move_runs(
+            self._h, _i64(tr), tr.shape[0], C.byref(got_tr), C.cast(base + 4 * runs_at, C.POINTER(C.c_int32)), r_cap,
+            C.cast(base + 4 * pages_at, C.POINTER(C.c_int32)), p_cap, C.cast(base + 4 * groups_at, C.POINTER(C.c_int32)),
+            _i64(index), _i64(sizes))
+        if rc != ABKV_OK:
+            raise RuntimeError(f"take_move_runs failed ({rc}): {self._err()}")
+        parts = [(g, *map(int, index[g])) for g in range(G) if index[g, 1] > 0]
+        layout = (runs_at, int(sizes[0]), pages_at, groups_at)
+        return tr[:got_tr.value], out[:need], layout, parts, int(sizes[2])
+
     def apply_events(self, events: np.ndarray) -> None:
         """Apply a batch of scheduler events (see abkv_planner_apply_events); raises on the first failure."""
         ev = np.ascontiguousarray(events, dtype=np.int64).reshape(-1, 6)

@@ -131,6 +131,49 @@ class MoveUploader:
         return trunc, device_move_lists(self._dev[:n], parts)
 
 
+class MoveRunUploader:
+    """A planner step's fused moves as run descriptors (KVPlanner.take_step_move_runs): the records, page windows and
+    group table go to the device in one asynchronous copy from pinned memory, and abkv_moves_expand writes the move
+    lists there -- the same lists as :class:`MoveUploader`, element for element, with the per-row work on the device.
+    The pinned and device buffers are reused; a call first waits for the copy that last read the pinned one, and the
+    move lists of a call stay valid until the next call's expansion (on the same stream) overwrites them."""
+
+    def __init__(self, device, capacity: int = 1 << 16, out_capacity: int = 1 << 20):
+        self.device = device
+        self._pinned = torch.empty(capacity, dtype=torch.int32, pin_memory=True)
+        self._dev = torch.empty(capacity, dtype=torch.int32, device=device)
+        self._out = torch.empty(out_capacity, dtype=torch.int32, device=device)
+        self._done = None
+
+    def take(self, planner):
+        """(trunc_rows, [(group, ordered ops, seg_offsets, independent ops)] on the device) of the pending step."""
+        need = planner.move_runs_capacity()
+        if self._done is not None:
+            self._done.synchronize()
+        if need > self._pinned.numel():
+            self._pinned = torch.empty(2 * need, dtype=torch.int32, pin_memory=True)
+            self._dev = torch.empty(2 * need, dtype=torch.int32, device=self.device)
+        trunc, desc, (runs_at, n_runs, pages_at, groups_at), parts, n_elems = \
+            planner.take_step_move_runs(self._pinned.numpy())
+        if not parts:
+            return trunc, []
+        n = desc.size
+        self._dev[:n].copy_(self._pinned[:n], non_blocking=True)
+        self._done = torch.cuda.Event()
+        self._done.record()
+        if n_elems > self._out.numel():
+            self._out = torch.empty(2 * n_elems, dtype=torch.int32, device=self.device)
+        base = self._dev.data_ptr()
+        shift = int(planner.block_size).bit_length() - 1
+        rc = lib().abkv_moves_expand(C.c_void_p(base + 4 * runs_at), n_runs, C.c_void_p(base + 4 * pages_at),
+                                     C.c_void_p(base + 4 * groups_at), planner.num_groups, shift,
+                                     C.c_void_p(self._out.data_ptr()), n_elems,
+                                     C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"abkv_moves_expand failed ({rc})")
+        return trunc, device_move_lists(self._out[:n_elems], parts)
+
+
 def device_move_lists(dev_buf: torch.Tensor, parts):
     """Views of an uploaded :func:`pack_fused_moves` buffer: [(group, ordered ops, seg_offsets, independent ops)]."""
     out = []

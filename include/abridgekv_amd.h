@@ -323,6 +323,26 @@ int64_t abkv_moves_pack(const int64_t* fused_rows, int64_t n, int num_groups, in
  * scheduler.py:2060-2204 and sched/output.py:221-225, in the fused form.) */
 int64_t abkv_planner_take_moves_packed(void* planner, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc,
                                        int32_t* out, int64_t out_cap, int64_t* index);
+/* Capacities of abkv_planner_take_move_runs for the pending step: run records and page-window entries. */
+int abkv_planner_pending_run_sizes(void* planner, int64_t* n_runs, int64_t* n_pages);
+/* The same step outputs as abkv_planner_take_moves_packed with the per-row work left to the device: trunc_rows and
+ * index as there, and per (request, group) run with moved rows one record of 30 int32 (the run's row count, its first
+ * row in its page window, output positions and counts of its ordered and independent ops, its segment entry, and the
+ * run's row map in closed form: up to 8 thresholds with their running removal lengths), the runs' page windows and
+ * groups [num_groups, 4] (segment-offset position, n_segments, end of padding, 0). abkv_moves_expand turns them into
+ * the int32 move lists take_moves_packed writes, element for element. sizes = (records, page entries, int32 elements
+ * of the move lists). Clears the step. Returns 0, ABKV_ERR_CAPACITY (nothing cleared) or ABKV_ERR_ARG (page size not
+ * a power of two, more than 8 removals of one request and group in one step, rows past a page list, or a step
+ * interleaved with an allocation). (scheduler.py:2060-2204 and gpu_model_runner.py:1194-1224, the op rows generated
+ * on the device.) */
+int abkv_planner_take_move_runs(void* planner, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc,
+                                int32_t* runs, int64_t runs_cap, int32_t* pages, int64_t pages_cap, int32_t* groups,
+                                int64_t* index, int64_t* sizes);
+/* Device expansion of abkv_planner_take_move_runs' outputs (runs, pages, groups on the device; out_elems = sizes[2])
+ * into `out`, ready for abkv_kv_move_mixed. page_shift = log2(page size). One launch of n_runs + num_groups
+ * workgroups on `stream`; every store is bounds-checked against the record's counts and out_elems. */
+int abkv_moves_expand(const int32_t* runs, int n_runs, const int32_t* pages, const int32_t* groups, int num_groups,
+                      int page_shift, int32_t* out, long out_elems, abkv_stream_t stream);
 int64_t abkv_planner_num_free(void* planner);
 int64_t abkv_planner_free_queue(void* planner, int32_t* out, int64_t cap);
 int64_t abkv_planner_block_ids(void* planner, int64_t rid, int group, int32_t* out, int64_t cap);

@@ -1,0 +1,107 @@
+"""The planner's run descriptors (abkv_planner_take_move_runs) on the CPU: expanded with the closed-form row map the
+device kernel uses (restated here in numpy), they give exactly the move lists the planner writes row by row
+(abkv_planner_take_moves_packed) -- same index, same int32 elements -- on the 64-sequence compaction step and on
+multi-step served schedules, with the same truncation rows and free queue."""
+import numpy as np
+import pytest
+
+from abridgekv_amd import workloads
+from abridgekv_amd.planner import KVPlanner
+from tests.planner_harness import make_schedule, run_events
+
+PAGE = 16
+F, M = KVPlanner.RUN_FIELDS, 8
+
+
+def expand(buf, layout, n_elems, G, shift=4):
+    """Host restatement of moves_expand_kernel: final row i came from f(i) = i + c[J(i)]; ordered ops are the rows of
+    A = [t_star, a_end) and of B = f(A), ranked by |A before i| + |B before i| - |A n B before i|."""
+    runs_at, n_runs, pages_at, groups_at = layout
+    out = np.full(n_elems, -7, np.int32)                   # any element left unwritten shows up
+    gr = buf[groups_at: groups_at + 4 * G].reshape(G, 4)
+    for g in range(G):
+        out[gr[g, 0]] = 0
+        out[gr[g, 0] + 1 + gr[g, 1]: gr[g, 2]] = 0
+    pages = buf[pages_at:]
+    for rec in buf[runs_at: runs_at + F * n_runs].reshape(n_runs, F):
+        n, lo_w, pat, ord_at, free_at, n_ch, n_free, seg_at, seg_val, m, t_star, a_end, win_n = map(int, rec[:13])
+        tau = [int(x) for x in rec[14:14 + m]]
+        c = [int(x) for x in rec[14 + M:14 + M + m]]
+        if seg_at >= 0:
+            out[seg_at] = seg_val
+
+        def f(x):
+            add = 0
+            for j in range(m):
+                add = c[j] if x >= tau[j] else add
+            return x + add
+
+        def inv(y):
+            for j in range(m + 1):
+                x = max(0 if j == 0 else tau[j - 1], y - (0 if j == 0 else c[j - 1]))
+                if j == m or x < tau[j]:
+                    return x
+
+        for i in range(t_star, n):
+            src, dst = lo_w + f(i), lo_w + i
+            gi = inv(i)
+            ordered = i < a_end or (t_star <= gi < a_end and f(gi) == i)
+            rank = (min(i - t_star, a_end - t_star) + max(0, min(a_end, gi) - t_star)
+                    - max(0, min(a_end, inv(min(i, a_end))) - t_star))
+            if ordered:
+                assert 0 <= rank < n_ch
+                pos = ord_at + 4 * rank
+            else:
+                assert 0 <= i - t_star - rank < n_free
+                pos = free_at + 4 * (i - t_star - rank)
+            assert src >> shift < win_n and dst >> shift < win_n
+            out[pos:pos + 4] = (pages[pat + (src >> shift)], src & (PAGE - 1), pages[pat + (dst >> shift)],
+                                dst & (PAGE - 1))
+    return out
+
+
+def test_runs_expand_to_the_packed_lists_on_the_64_sequence_step():
+    a = workloads.build_compaction_state(64, seed=0, op_rows=False)
+    b = workloads.build_compaction_state(64, seed=0, op_rows=False)
+    a.planner.apply_events(a.pending)
+    b.planner.apply_events(b.pending)
+    tr_a, buf_a, parts_a = a.planner.take_step_moves()
+    tr_b, desc, layout, parts_b, n_elems = b.planner.take_step_move_runs()
+    assert parts_a == parts_b and np.array_equal(tr_a, tr_b) and n_elems == buf_a.size
+    assert desc.size * 5 < buf_a.size                      # the descriptors are a fraction of the lists
+    assert np.array_equal(expand(desc, layout, n_elems, b.planner.num_groups), buf_a)
+    assert a.planner.free_queue() == b.planner.free_queue()
+    for g in range(a.planner.num_groups):
+        assert a.planner.fill_block_table(list(range(64)), g, 2100).tolist() == \
+            b.planner.fill_block_table(list(range(64)), g, 2100).tolist()
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_runs_expand_to_the_packed_lists_on_served_schedules(seed):
+    quotas = (256, 64, 64, 128, 128, 128)
+    steps, _ = make_schedule(seed, 4, 512, 256, quotas, max_prompt=3 * 512, max_closed=3)
+    perm = np.random.default_rng(100 + seed).permutation(np.arange(1, 4000)).astype(np.int32)
+    pa = KVPlanner(4000, len(quotas), PAGE, free_order=perm, op_rows=False)
+    pb = KVPlanner(4000, len(quotas), PAGE, free_order=perm, op_rows=False)
+    seen_a, seen_b = set(), set()
+    checked = 0
+    for events in steps:
+        run_events(pa, events, seen_a)
+        run_events(pb, events, seen_b)
+        tr_a, buf_a, parts_a = pa.take_step_moves()
+        tr_b, desc, layout, parts_b, n_elems = pb.take_step_move_runs()
+        assert parts_a == parts_b and np.array_equal(tr_a, tr_b)
+        if parts_a:
+            assert np.array_equal(expand(desc, layout, n_elems, len(quotas)), buf_a)
+            checked += 1
+        assert pa.free_queue() == pb.free_queue()
+    assert checked >= 3
+
+
+def test_runs_need_a_large_enough_buffer():
+    b = workloads.build_compaction_state(8, seed=0, op_rows=False)
+    b.planner.apply_events(b.pending)
+    with pytest.raises(ValueError, match="at least"):
+        b.planner.take_step_move_runs(np.zeros(8, np.int32))
+    _, desc, layout, parts, n_elems = b.planner.take_step_move_runs()   # the step was not cleared by the failure
+    assert parts and n_elems > 0
