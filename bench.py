@@ -296,9 +296,10 @@ def bench_compaction(args, torch):
     """Config 2: 64 sequences each close one 512-token block (256 code rows computed) in one step; Qwen3-4B shape,
     36 layers in 6 quota groups, page 16, seeded fragmented free list. Timed: the planner step (the span removals with
     the reference's bookkeeping -- spans, page lists, truncations, free queue -- without the reference-format op
-    rows the fused path does not execute), the op upload (the planner writes the packed move lists into pinned memory,
-    one copy to the device) and the fused device moves; algorithmic bytes = 2 x (kept code rows x 4096 B) summed over
-    layers."""
+    rows the fused path does not execute), the move-list preparation (the planner writes per-run descriptors into
+    pinned memory, one copy to the device, and abkv_moves_expand writes the move lists there) and the fused device
+    moves; algorithmic bytes = 2 x (kept code rows x 4096 B) summed over layers. The host-written move lists of the
+    same step (abkv_planner_take_moves_packed + upload) are timed beside it."""
     from abridgekv_amd import ops, worker, workloads
 
     B = 64
@@ -313,19 +314,31 @@ def bench_compaction(args, torch):
         caches.append(c)
     by_group = [[caches[i] for i in range(len(layers))] for layers in st.groups]
     st.planner.reserve_outputs(0, 0, B)
+    st_host = workloads.build_compaction_state(B, seed=args.seed, op_rows=False)   # the same step, host-packed lists
+    st_host.planner.reserve_outputs(0, 0, B)
     uploader = worker.MoveUploader(dev, capacity=8 << 20)     # pinned staging, sized once (8 Mi int32)
-    warm = workloads.build_compaction_state(B, seed=args.seed + 1, op_rows=False)
-    warm.planner.apply_events(warm.pending)
-    uploader.take(warm.planner)                                # first use pays one-off runtime setup
+    run_uploader = worker.MoveRunUploader(dev, capacity=1 << 20, out_capacity=8 << 20)
+    for up in (uploader, run_uploader):                        # first use pays one-off runtime setup
+        warm = workloads.build_compaction_state(B, seed=args.seed + 1, op_rows=False)
+        warm.planner.apply_events(warm.pending)
+        up.take(warm.planner)
     torch.cuda.synchronize()
     del warm
     t0 = time.perf_counter()
     st.planner.apply_events(st.pending)                        # the planner step (host C++), reference semantics
     plan_s = time.perf_counter() - t0
     t0 = time.perf_counter()
-    _, prepared = uploader.take(st.planner)                    # move lists written into pinned memory, one upload
+    _, prepared = run_uploader.take(st.planner)                # run descriptors uploaded, move lists written on device
     torch.cuda.synchronize()
     prep_s = time.perf_counter() - t0
+    st_host.planner.apply_events(st_host.pending)
+    t0 = time.perf_counter()
+    _, prepared_host = uploader.take(st_host.planner)          # move lists written into pinned memory, one upload
+    torch.cuda.synchronize()
+    prep_host_s = time.perf_counter() - t0
+    for (ga, oa, sa, fa), (gb, ob, sb, fb) in zip(prepared, prepared_host):   # the two paths give the same lists
+        if ga != gb or not (torch.equal(oa, ob) and torch.equal(sa, sb) and torch.equal(fa, fb)):
+            raise RuntimeError("device-expanded move lists differ from the host-written ones")
     n_fused = sum(int(o.shape[0]) + int(f.shape[0]) for _, o, _, f in prepared)
     st_ref = workloads.build_compaction_state(B, seed=args.seed)
     outs = st_ref.compact()                                    # same step, reference-format op dict for comparison
@@ -391,7 +404,8 @@ def bench_compaction(args, torch):
                                  "slices of a buffer larger than the last-level cache",
                          "mover_frac_of_copy": gbps / copy_gbps},
         "same_pattern_probe": probe,
-        "planner_ms": plan_s * 1e3, "op_upload_ms": prep_s * 1e3, "device_moves_ms": t * 1e3,
+        "planner_ms": plan_s * 1e3, "move_list_prep_ms": prep_s * 1e3, "host_packed_upload_ms": prep_host_s * 1e3,
+        "device_moves_ms": t * 1e3,
         "reference_format_moves_ms": t_ref * 1e3, "reference_format_rows": ref_rows, "fused_rows": n_fused,
     }
 
