@@ -65,18 +65,19 @@ struct SpanIndex {
     long i = (long)(std::upper_bound(gap_physical.begin(), gap_physical.end(), phys) - gap_physical.begin()) - 1;
     return gap_logical[i] + (phys - gap_physical[i]);
   }
-  // spans = merge(spans + [span])
+  // spans = merge(spans + [span]): the list is already sorted and merged, so the new span goes to its sorted place
+  // and can only merge with the span before it and the spans after it that it reaches (no temporary list)
   void add_merged(std::pair<int64_t, int64_t> span) {
-    spans.push_back(span);
-    std::sort(spans.begin(), spans.end());
-    std::vector<std::pair<int64_t, int64_t>> merged;
-    for (auto& s : spans) {
-      if (!merged.empty() && s.first <= merged.back().second)
-        merged.back().second = std::max(merged.back().second, s.second);
-      else
-        merged.push_back(s);
+    size_t i = (size_t)(std::lower_bound(spans.begin(), spans.end(), span) - spans.begin());
+    spans.insert(spans.begin() + (long)i, span);
+    if (i > 0 && spans[i].first <= spans[i - 1].second) {
+      spans[i - 1].second = std::max(spans[i - 1].second, spans[i].second);
+      spans.erase(spans.begin() + (long)i);
+      --i;
     }
-    spans.swap(merged);
+    size_t j = i + 1;
+    while (j < spans.size() && spans[j].first <= spans[i].second) spans[i].second = std::max(spans[i].second, spans[j++].second);
+    spans.erase(spans.begin() + (long)(i + 1), spans.begin() + (long)j);
     rebuild();
   }
 };
@@ -119,6 +120,9 @@ struct Planner {
   std::vector<int64_t> trunc_order;       // rids with a truncation record, first-insertion order
   std::string last_error;
   bool op_rows = true;                    // build the reference-format op batches (off: fused moves only)
+  // scratch of abkv_planner_mask_token_span, kept between calls
+  std::vector<int> mts_targets;
+  std::vector<int32_t> mts_free;
   // scratch of abkv_planner_take_moves_packed, kept between steps
   std::vector<int64_t> mv_origin;
   std::vector<uint8_t> mv_chained;
@@ -308,7 +312,8 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
   }
   const int64_t masked = end - start;
   const int G = p->num_groups;
-  std::vector<int> targets;
+  std::vector<int>& targets = p->mts_targets;
+  targets.clear();
   if (groups == nullptr || n_groups < 0) {
     for (int g = 0; g < G; ++g) targets.push_back(g);
   } else {
@@ -367,7 +372,8 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
       }
       // _truncate_compacted_blocks
       const int64_t needed = (pl.active - removed + bs - 1) / bs;
-      std::vector<int32_t> to_free;
+      std::vector<int32_t>& to_free = p->mts_free;
+      to_free.clear();
       for (int64_t i = needed; i < (int64_t)blocks.size(); ++i) {
         if (blocks[i] != p->null_block) {
           to_free.push_back(blocks[i]);
