@@ -29,19 +29,29 @@ struct SpanIndex {
   std::vector<int64_t> starts, cumulative, gap_physical, gap_logical;
   int64_t total = 0;
 
-  void rebuild() {
-    starts.clear();
-    cumulative.clear();
-    gap_physical.assign(1, 0);
-    gap_logical.assign(1, 0);
-    total = 0;
-    for (auto& s : spans) {
-      starts.push_back(s.first);
-      total += s.second - s.first;
-      cumulative.push_back(total);
-      gap_physical.push_back(s.second - total);
-      gap_logical.push_back(s.second);
+  void rebuild() { rebuild_from(0); }
+  // the derived arrays of spans[from:] (entries before `from` are unchanged by an insertion or merge at `from`)
+  void rebuild_from(size_t from) {
+    const size_t n = spans.size();
+    starts.resize(n);
+    cumulative.resize(n);
+    gap_physical.resize(n + 1);
+    gap_logical.resize(n + 1);
+    gap_physical[0] = 0;
+    gap_logical[0] = 0;
+    total = from > 0 ? cumulative[from - 1] : 0;
+    for (size_t k = from; k < n; ++k) {
+      starts[k] = spans[k].first;
+      total += spans[k].second - spans[k].first;
+      cumulative[k] = total;
+      gap_physical[k + 1] = spans[k].second - total;
+      gap_logical[k + 1] = spans[k].second;
     }
+  }
+  // some span overlaps [start, end) (the spans are sorted and disjoint)
+  bool overlaps(int64_t start, int64_t end) const {
+    long i = idx_le(end - 1);                     // the last span starting before end
+    return i >= 0 && spans[(size_t)i].second > start;
   }
   // bisect_right(starts, pos) - 1
   long idx_le(int64_t pos) const {
@@ -78,7 +88,7 @@ struct SpanIndex {
     size_t j = i + 1;
     while (j < spans.size() && spans[j].first <= spans[i].second) spans[i].second = std::max(spans[i].second, spans[j++].second);
     spans.erase(spans.begin() + (long)(i + 1), spans.begin() + (long)j);
-    rebuild();
+    rebuild_from(i);
   }
 };
 
@@ -331,11 +341,10 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
       p->last_error = "KV cache group " + std::to_string(g) + " out of range";
       return ABKV_ERR_SPAN;
     }
-    for (auto& s : r->spans[g].spans)
-      if (start < s.second && end > s.first) {
-        p->last_error = "Cannot compact an already-removed token span (group " + std::to_string(g) + ")";
-        return ABKV_ERR_SPAN;
-      }
+    if (r->spans[g].overlaps(start, end)) {
+      p->last_error = "Cannot compact an already-removed token span (group " + std::to_string(g) + ")";
+      return ABKV_ERR_SPAN;
+    }
     const int64_t ps = r->spans[g].l2p(start), pe = r->spans[g].l2p(end);
     if (pe - ps != masked) {
       p->last_error = "Logical span does not map to one active physical span (group " + std::to_string(g) + ")";
