@@ -198,3 +198,24 @@ def test_shape_errors_raise_before_launch():
         ops.decode_attention(torch.zeros((1, 32, 128), dtype=torch.bfloat16, device=dev), kv.float(),
                              torch.zeros((1, 2), dtype=torch.int32, device=dev),
                              torch.ones(1, dtype=torch.int32, device=dev), 0.1)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_seeded_random_batches(seed):
+    """Seeded random batches: sizes 1..40, lengths log-uniform in [1, 6000], split sizes of 2..48 pages, query scales
+    0.1..4 (flat to peaked softmax), stale rows garbage; every sequence against the fp64 oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 41))
+    lens = np.exp(rng.uniform(0, np.log(6000), B)).astype(int).clip(1, 6000).tolist()
+    split = [2, 4, 6, 8, 16, 48, 64][seed % 7]
+    scale = float(rng.choice([0.1, 1.0, 4.0]))
+    ks = [rng.standard_normal((n, 8, 128)) for n in lens]
+    vs = [rng.standard_normal((n, 8, 128)) for n in lens]
+    q = (rng.standard_normal((B, 32, 128)) * scale).astype(np.float32)
+    pages = sum(-(-n // 16) for n in lens) + 8
+    cache, tables, sl = _paged_cache(ks, vs, pages, rng, garbage=30.0)
+    print(f"case: seed {seed} B={B} max_len={max(lens)} split={split} q_scale={scale}", flush=True)
+    out, lse = _run(q, cache, tables, sl, split_pages=split)
+    ref_out, ref_lse = _oracle(q, cache, tables, sl)
+    assert np.abs(out - ref_out).max() <= TOL
+    assert np.abs(lse - ref_lse).max() <= TOL
