@@ -155,3 +155,19 @@ def test_config4_full_size_sampled_rows(prompts, quota):
         got_l = lse[b].cpu().numpy().T[rows]
         worst = max(worst, float(np.abs(got_o - ref_o).max()), float(np.abs(got_l - ref_l).max()))
     assert worst <= TOL, worst
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_seeded_random_layouts(seed):
+    """Seeded random layouts: block sizes aligned to the 64-row tiles or not, raw prompts anywhere in the first blocks,
+    per-KV-head code quotas in [1, K], and (for odd seeds) a static retained tail; against the fp64 oracle."""
+    rng = np.random.default_rng(2000 + seed)
+    C = int(rng.choice([64, 128, 40, 24]))
+    K = int(rng.choice([64, 16, 8]))
+    N = int(rng.integers(2, 4))
+    B = int(rng.integers(1, 3))
+    prompt = [int(x) for x in rng.integers(0, N * C // 2 + 1, B)]
+    quota = np.repeat(rng.integers(1, K + 1, 8), 4).tolist()
+    tail = int(rng.integers(1, max(2, C - K))) if seed % 2 and C > K else 0
+    print(f"case: seed {seed} C={C} K={K} N={N} B={B} prompt={prompt} tail={tail}", flush=True)
+    _check(C=C, K=K, N=N, B=B, prompt_len=prompt, head_quota=quota, seed=10 + seed, tail=tail)
