@@ -137,9 +137,9 @@ class ServingPlan:
 
     def advance(self, m):
         """Settle the step described by ``m`` in the state machine (compaction of the blocks whose code run ended, via
-        the planner), then schedule the next step. Returns the step's fused moves as device move lists
-        (``KVPlanner.take_step_moves``: buffer, parts; valid until the next step) to execute on the device (after the
-        step's attention, before the next step's appends), or None."""
+        the planner), then schedule the next step. Returns the step's fused moves as the planner's run descriptors
+        (``KVPlanner.take_step_move_runs``: descriptors, layout, parts, move-list elements; valid until the next step)
+        for the device to expand and execute (after the step's attention, before the next step's appends), or None."""
         B, G = self.B, self.G
         touched: set[int] = set()
         planner = self.planner
@@ -156,8 +156,8 @@ class ServingPlan:
                 raise RuntimeError(f"request {r} stopped; the stress loop keeps every request decoding")
         moves = None
         if touched:
-            _, buf, parts = planner.take_step_moves()
-            moves = (buf, parts)
+            _, desc, layout, parts, n_elems = planner.take_step_move_runs()
+            moves = (desc, layout, parts, n_elems)
             self.stats["moved_rows"] += sum(n for _, _, n, _, _, _ in parts)
             for r in touched:
                 self.compacted[:, r] = planner.compacted_counts(r)
@@ -222,6 +222,9 @@ class ServingStress:
         self.scale = ops.default_scale()
         self.decode_events = None          # a list: (start, end) events around every decode launch are appended
         self._code_ws = torch.empty(0, dtype=torch.uint8, device=self.dev)
+        # move lists of the staged compaction: written by abkv_moves_expand after the step's upload and read by the
+        # next launch's moves, both on the one stream, so one buffer serves every step
+        self._moves_out = torch.empty(1 << 20, dtype=torch.int32, device=self.dev)
         self._meta = self._stage(plan.prepare())
 
     @property
@@ -259,9 +262,9 @@ class ServingStress:
             "tile_req": m["tiles"][:, 0].astype(np.int32).copy(),
             "tile_q0": m["tiles"][:, 1].astype(np.int32).copy(),
         }
-        mv_buf, mv_parts = moves if moves else (None, [])
+        mv_desc, mv_layout, mv_parts, mv_elems = moves if moves else (None, None, [], 0)
         if mv_parts:
-            parts["moves"] = mv_buf                          # per-group sections, each 16-byte aligned
+            parts["move_runs"] = mv_desc                     # records, page windows, group table (16-byte aligned)
         if self.tag:                                       # (request, logical position) of every new row
             tp = m["tok_pos"]
             parts["tags"] = np.stack([m["tok_req"], tp // 256, tp % 256], axis=1).astype(np.int32).reshape(-1)
@@ -292,7 +295,17 @@ class ServingStress:
         v["upd_comp"] = v["upd_comp"].view(G, rows.size)
         if self.tag:
             v["tags"] = v["tags"].view(n_tok, 3)
-        mv = device_move_lists(v["moves"], mv_parts) if mv_parts else []
+        mv = []
+        if mv_parts:                                       # the move lists, written on the device from the descriptors
+            if mv_elems > self._moves_out.numel():
+                self._moves_out = torch.empty(2 * mv_elems, dtype=torch.int32, device=self.dev)
+            base = v["move_runs"].data_ptr()
+            runs_at, n_runs, pages_at, groups_at = mv_layout
+            check(lib().abkv_moves_expand(C.c_void_p(base + 4 * runs_at), n_runs, C.c_void_p(base + 4 * pages_at),
+                                          C.c_void_p(base + 4 * groups_at), G, PAGE.bit_length() - 1,
+                                          C.c_void_p(self._moves_out.data_ptr()), mv_elems,
+                                          C.c_void_p(torch.cuda.current_stream().cuda_stream)), "abkv_moves_expand")
+            mv = device_move_lists(self._moves_out[:mv_elems], mv_parts)
         # key splits of the code step per group (its few query tiles cannot fill the GPU on their own)
         n_tiles = int(m["tiles"].shape[0])
         code_split = [ops.paged_split_plan(n_tiles, int(m["limits"][g].max())) if nc else (1, 0) for g in range(G)]

@@ -1,10 +1,12 @@
 """The serving loop's host half (ServingPlan) without a GPU: the state machine settles every step through the planner,
-and each step's compaction moves come out of the planner as device move lists. Every list, run through the CPU model
-of the mixed launch (random interleavings of the workgroups' load and store phases), equals gather-then-scatter of
-its own ops -- the ordering the lists promise holds on the moves the loop really produces."""
+and each step's compaction moves come out of the planner as run descriptors, expanded here with the host restatement
+of the device expansion into the mixed launch's move lists. Every list, run through the CPU model of the mixed launch
+(random interleavings of the workgroups' load and store phases), equals gather-then-scatter of its own ops -- the
+ordering the lists promise holds on the moves the loop really produces."""
 import numpy as np
 
 from tests.test_move_pack import gather_then_scatter, phases, run_model, unpack
+from tests.test_move_runs import expand
 
 
 def test_serving_plan_moves_are_exact_under_any_interleaving():
@@ -21,7 +23,8 @@ def test_serving_plan_moves_are_exact_under_any_interleaving():
         moves = plan.advance(plan.prepare())
         if moves is None:
             continue
-        buf, parts = moves
+        desc, layout, parts, n_elems = moves
+        buf = expand(desc, layout, n_elems, plan.G)
         for gid, (ops_g, offs, nf) in unpack(buf, parts).items():
             rows = np.concatenate([np.zeros((len(ops_g), 2), np.int64), ops_g.astype(np.int64)], axis=1)
             ref = gather_then_scatter(cache, rows)
