@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256) void moves_expand_kernel(const int32_t* __rest
     for (int j = 1; j <= kRunRemovalsMax; ++j) {
       if (found || j > m) break;
       const int cand = max(tau[j - 1], y - c[j - 1]);
-      if (j == m || cand < tau[j]) {
+      if (j == m || (j < kRunRemovalsMax && cand < tau[j])) {
         x = cand;
         found = true;
       }

@@ -81,3 +81,19 @@ def test_mover_fed_from_device_lists_leaves_the_same_cache():
     torch.cuda.synchronize()
     assert torch.equal(tag_a, tag_b)
     assert not torch.equal(tag_a, torch.arange(P * words, dtype=torch.int32, device=dev))   # rows did move
+
+
+def test_expansion_of_eight_scrambled_removals():
+    """Eight span removals of one request in one step, in a scrambled order (the row map's largest case)."""
+    dev = torch.device("cuda")
+    pa, pb = (KVPlanner(200, 1, PAGE, op_rows=False) for _ in range(2))
+    for p in (pa, pb):
+        p.add_request(7)
+        assert p.allocate_slots(7, 1000) is not None
+        p.set_num_computed_tokens(7, 1000)
+        for k in range(8):
+            s = 40 + 100 * ((5 * k) % 8)
+            assert p.mask_token_span(7, s, s + 10 + k).success
+    print("case: eight removals", flush=True)
+    buf_a, got, parts, _ = _host_and_device(pa, pb, dev, worker.MoveRunUploader(dev))
+    assert parts and np.array_equal(got, buf_a)

@@ -105,3 +105,27 @@ def test_runs_need_a_large_enough_buffer():
         b.planner.take_step_move_runs(np.zeros(8, np.int32))
     _, desc, layout, parts, n_elems = b.planner.take_step_move_runs()   # the step was not cleared by the failure
     assert parts and n_elems > 0
+
+
+@pytest.mark.parametrize("n_removals", [8, 9])
+def test_many_removals_in_one_step(n_removals):
+    """Up to eight span removals of one request and group in one step expand to the packed lists; a ninth is refused
+    with the planner's message (the step is left pending, so the host-written lists can still be taken)."""
+    pa, pb = (KVPlanner(200, 1, PAGE, op_rows=False) for _ in range(2))
+    for p in (pa, pb):
+        p.add_request(7)
+        assert p.allocate_slots(7, 1000) is not None
+        p.set_num_computed_tokens(7, 1000)
+        for k in range(n_removals):                         # disjoint logical spans in a scrambled order
+            s = 40 + 100 * ((5 * k) % n_removals)
+            assert p.mask_token_span(7, s, s + 10 + k).success
+    tr_a, buf_a, parts_a = pa.take_step_moves()
+    if n_removals <= 8:
+        tr_b, desc, layout, parts_b, n_elems = pb.take_step_move_runs()
+        assert parts_a == parts_b and np.array_equal(tr_a, tr_b)
+        assert np.array_equal(expand(desc, layout, n_elems, 1), buf_a)
+    else:
+        with pytest.raises(RuntimeError, match="more than 8 span removals"):
+            pb.take_step_move_runs()
+        tr_b, buf_b, parts_b = pb.take_step_moves()
+        assert parts_a == parts_b and np.array_equal(buf_a, buf_b)
