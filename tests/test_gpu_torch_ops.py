@@ -4,6 +4,8 @@ into a HIP graph and replayed compute bit-identically to the direct (ctypes) cal
 The compiled caller uses the aot_eager backend: dynamo traces the whole caller as one graph (fullgraph) and AOT
 autograd functionalises the in-place ops, with no generated kernels around ours. Graph replays run with eager work and
 synchronisations between them, each against a fresh eager result."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -55,6 +57,17 @@ def _inputs(seed=0):
     d["mx"] = torch.from_numpy(run(3, 100, 16).astype(np.int32)).to(dev)
     d["mx_free"] = torch.from_numpy(run(4, 200, 64).astype(np.int32)).to(dev)
     d["mx_offs"] = torch.tensor([0, 32], dtype=torch.int32, device=dev)
+    # the planner's run descriptors of a step with two span removals (the device expansion of its move lists)
+    from abridgekv_amd.planner import KVPlanner
+    plan = KVPlanner(200, 1, 16, op_rows=False)
+    plan.add_request(7)
+    assert plan.allocate_slots(7, 1000) is not None
+    plan.set_num_computed_tokens(7, 1000)
+    assert plan.mask_token_span(7, 300, 340).success and plan.mask_token_span(7, 100, 164).success
+    _, desc, (r_at, n_runs, p_at, g_at), _, n_el = plan.take_step_move_runs()
+    dd = torch.from_numpy(desc.copy()).to(dev)
+    d["mr_runs"], d["mr_pages"], d["mr_groups"] = dd[r_at: r_at + 30 * n_runs], dd[p_at: g_at], dd[g_at: g_at + 4]
+    d["mr_n"] = n_el
     # masked prefill (C=64, K=16, N=3), 2 sequences, raw prompt 40 / 0
     S0 = 3 * 80
     d["pq"] = torch.randn((2, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
@@ -70,7 +83,8 @@ def _outputs(d):
     return dict(slots=torch.empty(B, dtype=torch.int64, device=dev), out=torch.empty_like(d["q"]),
                 lse=torch.empty((B, 32), dtype=torch.float32, device=dev), cout=torch.empty_like(d["cq"]),
                 clse=torch.empty((d["cq"].shape[0], 32), dtype=torch.float32, device=dev),
-                pout=torch.empty_like(d["pq"]), plse=torch.empty((2, 32, d["pq"].shape[1]), device=dev))
+                pout=torch.empty_like(d["pq"]), plse=torch.empty((2, 32, d["pq"].shape[1]), device=dev),
+                mvout=torch.empty(d["mr_n"], dtype=torch.int32, device=dev))
 
 
 def _via_torch_ops(d, o):
@@ -81,6 +95,7 @@ def _via_torch_ops(d, o):
                      d["bt"].shape[1] * 16 - 1)
     A.kv_move_segments([d["cache"]], d["mv"], d["offs"])
     A.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
+    A.moves_expand(d["mr_runs"], d["mr_pages"], d["mr_groups"], 4, o["mvout"], d["mr_n"])
     A.decode_attn(d["q"], d["cache"], d["bt"], d["lens"], scale, d["bt"].shape[1], 8, o["out"], o["lse"], d["ws"])
     m = d["meta"]
     A.paged_prefill_attn(d["cq"], d["cache"], d["bt"], m[0:2], m[2:3], m[3:4], d["tiles"][0], d["tiles"][1], m[4:5],
@@ -96,6 +111,10 @@ def _via_ctypes(d, o):
                        kv_cache=d["cache"], max_position=d["bt"].shape[1] * 16 - 1)
     ops.kv_move_segments([d["cache"]], d["mv"], d["offs"])
     ops.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
+    r = d["mr_runs"]
+    assert ops.lib().abkv_moves_expand(C.c_void_p(r.data_ptr()), r.numel() // 30, C.c_void_p(d["mr_pages"].data_ptr()),
+                                       C.c_void_p(d["mr_groups"].data_ptr()), 1, 4, C.c_void_p(o["mvout"].data_ptr()),
+                                       d["mr_n"], C.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
     ops.decode_attention(d["q"], d["cache"], d["bt"], d["lens"], scale, out=o["out"], lse=o["lse"], split_pages=8,
                          workspace=d["ws"])
     m = d["meta"].cpu().numpy()
