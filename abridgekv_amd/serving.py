@@ -8,14 +8,17 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py) decides every req
 ``KVPlanner.mask_token_span`` as its ``mask_span`` callback: the compaction of a block whose code run ended is exactly
 the processor's ``_finish_block`` (processor.py:419-557), and the planner turns it into fused row moves.
 
-Device side, per step on one HIP stream: the previous step's compaction moves (``abkv_kv_move_mixed``); the slot of
-every new row per KV-cache group (``abkv_slot_mapping``: logical position minus the group's compacted count through
-the group's page table, gpu_model_runner.py:1579-1661 + block_table.py:186-197); then for every layer the fused RoPE +
-KV append (``abkv_rope_kv_append``, bitrev RoPE positions of the abridged layout computed on the device,
+Device side, per step: the previous step's compaction moves (``abkv_kv_move_mixed``); the slot of every new row per
+KV-cache group (``abkv_slot_mapping``: logical position minus the group's compacted count through the group's page
+table, gpu_model_runner.py:1579-1661 + block_table.py:186-197); then for every layer the fused RoPE + KV append
+(``abkv_rope_kv_append``, bitrev RoPE positions of the abridged layout computed on the device,
 config/compresslm.py:208-216), decode attention for decoding requests (``abkv_decode_attn``) and code-step attention for
-coding requests (``abkv_paged_prefill_attn``, non-causal, key limit ``code_start + quota`` per group). The host work and
-metadata of step s+1 are prepared while step s runs: the metadata travels in one pinned, asynchronous host-to-device
-copy per step.
+coding requests (``abkv_paged_prefill_attn``, non-causal, key limit ``code_start + quota`` per group). The decoding
+and the coding requests of a step are disjoint and attention reads only a request's own rows, so the two are
+independent sub-batches through all layers: the code rows' appends and attention run on a second stream of the same
+priority, forked once after the slot mapping and joined once at the end of the step, beside the decode layers on the
+first. The host work and metadata of step s+1 are prepared while step s runs: the metadata travels in one pinned,
+asynchronous host-to-device copy per step.
 
 Queries, keys and values are synthetic (N(0,1) bf16 pools from the seed): the loop measures the attention path,
 not a model.
@@ -182,13 +185,15 @@ class ServingStress:
     """Device half: caches, synthetic q/k/v pools, and the per-step launches of a :class:`ServingPlan`."""
 
     def __init__(self, T, P, layer_quotas=QWEN3_4B_LAYER_QUOTAS, seed=0, device="cuda", split_pages=None,
-                 growth_tokens=2048, C=BLOCK_C, K=CODES_K_MAX, tag=False):
+                 growth_tokens=2048, C=BLOCK_C, K=CODES_K_MAX, tag=False, concurrent_code_step=True,
+                 code_target_blocks=None):
         plan = ServingPlan(T, P, layer_quotas, seed=seed, growth_tokens=growth_tokens, C=C, K=K)
         self.plan = plan
         self.C, self.K, self.B, self.L, self.G, self.W = C, K, plan.B, plan.L, plan.G, plan.W
         self.st = plan.st
         self.dev = torch.device(device)
         self.split_pages = split_pages
+        self.code_target_blocks = code_target_blocks     # workgroups a code step's key splits aim at (None: the CUs)
         self.tag = tag
         B = self.B
         n_tensors = max(len(g) for g in self.st.groups)
@@ -221,6 +226,11 @@ class ServingStress:
         self._ring = 0
         self.scale = ops.default_scale()
         self.decode_events = None          # a list: (start, end) events around every decode launch are appended
+        # the code rows of a step on a side stream (default priority, as every stream here): one fork and one join
+        # event, created once and re-recorded every step
+        self._code_stream = torch.cuda.Stream(device=self.dev) if concurrent_code_step else None
+        self._fork = [torch.cuda.Event()] if concurrent_code_step else None
+        self._join = [torch.cuda.Event()] if concurrent_code_step else None
         self._code_ws = torch.empty(0, dtype=torch.uint8, device=self.dev)
         # move lists of the staged compaction: written by abkv_moves_expand after the step's upload and read by the
         # next launch's moves, both on the one stream, so one buffer serves every step
@@ -308,7 +318,8 @@ class ServingStress:
             mv = device_move_lists(self._moves_out[:mv_elems], mv_parts)
         # key splits of the code step per group (its few query tiles cannot fill the GPU on their own)
         n_tiles = int(m["tiles"].shape[0])
-        code_split = [ops.paged_split_plan(n_tiles, int(m["limits"][g].max())) if nc else (1, 0) for g in range(G)]
+        code_split = [ops.paged_split_plan(n_tiles, int(m["limits"][g].max()), self.code_target_blocks) if nc
+                      else (1, 0) for g in range(G)]
         need = max((lib().abkv_paged_prefill_workspace_size(nc * self.K, n) for n, _ in code_split if n > 1),
                    default=0)
         if need > self._code_ws.numel():
@@ -316,11 +327,18 @@ class ServingStress:
         return dict(m, view=v, n_tiles=n_tiles, n_upd=int(rows.size), moves=mv, code_split=code_split)
 
     # -- device: one step ---------------------------------------------------------------------------------------
+    def _layer_out(self, layer):
+        """Output rows of a layer's attention (one buffer shared by every layer: the loop measures attention, and the
+        next layer's queries come from the synthetic pool, not from this output)."""
+        return self.out
+
     def _launch_step(self, m):
         v, nd, nc, n_tok = m["view"], m["nd"], m["nc"], m["n_tok"]
-        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        main = torch.cuda.current_stream()
+        stream = C.c_void_p(main.cuda_stream)
+        side = self._code_stream if nc and nd else None
         L = lib()
-        q, k, val, out = self.q_pool, self.k_pool, self.v_pool, self.out
+        q, k, val = self.q_pool, self.k_pool, self.v_pool
         if m["moves"]:
             launch_moves(m["moves"], self.by_group)
         if m["n_upd"]:
@@ -335,16 +353,22 @@ class ServingStress:
                                       self.W, PAGE, _ptr(self.comp_dev[g]), _ptr(self.slots[g]), stream),
                   "abkv_slot_mapping")
         dec_bt = [self.bt_dev[g].index_select(0, v["dec_idx"].long()) if nd else None for g in range(self.G)]
-        cod_bt = [self.bt_dev[g].index_select(0, v["cod_idx"].long()) if nc else None for g in range(self.G)]
-        cs = self.cos_sin
+        m["cod_bt"] = [self.bt_dev[g].index_select(0, v["cod_idx"].long()) if nc else None for g in range(self.G)]
+        code_stream = C.c_void_p(side.cuda_stream) if side is not None else stream
+        if side is not None:
+            # The decoding and the coding requests of a step are disjoint, and attention reads only a request's own
+            # rows: the two are independent sub-batches through every layer. The code rows' appends and attention of
+            # all layers run on the side stream, forked once here and joined once at the end of the step; layer by
+            # layer, the decode launches are issued first.
+            self._fork[0].record(main)
+            side.wait_event(self._fork[0])
         for layer in range(self.L):
             g = int(self.st.layer_group[layer])
             cache = self.caches[int(self.st.layer_slot[layer])]
-            # RoPE of q and k at the bitrev positions of the abridged layout + KV append, one launch
-            check(L.abkv_rope_kv_append(_ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), _ptr(val),
-                                        val.stride(0), _ptr(v["tok_pos"]), n_tok, self.C, self.K, 0, _ptr(cs),
-                                        cs.shape[0], _ptr(self.slots[g]), _ptr(cache), cache.shape[0], stream),
-                  "abkv_rope_kv_append")
+            out = self._layer_out(layer)
+            # RoPE of q and k at the bitrev positions of the abridged layout + KV append, one launch (the decode rows
+            # only when the code rows run on the side stream)
+            self._append(layer, g, cache, 0, nd if side is not None else n_tok, v, stream)
             if nd:
                 if self.decode_events is not None:
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -359,16 +383,40 @@ class ServingStress:
                     e1.record()
                     self.decode_events.append((e0, e1))
             if nc:
-                qc, oc = q[nd:], out[nd:]
-                n_sp, sp_tiles = m["code_split"][g]
-                check(L.abkv_paged_prefill_attn(_ptr(qc), qc.stride(0), qc.stride(1), _ptr(cache), cache.shape[0],
-                                                _ptr(cod_bt[g]), self.W, self.W, _ptr(v["q_start"]),
-                                                _ptr(v["kv_start"][g]), _ptr(v["limits"][g]), None, _ptr(v["tile_req"]),
-                                                _ptr(v["tile_q0"]), m["n_tiles"], None, 0, C.c_float(self.scale),
-                                                _ptr(oc), oc.stride(0), oc.stride(1), None, nc * self.K, n_sp,
-                                                sp_tiles, _ptr(self._code_ws) if n_sp > 1 else None,
-                                                C.c_size_t(self._code_ws.numel() if n_sp > 1 else 0), stream),
-                      "abkv_paged_prefill_attn")
+                if side is not None:
+                    self._append(layer, g, cache, nd, n_tok, v, code_stream)
+                self._code_step(m, g, cache, out, code_stream)
+        if side is not None:
+            self._join[0].record(side)
+            main.wait_event(self._join[0])               # the next step's moves and appends follow the code rows
+
+    def _append(self, layer, g, cache, t0, t1, v, stream):
+        """RoPE of the q and k rows [t0, t1) of the step at the bitrev positions of the abridged layout, and their K/V
+        rows appended at their slots of group g."""
+        if t1 <= t0:
+            return
+        q, k, val, cs = self.q_pool, self.k_pool, self.v_pool, self.cos_sin
+        check(lib().abkv_rope_kv_append(C.c_void_p(q.data_ptr() + t0 * q.stride(0) * 2), q.stride(0), q.stride(1),
+                                        C.c_void_p(k.data_ptr() + t0 * k.stride(0) * 2), k.stride(0),
+                                        C.c_void_p(val.data_ptr() + t0 * val.stride(0) * 2), val.stride(0),
+                                        C.c_void_p(v["tok_pos"].data_ptr() + 8 * t0), t1 - t0, self.C, self.K, 0,
+                                        _ptr(cs), cs.shape[0], C.c_void_p(self.slots[g].data_ptr() + 8 * t0),
+                                        _ptr(cache), cache.shape[0], stream), "abkv_rope_kv_append")
+
+    def _code_step(self, m, g, cache, out, stream):
+        """Code-step attention of the step's coding requests over one layer of group g (non-causal, per-request key
+        limit code_start + quota)."""
+        v, nd, nc = m["view"], m["nd"], m["nc"]
+        qc, oc = self.q_pool[nd:], out[nd:]
+        n_sp, sp_tiles = m["code_split"][g]
+        check(lib().abkv_paged_prefill_attn(_ptr(qc), qc.stride(0), qc.stride(1), _ptr(cache), cache.shape[0],
+                                            _ptr(m["cod_bt"][g]), self.W, self.W, _ptr(v["q_start"]),
+                                            _ptr(v["kv_start"][g]), _ptr(v["limits"][g]), None, _ptr(v["tile_req"]),
+                                            _ptr(v["tile_q0"]), m["n_tiles"], None, 0, C.c_float(self.scale),
+                                            _ptr(oc), oc.stride(0), oc.stride(1), None, nc * self.K, n_sp,
+                                            sp_tiles, _ptr(self._code_ws) if n_sp > 1 else None,
+                                            C.c_size_t(self._code_ws.numel() if n_sp > 1 else 0), stream),
+              "abkv_paged_prefill_attn")
 
     def flush(self) -> None:
         """Execute the compaction moves staged for the next step now (e.g. before reading the cache)."""

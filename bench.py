@@ -66,10 +66,15 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=None,
                     help="pages per decode split (default: ops.auto_split_pages per launch: 48, 40 or 32)")
     ap.add_argument("--workload", choices=["serving", "saturated", "full_model", "config1", "prefill", "prefill_bwd",
-                                           "compaction", "packed", "code_step", "copy", "lds"],
+                                           "compaction", "packed", "code_step", "copy"],
                     default="serving")
     ap.add_argument("--code-requests", type=int, default=1,
                     help="code_step: requests coding in one launch (the serving stress averages ~0.5 per step)")
+    ap.add_argument("--serial-code-step", action="store_true",
+                    help="serving: run each layer's code step after its decode on one stream (for an A/B against "
+                         "the default, the code step on a second stream)")
+    ap.add_argument("--code-target-blocks", type=int, default=None,
+                    help="serving: workgroups a code step's key splits aim at (default: one per compute unit)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     args = ap.parse_args()
@@ -754,7 +759,8 @@ def bench_serving(args, torch):
     copy_bw = copy_bandwidth(torch)                            # before the 212 GB of caches are allocated
     t0 = time.perf_counter()
     s = ServingStress(T, P, seed=args.seed, split_pages=args.split_pages,
-                      growth_tokens=args.steps + args.warmup + 16)
+                      growth_tokens=args.steps + args.warmup + 16, concurrent_code_step=not args.serial_code_step,
+                      code_target_blocks=args.code_target_blocks)
     build_s = time.perf_counter() - t0
     for _ in range(args.warmup):
         s.step()
@@ -790,7 +796,9 @@ def bench_serving(args, torch):
                                f"groups 256/128/64, 32q/8kv, d128, bf16, page 16), B={B}, T~U[2048,32768], "
                                f"P~U[128,1024]; a request closing a 512-token block runs its 256 code rows next step "
                                f"and is compacted", "global_batch": B, "layers": s.L, "kv_groups": s.G,
-                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)"},
+                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)",
+                   "code_step_stream": "main (serial)" if args.serial_code_step else "second stream (concurrent)",
+                   "code_target_blocks": args.code_target_blocks or "compute units"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": profiled_traffic("decode_attn_serving_b256_pmc_traffic.md"),
@@ -922,42 +930,6 @@ def bench_copy(args, torch):
             "bytes_read_per_launch": n, "bytes_written_per_launch": n, "ms_per_step": t * 1e3, "steps": args.steps}
 
 
-def bench_lds(args, torch):
-    """LDS read throughput per CU (abkv_probe_lds_read in libabridgekv_probes.so): ds_read_b128 and the transposed
-    ds_read_b64_tr_b16 with the masked-prefill kernels' operand addressing, at 1 and 2 workgroups of 4 waves per CU
-    (the prefill kernels run 8 waves per CU). B/clk from the probe's shader-clock cycle counts, GB/s from events."""
-    import ctypes as C
-    from pathlib import Path
-
-    path = Path(__file__).resolve().parent / "abridgekv_amd" / "libabridgekv_probes.so"
-    fn = C.CDLL(str(path)).abkv_probe_lds_read
-    fn.restype = C.c_int
-    fn.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    iters = 20000
-    sink = torch.empty(2 * cus * 256, dtype=torch.int32, device="cuda")
-    cycles = torch.empty(2 * cus, dtype=torch.int64, device="cuda")
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    res = {}
-    for wpc in (1, 2):
-        for mode, name, bpi in ((0, "ds_read_b128", 1024), (1, "ds_read_b64_tr_b16", 512)):
-            n_wg = wpc * cus
-            for _ in range(max(args.warmup, 1)):
-                assert fn(mode, n_wg, iters, 37, C.c_void_p(sink.data_ptr()), C.c_void_p(cycles.data_ptr()), stream) == 0
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            assert fn(mode, n_wg, iters, 37, C.c_void_p(sink.data_ptr()), C.c_void_p(cycles.data_ptr()), stream) == 0
-            e.record()
-            torch.cuda.synchronize()
-            per_cu = wpc * 4 * iters * 8 * bpi
-            cyc = float(cycles[:n_wg].double().mean())
-            res[f"{name} {wpc} WG/CU"] = {"bytes_per_clk_per_cu": per_cu / cyc,
-                                          "gbps_per_cu": per_cu / (s.elapsed_time(e) / 1e3) / 1e9,
-                                          "clock_ghz": cyc / (s.elapsed_time(e) / 1e3) / 1e9}
-    return {"metric": "LDS read throughput per CU (probe)", "unit": "B/clk/CU", "cus": cus, "iters": iters,
-            "results": res}
-
-
 def main():
     args = parse()
     if args.gpus != 1:
@@ -966,11 +938,10 @@ def main():
         return 2
     import torch
 
-    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "code_step", "copy",
-                         "lds"):
+    if args.workload in ("serving", "config1", "prefill", "prefill_bwd", "compaction", "packed", "code_step", "copy"):
         res = {"serving": bench_serving, "config1": bench_config1, "prefill": bench_prefill,
                "prefill_bwd": bench_prefill_bwd, "compaction": bench_compaction, "packed": bench_packed,
-               "code_step": bench_code_step, "copy": bench_copy, "lds": bench_lds}[args.workload](args, torch)
+               "code_step": bench_code_step, "copy": bench_copy}[args.workload](args, torch)
         print(json.dumps(res), flush=True)
         return 0
 
@@ -1070,7 +1041,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (N(0,1) K/V pages and queries from the seed; page tables from the compaction planner)",
         "config": {"workload": wl, "global_batch": B, "layers": L, "kv_groups": G,
-                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)"},
+                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)",
+                   "code_step_stream": "main (serial)" if args.serial_code_step else "second stream (concurrent)",
+                   "code_target_blocks": args.code_target_blocks or "compute units"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": (profiled_traffic(traffic_profile) if args.seed == 0 and

@@ -29,7 +29,7 @@ def test_profile_readers_parse_committed_summaries():
 
 def test_every_workload_parses_with_defaults(monkeypatch):
     for wl in ("serving", "saturated", "full_model", "config1", "prefill", "prefill_bwd", "compaction", "packed",
-               "code_step", "copy", "lds"):
+               "code_step", "copy"):
         monkeypatch.setattr(sys, "argv", ["bench.py", "--workload", wl])
         a = bench.parse()
         assert a.workload == wl and a.gpus == 1 and a.steps > 0 and a.warmup >= 0

@@ -41,7 +41,7 @@ def test_probe_library_loads_and_exports_only_the_probe():
     path = _lib.LIB_PATH.parent / "libabridgekv_probes.so"
     ctypes.CDLL(str(path))
     out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True).stdout
-    assert set(re.findall(r" T (abkv_[a-z0-9_]+)", out)) == {"abkv_probe_row_copy", "abkv_probe_lds_read"}
+    assert set(re.findall(r" T (abkv_[a-z0-9_]+)", out)) == {"abkv_probe_row_copy"}
 
 
 def test_binding_table_matches_header():

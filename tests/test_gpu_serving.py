@@ -82,3 +82,47 @@ def test_serving_loop_served_geometry():
             ref, _ = od.decode_fp64(q[b].float().numpy(), rows[:, 0], rows[:, 1], 128 ** -0.5)
             ok, err = _close(out[b].float().cpu().numpy(), ref)
             assert ok, (g, b, err)
+
+
+def _per_layer_stress(concurrent, **kw):
+    """A serving loop that keeps every layer's attention output in a buffer of its own (the product shares one
+    buffer between layers), so a code step that read queries already rotated by the next layer's append would show."""
+    from abridgekv_amd.serving import ServingStress
+
+    class PerLayer(ServingStress):
+        def _layer_out(self, layer):
+            if not hasattr(self, "_outs"):
+                self._outs = [torch.zeros_like(self.out) for _ in range(self.L)]
+            return self._outs[layer]
+
+    return PerLayer(concurrent_code_step=concurrent, **kw)
+
+
+@pytest.mark.parametrize("geometry", ["small", "served"])
+def test_concurrent_code_step_matches_serial(geometry):
+    """The code step on its own stream (forked after the layer's append, joined before the next layer's) gives every
+    layer's decode and code-step rows bit-identical to the same loop with the code step after the decode on one
+    stream, on every step of a run with code steps and compaction."""
+    rng = np.random.default_rng(3)
+    if geometry == "small":
+        B, steps = 8, 140
+        kw = dict(T=rng.integers(200, 600, B), P=rng.integers(10, 150, B), layer_quotas=(16, 4, 8, 4, 16, 8), C=64,
+                  K=16, growth_tokens=256)
+    else:
+        B, steps = 16, 40
+        # every request 1..8 tokens short of a block boundary, so code steps run within the first steps
+        T = 512 * rng.integers(4, 10, B) - rng.integers(1, 9, B)
+        kw = dict(T=T, P=rng.integers(128, 1025, B), growth_tokens=steps + 64)
+    a = _per_layer_stress(True, seed=5, **kw)
+    b = _per_layer_stress(False, seed=5, **kw)
+    code_steps = 0
+    for _ in range(steps):
+        ma, mb = a.step(), b.step()
+        assert ma["nc"] == mb["nc"] and ma["nd"] == mb["nd"]
+        torch.cuda.synchronize()
+        n = ma["n_tok"]
+        for layer in range(a.L):
+            assert torch.equal(a._outs[layer][:n], b._outs[layer][:n]), (layer, ma["nc"])
+        code_steps += int(ma["nc"] > 0)
+    assert code_steps >= (4 if geometry == "small" else 2), code_steps
+    assert a.stats == b.stats
