@@ -85,7 +85,7 @@ SIGNATURES = {
     "abkv_planner_pending_run_sizes": (C.c_int, [_vp, _i64p, _i64p]),
     "abkv_planner_take_move_runs": (C.c_int, [_vp, _i64p, C.c_int64, _i64p, _i32p, C.c_int64, _i32p, C.c_int64, _i32p,
                                               _i64p, _i64p]),
-    "abkv_moves_expand": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, C.c_long, _vp]),
+    "abkv_moves_expand": (C.c_int, [_vp, C.c_int, _vp, C.c_long, _vp, C.c_int, C.c_int, _vp, C.c_long, _vp]),
     "abkv_planner_num_free": (C.c_int64, [_vp]),
     "abkv_planner_free_queue": (C.c_int64, [_vp, _i32p, C.c_int64]),
     "abkv_planner_block_ids": (C.c_int64, [_vp, C.c_int64, C.c_int, _i32p, C.c_int64]),

@@ -402,19 +402,22 @@ __global__ __launch_bounds__(256) void packed_capture_kernel(CaptureArgs a) {
 // ordered when it reads a row the run writes (i in A = [t_star, a_end)) or writes a row the run reads (i in B =
 // f(A)); its rank among the run's ordered ops is |A before i| + |B before i| - |A n B before i|, all three read off
 // the monotone map, and independent ops take the remaining ranks in row order. Workgroups past n_runs write each
-// group's first segment offset (0) and padding. Every store is checked against the run's counts and out_elems, and
-// every page read against the run's window, so a record that disagrees with the map writes nothing out of place.
+// group's first segment offset (0) and padding. Every store is checked against the run's counts and out_elems, every
+// page read against the run's window and the window against the n_pages entries of `pages`; negative positions,
+// rows and offsets are skipped. A record that disagrees with the map therefore writes nothing out of place and reads
+// nothing outside its inputs.
 constexpr int kRunRemovalsMax = 8;
 constexpr int kRunFields = 14 + 2 * kRunRemovalsMax;
 
 __global__ __launch_bounds__(256) void moves_expand_kernel(const int32_t* __restrict__ runs, int n_runs,
-                                                           const int32_t* __restrict__ pages,
+                                                           const int32_t* __restrict__ pages, long n_pages,
                                                            const int32_t* __restrict__ groups, int page_shift,
                                                            int32_t* __restrict__ out, long out_elems) {
   const int r = blockIdx.x;
   if (r >= n_runs) {
     const int32_t* gr = groups + 4 * (r - n_runs);
     const int offs_at = gr[0], n_seg = gr[1], pad_end = gr[2];
+    if (offs_at < 0 || n_seg < 0) return;
     if (threadIdx.x == 0 && offs_at < out_elems) out[offs_at] = 0;
     for (long k = (long)offs_at + 1 + n_seg + threadIdx.x; k < pad_end && k < out_elems; k += blockDim.x) out[k] = 0;
     return;
@@ -423,6 +426,7 @@ __global__ __launch_bounds__(256) void moves_expand_kernel(const int32_t* __rest
   const int n = rec[0], lo_w = rec[1], pages_at = rec[2], ord_at = rec[3], free_at = rec[4], n_ch = rec[5];
   const int n_free = rec[6], seg_at = rec[7], seg_val = rec[8], m = rec[9], t_star = rec[10], a_end = rec[11];
   const int win_n = rec[12];
+  if (pages_at < 0 || win_n < 0 || (long)pages_at + win_n > n_pages) return;   // window outside `pages`
   int tau[kRunRemovalsMax], c[kRunRemovalsMax];
 #pragma unroll
   for (int j = 0; j < kRunRemovalsMax; ++j) {
@@ -469,7 +473,7 @@ __global__ __launch_bounds__(256) void moves_expand_kernel(const int32_t* __rest
       pos = (long)free_at + 4L * fr;
     }
     const int sp = src >> page_shift, dp = dst >> page_shift;
-    if (pos < 0 || pos + 4 > out_elems || sp >= win_n || dp >= win_n || dst < 0) continue;
+    if (pos < 0 || pos + 4 > out_elems || src < 0 || dst < 0 || sp >= win_n || dp >= win_n) continue;
     int32_t* o = out + pos;
     o[0] = pages[pages_at + sp];
     o[1] = src & mask;
@@ -639,15 +643,16 @@ int abkv_packed_capture(const void* const* layer_kv, void* const* layer_pool, co
 // Device half of the planner's fused moves: the run descriptors of abkv_planner_take_move_runs (runs [n_runs, 30]
 // int32, their page windows, groups [num_groups, 4]) expanded into `out` (out_elems = sizes[2] of that call), the
 // move lists abkv_planner_take_moves_packed would write for the same step. page_shift = log2 of the page size.
-int abkv_moves_expand(const int32_t* runs, int n_runs, const int32_t* pages, const int32_t* groups, int num_groups,
-                      int page_shift, int32_t* out, long out_elems, hipStream_t stream) {
+int abkv_moves_expand(const int32_t* runs, int n_runs, const int32_t* pages, long n_pages, const int32_t* groups,
+                      int num_groups, int page_shift, int32_t* out, long out_elems, hipStream_t stream) {
   using namespace abkv;
-  if (n_runs < 0 || num_groups < 0 || page_shift < 0 || page_shift > 16 || out_elems < 0) return (int)hipErrorInvalidValue;
+  if (n_runs < 0 || n_pages < 0 || num_groups < 0 || page_shift < 0 || page_shift > 16 || out_elems < 0)
+    return (int)hipErrorInvalidValue;
   if (n_runs + num_groups == 0) return 0;
   if ((n_runs > 0 && (runs == nullptr || pages == nullptr)) || (num_groups > 0 && groups == nullptr) || out == nullptr)
     return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(moves_expand_kernel, dim3(n_runs + num_groups), dim3(256), 0, stream, runs, n_runs, pages,
-                     groups, page_shift, out, out_elems);
+                     n_pages, groups, page_shift, out, out_elems);
   return (int)hipGetLastError();
 }
 

@@ -33,7 +33,7 @@ import torch
 from . import ops
 from ._lib import check, lib
 from .backend import code_step_key_limits
-from .worker import device_move_lists, launch_moves
+from .worker import device_move_lists, launch_moves, take_step_move_lists
 from .workloads import (BLOCK_C, CODES_K_MAX, MAX_MODEL_LEN, QWEN3_4B_LAYER_QUOTAS, SAMPLED_TOKEN,
                         build_decode_state)
 
@@ -140,9 +140,10 @@ class ServingPlan:
 
     def advance(self, m):
         """Settle the step described by ``m`` in the state machine (compaction of the blocks whose code run ended, via
-        the planner), then schedule the next step. Returns the step's fused moves as the planner's run descriptors
-        (``KVPlanner.take_step_move_runs``: descriptors, layout, parts, move-list elements; valid until the next step)
-        for the device to expand and execute (after the step's attention, before the next step's appends), or None."""
+        the planner), then schedule the next step. Returns the step's fused moves (``worker.take_step_move_lists``:
+        the planner's run descriptors for the device to expand, or its host-written move lists when it refuses
+        descriptors for the step; valid until the next step) for the device to execute after the step's attention,
+        before the next step's appends, or None."""
         B, G = self.B, self.G
         touched: set[int] = set()
         planner = self.planner
@@ -159,9 +160,8 @@ class ServingPlan:
                 raise RuntimeError(f"request {r} stopped; the stress loop keeps every request decoding")
         moves = None
         if touched:
-            _, desc, layout, parts, n_elems = planner.take_step_move_runs()
-            moves = (desc, layout, parts, n_elems)
-            self.stats["moved_rows"] += sum(n for _, _, n, _, _, _ in parts)
+            moves = take_step_move_lists(planner)
+            self.stats["moved_rows"] += sum(n for _, _, n, _, _, _ in moves[3])
             for r in touched:
                 self.compacted[:, r] = planner.compacted_counts(r)
         self.stats["decode_tokens"] += int(m["nd"])
@@ -272,9 +272,10 @@ class ServingStress:
             "tile_req": m["tiles"][:, 0].astype(np.int32).copy(),
             "tile_q0": m["tiles"][:, 1].astype(np.int32).copy(),
         }
-        mv_desc, mv_layout, mv_parts, mv_elems = moves if moves else (None, None, [], 0)
+        mv_kind, mv_desc, mv_layout, mv_parts, mv_elems = moves if moves else (None, None, None, [], 0)
         if mv_parts:
-            parts["move_runs"] = mv_desc                     # records, page windows, group table (16-byte aligned)
+            # run descriptors (records, page windows, group table; 16-byte aligned sections), or the move lists
+            parts["move_runs" if mv_kind == "runs" else "move_lists"] = mv_desc
         if self.tag:                                       # (request, logical position) of every new row
             tp = m["tok_pos"]
             parts["tags"] = np.stack([m["tok_req"], tp // 256, tp % 256], axis=1).astype(np.int32).reshape(-1)
@@ -306,13 +307,16 @@ class ServingStress:
         if self.tag:
             v["tags"] = v["tags"].view(n_tok, 3)
         mv = []
-        if mv_parts:                                       # the move lists, written on the device from the descriptors
+        if mv_parts and mv_kind == "packed":
+            mv = device_move_lists(v["move_lists"], mv_parts)
+        elif mv_parts:                                     # the move lists, written on the device from the descriptors
             if mv_elems > self._moves_out.numel():
                 self._moves_out = torch.empty(2 * mv_elems, dtype=torch.int32, device=self.dev)
             base = v["move_runs"].data_ptr()
             runs_at, n_runs, pages_at, groups_at = mv_layout
             check(lib().abkv_moves_expand(C.c_void_p(base + 4 * runs_at), n_runs, C.c_void_p(base + 4 * pages_at),
-                                          C.c_void_p(base + 4 * groups_at), G, PAGE.bit_length() - 1,
+                                          groups_at - pages_at, C.c_void_p(base + 4 * groups_at), G,
+                                          PAGE.bit_length() - 1,
                                           C.c_void_p(self._moves_out.data_ptr()), mv_elems,
                                           C.c_void_p(torch.cuda.current_stream().cuda_stream)), "abkv_moves_expand")
             mv = device_move_lists(self._moves_out[:mv_elems], mv_parts)

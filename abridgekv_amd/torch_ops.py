@@ -121,10 +121,11 @@ def _kv_move_mixed_fake(layer_caches, ops, seg_offsets, free_ops):
     _need(0 < len(layer_caches) <= 16, "between 1 and 16 layer caches per call")
 
 
-def _moves_expand_checks(runs, pages, groups, out, n_elems):
+def _moves_expand_checks(runs, n_runs, pages, groups, out, n_elems):
     for name, t in (("runs", runs), ("pages", pages), ("groups", groups), ("out", out)):
         _need(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous(), f"{name} must be contiguous cuda int32")
-    _need(runs.numel() % RUN_FIELDS == 0 and groups.numel() % 4 == 0, f"runs [n, {RUN_FIELDS}] and groups [G, 4]")
+    _need(0 <= n_runs and n_runs * RUN_FIELDS <= runs.numel() and groups.numel() % 4 == 0,
+          f"runs must hold n_runs records of {RUN_FIELDS} int32, groups [G, 4]")
     _need(0 <= n_elems <= out.numel(), "out must hold n_elems int32")
 
 
@@ -132,19 +133,21 @@ RUN_FIELDS = 30                                              # int32 per record 
 
 
 @torch.library.custom_op(f"{_NS}::moves_expand", mutates_args=("out",))
-def moves_expand(runs: Tensor, pages: Tensor, groups: Tensor, page_shift: int, out: Tensor, n_elems: int) -> None:
-    """abkv_moves_expand: the planner's run descriptors (records [n_runs, 30], page windows, group table [G, 4], all on
-    the device) written out as the step's move lists (n_elems int32 of out), ready for kv_move_mixed."""
-    _moves_expand_checks(runs, pages, groups, out, n_elems)
+def moves_expand(runs: Tensor, n_runs: int, pages: Tensor, groups: Tensor, page_shift: int, out: Tensor,
+                 n_elems: int) -> None:
+    """abkv_moves_expand: the planner's run descriptors (the n_runs records of take_step_move_runs' layout -- record
+    slots past them are stale -- the page windows and the group table [G, 4], all on the device) written out as the
+    step's move lists (n_elems int32 of out), ready for kv_move_mixed."""
+    _moves_expand_checks(runs, n_runs, pages, groups, out, n_elems)
     stream = C.c_void_p(torch.cuda.current_stream(out.device).cuda_stream)
-    check(lib().abkv_moves_expand(C.c_void_p(runs.data_ptr()), runs.numel() // RUN_FIELDS, C.c_void_p(pages.data_ptr()),
-                                  C.c_void_p(groups.data_ptr()), groups.numel() // 4, int(page_shift),
+    check(lib().abkv_moves_expand(C.c_void_p(runs.data_ptr()), int(n_runs), C.c_void_p(pages.data_ptr()),
+                                  pages.numel(), C.c_void_p(groups.data_ptr()), groups.numel() // 4, int(page_shift),
                                   C.c_void_p(out.data_ptr()), int(n_elems), stream), "abkv_moves_expand")
 
 
 @moves_expand.register_fake
-def _moves_expand_fake(runs, pages, groups, page_shift, out, n_elems):
-    _moves_expand_checks(runs, pages, groups, out, n_elems)
+def _moves_expand_fake(runs, n_runs, pages, groups, page_shift, out, n_elems):
+    _moves_expand_checks(runs, n_runs, pages, groups, out, n_elems)
 
 
 # -- paged multi-query attention (prompt chunks, code steps) --------------------------------------------------------

@@ -131,6 +131,22 @@ class MoveUploader:
         return trunc, device_move_lists(self._dev[:n], parts)
 
 
+def take_step_move_lists(planner):
+    """The pending step's fused moves, ready for upload: ("runs", buffer, layout, parts, n_elems) with the run
+    descriptors the device expands (KVPlanner.take_step_move_runs), or -- when the planner refuses descriptors for
+    the step (more than 8 span removals of one request and group in one step; the step then stays pending) --
+    ("packed", buffer, None, parts, n_elems) with the move lists written on the host (KVPlanner.take_step_moves).
+    ``parts`` as pack_fused_moves; n_elems = int32 elements of the move lists."""
+    try:
+        _, desc, layout, parts, n_elems = planner.take_step_move_runs()
+        return "runs", desc, layout, parts, n_elems
+    except RuntimeError as e:
+        if "more than 8 span removals" not in str(e):
+            raise
+    _, buf, parts = planner.take_step_moves()
+    return "packed", buf, None, parts, int(buf.size)
+
+
 class MoveRunUploader:
     """A planner step's fused moves as run descriptors (KVPlanner.take_step_move_runs): the records, page windows and
     group table go to the device in one asynchronous copy from pinned memory, and abkv_moves_expand writes the move
@@ -166,7 +182,7 @@ class MoveRunUploader:
         base = self._dev.data_ptr()
         shift = int(planner.block_size).bit_length() - 1
         rc = lib().abkv_moves_expand(C.c_void_p(base + 4 * runs_at), n_runs, C.c_void_p(base + 4 * pages_at),
-                                     C.c_void_p(base + 4 * groups_at), planner.num_groups, shift,
+                                     groups_at - pages_at, C.c_void_p(base + 4 * groups_at), planner.num_groups, shift,
                                      C.c_void_p(self._out.data_ptr()), n_elems,
                                      C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
         if rc != 0:

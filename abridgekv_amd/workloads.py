@@ -275,14 +275,17 @@ def full_model_decode_lengths(B=64, seed=0, prompt=512, closed_generated=32):
     return T, np.full(B, prompt)
 
 
-def visible_pairs_prompt_block(C, K, N):
+def visible_pairs_prompt_block(C, K, N, T=0):
     """Visible (query, key) pairs per head of the teacher-forced mask when block 0 is the raw prompt: block-b content
     queries see their block's content causally, b*K earlier codes and (b > 0) the C prompt rows; block-b code queries
-    see their block's C content and K codes, b*K earlier codes and (b > 0) the prompt rows."""
+    see their block's C content and K codes, b*K earlier codes and (b > 0) the prompt rows. A static retained tail of
+    T rows adds the last T content rows of the earlier non-prompt blocks (blocks 1 .. b-1) to both, and hides a block's
+    own last T content rows from its codes."""
     n = 0
     for b in range(N):
-        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0)
-        n += K * C + K * K + K * b * K + (K * C if b else 0)
+        tails = max(0, b - 1) * T
+        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0) + C * tails
+        n += K * (C - T) + K * K + K * b * K + (K * C if b else 0) + K * tails
     return n
 
 

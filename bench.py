@@ -75,6 +75,8 @@ def parse():
                          "the default, the code step on a second stream)")
     ap.add_argument("--code-target-blocks", type=int, default=None,
                     help="serving: workgroups a code step's key splits aim at (default: one per compute unit)")
+    ap.add_argument("--retain-tail", type=int, default=0,
+                    help="prefill / prefill_bwd: static retained tail of T content rows per block (default 0)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     args = ap.parse_args()
@@ -177,7 +179,7 @@ def bench_prefill(args, torch):
     from abridgekv_amd import ops
     from abridgekv_amd.workloads import visible_pairs_prompt_block
 
-    B, C, K, N, plen = 4, 512, 128, 16, 512
+    B, C, K, N, plen, T = 4, 512, 128, 16, 512, args.retain_tail
     S0 = N * (C + K)
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(args.seed)
@@ -189,18 +191,18 @@ def bench_prefill(args, torch):
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     warmup = max(args.warmup, MIN_PREFILL_WARMUP)
     for _ in range(warmup):
-        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse)
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):
-        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse)
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T)
     e.record()
     torch.cuda.synchronize()
     t = s.elapsed_time(e) / 1e3 / args.steps
-    flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N) * 32 * B
+    flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N, T) * 32 * B
     tflops = flops / t / 1e12
-    cpu = None if args.no_cpu_baseline else prefill_cpu_baseline(torch, C, K, plen, flops, B, S0)
+    cpu = None if args.no_cpu_baseline or T else prefill_cpu_baseline(torch, C, K, plen, flops, B, S0)
     return {
         **({"cpu_baseline": cpu} if cpu else {}),
         "metric": "masked teacher-forced prefill TFLOP/s (visible QK+PV flops); % of bf16 dense MFMA peak",
@@ -208,7 +210,8 @@ def bench_prefill(args, torch):
         "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic N(0,1) q/k/v from the seed",
         "config": {"workload": f"masked prefill B={B}, N={N} blocks of [{C} content | {K} codes], S0={S0}, "
-                               f"raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
+                               f"raw prompt {plen}, 32q/8kv heads, d128"
+                               + (f", static retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": tflops / 2500.0,
                      "traffic": profiled_traffic("prefill_masked_b4_s10240_pmc_traffic.md"),
@@ -256,7 +259,7 @@ def bench_prefill_bwd(args, torch):
     from abridgekv_amd import ops
     from abridgekv_amd.workloads import visible_pairs_prompt_block
 
-    B, C, K, N, plen = 4, 512, 128, 16, 512
+    B, C, K, N, plen, T = 4, 512, 128, 16, 512, args.retain_tail
     S0 = N * (C + K)
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(args.seed)
@@ -266,19 +269,19 @@ def bench_prefill_bwd(args, torch):
     dout = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
     pl = torch.full((B,), plen, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
-    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse, retain_tail=T)
     warmup = max(args.warmup, MIN_PREFILL_WARMUP)
     for _ in range(warmup):
-        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):
-        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl)
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T)
     e.record()
     torch.cuda.synchronize()
     t = s.elapsed_time(e) / 1e3 / args.steps
-    flops = 10.0 * 128 * visible_pairs_prompt_block(C, K, N) * 32 * B
+    flops = 10.0 * 128 * visible_pairs_prompt_block(C, K, N, T) * 32 * B
     tflops = flops / t / 1e12
     return {
         "metric": "masked teacher-forced attention backward TFLOP/s (visible-pair flops, 2.5x forward); % of bf16 "
@@ -287,7 +290,8 @@ def bench_prefill_bwd(args, torch):
         "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic N(0,1) q/k/v/dout from the seed",
         "config": {"workload": f"masked prefill backward B={B}, N={N} blocks of [{C} content | {K} codes], "
-                               f"S0={S0}, raw prompt {plen}, 32q/8kv heads, d128", "global_batch": B, "seq_len": S0},
+                               f"S0={S0}, raw prompt {plen}, 32q/8kv heads, d128"
+                               + (f", static retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
                      "traffic": profiled_traffic("prefill_masked_bwd_b4_s10240_pmc_traffic.md"),
                      "traffic_source": "profiles/prefill_masked_bwd_b4_s10240_pmc_traffic.md (the three kernels)",

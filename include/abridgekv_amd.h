@@ -338,11 +338,13 @@ int abkv_planner_pending_run_sizes(void* planner, int64_t* n_runs, int64_t* n_pa
 int abkv_planner_take_move_runs(void* planner, int64_t* trunc_rows, int64_t trunc_cap, int64_t* n_trunc,
                                 int32_t* runs, int64_t runs_cap, int32_t* pages, int64_t pages_cap, int32_t* groups,
                                 int64_t* index, int64_t* sizes);
-/* Device expansion of abkv_planner_take_move_runs' outputs (runs, pages, groups on the device; out_elems = sizes[2])
- * into `out`, ready for abkv_kv_move_mixed. page_shift = log2(page size). One launch of n_runs + num_groups
- * workgroups on `stream`; every store is bounds-checked against the record's counts and out_elems. */
-int abkv_moves_expand(const int32_t* runs, int n_runs, const int32_t* pages, const int32_t* groups, int num_groups,
-                      int page_shift, int32_t* out, long out_elems, abkv_stream_t stream);
+/* Device expansion of abkv_planner_take_move_runs' outputs (runs, pages, groups on the device; n_runs = sizes[0],
+ * the records that call wrote -- record slots past it are not cleared and must not be passed; n_pages = entries of
+ * `pages`; out_elems = sizes[2]) into `out`, ready for abkv_kv_move_mixed. page_shift = log2(page size). One launch of
+ * n_runs + num_groups workgroups on `stream`; every store is bounds-checked against the record's counts and
+ * out_elems, every page read against the record's window and n_pages, and negative positions are skipped. */
+int abkv_moves_expand(const int32_t* runs, int n_runs, const int32_t* pages, long n_pages, const int32_t* groups,
+                      int num_groups, int page_shift, int32_t* out, long out_elems, abkv_stream_t stream);
 int64_t abkv_planner_num_free(void* planner);
 int64_t abkv_planner_free_queue(void* planner, int32_t* out, int64_t cap);
 int64_t abkv_planner_block_ids(void* planner, int64_t rid, int group, int32_t* out, int64_t cap);

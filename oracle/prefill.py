@@ -241,9 +241,9 @@ def dense_masked_attention_ref_torch(q, k, v, mask, scale):
     return torch.matmul(w, vv)
 
 
-def visible_pairs(C, K, N, prompt_len=None):
+def visible_pairs(C, K, N, prompt_len=None, retain_tail=0):
     """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
-    m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len])
+    m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len], retain_tail=retain_tail)
     return int(m.sum())
 
 

@@ -15,7 +15,7 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:
 The machine is planner-agnostic: it emits the scheduler-visible events (allocate ``n`` new tokens, then compact
 spans) and is shared by the oracle planner and the product planner so that both see identical event streams.
 
-Pinning: tests/test_oracle_trace.py checks the reference's invariants (scripts/test_compresslm_physical_quotas.py:
+Pinning: tests/test_oracle_compaction.py checks the reference's invariants (scripts/test_compresslm_physical_quotas.py:
 68-138): every compacted block keeps exactly codes[:q_g] and no response content in group g; removed rows per
 group differ from group 0 by (K - q_g) per compacted block; and the closed form of oracle.layout.rows_per_layer.
 The static tail: tests/test_static_tail.py checks the kept rows against their closed form (prompt content, the last T

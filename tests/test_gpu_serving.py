@@ -126,3 +126,25 @@ def test_concurrent_code_step_matches_serial(geometry):
         code_steps += int(ma["nc"] > 0)
     assert code_steps >= (4 if geometry == "small" else 2), code_steps
     assert a.stats == b.stats
+
+
+def test_serving_loop_with_host_written_move_lists():
+    """The loop's fallback when the planner refuses run descriptors for a step (more than eight removals of one
+    request and group): every step's moves taken as host-written lists instead. Every row written during the run still
+    holds the logical position the planner maps it to."""
+    from abridgekv_amd.serving import ServingStress
+    rng = np.random.default_rng(0)
+    B = 8
+    s = ServingStress(rng.integers(200, 600, B), rng.integers(10, 150, B), layer_quotas=(16, 4, 8, 4, 16, 8), seed=0,
+                      C=64, K=16, growth_tokens=256, tag=True)
+    planner = s.plan.planner
+
+    def refuse(*a, **k):
+        raise RuntimeError("take_move_runs failed (-2): more than 8 span removals of one request and group")
+
+    planner.take_step_move_runs = refuse
+    s.run(150)
+    s.flush()
+    torch.cuda.synchronize()
+    assert s.stats["moved_rows"] > 0 and s.stats["code_steps"] >= B
+    assert s.check_layout() > B * 100

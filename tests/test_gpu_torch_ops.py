@@ -95,7 +95,7 @@ def _via_torch_ops(d, o):
                      d["bt"].shape[1] * 16 - 1)
     A.kv_move_segments([d["cache"]], d["mv"], d["offs"])
     A.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
-    A.moves_expand(d["mr_runs"], d["mr_pages"], d["mr_groups"], 4, o["mvout"], d["mr_n"])
+    A.moves_expand(d["mr_runs"], d["mr_runs"].numel() // 30, d["mr_pages"], d["mr_groups"], 4, o["mvout"], d["mr_n"])
     A.decode_attn(d["q"], d["cache"], d["bt"], d["lens"], scale, d["bt"].shape[1], 8, o["out"], o["lse"], d["ws"])
     m = d["meta"]
     A.paged_prefill_attn(d["cq"], d["cache"], d["bt"], m[0:2], m[2:3], m[3:4], d["tiles"][0], d["tiles"][1], m[4:5],
@@ -113,7 +113,8 @@ def _via_ctypes(d, o):
     ops.kv_move_mixed([d["cache"]], d["mx"], d["mx_offs"], d["mx_free"])
     r = d["mr_runs"]
     assert ops.lib().abkv_moves_expand(C.c_void_p(r.data_ptr()), r.numel() // 30, C.c_void_p(d["mr_pages"].data_ptr()),
-                                       C.c_void_p(d["mr_groups"].data_ptr()), 1, 4, C.c_void_p(o["mvout"].data_ptr()),
+                                       d["mr_pages"].numel(), C.c_void_p(d["mr_groups"].data_ptr()), 1, 4,
+                                       C.c_void_p(o["mvout"].data_ptr()),
                                        d["mr_n"], C.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
     ops.decode_attention(d["q"], d["cache"], d["bt"], d["lens"], scale, out=o["out"], lse=o["lse"], split_pages=8,
                          workspace=d["ws"])

@@ -203,3 +203,41 @@ def test_planner_writes_the_same_move_lists_directly(op_rows):
             if parts:
                 assert np.array_equal(buf, ref_buf)
             assert {pb.request_id(int(r[0])): tuple(int(x) for x in r[1:]) for r in tr} == out.block_table_truncations
+
+
+def test_config2_fused_moves_equal_oracle_batches():
+    """The 64-sequence compaction step: the native planner's fused moves (gather-then-scatter per group) and the
+    oracle planner's ordered op batches (oracle.compaction.execute_kv_copy_operations, the reference executor's
+    batch order, gpu_model_runner.py:1147-1224), both applied to a row-id image of the pool (every slot holds its own
+    id), leave every kept row of every request and group holding the same id; the page lists and compacted counts
+    of both planners agree."""
+    from oracle import compaction as oc
+
+    st = workloads.build_compaction_state(64, seed=0, op_rows=False)
+    G = len(st.groups)
+    orc = oc.Planner(st.num_pages, G, PAGE, free_order=st.free_order)
+    orc.apply_events(st.history)
+    orc.take_step_outputs()
+    orc.apply_events(st.pending)
+    batches, _ = orc.take_step_outputs()
+    out = st.compact()
+    fused = np.asarray(out.fused_moves, np.int64)
+    assert fused.size and len(batches) == 64
+    image = np.arange(st.num_pages * PAGE, dtype=np.int64).reshape(st.num_pages, PAGE)
+    kept_rows = 0
+    for g in range(G):
+        mine = gather_then_scatter(image, fused[fused[:, 1] == g])
+        ref = np.stack([image, image], axis=1).copy()                 # [pages, 2 (K, V), 16]
+        oc.execute_kv_copy_operations({r: b for r, b in batches.items()},
+                                      [[ref] if i == g else [] for i in range(G)])
+        assert np.array_equal(ref[:, 0], ref[:, 1])
+        for r in range(64):
+            blocks = st.planner.get_blocks(r)[g]
+            assert blocks == orc.block_ids(r)[g]
+            assert st.planner.compacted_counts(r)[g] == orc.requests[r].compacted_counts()[g]
+            active = st.planner.num_computed_tokens(r) - st.planner.compacted_counts(r)[g]
+            slots = oc.slot_mapping(blocks, np.arange(active))
+            got, want = mine[slots // PAGE, slots % PAGE], ref[slots // PAGE, 0, slots % PAGE]
+            assert np.array_equal(got, want), (r, g)
+            kept_rows += active
+    assert kept_rows > 64 * G * 128

@@ -19,12 +19,15 @@ def expand(buf, layout, n_elems, G, shift=4):
     runs_at, n_runs, pages_at, groups_at = layout
     out = np.full(n_elems, -7, np.int32)                   # any element left unwritten shows up
     gr = buf[groups_at: groups_at + 4 * G].reshape(G, 4)
+    n_pages = groups_at - pages_at                          # the kernel's n_pages: entries of the page section
     for g in range(G):
+        assert gr[g, 0] >= 0 and gr[g, 1] >= 0                # the kernel skips a group row that fails this
         out[gr[g, 0]] = 0
         out[gr[g, 0] + 1 + gr[g, 1]: gr[g, 2]] = 0
     pages = buf[pages_at:]
     for rec in buf[runs_at: runs_at + F * n_runs].reshape(n_runs, F):
         n, lo_w, pat, ord_at, free_at, n_ch, n_free, seg_at, seg_val, m, t_star, a_end, win_n = map(int, rec[:13])
+        assert 0 <= pat and 0 <= win_n and pat + win_n <= n_pages     # the kernel skips a record that fails this
         tau = [int(x) for x in rec[14:14 + m]]
         c = [int(x) for x in rec[14 + M:14 + M + m]]
         if seg_at >= 0:
@@ -54,7 +57,7 @@ def expand(buf, layout, n_elems, G, shift=4):
             else:
                 assert 0 <= i - t_star - rank < n_free
                 pos = free_at + 4 * (i - t_star - rank)
-            assert src >> shift < win_n and dst >> shift < win_n
+            assert 0 <= src and 0 <= dst and src >> shift < win_n and dst >> shift < win_n
             out[pos:pos + 4] = (pages[pat + (src >> shift)], src & (PAGE - 1), pages[pat + (dst >> shift)],
                                 dst & (PAGE - 1))
     return out
@@ -129,3 +132,24 @@ def test_many_removals_in_one_step(n_removals):
             pb.take_step_move_runs()
         tr_b, buf_b, parts_b = pb.take_step_moves()
         assert parts_a == parts_b and np.array_equal(buf_a, buf_b)
+
+
+@pytest.mark.parametrize("n_removals", [8, 9])
+def test_step_move_lists_fall_back_to_host_lists(n_removals):
+    """worker.take_step_move_lists: run descriptors while the planner accepts them; past eight removals of one request
+    and group in a step, the host-written lists of the still-pending step -- the same lists either way."""
+    from abridgekv_amd.worker import take_step_move_lists
+    pa, pb = (KVPlanner(200, 1, PAGE, op_rows=False) for _ in range(2))
+    for p in (pa, pb):
+        p.add_request(7)
+        assert p.allocate_slots(7, 1000) is not None
+        p.set_num_computed_tokens(7, 1000)
+        for k in range(n_removals):
+            s = 40 + 100 * ((7 * k) % n_removals)
+            assert p.mask_token_span(7, s, s + 10 + k).success
+    _, want, parts_a = pa.take_step_moves()
+    kind, buf, layout, parts_b, n_elems = take_step_move_lists(pb)
+    assert kind == ("runs" if n_removals <= 8 else "packed") and parts_a == parts_b
+    got = expand(buf, layout, n_elems, 1) if kind == "runs" else buf
+    assert np.array_equal(got, want) and n_elems == want.size
+    assert pb.take_step_moves()[2] == []                   # the step was taken

@@ -23,7 +23,8 @@ def test_serving_plan_moves_are_exact_under_any_interleaving():
         moves = plan.advance(plan.prepare())
         if moves is None:
             continue
-        desc, layout, parts, n_elems = moves
+        kind, desc, layout, parts, n_elems = moves
+        assert kind == "runs"                               # the loop's steps stay within the descriptors' limits
         buf = expand(desc, layout, n_elems, plan.G)
         for gid, (ops_g, offs, nf) in unpack(buf, parts).items():
             rows = np.concatenate([np.zeros((len(ops_g), 2), np.int64), ops_g.astype(np.int64)], axis=1)

@@ -41,7 +41,7 @@ def test_fake_tracing_keeps_each_op_as_one_node():
                                                0.088, 4, 2, 1, out, lse, ws)
         torch.ops.abridgekv.kv_move_segments([cache], mv_ops, offs)
         torch.ops.abridgekv.kv_move_mixed([cache], mv_ops, offs, mv_ops)
-        torch.ops.abridgekv.moves_expand(meta[:0], meta, meta[:4], 4, offs, 2)
+        torch.ops.abridgekv.moves_expand(meta[:0], 0, meta, meta[:4], 4, offs, 2)
         torch.ops.abridgekv.prefill_masked_attn(pq, pk, pv, 8, 4, 2, None, None, 0.088, pout, plse)
         dq, dk, dv = torch.ops.abridgekv.prefill_masked_attn_bwd(pq, pk, pv, pout, plse, pout, 8, 4, 2, None, None,
                                                                 0.088)
