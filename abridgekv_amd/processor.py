@@ -30,12 +30,19 @@ class RequestStatus(enum.IntEnum):
 
 @dataclass
 class SamplingSpec:
-    """The sampling fields the state machine reads."""
+    """The sampling fields the state machine reads, and those prepare_request refuses to see changed from their
+    defaults (vllm SamplingParams names)."""
     max_tokens: int = 1 << 30
     ignore_eos: bool = False
     stop_token_ids: tuple[int, ...] = ()
     min_tokens: int = 0
     bad_words_token_ids: list = field(default_factory=list)
+    frequency_penalty: float = 0.0
+    presence_penalty: float = 0.0
+    repetition_penalty: float = 1.0
+    stop: list | None = None
+    logprobs: int | None = None
+    prompt_logprobs: int | None = None
 
 
 @dataclass
@@ -75,9 +82,25 @@ class ServingRequest:
     """Minimal request object with the fields the state machine and the planner read (vllm.v1.request.Request)."""
 
     def __init__(self, request_id, prompt_token_ids, sampling: SamplingSpec | None = None, eos_token_id=None,
-                 planner=None):
+                 planner=None, prompt_embeds=None, pooling_params=None, use_structured_output=False):
         self.request_id = request_id
-        self.prompt_token_ids = list(prompt_token_ids)
+        self.prompt_token_ids = None if prompt_token_ids is None else list(prompt_token_ids)
+        self.prompt_embeds = prompt_embeds
+        self.pooling_params = pooling_params
+        self.use_structured_output = use_structured_output
+        if self.prompt_token_ids is None:
+            self.num_prompt_tokens = 0
+            self._all_token_ids: list[int] = []
+            self._output_token_ids: list[int] = []
+            self.num_computed_tokens = 0
+            self.sampling_params = sampling or SamplingSpec()
+            self.max_tokens = self.sampling_params.max_tokens
+            self.eos_token_id = eos_token_id
+            self.status = RequestStatus.RUNNING
+            self.stop_reason = None
+            self.compresslm_state = None
+            self.planner = planner
+            return
         self.num_prompt_tokens = len(self.prompt_token_ids)
         self._all_token_ids = list(self.prompt_token_ids)
         self._output_token_ids: list[int] = []
@@ -142,11 +165,35 @@ class CompressLMProcessor:
 
     # -- request set-up -------------------------------------------------------------------------------------------
     def prepare_request(self, request) -> CompressLMState:
+        """Validate a new request and open its first block (processor.py:42-105): the requests CompressLM decoding
+        cannot serve are refused with the reference's messages, in its order."""
         sampling = request.sampling_params
-        if sampling is None:
-            raise ValueError("CompressLM decoding requires sampling parameters")
-        if getattr(sampling, "min_tokens", 0) != 0:
-            raise ValueError("CompressLM decoding currently requires min_tokens=0")
+        ga = getattr
+        refusals = (
+            (request.prompt_token_ids is None, "CompressLM decoding requires prompt token IDs"),
+            (ga(request, "prompt_embeds", None) is not None, "CompressLM decoding does not support prompt_embeds"),
+            (ga(request, "pooling_params", None) is not None, "CompressLM decoding only supports generation requests"),
+            (sampling is None, "CompressLM decoding requires sampling parameters"),
+        )
+        for refused, message in refusals:
+            if refused:
+                raise ValueError(message)
+        refusals = (
+            (ga(sampling, "frequency_penalty", 0.0) != 0.0, "CompressLM decoding requires frequency_penalty=0"),
+            (ga(sampling, "presence_penalty", 0.0) != 0.0, "CompressLM decoding requires presence_penalty=0"),
+            (ga(sampling, "repetition_penalty", 1.0) != 1.0, "CompressLM decoding requires repetition_penalty=1"),
+            (bool(ga(sampling, "stop", None)),
+             "CompressLM decoding currently supports token/EOS stops, not stop strings"),
+            (ga(sampling, "min_tokens", 0) != 0, "CompressLM decoding currently requires min_tokens=0"),
+            (ga(sampling, "logprobs", None) is not None and not self.config.debug,
+             "CompressLM output logprobs are only available in debug mode"),
+            (ga(sampling, "prompt_logprobs", None) is not None, "CompressLM decoding does not support prompt logprobs"),
+            (bool(ga(request, "use_structured_output", False)),
+             "CompressLM decoding does not support structured output"),
+        )
+        for refused, message in refusals:
+            if refused:
+                raise ValueError(message)
         banned = {ids[0] for ids in (getattr(sampling, "bad_words_token_ids", None) or []) if len(ids) == 1}
         missing = set(self.config.code_token_ids) - banned
         if missing:

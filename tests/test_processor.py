@@ -176,6 +176,46 @@ def test_request_validation():
         CompressLMProcessor(CompressLMConfig(enable=True, block_size=4, num_code_tokens=4))
 
 
+@pytest.mark.parametrize("change,message", [
+    (dict(prompt_token_ids=None), "requires prompt token IDs"),
+    (dict(prompt_embeds=[[0.0]]), "does not support prompt_embeds"),
+    (dict(pooling_params=object()), "only supports generation requests"),
+    (dict(sampling=None), "requires sampling parameters"),
+    (dict(frequency_penalty=0.5), "frequency_penalty=0"),
+    (dict(presence_penalty=-0.1), "presence_penalty=0"),
+    (dict(repetition_penalty=1.1), "repetition_penalty=1"),
+    (dict(stop=["\n\n"]), "not stop strings"),
+    (dict(min_tokens=3), "min_tokens=0"),
+    (dict(logprobs=2), "only available in debug mode"),
+    (dict(prompt_logprobs=0), "does not support prompt logprobs"),
+    (dict(use_structured_output=True), "does not support structured output"),
+])
+def test_request_refusals_match_the_reference(change, message):
+    """Each request the reference's prepare_request refuses (processor.py:42-80) is refused with its message; the
+    same request with the field at its default is accepted."""
+    _, proc = make()
+    bans = [[c] for c in CODES]
+    spec = {k: v for k, v in change.items() if k in SamplingSpec.__dataclass_fields__}
+    req_kw = {k: v for k, v in change.items() if k not in spec and k not in ("prompt_token_ids", "sampling")}
+    sampling = None if "sampling" in change else SamplingSpec(bad_words_token_ids=bans, **spec)
+    prompt = change.get("prompt_token_ids", [1, 2, 3])
+    req = ServingRequest("a", prompt, sampling, **req_kw)
+    if sampling is None:
+        req.sampling_params = None
+    with pytest.raises(ValueError, match=message):
+        proc.prepare_request(req)
+    ok = ServingRequest("b", [1, 2, 3], SamplingSpec(bad_words_token_ids=bans))
+    assert proc.prepare_request(ok).pending_prompt_index == 3
+
+
+def test_logprobs_are_allowed_in_debug_mode():
+    cfg = CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, debug=True)
+    cfg.set_code_token_ids([90, 91])
+    proc = CompressLMProcessor(cfg)
+    req = ServingRequest("a", [1, 2], SamplingSpec(bad_words_token_ids=[[90], [91]], logprobs=1))
+    assert proc.prepare_request(req).pending_prompt_index == 2
+
+
 def test_config_json_round_trip_and_schedule_loading(tmp_path):
     """compresslm_config.json written as the reference's exporter writes it, read back the way its serving entry
     points read it, with per-layer quotas from the reference's schedule file (tests/golden)."""
