@@ -199,8 +199,9 @@ __device__ __forceinline__ void tile_scores(const __bf16* Kbuf, const bf16x8 (&q
       }
 }
 
-// Hidden keys of a partial tile get score -inf (tm.mode 0: nothing hidden).
-template <int H, bool kAligned, bool kHole = false>
+// Hidden keys of a partial tile get score -inf (tm.mode 0: nothing hidden). kElem: an aligned walk that may yield
+// per-element tiles (mode 3, the full predicate MaskGeom::visible) beside the limit modes.
+template <int H, bool kAligned, bool kHole = false, bool kElem = false>
 __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const TileMask& tm, int lane_limit,
                                           const MaskGeom& geo, int j) {
   static_assert(H <= 2, "TileMask holds two per-head limits");
@@ -235,7 +236,9 @@ __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const T
         for (int r = 0; r < 4; ++r) {
           const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
           bool ok;
-          if constexpr (kAligned) {
+          if constexpr (kAligned && kElem) {
+            ok = tm.mode == 3 ? geo.visible(kv, u) : kv < lim[u];
+          } else if constexpr (kAligned) {
             ok = kv < lim[u];
           } else {
             ok = geo.visible(kv, u);
@@ -391,7 +394,7 @@ __device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n
     __builtin_amdgcn_s_barrier();
     issue_half<kWaves, false>(rows, src_k, n_keys, K[slot], w, lane);
     issue_half<kWaves, true>(rows, src_v, n_keys, V[slot2], w, lane);
-    tile_mask<H, kAligned, Walk::kHole>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
+    tile_mask<H, kAligned, Walk::kHole, Walk::kElem>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
     bf16x8 pop[2][H];
     tile_softmax<H>(s_cur, o, m_run, lsum, scale_log2, pop);
     // Unconditional so that the MFMAs can overlap the softmax work: after the last tile the scores are computed from

@@ -70,6 +70,7 @@ struct PackedRows {
 // that meet the excluded key range [ex_lo, ex_hi) (empty when ex_lo >= ex_hi) mask it as well.
 struct RangeWalk {
   static constexpr bool kHole = true;
+  static constexpr bool kElem = false;
   int kt_begin, kt_end, k_full, ex_lo, ex_hi;
   __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
     kt = first ? kt_begin : kt + 1;

@@ -18,13 +18,14 @@
 //   it by > 8)
 //   O^T[128 dims x 32 cols] += V^T . P^T          2 key halves x 8 dim tiles x 2 heads; V^T by LDS transpose reads
 // Aligned layouts (C and K multiples of 64) walk only the visible tiles, jumping over hidden segments, and tag each
-// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit). Unaligned shapes and layouts with a
-// retained tail run every tile of the visible prefix with the mask evaluated per element (correct, slower).
+// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit); with a static retained tail the walk
+// also visits each earlier block's tail tiles, and the tile that mixes hidden and visible rows takes the per-element
+// mask. Unaligned shapes run every tile of the visible prefix with the mask evaluated per element (correct, slower).
 #include "prefill_common.h"
 
 namespace abkv {
 
-template <int H, bool kAligned>
+template <int H, bool kAligned, bool kTail>
 __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(PrefillArgs a) {
   constexpr int kWaves = 4 * (4 / H);                       // 16 query rows x H heads per wave
   __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], K2[kTileElems];
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}, a.tail};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
-  TileWalk<kAligned> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1);
+  TileWalk<kAligned, kTail> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1, a.tail);
   attend_tiles<H, kAligned, kWaves>(rows, walk, a.S0, Kbuf, Vbuf, qop, o, m_run, l_run, qrow + 1, a.scale_log2, geo, w,
                                     lane);
 
@@ -139,14 +140,16 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;
   a.lse = lse;
   a.tail = retain_tail;
-  a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && retain_tail == 0;
+  a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
   // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).
   const unsigned grid = prefill_grid(a.num_q_tiles, batch, 512);
   if (grid == 0) return (int)hipErrorInvalidValue;
-  if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true>), grid, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_masked_kernel<2, false>), grid, dim3(512), 0, stream, a);
+  if (a.aligned && retain_tail == 0)
+    hipLaunchKernelGGL((prefill_masked_kernel<2, true, false>), grid, dim3(512), 0, stream, a);
+  else if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true, true>), grid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_masked_kernel<2, false, false>), grid, dim3(512), 0, stream, a);
   return (int)hipGetLastError();
 }
 

@@ -104,7 +104,7 @@ struct Buf {
   static constexpr int value = N;
 };
 
-template <bool kAligned>
+template <bool kAligned, bool kTail>
 __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a) {
   constexpr int H = 2, kWaves = 8;
   __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], V0[kTileElems], V1[kTileElems];
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
   const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail};
   const int q_last = min(q0 + kBM, f.S0) - 1;
-  TileWalk<kAligned> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1);
+  TileWalk<kAligned, kTail> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1, f.tail);
 
   int tc = 0;
   TileMask mc;
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
       floatx4 s[2][2][H], dp[2][2][H];
       tile_scores<H>(Kb[sl], qop, s, m16, j);
       tile_scores<H>(Vb[sl], gop, dp, m16, j);
-      tile_mask<H, kAligned>(s, tc * kBN, mc, qrow + 1, geo, j);
+      tile_mask<H, kAligned, kTail>(s, tc * kBN, mc, qrow + 1, geo, j);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -226,8 +226,11 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
 
 // Visibility of the 64-key tile kt to the 64-row query tile qt for a head of code quota qh, aligned layouts (C, K
 // multiples of 64; the classification of the forward's TileWalk::seek / mask for one key tile): -1 hidden, 0 every
-// pair visible, 1 key <= query, 2 key < limit.
-__device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, int per, int plen, int& limit) {
+// pair visible, 1 key <= query, 2 key < lim0 (without a tail the per-element predicate decides these tiles),
+// kTail: 4 key outside [lim0, lim1) (the tile of an earlier block where hidden rows give way to its retained tail).
+template <bool kTail>
+__device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, int per, int plen, int tail,
+                                         int& lim0, int& lim1) {
   const int q0 = qt * kBN, k0 = kt * kBN;
   const int qb = q0 / per, kb = k0 / per;
   if (kb > qb) return -1;
@@ -235,20 +238,43 @@ __device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, 
   const int tw = (k0 - kb * per) / kBN, ct = C / kBN;
   if (tw < ct) {
     if (kb == qb) {
+      if (kTail && q_code) {                                // codes see their block's content below C - T
+        const int lo = kBN * tw;
+        if (lo >= C - tail) return -1;
+        if (lo + kBN > C - tail) {
+          lim0 = kb * per + C - tail;
+          return 2;
+        }
+        return 0;
+      }
       const int q_last = min(q0 + kBN, S0) - 1;
       if (!(q_code || k0 <= q_last)) return -1;
       return (!q_code && k0 + kBN - 1 > q0) ? 1 : 0;
     }
+    if constexpr (kTail) {
+      const int pl = min(max(plen - kb * C, 0), C);         // raw-prompt rows of this block's content
+      const int lo = kBN * tw, hi = lo + kBN;
+      if (hi <= pl || lo >= C - tail) return 0;             // all prompt, or all tail
+      if (hi <= C - tail) {                                 // no tail rows: a prompt prefix or nothing
+        if (lo >= pl) return -1;
+        lim0 = kb * per + pl;
+        return 2;
+      }
+      if (pl >= C - tail) return 0;                         // prompt rows up to the tail
+      lim0 = kb * per + pl;                                 // [prompt rows,] hidden rows, tail rows
+      lim1 = kb * per + C - tail;
+      return 4;
+    }
     if (kb * C + kBN * tw >= plen) return -1;
     if (kb * C + kBN * tw + kBN > plen) {
-      limit = kb * per + (plen - kb * C);
+      lim0 = kb * per + (plen - kb * C);
       return 2;
     }
     return 0;
   }
   if (!(kb < qb || q_code) || kBN * (tw - ct) >= qh) return -1;
   if (kBN * (tw - ct) + kBN > qh) {
-    limit = kb * per + C + qh;
+    lim0 = kb * per + C + qh;
     return 2;
   }
   return 0;
@@ -308,7 +334,7 @@ __device__ __forceinline__ void dkv_acc(const __bf16* Qbuf, const __bf16* Gbuf, 
   __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
 }
 
-template <bool kAligned>
+template <bool kAligned, bool kTail>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs a) {
   constexpr int kWaves = 4;
   __shared__ __attribute__((aligned(16))) __bf16 Q0[kTileElems], Q1[kTileElems], G0[kTileElems], G1[kTileElems];
@@ -353,11 +379,13 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 
   // (query tile, head) pairs that can see this key tile, head fastest; queries start at the key's block
   const int qt_lo = (k0 / per) * per / kBN;
-  // aligned: a content tile outside the raw prompt is seen by its own block's rows only, so the walk ends there
+  // aligned: a content tile outside the raw prompt and the retained tail is seen by its own block's rows only, so
+  // the walk ends there
+  const int tail = kTail ? f.tail : 0;
   int qt_end = f.num_q_tiles;
-  if (kAligned && k0 - (k0 / per) * per < f.C && (k0 / per) * f.C + (k0 - (k0 / per) * per) >= plen)
+  if (kAligned && k0 - (k0 / per) * per + kBN <= f.C - tail && (k0 / per) * f.C + (k0 - (k0 / per) * per) >= plen)
     qt_end = min(qt_end, (k0 / per + 1) * per / kBN);
-  int qt = qt_lo, h = -1, mode = 0, limit = 0;
+  int qt = qt_lo, h = -1, mode = 0, lim0 = 0, lim1 = 0;
   auto next_pair = [&]() -> bool {
     for (;;) {
       if (++h == kGroup) {
@@ -367,7 +395,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
       if (qt >= qt_end) return false;
       if constexpr (kAligned) {
         const int qh = h == 0 ? quota_all[0] : h == 1 ? quota_all[1] : h == 2 ? quota_all[2] : quota_all[3];
-        mode = pair_mode(qt, kt, qh, f.S0, f.C, per, plen, limit);
+        mode = pair_mode<kTail>(qt, kt, qh, f.S0, f.C, per, plen, tail, lim0, lim1);
         if (mode >= 0) return true;
       } else {
         mode = 3;
@@ -392,6 +420,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
     auto step = [&](auto buf_c) -> bool {
       constexpr int sl = decltype(buf_c)::value;
       const int cq = qt, ch = h, cmode = mode;
+      const int clim0 = kTail ? lim0 : 0, clim1 = kTail ? lim1 : 0;
       const bool hn = next_pair();
       __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
@@ -414,6 +443,23 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
               dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
             }
           }
+      } else if (kTail && (cmode == 2 || cmode == 4)) {     // visibility independent of the query row
+        // mode 2 key < lim0; mode 4 key outside [lim0, lim1): one flag for this lane's key column
+        const bool vis = cmode == 2 ? key < clim0 : (key < clim0 || key >= clim1);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int r0 = 32 * kk + 16 * t + 4 * j;
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(Lb[sl] + r0);
+            const floatx4 e4 = *reinterpret_cast<const floatx4*>(Eb[sl] + r0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
+              s[kk][t][0][r] = pr;
+              dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
+            }
+          }
       } else {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
@@ -425,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int qrow = cq * kBN + r0 + r;
-              // diagonal tiles: key <= row; bounded (mode 2) and unaligned tiles: the per-element predicate
+              // diagonal tiles: key <= row; bounded (mode 2, no tail) and unaligned tiles: the per-element predicate
               const bool vis = cmode == 1 ? key <= qrow : elem_visible(qrow, key, f.S0, f.C, per, plen, qh, f.tail);
               const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
               s[kk][t][0][r] = pr;
@@ -499,7 +545,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.out = nullptr; f.o_sb = f.o_ss = f.o_sh = 0;
   f.lse = nullptr;
   f.tail = retain_tail;
-  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && retain_tail == 0;
+  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;
@@ -523,13 +569,16 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned gq = prefill_grid(f.num_q_tiles, batch, 512);
-  if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true>), gq, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_bwd_dq_kernel<false>), gq, dim3(512), 0, stream, a);
+  if (f.aligned && retain_tail == 0) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, false>), gq, dim3(512), 0, stream, a);
+  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, true>), gq, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_bwd_dq_kernel<false, false>), gq, dim3(512), 0, stream, a);
   err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned gk = prefill_grid(f.num_q_tiles, batch, 256);
-  if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true>), gk, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_bwd_dkv_kernel<false>), gk, dim3(256), 0, stream, a);
+  if (f.aligned && retain_tail == 0)
+    hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, false>), gk, dim3(256), 0, stream, a);
+  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, true>), gk, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_bwd_dkv_kernel<false, false>), gk, dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 

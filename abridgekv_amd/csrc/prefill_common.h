@@ -16,7 +16,7 @@ struct PrefillArgs {
   float scale_log2;
   __bf16* out;      long o_sb, o_ss, o_sh;   // [B, S0, 32, 128]
   float* lse;                                // [B, 32, S0] natural log, or nullptr
-  int aligned;                               // C % 64 == 0 && K % 64 == 0 and no retained tail
+  int aligned;                               // C % 64 == 0 && K % 64 == 0 (the walk over visible tiles)
   int num_q_tiles;
   int tail;                                  // static retained tail T (0: none)
 };
@@ -37,19 +37,24 @@ __device__ __forceinline__ GridPos grid_pos(int batch) {
 // Aligned layouts (C and K multiples of 64): a key tile is named by (block kb, tile tw of the block's C + K rows).
 // Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
 // ends the segment and the walk jumps to the next one: no per-tile test of skipped tiles and no integer division.
+// kTail (aligned layouts with a static retained tail of T rows): an earlier block's content is visible where it is
+// raw prompt (a prefix) or tail (the last T rows), so after the prompt prefix the walk jumps to the tail's first tile;
+// a code query tile sees its own block's content below C - T only. The tile where hidden rows give way to the tail
+// (at most one per earlier block) hides the key range between the prompt's end and the tail (mode 4).
 // Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
-template <bool kAligned>
+template <bool kAligned, bool kTail = false>
 struct TileWalk {
-  static constexpr bool kHole = false;                      // never yields an excluded key range (mode 4)
-  int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles;
+  static constexpr bool kHole = kTail;                      // yields excluded key ranges (mode 4) with a tail
+  static constexpr bool kElem = false;                      // aligned walks never yield per-element tiles
+  int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles, tail;
   bool q_code;
   int kb, tw;
   int wq0, wq1;                                             // code quotas of this wave's two heads
 
   __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_,
-                                      int wq0_, int wq1_)
-      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), kb(0), tw(0),
-        wq0(wq0_), wq1(wq1_) {
+                                      int wq0_, int wq1_, int tail_ = 0)
+      : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), tail(kTail ? tail_ : 0),
+        kb(0), tw(0), wq0(wq0_), wq1(wq1_) {
     qb = q0 / per;
     q_code = q0 - qb * per >= C;
     tpb = per / kBN;
@@ -62,9 +67,22 @@ struct TileWalk {
     for (;;) {
       if (kb > qb) return false;
       if (tw < ct) {
-        const bool vis = kb == qb ? (q_code || kb * per + kBN * tw <= q_last) : (kb * C + kBN * tw < plen);
-        if (vis) return true;
-        tw = ct;                                            // the rest of this block's content is hidden too
+        if (kb == qb) {
+          // own block: content rows causally; codes see the content below C - T
+          if (q_code ? (!kTail || kBN * tw < C - tail) : kb * per + kBN * tw <= q_last) return true;
+          tw = ct;                                          // the rest of this block's content is hidden too
+        } else {
+          if (kb * C + kBN * tw < plen) return true;        // raw-prompt prefix
+          if constexpr (kTail) {
+            const int tail_tile = (C - tail) / kBN;         // first tile holding tail rows
+            if (tail > 0 && tw <= tail_tile) {
+              tw = tail_tile;
+              return true;
+            }
+            if (tail > 0 && tw < ct) return true;           // later tiles of the tail
+          }
+          tw = ct;
+        }
       }
       if ((kb < qb || q_code) && tw < tpb && kBN * (tw - ct) < qmax) return true;
       if (kb == qb) return false;                           // blocks after the query's own block are hidden
@@ -80,9 +98,25 @@ struct TileWalk {
     if (tw < ct) {
       if (kb == qb) {
         if (!q_code && k0 + kBN - 1 > q0) tm.mode = 1;      // diagonal tile of the block's content
-      } else if (kb * C + kBN * tw + kBN > plen) {
-        tm.mode = 2;                                        // raw-prompt boundary inside the tile
-        tm.limit[0] = tm.limit[1] = kb * per + (plen - kb * C);
+        if (kTail && q_code && kBN * tw + kBN > C - tail) {
+          tm.mode = 2;                                      // the codes' own tail begins inside the tile
+          tm.limit[0] = tm.limit[1] = kb * per + C - tail;
+        }
+      } else {
+        const int pl = min(max(plen - kb * C, 0), C);       // raw-prompt rows of this block's content
+        const int lo = kBN * tw, hi = lo + kBN;
+        const bool in_prompt = hi <= pl;
+        const bool in_tail = kTail && lo >= C - tail;
+        if (!in_prompt && !in_tail) {
+          if (!kTail || hi <= C - tail) {                   // raw-prompt boundary inside the tile
+            tm.mode = 2;
+            tm.limit[0] = tm.limit[1] = kb * per + pl;
+          } else if (pl < C - tail) {                       // [prompt rows,] hidden rows, tail rows
+            tm.mode = 4;
+            tm.limit[0] = kb * per + pl;
+            tm.limit[1] = kb * per + C - tail;
+          }                                                 // else prompt rows up to the tail: all visible
+        }
       }
     } else if (kBN * (tw - ct) + kBN > qmin) {
       tm.mode = 2;                                          // quota boundary inside a code tile
