@@ -1,12 +1,15 @@
 """Serving configuration of the abridged cache (API-compatible subset of the reference's CompressLMConfig).
 
 Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309 for the configuration this path serves: one pause
-pass, raw prompt, bitrev code positions, an optional STATIC retained tail (retain_tail_kv = T with
-retain_tail_policy="static": the last T content rows of every block stay resident and the codes summarize only the
-first C - T, compresslm.py:22-25, 192-206), optional per-layer quotas with physical removal, or per-head quotas in
-packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as at compresslm.py:145-190). Options of the
-reference that belong to other modes (replay / raw tails, the rolling and sticky window tails, selective
-full-history evaluation) are rejected with ValueError instead of being silently ignored.
+pass, raw prompt, bitrev code positions, an optional retained tail of T = retain_tail_kv original content rows
+per block (compresslm.py:22-26): "static" keeps the last T content rows of every block resident for every later
+query; the window policies keep the previous block's tail for the next block's content queries only, "rolling"
+expiring one row per next-block content token and "sticky" all of it before the next block's codes. The codes of a
+block summarize only its first C - T content rows (compresslm.py:192-206, 254-257). Optional per-layer quotas with
+physical removal, or per-head quotas in packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as
+at compresslm.py:145-190; packed KV takes only the static tail). Options of the reference that belong to other modes
+(replay / raw tails, selective full-history evaluation) are rejected with ValueError instead of being silently
+ignored.
 """
 from __future__ import annotations
 
@@ -121,9 +124,6 @@ class CompressLMConfig:
             raise ValueError("retain_tail_kv must be in [0, block_size)")
         if self.retain_tail_policy == "sticky" and not self.retain_tail_kv:
             raise ValueError("retain_tail_policy='sticky' requires retain_tail_kv > 0")
-        if self.retain_tail_kv and self.retain_tail_policy != "static":
-            raise ValueError("only the static retained tail is served (retain_tail_policy='static'); the rolling / "
-                             "sticky window tails are not")
         if C - self.retain_tail_kv < K:
             raise ValueError(f"bitrev code span {C - self.retain_tail_kv} < num_code_tokens {K}")
         if self.num_passes != 1:
@@ -140,6 +140,9 @@ class CompressLMConfig:
         if self.packed_kv and any(q < K for q in self.layer_code_quotas):
             raise ValueError("layer_code_quotas and packed KV are mutually exclusive")
         if self.packed_kv:
+            if self.retain_tail_kv and self.retain_tail_policy != "static":
+                raise ValueError("packed KV supports code/replay checkpoints and the static retained tail, not window "
+                                 "(rolling/sticky) or raw tails")
             if self.packed_kv_k_max != K:
                 raise ValueError("packed_kv_k_max must equal num_code_tokens so the dense code pass computes every "
                                  "schedulable slot")
@@ -201,7 +204,7 @@ class CompressLMConfig:
     @property
     def code_excluded_tail(self) -> int:
         """Content rows at the end of each block that the block's own codes never see and do not summarize (the
-        static retained tail: compresslm.py:254-257 with no replay tail)."""
+        retained tail, whatever its policy: compresslm.py:254-257 with no replay tail)."""
         return self.retain_tail_kv
 
     def bitrev_code_offsets(self) -> np.ndarray:

@@ -2,12 +2,19 @@
 
 API-compatible with the reference's CompressLMProcessor (third_party/vllm_overlay/vllm/v1/core/compresslm/
 processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay tail, an optional
-static retained tail, physical per-layer quotas or per-head packed KV pages): prepare_request :42-105, is_code_ready /
-num_code_rows_pending :106-121, limit_num_new_tokens :123-151, should_skip_sampling :153-168, update_after_step
-:170-257, reset_for_preemption :259-260, code_excluded_logical_range :262-274, code_physical_spans :276-316,
-_stage_codes :369-400, _finish_block :419-465, _compact_response_content :467-557, _mask_or_raise :648-661,
-_check_stop :663-685; the physical exclusion ranges of a code step restate sched/scheduler.py:979-991. The compaction
-callback ``mask_span(request_id, start, end, groups=None)`` is KVPlanner.mask_token_span.
+retained tail under the static, rolling or sticky policy, physical per-layer quotas or per-head packed KV pages):
+prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121, limit_num_new_tokens :123-151,
+should_skip_sampling :153-168, update_after_step :170-257, reset_for_preemption :259-260 (state.py:46-50),
+code_excluded_logical_range :262-274, code_physical_spans :276-316, _record_content :318-353, _stage_codes :369-400,
+_finish_block :419-465, _compact_response_content :467-557, _expire_sticky_retained_tail_at_boundary :559-592,
+_expire_retained_tail_after_content :614-646, _mask_or_raise :648-661, _check_stop :663-685; the physical exclusion
+ranges of a code step restate sched/scheduler.py:979-991. The compaction callback
+``mask_span(request_id, start, end, groups=None)`` is KVPlanner.mask_token_span.
+
+Window tails: a block's last T content rows survive its compaction; under "rolling" the i-th content token of the
+next block removes the tail's i-th row (a response row; raw-prompt rows stay) after its step, and a content chunk
+ends at every such token so each removal follows a query of its own; under "sticky" the tail's response rows go as
+one span after the next block's last content token and before its codes.
 """
 from __future__ import annotations
 
@@ -69,12 +76,17 @@ class CompressLMState:
     compacted_block_ids: set[int] = field(default_factory=set)
     current_block_id: int = 0
     worker_token_ids_dirty: bool = False
+    content_to_expired_retained_tail: dict[int, int] = field(default_factory=dict)
+    expired_retained_tail_positions: set[int] = field(default_factory=set)
+    expired_sticky_retained_block_ids: set[int] = field(default_factory=set)
 
     @property
     def current_block(self) -> CompressLMBlock:
         return self.blocks[self.current_block_id]
 
     def reset_compaction_progress(self) -> None:
+        self.expired_retained_tail_positions.clear()
+        self.expired_sticky_retained_block_ids.clear()
         self.compacted_block_ids.clear()
 
 
@@ -138,7 +150,7 @@ def _run_end(roles: list[int], start: int, stop: int) -> int:
 
 
 def _no_mask(*_args, **_kwargs):
-    raise RuntimeError("a replayed decode step cannot compact a block")
+    raise RuntimeError("a replayed decode step cannot compact a block or expire a retained tail")
 
 
 class CompressLMProcessor:
@@ -148,6 +160,9 @@ class CompressLMProcessor:
         self.config = config
         self.group_quotas: tuple[int, ...] | None = None
         self._code_removals: list[tuple[int, list[int]]] = []
+        T = config.retain_tail_kv
+        self._rolling = T if config.retain_tail_policy == "rolling" else 0
+        self._sticky = bool(T) and config.retain_tail_policy == "sticky"
 
     def set_group_quotas(self, group_quotas: Sequence[int] | None) -> None:
         if group_quotas is None:
@@ -238,7 +253,13 @@ class CompressLMProcessor:
         remaining = _run_end(state.roles, start, request.num_tokens) - start
         if role == CODE:
             return remaining if proposed >= remaining else 0
-        return min(proposed, remaining)
+        limit = min(proposed, remaining)
+        expiring = state.content_to_expired_retained_tail
+        if expiring:                                      # a rolling expiry ends the chunk
+            for pos in range(start, start + limit):
+                if pos in expiring:
+                    return pos - start + 1
+        return limit
 
     def should_skip_sampling(self, request, num_scheduled_tokens: int) -> bool:
         state = request.compresslm_state
@@ -266,6 +287,8 @@ class CompressLMProcessor:
         role = state.roles[start]
         if _run_end(state.roles, start, end) != end:
             raise RuntimeError("CompressLM scheduled a mixed-role model step")
+        if role == CONTENT and state.content_to_expired_retained_tail:
+            self._expire_retained_tail_after_content(state, request, start, end, mask_span)
         sampled = sampled_token_ids[0] if sampled_token_ids else None
         visible: list[int] = []
         if sampled is not None:
@@ -277,6 +300,10 @@ class CompressLMProcessor:
         role_end = end == request.num_tokens or state.roles[end] != role
         if role == CONTENT:
             if len(block.content_positions) == self.config.block_size and end == block.content_positions[-1] + 1:
+                if self._sticky:
+                    # after the block's last content query, before its codes (also in a preemption replay, where
+                    # the codes exist already)
+                    self._expire_sticky_retained_tail_at_boundary(request, state, block, mask_span)
                 if block.code_span is None:
                     if end + self.config.num_code_tokens >= max_model_len:
                         request.status = RequestStatus.FINISHED_LENGTH_CAPPED
@@ -311,6 +338,7 @@ class CompressLMProcessor:
                 and state.roles[start] == CONTENT and block is state.current_block
                 and len(block.content_positions) + m <= self.config.block_size
                 and block.content_positions[-1] == start and (not stops or stops.isdisjoint(ids))
+                and (not self._rolling or not block.block_id or len(block.content_positions) > self._rolling)
                 and request.num_tokens + m < max_model_len
                 and len(state.visible_output_token_ids) + m < request.max_tokens)
         if not fast:
@@ -328,14 +356,20 @@ class CompressLMProcessor:
         state.reset_compaction_progress()
 
     def code_excluded_logical_range(self, request) -> tuple[int, int] | None:
-        """Logical [start, end) of the current block's content rows its own codes must not see (the static tail),
-        or None without a tail."""
+        """Logical [start, end) of the content rows the scheduled code step's codes must not see (their block's
+        retained tail), or None without a tail. The block is the one whose code rows are scheduled: the current
+        block, except in a preemption replay, where earlier blocks' code steps run again (the reference reads the
+        current block there, processor.py:262-274, which fails or names the wrong rows in a replay)."""
         if not self.config.code_excluded_tail:
             return None
         state = request.compresslm_state
         if state is None:
             raise RuntimeError("CompressLM request has no state")
-        block = state.current_block
+        start = request.num_computed_tokens
+        if start < len(state.roles) and state.roles[start] == CODE:
+            block = state.blocks[state.position_to_block[start]]
+        else:
+            block = state.current_block
         if block.code_excluded_content_span is None:
             raise RuntimeError("tail-exclusive code block has no source span")
         return block.code_excluded_content_span
@@ -383,12 +417,22 @@ class CompressLMProcessor:
     def _record_content(self, state: CompressLMState, start: int, token_ids, is_prompt: bool) -> None:
         block = state.current_block
         n = len(token_ids)
+        within = len(block.content_positions)
         positions = range(start, start + n)
         block.content_positions.extend(positions)
         block.content_token_ids.extend(token_ids)
         (block.prompt_content_positions if is_prompt else block.response_content_positions).extend(positions)
         state.roles.extend([CONTENT] * n)
         state.position_to_block.extend([block.block_id] * n)
+        if self._rolling and block.block_id and within < self._rolling:
+            # the i-th content token of the block expires the previous block's i-th tail row if it is a response
+            # row (a block's response rows are one contiguous run after its prompt rows)
+            prev = state.blocks[block.block_id - 1]
+            tail, resp = prev.retained_tail_positions, prev.response_content_positions
+            for i in range(within, min(within + n, len(tail))):
+                row = tail[i]
+                if resp and resp[0] <= row <= resp[-1]:
+                    state.content_to_expired_retained_tail[start + i - within] = row
 
     def _append_content(self, request, state, token_ids, is_prompt: bool) -> None:
         if not token_ids:
@@ -414,6 +458,8 @@ class CompressLMProcessor:
         state.worker_token_ids_dirty = True
 
     def _finish_block(self, request, state, block, mask_span, pack_code_span=None) -> None:
+        if self._sticky:                                      # done at the block's last content step already
+            self._expire_sticky_retained_tail_at_boundary(request, state, block, mask_span)
         self._compact_response_content(request, state, block, mask_span, pack_code_span)
         if block.code_span[1] < request.num_tokens:          # preemption replay: later tokens already exist
             return
@@ -480,6 +526,33 @@ class CompressLMProcessor:
         for start, end, groups in spans:
             self._mask_or_raise(mask_span, request.request_id, start, end, groups=groups)
         state.compacted_block_ids.add(block.block_id)
+
+    def _expire_sticky_retained_tail_at_boundary(self, request, state, block, mask_span) -> None:
+        """Sticky policy: remove the previous block's retained response rows as one span, once per block
+        (processor.py:559-592)."""
+        if not block.block_id:
+            return
+        prev = state.blocks[block.block_id - 1]
+        if prev.block_id in state.expired_sticky_retained_block_ids:
+            return
+        resp = prev.response_content_positions
+        rows = [p for p in prev.retained_tail_positions if resp and resp[0] <= p <= resp[-1]]
+        if rows:
+            if rows[-1] - rows[0] + 1 != len(rows):
+                raise RuntimeError("sticky retained response tail must be contiguous")
+            self._mask_or_raise(mask_span, request.request_id, rows[0], rows[-1] + 1)
+        state.expired_sticky_retained_block_ids.add(prev.block_id)
+
+    def _expire_retained_tail_after_content(self, state, request, start, end, mask_span) -> None:
+        """Rolling policy: remove each previous-block tail row whose expiring content token ran in [start, end)
+        (processor.py:614-646)."""
+        expiring, expired = state.content_to_expired_retained_tail, state.expired_retained_tail_positions
+        for pos in range(start, end):
+            row = expiring.get(pos)
+            if row is None or row in expired:
+                continue
+            self._mask_or_raise(mask_span, request.request_id, row, row + 1)
+            expired.add(row)
 
     @staticmethod
     def _mask_or_raise(mask_span, request_id, start, end, groups=None) -> None:

@@ -6,17 +6,23 @@ tokens, optional per-query-head code quota):
   causal & (own-block content | earlier blocks' codes | raw-prompt content)  |  (code query & code key & same block)
   and, with a quota, a code key is visible to head h only if its slot < quota[h].
 
-With a static retained tail of T rows (retain_tail_kv = T, policy "static"): the last T content rows of every earlier
-block are visible to every later query (causal), and a block's codes never see its own last T content rows.
+With a retained tail of T rows (retain_tail_kv = T) a block's codes never see its own last T content rows, and the
+last T content rows of an earlier block are visible, by ``tail_policy``
+(abridgekv/compress_forward.py:99-124, _retained_tail_visible):
+  "static"  -- to every later query (content and codes);
+  "sticky"  -- to the content queries of the next block only;
+  "rolling" -- to the content queries of the next block through a sliding window: content query i of block b sees
+               row j of block b - 1 iff (b C + i) - ((b - 1) C + j) <= T, i.e. j >= C - T + i.
 
 Two independent restatements of the reference are kept and cross-checked:
 * ``arith_mask``  -- closed-form integer arithmetic: abridgekv/compress_forward.py:695-727 (_arith_mask_mod) with
-                     the quota term of :725-726 and the static-tail terms of :714-715, :721-722.
+                     the quota term of :725-726 and the static-tail terms of :714-715, :721-722; the window policies
+                     (which the reference sends to its gather-based _mask_mod, :566-649) as the same integer terms.
 * ``role_mask``   -- role/block/content-position gathers: abridgekv/gen_compress.py:1062-1140 (_dense_mask, the
-                     reference's own dense oracle) restricted to L=1, no replay / raw tail, with its static
-                     ``retained_tail`` term (:1088-1094) and the own-tail exclusion of compress_forward.py:139-155
-                     (_code_content_tail_excluded), plus the quota rule of abridgekv/compress_forward.py:230-236
-                     (_quota_key_allowed).
+                     reference's own dense oracle) restricted to L=1, no replay / raw tail, with its
+                     ``retained_tail`` term for the three policies (:1088-1112) and the own-tail exclusion of
+                     compress_forward.py:139-155 (_code_content_tail_excluded), plus the quota rule of
+                     abridgekv/compress_forward.py:230-236 (_quota_key_allowed).
 Pinning: the two agree element by element on every tested shape; brute-force per-element predicates written from
 the prose rule (tests/test_oracle_prefill.py); N=1 without codes reduces to the causal mask; masked_attention_fp64
 reduces to textbook causal attention under the causal mask and to per-row softmax identities (rows sum to one,
@@ -27,13 +33,16 @@ from __future__ import annotations
 import numpy as np
 
 
-def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0):
+TAIL_POLICIES = ("static", "rolling", "sticky")
+
+
+def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
     """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
     S0 = N * (C + K)
-    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail)
+    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail, tail_policy)
 
 
-def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0):
+def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
     per = C + K
@@ -44,9 +53,17 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     k_content = kw < C
     same_blk = kb == qb
     T = int(retain_tail)
+    if tail_policy not in TAIL_POLICIES:
+        raise ValueError(f"unknown tail policy {tail_policy!r}")
     vis = (k_content & same_blk) | ((~k_content) & (kb < qb))
-    if T:
+    if T and tail_policy == "static":
         vis = vis | (k_content & (kb < qb) & (kw >= C - T))                 # earlier blocks' static tails
+    elif T:
+        nxt = (qw < C) & k_content & (kb + 1 == qb)                         # next block's content queries
+        if tail_policy == "sticky":
+            vis = vis | (nxt & (kw >= C - T))
+        else:
+            vis = vis | (nxt & (C + qw - kw <= T))                          # sliding window
     if prompt_len is not None:
         pl = np.asarray(prompt_len, dtype=np.int64).reshape(-1, 1, 1)
         vis = vis[None] | (k_content & (kb * C + kw < pl))[...]
@@ -64,7 +81,7 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     return vis
 
 
-def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0):
+def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
     """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
     per = C + K
     S0 = N * per
@@ -81,7 +98,14 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0):
     pause_q = qr == 1
     samepass = pause_q & (kr == qr) & (kb == qb)
     T = int(retain_tail)
-    retained = (kr == 0) & (kb < qb) & (content_abs.reshape(1, S0) % C >= C - T) & (T > 0)
+    qa, ka = content_abs.reshape(S0, 1), content_abs.reshape(1, S0)
+    if tail_policy == "static":
+        retained = (kr == 0) & (kb < qb) & (ka % C >= C - T) & (T > 0)
+    elif tail_policy in ("rolling", "sticky"):
+        window = (ka % C >= C - T) if tail_policy == "sticky" else (qa - ka <= T)
+        retained = (qr == 0) & (kr == 0) & (kb + 1 == qb) & window & (T > 0)
+    else:
+        raise ValueError(f"unknown tail policy {tail_policy!r}")
     base = (causal & (content_vis | earlier_final | retained)) | samepass
     if prompt_len is not None:
         pl = np.asarray(prompt_len).reshape(-1, 1, 1)
@@ -241,9 +265,10 @@ def dense_masked_attention_ref_torch(q, k, v, mask, scale):
     return torch.matmul(w, vv)
 
 
-def visible_pairs(C, K, N, prompt_len=None, retain_tail=0):
+def visible_pairs(C, K, N, prompt_len=None, retain_tail=0, tail_policy="static"):
     """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
-    m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len], retain_tail=retain_tail)
+    m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len], retain_tail=retain_tail,
+                   tail_policy=tail_policy)
     return int(m.sum())
 
 

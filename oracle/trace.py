@@ -8,9 +8,18 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:
   a CONTENT run up to its end), should_skip_sampling :153-168, update_after_step :170-257 (a full block stages
   its K codes and holds the sampled token), _stage_codes :369-400, _finish_block :419-465 (compact, then open the
   next block with the next prompt chunk or the held token), _compact_response_content :467-557 (response content
-  in every group, then code slots [q, K) per distinct quota q < K in ascending order). With a static retained tail
-  (``retain_tail`` = T, compresslm.py:22-25) the block's last T content rows are never removed (:480-482): the
-  response content before them goes.
+  in every group, then code slots [q, K) per distinct quota q < K in ascending order). With a retained tail
+  (``retain_tail`` = T, compresslm.py:22-26) the block's last T content rows are not removed with the block
+  (:480-482): the response content before them goes. Their fate is the tail policy's:
+    "static"  -- they stay for the rest of the request;
+    "rolling" -- the i-th content token of the next block expires the tail's i-th row once it has run (a one-row
+                 removal of a response row; :320-353 maps it, :123-151 ends a chunk at every such token so each
+                 expiry has a query of its own, :614-646 removes it);
+    "sticky"  -- the tail's response rows go as one span after the next block's last content token has run,
+                 before that block's codes (:559-592, called from :215-224 and again, as a no-op, from :427-430).
+  Preemption (``preempt``) restarts the request at token 0 with its logical stream and block structure kept and
+  its compaction progress cleared (state.py:46-50); the replay compacts every closed block again and opens no block
+  that already exists (:429-431).
 
 The machine is planner-agnostic: it emits the scheduler-visible events (allocate ``n`` new tokens, then compact
 spans) and is shared by the oracle planner and the product planner so that both see identical event streams.
@@ -41,11 +50,17 @@ class Block:
 class RequestTrace:
     """Logical token stream of one request and its block structure."""
 
-    def __init__(self, prompt_len, max_tokens, C, K, group_quotas, retain_tail=0):
+    def __init__(self, prompt_len, max_tokens, C, K, group_quotas, retain_tail=0, tail_policy="static"):
         if prompt_len <= 0:
             raise ValueError("CompressLM decoding requires a non-empty prompt")
+        if tail_policy not in ("static", "rolling", "sticky"):
+            raise ValueError(f"unknown tail policy {tail_policy!r}")
         self.C, self.K = C, K
         self.T = retain_tail
+        self.policy = tail_policy
+        self.expire_at: dict[int, int] = {}     # rolling: content position -> previous block's tail row it expires
+        self.expired: set[int] = set()          # rolling tail rows removed so far
+        self.sticky_done: set[int] = set()      # blocks whose tail the sticky policy has removed
         self.group_quotas = tuple(group_quotas)
         self.prompt_len = prompt_len
         self.max_tokens = max_tokens
@@ -70,14 +85,24 @@ class RequestTrace:
     def current_block(self):
         return self.blocks[-1]
 
-    def _record_content(self, n, is_prompt):       # processor.py:318-353 (no tails)
+    def _tail_rows(self, block):
+        """The block's retained tail (its last T content rows) once its codes are staged."""
+        return block.content_positions[-self.T:] if self.T and block.code_span else []
+
+    def _record_content(self, n, is_prompt):       # processor.py:318-353
         block = self.current_block
+        prev = self.blocks[-2] if len(self.blocks) > 1 else None
         for _ in range(n):
             pos = len(self.roles)
+            within = len(block.content_positions)
             block.content_positions.append(pos)
             (block.prompt_positions if is_prompt else block.response_positions).append(pos)
             self.roles.append(CONTENT)
             self.kind.append("prompt" if is_prompt else "response")
+            if self.policy == "rolling" and prev is not None and within < len(self._tail_rows(prev)):
+                row = self._tail_rows(prev)[within]
+                if self.kind[row] == "response":   # raw-prompt rows never leave
+                    self.expire_at[pos] = row
 
     def next_chunk(self):
         """Tokens the scheduler runs next for this request (limit_num_new_tokens with an unbounded budget)."""
@@ -88,7 +113,18 @@ class RequestTrace:
         end = start + 1
         while end < self.num_tokens and self.roles[end] == role:
             end += 1
+        if role == CONTENT:
+            for pos in range(start, end):          # a rolling expiry ends the chunk
+                if pos in self.expire_at:
+                    return pos - start + 1
         return end - start
+
+    def preempt(self):
+        """Restart at token 0 with the logical stream kept and the compaction progress cleared."""
+        self.num_computed_tokens = 0
+        self.compacted_block_ids.clear()
+        self.expired.clear()
+        self.sticky_done.clear()
 
     def should_skip_sampling(self, n):             # processor.py:153-168
         start = self.num_computed_tokens - n
@@ -107,6 +143,12 @@ class RequestTrace:
         role = self.roles[start]
         sampled = not self.should_skip_sampling(n)
         calls = []
+        if role == CONTENT:                            # rolling expiries of the rows this step's queries saw last
+            for pos in range(start, end):
+                row = self.expire_at.get(pos)
+                if row is not None and row not in self.expired:
+                    calls.append((row, row + 1, None))
+                    self.expired.add(row)
         if sampled:
             self.visible += 1
             if self.visible >= self.max_tokens:        # _check_stop (processor.py:663-685), length cap
@@ -116,6 +158,7 @@ class RequestTrace:
         role_end = end == self.num_tokens or self.roles[end] != role
         if role == CONTENT:
             if len(block.content_positions) == self.C and end == block.content_positions[-1] + 1:
+                calls += self._sticky_expire(block)
                 if block.code_span is None:
                     self.held = sampled
                     cs = self.num_tokens                    # _stage_codes (processor.py:369-400)
@@ -136,8 +179,21 @@ class RequestTrace:
                     return b.block_id
         raise RuntimeError(f"position {pos} outside every block")
 
+    def _sticky_expire(self, block):               # processor.py:559-592
+        """Sticky policy: the previous block's tail response rows as one removal, once."""
+        if self.policy != "sticky" or not block.block_id or block.block_id - 1 in self.sticky_done:
+            return []
+        prev = self.blocks[block.block_id - 1]
+        self.sticky_done.add(prev.block_id)
+        rows = [p for p in self._tail_rows(prev) if self.kind[p] == "response"]
+        if not rows:
+            return []
+        if rows != list(range(rows[0], rows[-1] + 1)):
+            raise RuntimeError("sticky retained response tail must be contiguous")
+        return [(rows[0], rows[-1] + 1, None)]
+
     def _finish_block(self, block):                # processor.py:419-465, :467-557
-        calls = []
+        calls = self._sticky_expire(block)
         if block.block_id not in self.compacted_block_ids:
             tail = set(block.content_positions[-self.T:]) if self.T else set()
             pos = [p for p in block.response_positions if p not in tail]
@@ -151,6 +207,8 @@ class RequestTrace:
                     continue
                 calls.append((cs + q, ce, [g for g, gq in enumerate(self.group_quotas) if gq == q]))
             self.compacted_block_ids.add(block.block_id)
+        if block.code_span[1] < self.num_tokens:       # a preemption replay: the next block exists
+            return calls
         nxt = Block(len(self.blocks))
         self.blocks.append(nxt)
         if self.pending_prompt < self.prompt_len:
@@ -172,8 +230,14 @@ class RequestTrace:
             compacted = b.block_id in self.compacted_block_ids
             tail = set(b.content_positions[-self.T:]) if self.T else set()
             for p in b.content_positions:
-                if p < self.num_computed_tokens and not (compacted and self.kind[p] == "response" and p not in tail):
-                    keep.append(p)
+                if p >= self.num_computed_tokens:
+                    continue
+                if self.kind[p] == "response":
+                    if compacted and p not in tail:
+                        continue                       # summarized response content
+                    if p in self.expired or (p in tail and b.block_id in self.sticky_done):
+                        continue                       # an expired window-tail row
+                keep.append(p)
             if b.code_span:
                 cs, ce = b.code_span
                 for p in range(cs, min(ce, self.num_computed_tokens)):

@@ -12,11 +12,14 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None, tail=0):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static"):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
-    all later queries (content and code rows), and the codes summarize only the first block_size - T tokens"."""
+    all later queries (content and code rows), and the codes summarize only the first block_size - T tokens".
+    Window tails (compresslm.py:23, "window tails of the previous block (content queries only, expire)"): sticky
+    keeps the previous block's whole tail for every content query of the block; rolling lets the i-th content token
+    of the block see the previous block's tail rows from the i-th on (one tail row expires per content token)."""
     per = C + K
     S = N * per
     m = np.zeros((S, S), bool)
@@ -28,8 +31,12 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0):
             vis = (k_content and kb == qb) or ((not k_content) and kb < qb)
             if prompt_len is not None and k_content and kb * C + kw < prompt_len:
                 vis = True
-            if tail and k_content and kb < qb and kw >= C - tail:
+            if tail and policy == "static" and k_content and kb < qb and kw >= C - tail:
                 vis = True                       # an earlier block's tail row: resident, seen by every later query
+            if tail and policy != "static" and qw < C and k_content and kb == qb - 1:
+                row = kw - (C - tail)            # index of the key in the previous block's tail (< 0: not in it)
+                if row >= 0 and (policy == "sticky" or row >= qw):
+                    vis = True
             vis = vis and k <= q
             if qw >= C and not k_content and kb == qb:
                 vis = True
@@ -67,6 +74,42 @@ def test_static_tail_arith_equals_role_equals_brute(C, K, N, T):
     for b, p in enumerate(pl):
         for h, q in enumerate(hq):
             assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T))
+
+
+@pytest.mark.parametrize("policy", ["rolling", "sticky"])
+@pytest.mark.parametrize("C,K,N,T", [(4, 2, 3, 2), (8, 4, 3, 3), (8, 2, 4, 1), (6, 4, 3, 5)])
+def test_window_tail_arith_equals_role_equals_brute(C, K, N, T, policy):
+    a = op.arith_mask(C, K, N, retain_tail=T, tail_policy=policy)
+    assert np.array_equal(a, op.role_mask(C, K, N, retain_tail=T, tail_policy=policy))
+    assert np.array_equal(a, brute(C, K, N, tail=T, policy=policy))
+    assert not np.array_equal(a, op.arith_mask(C, K, N, retain_tail=T))       # not the static mask
+    pl = [0, 3, C + 1, N * C]
+    hq = [1, K, 2, K]
+    ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, retain_tail=T, tail_policy=policy)
+    assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, retain_tail=T, tail_policy=policy))
+    for b, p in enumerate(pl):
+        for h, q in enumerate(hq):
+            assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T, policy=policy))
+
+
+def test_window_tail_spot_checks():
+    """Rolling: block 1's i-th content row sees block 0's tail rows i.. only, block 2 sees none of block 0's tail,
+    codes see no earlier tail. Sticky: all of block 0's tail for every content row of block 1, none for its codes.
+    Both: a raw-prompt tail row stays visible to everyone."""
+    C, K, N, T = 8, 4, 3, 3
+    per = C + K
+    r = op.arith_mask(C, K, N, retain_tail=T, tail_policy="rolling")
+    assert r[per, C - T] and r[per, C - 1] and not r[per, C - T - 1]
+    assert not r[per + 1, C - T] and r[per + 1, C - T + 1] and r[per + 2, C - 1] and not r[per + 3, C - 1]
+    assert not r[2 * per, C - 1] and not r[per + C, C - 1] and not r[2 * per + C, per + C - 1]
+    assert r[2 * per, per + C - 1] and r[C, 0] and not r[C, C - T]          # own-tail exclusion kept
+    s = op.arith_mask(C, K, N, retain_tail=T, tail_policy="sticky")
+    assert all(s[per + i, C - T] and s[per + i, C - 1] for i in range(C)) and not s[per, C - T - 1]
+    assert not s[per + C, C - 1] and not s[2 * per, C - 1]
+    for pol in ("rolling", "sticky"):
+        m = op.arith_mask(C, K, N, prompt_len=[C], retain_tail=T, tail_policy=pol)[0]
+        assert m[2 * per + C, C - 1] and m[per + C, C - T]                   # prompt rows: raw prompt
+        assert not m[C, C - 1]                                               # but not for their own block's codes
 
 
 def test_static_tail_spot_checks():

@@ -58,7 +58,7 @@ def run_case(prompt, generated, T=2, packed=False, quotas=None, C=4, K=2):
     return req, state, masks, packs
 
 
-def test_config_accepts_only_the_static_tail():
+def test_config_static_tail():
     cfg = CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy="static",
                            packed_kv=True, packed_kv_k_max=4)
     assert cfg.code_excluded_tail == 2
@@ -69,9 +69,10 @@ def test_config_accepts_only_the_static_tail():
         CompressLMConfig(retain_tail_policy="invalid")
     with pytest.raises(ValueError, match="retain_tail_kv > 0"):
         CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_policy="sticky")
-    for policy in ("rolling", "sticky"):                                     # window tails are not served
+    for policy in ("rolling", "sticky"):                                     # window tails: not with packed KV
         with pytest.raises(ValueError, match="static"):
-            CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy=policy)
+            CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy=policy,
+                             packed_kv=True, packed_kv_k_max=4)
     with pytest.raises(ValueError, match="block_size"):
         CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=8, retain_tail_policy="static")
     with pytest.raises(ValueError, match="span"):
