@@ -2,17 +2,19 @@
 
 Mirrors the served subset of abridgekv/compress_forward.py:240-1230 (``CompressLM``): one pause pass (L=1) with
 bidirectional code<->code attention in a block (``pause_xattn="full"``), optional raw prompt, optional fixed
-per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` / ``bitrev`` code positions and the static
-retained tail (``retain_tail_kv`` = T with ``retain_tail_policy="static"``: every earlier block's last T content rows
-stay visible, a block's codes do not see or summarize its own; bitrev codes spread over the first C - T). The sequence
+per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` / ``bitrev`` code positions and the retained
+tail (``retain_tail_kv`` = T: a block's codes do not see or summarize its last T content rows, bitrev codes spread
+over the first C - T; by ``retain_tail_policy`` those rows stay visible to every later row ("static"), to the next
+block's content rows ("sticky"), or to the next block's i-th content row from tail row i on ("rolling"),
+compress_forward.py:99-124). The sequence
 layout, RoPE positions, loss positions and loss reductions follow the reference (compress_forward.py:20-88,
 1044-1071, 957-1042, 1134-1230); the attention of every decoder layer runs ``abkv_prefill_masked_attn`` through a
 HuggingFace attention function registered as ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask
 (``_arith_mask_mod`` / ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 695-727,
 815-894). The mask is never materialised: the kernel evaluates it from (C, K, N, prompt_len, head quota).
 
-Options of the reference that belong to other experiments (replay / raw tails, the rolling / sticky window tails,
-learned or segment pooling, query residuals, copy and distillation losses, external block masks) raise
+Options of the reference that belong to other experiments (replay / raw tails, learned or segment pooling, query
+residuals, copy and distillation losses, external block masks) raise
 NotImplementedError. Gradients
 flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module trains.
 """
@@ -34,14 +36,15 @@ ATTN_IMPLEMENTATION = "abridgekv_hip"
 class CompressMask:
     """What the kernel needs to evaluate the compression mask (the analogue of the reference's BlockMask):
     N blocks of [C content | K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
-    ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a static
-    retained tail (0: none)."""
+    ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a retained
+    tail (0: none) under ``tail_policy`` ("static", "rolling" or "sticky")."""
     block_c: int
     codes_k: int
     num_blocks: int
     prompt_len: torch.Tensor | None = None
     head_quota: torch.Tensor | None = None
     retain_tail: int = 0
+    tail_policy: str = "static"
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -59,7 +62,7 @@ class _MaskedPrefill(torch.autograd.Function):
             lse = torch.empty((q.shape[0], ops.HEADS_Q, q.shape[1]), dtype=torch.float32, device=q.device)
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
                                               prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
-                                              retain_tail=mask.retain_tail)
+                                              retain_tail=mask.retain_tail, tail_policy=mask.tail_policy)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -72,7 +75,8 @@ class _MaskedPrefill(torch.autograd.Function):
         g = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
         dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, g, m.block_c, m.codes_k, m.num_blocks,
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
-                                                           scale=ctx.scale, retain_tail=m.retain_tail)
+                                                           scale=ctx.scale, retain_tail=m.retain_tail,
+                                                           tail_policy=m.tail_policy)
         return dq, dk, dv, None, None, None
 
 
@@ -161,8 +165,6 @@ class CompressLM(nn.Module):
             raise ValueError(f"retain_tail_policy must be 'rolling', 'sticky' or 'static', got {retain_tail_policy!r}")
         if retain_tail_policy != "rolling" and not retain_tail_kv:
             raise ValueError(f"retain_tail_policy={retain_tail_policy!r} requires retain_tail_kv > 0")
-        if retain_tail_kv and retain_tail_policy != "static":
-            raise NotImplementedError("only the static retained tail is supported by the native forward")
         if code_positions not in ("appended", "bitrev"):
             raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
         if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1)):
@@ -252,7 +254,8 @@ class CompressLM(nn.Module):
             prompt_len = prompt_len.to(device=self.pause.device, dtype=torch.int32).contiguous()
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
-        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv)
+        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
+                            self.retain_tail_policy if self.retain_tail_kv else "static")
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:

@@ -41,7 +41,8 @@ struct F32Args {
   int block_c, codes_k, seq_len;
   const int32_t* prompt_len;   // [B] or nullptr
   const int32_t* head_quota;   // [32] or nullptr
-  int retain_tail;             // static retained tail T (0: none)
+  int retain_tail;             // retained tail T (0: none)
+  int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky)
   int num_tokens;
   float scale;
   float* out;
@@ -59,17 +60,18 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Compression-mask visibility of key row kr for query row qr (L = 1; _arith_mask_mod, abridgekv/compress_forward.py:
-// 695-727):
-//   (k <= q) & (own-block content | earlier blocks' codes | raw-prompt content | earlier blocks' last T content rows)
-//   | (code q & code k & same block), a code query never sees its own block's last T content rows (static retained
-//   tail T), and a code key of slot s is visible to a head only if s < quota.
+// 695-727, with the retained-tail term of _retained_tail_visible :99-124):
+//   (k <= q) & (own-block content | earlier blocks' codes | raw-prompt content | earlier blocks' tail rows the policy
+//   shows this row) | (code q & code k & same block), a code query never sees its own block's last T content rows,
+//   and a code key of slot s is visible to a head only if s < quota.
 __device__ __forceinline__ bool f32_visible(const F32Args& a, int qr, int kr, int plen, int quota) {
   const int per = a.block_c + a.codes_k;
   const int qb = qr / per, kb = kr / per;
   const int qw = qr - qb * per, kw = kr - kb * per;
   const bool kc = kw < a.block_c;
   const bool in_tail = kc && kw >= a.block_c - a.retain_tail;
-  bool vis = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * a.block_c + kw < plen) || (in_tail && kb < qb);
+  bool vis = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * a.block_c + kw < plen) ||
+             tail_visible(a.tail_policy, a.retain_tail, a.block_c, qb, qw, kb, kw);
   vis = (kr <= qr) && vis;
   vis = vis || (qw >= a.block_c && !kc && kb == qb);
   vis = vis && !(qw >= a.block_c && kb == qb && in_tail);
@@ -304,12 +306,13 @@ int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h
 int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh, const float* k, long k_sb,
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, float scale, float* out, long o_sb,
-                                 long o_ss, long o_sh, float* lse, hipStream_t stream) {
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale,
+                                 float* out, long o_sb, long o_ss, long o_sh, float* lse, hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
-      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c)
+      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
+      tail_policy < kTailStatic || tail_policy > kTailSticky)
     return (int)hipErrorInvalidValue;
   F32Args a = f32_defaults();
   a.mode = 1;
@@ -331,6 +334,7 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
   a.prompt_len = prompt_len;
   a.head_quota = head_quota;
   a.retain_tail = retain_tail;
+  a.tail_policy = tail_policy;
   a.num_tokens = batch * seq_len;
   a.scale = scale;
   a.out = out;

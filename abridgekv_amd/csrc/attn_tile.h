@@ -12,21 +12,22 @@ constexpr int kBM = 64;                  // query rows per workgroup
 constexpr int kBN = 64;                  // keys per tile
 constexpr int kTileElems = kBN * kHeadDim;
 
-// Per-element visibility for layouts whose tiles cannot be classified (unaligned masked prefill, or any layout with a
-// static retained tail); other kernels never call it (their tiles are always aligned: kAligned = true). quota[u]:
-// code slots visible to this wave's head u; tail: the static retained tail T (the last T content rows of an earlier
-// block are visible to every later row; a block's codes never see its own last T content rows).
+// Per-element visibility for layouts whose tiles cannot be classified (unaligned masked prefill); other kernels never
+// call it (their tiles are always aligned: kAligned = true). quota[u]: code slots visible to this wave's head u;
+// tail: the retained tail T under ``policy`` (a block's codes never see its own last T content rows).
 struct MaskGeom {
   int qrow, S0, C, per, plen;
   int quota[2];
   int tail;
+  int policy;
   __device__ __forceinline__ bool visible(int kv, int u) const {
     if (kv >= S0 || qrow >= S0) return false;
     const int qb = qrow / per, kb = kv / per;
     const int qw = qrow - qb * per, kw = kv - kb * per;
     const bool kc = kw < C;
     const bool in_tail = kc && kw >= C - tail;
-    bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) || (in_tail && kb < qb);
+    bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) ||
+             tail_visible(policy, tail, C, qb, qw, kb, kw);
     v = v && kv <= qrow;
     v = v || (qw >= C && !kc && kb == qb);
     v = v && !(qw >= C && kb == qb && in_tail);
@@ -135,7 +136,8 @@ __device__ __forceinline__ void store_bf16x8(__bf16* dst, const floatx4& lo, con
 
 struct TileMask {
   int mode;        // 0 none, 1 key < this lane's limit, 2 key < limit[u] (this wave's head u), 3 per-element mask,
-                   // 4 key < this lane's limit and outside the excluded range [limit[0], limit[1])
+                   // 4 key < this lane's limit and outside the excluded range [limit[0], limit[1]),
+                   // 5 key < limit[0] or key >= this lane's limit + limit[1] (a band that moves with the query row)
   int limit[2];
 };
 
@@ -200,14 +202,16 @@ __device__ __forceinline__ void tile_scores(const __bf16* Kbuf, const bf16x8 (&q
 }
 
 // Hidden keys of a partial tile get score -inf (tm.mode 0: nothing hidden). kElem: an aligned walk that may yield
-// per-element tiles (mode 3, the full predicate MaskGeom::visible) beside the limit modes.
-template <int H, bool kAligned, bool kHole = false, bool kElem = false>
+// per-element tiles (mode 3, the full predicate MaskGeom::visible) beside the limit modes. kBand: a walk that may
+// yield band tiles (mode 5, the rolling retained tail).
+template <int H, bool kAligned, bool kHole = false, bool kElem = false, bool kBand = false>
 __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const TileMask& tm, int lane_limit,
                                           const MaskGeom& geo, int j) {
   static_assert(H <= 2, "TileMask holds two per-head limits");
   if (tm.mode == 0) return;
   if constexpr (kHole) {
-    if (tm.mode == 4) {                                  // a walk with an excluded key range (code step, static tail)
+    if (tm.mode == 4 || (kBand && tm.mode == 5)) {       // an excluded key range (code step, retained tail) or a band
+      const bool band = kBand && tm.mode == 5;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -215,7 +219,8 @@ __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const T
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int kv = k0 + 32 * kk + 16 * t + 4 * j + r;
-            const bool ok = kv < lane_limit && (kv < tm.limit[0] || kv >= tm.limit[1]);
+            const bool ok = band ? (kv < tm.limit[0] || kv >= lane_limit + tm.limit[1])
+                                 : kv < lane_limit && (kv < tm.limit[0] || kv >= tm.limit[1]);
 #pragma unroll
             for (int u = 0; u < H; ++u) s[kk][t][u][r] = ok ? s[kk][t][u][r] : -INFINITY;
           }
@@ -394,7 +399,7 @@ __device__ __forceinline__ void attend_tiles(const Rows& rows, Walk& walk, int n
     __builtin_amdgcn_s_barrier();
     issue_half<kWaves, false>(rows, src_k, n_keys, K[slot], w, lane);
     issue_half<kWaves, true>(rows, src_v, n_keys, V[slot2], w, lane);
-    tile_mask<H, kAligned, Walk::kHole, Walk::kElem>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
+    tile_mask<H, kAligned, Walk::kHole, Walk::kElem, Walk::kBand>(s_cur, t0 * kBN, m0, lane_limit, geo, j);
     bf16x8 pop[2][H];
     tile_softmax<H>(s_cur, o, m_run, lsum, scale_log2, pop);
     // Unconditional so that the MFMAs can overlap the softmax work: after the last tile the scores are computed from

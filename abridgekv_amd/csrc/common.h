@@ -21,6 +21,20 @@ constexpr int kSlotElems = kHeadsKV * kHeadDim;            // 1024 elements = 2 
 constexpr int kHalfElems = kPage * kSlotElems;             // 16384 elements = 32 KiB (K half of a page)
 constexpr int kPageElems = 2 * kHalfElems;                 // 32768 elements = 64 KiB
 
+// Retained-tail policies (retain_tail_policy): which later rows see an earlier block's last T content rows.
+constexpr int kTailStatic = 0;   // every later row
+constexpr int kTailRolling = 1;  // the next block's i-th content row sees the tail's rows i .. T-1
+constexpr int kTailSticky = 2;   // every content row of the next block
+
+// Whether content row kw (in-block offset) of block kb is a retained-tail row visible to row qw of block qb under the
+// policy (abridgekv/compress_forward.py:99-124; the caller adds causality, the raw prompt and the codes' exclusion of
+// their own block's tail).
+__device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb, int qw, int kb, int kw) {
+  if (kw >= C || kw < C - tail) return false;
+  if (policy == kTailStatic) return kb < qb;
+  return qw < C && kb + 1 == qb && (policy == kTailSticky || kw - (C - tail) >= qw);
+}
+
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8 a, const bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

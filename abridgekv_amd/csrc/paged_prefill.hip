@@ -71,6 +71,7 @@ struct PackedRows {
 struct RangeWalk {
   static constexpr bool kHole = true;
   static constexpr bool kElem = false;
+  static constexpr bool kBand = false;
   int kt_begin, kt_end, k_full, ex_lo, ex_hi;
   __device__ __forceinline__ bool next(int& kt, TileMask& tm, bool first) {
     kt = first ? kt_begin : kt + 1;

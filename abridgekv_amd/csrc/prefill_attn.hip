@@ -1,13 +1,16 @@
 // Block-masked teacher-forced attention (the compression mask) for gfx950.
 //
 // Replaces the FlexAttention call of CompressLM.forward (abridgekv/compress_forward.py:1134-1230) for the production
-// configuration (L=1, full code<->code attention, no replay / raw tail, an optional static retained tail), whose
-// mask is the closed form _arith_mask_mod (abridgekv/compress_forward.py:695-727) plus the per-query-head code quota
-// (:725-726, _quota_key_allowed :230-236). Sequence layout: N blocks of [C content | K codes], S0 = N * (C + K):
+// configuration (L=1, full code<->code attention, no replay / raw tail, an optional retained tail), whose mask is the
+// closed form _arith_mask_mod (abridgekv/compress_forward.py:695-727) plus the per-query-head code quota (:725-726,
+// _quota_key_allowed :230-236), and for the window tail policies the retained-tail term of _mask_mod (:566-649,
+// _retained_tail_visible :99-124). Sequence layout: N blocks of [C content | K codes], S0 = N * (C + K):
 //   visible(q, kv) = (kv <= q) & (own-block content | earlier blocks' codes | raw-prompt content
-//                                 | earlier blocks' last T content rows)
+//                                 | retained-tail rows of earlier blocks)
 //                  | (code query & code key & same block),     and a code key needs slot < quota[head];
-//   a code query never sees its own block's last T content rows (static retained tail T, :714-715, :721-722).
+//   a code query never sees its own block's last T content rows (retained tail T, :714-715, :721-722). The tail
+//   rows (the last T content rows of a block) are visible to every later row (static), to every content row of the
+//   next block (sticky), or to content row i of the next block from tail row i on (rolling).
 //
 // Work decomposition: one workgroup of 8 waves per (sequence, KV head, 64-row query tile). A wave owns 16 query rows
 // for 2 of the 4 query heads of the KV head: 32 MFMA columns (column = head u x row), so one K operand feeds 2 heads
@@ -18,14 +21,15 @@
 //   it by > 8)
 //   O^T[128 dims x 32 cols] += V^T . P^T          2 key halves x 8 dim tiles x 2 heads; V^T by LDS transpose reads
 // Aligned layouts (C and K multiples of 64) walk only the visible tiles, jumping over hidden segments, and tag each
-// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit); with a static retained tail the walk
-// also visits each earlier block's tail tiles, and the tile that mixes hidden and visible rows takes the per-element
-// mask. Unaligned shapes run every tile of the visible prefix with the mask evaluated per element (correct, slower).
+// tile full (unmasked), diagonal (key <= row) or bounded (key < per-head limit); with a retained tail the walk also
+// visits the tail tiles the policy shows the query tile, the tile that mixes hidden and tail rows takes an excluded
+// range and the rolling policy's band a per-lane bound. Unaligned shapes run every tile of the visible prefix with the
+// mask evaluated per element (correct, slower).
 #include "prefill_common.h"
 
 namespace abkv {
 
-template <int H, bool kAligned, bool kTail>
+template <int H, bool kAligned, bool kTail, bool kWindow>
 __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(PrefillArgs a) {
   constexpr int kWaves = 4 * (4 / H);                       // 16 query rows x H heads per wave
   __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], K2[kTileElems];
@@ -86,10 +90,10 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
                        a.k_ss, a.v_ss};
   // this wave's heads hbase, hbase + 1 (hbase is 0 or 2): quotas by selection, not by a computed index
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
-  const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}, a.tail};
+  const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}, a.tail, a.policy};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
-  TileWalk<kAligned, kTail> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1, a.tail);
+  TileWalk<kAligned, kTail, kWindow> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1, a.tail, a.policy);
   attend_tiles<H, kAligned, kWaves>(rows, walk, a.S0, Kbuf, Vbuf, qop, o, m_run, l_run, qrow + 1, a.scale_log2, geo, w,
                                     lane);
 
@@ -118,12 +122,13 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             float scale, void* out, long out_stride_b, long out_stride_s, long out_stride_h,
-                             float* lse, hipStream_t stream) {
+                             int tail_policy, float scale, void* out, long out_stride_b, long out_stride_s,
+                             long out_stride_h, float* lse, hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
-      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c)
+      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
+      tail_policy < kTailStatic || tail_policy > kTailSticky)
     return (int)hipErrorInvalidValue;
   PrefillArgs a;
   a.q = static_cast<const __bf16*>(q);
@@ -140,6 +145,7 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;
   a.lse = lse;
   a.tail = retain_tail;
+  a.policy = tail_policy;
   a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
@@ -147,9 +153,11 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   const unsigned grid = prefill_grid(a.num_q_tiles, batch, 512);
   if (grid == 0) return (int)hipErrorInvalidValue;
   if (a.aligned && retain_tail == 0)
-    hipLaunchKernelGGL((prefill_masked_kernel<2, true, false>), grid, dim3(512), 0, stream, a);
-  else if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true, true>), grid, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_masked_kernel<2, false, false>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((prefill_masked_kernel<2, true, false, false>), grid, dim3(512), 0, stream, a);
+  else if (a.aligned && tail_policy == kTailStatic)
+    hipLaunchKernelGGL((prefill_masked_kernel<2, true, true, false>), grid, dim3(512), 0, stream, a);
+  else if (a.aligned) hipLaunchKernelGGL((prefill_masked_kernel<2, true, true, true>), grid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_masked_kernel<2, false, false, false>), grid, dim3(512), 0, stream, a);
   return (int)hipGetLastError();
 }
 

@@ -85,14 +85,16 @@ __device__ __forceinline__ void pack_tile_op(const floatx4 (&x)[2][2][H], bf16x8
 }
 
 // Visibility of key kv to query row q under the compression mask (the per-element predicate of MaskGeom::visible
-// with the query as an argument), for unaligned layouts and layouts with a static retained tail.
-__device__ __forceinline__ bool elem_visible(int q, int kv, int S0, int C, int per, int plen, int quota, int tail) {
+// with the query as an argument), for unaligned layouts and the partial tiles of layouts with a retained tail.
+__device__ __forceinline__ bool elem_visible(int q, int kv, int S0, int C, int per, int plen, int quota, int tail,
+                                             int policy) {
   if (kv >= S0 || q >= S0) return false;
   const int qb = q / per, kb = kv / per;
   const int qw = q - qb * per, kw = kv - kb * per;
   const bool kc = kw < C;
   const bool in_tail = kc && kw >= C - tail;
-  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) || (in_tail && kb < qb);
+  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) ||
+           tail_visible(policy, tail, C, qb, qw, kb, kw);
   v = v && kv <= q;
   v = v || (qw >= C && !kc && kb == qb);
   v = v && !(qw >= C && kb == qb && in_tail);
@@ -104,7 +106,7 @@ struct Buf {
   static constexpr int value = N;
 };
 
-template <bool kAligned, bool kTail>
+template <bool kAligned, bool kTail, bool kWindow>
 __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a) {
   constexpr int H = 2, kWaves = 8;
   __shared__ __attribute__((aligned(16))) __bf16 K0[kTileElems], K1[kTileElems], V0[kTileElems], V1[kTileElems];
@@ -162,9 +164,9 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const DenseRows<kAligned> rows{f.k + (long)b * f.k_sb + (long)kvh * f.k_sh, f.v + (long)b * f.v_sb + (long)kvh * f.v_sh,
                                  f.k_ss, f.v_ss};
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
-  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail};
+  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail, f.policy};
   const int q_last = min(q0 + kBM, f.S0) - 1;
-  TileWalk<kAligned, kTail> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1, f.tail);
+  TileWalk<kAligned, kTail, kWindow> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1, f.tail, f.policy);
 
   int tc = 0;
   TileMask mc;
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
       floatx4 s[2][2][H], dp[2][2][H];
       tile_scores<H>(Kb[sl], qop, s, m16, j);
       tile_scores<H>(Vb[sl], gop, dp, m16, j);
-      tile_mask<H, kAligned, kTail>(s, tc * kBN, mc, qrow + 1, geo, j);
+      tile_mask<H, kAligned, kTail, false, kWindow>(s, tc * kBN, mc, qrow + 1, geo, j);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -228,9 +230,11 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
 // multiples of 64; the classification of the forward's TileWalk::seek / mask for one key tile): -1 hidden, 0 every
 // pair visible, 1 key <= query, 2 key < lim0 (without a tail the per-element predicate decides these tiles),
 // kTail: 4 key outside [lim0, lim1) (the tile of an earlier block where hidden rows give way to its retained tail).
-template <bool kTail>
+// kWindow (rolling / sticky tails: only the next block's content tiles see a block's tail): rolling, 5 key < lim0 or
+// key - query >= lim1 (query row i of the block sees tail rows i..).
+template <bool kTail, bool kWindow>
 __device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, int per, int plen, int tail,
-                                         int& lim0, int& lim1) {
+                                         bool rolling, int& lim0, int& lim1) {
   const int q0 = qt * kBN, k0 = kt * kBN;
   const int qb = q0 / per, kb = k0 / per;
   if (kb > qb) return -1;
@@ -254,6 +258,22 @@ __device__ __forceinline__ int pair_mode(int qt, int kt, int qh, int S0, int C, 
     if constexpr (kTail) {
       const int pl = min(max(plen - kb * C, 0), C);         // raw-prompt rows of this block's content
       const int lo = kBN * tw, hi = lo + kBN;
+      if constexpr (kWindow) {
+        if (hi <= pl) return 0;                             // all prompt
+        const int first = C - tail + (rolling ? q0 - qb * per : 0);   // first tail row the query tile sees
+        if (q_code || kb + 1 != qb || first >= C || hi <= C - tail) {  // no tail rows seen: a prompt prefix or nothing
+          if (lo >= pl) return -1;
+          lim0 = kb * per + pl;
+          return 2;
+        }
+        if (rolling) {
+          if (lo >= pl && hi <= first) return -1;           // no prompt row, no row of any query row's band
+          if (lo >= first + kBN - 1) return 0;              // past every query row's band start
+          lim0 = kb * per + pl;
+          lim1 = C - tail - per;
+          return 5;
+        }
+      }
       if (hi <= pl || lo >= C - tail) return 0;             // all prompt, or all tail
       if (hi <= C - tail) {                                 // no tail rows: a prompt prefix or nothing
         if (lo >= pl) return -1;
@@ -334,7 +354,7 @@ __device__ __forceinline__ void dkv_acc(const __bf16* Qbuf, const __bf16* Gbuf, 
   __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
 }
 
-template <bool kAligned, bool kTail>
+template <bool kAligned, bool kTail, bool kWindow>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs a) {
   constexpr int kWaves = 4;
   __shared__ __attribute__((aligned(16))) __bf16 Q0[kTileElems], Q1[kTileElems], G0[kTileElems], G1[kTileElems];
@@ -385,6 +405,14 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   int qt_end = f.num_q_tiles;
   if (kAligned && k0 - (k0 / per) * per + kBN <= f.C - tail && (k0 / per) * f.C + (k0 - (k0 / per) * per) >= plen)
     qt_end = min(qt_end, (k0 / per + 1) * per / kBN);
+  if constexpr (kWindow) {                                  // a window tail: the next block's rows at most
+    if (k0 - (k0 / per) * per < f.C && (k0 / per) * f.C + (k0 - (k0 / per) * per) >= plen)
+      qt_end = min(qt_end, (k0 / per + 2) * per / kBN);
+  }
+  const bool rolling = kWindow && f.policy == kTailRolling;
+  // the per-element predicate's tail: none in the aligned no-tail instance, static in the aligned static one
+  const int etail = kAligned && !kTail ? 0 : f.tail;
+  const int epolicy = kAligned && !kWindow ? kTailStatic : f.policy;
   int qt = qt_lo, h = -1, mode = 0, lim0 = 0, lim1 = 0;
   auto next_pair = [&]() -> bool {
     for (;;) {
@@ -395,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
       if (qt >= qt_end) return false;
       if constexpr (kAligned) {
         const int qh = h == 0 ? quota_all[0] : h == 1 ? quota_all[1] : h == 2 ? quota_all[2] : quota_all[3];
-        mode = pair_mode<kTail>(qt, kt, qh, f.S0, f.C, per, plen, tail, lim0, lim1);
+        mode = pair_mode<kTail, kWindow>(qt, kt, qh, f.S0, f.C, per, plen, tail, rolling, lim0, lim1);
         if (mode >= 0) return true;
       } else {
         mode = 3;
@@ -471,8 +499,12 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int qrow = cq * kBN + r0 + r;
-              // diagonal tiles: key <= row; bounded (mode 2, no tail) and unaligned tiles: the per-element predicate
-              const bool vis = cmode == 1 ? key <= qrow : elem_visible(qrow, key, f.S0, f.C, per, plen, qh, f.tail);
+              // diagonal tiles: key <= row; a rolling tail's band (mode 5); bounded (mode 2, no tail) and unaligned
+              // tiles: the per-element predicate
+              const bool vis = cmode == 1                   ? key <= qrow
+                               : (kWindow && cmode == 5) ? (key < clim0 || key - qrow >= clim1)
+                                                         : elem_visible(qrow, key, f.S0, f.C, per, plen, qh, etail,
+                                                                        epolicy);
               const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
               s[kk][t][0][r] = pr;
               dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
@@ -518,15 +550,16 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long out_stride_s, long out_stride_h, const void* dout, long dout_stride_b,
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, float scale, void* dq, long dq_stride_b,
-                                 long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b, long dk_stride_s,
-                                 long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s, long dv_stride_h,
-                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale, void* dq,
+                                 long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
+                                 long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
+                                 long dv_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || dout == nullptr || lse == nullptr ||
       dq == nullptr || dk == nullptr || dv == nullptr || block_c <= 0 || codes_k <= 0 || num_blocks <= 0 ||
-      seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c)
+      seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
+      tail_policy < kTailStatic || tail_policy > kTailSticky)
     return (int)hipErrorInvalidValue;
   if (workspace == nullptr || workspace_bytes < abkv_prefill_masked_bwd_workspace_size(batch, seq_len))
     return (int)hipErrorInvalidValue;
@@ -545,6 +578,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.out = nullptr; f.o_sb = f.o_ss = f.o_sh = 0;
   f.lse = nullptr;
   f.tail = retain_tail;
+  f.policy = tail_policy;
   f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0);
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
@@ -569,16 +603,22 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned gq = prefill_grid(f.num_q_tiles, batch, 512);
-  if (f.aligned && retain_tail == 0) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, false>), gq, dim3(512), 0, stream, a);
-  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, true>), gq, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_bwd_dq_kernel<false, false>), gq, dim3(512), 0, stream, a);
+  const bool window = retain_tail > 0 && tail_policy != kTailStatic;
+  if (f.aligned && retain_tail == 0)
+    hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, false, false>), gq, dim3(512), 0, stream, a);
+  else if (f.aligned && !window)
+    hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, true, false>), gq, dim3(512), 0, stream, a);
+  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dq_kernel<true, true, true>), gq, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_bwd_dq_kernel<false, false, false>), gq, dim3(512), 0, stream, a);
   err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned gk = prefill_grid(f.num_q_tiles, batch, 256);
   if (f.aligned && retain_tail == 0)
-    hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, false>), gk, dim3(256), 0, stream, a);
-  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, true>), gk, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_bwd_dkv_kernel<false, false>), gk, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, false, false>), gk, dim3(256), 0, stream, a);
+  else if (f.aligned && !window)
+    hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, true, false>), gk, dim3(256), 0, stream, a);
+  else if (f.aligned) hipLaunchKernelGGL((prefill_bwd_dkv_kernel<true, true, true>), gk, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_bwd_dkv_kernel<false, false, false>), gk, dim3(256), 0, stream, a);
   return (int)hipGetLastError();
 }
 

@@ -18,7 +18,8 @@ struct PrefillArgs {
   float* lse;                                // [B, 32, S0] natural log, or nullptr
   int aligned;                               // C % 64 == 0 && K % 64 == 0 (the walk over visible tiles)
   int num_q_tiles;
-  int tail;                                  // static retained tail T (0: none)
+  int tail;                                  // retained tail T (0: none)
+  int policy;                                // its policy: kTailStatic, kTailRolling or kTailSticky
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,
@@ -37,22 +38,30 @@ __device__ __forceinline__ GridPos grid_pos(int batch) {
 // Aligned layouts (C and K multiples of 64): a key tile is named by (block kb, tile tw of the block's C + K rows).
 // Within a segment (one block's content, one block's codes) visibility is monotone in tw, so the first invisible tile
 // ends the segment and the walk jumps to the next one: no per-tile test of skipped tiles and no integer division.
-// kTail (aligned layouts with a static retained tail of T rows): an earlier block's content is visible where it is
-// raw prompt (a prefix) or tail (the last T rows), so after the prompt prefix the walk jumps to the tail's first tile;
-// a code query tile sees its own block's content below C - T only. The tile where hidden rows give way to the tail
-// (at most one per earlier block) hides the key range between the prompt's end and the tail (mode 4).
+// kTail (aligned layouts with a retained tail of T rows): an earlier block's content is visible where it is raw
+// prompt (a prefix) or tail (the last T rows, to the rows the policy names), so after the prompt prefix the walk jumps
+// to the first tile holding visible tail rows; a code query tile sees its own block's content below C - T only. The
+// tile where hidden rows give way to the tail (at most one per earlier block) hides the key range between the prompt's
+// end and the tail (mode 4). kWindow (the rolling and sticky policies): only content query tiles of the next block see
+// a block's tail; under "rolling" query row i of the block sees tail rows i.. (content rows >= C - T + i), so the tile
+// where the band starts, and those it crosses, take the band mask (mode 5).
 // Unaligned layouts: every tile up to the last visible block, mask evaluated per element (mode 3).
-template <bool kAligned, bool kTail = false>
+template <bool kAligned, bool kTail = false, bool kWindow = false>
 struct TileWalk {
+  static_assert(kTail || !kWindow, "a window tail is a retained tail");
   static constexpr bool kHole = kTail;                      // yields excluded key ranges (mode 4) with a tail
   static constexpr bool kElem = false;                      // aligned walks never yield per-element tiles
+  static constexpr bool kBand = kWindow;                    // yields band tiles (mode 5) under the rolling policy
   int q0, q_last, qb, C, per, tpb, ct, plen, qmin, qmax, n_tiles, tail;
   bool q_code;
   int kb, tw;
   int wq0, wq1;                                             // code quotas of this wave's two heads
+  int first_tail;                                           // first content row of the previous block's tail that
+                                                            // this query tile sees (kWindow)
+  bool rolling;
 
   __device__ __forceinline__ TileWalk(int q0_, int q_last_, int C_, int per_, int S0, int plen_, int qmin_, int qmax_,
-                                      int wq0_, int wq1_, int tail_ = 0)
+                                      int wq0_, int wq1_, int tail_ = 0, int policy_ = kTailStatic)
       : q0(q0_), q_last(q_last_), C(C_), per(per_), plen(plen_), qmin(qmin_), qmax(qmax_), tail(kTail ? tail_ : 0),
         kb(0), tw(0), wq0(wq0_), wq1(wq1_) {
     qb = q0 / per;
@@ -60,6 +69,15 @@ struct TileWalk {
     tpb = per / kBN;
     ct = C / kBN;
     n_tiles = (S0 + kBN - 1) / kBN;
+    rolling = kWindow && policy_ == kTailRolling;
+    first_tail = C - tail + (rolling ? q0 - qb * per : 0);
+  }
+
+  // whether an earlier block kb's tail rows are visible to this query tile at all
+  __device__ __forceinline__ bool sees_tail() const {
+    if (!kTail || tail <= 0) return false;
+    if constexpr (kWindow) return !q_code && kb + 1 == qb && first_tail < C;
+    return true;
   }
 
   // aligned: move (kb, tw) to the first visible tile at or after it; false when none is left
@@ -74,12 +92,14 @@ struct TileWalk {
         } else {
           if (kb * C + kBN * tw < plen) return true;        // raw-prompt prefix
           if constexpr (kTail) {
-            const int tail_tile = (C - tail) / kBN;         // first tile holding tail rows
-            if (tail > 0 && tw <= tail_tile) {
-              tw = tail_tile;
-              return true;
+            if (sees_tail()) {
+              const int tail_tile = (kWindow ? first_tail : C - tail) / kBN;   // first tile holding visible tail rows
+              if (tw <= tail_tile) {
+                tw = tail_tile;
+                return true;
+              }
+              if (tw < ct) return true;                     // later tiles of the tail
             }
-            if (tail > 0 && tw < ct) return true;           // later tiles of the tail
           }
           tw = ct;
         }
@@ -106,11 +126,16 @@ struct TileWalk {
         const int pl = min(max(plen - kb * C, 0), C);       // raw-prompt rows of this block's content
         const int lo = kBN * tw, hi = lo + kBN;
         const bool in_prompt = hi <= pl;
-        const bool in_tail = kTail && lo >= C - tail;
+        const bool tail_seen = kTail && sees_tail();
+        const bool in_tail = tail_seen && lo >= first_tail + (rolling ? kBN - 1 : 0);
         if (!in_prompt && !in_tail) {
-          if (!kTail || hi <= C - tail) {                   // raw-prompt boundary inside the tile
+          if (!tail_seen || hi <= C - tail) {               // raw-prompt boundary inside the tile
             tm.mode = 2;
             tm.limit[0] = tm.limit[1] = kb * per + pl;
+          } else if (rolling) {                             // [prompt rows,] rows >= C - T + (query row's offset)
+            tm.mode = 5;
+            tm.limit[0] = kb * per + pl;
+            tm.limit[1] = C - tail - per - 1;               // key >= row + 1 + limit[1] <=> kw >= C - T + qw
           } else if (pl < C - tail) {                       // [prompt rows,] hidden rows, tail rows
             tm.mode = 4;
             tm.limit[0] = kb * per + pl;

@@ -2,7 +2,7 @@
 
 Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``: ``feed_content``, ``compress``,
 ``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, bidirectional codes,
-raw prompt, per-layer code quotas, no replay / raw tail, an optional static retained tail). The reference keeps a
+raw prompt, per-layer code quotas, no replay / raw tail, an optional retained tail). The reference keeps a
 dense per-layer store and masks it; here every layer's rows live in paged caches, quotas are physical, and the block
 boundary is a compaction:
 
@@ -19,9 +19,13 @@ boundary is a compaction:
   moves the surviving rows with the HIP mover. The generator's API hands over the next token only after
   ``compress()``, so it runs the processor's block compaction directly rather than through ``update_after_step``
   (which needs that token to open the next block).
-* a static retained tail of T rows (``retain_tail_kv`` with ``retain_tail_policy="static"``): the block's last T
-  content rows are never removed, so every later row sees them as resident rows; the code step hides them from the
-  block's own codes (an excluded key range) and the bitrev code positions spread over the first C - T offsets.
+* a retained tail of T rows (``retain_tail_kv``): the block's last T content rows survive its compaction; the code
+  step hides them from the block's own codes (an excluded key range) and the bitrev code positions spread over the
+  first C - T offsets. ``retain_tail_policy="static"`` keeps them for every later row. The window policies keep a
+  block's response tail rows for the next block's content only, as the serving state machine does
+  (compresslm/processor.py:318-353, 559-646): "sticky" removes them all before that block's code step; "rolling"
+  removes tail row i once content token i of the next block has run, and a content chunk ends at every such token
+  so that each removal follows that token's query (processor.py:123-151). Raw-prompt rows never leave.
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
@@ -91,8 +95,7 @@ class CompressGen:
         if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail")):
             raise NotImplementedError("the paged path serves no replay / raw tails")
         self.T = int(getattr(clm, "retain_tail_kv", 0) or 0)
-        if self.T and getattr(clm, "retain_tail_policy", "rolling") != "static":
-            raise NotImplementedError("the paged path serves the static retained tail only")
+        self.policy = getattr(clm, "retain_tail_policy", "rolling") if self.T else "static"
         self.clm = clm
         self.inner = clm.model.model
         self.layers = self.inner.layers
@@ -115,6 +118,9 @@ class CompressGen:
         self.packed = _per_head(head_code_quotas)
         if self.packed:
             self.quotas = [self.K] * self.num_layers
+        if self.packed and self.policy != "static":
+            raise NotImplementedError("per-head packed pages take the static retained tail only "
+                                      "(config/compresslm.py:160-167)")
 
         # KV-cache groups: layers of equal quota, in order of first appearance; tensor i = i-th layer of each group
         distinct = list(dict.fromkeys(self.quotas))
@@ -136,7 +142,7 @@ class CompressGen:
         # bitrev positions, power-of-two sizes -- is the vLLM path's; the generator also runs appended positions)
         pcfg = CompressLMConfig(block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
                                 packed_kv_k_max=self.K, retain_tail_kv=self.T,
-                                retain_tail_policy="static" if self.T else "rolling")
+                                retain_tail_policy=self.policy if self.T else "rolling")
         pcfg.set_code_token_ids(range(1 << 20, (1 << 20) + self.K))
         self.proc = CompressLMProcessor(pcfg)
         if not self.packed:
@@ -152,6 +158,8 @@ class CompressGen:
                                            max_pages_per_request=min(blocks, 2048), device=self.device)
         self.b = 0                      # current block index
         self.f = 0                      # content tokens committed in the current block
+        # window tails: the previous block's tail rows still resident, by tail index (None: raw prompt or gone)
+        self._window: list[int | None] = []
         self.logical_len = 0            # tokens in the planner's logical sequence (content + code rows)
         self._cur_ids: list[int] = []
         self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C - self.T)).to(self.device)
@@ -237,22 +245,51 @@ class CompressGen:
         return hidden
 
     # -- reference surface ----------------------------------------------------------------------------------------
+    def _remove(self, spans):
+        """Run span removals (logical [start, end), every group) through the planner and move the rows."""
+        for start, end in spans:
+            CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end)
+        _, _, fused = self.planner.take_step_outputs(as_arrays=True)
+        execute_fused_moves(fused.copy(), self.caches_by_group)
+
     def feed_content(self, ids):
-        """Feed <= C - f content tokens as one chunk; returns the final-normed hidden states (n, d)."""
+        """Feed <= C - f content tokens as one chunk (split where a rolling tail row expires); returns the final-normed
+        hidden states (n, d)."""
         n = len(ids)
         if n == 0 or self.f + n > self.C:
             raise ValueError(f"chunk of {n} tokens does not fit the block ({self.f}/{self.C} used)")
-        hidden = self.inner.embed_tokens(torch.tensor([list(ids)], device=self.device))
-        hidden = self._forward_rows(hidden, code_step=False)
-        self.f += n
-        self._cur_ids += [int(t) for t in ids]
-        return self.inner.norm(hidden)[0]
+        outs, i = [], 0
+        while i < n:
+            take = n - i
+            if self.policy == "rolling":
+                # the chunk ends at the first content token whose tail row of the previous block expires
+                for j in range(self.f, min(self.f + take, len(self._window))):
+                    if self._window[j] is not None:
+                        take = j - self.f + 1
+                        break
+            part = ids[i:i + take]
+            hidden = self.inner.embed_tokens(torch.tensor([list(part)], device=self.device))
+            outs.append(self._forward_rows(hidden, code_step=False))
+            if self.policy == "rolling" and self.f + take - 1 < len(self._window) and \
+                    self._window[self.f + take - 1] is not None:
+                row, self._window[self.f + take - 1] = self._window[self.f + take - 1], None
+                self._remove([(row, row + 1)])
+            self.f += take
+            self._cur_ids += [int(t) for t in part]
+            i += take
+        return self.inner.norm(torch.cat(outs, dim=1))[0]
 
     def compress(self):
         """Code step of the full block, then compaction of its response content and of code rows >= quota."""
         if self.f != self.C:
             raise RuntimeError("compress() needs a full block")
         K, C = self.K, self.C
+        if self.policy == "sticky":
+            # the previous block's response tail leaves after this block's last content row, before its codes
+            rows = [r for r in self._window if r is not None]
+            self._window = []
+            if rows:
+                self._remove([(rows[0], rows[-1] + 1)])
         hidden = self.clm.pause[:K].to(self.dtype).view(1, K, self.d)
         code_start = self.logical_len
         self._forward_rows(hidden, code_step=True)
@@ -275,6 +312,9 @@ class CompressGen:
             CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end, groups)
         _, _, fused = self.planner.take_step_outputs(as_arrays=True)
         execute_fused_moves(fused.copy(), self.caches_by_group)
+        if self.policy != "static":
+            # this block's tail rows, by tail index, that the next block's content may still expire (response rows)
+            self._window = [p if p >= resp_from else None for p in range(code_start - self.T, code_start)]
         self.b += 1
         self.f = 0
         self._cur_ids = []

@@ -275,17 +275,25 @@ def full_model_decode_lengths(B=64, seed=0, prompt=512, closed_generated=32):
     return T, np.full(B, prompt)
 
 
-def visible_pairs_prompt_block(C, K, N, T=0):
+def visible_pairs_prompt_block(C, K, N, T=0, policy="static"):
     """Visible (query, key) pairs per head of the teacher-forced mask when block 0 is the raw prompt: block-b content
     queries see their block's content causally, b*K earlier codes and (b > 0) the C prompt rows; block-b code queries
-    see their block's C content and K codes, b*K earlier codes and (b > 0) the prompt rows. A static retained tail of
-    T rows adds the last T content rows of the earlier non-prompt blocks (blocks 1 .. b-1) to both, and hides a block's
-    own last T content rows from its codes."""
+    see their block's C content and K codes, b*K earlier codes and (b > 0) the prompt rows. A retained tail of T rows
+    hides a block's own last T content rows from its codes, and adds the last T content rows of earlier non-prompt
+    blocks (blocks 1 ..): static, those of blocks 1 .. b-1 for every query of block b; sticky, those of block b-1 for
+    its content queries; rolling, T - i of them for its i-th content query (i < T)."""
     n = 0
     for b in range(N):
-        tails = max(0, b - 1) * T
-        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0) + C * tails
-        n += K * (C - T) + K * K + K * b * K + (K * C if b else 0) + K * tails
+        if policy == "static":
+            tail_c, tail_k = C * max(0, b - 1) * T, K * max(0, b - 1) * T
+        elif policy == "sticky":
+            tail_c, tail_k = (C * T if b >= 2 else 0), 0
+        elif policy == "rolling":
+            tail_c, tail_k = (T * (T + 1) // 2 if b >= 2 else 0), 0
+        else:
+            raise ValueError(f"unknown tail policy {policy!r}")
+        n += C * (C + 1) // 2 + C * b * K + (C * C if b else 0) + tail_c
+        n += K * (C - T) + K * K + K * b * K + (K * C if b else 0) + tail_k
     return n
 
 

@@ -76,7 +76,9 @@ def parse():
     ap.add_argument("--code-target-blocks", type=int, default=None,
                     help="serving: workgroups a code step's key splits aim at (default: one per compute unit)")
     ap.add_argument("--retain-tail", type=int, default=0,
-                    help="prefill / prefill_bwd: static retained tail of T content rows per block (default 0)")
+                    help="prefill / prefill_bwd: retained tail of T content rows per block (default 0)")
+    ap.add_argument("--tail-policy", default="static", choices=("static", "rolling", "sticky"),
+                    help="prefill / prefill_bwd: the retained tail's policy (default static)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     args = ap.parse_args()
@@ -180,6 +182,7 @@ def bench_prefill(args, torch):
     from abridgekv_amd.workloads import visible_pairs_prompt_block
 
     B, C, K, N, plen, T = 4, 512, 128, 16, 512, args.retain_tail
+    P = args.tail_policy if T else "static"
     S0 = N * (C + K)
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(args.seed)
@@ -191,16 +194,18 @@ def bench_prefill(args, torch):
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     warmup = max(args.warmup, MIN_PREFILL_WARMUP)
     for _ in range(warmup):
-        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T)
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T,
+                                     tail_policy=P)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):
-        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T)
+        ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, out=out, lse=lse, retain_tail=T,
+                                     tail_policy=P)
     e.record()
     torch.cuda.synchronize()
     t = s.elapsed_time(e) / 1e3 / args.steps
-    flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N, T) * 32 * B
+    flops = 4.0 * 128 * visible_pairs_prompt_block(C, K, N, T, P) * 32 * B
     tflops = flops / t / 1e12
     cpu = None if args.no_cpu_baseline or T else prefill_cpu_baseline(torch, C, K, plen, flops, B, S0)
     return {
@@ -211,7 +216,7 @@ def bench_prefill(args, torch):
         "data": "synthetic N(0,1) q/k/v from the seed",
         "config": {"workload": f"masked prefill B={B}, N={N} blocks of [{C} content | {K} codes], S0={S0}, "
                                f"raw prompt {plen}, 32q/8kv heads, d128"
-                               + (f", static retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
+                               + (f", {P} retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": tflops / 2500.0,
                      "traffic": profiled_traffic("prefill_masked_b4_s10240_pmc_traffic.md"),
@@ -260,6 +265,7 @@ def bench_prefill_bwd(args, torch):
     from abridgekv_amd.workloads import visible_pairs_prompt_block
 
     B, C, K, N, plen, T = 4, 512, 128, 16, 512, args.retain_tail
+    P = args.tail_policy if T else "static"
     S0 = N * (C + K)
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(args.seed)
@@ -269,19 +275,21 @@ def bench_prefill_bwd(args, torch):
     dout = torch.randn((B, S0, 32, 128), generator=g, device=dev).to(torch.bfloat16)
     pl = torch.full((B,), plen, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
-    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse, retain_tail=T)
+    out, _ = ops.prefill_masked_attention(q, k, v, C, K, N, prompt_len=pl, lse=lse, retain_tail=T, tail_policy=P)
     warmup = max(args.warmup, MIN_PREFILL_WARMUP)
     for _ in range(warmup):
-        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T)
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T,
+                                              tail_policy=P)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):
-        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T)
+        ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, C, K, N, prompt_len=pl, retain_tail=T,
+                                              tail_policy=P)
     e.record()
     torch.cuda.synchronize()
     t = s.elapsed_time(e) / 1e3 / args.steps
-    flops = 10.0 * 128 * visible_pairs_prompt_block(C, K, N, T) * 32 * B
+    flops = 10.0 * 128 * visible_pairs_prompt_block(C, K, N, T, P) * 32 * B
     tflops = flops / t / 1e12
     return {
         "metric": "masked teacher-forced attention backward TFLOP/s (visible-pair flops, 2.5x forward); % of bf16 "
@@ -291,7 +299,7 @@ def bench_prefill_bwd(args, torch):
         "data": "synthetic N(0,1) q/k/v/dout from the seed",
         "config": {"workload": f"masked prefill backward B={B}, N={N} blocks of [{C} content | {K} codes], "
                                f"S0={S0}, raw prompt {plen}, 32q/8kv heads, d128"
-                               + (f", static retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
+                               + (f", {P} retained tail {T}" if T else ""), "global_batch": B, "seq_len": S0},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
                      "traffic": profiled_traffic("prefill_masked_bwd_b4_s10240_pmc_traffic.md"),
                      "traffic_source": "profiles/prefill_masked_bwd_b4_s10240_pmc_traffic.md (the three kernels)",

@@ -131,17 +131,22 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
  * layout N blocks of [block_c content | codes_k codes], seq_len = N * (block_c + codes_k).
  * q [batch, seq_len, 32, 128], k/v [batch, seq_len, 8, 128], out [batch, seq_len, 32, 128] bf16 with element strides
  * (dims contiguous); prompt_len [batch] int32 raw-prompt content tokens (NULL: none); head_quota [32] int32 code slots
- * visible per query head (NULL: all); retain_tail = T of a static retained tail (retain_tail_kv with
- * retain_tail_policy="static", :714-715, :721-722: the last T content rows of every earlier block are visible to every
- * later row, a block's codes never see its own last T content rows; 0: none; 0 <= T < block_c); lse [batch, 32,
- * seq_len] fp32 natural log (NULL: not written).
+ * visible per query head (NULL: all); retain_tail = T of a retained tail (retain_tail_kv; 0: none; 0 <= T <
+ * block_c): a block's codes never see its own last T content rows (:714-715, :721-722), and tail_policy
+ * (retain_tail_policy, _retained_tail_visible :99-124) names the later rows that see them: ABKV_TAIL_STATIC every
+ * later row, ABKV_TAIL_STICKY every content row of the next block, ABKV_TAIL_ROLLING content row i of the next block
+ * from tail row i on (key in-block offset >= block_c - T + i); lse [batch, 32, seq_len] fp32 natural log (NULL: not
+ * written).
  * ------------------------------------------------------------------------------------------------------------- */
+#define ABKV_TAIL_STATIC 0
+#define ABKV_TAIL_ROLLING 1
+#define ABKV_TAIL_STICKY 2
 int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             float scale, void* out, long out_stride_b, long out_stride_s, long out_stride_h,
-                             float* lse, abkv_stream_t stream);
+                             int tail_policy, float scale, void* out, long out_stride_b, long out_stride_s,
+                             long out_stride_h, float* lse, abkv_stream_t stream);
 
 /* Backward of abkv_prefill_masked_attn: the gradients dq [batch, seq_len, 32, 128] and dk, dv [batch, seq_len, 8,
  * 128] (bf16, element strides, dims contiguous; written, not accumulated) of sum(dout * out) under the same mask,
@@ -155,10 +160,10 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long out_stride_s, long out_stride_h, const void* dout, long dout_stride_b,
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, float scale, void* dq, long dq_stride_b,
-                                 long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b, long dk_stride_s,
-                                 long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s, long dv_stride_h,
-                                 void* workspace, size_t workspace_bytes, abkv_stream_t stream);
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale, void* dq,
+                                 long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
+                                 long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
+                                 long dv_stride_h, void* workspace, size_t workspace_bytes, abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Multi-query attention over the paged cache: prompt-chunk prefill (causal) and the CompressLM code step.
@@ -267,8 +272,8 @@ int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h
 int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh, const float* k, long k_sb,
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, float scale, float* out, long o_sb,
-                                 long o_ss, long o_sh, float* lse, abkv_stream_t stream);
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale,
+                                 float* out, long o_sb, long o_ss, long o_sh, float* lse, abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager

@@ -6,8 +6,8 @@ decoder layer manual attention under the dense boolean mask of ``oracle.prefill.
 ``_dense_mask`` / ``_arith_mask_mod``), with the per-layer query-head quota of compress_forward.py:230-236. Runs the
 HuggingFace layer modules of ``model`` in whatever dtype the model is in (float64 on the CPU for a tight bound).
 
-With a static retained tail of T rows the mask is ``arith_mask(..., retain_tail=T)`` and the bitrev code rows spread
-over the first C - T in-block offsets (compress_forward.py:1059).
+With a retained tail of T rows the mask is ``arith_mask(..., retain_tail=T, tail_policy=...)`` and the bitrev code
+rows spread over the first C - T in-block offsets (compress_forward.py:1059).
 
 Pinning: tests/test_oracle_model.py checks that with one block the content logits equal the model's own causal
 forward (code rows come after the content and are invisible to it), that all-K quotas equal no quotas, and that
@@ -48,10 +48,10 @@ def _rotate_half(x):
 
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                 layer_head_quota=None, retain_tail=0):
+                 layer_head_quota=None, retain_tail=0, tail_policy="static"):
     """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
-    static retained tail."""
+    retained tail under ``tail_policy``."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
@@ -67,7 +67,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq, retain_tail)     # [B?, H?, S0, S0]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy)     # [B?, H?, S0, S0]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -98,8 +98,9 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                      layer_head_quota=None, retain_tail=0):
+                      layer_head_quota=None, retain_tail=0, tail_policy="static"):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
-    h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail)
+    h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail,
+                     tail_policy)
     rows = torch.from_numpy(loss_rows(C, N, K))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

@@ -28,6 +28,11 @@ CASES = [
     # block's last 12 content rows stay resident; the codes neither see nor span them
     (64, 4, 16, "bitrev", [40, 100], [16, 4], [1], 12),
     (64, 3, 16, "bitrev", [70, 0], [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], [0], 12),
+    # window tails (per-layer quotas): the previous block's last 12 content rows for the block's content only --
+    # rolling (content token i sees tail rows i..; fed token by token and as whole blocks split at each expiry) and
+    # sticky (all 12 until the block's codes)
+    (64, 4, 16, "bitrev", [40, 100], [16, 4], [1], 12, "rolling"),
+    (64, 4, 16, "bitrev", [40, 100], [16, 4], [0], 12, "sticky"),
 ]
 
 
@@ -48,11 +53,12 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
 
     C, N, K, code_positions, prompt, quota, stepwise = CASES[case][:7]
     T = CASES[case][7] if len(CASES[case]) > 7 else 0
+    policy = CASES[case][8] if len(CASES[case]) > 8 else "static"
     hcq = None if quota is None else [list(q) if isinstance(q, list) else [q] * 8 for q in quota]
     per_head = hcq is not None and any(len(set(row)) > 1 for row in hcq)
     base = _model(case)
     dev = torch.device("cuda")
-    tail = dict(retain_tail_kv=T, retain_tail_policy="static") if T else {}
+    tail = dict(retain_tail_kv=T, retain_tail_policy=policy) if T else {}
     clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=code_positions,
                      head_code_quotas=hcq, **tail).eval()
     torch.manual_seed(100 + case)
@@ -63,9 +69,9 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
     pause = clm.pause.detach().cpu()
 
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
-                               lhq, retain_tail=T)
+                               lhq, retain_tail=T, tail_policy=policy)
     eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq,
-                                 retain_tail=T)
+                                 retain_tail=T, tail_policy=policy)
     tol = 2 * (eager - ref).abs().max().item() + 2e-3
 
     pl = None if prompt is None else torch.tensor(prompt, dtype=torch.int32, device=dev)
@@ -88,8 +94,11 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
             got.append(clm.model.lm_head(hs).float()[: C - 1].double().cpu())
             g.compress()
             kept_prompt = min(p, (blk + 1) * C)
-            # each closed block also keeps the part of its last T content rows that lies past the raw prompt
-            tails = sum(min(T, (b + 1) * C - max(p, b * C)) for b in range(blk + 1) if (b + 1) * C > p) if T else 0
+            # each closed block also keeps the part of its last T content rows that lies past the raw prompt (a
+            # window tail: the last closed block only)
+            first = 0 if policy == "static" else blk
+            tails = sum(min(T, (b + 1) * C - max(p, b * C)) for b in range(first, blk + 1) if (b + 1) * C > p) \
+                if T else 0
             if per_head:
                 assert g.resident_rows() == [kept_prompt + tails] * 2
                 assert g.packed_rows() == [(blk + 1) * sum(row) for row in hcq]
@@ -126,19 +135,19 @@ def test_forward_losses_match_dense_cross_entropy():
     assert blk["block_ce"].shape == (N,)
 
 
-@pytest.mark.parametrize("tail", [0, 12])
-def test_training_gradients_match_dense_float64(tail):
+@pytest.mark.parametrize("tail,policy", [(0, "static"), (12, "static"), (12, "rolling"), (12, "sticky")])
+def test_training_gradients_match_dense_float64(tail, policy):
     """CompressLM trains through the kernels: the CE loss's gradients (attention and MLP weights, the pause rows)
     through the masked-prefill forward + backward kernels match the dense float64 model's autograd, within 2x the
-    error of the same dense model run in bf16 autograd (plus 1e-3 of the gradient's scale); also with a static
-    retained tail."""
+    error of the same dense model run in bf16 autograd (plus 1e-3 of the gradient's scale); also with a retained
+    tail under each policy."""
     from abridgekv_amd.compress_forward import CompressLM
 
     C, N, K = 64, 3, 32 if tail else 64
     quota = [[32] * 8, [32, 16, 24, 32, 8, 32, 32, 24]] if tail else [[32] * 8, [64, 16, 48, 64, 8, 32, 64, 24]]
     base = _model(11)
     dev = torch.device("cuda")
-    extra = dict(retain_tail_kv=tail, retain_tail_policy="static") if tail else {}
+    extra = dict(retain_tail_kv=tail, retain_tail_policy=policy) if tail else {}
     clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions="bitrev", head_code_quotas=quota,
                      **extra).eval()
     torch.manual_seed(12)
@@ -165,7 +174,8 @@ def test_training_gradients_match_dense_float64(tail):
     def dense_grads(dtype):
         m = copy.deepcopy(base).to(dtype)
         pause = clm.pause.detach().cpu().to(dtype).requires_grad_()
-        logits = om.dense_loss_logits(m, pause, ids, C, N, K, "bitrev", [70, 5], lhq, retain_tail=tail)
+        logits = om.dense_loss_logits(m, pause, ids, C, N, K, "bitrev", [70, 5], lhq, retain_tail=tail,
+                                      tail_policy=policy)
         ce = torch.nn.functional.cross_entropy(logits.double(), tgt, reduction="none")
         ((ce * tm).sum() / tm.sum()).backward()
         params = dict(m.named_parameters())

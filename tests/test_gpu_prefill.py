@@ -14,7 +14,7 @@ def _bf16(x):
     return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static"):
     from abridgekv_amd import ops
     S0 = N * (C + K)
     g = torch.Generator().manual_seed(seed)
@@ -26,13 +26,14 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
-                                          lse=lse, retain_tail=tail)
+                                          lse=lse, retain_tail=tail, tail_policy=policy)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail)
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
+                             tail_policy=policy)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -85,6 +86,31 @@ def test_static_tail_served_block_geometry():
     """C=512, K=128, T=64 (span 448 for the codes) with 4 blocks; rows sampled across blocks and regions."""
     rows = np.r_[0:70, 440:520, 600:700, 1250:1300, 2400:2560]
     _check(C=512, K=128, N=4, B=1, prompt_len=[512], rows=rows, seed=8, tail=64)
+
+
+@pytest.mark.parametrize("policy", ["rolling", "sticky"])
+@pytest.mark.parametrize("tail", [32, 100])
+def test_window_tail_aligned_blocks(policy, tail):
+    """Window tails on 64-aligned blocks: the previous block's last T content rows for the block's content rows only
+    (rolling: content row i from tail row i on, a band across one or two key tiles); a raw prompt that covers part of
+    block 0's tail; per-head quotas."""
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    print(f"case: {policy} T={tail}", flush=True)
+    _check(C=128, K=64, N=4, B=2, prompt_len=[100, 0], head_quota=quota, seed=16, tail=tail, policy=policy)
+
+
+@pytest.mark.parametrize("policy", ["rolling", "sticky"])
+def test_window_tail_unaligned_blocks(policy):
+    """C=8, K=4, T=3 (the per-element predicate) with a partial last tile."""
+    quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+    _check(C=8, K=4, N=5, B=2, prompt_len=[8, 13], head_quota=quota, seed=17, tail=3, policy=policy)
+
+
+@pytest.mark.parametrize("policy", ["rolling", "sticky"])
+def test_window_tail_served_block_geometry(policy):
+    """C=512, K=128, T=200 (a rolling band over four key tiles) with 4 blocks; rows sampled where the window acts."""
+    rows = np.r_[0:70, 600:780, 1200:1300, 1900:1990, 2400:2560]
+    _check(C=512, K=128, N=4, B=1, prompt_len=[300], rows=rows, seed=18, tail=200, policy=policy)
 
 
 def test_strided_hf_layout():
@@ -157,10 +183,11 @@ def test_config4_full_size_sampled_rows(prompts, quota):
     assert worst <= TOL, worst
 
 
-@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("seed", range(6))
 def test_seeded_random_layouts(seed):
     """Seeded random layouts: block sizes aligned to the 64-row tiles or not, raw prompts anywhere in the first blocks,
-    per-KV-head code quotas in [1, K], and (for odd seeds) a static retained tail; against the fp64 oracle."""
+    per-KV-head code quotas in [1, K], and (for odd seeds) a retained tail under one of the three policies; against
+    the fp64 oracle."""
     rng = np.random.default_rng(2000 + seed)
     C = int(rng.choice([64, 128, 40, 24]))
     K = int(rng.choice([64, 16, 8]))
@@ -169,5 +196,6 @@ def test_seeded_random_layouts(seed):
     prompt = [int(x) for x in rng.integers(0, N * C // 2 + 1, B)]
     quota = np.repeat(rng.integers(1, K + 1, 8), 4).tolist()
     tail = int(rng.integers(1, max(2, C - K))) if seed % 2 and C > K else 0
-    print(f"case: seed {seed} C={C} K={K} N={N} B={B} prompt={prompt} tail={tail}", flush=True)
-    _check(C=C, K=K, N=N, B=B, prompt_len=prompt, head_quota=quota, seed=10 + seed, tail=tail)
+    policy = ("static", "rolling", "sticky")[seed % 3] if tail else "static"
+    print(f"case: seed {seed} C={C} K={K} N={N} B={B} prompt={prompt} tail={tail} {policy}", flush=True)
+    _check(C=C, K=K, N=N, B=B, prompt_len=prompt, head_quota=quota, seed=10 + seed, tail=tail, policy=policy)

@@ -204,10 +204,12 @@ def test_visible_pair_count(C, K, N):
 
 @pytest.mark.parametrize("C,K,N,T", [(8, 4, 3, 0), (8, 4, 4, 3), (16, 8, 5, 5), (64, 16, 6, 16), (512, 128, 16, 32)])
 def test_benchmark_pair_count_matches_the_mask(C, K, N, T):
-    """The masked-prefill bench's FLOP accounting (workloads.visible_pairs_prompt_block, with a static retained tail
-    of T rows) counts exactly the pairs the oracle mask shows, raw prompt = block 0."""
+    """The masked-prefill bench's FLOP accounting (workloads.visible_pairs_prompt_block, with a retained tail of T
+    rows under each policy) counts exactly the pairs the oracle mask shows, raw prompt = block 0."""
     from abridgekv_amd.workloads import visible_pairs_prompt_block
-    assert visible_pairs_prompt_block(C, K, N, T) == op.visible_pairs(C, K, N, prompt_len=C, retain_tail=T)
+    for policy in ("static", "rolling", "sticky"):
+        assert visible_pairs_prompt_block(C, K, N, T, policy) == op.visible_pairs(C, K, N, prompt_len=C,
+                                                                                  retain_tail=T, tail_policy=policy)
 
 
 def test_masked_attention_grads_match_autograd_and_finite_differences():
