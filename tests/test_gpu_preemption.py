@@ -6,7 +6,10 @@ are not restaged), each closed block compacted again by the planner and its rows
 later tokens exist (processor.py:276-316, 419-465; gpu_model_runner.py:888-930). K/V rows are a fixed function of
 (request, logical position), so once the replay has caught up every kept row must sit where it sat before the
 preemption and hold that token's bytes exactly; every replayed chunk and code step, and the first decode after the
-catch-up, must match fp64 attention under the reference's masks (2e-2, bf16)."""
+catch-up, must match fp64 attention under the reference's masks (2e-2, bf16). With a retained tail (rolling or sticky
+window, T=12) the code steps hide their block's tail (an excluded physical range, sched/scheduler.py:979-991) and the
+previous block's tail leaves through one-row (rolling) or one-span (sticky) removals, replayed after the preemption;
+the kept rows must then be the oracle trace's (oracle.trace.RequestTrace, stepped in lockstep)."""
 import numpy as np
 import pytest
 import torch
@@ -17,6 +20,7 @@ from abridgekv_amd.config import CompressLMConfig
 from abridgekv_amd.planner import KVPlanner
 from abridgekv_amd.processor import CompressLMProcessor, SamplingSpec, ServingRequest
 from oracle import masks as om
+from oracle import trace as ot
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -32,10 +36,12 @@ class Engine:
     """Scheduler + worker loop over the real state machine, native planner, attention backend and mover, one
     layer per KV-cache group."""
 
-    def __init__(self, num_pages=600, seed=0):
+    def __init__(self, num_pages=600, seed=0, tail=0, policy="static"):
         self.dev = torch.device("cuda")
+        self.T, self.policy = tail, policy
         cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev",
-                               layer_code_quotas=QUOTAS, physical_layer_quotas=True)
+                               layer_code_quotas=QUOTAS, physical_layer_quotas=True, retain_tail_kv=tail,
+                               retain_tail_policy=policy)
         cfg.set_code_token_ids(CODES)
         self.proc = CompressLMProcessor(cfg)
         self.proc.set_group_quotas(QUOTAS)
@@ -53,6 +59,7 @@ class Engine:
         self.builder = bk.AbridgeMetadataBuilder(max_num_seqs=4, max_pages=MAX_LEN // PAGE, device=self.dev)
         self.impl = bk.AbridgeAttentionImpl()
         self.reqs = []
+        self.traces = {}
         self.checks = 0
 
     def add(self, rid, prompt_len):
@@ -61,6 +68,8 @@ class Engine:
         req.compresslm_state = self.proc.prepare_request(req)
         self.planner.add_request(rid)
         self.reqs.append(req)
+        self.traces[rid] = ot.RequestTrace(prompt_len, 1 << 30, C, K, QUOTAS, retain_tail=self.T,
+                                           tail_policy=self.policy)
         return req
 
     def preempt(self, req):
@@ -70,13 +79,14 @@ class Engine:
         req.num_computed_tokens = 0
         self.proc.reset_for_preemption(req.compresslm_state)
         self.planner.add_request(req.request_id)
+        self.traces[req.request_id].preempt()
 
     def step(self, check_rids=(), preempt_after=None):
         """One scheduler step over every request (each runs its whole next role run), the worker's appends and
         attention per group, the state machine's update (compaction through the planner); ``preempt_after`` is
         preempted before the step's outputs are taken, so its moves of this step are dropped as the worker drops
         those of preempted requests. Launches of requests in ``check_rids`` are checked against fp64."""
-        sched = []
+        sched, excluded = [], {}
         for req in self.reqs:
             start = req.num_computed_tokens
             n = self.proc.limit_num_new_tokens(req, req.num_tokens - start)
@@ -84,6 +94,11 @@ class Engine:
                 continue
             code = self.proc.is_code_ready(req)
             skip = self.proc.should_skip_sampling(req, n)
+            assert n == self.traces[req.request_id].next_chunk()
+            # a code step hides its block's retained tail: the physical range in each group's layout, taken at
+            # scheduling time (sched/scheduler.py:979-991)
+            excluded[req.request_id] = self.proc.code_excluded_physical_ranges(req, self.G) if code and self.T \
+                else [(0, 0)] * self.G
             assert self.planner.allocate_slots(req.request_id, n) is not None, "pool exhausted"
             self.planner.set_num_computed_tokens(req.request_id, start + n)
             req.num_computed_tokens = start + n
@@ -98,10 +113,11 @@ class Engine:
             seq_lens = np.array([s + n for _, s, n, _, _ in sched]) - comp
             spans = [self.proc.code_physical_spans(req, g, s + n) if code else [] for req, s, n, code, _ in sched]
             limits = bk.code_step_key_limits(qsl, seq_lens, [sp[-1] if sp else None for sp in spans], QUOTAS[g], K)
+            excl = np.array([excluded[req.request_id][g] for req, _, _, _, _ in sched], dtype=np.int64)
             table = self.planner.fill_block_table(rids, g, width)
             md = self.builder.build(qsl, seq_lens, torch.from_numpy(table).to(self.dev), positions=positions,
                                     compacted=torch.from_numpy(comp.astype(np.int32)).to(self.dev),
-                                    code_key_limit=limits)
+                                    code_key_limit=limits, code_excluded=excl if self.T else None)
             idx = [(int(req.request_id), s, n) for req, s, n, _, _ in sched]
             q = torch.cat([self.qtab[r, s: s + n, g] for r, s, n in idx]).to(self.dev)
             k = torch.cat([self.ktab[r, s: s + n, g] for r, s, n in idx]).to(self.dev)
@@ -114,7 +130,8 @@ class Engine:
                 if req.request_id not in check_rids:
                     continue
                 sl = int(seq_lens[i])
-                mask = om.request_mask(n, sl, spans[i], None, QUOTAS[g], K, causal=not code)
+                ex = tuple(excl[i]) if excl[i, 1] > excl[i, 0] else None
+                mask = om.request_mask(n, sl, spans[i], ex, QUOTAS[g], K, causal=not code)
                 ref, _ = om.masked_paged_attention_fp64(q[qsl[i]: qsl[i + 1]].float().cpu().numpy(),
                                                         self.caches[g].float().cpu().numpy(), table[i], sl, mask,
                                                         128 ** -0.5)
@@ -125,6 +142,9 @@ class Engine:
             _, stopped = self.proc.update_after_step(req, n, [] if skip else [TOKEN], self.planner.mask_token_span,
                                                      MAX_LEN)
             assert not stopped
+            tr = self.traces[req.request_id]
+            tr.num_computed_tokens += n
+            tr.after_step(n)
         if preempt_after is not None:
             self.preempt(preempt_after)
         out = self.planner.take_step_outputs()
@@ -149,9 +169,14 @@ def _closed_blocks(req):
     return len(req.compresslm_state.compacted_block_ids)
 
 
-@pytest.mark.parametrize("where", ["mid_block", "at_block_close"])
-def test_preempted_request_replays_to_the_same_layout(where):
-    eng = Engine(seed=3 if where == "mid_block" else 4)
+CASES = [("mid_block", 0, "static"), ("at_block_close", 0, "static"), ("mid_block", 12, "rolling"),
+         ("at_block_close", 12, "rolling"), ("mid_block", 12, "sticky"), ("at_block_close", 12, "sticky")]
+
+
+@pytest.mark.parametrize("where,tail,policy", CASES, ids=[f"{w}-{p if t else 'no_tail'}" for w, t, p in CASES])
+def test_preempted_request_replays_to_the_same_layout(where, tail, policy):
+    print(f"case: {where} tail={tail} {policy}", flush=True)
+    eng = Engine(seed=3 if where == "mid_block" else 4, tail=tail, policy=policy)
     r0 = eng.add(0, 100)                       # prompt spans block 0 and part of block 1
     r1 = eng.add(1, 30)
     # run until r0 has closed two blocks (then, mid-block: 20 more decode steps)
@@ -189,6 +214,7 @@ def test_preempted_request_replays_to_the_same_layout(where):
     # every kept row sits at the logical position the planner maps it to and holds that token's bytes
     for g, (logical, rows) in enumerate(eng.layout(r0)):
         assert np.all(np.diff(logical) > 0)
+        assert logical.tolist() == eng.traces[0].kept_positions(g)
         want_k = eng.ktab[0, torch.from_numpy(logical), g]
         want_v = eng.vtab[0, torch.from_numpy(logical), g]
         assert torch.equal(rows[:, 0], want_k) and torch.equal(rows[:, 1], want_v), g
