@@ -16,7 +16,7 @@ reorder FlashInfer applies with decode threshold 1) and then multi-token request
 * CompressLM code-step requests -> ``abkv_paged_prefill_attn`` non-causal with the key limit
   ``code_start + quota``: the physical-quota code mask of gpu_model_runner.py:2042-2107 (all resident rows, the
   block's own code slots ``>= quota`` hidden; compresslm_masks.py:165-239) expressed as a per-request limit, and with
-  a static retained tail the block's own tail rows hidden as a per-request excluded range (:2086-2094).
+  a retained tail the block's own tail rows hidden as a per-request excluded range (:2086-2094).
 
 New K/V rows are written by ``abkv_kv_append`` (``torch.ops.abridgekv.kv_append``) before attention
 (``reshape_and_cache`` semantics: slot < 0 skips).
@@ -42,7 +42,7 @@ class AbridgeAttentionMetadata:
     int arrays; ``block_table`` [B, W] int32, ``slot_mapping`` [T] int64 and ``seq_lens_dev`` [B] int32 live on the
     GPU. ``code_key_limit`` [B] holds, for a code-step request, the physical key limit (code start + the group's
     quota) and ``NOT_CODE`` for every other request; ``code_excluded`` [B, 2] the physical rows a code-step request
-    must not see (its block's static tail; an empty range otherwise), or None. ``num_decodes`` leading requests have
+    must not see (its block's retained tail; an empty range otherwise), or None. ``num_decodes`` leading requests have
     one query token.
     """
     query_start_loc: np.ndarray
@@ -97,7 +97,7 @@ def code_step_key_limits(query_start_loc, seq_lens, code_spans, group_quota: int
 
 
 def code_step_excluded_ranges(code_spans, excluded_ranges, query_start_loc, seq_lens) -> np.ndarray | None:
-    """Per-request excluded key ranges [B, 2] of a code step in one group (the block's own static retained tail,
+    """Per-request excluded key ranges [B, 2] of a code step in one group (the block's own retained tail,
     ``CompressLMProcessor.code_excluded_physical_ranges`` of the group), checked as the worker checks them
     (gpu_model_runner.py:2086-2091: ``0 <= start < end <= seq_len - query_len``); None when no request has one."""
     qsl = np.asarray(query_start_loc, dtype=np.int64)

@@ -194,7 +194,7 @@ class CompressGen:
             seq_len = start + n
             table = torch.from_numpy(np.asarray(blocks[g], dtype=np.int32)).view(1, -1).to(self.device)
             limit = [start + min(q, self.K)] if code_step else None
-            # the block's own static tail: its last T content rows, just before the code rows in every group
+            # the block's own retained tail: its last T content rows, just before the code rows in every group
             excluded = [[start - self.T, start]] if code_step and self.T else None
             out.append(self.builder.build([0, n], [seq_len], table, code_key_limit=limit, positions=logical,
                                           compacted=comp_dev[g:g + 1], code_excluded=excluded))

@@ -331,7 +331,7 @@ def rope_kv_append(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, posi
     slot_mapping (int64, < 0 = skip; None = rotate only). positions [T] int64: RoPE positions, or logical positions
     of the abridged layout when block_c > 0 (mapped to bitrev RoPE positions on the device; codes_k a power of two
     <= block_c; the code rows spread over in-block offsets [0, code_span), 0 meaning block_c, block_c - T with a
-    static retained tail). ``max_position``: a host bound on ``positions`` (None: read back from the device, which
+    retained tail). ``max_position``: a host bound on ``positions`` (None: read back from the device, which
     synchronises); the RoPE positions it implies must lie inside ``cos_sin`` (ValueError otherwise)."""
     T = positions.numel()
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (HEADS_Q, HEAD_DIM)
@@ -562,7 +562,7 @@ def paged_prefill_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table
     physical positions kv_start[r] + i, seeing keys < kv_limit[r] (and <= their own position when causal).
     ``causal``: a bool for the whole batch or one flag per request (code steps and prompt chunks may share a batch).
     ``excluded``: None, or per request a physical (start, end) its queries must not see (None: nothing), e.g. the
-    code step's own-block static tail. ``split``: key splits (None: chosen by :func:`paged_split_plan`; 1: no split).
+    code step's own-block retained tail. ``split``: key splits (None: chosen by :func:`paged_split_plan`; 1: no split).
     Returns (out [T, 32, 128] bf16, lse [T, 32] fp32 or None). fp32 q and cache select the fp32 mode (out fp32).
     """
     import numpy as np

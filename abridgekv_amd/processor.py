@@ -483,8 +483,9 @@ class CompressLMProcessor:
         ``groups`` None for every KV-cache group (compresslm/processor.py:467-557). Response content goes from every
         group, then (physical quotas) code slots [q, K) from the groups of each quota q < K, ascending q, each on the
         layout the previous removal left. Packed KV: the response content and the codes as one span (the codes are
-        archived into packed pages before it runs). A static retained tail (the block's last T content rows) is never
-        removed: the response content before it goes, and with packed KV the codes go as a span of their own."""
+        archived into packed pages before it runs). A retained tail (the block's last T content rows) is not removed
+        with the block: the response content before it goes, and with packed KV (static tail only) the codes go as a
+        span of their own; the window policies remove the tail later (``_expire_*``)."""
         pos = block.response_content_positions
         if self.config.retain_tail_kv:
             kept = set(block.retained_tail_positions)

@@ -106,7 +106,7 @@ int abkv_kv_append(const void* key, long key_stride, const void* value, long val
  * positions [T] int64: RoPE positions when block_c == 0; otherwise logical positions of the abridged layout (period
  * block_c + codes_k, codes_k a power of two <= block_c) mapped on the device to block * block_c + (offset < block_c ?
  * offset : floor(bitrev(offset - block_c) * span / codes_k)) with span = code_span, the in-block range the codes
- * summarize (0: block_c; block_c - T with a static retained tail of T rows, config/compresslm.py:192-206; codes_k <=
+ * summarize (0: block_c; block_c - T with a retained tail of T rows, config/compresslm.py:192-206; codes_k <=
  * span <= block_c). cos_sin [max_pos, 128] fp32: cos of the 64 rotary
  * frequencies then their sin. The caller guarantees every RoPE position is < max_pos (the Python wrapper checks it);
  * the kernel clamps positions into [0, max_pos) only so that no read leaves the table. */
@@ -174,7 +174,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
  * q [T, 32, 128] (token stride, head stride), request r's queries are tokens [q_start[r], q_start[r+1]) at physical
  * positions kv_start[r] + i and see keys < kv_limit[r] (and <= their position when request r is causal: causal[r] != 0,
  * or causal_default when causal is NULL), except the keys of kv_excluded[r] = [start, end) (NULL: none; the code
- * step's own-block static retained tail, gpu_model_runner.py:2086-2094 "excluded" ranges, compresslm_masks.py:206-213;
+ * step's own-block retained tail, gpu_model_runner.py:2086-2094 "excluded" ranges, compresslm_masks.py:206-213;
  * start >= end: none). tile_req / tile_q0 [num_tiles] list the 64-row query tiles (request, first
  * row). All index arrays are device int32. lse [T, 32] or NULL. num_splits > 1 splits every tile's keys into
  * num_splits ranges of split_tiles 64-key tiles (split z covers tiles [z * split_tiles, (z + 1) * split_tiles); the
