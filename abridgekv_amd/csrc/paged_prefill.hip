@@ -31,8 +31,8 @@ struct PagedPrefillArgs {
   int num_tiles;                               // query tiles; the grid is 8 x num_tiles x splits (linear_block)
   int split_tiles;                             // > 0: key tiles per split, partials to part_*
   int num_tokens;
-  float* part_o;                               // [splits, T, 32, 128] un-normalised
-  float* part_ml;                              // [splits, T, 32, 2] (running max in log2 units, sum)
+  _Float16* part_o;                            // [splits, T, 32, 128] split output / (l * scale), fp16
+  float* part_ml;                              // [splits, T, 32, 4] (max in log2 units, weight sum l, scale, unused)
   int split_base;                              // first partial slot of this launch's splits
   const int32_t* head_quota;                   // [8] or nullptr: a non-causal request sees keys < kv_start + q_h
   // side rows (per-head packed code pages, attended by every query of the request); see PackedRows
@@ -40,6 +40,20 @@ struct PagedPrefillArgs {
   const int32_t* side_table; long side_stride; const int32_t* side_count; int side_max_pages;
   int side_q[kHeadsKV], side_o[kHeadsKV];
 };
+
+// Dims 8p .. 8p + 7 of an accumulator column (lane group j) times f, as one 16-byte fp16 store (the column layout of
+// store_acc_bf16x8).
+__device__ __forceinline__ void store_acc_f16x8(_Float16* dst, const floatx4& a, const floatx4& b, int j, float f) {
+  const bool odd = j & 1;
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  f16x8 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    h[r] = (_Float16)((odd ? b[r] : a[r]) * f);
+    h[4 + r] = (_Float16)((odd ? a[r] : b[r]) * f);
+  }
+  *reinterpret_cast<f16x8*>(dst) = h;
+}
 
 constexpr int kMaxSideTable = 2048;             // packed pages per request the side launch stages in LDS
 
@@ -180,20 +194,36 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
                                   w, lane);
   }
 
+  // Split partials: the split's output normalised by its weight sum l, in fp16 (half the bytes the epilogue writes
+  // and the merge reads), divided by a scale that keeps every value within +-32768 (1 unless the split's V rows
+  // exceed that), and the record (m, l, scale). The scale needs the row's largest |o| over its 128 dims, which lie in
+  // the row's four lane groups (lanes m16 + 16j): reduced before any lane leaves.
+  float amax[H];
+  if (a.split_tiles > 0) {
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      float x = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x = fmaxf(x, fabsf(o[t][u][r]));
+      amax[u] = max_xor32(max_xor16(x));
+    }
+  }
   if (!qvalid) return;
   if (a.split_tiles > 0) {                                   // partials of this key split
 #pragma unroll
     for (int u = 0; u < H; ++u) {
       const float l = l_run[u];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float an = amax[u] * inv;
+      const float scale = an > 32768.f ? an * (1.f / 32768.f) : 1.f;
       const int head = kvh * kGroup + hbase + u;
       const long row = ((long)(a.split_base + split) * a.num_tokens + (t0 + qi)) * kHeadsQ + head;
-      float* po = a.part_o + row * kHeadDim + 32 * j;
+      _Float16* po = a.part_o + row * kHeadDim + 32 * j;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(po + 4 * acc_tile(t, j)) = o[t][u];
-      if (j == 0) {
-        a.part_ml[row * 2] = m_run[u];
-        a.part_ml[row * 2 + 1] = l;
-      }
+      for (int p = 0; p < 4; ++p) store_acc_f16x8(po + 8 * p, o[2 * p][u], o[2 * p + 1][u], j, inv / scale);
+      if (j == 0) *reinterpret_cast<floatx4*>(a.part_ml + row * 4) = floatx4{m_run[u], l, scale, 0.f};
     }
     return;
   }
@@ -213,22 +243,27 @@ __global__ __launch_bounds__(512, 1) void paged_prefill_kernel(PagedPrefillArgs 
 // Combine the key-split partials of every query token: workgroup (token, group of 8 heads); thread t handles head
 // 8 * blockIdx.y + t / 32 and dims 4 * (t % 32) .. +4.
 __global__ __launch_bounds__(256) void paged_merge_kernel(PagedPrefillArgs a, int n_splits) {
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   const long tok = blockIdx.x;
   const int head = 8 * blockIdx.y + (threadIdx.x >> 5);
   const int d0 = (threadIdx.x & 31) * 4;
   const long stride = (long)a.num_tokens * kHeadsQ;          // rows per split
-  const float* pml = a.part_ml + (tok * kHeadsQ + head) * 2;
+  const float* pml = a.part_ml + (tok * kHeadsQ + head) * 4;
   float M = -INFINITY;
 #pragma unroll 8
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[s * stride * 2]);
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pml[s * stride * 4]);
   float L = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   if (M != -INFINITY) {
 #pragma unroll 8
     for (int s = 0; s < n_splits; ++s) {
-      const float w = fast_exp2(pml[s * stride * 2] - M);
-      L += w * pml[s * stride * 2 + 1];
-      acc += w * *reinterpret_cast<const floatx4*>(a.part_o + ((s * stride) + tok * kHeadsQ + head) * kHeadDim + d0);
+      const floatx4 rec = *reinterpret_cast<const floatx4*>(pml + s * stride * 4);     // m, l, scale
+      const float w = fast_exp2(rec[0] - M) * rec[1];      // the split's weight (0 for a split that saw no key)
+      const float ws = w * rec[2];
+      L += w;
+      const f16x4 h = *reinterpret_cast<const f16x4*>(a.part_o + ((s * stride) + tok * kHeadsQ + head) * kHeadDim + d0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += ws * (float)h[r];
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -255,7 +290,8 @@ unsigned paged_grid(int num_tiles, int splits) {
 extern "C" {
 
 size_t abkv_paged_prefill_workspace_size(int num_tokens, int num_splits) {
-  return (size_t)num_tokens * (size_t)num_splits * abkv::kHeadsQ * (abkv::kHeadDim + 2) * sizeof(float);
+  return (size_t)num_tokens * (size_t)num_splits * abkv::kHeadsQ *
+         (abkv::kHeadDim * sizeof(_Float16) + 4 * sizeof(float));
 }
 
 
@@ -298,7 +334,8 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
   a.lse = lse;
   a.num_tokens = num_tokens;
   a.split_tiles = 0;
-  a.part_o = a.part_ml = nullptr;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
   a.split_base = 0;
   a.head_quota = nullptr;
   a.side_count = nullptr;
@@ -307,8 +344,8 @@ int abkv_paged_prefill_attn(const void* q, long q_stride_t, long q_stride_h, con
         workspace_bytes < abkv_paged_prefill_workspace_size(num_tokens, num_splits))
       return (int)hipErrorInvalidValue;
     a.split_tiles = split_tiles;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = a.part_o + (size_t)num_splits * num_tokens * kHeadsQ * kHeadDim;
+    a.part_o = static_cast<_Float16*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(a.part_o + (size_t)num_splits * num_tokens * kHeadsQ * kHeadDim);
   }
   const unsigned grid = paged_grid(num_tiles, num_splits > 1 ? num_splits : 1);
   if (grid == 0) return (int)hipErrorInvalidValue;
@@ -379,8 +416,8 @@ int abkv_paged_prefill_attn_packed(const void* q, long q_stride_t, long q_stride
   a.o_sh = out_stride_h;
   a.lse = lse;
   a.num_tokens = num_tokens;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + (size_t)total * num_tokens * kHeadsQ * kHeadDim;
+  a.part_o = static_cast<_Float16*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(a.part_o + (size_t)total * num_tokens * kHeadsQ * kHeadDim);
   a.head_quota = head_quota_dev;
   a.side_kv = static_cast<const __bf16*>(packed_kv);
   a.side_rows = packed_rows;
