@@ -42,8 +42,10 @@ class AbridgeAttentionMetadata:
     int arrays; ``block_table`` [B, W] int32, ``slot_mapping`` [T] int64 and ``seq_lens_dev`` [B] int32 live on the
     GPU. ``code_key_limit`` [B] holds, for a code-step request, the physical key limit (code start + the group's
     quota) and ``NOT_CODE`` for every other request; ``code_excluded`` [B, 2] the physical rows a code-step request
-    must not see (its block's retained tail; an empty range otherwise), or None. ``num_decodes`` leading requests have
-    one query token.
+    must not see (its block's retained tail; an empty range otherwise), or None; ``code_causal`` [B] bool, for a
+    code-step request whose code rows see their own block's codes causally (``pause_xattn="causal"`` of the
+    generator; the serving path's code steps are bidirectional), or None. ``num_decodes`` leading requests have one
+    query token.
     """
     query_start_loc: np.ndarray
     seq_lens: np.ndarray
@@ -57,6 +59,7 @@ class AbridgeAttentionMetadata:
     causal: bool = True
     split_pages: int = ops.DEFAULT_SPLIT_PAGES
     code_excluded: np.ndarray | None = None
+    code_causal: np.ndarray | None = None
 
     @property
     def num_reqs(self) -> int:
@@ -197,12 +200,14 @@ class AbridgeMetadataBuilder:
 
     def build(self, query_start_loc, seq_lens, block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
               code_key_limit=None, seq_lens_dev: torch.Tensor | None = None, positions: torch.Tensor | None = None,
-              compacted: torch.Tensor | None = None, code_excluded=None) -> AbridgeAttentionMetadata:
+              compacted: torch.Tensor | None = None, code_excluded=None, code_causal=None) -> AbridgeAttentionMetadata:
         """One group's metadata of a step. ``slot_mapping`` [T] int64 (device), or None to compute it on the device
         from ``positions`` [T] int64 (the tokens' logical positions) and ``compacted`` [B] int32 (tokens the group
         removed per request): slot = table[r][p // 16] * 16 + p % 16 with p = position - compacted[r]
         (gpu_model_runner.py:1579-1661, block_table.py:186-197). ``code_excluded``: None, or [B, 2] physical key
-        ranges the code-step requests must not see (:func:`code_step_excluded_ranges`)."""
+        ranges the code-step requests must not see (:func:`code_step_excluded_ranges`). ``code_causal``: None, or [B]
+        flags of code-step requests whose rows see their own codes causally (up to their own row and the key
+        limit)."""
         qsl = np.asarray(query_start_loc, dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64)
         B = sl.size
@@ -234,6 +239,10 @@ class AbridgeMetadataBuilder:
                 raise RuntimeError("an excluded key range must lie before the request's own query rows")
             if not has.any():
                 code_excluded = None
+        if code_causal is not None:
+            code_causal = np.asarray(code_causal, dtype=bool).reshape(B)
+            if np.any(code_causal & ~code):
+                raise RuntimeError("only code-step requests may be causal code steps")
         max_pages = int(-(-sl[:nd].max() // ops.PAGE)) if nd else 0
         if max_pages > self.max_pages:
             raise RuntimeError(f"decode needs {max_pages} pages > max_pages={self.max_pages}")
@@ -246,7 +255,7 @@ class AbridgeMetadataBuilder:
             slot_mapping = ops.slot_mapping(req_idx, positions, block_table, compacted=compacted)
         return AbridgeAttentionMetadata(query_start_loc=qsl, seq_lens=sl, block_table=block_table,
                                         slot_mapping=slot_mapping, seq_lens_dev=seq_lens_dev, num_decodes=nd,
-                                        code_key_limit=limits, code_excluded=code_excluded,
+                                        code_key_limit=limits, code_excluded=code_excluded, code_causal=code_causal,
                                         max_decode_pages=max(max_pages, 1),
                                         workspace=self.workspace() if nd else None,
                                         split_pages=self.split_pages or (ops.auto_split_pages(sl[:nd]) if nd
@@ -302,8 +311,11 @@ class AbridgeAttentionImpl:
             code = lim != NOT_CODE
             ex = None if md.code_excluded is None else [tuple(e) if e[1] > e[0] else None
                                                          for e in md.code_excluded[nd:]]
+            causal = md.causal & ~code
+            if md.code_causal is not None:
+                causal = causal | (code & md.code_causal[nd:])
             ops.paged_prefill_attention(q[nd_tok:n_tok], kv_cache, md.block_table[nd:], qsl, sl - qlen,
-                                        np.where(code, lim, sl), md.causal & ~code, self.scale,
+                                        np.where(code, lim, sl), causal, self.scale,
                                         out=out[nd_tok:n_tok], lse=None if lse is None else lse[nd_tok:n_tok],
                                         excluded=ex)
 

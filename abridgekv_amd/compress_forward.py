@@ -1,7 +1,8 @@
 """Teacher-forced CompressLM forward over the masked-prefill kernel (the training/evaluation entry point).
 
 Mirrors the served subset of abridgekv/compress_forward.py:240-1230 (``CompressLM``): one pause pass (L=1) with
-bidirectional code<->code attention in a block (``pause_xattn="full"``), optional raw prompt, optional fixed
+code<->code attention in a block bidirectional (``pause_xattn="full"``, the served setting), causal or absent
+(``"causal"``, ``"none"``: :313-314, 622-625; the kernel evaluates those per element), optional raw prompt, optional fixed
 per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` / ``bitrev`` code positions and the retained
 tail (``retain_tail_kv`` = T: a block's codes do not see or summarize its last T content rows, bitrev codes spread
 over the first C - T; by ``retain_tail_policy`` those rows stay visible to every later row ("static"), to the next
@@ -45,6 +46,7 @@ class CompressMask:
     head_quota: torch.Tensor | None = None
     retain_tail: int = 0
     tail_policy: str = "static"
+    pause_xattn: str = "full"
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -62,7 +64,8 @@ class _MaskedPrefill(torch.autograd.Function):
             lse = torch.empty((q.shape[0], ops.HEADS_Q, q.shape[1]), dtype=torch.float32, device=q.device)
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
                                               prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
-                                              retain_tail=mask.retain_tail, tail_policy=mask.tail_policy)
+                                              retain_tail=mask.retain_tail, tail_policy=mask.tail_policy,
+                                              pause_xattn=mask.pause_xattn)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -76,7 +79,7 @@ class _MaskedPrefill(torch.autograd.Function):
         dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, g, m.block_c, m.codes_k, m.num_blocks,
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
                                                            scale=ctx.scale, retain_tail=m.retain_tail,
-                                                           tail_policy=m.tail_policy)
+                                                           tail_policy=m.tail_policy, pause_xattn=m.pause_xattn)
         return dq, dk, dv, None, None, None
 
 
@@ -157,8 +160,8 @@ class CompressLM(nn.Module):
             raise NotImplementedError(f"CompressLM options {used} are not supported by the native forward")
         if L != 1:
             raise NotImplementedError("only one pause pass (L=1) is supported")
-        if pause_xattn != "full":
-            raise NotImplementedError("only pause_xattn='full' (bidirectional codes) is supported")
+        if pause_xattn not in ("none", "causal", "full"):
+            raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {pause_xattn!r}")
         if not 0 <= retain_tail_kv < C:
             raise ValueError(f"retain_tail_kv must be in [0, C={C}), got {retain_tail_kv}")
         if retain_tail_policy not in ("rolling", "sticky", "static"):
@@ -255,7 +258,7 @@ class CompressLM(nn.Module):
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
         return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
-                            self.retain_tail_policy if self.retain_tail_kv else "static")
+                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn)
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:

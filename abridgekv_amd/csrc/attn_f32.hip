@@ -43,6 +43,7 @@ struct F32Args {
   const int32_t* head_quota;   // [32] or nullptr
   int retain_tail;             // retained tail T (0: none)
   int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky)
+  int pause_xattn;             // code <-> code attention in a block (kXattn*)
   int num_tokens;
   float scale;
   float* out;
@@ -73,7 +74,8 @@ __device__ __forceinline__ bool f32_visible(const F32Args& a, int qr, int kr, in
   bool vis = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * a.block_c + kw < plen) ||
              tail_visible(a.tail_policy, a.retain_tail, a.block_c, qb, qw, kb, kw);
   vis = (kr <= qr) && vis;
-  vis = vis || (qw >= a.block_c && !kc && kb == qb);
+  vis = vis || (qw >= a.block_c && !kc && kb == qb &&
+                (a.pause_xattn == kXattnFull || (a.pause_xattn == kXattnCausal && kr <= qr)));
   vis = vis && !(qw >= a.block_c && kb == qb && in_tail);
   return vis && (kc || kw - a.block_c < quota);
 }
@@ -306,13 +308,14 @@ int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h
 int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh, const float* k, long k_sb,
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale,
-                                 float* out, long o_sb, long o_ss, long o_sh, float* lse, hipStream_t stream) {
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
+                                 float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
+                                 hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
       num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
-      tail_policy < kTailStatic || tail_policy > kTailSticky)
+      tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull || pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   F32Args a = f32_defaults();
   a.mode = 1;
@@ -335,6 +338,7 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
   a.head_quota = head_quota;
   a.retain_tail = retain_tail;
   a.tail_policy = tail_policy;
+  a.pause_xattn = pause_xattn;
   a.num_tokens = batch * seq_len;
   a.scale = scale;
   a.out = out;

@@ -20,6 +20,7 @@ struct MaskGeom {
   int quota[2];
   int tail;
   int policy;
+  int xattn;      // code rows' attention to their own block's code rows (kXattn*)
   __device__ __forceinline__ bool visible(int kv, int u) const {
     if (kv >= S0 || qrow >= S0) return false;
     const int qb = qrow / per, kb = kv / per;
@@ -29,7 +30,7 @@ struct MaskGeom {
     bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) ||
              tail_visible(policy, tail, C, qb, qw, kb, kw);
     v = v && kv <= qrow;
-    v = v || (qw >= C && !kc && kb == qb);
+    v = v || (qw >= C && !kc && kb == qb && (xattn == kXattnFull || (xattn == kXattnCausal && kv <= qrow)));
     v = v && !(qw >= C && kb == qb && in_tail);
     return v && (kc || kw - C < quota[u]);
   }

@@ -29,6 +29,11 @@ constexpr int kTailSticky = 2;   // every content row of the next block
 // Whether content row kw (in-block offset) of block kb is a retained-tail row visible to row qw of block qb under the
 // policy (abridgekv/compress_forward.py:99-124; the caller adds causality, the raw prompt and the codes' exclusion of
 // their own block's tail).
+// pause_xattn: which code rows of its own block a code row sees (compress_forward.py:313-314, 622-625).
+constexpr int kXattnFull = 0;     // all of them (bidirectional)
+constexpr int kXattnCausal = 1;   // those at or before its own position
+constexpr int kXattnNone = 2;     // none, itself included
+
 __device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb, int qw, int kb, int kw) {
   if (kw >= C || kw < C - tail) return false;
   if (policy == kTailStatic) return kb < qb;

@@ -20,6 +20,8 @@ struct PrefillArgs {
   int num_q_tiles;
   int tail;                                  // retained tail T (0: none)
   int policy;                                // its policy: kTailStatic, kTailRolling or kTailSticky
+  int xattn;                                 // code <-> code attention in a block (kXattn*; the aligned walks
+                                             // serve kXattnFull, the others take the per-element walk)
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,

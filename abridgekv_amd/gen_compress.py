@@ -1,8 +1,9 @@
 """Incremental CompressLM generator over the paged abridged cache (the serving path for one sequence).
 
 Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``: ``feed_content``, ``compress``,
-``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, bidirectional codes,
-raw prompt, per-layer code quotas, no replay / raw tail, an optional retained tail). The reference keeps a
+``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, raw prompt, per-layer code
+quotas, no replay / raw tail, an optional retained tail) with bidirectional, causal or no code<->code attention in a
+code step (``pause_xattn``; only bidirectional with per-head packed pages). The reference keeps a
 dense per-layer store and masks it; here every layer's rows live in paged caches, quotas are physical, and the block
 boundary is a compaction:
 
@@ -90,8 +91,12 @@ class CompressGen:
             raise NotImplementedError(f"CompressGen options {used} are not supported on the paged path")
         if not code_attend_current_content:
             raise NotImplementedError("code rows always attend the current block's content on the paged path")
-        if getattr(clm, "L", 1) != 1 or getattr(clm, "pause_xattn", "full") != "full":
-            raise NotImplementedError("the paged path serves L=1 with bidirectional code attention")
+        if getattr(clm, "L", 1) != 1:
+            raise NotImplementedError("the paged path serves one pause pass (L=1)")
+        # code <-> code attention of a code step (gen_compress.py:953-959): bidirectional, causal, or none
+        self.xattn = getattr(clm, "pause_xattn", "full")
+        if self.xattn not in ("full", "causal", "none"):
+            raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {self.xattn!r}")
         if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail")):
             raise NotImplementedError("the paged path serves no replay / raw tails")
         self.T = int(getattr(clm, "retain_tail_kv", 0) or 0)
@@ -121,6 +126,8 @@ class CompressGen:
         if self.packed and self.policy != "static":
             raise NotImplementedError("per-head packed pages take the static retained tail only "
                                       "(config/compresslm.py:160-167)")
+        if self.packed and self.xattn != "full":
+            raise NotImplementedError("per-head packed pages serve bidirectional code steps (pause_xattn='full')")
 
         # KV-cache groups: layers of equal quota, in order of first appearance; tensor i = i-th layer of each group
         distinct = list(dict.fromkeys(self.quotas))
@@ -193,11 +200,14 @@ class CompressGen:
             start = self.logical_len - comp[g]
             seq_len = start + n
             table = torch.from_numpy(np.asarray(blocks[g], dtype=np.int32)).view(1, -1).to(self.device)
-            limit = [start + min(q, self.K)] if code_step else None
+            # the block's own code rows a code row sees: the first q (bidirectional or causal) or none
+            own = min(q, self.K) if self.xattn != "none" else 0
+            limit = [start + own] if code_step else None
             # the block's own retained tail: its last T content rows, just before the code rows in every group
             excluded = [[start - self.T, start]] if code_step and self.T else None
+            causal = [self.xattn == "causal"] if code_step else None
             out.append(self.builder.build([0, n], [seq_len], table, code_key_limit=limit, positions=logical,
-                                          compacted=comp_dev[g:g + 1], code_excluded=excluded))
+                                          compacted=comp_dev[g:g + 1], code_excluded=excluded, code_causal=causal))
         return out
 
     @torch.no_grad()

@@ -395,22 +395,25 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
                              num_blocks: int, prompt_len: torch.Tensor | None = None,
                              head_quota: torch.Tensor | None = None, scale: float | None = None,
                              out: torch.Tensor | None = None, lse: torch.Tensor | None = None, retain_tail: int = 0,
-                             tail_policy: str = "static"):
+                             tail_policy: str = "static", pause_xattn: str = "full"):
     """Teacher-forced attention under the compression mask (N blocks of [C content | K codes]).
 
     q [B, S0, 32, 128], k/v [B, S0, 8, 128] bf16 (any strides with contiguous dims, e.g. the [B, H, S, D]
     transposed views HF attention receives, permuted back); prompt_len [B] int32 raw-prompt content tokens;
     head_quota [32] int32 code slots visible per query head; retain_tail = T of a retained tail (a block's last T
     content rows, hidden from its own codes) and ``tail_policy`` the later rows that see it: "static" every later row,
-    "sticky" the next block's content rows, "rolling" the next block's i-th content row from tail row i on. Returns
+    "sticky" the next block's content rows, "rolling" the next block's i-th content row from tail row i on;
+    ``pause_xattn`` a code row's attention to its block's code rows ("full", "causal", "none"; the non-full ones
+    evaluate the mask per element). Returns
     (out [B, S0, 32, 128] bf16, lse [B, 32, S0] fp32 natural log or None). fp32 q/k/v select the fp32 mode (out fp32).
     """
     B, S0 = q.shape[0], q.shape[1]
     _require(0 <= int(retain_tail) < block_c, "retain_tail must be in [0, block_c)")
     policy = tail_policy_code(tail_policy)
+    xattn = xattn_code(pause_xattn)
     if q.dtype == torch.float32:
         return _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse,
-                                   int(retain_tail), policy)
+                                   int(retain_tail), policy, xattn)
     _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
         _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
@@ -432,8 +435,8 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     rc = lib().abkv_prefill_masked_attn(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
                                         k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2), B,
                                         block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota),
-                                        int(retain_tail), policy, scale, _ptr(out), out.stride(0), out.stride(1),
-                                        out.stride(2), _ptr(lse), C.c_void_p(_stream()))
+                                        int(retain_tail), policy, xattn, scale, _ptr(out), out.stride(0),
+                                        out.stride(1), out.stride(2), _ptr(lse), C.c_void_p(_stream()))
     check(rc, "abkv_prefill_masked_attn")
     return out, lse
 
@@ -442,12 +445,13 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
                                       lse: torch.Tensor, dout: torch.Tensor, block_c: int, codes_k: int,
                                       num_blocks: int, prompt_len: torch.Tensor | None = None,
                                       head_quota: torch.Tensor | None = None, scale: float | None = None,
-                                      retain_tail: int = 0, tail_policy: str = "static"):
+                                      retain_tail: int = 0, tail_policy: str = "static", pause_xattn: str = "full"):
     """Gradients (dq [B, S0, 32, 128], dk, dv [B, S0, 8, 128], bf16) of sum(dout * out) for
     :func:`prefill_masked_attention` under the same mask, from its out and lse (bf16 path only)."""
     B, S0 = q.shape[0], q.shape[1]
     _require(0 <= int(retain_tail) < block_c, "retain_tail must be in [0, block_c)")
     policy = tail_policy_code(tail_policy)
+    xattn = xattn_code(pause_xattn)
     _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV), ("out", out, HEADS_Q),
                        ("dout", dout, HEADS_Q)):
@@ -470,7 +474,7 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
     for t in (q, k, v, out, dout):
         args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
     args += [_ptr(lse), B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota), int(retain_tail),
-             policy, scale]
+             policy, xattn, scale]
     for t in (dq, dk, dv):
         args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
     rc = lib().abkv_prefill_masked_attn_bwd(*args, _ptr(ws), ws.numel(), C.c_void_p(_stream()))
@@ -487,8 +491,17 @@ def tail_policy_code(tail_policy: str) -> int:
     return TAIL_POLICIES.index(tail_policy)
 
 
+XATTN = ("full", "causal", "none")                  # the kernels' pause_xattn codes 0, 1, 2
+
+
+def xattn_code(pause_xattn: str) -> int:
+    """Kernel code of a pause_xattn name."""
+    _require(pause_xattn in XATTN, f"pause_xattn must be one of {XATTN}, got {pause_xattn!r}")
+    return XATTN.index(pause_xattn)
+
+
 def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse, retain_tail,
-                        policy):
+                        policy, xattn):
     B, S0 = q.shape[0], q.shape[1]
     _require(S0 == num_blocks * (block_c + codes_k), "seq_len must be num_blocks * (block_c + codes_k)")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
@@ -512,7 +525,7 @@ def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_
     rc = lib().abkv_prefill_masked_attn_f32(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
                                             k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2),
                                             B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota),
-                                            retain_tail, policy, scale, _ptr(out), out.stride(0),
+                                            retain_tail, policy, xattn, scale, _ptr(out), out.stride(0),
                                             out.stride(1), out.stride(2), _ptr(lse), C.c_void_p(_stream()))
     check(rc, "abkv_prefill_masked_attn_f32")
     return out, lse

@@ -141,12 +141,18 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
 #define ABKV_TAIL_STATIC 0
 #define ABKV_TAIL_ROLLING 1
 #define ABKV_TAIL_STICKY 2
+/* pause_xattn: a code row's attention to its own block's code rows (compress_forward.py:313-314, 622-625): all of
+ * them (ABKV_XATTN_FULL, the served setting), those at or before its own row (ABKV_XATTN_CAUSAL), none
+ * (ABKV_XATTN_NONE). The non-full settings run the per-element mask on every tile up to the query's block. */
+#define ABKV_XATTN_FULL 0
+#define ABKV_XATTN_CAUSAL 1
+#define ABKV_XATTN_NONE 2
 int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, long q_stride_h, const void* k,
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             int tail_policy, float scale, void* out, long out_stride_b, long out_stride_s,
-                             long out_stride_h, float* lse, abkv_stream_t stream);
+                             int tail_policy, int pause_xattn, float scale, void* out, long out_stride_b,
+                             long out_stride_s, long out_stride_h, float* lse, abkv_stream_t stream);
 
 /* Backward of abkv_prefill_masked_attn: the gradients dq [batch, seq_len, 32, 128] and dk, dv [batch, seq_len, 8,
  * 128] (bf16, element strides, dims contiguous; written, not accumulated) of sum(dout * out) under the same mask,
@@ -160,7 +166,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long out_stride_s, long out_stride_h, const void* dout, long dout_stride_b,
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale, void* dq,
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
+                                 float scale, void* dq,
                                  long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
                                  long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
                                  long dv_stride_h, void* workspace, size_t workspace_bytes, abkv_stream_t stream);
@@ -272,8 +279,9 @@ int abkv_paged_prefill_attn_f32(const float* q, long q_stride_t, long q_stride_h
 int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh, const float* k, long k_sb,
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
-                                 const int32_t* head_quota, int retain_tail, int tail_policy, float scale,
-                                 float* out, long o_sb, long o_ss, long o_sh, float* lse, abkv_stream_t stream);
+                                 const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
+                                 float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
+                                 abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Compaction planner (kernel 2, host half). Bit-exact restatement of the reference's scheduler/KV-manager

@@ -48,10 +48,10 @@ def _rotate_half(x):
 
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                 layer_head_quota=None, retain_tail=0, tail_policy="static"):
+                 layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
     """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
-    retained tail under ``tail_policy``."""
+    retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own block's codes."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
@@ -67,7 +67,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy)     # [B?, H?, S0, S0]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn)     # [B?, H?, S0, S0]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -98,9 +98,9 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                      layer_head_quota=None, retain_tail=0, tail_policy="static"):
+                      layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
     h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail,
-                     tail_policy)
+                     tail_policy, pause_xattn)
     rows = torch.from_numpy(loss_rows(C, N, K))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

@@ -14,6 +14,10 @@ last T content rows of an earlier block are visible, by ``tail_policy``
   "rolling" -- to the content queries of the next block through a sliding window: content query i of block b sees
                row j of block b - 1 iff (b C + i) - ((b - 1) C + j) <= T, i.e. j >= C - T + i.
 
+Code rows attend their own block's code rows by ``pause_xattn`` (compress_forward.py:622-625, 871-874,
+gen_compress.py:1121-1123): "full" all of them (bidirectional, the served setting), "causal" those at or before their own position,
+"none" none (not even themselves).
+
 Two independent restatements of the reference are kept and cross-checked:
 * ``arith_mask``  -- closed-form integer arithmetic: abridgekv/compress_forward.py:695-727 (_arith_mask_mod) with
                      the quota term of :725-726 and the static-tail terms of :714-715, :721-722; the window policies
@@ -36,13 +40,18 @@ import numpy as np
 TAIL_POLICIES = ("static", "rolling", "sticky")
 
 
-def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
+XATTN = ("full", "causal", "none")
+
+
+def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
     """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
     S0 = N * (C + K)
-    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail, tail_policy)
+    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail, tail_policy,
+                            pause_xattn)
 
 
-def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
+def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static",
+                     pause_xattn="full"):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
     per = C + K
@@ -68,7 +77,10 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
         pl = np.asarray(prompt_len, dtype=np.int64).reshape(-1, 1, 1)
         vis = vis[None] | (k_content & (kb * C + kw < pl))[...]
     vis = (kv <= q) & vis
-    vis = vis | ((qw >= C) & (~k_content) & same_blk)
+    if pause_xattn not in XATTN:
+        raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
+    if pause_xattn != "none":                                               # code <-> code, same block
+        vis = vis | ((qw >= C) & (~k_content) & same_blk & ((kv <= q) if pause_xattn == "causal" else True))
     if T:
         vis = vis & ~((qw >= C) & same_blk & k_content & (kw >= C - T))    # codes never see their own tail
     if head_quota is not None:
@@ -81,7 +93,7 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     return vis
 
 
-def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static"):
+def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
     """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
     per = C + K
     S0 = N * per
@@ -97,6 +109,12 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_pol
     earlier_final = (kr == 1) & (kb < qb)
     pause_q = qr == 1
     samepass = pause_q & (kr == qr) & (kb == qb)
+    if pause_xattn not in XATTN:
+        raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
+    if pause_xattn == "causal":
+        samepass = samepass & causal
+    elif pause_xattn == "none":
+        samepass = np.zeros_like(samepass)
     T = int(retain_tail)
     qa, ka = content_abs.reshape(S0, 1), content_abs.reshape(1, S0)
     if tail_policy == "static":
@@ -265,10 +283,10 @@ def dense_masked_attention_ref_torch(q, k, v, mask, scale):
     return torch.matmul(w, vv)
 
 
-def visible_pairs(C, K, N, prompt_len=None, retain_tail=0, tail_policy="static"):
+def visible_pairs(C, K, N, prompt_len=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
     """Number of visible (query, key) pairs of one sequence (FLOP accounting: 4 * D * pairs per head)."""
     m = arith_mask(C, K, N, None if prompt_len is None else [prompt_len], retain_tail=retain_tail,
-                   tail_policy=tail_policy)
+                   tail_policy=tail_policy, pause_xattn=pause_xattn)
     return int(m.sum())
 
 

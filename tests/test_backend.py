@@ -170,6 +170,11 @@ def test_metadata_builder_validation():
                 code_excluded=[[10, 17]])
     with pytest.raises(RuntimeError):                  # only code-step requests carry one
         b.build([0, 4], [20], bt, sm, seq_lens_dev=torch.zeros(1, dtype=torch.int32), code_excluded=[[10, 12]])
+    md = b.build([0, 4], [20], bt, sm, code_key_limit=[18], seq_lens_dev=torch.zeros(1, dtype=torch.int32),
+                 code_causal=[True])                   # a causal code step (pause_xattn="causal" of the generator)
+    assert md.code_causal.tolist() == [True]
+    with pytest.raises(RuntimeError):                  # only code-step requests may be causal code steps
+        b.build([0, 4], [20], bt, sm, seq_lens_dev=torch.zeros(1, dtype=torch.int32), code_causal=[True])
 
 
 def test_backend_surface_and_hook_is_inert_without_impl():

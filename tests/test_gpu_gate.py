@@ -33,6 +33,10 @@ CASES = [
     # sticky (all 12 until the block's codes)
     (64, 4, 16, "bitrev", [40, 100], [16, 4], [1], 12, "rolling"),
     (64, 4, 16, "bitrev", [40, 100], [16, 4], [0], 12, "sticky"),
+    # code rows attending their own block's codes causally, or not at all (gen_compress.py:953-959, the reference
+    # gate's xattn="causal" case), the second with a rolling tail
+    (64, 3, 16, "bitrev", [40, 100], [16, 4], [1], 0, "static", "causal"),
+    (64, 3, 16, "bitrev", [70, 0], [8, 16], [0], 12, "rolling", "none"),
 ]
 
 
@@ -54,13 +58,14 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
     C, N, K, code_positions, prompt, quota, stepwise = CASES[case][:7]
     T = CASES[case][7] if len(CASES[case]) > 7 else 0
     policy = CASES[case][8] if len(CASES[case]) > 8 else "static"
+    xattn = CASES[case][9] if len(CASES[case]) > 9 else "full"
     hcq = None if quota is None else [list(q) if isinstance(q, list) else [q] * 8 for q in quota]
     per_head = hcq is not None and any(len(set(row)) > 1 for row in hcq)
     base = _model(case)
     dev = torch.device("cuda")
     tail = dict(retain_tail_kv=T, retain_tail_policy=policy) if T else {}
     clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=code_positions,
-                     head_code_quotas=hcq, **tail).eval()
+                     head_code_quotas=hcq, pause_xattn=xattn, **tail).eval()
     torch.manual_seed(100 + case)
     with torch.no_grad():
         clm.pause.normal_(0, 0.05)
@@ -69,9 +74,9 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
     pause = clm.pause.detach().cpu()
 
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
-                               lhq, retain_tail=T, tail_policy=policy)
+                               lhq, retain_tail=T, tail_policy=policy, pause_xattn=xattn)
     eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq,
-                                 retain_tail=T, tail_policy=policy)
+                                 retain_tail=T, tail_policy=policy, pause_xattn=xattn)
     tol = 2 * (eager - ref).abs().max().item() + 2e-3
 
     pl = None if prompt is None else torch.tensor(prompt, dtype=torch.int32, device=dev)

@@ -14,7 +14,7 @@ def _bf16(x):
     return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static"):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static", xattn="full"):
     from abridgekv_amd import ops
     S0 = N * (C + K)
     g = torch.Generator().manual_seed(seed)
@@ -26,14 +26,14 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
-                                          lse=lse, retain_tail=tail, tail_policy=policy)
+                                          lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy)
+                             tail_policy=policy, pause_xattn=xattn)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -111,6 +111,20 @@ def test_window_tail_served_block_geometry(policy):
     """C=512, K=128, T=200 (a rolling band over four key tiles) with 4 blocks; rows sampled where the window acts."""
     rows = np.r_[0:70, 600:780, 1200:1300, 1900:1990, 2400:2560]
     _check(C=512, K=128, N=4, B=1, prompt_len=[300], rows=rows, seed=18, tail=200, policy=policy)
+
+
+@pytest.mark.parametrize("xattn", ["causal", "none"])
+@pytest.mark.parametrize("shape", ["aligned", "unaligned"])
+def test_pause_xattn(xattn, shape):
+    """Code rows attending their own block's codes causally or not at all (the per-element walk), with a raw prompt,
+    per-head quotas and a rolling tail."""
+    if shape == "aligned":
+        quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+        _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=19, tail=20, policy="rolling",
+               xattn=xattn)
+    else:
+        quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+        _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=20, xattn=xattn)
 
 
 def test_strided_hf_layout():

@@ -9,7 +9,7 @@ from oracle import prefill as op
 pytestmark = pytest.mark.gpu
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy="static"):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy="static", xattn="full"):
     from abridgekv_amd import ops
     S0 = N * (C + K)
     g = torch.Generator().manual_seed(seed)
@@ -23,15 +23,16 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy=
     qd, kd, vd, gd = (t.to(dev) for t in (q, k, v, dout))
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse,
-                                          retain_tail=tail, tail_policy=policy)
+                                          retain_tail=tail, tail_policy=policy, pause_xattn=xattn)
     dq, dk, dv = ops.prefill_masked_attention_backward(qd, kd, vd, out, lse, gd, C, K, N, prompt_len=pl,
-                                                       head_quota=hq, retain_tail=tail, tail_policy=policy)
+                                                       head_quota=hq, retain_tail=tail, tail_policy=policy,
+                                                       pause_xattn=xattn)
     torch.cuda.synchronize()
     got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy)
+                             tail_policy=policy, pause_xattn=xattn)
         if prompt_len is not None:
             mask = mask[0]
         ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
@@ -91,6 +92,13 @@ def test_window_tail_aligned_blocks(policy, tail):
 def test_window_tail_unaligned_blocks(policy):
     quota = np.repeat([12, 3, 7, 12, 1, 5, 9, 12], 4).tolist()
     _check(C=40, K=12, N=4, B=1, prompt_len=[45], head_quota=quota, seed=26, tail=7, policy=policy)
+
+
+@pytest.mark.parametrize("xattn", ["causal", "none"])
+def test_pause_xattn(xattn):
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=27, tail=20, policy="sticky",
+           xattn=xattn)
 
 
 def test_autograd_through_hf_attention_layout():

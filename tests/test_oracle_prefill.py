@@ -12,14 +12,16 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static"):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full"):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
     all later queries (content and code rows), and the codes summarize only the first block_size - T tokens".
     Window tails (compresslm.py:23, "window tails of the previous block (content queries only, expire)"): sticky
     keeps the previous block's whole tail for every content query of the block; rolling lets the i-th content token
-    of the block see the previous block's tail rows from the i-th on (one tail row expires per content token)."""
+    of the block see the previous block's tail rows from the i-th on (one tail row expires per content token).
+    pause_xattn (compress_forward.py:313-314, "within-pass code<->code attention"): "full" every code row of the
+    block, "causal" the ones up to the query, "none" no code row of its own block."""
     per = C + K
     S = N * per
     m = np.zeros((S, S), bool)
@@ -38,7 +40,7 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static"):
                 if row >= 0 and (policy == "sticky" or row >= qw):
                     vis = True
             vis = vis and k <= q
-            if qw >= C and not k_content and kb == qb:
+            if qw >= C and not k_content and kb == qb and (xattn == "full" or (xattn == "causal" and k <= q)):
                 vis = True
             if tail and qw >= C and k_content and kb == qb and kw >= C - tail:
                 vis = False                      # a code row does not summarize its own block's tail
@@ -90,6 +92,28 @@ def test_window_tail_arith_equals_role_equals_brute(C, K, N, T, policy):
     for b, p in enumerate(pl):
         for h, q in enumerate(hq):
             assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T, policy=policy))
+
+
+@pytest.mark.parametrize("xattn", ["causal", "none"])
+@pytest.mark.parametrize("C,K,N,T", [(4, 2, 3, 0), (8, 4, 3, 3), (6, 4, 3, 2)])
+def test_pause_xattn_arith_equals_role_equals_brute(C, K, N, T, xattn):
+    for policy in ("static", "rolling"):
+        kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn)
+        a = op.arith_mask(C, K, N, **kw)
+        assert np.array_equal(a, op.role_mask(C, K, N, **kw))
+        assert np.array_equal(a, brute(C, K, N, tail=T, policy=policy, xattn=xattn))
+        assert not np.array_equal(a, op.arith_mask(C, K, N, retain_tail=T, tail_policy=policy))
+        pl, hq = [0, C + 1], [1, K, 2, K]
+        ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, **kw)
+        assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, **kw))
+        for b, p in enumerate(pl):
+            for h, q in enumerate(hq):
+                assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T, policy=policy,
+                                                      xattn=xattn))
+    per = C + K
+    m = op.arith_mask(C, K, N, pause_xattn=xattn)
+    assert m[C, C] == (xattn == "causal") and not m[C, C + 1]          # a code row and the next code row
+    assert m[C + 1, C] == (xattn == "causal") and m[per + C, C]        # earlier codes stay visible
 
 
 def test_window_tail_spot_checks():
