@@ -1,23 +1,25 @@
 """Teacher-forced CompressLM forward over the masked-prefill kernel (the training/evaluation entry point).
 
-Mirrors the served subset of abridgekv/compress_forward.py:240-1230 (``CompressLM``): one pause pass (L=1) with
-code<->code attention in a block bidirectional (``pause_xattn="full"``, the served setting), causal or absent
-(``"causal"``, ``"none"``: :313-314, 622-625; the kernel evaluates those per element), optional raw prompt, optional fixed
-per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` / ``bitrev`` code positions and the retained
-tail (``retain_tail_kv`` = T: a block's codes do not see or summarize its last T content rows, bitrev codes spread
-over the first C - T; by ``retain_tail_policy`` those rows stay visible to every later row ("static"), to the next
-block's content rows ("sticky"), or to the next block's i-th content row from tail row i on ("rolling"),
-compress_forward.py:99-124). The sequence
-layout, RoPE positions, loss positions and loss reductions follow the reference (compress_forward.py:20-88,
-1044-1071, 957-1042, 1134-1230); the attention of every decoder layer runs ``abkv_prefill_masked_attn`` through a
-HuggingFace attention function registered as ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask
-(``_arith_mask_mod`` / ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 695-727,
-815-894). The mask is never materialised: the kernel evaluates it from (C, K, N, prompt_len, head quota).
+Mirrors abridgekv/compress_forward.py:240-1230 (``CompressLM``): L pause passes (pass l of a block refines pass
+l - 1; later blocks read the final pass, :566-649), code<->code attention within a pass bidirectional
+(``pause_xattn="full"``, the served setting), causal or absent (``"causal"``, ``"none"``: :313-314, 622-625),
+optional raw prompt, optional fixed per-(layer, KV head) code quotas, ``active_code_rows``, ``appended`` /
+``bitrev`` code positions and the retained tail (``retain_tail_kv`` = T: a block's codes do not see or summarize its
+last T content rows, bitrev codes spread over the first C - T; by ``retain_tail_policy`` those rows stay visible to
+every later row ("static"), to the next block's content rows ("sticky"), or to the next block's i-th content row
+from tail row i on ("rolling"), compress_forward.py:99-124); the code-seed pools (``seg_pool``,
+``gated_seg_pool``, ``pool_init``, :315-343, 1147-1178) and the code-row projections (``query_residual``,
+``code_q_heads``, ``code_kv_heads``, :181-222, 397-432). The sequence layout, RoPE positions, loss positions and
+loss reductions follow the reference (compress_forward.py:20-88, 1044-1071, 957-1042, 1134-1230); the attention of
+every decoder layer runs ``abkv_prefill_masked_attn`` through a HuggingFace attention function registered as
+``"abridgekv_hip"`` in place of FlexAttention with a BlockMask (``_arith_mask_mod`` / ``_mask_mod`` /
+``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 566-649, 695-727, 815-894). The mask
+is never materialised: the kernel evaluates it from (C, K, L, N, prompt_len, head quota, tail, xattn); layouts off
+the 64-row tile grid, L > 1 and non-full xattn take its per-element walk.
 
-Options of the reference that belong to other experiments (replay / raw tails, learned or segment pooling, query
-residuals, copy and distillation losses, external block masks) raise
-NotImplementedError. Gradients
-flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module trains.
+Replay / raw tails (legacy appended-layout checkpoints), the full-context baseline, copy and distillation losses
+and external block masks raise NotImplementedError. Gradients flow through the attention by the kernel's HIP
+backward (dq, dk, dv under the same mask), so the module trains.
 """
 from __future__ import annotations
 
@@ -36,7 +38,7 @@ ATTN_IMPLEMENTATION = "abridgekv_hip"
 @dataclass(frozen=True)
 class CompressMask:
     """What the kernel needs to evaluate the compression mask (the analogue of the reference's BlockMask):
-    N blocks of [C content | K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
+    N blocks of [C content | ``passes`` passes of K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
     ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a retained
     tail (0: none) under ``tail_policy`` ("static", "rolling" or "sticky")."""
     block_c: int
@@ -47,6 +49,7 @@ class CompressMask:
     retain_tail: int = 0
     tail_policy: str = "static"
     pause_xattn: str = "full"
+    passes: int = 1
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -65,7 +68,7 @@ class _MaskedPrefill(torch.autograd.Function):
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
                                               prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
                                               retain_tail=mask.retain_tail, tail_policy=mask.tail_policy,
-                                              pause_xattn=mask.pause_xattn)
+                                              pause_xattn=mask.pause_xattn, pause_passes=mask.passes)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -79,7 +82,8 @@ class _MaskedPrefill(torch.autograd.Function):
         dq, dk, dv = ops.prefill_masked_attention_backward(q, k, v, out, lse, g, m.block_c, m.codes_k, m.num_blocks,
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
                                                            scale=ctx.scale, retain_tail=m.retain_tail,
-                                                           tail_policy=m.tail_policy, pause_xattn=m.pause_xattn)
+                                                           tail_policy=m.tail_policy, pause_xattn=m.pause_xattn,
+                                                           pause_passes=m.passes)
         return dq, dk, dv, None, None, None
 
 
@@ -104,27 +108,29 @@ def register_attention() -> None:
     AttentionInterface.register(ATTN_IMPLEMENTATION, masked_attention_forward)
 
 
-def roles(C: int, N: int, K: int, device=None):
-    """(blk, role) per row of the L=1 layout: role 0 = content, 1 = code (compress_forward.py:20-31)."""
-    per = C + K
+def roles(C: int, N: int, K: int, device=None, L: int = 1):
+    """(blk, role) per row of the layout of N blocks of [C content | L passes of K codes]: role 0 = content,
+    1..L = pause pass (compress_forward.py:20-31)."""
+    per = C + L * K
     within = torch.arange(per, device=device).repeat(N)
     blk = torch.arange(N, device=device).repeat_interleave(per)
-    return blk, (within >= C).long()
+    return blk, torch.where(within < C, torch.zeros_like(within), torch.div(within - C, K, rounding_mode="floor") + 1)
 
 
-def content_abs_pos(C: int, N: int, K: int, device=None) -> torch.Tensor:
+def content_abs_pos(C: int, N: int, K: int, device=None, L: int = 1) -> torch.Tensor:
     """Absolute content index b*C + j of content rows; N*C for code rows (compress_forward.py:72-88, no replay)."""
-    per = C + K
+    per = C + L * K
     within = torch.arange(per, device=device).repeat(N)
     blk = torch.arange(N, device=device).repeat_interleave(per)
     return torch.where(within < C, blk * C + within, torch.full_like(within, N * C))
 
 
 def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, device=None,
-                      code_excluded_tail: int = 0) -> torch.Tensor:
-    """(1, N*(C+K_act)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, L=1,
-    no replay tail, no copy rows); bitrev code rows spread over the first C - code_excluded_tail in-block offsets."""
-    per_full, per_act = C + K, C + K_act
+                      code_excluded_tail: int = 0, L: int = 1) -> torch.Tensor:
+    """(1, N*(C+L*K_act)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, no replay
+    tail, no copy rows): appended code row p of a block sits at C + (p // K_act) K + p % K_act of the full layout;
+    bitrev code rows (L = 1) spread over the first C - code_excluded_tail in-block offsets."""
+    per_full, per_act = C + L * K, C + L * K_act
     idx = torch.arange(N * per_act, device=device)
     within, blk = idx % per_act, idx // per_act
     is_code = within >= C
@@ -133,33 +139,118 @@ def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, d
         offs = torch.from_numpy(bitrev_offsets(K, C - code_excluded_tail)).to(device)
         pos = torch.where(is_code, blk * C + offs[p.clamp_max(K - 1)], blk * C + within)
     else:
-        pos = torch.where(is_code, blk * per_full + C + p, blk * per_full + within)
+        slot = torch.div(p, K_act, rounding_mode="floor") * K + p % K_act
+        pos = torch.where(is_code, blk * per_full + C + slot, blk * per_full + within)
     return pos.view(1, -1)
 
 
-_UNSUPPORTED = ("pool_init", "query_residual", "code_q_heads", "code_kv_heads", "seg_pool", "gated_seg_pool",
-                "raw_tail", "replay_tail", "code_exclude_replay_tail")
+class _CodeRows:
+    """The code rows of the current teacher-forced layout (sequence indices and slot 0..L*K_act-1 within the block),
+    shared by the code-row projections and kept current by :meth:`CompressLM.set_N`."""
+
+    def __init__(self):
+        self.rows = self.slots = None
+        self.S0 = -1
+
+
+class _QProjQRes(nn.Module):
+    """q_proj of one layer plus a learned query residual per code slot, added at the code rows of the compressed
+    layout (``query_residual``, compress_forward.py:181-199, 397-413). ``qres`` starts at zero (an exact no-op) and
+    sequences of another length (not the layout's S0) pass through unchanged. Names ``orig`` / ``qres`` as in the
+    reference's state dict."""
+
+    def __init__(self, orig: nn.Linear, num_slots: int, code_rows: _CodeRows):
+        super().__init__()
+        self.orig = orig
+        self.qres = nn.Parameter(torch.zeros(num_slots, orig.out_features, device=orig.weight.device))
+        self._code_rows = code_rows
+
+    def forward(self, x):
+        out = self.orig(x)
+        cr = self._code_rows
+        if out.size(1) != cr.S0:
+            return out
+        res = self.qres.index_select(0, cr.slots).to(out.dtype)
+        return out.index_add(1, cr.rows, res.unsqueeze(0).expand(out.size(0), -1, -1))
+
+
+class _QProjCode(nn.Module):
+    """A projection (q_proj, or k_proj / v_proj) of one layer whose code rows go through their own copy of the
+    weights (``code_q_heads`` / ``code_kv_heads``, compress_forward.py:202-222, 414-432): ``code`` starts as a copy of
+    ``orig`` (an exact no-op), content rows and sequences of another length keep ``orig``."""
+
+    def __init__(self, orig: nn.Linear, code_rows: _CodeRows):
+        super().__init__()
+        self.orig = orig
+        self.code = nn.Linear(orig.in_features, orig.out_features, bias=orig.bias is not None,
+                              device=orig.weight.device, dtype=orig.weight.dtype)
+        with torch.no_grad():
+            self.code.weight.copy_(orig.weight)
+            if orig.bias is not None:
+                self.code.bias.copy_(orig.bias)
+        self._code_rows = code_rows
+
+    def forward(self, x):
+        out = self.orig(x)
+        cr = self._code_rows
+        if out.size(1) != cr.S0:
+            return out
+        return out.index_copy(1, cr.rows, self.code(x.index_select(1, cr.rows)).to(out.dtype))
+
+
+def code_seeds(clm, tok_e: torch.Tensor, segment_mean: bool = False) -> torch.Tensor:
+    """Input embeddings [..., K, d] of one pass of code rows for blocks whose content embeddings are tok_e
+    [..., C, d] (compress_forward.py:1147-1178, gen_compress.py:867-898): the learned seeds ``pause``, plus the
+    mean of K contiguous segments of the block's content (``seg_pool``, ``gated_seg_pool`` times a learned per-slot
+    gate; ``segment_mean`` forces it) or a learned softmax pooling of the content (``pool_init``). Both pools read
+    the content rows the codes summarise (the first C - T under a retained tail)."""
+    K = getattr(clm, "K_act", clm.K)
+    mdt = tok_e.dtype
+    d = tok_e.size(-1)
+    lead = tok_e.shape[:-2]
+    T = getattr(clm, "code_excluded_tail", 0)
+    src = tok_e[..., : tok_e.size(-2) - T, :] if T else tok_e
+    n = src.size(-2)
+    pause = clm.pause[:K].to(mdt)
+    gated = getattr(clm, "gated_seg_pool", False)
+    if segment_mean or gated or getattr(clm, "seg_pool", False):
+        seg = n // K
+        if seg >= 1:
+            tm = src[..., : K * seg, :].reshape(*lead, K, seg, d).mean(-2)
+        else:                                                      # fewer content rows than codes: the block mean
+            tm = src.mean(-2, keepdim=True).expand(*lead, K, d)
+        if gated:
+            tm = tm * clm.seg_pool_gate.to(mdt).view(K, 1)
+        return pause + tm.to(mdt)
+    if getattr(clm, "pool_init", False):
+        keys = F.linear(src, clm.pool_k.weight.to(mdt))
+        vals = F.linear(src, clm.pool_v.weight.to(mdt))
+        sc = torch.matmul(keys, clm.pool_q.to(mdt).t()).transpose(-1, -2) * (d ** -0.5)      # [..., K, n]
+        return pause + torch.matmul(sc.float().softmax(-1).to(mdt), vals)
+    return pause.expand(*lead, K, d)
+
+
+_UNSUPPORTED = ("raw_tail", "replay_tail", "code_exclude_replay_tail")
 
 
 class CompressLM(nn.Module):
-    """API-compatible subset of the reference ``CompressLM(base_model, C, N, K, ...)``.
+    """API-compatible ``CompressLM(base_model, C, N, K, ...)`` (compress_forward.py:239-433), same positional order.
 
     ``base_model`` is a HuggingFace causal LM with 32 query heads, 8 KV heads and head size 128 in bf16 (e.g.
     Qwen3-4B or a random model of that attention shape); its attention implementation is switched to
-    ``"abridgekv_hip"``.
+    ``"abridgekv_hip"``. Replay and raw tails (legacy appended-layout checkpoints) raise NotImplementedError.
     """
 
-    def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", head_code_quotas=None, active_code_rows=None,
-                 code_positions="appended", retain_tail_kv=0, retain_tail_policy="rolling", **options):
+    def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", pool_init=False, query_residual=False,
+                 code_q_heads=False, code_kv_heads=False, seg_pool=False, gated_seg_pool=False, raw_tail=0,
+                 replay_tail=0, code_exclude_replay_tail=False, retain_tail_kv=0, retain_tail_policy="rolling",
+                 head_code_quotas=None, active_code_rows=None, code_positions="appended"):
         super().__init__()
-        bad = sorted(name for name in options if name not in _UNSUPPORTED)
-        if bad:
-            raise TypeError(f"unexpected CompressLM options {bad}")
-        used = sorted(name for name, value in options.items() if value)
+        used = [name for name, value in zip(_UNSUPPORTED, (raw_tail, replay_tail, code_exclude_replay_tail)) if value]
         if used:
             raise NotImplementedError(f"CompressLM options {used} are not supported by the native forward")
-        if L != 1:
-            raise NotImplementedError("only one pause pass (L=1) is supported")
+        if int(L) != L or L < 1:
+            raise ValueError(f"L must be a positive integer, got {L}")
         if pause_xattn not in ("none", "causal", "full"):
             raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {pause_xattn!r}")
         if not 0 <= retain_tail_kv < C:
@@ -170,8 +261,10 @@ class CompressLM(nn.Module):
             raise ValueError(f"retain_tail_policy={retain_tail_policy!r} requires retain_tail_kv > 0")
         if code_positions not in ("appended", "bitrev"):
             raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
-        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1)):
+        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1) or L != 1):
             raise ValueError("code_positions='bitrev' needs power-of-two C and K, L=1 and no tails")
+        if query_residual and code_q_heads:
+            raise ValueError("query_residual and code_q_heads both replace q_proj; enable one of them")
         cfg = base_model.config
         heads, kv_heads = int(cfg.num_attention_heads), int(getattr(cfg, "num_key_value_heads", cfg.num_attention_heads))
         head_dim = int(getattr(cfg, "head_dim", None) or cfg.hidden_size // heads)
@@ -181,7 +274,7 @@ class CompressLM(nn.Module):
         register_attention()
         self.model = base_model
         self.model.config._attn_implementation = ATTN_IMPLEMENTATION
-        self.C, self.N, self.K, self.L = int(C), int(N), int(K), 1
+        self.C, self.N, self.K, self.L = int(C), int(N), int(K), int(L)
         self.pause_xattn, self.code_positions = pause_xattn, code_positions
         self.replay_tail = self.raw_tail = 0
         self.retain_tail_kv = self.code_excluded_tail = int(retain_tail_kv)
@@ -191,29 +284,58 @@ class CompressLM(nn.Module):
         self.K_act = int(active_code_rows) if active_code_rows else self.K
         if not 1 <= self.K_act <= self.K:
             raise ValueError(f"active_code_rows must be in [1, K={K}], got {active_code_rows}")
+        if self.K_act != self.K and (pool_init or seg_pool or gated_seg_pool):
+            raise ValueError("active_code_rows < K is not supported with pool_init/seg_pool")
         d = int(cfg.hidden_size)
         std = getattr(cfg, "initializer_range", 0.02)
         dev = next(base_model.parameters()).device
         self.pause = nn.Parameter(torch.empty(self.K, d, device=dev).normal_(0, std))
+        # code-seed pools (compress_forward.py:315-343): a per-slot gate on the segment means (zero: the generic
+        # seeds), or K learned queries over the content with a zero value map (likewise an exact no-op at first)
+        self.pool_init, self.seg_pool, self.gated_seg_pool = bool(pool_init), bool(seg_pool), bool(gated_seg_pool)
+        if gated_seg_pool:
+            self.seg_pool_gate = nn.Parameter(torch.zeros(self.K, device=dev))
+        if pool_init:
+            self.pool_q = nn.Parameter(torch.empty(self.K, d, device=dev).normal_(0, std))
+            self.pool_k = nn.Linear(d, d, bias=False, device=dev)
+            self.pool_v = nn.Linear(d, d, bias=False, device=dev)
+            nn.init.zeros_(self.pool_v.weight)
         self.num_layers = len(self.model.model.layers)
         self.num_attention_heads, self.num_kv_heads = heads, kv_heads
         self.num_key_value_groups = heads // kv_heads
+        # projections of the code rows (compress_forward.py:397-432)
+        self.query_residual, self.code_q_heads, self.code_kv_heads = (bool(query_residual), bool(code_q_heads),
+                                                                       bool(code_kv_heads))
+        self._code_rows = _CodeRows()
+        for layer in self.model.model.layers:
+            attn = layer.self_attn
+            if query_residual:
+                attn.q_proj = _QProjQRes(attn.q_proj, self.L * self.K_act, self._code_rows)
+            if code_q_heads:
+                attn.q_proj = _QProjCode(attn.q_proj, self._code_rows)
+            if code_kv_heads:
+                attn.k_proj = _QProjCode(attn.k_proj, self._code_rows)
+                attn.v_proj = _QProjCode(attn.v_proj, self._code_rows)
         self._set_layout(self.N)
         self.set_head_code_quotas(head_code_quotas)
 
     def _set_layout(self, N):
         dev = self.pause.device
-        C, Ka = self.C, self.K_act
-        blk, role = roles(C, N, Ka, dev)
+        C, Ka, L = self.C, self.K_act, self.L
+        blk, role = roles(C, N, Ka, dev, L)
         content = role == 0
         pf = torch.tensor([k for k in range(N * C) if k % C != C - 1], device=dev, dtype=torch.long)
-        layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev),
+        layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev, L),
                   "loss_pos": content & torch.roll(content, -1), "content_pos": content.nonzero(as_tuple=True)[0],
                   "predict_flat": pf, "predict_block": pf // C,
                   "_pos_ids": rope_position_ids(C, N, self.K, Ka, self.code_positions, dev,
-                                                self.code_excluded_tail)}
+                                                self.code_excluded_tail, L)}
         for name, value in layout.items():
             self.register_buffer(name, value, persistent=False)
+        code = (role > 0).nonzero(as_tuple=True)[0]
+        self._code_rows.rows = code
+        self._code_rows.slots = code % (C + L * Ka) - C
+        self._code_rows.S0 = N * (C + L * Ka)
 
     def set_N(self, N):
         """Rebuild the N-dependent layout for a new block count (compress_forward.py set_N)."""
@@ -258,7 +380,7 @@ class CompressLM(nn.Module):
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
         return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
-                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn)
+                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn, self.L)
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:
@@ -292,11 +414,13 @@ class CompressLM(nn.Module):
             raise ValueError(f"content_ids block size {C} != C={self.C}")
         if N != self.N:
             self.set_N(N)
-        K = self.K_act
+        K, L = self.K_act, self.L
         tok_e = self.model.model.embed_tokens(content_ids)
         d = tok_e.size(-1)
-        pause_e = self.pause[:K].to(tok_e.dtype).view(1, 1, K, d).expand(B, N, K, d)
-        x = torch.cat([tok_e, pause_e], dim=2).reshape(B, N * (C + K), d)
+        pause_e = code_seeds(self, tok_e).expand(B, N, K, d)
+        if L > 1:
+            pause_e = pause_e.repeat(1, 1, L, 1)                      # every pass starts from the same seeds
+        x = torch.cat([tok_e, pause_e], dim=2).reshape(B, N * (C + L * K), d)
         if torch.is_autocast_enabled(x.device.type):
             x = x.to(torch.get_autocast_dtype(x.device.type))
         mask = self.compress_mask(B, prompt_len, N)
@@ -326,7 +450,7 @@ class CompressLM(nn.Module):
             prompt_len = (rmf.cumsum(1) == 0).sum(1).to(torch.int32)      # leading zeros = prompt length
         out = self.hidden_states(content_ids, prompt_len)
         d = out.size(-1)
-        S0 = N * (C + self.K_act)
+        S0 = N * (C + self.L * self.K_act)
         if include_cross_block:
             pred_flat = torch.arange(N * C - 1, device=dev)
             hid = out[:, :S0, :][:, self.content_pos, :][:, :-1, :].reshape(-1, d)

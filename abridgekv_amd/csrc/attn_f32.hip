@@ -44,6 +44,7 @@ struct F32Args {
   int retain_tail;             // retained tail T (0: none)
   int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky)
   int pause_xattn;             // code <-> code attention in a block (kXattn*)
+  int pause_passes;            // pause passes of codes_k rows per block
   int num_tokens;
   float scale;
   float* out;
@@ -66,18 +67,9 @@ __device__ __forceinline__ void wave_sync() {
 //   shows this row) | (code q & code k & same block), a code query never sees its own block's last T content rows,
 //   and a code key of slot s is visible to a head only if s < quota.
 __device__ __forceinline__ bool f32_visible(const F32Args& a, int qr, int kr, int plen, int quota) {
-  const int per = a.block_c + a.codes_k;
-  const int qb = qr / per, kb = kr / per;
-  const int qw = qr - qb * per, kw = kr - kb * per;
-  const bool kc = kw < a.block_c;
-  const bool in_tail = kc && kw >= a.block_c - a.retain_tail;
-  bool vis = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * a.block_c + kw < plen) ||
-             tail_visible(a.tail_policy, a.retain_tail, a.block_c, qb, qw, kb, kw);
-  vis = (kr <= qr) && vis;
-  vis = vis || (qw >= a.block_c && !kc && kb == qb &&
-                (a.pause_xattn == kXattnFull || (a.pause_xattn == kXattnCausal && kr <= qr)));
-  vis = vis && !(qw >= a.block_c && kb == qb && in_tail);
-  return vis && (kc || kw - a.block_c < quota);
+  return compress_visible(qr, kr, a.seq_len, a.block_c, a.codes_k, a.pause_passes,
+                          a.block_c + a.pause_passes * a.codes_k, plen, quota, a.retain_tail, a.tail_policy,
+                          a.pause_xattn);
 }
 
 __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
@@ -96,7 +88,7 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
   if (a.mode == 1) {
     b = t / a.seq_len;
     qrow = t - b * a.seq_len;
-    const int per = a.block_c + a.codes_k;
+    const int per = a.block_c + a.pause_passes * a.codes_k;
     n_keys = min(a.seq_len, (qrow / per + 1) * per);   // nothing after the query's own block is visible
     plen = a.prompt_len ? a.prompt_len[b] : 0;
     if (a.head_quota)
@@ -309,13 +301,15 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
+                                 int pause_passes, float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
                                  hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
-      num_blocks <= 0 || seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
-      tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull || pause_xattn > kXattnNone)
+      num_blocks <= 0 || pause_passes <= 0 ||
+      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) || retain_tail < 0 ||
+      retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
+      pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   F32Args a = f32_defaults();
   a.mode = 1;
@@ -339,6 +333,7 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
   a.retain_tail = retain_tail;
   a.tail_policy = tail_policy;
   a.pause_xattn = pause_xattn;
+  a.pause_passes = pause_passes;
   a.num_tokens = batch * seq_len;
   a.scale = scale;
   a.out = out;

@@ -20,19 +20,10 @@ struct MaskGeom {
   int quota[2];
   int tail;
   int policy;
-  int xattn;      // code rows' attention to their own block's code rows (kXattn*)
+  int xattn;      // code rows' attention to their own pass's code rows (kXattn*)
+  int K, L;       // code rows per pause pass, passes per block
   __device__ __forceinline__ bool visible(int kv, int u) const {
-    if (kv >= S0 || qrow >= S0) return false;
-    const int qb = qrow / per, kb = kv / per;
-    const int qw = qrow - qb * per, kw = kv - kb * per;
-    const bool kc = kw < C;
-    const bool in_tail = kc && kw >= C - tail;
-    bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) ||
-             tail_visible(policy, tail, C, qb, qw, kb, kw);
-    v = v && kv <= qrow;
-    v = v || (qw >= C && !kc && kb == qb && (xattn == kXattnFull || (xattn == kXattnCausal && kv <= qrow)));
-    v = v && !(qw >= C && kb == qb && in_tail);
-    return v && (kc || kw - C < quota[u]);
+    return compress_visible(qrow, kv, S0, C, K, L, per, plen, quota[u], tail, policy, xattn);
   }
 };
 

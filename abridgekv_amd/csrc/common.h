@@ -26,18 +26,43 @@ constexpr int kTailStatic = 0;   // every later row
 constexpr int kTailRolling = 1;  // the next block's i-th content row sees the tail's rows i .. T-1
 constexpr int kTailSticky = 2;   // every content row of the next block
 
-// Whether content row kw (in-block offset) of block kb is a retained-tail row visible to row qw of block qb under the
-// policy (abridgekv/compress_forward.py:99-124; the caller adds causality, the raw prompt and the codes' exclusion of
-// their own block's tail).
-// pause_xattn: which code rows of its own block a code row sees (compress_forward.py:313-314, 622-625).
+// pause_xattn: which code rows of its own pass and block a code row sees (compress_forward.py:313-314, 622-625).
 constexpr int kXattnFull = 0;     // all of them (bidirectional)
 constexpr int kXattnCausal = 1;   // those at or before its own position
 constexpr int kXattnNone = 2;     // none, itself included
 
+// Whether content row kw (in-block offset) of block kb is a retained-tail row visible to row qw of block qb under the
+// policy (abridgekv/compress_forward.py:99-124; the caller adds causality, the raw prompt and the codes' exclusion of
+// their own block's tail).
 __device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb, int qw, int kb, int kw) {
   if (kw >= C || kw < C - tail) return false;
   if (policy == kTailStatic) return kb < qb;
   return qw < C && kb + 1 == qb && (policy == kTailSticky || kw - (C - tail) >= qw);
+}
+
+// Visibility of key row kv to query row q (sequence rows) under the compression mask over blocks of
+// [C content | L pause passes of K code rows] (per = C + L K; abridgekv/compress_forward.py:566-649, _mask_mod):
+//   causal & (own-block content | earlier blocks' final-pass codes | raw-prompt content (< plen) | retained tail)
+//   | a code row's own block's previous pass | its own pass by xattn,
+// less a code row's own block's last `tail` content rows, and less a code key whose slot (its index within its pass)
+// is >= quota. With L = 1 (a compile-time constant at most call sites) the pass arithmetic folds away.
+__device__ __forceinline__ bool compress_visible(int q, int kv, int S0, int C, int K, int L, int per, int plen,
+                                                 int quota, int tail, int policy, int xattn) {
+  if (kv >= S0 || q >= S0) return false;
+  const int qb = q / per, kb = kv / per;
+  const int qw = q - qb * per, kw = kv - kb * per;
+  const bool kc = kw < C, qc = qw < C;
+  const int kp = L == 1 ? 1 : (kw - C) / K + 1;            // pass of a code key (1..L)
+  const int qp = L == 1 ? 1 : (qw - C) / K + 1;            // pass of a code query
+  const bool in_tail = kc && kw >= C - tail;
+  bool v = (kc && kb == qb) || (!kc && kp == L && kb < qb) || (kc && kb * C + kw < plen) ||
+           tail_visible(policy, tail, C, qb, qw, kb, kw);
+  v = v && kv <= q;
+  const bool own_codes = !qc && !kc && kb == qb;
+  v = v || (own_codes && kp + 1 == qp);
+  v = v || (own_codes && kp == qp && (xattn == kXattnFull || (xattn == kXattnCausal && kv <= q)));
+  v = v && !(!qc && kb == qb && in_tail);
+  return v && (kc || kw - C - (kp - 1) * K < quota);
 }
 
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8 a, const bf16x8 b, floatx4 c) {

@@ -84,23 +84,6 @@ __device__ __forceinline__ void pack_tile_op(const floatx4 (&x)[2][2][H], bf16x8
     }
 }
 
-// Visibility of key kv to query row q under the compression mask (the per-element predicate of MaskGeom::visible
-// with the query as an argument), for unaligned layouts and the partial tiles of layouts with a retained tail.
-__device__ __forceinline__ bool elem_visible(int q, int kv, int S0, int C, int per, int plen, int quota, int tail,
-                                             int policy, int xattn) {
-  if (kv >= S0 || q >= S0) return false;
-  const int qb = q / per, kb = kv / per;
-  const int qw = q - qb * per, kw = kv - kb * per;
-  const bool kc = kw < C;
-  const bool in_tail = kc && kw >= C - tail;
-  bool v = (kc && kb == qb) || (!kc && kb < qb) || (kc && kb * C + kw < plen) ||
-           tail_visible(policy, tail, C, qb, qw, kb, kw);
-  v = v && kv <= q;
-  v = v || (qw >= C && !kc && kb == qb && (xattn == kXattnFull || (xattn == kXattnCausal && kv <= q)));
-  v = v && !(qw >= C && kb == qb && in_tail);
-  return v && (kc || kw - C < quota);
-}
-
 template <int N>
 struct Buf {
   static constexpr int value = N;
@@ -121,7 +104,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
   const int rg = w / 2, hbase = H * (w % 2);
-  const int per = f.C + f.K;
+  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K;
   const int q0 = qt * kBM;
   const int qrow = q0 + 16 * rg + m16;
   const int plen = f.prompt_len ? f.prompt_len[b] : 0;
@@ -164,7 +147,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const DenseRows<kAligned> rows{f.k + (long)b * f.k_sb + (long)kvh * f.k_sh, f.v + (long)b * f.v_sb + (long)kvh * f.v_sh,
                                  f.k_ss, f.v_ss};
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
-  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail, f.policy, f.xattn};
+  const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail, f.policy, f.xattn, f.K, kAligned ? 1 : f.L};
   const int q_last = min(q0 + kBM, f.S0) - 1;
   TileWalk<kAligned, kTail, kWindow> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1, f.tail, f.policy);
 
@@ -371,7 +354,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
-  const int per = f.C + f.K;
+  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K;
   const int k0 = kt * kBN;
   const int key = k0 + 16 * w + m16;                        // this lane's column
   const int plen = f.prompt_len ? f.prompt_len[b] : 0;
@@ -414,6 +397,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   const int etail = kAligned && !kTail ? 0 : f.tail;
   const int epolicy = kAligned && !kWindow ? kTailStatic : f.policy;
   const int exattn = kAligned ? kXattnFull : f.xattn;
+  const int epasses = kAligned ? 1 : f.L;
   int qt = qt_lo, h = -1, mode = 0, lim0 = 0, lim1 = 0;
   auto next_pair = [&]() -> bool {
     for (;;) {
@@ -504,8 +488,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
               // tiles: the per-element predicate
               const bool vis = cmode == 1                   ? key <= qrow
                                : (kWindow && cmode == 5) ? (key < clim0 || key - qrow >= clim1)
-                                                         : elem_visible(qrow, key, f.S0, f.C, per, plen, qh, etail,
-                                                                        epolicy, exattn);
+                                                         : compress_visible(qrow, key, f.S0, f.C, f.K, epasses, per,
+                                                                            plen, qh, etail, epolicy, exattn);
               const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
               s[kk][t][0][r] = pr;
               dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
@@ -552,7 +536,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 float scale, void* dq,
+                                 int pause_passes, float scale, void* dq,
                                  long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
                                  long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
                                  long dv_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -560,8 +544,9 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || dout == nullptr || lse == nullptr ||
       dq == nullptr || dk == nullptr || dv == nullptr || block_c <= 0 || codes_k <= 0 || num_blocks <= 0 ||
-      seq_len != num_blocks * (block_c + codes_k) || retain_tail < 0 || retain_tail >= block_c ||
-      tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull || pause_xattn > kXattnNone)
+      pause_passes <= 0 || (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) ||
+      retain_tail < 0 || retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky ||
+      pause_xattn < kXattnFull || pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   if (workspace == nullptr || workspace_bytes < abkv_prefill_masked_bwd_workspace_size(batch, seq_len))
     return (int)hipErrorInvalidValue;
@@ -582,7 +567,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.tail = retain_tail;
   f.policy = tail_policy;
   f.xattn = pause_xattn;
-  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull;
+  f.L = pause_passes;
+  f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull && pause_passes == 1;
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;

@@ -22,6 +22,7 @@ struct PrefillArgs {
   int policy;                                // its policy: kTailStatic, kTailRolling or kTailSticky
   int xattn;                                 // code <-> code attention in a block (kXattn*; the aligned walks
                                              // serve kXattnFull, the others take the per-element walk)
+  int L;                                     // pause passes of K code rows per block (the aligned walks serve 1)
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,

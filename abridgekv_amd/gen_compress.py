@@ -31,6 +31,12 @@ boundary is a compaction:
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
 
+Code-step inputs follow the model's seed pools (``seg_pool``, ``gated_seg_pool``, ``pool_init`` or
+``code_init_override="segment_mean"``: gen_compress.py:867-898). A model trained with code-row projections
+(``query_residual``, ``code_q_heads``, ``code_kv_heads``) runs its code rows through them here too, as its
+teacher-forced forward does; the reference's generator leaves them to the layer's own weights
+(compress_forward.py:203-207 notes the step "would need the same swap"), which would not reproduce that forward.
+
 Per-head quotas (a layer whose KV heads keep different numbers of codes) use the per-head packed pages of the
 serving sidecar (compresslm_packed_kv.py): one KV-cache group; the code step hides paged code rows ``>= q_h`` per KV
 head (``abkv_paged_prefill_attn_packed``); ``compress`` then copies the block's code rows into one packed page per
@@ -45,13 +51,14 @@ import torch.nn.functional as F
 
 from . import backend as bk
 from . import ops
+from .compress_forward import _QProjCode, _QProjQRes, code_seeds
 from .config import CompressLMConfig, bitrev_offsets
 from .packed_kv import PackedKVLayout, PackedKVSidecar
 from .planner import KVPlanner
 from .processor import CompressLMBlock, CompressLMProcessor
 from .worker import execute_fused_moves
 
-_UNSUPPORTED = ("capture_hidden", "capture_attention", "code_init_override", "raw_tail_override",
+_UNSUPPORTED = ("capture_hidden", "capture_attention", "raw_tail_override",
                 "oracle_full_history", "oracle_history_layers", "preserve_full_history", "retain_full_history_layers",
                 "history_replaces_codes_layers", "capture_content_attention", "content_attention_offsets",
                 "content_head_callback", "evict_policy", "keep_per_block", "evict_seed", "skip_unused_codes")
@@ -76,13 +83,26 @@ def _per_head(head_code_quotas) -> bool:
     return bool((q != q[:, :1]).any())
 
 
+def _project(proj, x, code_step):
+    """A layer projection of the generator's rows x [1, n, d]. Code steps (n = K code rows, slots 0..K-1) take the
+    code rows' own weights (code_q_heads / code_kv_heads) or the query residual of their slot (query_residual), as
+    the teacher-forced forward does at its code rows (compress_forward.py:181-222); content rows and plain
+    projections run the layer's own weights."""
+    if isinstance(proj, _QProjCode):
+        return (proj.code if code_step else proj.orig)(x)
+    if isinstance(proj, _QProjQRes):
+        out = proj.orig(x)
+        return out + proj.qres[: x.size(1)].to(out.dtype) if code_step else out
+    return proj(x)
+
+
 class CompressGen:
     """One sequence's incremental generator. ``clm`` is a :class:`abridgekv_amd.compress_forward.CompressLM` (or any
     object with ``model``, ``C``, ``K``, ``pause``, ``code_positions``); ``max_tokens`` bounds the logical length the
     page pool must hold."""
 
     def __init__(self, clm, device, raw_prompt_len=0, head_code_quotas=None, code_attend_current_content=True,
-                 max_tokens: int = 1 << 15, **options):
+                 code_init_override=None, max_tokens: int = 1 << 15, **options):
         bad = sorted(name for name in options if name not in _UNSUPPORTED)
         if bad:
             raise TypeError(f"unexpected CompressGen options {bad}")
@@ -93,6 +113,11 @@ class CompressGen:
             raise NotImplementedError("code rows always attend the current block's content on the paged path")
         if getattr(clm, "L", 1) != 1:
             raise NotImplementedError("the paged path serves one pause pass (L=1)")
+        if code_init_override not in (None, "segment_mean"):
+            raise ValueError(f"unsupported code_init_override={code_init_override!r}")
+        # code seeds of a code step: the generic seeds or the block's segment means / learned pool (gen_compress.py:
+        # 867-898; "segment_mean" forces the segment means, :194-200)
+        self.code_init_override = code_init_override
         # code <-> code attention of a code step (gen_compress.py:953-959): bidirectional, causal, or none
         self.xattn = getattr(clm, "pause_xattn", "full")
         if self.xattn not in ("full", "causal", "none"):
@@ -227,15 +252,15 @@ class CompressGen:
             md = mds[self.group_of[li]]
             cache = self.caches[self.tensor_of[li]]
             normed = layer.input_layernorm(hidden)
-            q = attn.q_proj(normed).view(1, n, -1, attn.head_dim)
-            k = attn.k_proj(normed).view(1, n, -1, attn.head_dim)
+            q = _project(attn.q_proj, normed, code_step).view(1, n, -1, attn.head_dim)
+            k = _project(attn.k_proj, normed, code_step).view(1, n, -1, attn.head_dim)
             if getattr(attn, "q_norm", None) is not None:
                 q = attn.q_norm(q)
             if getattr(attn, "k_norm", None) is not None:
                 k = attn.k_norm(k)
             q = q[0].to(self.dtype).contiguous()
             k = k[0].to(self.dtype).contiguous()
-            v = attn.v_proj(normed).view(n, -1, attn.head_dim).contiguous()
+            v = _project(attn.v_proj, normed, code_step).view(n, -1, attn.head_dim).contiguous()
             ops.rope_kv_append(q, k, v, logical, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache,
                                block_c=bc, codes_k=bk, max_position=last, code_span=bc - self.T if bc else 0)
             o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
@@ -253,6 +278,11 @@ class CompressGen:
         self.logical_len += n
         self.planner.set_num_computed_tokens(self.rid, self.logical_len)
         return hidden
+
+    def _code_seeds(self):
+        """Inputs [K, d] of the block's code rows (the content embeddings feed the seed pools)."""
+        tok_e = self.inner.embed_tokens(torch.tensor([self._cur_ids], device=self.device))
+        return code_seeds(self.clm, tok_e, self.code_init_override == "segment_mean")[0].to(self.dtype)
 
     # -- reference surface ----------------------------------------------------------------------------------------
     def _remove(self, spans):
@@ -300,7 +330,7 @@ class CompressGen:
             self._window = []
             if rows:
                 self._remove([(rows[0], rows[-1] + 1)])
-        hidden = self.clm.pause[:K].to(self.dtype).view(1, K, self.d)
+        hidden = self._code_seeds().view(1, K, self.d)
         code_start = self.logical_len
         self._forward_rows(hidden, code_step=True)
         block_start = code_start - C

@@ -128,7 +128,10 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
  * Block-masked teacher-forced attention (kernel 3).
  * Replaces the FlexAttention call of CompressLM.forward (abridgekv/compress_forward.py:1134-1230) with the mask of
  * _arith_mask_mod (abridgekv/compress_forward.py:695-727) and the per-query-head code quota (:725-726, :230-236):
- * layout N blocks of [block_c content | codes_k codes], seq_len = N * (block_c + codes_k).
+ * layout N blocks of [block_c content | pause_passes passes of codes_k codes], seq_len = N * (block_c + pause_passes
+ * * codes_k) (L = pause_passes, compress_forward.py:20-31, 566-649: pass l of a block reads its block's content, its
+ * pass l - 1 and its own pass (by pause_xattn); later blocks read only the final pass; the quota counts a code row's
+ * slot within its pass; L > 1 runs the per-element mask).
  * q [batch, seq_len, 32, 128], k/v [batch, seq_len, 8, 128], out [batch, seq_len, 32, 128] bf16 with element strides
  * (dims contiguous); prompt_len [batch] int32 raw-prompt content tokens (NULL: none); head_quota [32] int32 code slots
  * visible per query head (NULL: all); retain_tail = T of a retained tail (retain_tail_kv; 0: none; 0 <= T <
@@ -151,8 +154,9 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             int tail_policy, int pause_xattn, float scale, void* out, long out_stride_b,
-                             long out_stride_s, long out_stride_h, float* lse, abkv_stream_t stream);
+                             int tail_policy, int pause_xattn, int pause_passes, float scale, void* out,
+                             long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
+                             abkv_stream_t stream);
 
 /* Backward of abkv_prefill_masked_attn: the gradients dq [batch, seq_len, 32, 128] and dk, dv [batch, seq_len, 8,
  * 128] (bf16, element strides, dims contiguous; written, not accumulated) of sum(dout * out) under the same mask,
@@ -167,7 +171,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 float scale, void* dq,
+                                 int pause_passes, float scale, void* dq,
                                  long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
                                  long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
                                  long dv_stride_h, void* workspace, size_t workspace_bytes, abkv_stream_t stream);
@@ -280,7 +284,7 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
+                                 int pause_passes, float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
                                  abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------

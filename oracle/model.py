@@ -9,9 +9,18 @@ HuggingFace layer modules of ``model`` in whatever dtype the model is in (float6
 With a retained tail of T rows the mask is ``arith_mask(..., retain_tail=T, tail_policy=...)`` and the bitrev code
 rows spread over the first C - T in-block offsets (compress_forward.py:1059).
 
+With L = ``passes`` pause passes every block is [C content | L passes of K code rows], each pass fed the same seeds
+(compress_forward.py:1179, ``pause_base.repeat(1, 1, L, 1)``), appended positions. ``seeds`` replaces the generic
+seeds by per-block code inputs (:func:`code_seeds`, the pools of compress_forward.py:1147-1178); ``code_proj``
+gives per layer the code rows' own projections (compress_forward.py:181-222): a query residual per code slot
+("qres"), or separate (weight, bias) for q / k / v at the code rows.
+
 Pinning: tests/test_oracle_model.py checks that with one block the content logits equal the model's own causal
-forward (code rows come after the content and are invisible to it), that all-K quotas equal no quotas, and that
-``rope_positions`` matches the closed-form bitrev / appended layout (with and without a code span).
+forward (code rows come after the content and are invisible to it, whatever their seeds, passes and projections),
+that all-K quotas equal no quotas, that zero residuals and copied projections change nothing while a changed code
+projection moves the later blocks' logits only, and that ``rope_positions`` matches the closed-form bitrev /
+appended layout (with and without a code span, with passes); :func:`code_seeds` against explicit segment sums, the
+block-mean fallback, a zero value map and a one-hot pooling.
 """
 from __future__ import annotations
 
@@ -23,23 +32,58 @@ from . import layout as ol
 from . import prefill as op
 
 
-def rope_positions(C, N, K, code_positions, span=None):
-    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071, L=1, no replay tail); bitrev
-    code rows spread over in-block offsets [0, span) (span None: C)."""
-    pos = np.zeros(N * (C + K), dtype=np.int64)
+def rope_positions(C, N, K, code_positions, span=None, passes=1):
+    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071, no replay tail); bitrev
+    code rows (one pass) spread over in-block offsets [0, span) (span None: C); appended rows keep their index."""
+    per = C + passes * K
+    pos = np.zeros(N * per, dtype=np.int64)
     offs = ol.bitrev_code_offsets(K, C, span) if code_positions == "bitrev" else None
     for b in range(N):
-        for j in range(C + K):
+        for j in range(per):
             if code_positions == "bitrev":
-                pos[b * (C + K) + j] = b * C + (j if j < C else int(offs[j - C]))
+                pos[b * per + j] = b * C + (j if j < C else int(offs[j - C]))
             else:
-                pos[b * (C + K) + j] = b * (C + K) + j
+                pos[b * per + j] = b * per + j
     return pos
 
 
-def loss_rows(C, N, K):
+def loss_rows(C, N, K, passes=1):
     """Rows whose hidden state predicts the next content token of the same block (content j = 0..C-2)."""
-    return np.array([b * (C + K) + j for b in range(N) for j in range(C - 1)], dtype=np.int64)
+    per = C + passes * K
+    return np.array([b * per + j for b in range(N) for j in range(C - 1)], dtype=np.int64)
+
+
+def code_seeds(tok_e, pause, K, excluded_tail=0, segment_mean=False, seg_gate=None, pool=None):
+    """Code-row inputs [B, N, K, d] of blocks with content embeddings tok_e [B, N, C, d] (compress_forward.py:
+    1147-1178): ``pause`` [K, d] plus, with ``segment_mean`` (seg_pool), the mean of segment k of the first
+    C - excluded_tail content rows split into K runs of (C - T) // K (the block mean when that is 0), times
+    ``seg_gate`` [K] when given (gated_seg_pool); with ``pool`` = (pool_q [K, d], W_k [d, d], W_v [d, d])
+    (pool_init) the softmax over the content of pool_q[k] . (W_k x) / sqrt(d) weighting W_v x. Loops, float64."""
+    tok_e = torch.as_tensor(tok_e, dtype=torch.float64)
+    pause = torch.as_tensor(pause, dtype=torch.float64)
+    B, N, C, d = tok_e.shape
+    n = C - excluded_tail
+    out = torch.zeros(B, N, K, d, dtype=torch.float64)
+    for b in range(B):
+        for blk in range(N):
+            rows = tok_e[b, blk, :n]
+            for k in range(K):
+                extra = torch.zeros(d, dtype=torch.float64)
+                if segment_mean:
+                    seg = n // K
+                    part = rows[k * seg:(k + 1) * seg] if seg >= 1 else rows
+                    extra = sum(part[i] for i in range(part.shape[0])) / part.shape[0]
+                    if seg_gate is not None:
+                        extra = extra * torch.as_tensor(seg_gate, dtype=torch.float64)[k]
+                elif pool is not None:
+                    pq, wk, wv = (torch.as_tensor(t, dtype=torch.float64) for t in pool)
+                    scores = [pq[k] @ (wk @ rows[i]) / d ** 0.5 for i in range(n)]
+                    top = max(float(x) for x in scores)
+                    w = [torch.exp(x - top) for x in scores]
+                    z = sum(w)
+                    extra = sum((w[i] / z) * (wv @ rows[i]) for i in range(n))
+                out[b, blk, k] = pause[k] + extra
+    return out
 
 
 def _rotate_half(x):
@@ -48,18 +92,25 @@ def _rotate_half(x):
 
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                 layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
+                 layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
+                 seeds=None, code_proj=None):
     """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
-    retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own block's codes."""
+    retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own pass's codes;
+    ``passes``: pause passes per block; ``seeds`` [B, N, K, d] code inputs (None: ``pause``); ``code_proj``: per
+    layer a dict of the code rows' projections ("qres" [passes * K, dq]; "q" / "k" / "v": (weight, bias or None))."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
     tok_e = inner.embed_tokens(content_ids)
     d = tok_e.shape[-1]
-    x = torch.cat([tok_e, pause.to(dt).view(1, 1, K, d).expand(B, N, K, d)], dim=2).reshape(B, N * (C + K), d)
+    L = int(passes)
+    code_in = pause.to(dt).view(1, 1, K, d).expand(B, N, K, d) if seeds is None else seeds.to(dt)
+    x = torch.cat([tok_e] + [code_in] * L, dim=2).reshape(B, N * (C + L * K), d)
     S0 = x.shape[1]
-    pos = torch.from_numpy(rope_positions(C, N, K, code_positions, C - retain_tail)).view(1, -1)
+    code_rows = torch.from_numpy(np.array([r for r in range(S0) if r % (C + L * K) >= C], dtype=np.int64))
+    slots = code_rows % (C + L * K) - C
+    pos = torch.from_numpy(rope_positions(C, N, K, code_positions, C - retain_tail, L)).view(1, -1)
     cos, sin = inner.rotary_emb(x, pos)
     cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
     pl = None if prompt_len is None else np.asarray(prompt_len, dtype=np.int64)
@@ -67,7 +118,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn)     # [B?, H?, S0, S0]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L)  # [B?, H?, S0, S0]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -76,14 +127,25 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
         add = torch.zeros(vis.shape, dtype=dt).masked_fill(~vis, torch.finfo(dt).min)
         normed = layer.input_layernorm(h)
         hs = (B, S0, -1, attn.head_dim)
-        q = attn.q_proj(normed).view(hs)
-        k = attn.k_proj(normed).view(hs)
+        cp = {} if code_proj is None else code_proj[li]
+
+        def project(base, name):
+            out = base(normed)
+            if name in cp:                                      # the code rows' own (weight, bias)
+                w, bias = cp[name]
+                out[:, code_rows] = F.linear(normed[:, code_rows], w.to(dt), None if bias is None else bias.to(dt))
+            if name == "q" and "qres" in cp:                    # plus the residual of the row's slot
+                out[:, code_rows] = out[:, code_rows] + cp["qres"].to(dt)[slots]
+            return out
+
+        q = project(attn.q_proj, "q").view(hs)
+        k = project(attn.k_proj, "k").view(hs)
         if getattr(attn, "q_norm", None) is not None:
             q = attn.q_norm(q)
         if getattr(attn, "k_norm", None) is not None:
             k = attn.k_norm(k)
         q, k = q.transpose(1, 2), k.transpose(1, 2)
-        v = attn.v_proj(normed).view(hs).transpose(1, 2)
+        v = project(attn.v_proj, "v").view(hs).transpose(1, 2)
         q = q * cos + _rotate_half(q) * sin
         k = k * cos + _rotate_half(k) * sin
         rep = q.shape[1] // k.shape[1]
@@ -98,9 +160,10 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
-                      layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
+                      layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
+                      seeds=None, code_proj=None):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
     h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail,
-                     tail_policy, pause_xattn)
-    rows = torch.from_numpy(loss_rows(C, N, K))
+                     tail_policy, pause_xattn, passes, seeds, code_proj)
+    rows = torch.from_numpy(loss_rows(C, N, K, passes))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

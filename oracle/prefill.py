@@ -6,6 +6,11 @@ tokens, optional per-query-head code quota):
   causal & (own-block content | earlier blocks' codes | raw-prompt content)  |  (code query & code key & same block)
   and, with a quota, a code key is visible to head h only if its slot < quota[h].
 
+With L = ``passes`` > 1 pause passes a block is [C content | L passes of K code rows] (per = C + L K,
+compress_forward.py:20-31): pass l >= 1 reads its block's content and its pass l - 1 ("refine"), its own pass by
+``pause_xattn``, and later blocks read only the final pass L ("earlier_final", compress_forward.py:594-600); the
+quota counts a code row's slot within its pass ((within - C) % K, :576-577).
+
 With a retained tail of T rows (retain_tail_kv = T) a block's codes never see its own last T content rows, and the
 last T content rows of an earlier block are visible, by ``tail_policy``
 (abridgekv/compress_forward.py:99-124, _retained_tail_visible):
@@ -43,28 +48,32 @@ TAIL_POLICIES = ("static", "rolling", "sticky")
 XATTN = ("full", "causal", "none")
 
 
-def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
+def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
+               passes=1):
     """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
-    S0 = N * (C + K)
+    S0 = N * (C + passes * K)
     return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail, tail_policy,
-                            pause_xattn)
+                            pause_xattn, passes)
 
 
 def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static",
-                     pause_xattn="full"):
+                     pause_xattn="full", passes=1):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
-    per = C + K
+    L = int(passes)
+    per = C + L * K
     q = np.asarray(rows, dtype=np.int64).reshape(-1, 1)
     kv = np.asarray(cols, dtype=np.int64).reshape(1, -1)
     qb, kb = q // per, kv // per
     qw, kw = q - qb * per, kv - kb * per
     k_content = kw < C
     same_blk = kb == qb
+    kp = np.where(k_content, 0, (kw - C) // K + 1)                         # pause pass of a code key (1..L)
+    qp = np.where(qw < C, 0, (qw - C) // K + 1)
     T = int(retain_tail)
     if tail_policy not in TAIL_POLICIES:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
-    vis = (k_content & same_blk) | ((~k_content) & (kb < qb))
+    vis = (k_content & same_blk) | ((kp == L) & (kb < qb))
     if T and tail_policy == "static":
         vis = vis | (k_content & (kb < qb) & (kw >= C - T))                 # earlier blocks' static tails
     elif T:
@@ -79,13 +88,16 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     vis = (kv <= q) & vis
     if pause_xattn not in XATTN:
         raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
-    if pause_xattn != "none":                                               # code <-> code, same block
-        vis = vis | ((qw >= C) & (~k_content) & same_blk & ((kv <= q) if pause_xattn == "causal" else True))
+    own = (qw >= C) & (~k_content) & same_blk                               # code query, code key, same block
+    if L > 1:
+        vis = vis | (own & (kp == qp - 1))                                  # pass l reads pass l - 1
+    if pause_xattn != "none":                                               # code <-> code, same pass
+        vis = vis | (own & (kp == qp) & ((kv <= q) if pause_xattn == "causal" else True))
     if T:
         vis = vis & ~((qw >= C) & same_blk & k_content & (kw >= C - T))    # codes never see their own tail
     if head_quota is not None:
         hq = np.asarray(head_quota, dtype=np.int64).reshape(-1, 1, 1)
-        quota_ok = k_content | ((kw - C) < hq)                    # [H, 1, S0]
+        quota_ok = k_content | ((kw - C) % K < hq)                # [H, 1, S0]: the slot within its pass
         if vis.ndim == 3:
             vis = vis[:, None] & quota_ok[None]
         else:
@@ -93,21 +105,24 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     return vis
 
 
-def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full"):
+def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
+              passes=1):
     """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
-    per = C + K
+    L = int(passes)
+    per = C + L * K
     S0 = N * per
     idx = np.arange(S0)
     within, blk = idx % per, idx // per
-    role = (within >= C).astype(np.int64)                           # 0 content, 1 code (L = 1)
+    role = np.where(within < C, 0, (within - C) // K + 1)          # 0 content, 1..L pause pass (_roles)
     content_abs = np.where(role == 0, blk * C + within, -1)
-    code_slot = np.where(role == 1, within - C, -1)
+    code_slot = np.where(role > 0, (within - C) % K, -1)
     qr, kr = role.reshape(S0, 1), role.reshape(1, S0)
     qb, kb = blk.reshape(S0, 1), blk.reshape(1, S0)
     causal = idx.reshape(1, S0) <= idx.reshape(S0, 1)
     content_vis = (kr == 0) & (kb == qb)
-    earlier_final = (kr == 1) & (kb < qb)
-    pause_q = qr == 1
+    earlier_final = (kr == L) & (kb < qb)
+    pause_q = qr > 0
+    refine = pause_q & (kr == qr - 1) & (kb == qb)
     samepass = pause_q & (kr == qr) & (kb == qb)
     if pause_xattn not in XATTN:
         raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
@@ -124,7 +139,7 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_pol
         retained = (qr == 0) & (kr == 0) & (kb + 1 == qb) & window & (T > 0)
     else:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
-    base = (causal & (content_vis | earlier_final | retained)) | samepass
+    base = (causal & (content_vis | earlier_final | refine | retained)) | samepass
     if prompt_len is not None:
         pl = np.asarray(prompt_len).reshape(-1, 1, 1)
         prompt_raw = (kr == 0)[None] & (content_abs.reshape(1, 1, S0) < pl) & (content_abs.reshape(1, 1, S0) >= 0)

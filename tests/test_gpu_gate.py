@@ -50,45 +50,81 @@ def _model(seed):
     return transformers.Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
 
 
-@pytest.mark.parametrize("case", range(len(CASES)))
-def test_generator_and_teacher_forced_match_dense_forward(case):
+def _code_options(clm):
+    """The oracle's view of a CompressLM's code-row projections (per layer), float64; None without any."""
+    if not (clm.query_residual or clm.code_q_heads or clm.code_kv_heads):
+        return None
+    out = []
+    for layer in clm.model.model.layers:
+        a, cp = layer.self_attn, {}
+        if clm.query_residual:
+            cp["qres"] = a.q_proj.qres.detach().double().cpu()
+        for name in ("q", "k", "v"):
+            proj = getattr(a, name + "_proj")
+            if hasattr(proj, "code"):
+                cp[name] = (proj.code.weight.detach().double().cpu(),
+                            None if proj.code.bias is None else proj.code.bias.detach().double().cpu())
+        out.append(cp)
+    return out
+
+
+def _seeds(clm, base, ids, segment_mean=False):
+    """The oracle's code inputs of every block, or None for the generic seeds."""
+    if not (segment_mean or clm.seg_pool or clm.gated_seg_pool or clm.pool_init):
+        return None
+    tok = copy.deepcopy(base).double().model.embed_tokens(ids).detach()
+    pool = None
+    if clm.pool_init:
+        pool = tuple(t.detach().double().cpu() for t in (clm.pool_q, clm.pool_k.weight, clm.pool_v.weight))
+    gate = clm.seg_pool_gate.detach().double().cpu() if clm.gated_seg_pool else None
+    return om.code_seeds(tok, clm.pause.detach().double().cpu(), clm.K, clm.code_excluded_tail,
+                         segment_mean or clm.seg_pool or clm.gated_seg_pool, gate, pool)
+
+
+def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="static", xattn="full", options=None,
+          perturb=None, generator=True, teacher_forced=True, gen_options=None):
     from abridgekv_amd.compress_forward import CompressLM
     from abridgekv_amd.gen_compress import CompressGen
 
-    C, N, K, code_positions, prompt, quota, stepwise = CASES[case][:7]
-    T = CASES[case][7] if len(CASES[case]) > 7 else 0
-    policy = CASES[case][8] if len(CASES[case]) > 8 else "static"
-    xattn = CASES[case][9] if len(CASES[case]) > 9 else "full"
     hcq = None if quota is None else [list(q) if isinstance(q, list) else [q] * 8 for q in quota]
     per_head = hcq is not None and any(len(set(row)) > 1 for row in hcq)
     base = _model(case)
     dev = torch.device("cuda")
     tail = dict(retain_tail_kv=T, retain_tail_policy=policy) if T else {}
     clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=code_positions,
-                     head_code_quotas=hcq, pause_xattn=xattn, **tail).eval()
+                     head_code_quotas=hcq, pause_xattn=xattn, **tail, **(options or {})).eval()
+    L = clm.L
     torch.manual_seed(100 + case)
     with torch.no_grad():
         clm.pause.normal_(0, 0.05)
+        if perturb is not None:
+            perturb(clm)
     ids = torch.randint(0, 257, (2, N, C))
     lhq = None if hcq is None else np.repeat(np.asarray(hcq), 4, axis=1)
     pause = clm.pause.detach().cpu()
-
+    seg_mean = (gen_options or {}).get("code_init_override") == "segment_mean"
+    seeds, proj = _seeds(clm, base, ids, seg_mean), _code_options(clm)
+    kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L)
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
-                               lhq, retain_tail=T, tail_policy=policy, pause_xattn=xattn)
+                               lhq, seeds=seeds, code_proj=proj, **kw)
     eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq,
-                                 retain_tail=T, tail_policy=policy, pause_xattn=xattn)
+                                 seeds=seeds, code_proj=proj, **kw)
     tol = 2 * (eager - ref).abs().max().item() + 2e-3
 
     pl = None if prompt is None else torch.tensor(prompt, dtype=torch.int32, device=dev)
-    tf = clm.loss_logits(ids.to(dev), pl).double().cpu()
-    err_tf = (tf - ref).abs().max().item()
-    print(f"case {case}: eager-bf16 {(eager - ref).abs().max().item():.3e}  teacher-forced {err_tf:.3e}")
-    assert err_tf <= tol
+    if teacher_forced:
+        tf = clm.loss_logits(ids.to(dev), pl).double().cpu()
+        err_tf = (tf - ref).abs().max().item()
+        print(f"case {case}: eager-bf16 {(eager - ref).abs().max().item():.3e}  teacher-forced {err_tf:.3e}")
+        assert err_tf <= tol
+    if not generator:
+        return
 
     rows_per_seq = N * (C - 1)
     for bi in range(2):
         p = 0 if prompt is None else prompt[bi]
-        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=hcq, max_tokens=N * (C + K) + 16)
+        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=hcq, max_tokens=N * (C + K) + 16,
+                        **(gen_options or {}))
         got = []
         for blk in range(N):
             toks = ids[bi, blk].tolist()
@@ -113,6 +149,61 @@ def test_generator_and_teacher_forced_match_dense_forward(case):
         err = (torch.cat(got) - ref[bi * rows_per_seq: (bi + 1) * rows_per_seq]).abs().max().item()
         print(f"case {case} seq {bi}: generator {err:.3e}")
         assert err <= tol
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_generator_and_teacher_forced_match_dense_forward(case):
+    C, N, K, code_positions, prompt, quota, stepwise = CASES[case][:7]
+    T = CASES[case][7] if len(CASES[case]) > 7 else 0
+    policy = CASES[case][8] if len(CASES[case]) > 8 else "static"
+    xattn = CASES[case][9] if len(CASES[case]) > 9 else "full"
+    _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T, policy, xattn)
+
+
+def _perturb(**scales):
+    """Move the options' parameters off their no-op initial values (zero gate / value map / residual, copied
+    projections), so that each option changes the logits."""
+    def apply(clm):
+        for name, module in clm.named_modules():
+            if name.endswith("_proj") and hasattr(module, "qres"):
+                module.qres.normal_(0, scales.get("qres", 0.3))
+            if name.endswith("_proj") and hasattr(module, "code"):
+                module.code.weight.add_(torch.randn_like(module.code.weight) * scales.get("code", 0.02))
+        if clm.gated_seg_pool:
+            clm.seg_pool_gate.normal_(0, 1.0)
+        if clm.pool_init:
+            clm.pool_v.weight.normal_(0, 0.05)
+    return apply
+
+
+# the training options beyond the served configuration: (name, C, N, K, code positions, CompressLM options, prompt,
+# quota per layer, whether the paged generator runs it too (it serves one pause pass), generator options)
+OPTION_CASES = [
+    ("two pause passes", 64, 3, 16, "appended", dict(L=2), [40, 100], [16, 4], False, None),
+    ("three passes, causal codes, static tail", 64, 3, 16, "appended",
+     dict(L=3, pause_xattn="causal", retain_tail_kv=12, retain_tail_policy="static"), [70, 0], None, False, None),
+    ("segment-mean seeds, static tail", 64, 3, 16, "bitrev",
+     dict(seg_pool=True, retain_tail_kv=12, retain_tail_policy="static"), [40, 100], [16, 4], True, None),
+    ("gated segment means", 64, 3, 16, "bitrev", dict(gated_seg_pool=True), [40, 0], [16, 8], True, None),
+    ("learned pooled seeds", 64, 3, 16, "bitrev", dict(pool_init=True), [40, 100], None, True, None),
+    ("query residual", 64, 3, 16, "bitrev", dict(query_residual=True), [40, 100], [16, 4], True, None),
+    ("code-row query projection", 64, 3, 16, "bitrev", dict(code_q_heads=True), [70, 0], [16, 4], True, None),
+    ("code-row key/value projections, rolling tail", 64, 3, 16, "bitrev",
+     dict(code_kv_heads=True, retain_tail_kv=12, retain_tail_policy="rolling"), [40, 100], [16, 4], True, None),
+    ("segment-mean override of the generator", 64, 3, 16, "bitrev", {}, [40, 100], [16, 4], True,
+     {"code_init_override": "segment_mean"}),
+]
+
+
+@pytest.mark.parametrize("case", range(len(OPTION_CASES)), ids=[c[0] for c in OPTION_CASES])
+def test_training_options_match_dense_forward(case):
+    name, C, N, K, code_positions, options, prompt, quota, generator, gen_options = OPTION_CASES[case]
+    options = dict(options)
+    xattn = options.pop("pause_xattn", "full")
+    T = options.pop("retain_tail_kv", 0)
+    policy = options.pop("retain_tail_policy", "static")
+    _gate(200 + case, C, N, K, code_positions, prompt, quota, [1], T, policy, xattn, options, _perturb(),
+          generator=generator, teacher_forced=gen_options is None, gen_options=gen_options)
 
 
 def test_forward_losses_match_dense_cross_entropy():
@@ -195,4 +286,67 @@ def test_training_gradients_match_dense_float64(tail, policy):
         e_eager = (eager[n] - ref[n]).abs().max().item()
         scale = ref[n].abs().max().item()
         print(f"{n}: ours {e_ours:.3e}  eager-bf16 {e_eager:.3e}  scale {scale:.3e}")
+        assert e_ours <= 2 * e_eager + 1e-3 * scale, n
+
+
+def test_training_option_gradients_match_dense_float64():
+    """Gradients through two pause passes, a query residual, code-row key/value projections and gated segment-mean
+    seeds (the kernels' per-element walk and the host-side option modules) against the dense float64 model's
+    autograd, as test_training_gradients_match_dense_float64 bounds them."""
+    from abridgekv_amd.compress_forward import CompressLM
+
+    C, N, K, L = 64, 3, 16, 2
+    quota = [[16] * 8, [16, 4, 8, 16, 2, 16, 12, 16]]
+    base = _model(13)
+    dev = torch.device("cuda")
+    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, L=L, head_code_quotas=quota, query_residual=True,
+                     code_kv_heads=True, gated_seg_pool=True).eval()
+    torch.manual_seed(14)
+    with torch.no_grad():
+        clm.pause.normal_(0, 0.05)
+        _perturb()(clm)
+    ids = torch.randint(0, 257, (2, N, C))
+    resp = torch.ones((2, N, C), dtype=torch.long)
+    resp.view(2, -1)[0, :70] = 0
+    loss = clm(ids.to(dev), resp_mask=resp.to(dev), raw_prompt=True)["ce"]
+    loss.backward()
+    layers = clm.model.model.layers
+    got = {"q0": layers[0].self_attn.q_proj.orig.weight.grad, "qres0": layers[0].self_attn.q_proj.qres.grad,
+           "kcode1": layers[1].self_attn.k_proj.code.weight.grad, "vcode0": layers[0].self_attn.v_proj.code.weight.grad,
+           "gate": clm.seg_pool_gate.grad, "pause": clm.pause.grad}
+    got = {n: g.double().cpu() for n, g in got.items()}
+
+    lhq = np.repeat(np.asarray(quota), 4, axis=1)
+    keep = torch.from_numpy(np.array([k for k in range(N * C) if k % C != C - 1]))
+    tgt = ids.view(2, -1)[:, keep + 1].reshape(-1)
+    tm = resp.view(2, -1)[:, keep + 1].reshape(-1).double()
+
+    def dense_grads(dtype):
+        m = copy.deepcopy(base).to(dtype)
+        leaf = lambda t: t.detach().cpu().to(dtype).requires_grad_()
+        pause, gate = leaf(clm.pause), leaf(clm.seg_pool_gate)
+        proj = []
+        for layer in layers:
+            a = layer.self_attn
+            proj.append({"qres": leaf(a.q_proj.qres), "k": (leaf(a.k_proj.code.weight), None),
+                         "v": (leaf(a.v_proj.code.weight), None)})
+        tok = m.model.embed_tokens(ids)
+        seeds = om.code_seeds(tok, pause, K, segment_mean=True, seg_gate=gate)
+        logits = om.dense_loss_logits(m, pause, ids, C, N, K, "appended", [70, 0], lhq, passes=L, seeds=seeds,
+                                      code_proj=proj)
+        ce = torch.nn.functional.cross_entropy(logits.double(), tgt, reduction="none")
+        ((ce * tm).sum() / tm.sum()).backward()
+        params = dict(m.named_parameters())
+        return {"q0": params["model.layers.0.self_attn.q_proj.weight"].grad.double(),
+                "qres0": proj[0]["qres"].grad.double(), "kcode1": proj[1]["k"][0].grad.double(),
+                "vcode0": proj[0]["v"][0].grad.double(), "gate": gate.grad.double(), "pause": pause.grad.double()}
+
+    ref = dense_grads(torch.float64)
+    eager = dense_grads(torch.bfloat16)
+    for n in got:
+        e_ours = (got[n] - ref[n]).abs().max().item()
+        e_eager = (eager[n] - ref[n]).abs().max().item()
+        scale = ref[n].abs().max().item()
+        print(f"{n}: ours {e_ours:.3e}  eager-bf16 {e_eager:.3e}  scale {scale:.3e}")
+        assert scale > 0, n
         assert e_ours <= 2 * e_eager + 1e-3 * scale, n

@@ -14,9 +14,10 @@ def _bf16(x):
     return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static", xattn="full"):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static", xattn="full",
+           passes=1):
     from abridgekv_amd import ops
-    S0 = N * (C + K)
+    S0 = N * (C + passes * K)
     g = torch.Generator().manual_seed(seed)
     q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
@@ -26,14 +27,15 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     hq = None if head_quota is None else torch.tensor(head_quota, dtype=torch.int32, device=dev)
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
-                                          lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn)
+                                          lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
+                                          pause_passes=passes)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn)
+                             tail_policy=policy, pause_xattn=xattn, passes=passes)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -125,6 +127,20 @@ def test_pause_xattn(xattn, shape):
     else:
         quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
         _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=20, xattn=xattn)
+
+
+@pytest.mark.parametrize("passes,shape", [(2, "aligned"), (3, "unaligned"), (2, "unaligned")])
+def test_pause_passes(passes, shape):
+    """L pause passes per block (pass l reads pass l - 1, later blocks the final pass; the per-element walk), with a
+    raw prompt, per-head quotas (a slot within its pass), a tail and non-full xattn."""
+    if shape == "aligned":
+        quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+        _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=21, tail=20, policy="static",
+               passes=passes)
+    else:
+        quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+        _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=22 + passes, tail=3,
+               policy="rolling", xattn="causal" if passes == 3 else "none", passes=passes)
 
 
 def test_strided_hf_layout():

@@ -9,9 +9,9 @@ from oracle import prefill as op
 pytestmark = pytest.mark.gpu
 
 
-def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy="static", xattn="full"):
+def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy="static", xattn="full", passes=1):
     from abridgekv_amd import ops
-    S0 = N * (C + K)
+    S0 = N * (C + passes * K)
     g = torch.Generator().manual_seed(seed)
     q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
@@ -23,16 +23,17 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy=
     qd, kd, vd, gd = (t.to(dev) for t in (q, k, v, dout))
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse,
-                                          retain_tail=tail, tail_policy=policy, pause_xattn=xattn)
+                                          retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
+                                          pause_passes=passes)
     dq, dk, dv = ops.prefill_masked_attention_backward(qd, kd, vd, out, lse, gd, C, K, N, prompt_len=pl,
                                                        head_quota=hq, retain_tail=tail, tail_policy=policy,
-                                                       pause_xattn=xattn)
+                                                       pause_xattn=xattn, pause_passes=passes)
     torch.cuda.synchronize()
     got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn)
+                             tail_policy=policy, pause_xattn=xattn, passes=passes)
         if prompt_len is not None:
             mask = mask[0]
         ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
@@ -99,6 +100,13 @@ def test_pause_xattn(xattn):
     quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
     _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=27, tail=20, policy="sticky",
            xattn=xattn)
+
+
+@pytest.mark.parametrize("passes", [2, 3])
+def test_pause_passes(passes):
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=28 + passes, tail=20,
+           policy="rolling" if passes == 2 else "static", xattn="full" if passes == 2 else "causal", passes=passes)
 
 
 def test_autograd_through_hf_attention_layout():

@@ -12,7 +12,7 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full"):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
@@ -21,16 +21,21 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
     keeps the previous block's whole tail for every content query of the block; rolling lets the i-th content token
     of the block see the previous block's tail rows from the i-th on (one tail row expires per content token).
     pause_xattn (compress_forward.py:313-314, "within-pass code<->code attention"): "full" every code row of the
-    block, "causal" the ones up to the query, "none" no code row of its own block."""
-    per = C + K
+    block, "causal" the ones up to the query, "none" no code row of its own block.
+    L = passes pause passes (compress_forward.py:594-600, "pause^l <- own pause^{l-1}", "earlier blocks' final
+    codes"): a code row of pass l also reads its block's pass l - 1, the xattn rule speaks of its own pass, later
+    blocks read the final pass only, and a quota counts a row's slot within its pass."""
+    per = C + passes * K
     S = N * per
     m = np.zeros((S, S), bool)
     for q in range(S):
         qb, qw = divmod(q, per)
+        q_pass = 0 if qw < C else (qw - C) // K + 1
         for k in range(S):
             kb, kw = divmod(k, per)
             k_content = kw < C
-            vis = (k_content and kb == qb) or ((not k_content) and kb < qb)
+            k_pass = 0 if k_content else (kw - C) // K + 1
+            vis = (k_content and kb == qb) or (k_pass == passes and kb < qb)
             if prompt_len is not None and k_content and kb * C + kw < prompt_len:
                 vis = True
             if tail and policy == "static" and k_content and kb < qb and kw >= C - tail:
@@ -40,11 +45,15 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
                 if row >= 0 and (policy == "sticky" or row >= qw):
                     vis = True
             vis = vis and k <= q
-            if qw >= C and not k_content and kb == qb and (xattn == "full" or (xattn == "causal" and k <= q)):
+            same_pass = q_pass == k_pass
+            if qw >= C and not k_content and kb == qb and same_pass and (xattn == "full" or
+                                                                         (xattn == "causal" and k <= q)):
                 vis = True
+            if qw >= C and not k_content and kb == qb and k_pass == q_pass - 1:
+                vis = True                       # the previous pass of the same block
             if tail and qw >= C and k_content and kb == qb and kw >= C - tail:
                 vis = False                      # a code row does not summarize its own block's tail
-            if quota is not None and not k_content and kw - C >= quota:
+            if quota is not None and not k_content and (kw - C) % K >= quota:
                 vis = False
             m[q, k] = vis
     return m
@@ -114,6 +123,31 @@ def test_pause_xattn_arith_equals_role_equals_brute(C, K, N, T, xattn):
     m = op.arith_mask(C, K, N, pause_xattn=xattn)
     assert m[C, C] == (xattn == "causal") and not m[C, C + 1]          # a code row and the next code row
     assert m[C + 1, C] == (xattn == "causal") and m[per + C, C]        # earlier codes stay visible
+
+
+@pytest.mark.parametrize("C,K,N,L", [(4, 2, 3, 2), (4, 2, 2, 3), (6, 4, 3, 2), (2, 3, 3, 3)])
+def test_pause_passes_arith_equals_role_equals_brute(C, K, N, L):
+    for T, policy, xattn in ((0, "static", "full"), (1, "static", "causal"), (2 if C > 2 else 1, "rolling", "none"),
+                             (1, "sticky", "full")):
+        kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L)
+        a = op.arith_mask(C, K, N, **kw)
+        assert np.array_equal(a, op.role_mask(C, K, N, **kw))
+        assert np.array_equal(a, brute(C, K, N, tail=T, policy=policy, xattn=xattn, passes=L))
+        pl, hq = [0, C + 1], [1, K, 2, K]
+        ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, **kw)
+        assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, **kw))
+        for b, p in enumerate(pl):
+            for h, q in enumerate(hq):
+                assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, tail=T, policy=policy,
+                                                      xattn=xattn, passes=L))
+    per = C + L * K
+    m = op.arith_mask(C, K, N, passes=L)
+    first, final = C, C + (L - 1) * K                        # the first rows of pass 1 and of the final pass
+    assert m[per + C, final] and not m[per + C, first]       # a later block reads the final pass only
+    assert m[C + K, first] and m[C + K, first + K - 1]       # pass 2 reads all of pass 1 (after it)
+    assert not m[C, C + K] and m[C + K, C + K + K - 1]       # pass 1 does not read pass 2; pass 2 reads itself
+    assert L < 3 or not m[C + 2 * K, first]                  # pass 3 does not read pass 1
+    assert np.array_equal(op.arith_mask(C, K, N, passes=1), op.arith_mask(C, K, N))
 
 
 def test_window_tail_spot_checks():
