@@ -38,7 +38,8 @@ ATTN_IMPLEMENTATION = "abridgekv_hip"
 @dataclass(frozen=True)
 class CompressMask:
     """What the kernel needs to evaluate the compression mask (the analogue of the reference's BlockMask):
-    N blocks of [C content | ``passes`` passes of K code rows]; ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
+    N blocks of [C content | ``passes`` passes of K code rows] and ``copy_rows`` copy-region rows (codes_k = 0: causal
+    attention within blocks of C rows); ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
     ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a retained
     tail (0: none) under ``tail_policy`` ("static", "rolling" or "sticky")."""
     block_c: int
@@ -50,6 +51,7 @@ class CompressMask:
     tail_policy: str = "static"
     pause_xattn: str = "full"
     passes: int = 1
+    copy_rows: int = 0
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -68,7 +70,8 @@ class _MaskedPrefill(torch.autograd.Function):
         out, _ = ops.prefill_masked_attention(q, k, v, mask.block_c, mask.codes_k, mask.num_blocks,
                                               prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
                                               retain_tail=mask.retain_tail, tail_policy=mask.tail_policy,
-                                              pause_xattn=mask.pause_xattn, pause_passes=mask.passes)
+                                              pause_xattn=mask.pause_xattn, pause_passes=mask.passes,
+                                              copy_rows=mask.copy_rows)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -83,15 +86,20 @@ class _MaskedPrefill(torch.autograd.Function):
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
                                                            scale=ctx.scale, retain_tail=m.retain_tail,
                                                            tail_policy=m.tail_policy, pause_xattn=m.pause_xattn,
-                                                           pause_passes=m.passes)
+                                                           pause_passes=m.passes, copy_rows=m.copy_rows)
         return dq, dk, dv, None, None, None
 
 
 def masked_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
-    """HuggingFace attention function: query [B, 32, S0, 128], key/value [B, 8, S0, 128] bf16 ->
-    (out [B, S0, 32, 128], None). ``attention_mask`` must be a :class:`CompressMask`."""
+    """HuggingFace attention function: query [B, 32, S, 128], key/value [B, 8, S, 128] bf16 ->
+    (out [B, S, 32, 128], None). ``attention_mask`` is a :class:`CompressMask`, or None for a plain causal forward
+    of the model (the full-context baseline and teacher, compress_forward.py:952-956, 1095-1105), which runs the
+    same kernel without code rows."""
+    if attention_mask is None:
+        attention_mask = CompressMask(query.shape[2], 0, 1)
     if not isinstance(attention_mask, CompressMask):
-        raise TypeError(f"{ATTN_IMPLEMENTATION} attention needs a CompressMask, got {type(attention_mask).__name__}")
+        raise TypeError(f"{ATTN_IMPLEMENTATION} attention needs a CompressMask or None, got "
+                        f"{type(attention_mask).__name__}")
     if dropout:
         raise NotImplementedError("attention dropout is not supported")
     if kwargs.get("sliding_window"):
@@ -151,12 +159,13 @@ class _CodeRows:
     def __init__(self):
         self.rows = self.slots = None
         self.S0 = -1
+        self.lengths = ()           # sequence lengths of the layout: S0, and S0 + 1 + C with the copy region
 
 
 class _QProjQRes(nn.Module):
     """q_proj of one layer plus a learned query residual per code slot, added at the code rows of the compressed
     layout (``query_residual``, compress_forward.py:181-199, 397-413). ``qres`` starts at zero (an exact no-op) and
-    sequences of another length (not the layout's S0) pass through unchanged. Names ``orig`` / ``qres`` as in the
+    sequences of another length than the layout's pass through unchanged. Names ``orig`` / ``qres`` as in the
     reference's state dict."""
 
     def __init__(self, orig: nn.Linear, num_slots: int, code_rows: _CodeRows):
@@ -168,7 +177,7 @@ class _QProjQRes(nn.Module):
     def forward(self, x):
         out = self.orig(x)
         cr = self._code_rows
-        if out.size(1) != cr.S0:
+        if out.size(1) not in cr.lengths:
             return out
         res = self.qres.index_select(0, cr.slots).to(out.dtype)
         return out.index_add(1, cr.rows, res.unsqueeze(0).expand(out.size(0), -1, -1))
@@ -193,7 +202,7 @@ class _QProjCode(nn.Module):
     def forward(self, x):
         out = self.orig(x)
         cr = self._code_rows
-        if out.size(1) != cr.S0:
+        if out.size(1) not in cr.lengths:
             return out
         return out.index_copy(1, cr.rows, self.code(x.index_select(1, cr.rows)).to(out.dtype))
 
@@ -290,6 +299,7 @@ class CompressLM(nn.Module):
         std = getattr(cfg, "initializer_range", 0.02)
         dev = next(base_model.parameters()).device
         self.pause = nn.Parameter(torch.empty(self.K, d, device=dev).normal_(0, std))
+        self.copy_token = nn.Parameter(torch.empty(d, device=dev).normal_(0, std))   # heads the copy region
         # code-seed pools (compress_forward.py:315-343): a per-slot gate on the segment means (zero: the generic
         # seeds), or K learned queries over the content with a zero value map (likewise an exact no-op at first)
         self.pool_init, self.seg_pool, self.gated_seg_pool = bool(pool_init), bool(seg_pool), bool(gated_seg_pool)
@@ -336,6 +346,7 @@ class CompressLM(nn.Module):
         self._code_rows.rows = code
         self._code_rows.slots = code % (C + L * Ka) - C
         self._code_rows.S0 = N * (C + L * Ka)
+        self._code_rows.lengths = (self._code_rows.S0, self._code_rows.S0 + 1 + C)
 
     def set_N(self, N):
         """Rebuild the N-dependent layout for a new block count (compress_forward.py set_N)."""
@@ -373,14 +384,16 @@ class CompressLM(nn.Module):
     def has_head_code_quotas(self) -> bool:
         return self.head_code_quotas.numel() > 0
 
-    def compress_mask(self, batch: int, prompt_len: torch.Tensor | None = None, N: int | None = None) -> CompressMask:
+    def compress_mask(self, batch: int, prompt_len: torch.Tensor | None = None, N: int | None = None,
+                      copy_rows: int = 0) -> CompressMask:
         N = self.N if N is None else int(N)
         if prompt_len is not None:
             prompt_len = prompt_len.to(device=self.pause.device, dtype=torch.int32).contiguous()
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
         return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
-                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn, self.L)
+                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn, self.L,
+                            copy_rows)
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:
@@ -407,48 +420,147 @@ class CompressLM(nn.Module):
         c = ce.new_zeros(nblk).scatter_add_(0, blk, torch.ones_like(ce))
         return ce.mean(), s / c.clamp_min(1.0)
 
-    def hidden_states(self, content_ids, prompt_len=None):
-        """Final-normed hidden states [B, S0, d] of the compressed teacher-forced layout."""
+    def _compressed_forward(self, content_ids, prompt_len=None, with_copy=False, mask=None, need_rep=False):
+        """The decoder over the compressed layout (compress_forward.py:1146-1229): content embeddings, L passes of
+        code seeds per block, then with ``with_copy`` the copy region [copy_token | last block's content]; returns
+        the HF model output (``hidden_states`` with ``need_rep``)."""
         B, N, C = content_ids.shape
         if C != self.C:
             raise ValueError(f"content_ids block size {C} != C={self.C}")
         if N != self.N:
             self.set_N(N)
         K, L = self.K_act, self.L
-        tok_e = self.model.model.embed_tokens(content_ids)
+        emb = self.model.model.embed_tokens
+        tok_e = emb(content_ids)
         d = tok_e.size(-1)
         pause_e = code_seeds(self, tok_e).expand(B, N, K, d)
         if L > 1:
             pause_e = pause_e.repeat(1, 1, L, 1)                      # every pass starts from the same seeds
         x = torch.cat([tok_e, pause_e], dim=2).reshape(B, N * (C + L * K), d)
+        pos = self._pos_ids
+        if with_copy:
+            copy_in = torch.cat([self.copy_token.to(tok_e.dtype).view(1, 1, d).expand(B, 1, d),
+                                 emb(content_ids[:, -1, :])], dim=1)
+            x = torch.cat([x, copy_in], dim=1)
+            start = N * C if self.code_positions == "bitrev" else N * (C + L * self.K)
+            pos = torch.cat([pos, start + torch.arange(1 + C, device=pos.device).view(1, -1)], dim=1)
         if torch.is_autocast_enabled(x.device.type):
             x = x.to(torch.get_autocast_dtype(x.device.type))
-        mask = self.compress_mask(B, prompt_len, N)
-        out = self.model.model(inputs_embeds=x, attention_mask={"full_attention": mask},
-                               position_ids=self._pos_ids, use_cache=False)
-        return out.last_hidden_state
+        if mask is None:
+            mask = self.compress_mask(B, prompt_len, N, copy_rows=1 + C if with_copy else 0)
+        return self.model.model(inputs_embeds=x, attention_mask={"full_attention": mask}, position_ids=pos,
+                                use_cache=False, output_hidden_states=need_rep)
+
+    def hidden_states(self, content_ids, prompt_len=None):
+        """Final-normed hidden states [B, S0, d] of the compressed teacher-forced layout."""
+        return self._compressed_forward(content_ids, prompt_len).last_hidden_state
+
+    def _embed_for_plain_forward(self, ids):
+        """Token embeddings for a plain (uncompressed) forward, in the active autocast dtype (compress_forward.py:
+        940-950)."""
+        e = self.model.model.embed_tokens(ids)
+        if torch.is_autocast_enabled(e.device.type):
+            e = e.to(torch.get_autocast_dtype(e.device.type))
+        return e
+
+    @torch.no_grad()
+    def full_ctx_logits(self, content_ids):
+        """Logits of the plain causal forward over all N * C content tokens (the full-context teacher,
+        compress_forward.py:952-956); the attention runs the masked-prefill kernel without code rows."""
+        B, N, C = content_ids.shape
+        return self.model(inputs_embeds=self._embed_for_plain_forward(content_ids.reshape(B, N * C)),
+                          use_cache=False).logits
+
+    def baseline_loss(self, content_ids, ce_chunk=0, ctx_blocks=0, block_ce=False, resp_mask=None, per_token=False,
+                      include_cross_block=False):
+        """Plain causal LM without compression on the same predict positions (compress_forward.py:1095-1132):
+        sequences of ``ctx_blocks`` contiguous blocks (0: all N, the full-context ceiling; 1: the floor)."""
+        B, N, C = content_ids.shape
+        G = ctx_blocks if ctx_blocks else N
+        if N % G:
+            raise ValueError(f"ctx_blocks={G} must divide N={N}")
+        flat = content_ids.reshape(B * (N // G), G * C)
+        out = self.model.model(inputs_embeds=self._embed_for_plain_forward(flat), use_cache=False).last_hidden_state
+        ar = torch.arange(G * C, device=flat.device)
+        pos = ar[:-1] if include_cross_block else ar[(ar % C) != (C - 1)]
+        hid = out[:, pos, :].reshape(-1, out.size(-1))
+        tgt = flat[:, pos + 1].reshape(-1)
+        if block_ce:
+            m, bc = self._perblock_ce(hid, tgt, pos // C, G, flat.size(0))
+            return {"ce": m, "block_ce": bc}
+        if resp_mask is not None:
+            rm = resp_mask.reshape(flat.shape)[:, pos + 1].reshape(-1).float()
+            if per_token:
+                ce = self._per_token_lm_ce(hid, tgt, ce_chunk)
+                reps = flat.size(0)
+                if include_cross_block:
+                    target = pos + 1
+                    return {"ce_pt": ce, "tmask": rm, "blk": (target // C).repeat(reps),
+                            "pos": (target % C).repeat(reps), "supervised": ((pos % C) != C - 1).repeat(reps)}
+                return {"ce_pt": ce, "tmask": rm, "blk": (pos // C).repeat(reps), "pos": (pos % C).repeat(reps)}
+            return {"ce": self._masked_lm_ce(hid, tgt, rm, ce_chunk)}
+        return {"ce": self._lm_ce(hid, tgt, ce_chunk)}
+
+    def _masked_ce_kl_chunked(self, hid, tgt, mask, teacher_rows, teacher_head, temp, chunk):
+        """Response-masked CE and KL(teacher || student) at temperature ``temp`` from a frozen teacher's final
+        hidden rows, chunked over rows with activation checkpointing (compress_forward.py:978-1020)."""
+        import torch.utils.checkpoint as ckpt
+        if teacher_rows.shape[0] != hid.shape[0]:
+            raise ValueError(f"teacher_rows {tuple(teacher_rows.shape)} misaligned with student rows "
+                             f"{tuple(hid.shape)}")
+        den = mask.sum().clamp_min(1.0)
+        T = float(temp)
+        lm_head = self.model.lm_head
+
+        def part(h, t, m, tr):
+            logits = lm_head(h).float()
+            ce = F.cross_entropy(logits, t, reduction="none")
+            with torch.no_grad():
+                tl = teacher_head(tr).float()
+                tp, tlp = F.softmax(tl / T, -1), F.log_softmax(tl / T, -1)
+            kl = (tp * (tlp - F.log_softmax(logits / T, -1))).sum(-1) * (T * T)
+            return (ce * m).sum(), (kl * m).sum()
+
+        step = hid.size(0) if chunk <= 0 else chunk
+        ce_tot = hid.new_zeros((), dtype=torch.float32)
+        kl_tot = hid.new_zeros((), dtype=torch.float32)
+        for i in range(0, hid.size(0), step):
+            sl = slice(i, i + step)
+            args = (hid[sl], tgt[sl], mask[sl], teacher_rows[sl])
+            c, k = ckpt.checkpoint(part, *args, use_reentrant=False) if torch.is_grad_enabled() else part(*args)
+            ce_tot, kl_tot = ce_tot + c, kl_tot + k
+        return ce_tot / den, kl_tot / den
 
     def forward(self, content_ids, distill_lambda=0.0, copy_lambda=0.0, distill_temp=1.0, ce_chunk=0, baseline=False,
                 ctx_blocks=0, teacher_logits=None, teacher_hidden=None, block_ce=False, resp_mask=None,
                 raw_prompt=False, blockmask=None, per_token=False, include_cross_block=False,
                 boundary_recovery_width=0, boundary_recovery_weight=1.0, teacher_rows=None, teacher_head=None):
-        """Losses of the compressed teacher-forced forward, same signature and return dicts as
-        compress_forward.py:1134-1230 for the supported arguments (the full-context baseline, distillation, copy
-        and representation losses and external block masks raise NotImplementedError)."""
-        unsupported = {"baseline": bool(baseline), "ctx_blocks": bool(ctx_blocks), "distill_lambda": distill_lambda > 0,
-                       "copy_lambda": copy_lambda > 0, "teacher_logits": teacher_logits is not None,
-                       "teacher_hidden": teacher_hidden is not None, "blockmask": blockmask is not None,
-                       "teacher_rows": teacher_rows is not None, "teacher_head": teacher_head is not None}
-        used = sorted(name for name, on in unsupported.items() if on)
-        if used:
-            raise NotImplementedError(f"CompressLM.forward arguments {used} are not supported by the native forward")
+        """Losses of the compressed teacher-forced forward, same signature, control flow and return dicts as
+        compress_forward.py:1134-1315: the full-context baseline, CE (masked by ``resp_mask``, per block, per
+        token), self- or teacher distillation (KL at ``distill_temp``), the chunked frozen-teacher KD
+        (``teacher_rows`` / ``teacher_head``), the copy loss (``copy_lambda``: the copy region reproduces the last
+        block from its codes) and the representation loss (``teacher_hidden``). ``blockmask``: a prebuilt
+        :class:`CompressMask` (the analogue of the reference's prebuilt BlockMask)."""
+        if baseline:
+            return self.baseline_loss(content_ids, ce_chunk, ctx_blocks, block_ce=block_ce, resp_mask=resp_mask,
+                                      per_token=per_token, include_cross_block=include_cross_block)
         B, N, C = content_ids.shape
         dev = content_ids.device
-        prompt_len = None
-        if raw_prompt and resp_mask is not None:
+        with_copy = copy_lambda > 0
+        need_rep = teacher_hidden is not None
+        prompt_len, mask = None, None
+        if blockmask is not None:
+            if self.has_head_code_quotas:
+                raise ValueError("an external blockmask cannot encode layer/head quotas; "
+                                 "omit blockmask when head_code_quotas are enabled")
+            if not isinstance(blockmask, CompressMask):
+                raise TypeError(f"blockmask must be a CompressMask, got {type(blockmask).__name__}")
+            mask = blockmask
+        elif raw_prompt and resp_mask is not None and not with_copy:
             rmf = resp_mask.reshape(B, N * C)
             prompt_len = (rmf.cumsum(1) == 0).sum(1).to(torch.int32)      # leading zeros = prompt length
-        out = self.hidden_states(content_ids, prompt_len)
+        mo = self._compressed_forward(content_ids, prompt_len, with_copy, mask, need_rep)
+        out = mo.last_hidden_state
         d = out.size(-1)
         S0 = N * (C + self.L * self.K_act)
         if include_cross_block:
@@ -461,21 +573,59 @@ class CompressLM(nn.Module):
         if block_ce:
             m, bc = self._perblock_ce(hid, tgt, pred_flat // C, N, B)
             return {"ce": m, "block_ce": bc}
-        if resp_mask is None:
-            return {"ce": self._lm_ce(hid, tgt, ce_chunk)}
-        tmask = resp_mask.reshape(B, N * C)[:, pred_flat + 1].reshape(-1).float()
-        target = pred_flat + 1
-        if per_token and include_cross_block:
-            return {"ce_pt": self._per_token_lm_ce(hid, tgt, ce_chunk), "tmask": tmask,
-                    "blk": (target // C).repeat(B), "pos": (target % C).repeat(B),
-                    "supervised": ((pred_flat % C) != C - 1).repeat(B)}
-        if boundary_recovery_width > 0 and boundary_recovery_weight != 1.0:
-            recovery = ((target // C > 0) & (target % C >= 1) & (target % C <= boundary_recovery_width)).repeat(B)
-            tmask = tmask * torch.where(recovery, tmask.new_tensor(boundary_recovery_weight), tmask.new_tensor(1.0))
-        if not per_token:
-            return {"ce": self._masked_lm_ce(hid, tgt, tmask, ce_chunk)}
-        return {"ce_pt": self._per_token_lm_ce(hid, tgt, 0), "tmask": tmask, "blk": self.predict_block.repeat(B),
-                "pos": (self.predict_flat % C).repeat(B)}
+        if resp_mask is not None:
+            tmask = resp_mask.reshape(B, N * C)[:, pred_flat + 1].reshape(-1).float()
+            target = pred_flat + 1
+            if per_token and include_cross_block:
+                return {"ce_pt": self._per_token_lm_ce(hid, tgt, ce_chunk), "tmask": tmask,
+                        "blk": (target // C).repeat(B), "pos": (target % C).repeat(B),
+                        "supervised": ((pred_flat % C) != C - 1).repeat(B)}
+            if boundary_recovery_width > 0 and boundary_recovery_weight != 1.0:
+                recovery = ((target // C > 0) & (target % C >= 1) & (target % C <= boundary_recovery_width)).repeat(B)
+                tmask = tmask * torch.where(recovery, tmask.new_tensor(boundary_recovery_weight),
+                                            tmask.new_tensor(1.0))
+            if teacher_rows is not None and not per_token:
+                ce, kl = self._masked_ce_kl_chunked(hid, tgt, tmask, teacher_rows, teacher_head, distill_temp, ce_chunk)
+                return {"ce": ce, "distill": kl}
+            if not per_token and teacher_logits is None:
+                return {"ce": self._masked_lm_ce(hid, tgt, tmask, ce_chunk)}
+            logits = self.model.lm_head(hid).float()
+            ce = F.cross_entropy(logits, tgt, reduction="none")
+            if per_token:
+                return {"ce_pt": ce, "tmask": tmask, "blk": self.predict_block.repeat(B),
+                        "pos": (self.predict_flat % C).repeat(B)}
+            den = tmask.sum().clamp_min(1.0)
+            outd = {"ce": (ce * tmask).sum() / den}
+            if teacher_logits is not None:
+                T = distill_temp
+                kl = F.kl_div(F.log_softmax(logits / T, -1), F.softmax(teacher_logits.float() / T, -1),
+                              reduction="none").sum(-1) * (T * T)
+                outd["distill"] = (kl * tmask).sum() / den
+            return outd
+        if distill_lambda > 0:
+            logits = self.model.lm_head(hid).float()
+            losses = {"ce": F.cross_entropy(logits, tgt)}
+            if teacher_logits is None:                                     # self-teacher: the full-context forward
+                with torch.no_grad():
+                    teacher_logits = self.full_ctx_logits(content_ids)[:, pred_flat, :].reshape(-1, logits.size(-1))
+            T = distill_temp
+            losses["distill"] = F.kl_div(F.log_softmax(logits / T, -1), F.softmax(teacher_logits.float() / T, -1),
+                                         reduction="batchmean") * (T * T)
+        else:
+            losses = {"ce": self._lm_ce(hid, tgt, ce_chunk)}
+        if with_copy:
+            losses["copy"] = self._lm_ce(out[:, S0:S0 + C, :].reshape(-1, d), content_ids[:, -1, :].reshape(-1),
+                                         ce_chunk)
+        if need_rep:
+            rep = out.new_zeros((), dtype=torch.float32)
+            for li in range(teacher_hidden.shape[0]):
+                hs = mo.hidden_states[li + 1][:, self.content_pos, :].float()
+                ht = teacher_hidden[li].float()
+                hs = hs / hs.pow(2).mean(-1, keepdim=True).clamp_min(1e-12).sqrt()
+                ht = ht / ht.pow(2).mean(-1, keepdim=True).clamp_min(1e-12).sqrt()
+                rep = rep + (hs - ht).pow(2).mean()
+            losses["rep"] = rep / teacher_hidden.shape[0]
+        return losses
 
     @torch.no_grad()
     def loss_logits(self, content_ids, prompt_len=None):

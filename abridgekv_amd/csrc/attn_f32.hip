@@ -45,6 +45,7 @@ struct F32Args {
   int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky)
   int pause_xattn;             // code <-> code attention in a block (kXattn*)
   int pause_passes;            // pause passes of codes_k rows per block
+  int copy_rows;               // copy-region rows at the end of the seq_len rows
   int num_tokens;
   float scale;
   float* out;
@@ -67,7 +68,7 @@ __device__ __forceinline__ void wave_sync() {
 //   shows this row) | (code q & code k & same block), a code query never sees its own block's last T content rows,
 //   and a code key of slot s is visible to a head only if s < quota.
 __device__ __forceinline__ bool f32_visible(const F32Args& a, int qr, int kr, int plen, int quota) {
-  return compress_visible(qr, kr, a.seq_len, a.block_c, a.codes_k, a.pause_passes,
+  return compress_visible(qr, kr, a.seq_len, a.copy_rows, a.block_c, a.codes_k, a.pause_passes,
                           a.block_c + a.pause_passes * a.codes_k, plen, quota, a.retain_tail, a.tail_policy,
                           a.pause_xattn);
 }
@@ -89,7 +90,9 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
     b = t / a.seq_len;
     qrow = t - b * a.seq_len;
     const int per = a.block_c + a.pause_passes * a.codes_k;
-    n_keys = min(a.seq_len, (qrow / per + 1) * per);   // nothing after the query's own block is visible
+    const int s0 = a.seq_len - a.copy_rows;
+    // nothing after the query's own block is visible; a copy row sees up to itself
+    n_keys = qrow >= s0 ? qrow + 1 : min(s0, (qrow / per + 1) * per);
     plen = a.prompt_len ? a.prompt_len[b] : 0;
     if (a.head_quota)
 #pragma unroll
@@ -301,13 +304,14 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 int pause_passes, float scale, float* out, long o_sb, long o_ss, long o_sh, float* lse,
+                                 int pause_passes, int copy_rows, float scale, float* out, long o_sb, long o_ss,
+                                 long o_sh, float* lse,
                                  hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
-  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k <= 0 ||
-      num_blocks <= 0 || pause_passes <= 0 ||
-      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) || retain_tail < 0 ||
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k < 0 ||
+      num_blocks <= 0 || pause_passes <= 0 || copy_rows < 0 || (codes_k == 0 && (pause_passes != 1 || copy_rows)) ||
+      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) + copy_rows || retain_tail < 0 ||
       retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
       pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
@@ -334,6 +338,7 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
   a.tail_policy = tail_policy;
   a.pause_xattn = pause_xattn;
   a.pause_passes = pause_passes;
+  a.copy_rows = copy_rows;
   a.num_tokens = batch * seq_len;
   a.scale = scale;
   a.out = out;

@@ -45,10 +45,20 @@ __device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb
 //   causal & (own-block content | earlier blocks' final-pass codes | raw-prompt content (< plen) | retained tail)
 //   | a code row's own block's previous pass | its own pass by xattn,
 // less a code row's own block's last `tail` content rows, and less a code key whose slot (its index within its pass)
-// is >= quota. With L = 1 (a compile-time constant at most call sites) the pass arithmetic folds away.
-__device__ __forceinline__ bool compress_visible(int q, int kv, int S0, int C, int K, int L, int per, int plen,
-                                                 int quota, int tail, int policy, int xattn) {
-  if (kv >= S0 || q >= S0) return false;
+// is >= quota. The last `copy` of the S rows are the copy region (copy_lambda, :631-633): they see the last block's
+// final pass (slot < quota) and the copy rows up to themselves, and no other row sees them. K = 0 (no codes) is
+// block-local causal attention. With L = 1 and copy = 0 (compile-time constants at most call sites) the pass and
+// copy arithmetic folds away.
+__device__ __forceinline__ bool compress_visible(int q, int kv, int S, int copy, int C, int K, int L, int per,
+                                                 int plen, int quota, int tail, int policy, int xattn) {
+  if (kv >= S || q >= S) return false;
+  const int S0 = S - copy;                                  // rows of the compressed layout
+  if (copy > 0 && q >= S0) {
+    if (kv >= S0) return kv <= q;
+    const int lo = S0 - per + C + (L - 1) * K;              // the last block's final pass
+    return kv >= lo && kv - lo < min(K, quota);
+  }
+  if (copy > 0 && kv >= S0) return false;
   const int qb = q / per, kb = kv / per;
   const int qw = q - qb * per, kw = kv - kb * per;
   const bool kc = kw < C, qc = qw < C;

@@ -23,6 +23,7 @@ struct PrefillArgs {
   int xattn;                                 // code <-> code attention in a block (kXattn*; the aligned walks
                                              // serve kXattnFull, the others take the per-element walk)
   int L;                                     // pause passes of K code rows per block (the aligned walks serve 1)
+  int copy;                                  // copy-region rows after the N blocks (S0 counts them; aligned: 0)
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,

@@ -93,12 +93,14 @@ def _rotate_half(x):
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                  layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
-                 seeds=None, code_proj=None):
-    """Final-normed hidden states [B, S0, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
+                 seeds=None, code_proj=None, copy_token=None, output_layers=False):
+    """Final-normed hidden states [B, S, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
     retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own pass's codes;
     ``passes``: pause passes per block; ``seeds`` [B, N, K, d] code inputs (None: ``pause``); ``code_proj``: per
-    layer a dict of the code rows' projections ("qres" [passes * K, dq]; "q" / "k" / "v": (weight, bias or None))."""
+    layer a dict of the code rows' projections ("qres" [passes * K, dq]; "q" / "k" / "v": (weight, bias or None));
+    ``copy_token`` [d]: append the copy region [copy_token | last block's content] (compress_forward.py:1185-1189),
+    at positions after the layout's; ``output_layers``: also return every layer's output hidden states."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
@@ -111,14 +113,22 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     code_rows = torch.from_numpy(np.array([r for r in range(S0) if r % (C + L * K) >= C], dtype=np.int64))
     slots = code_rows % (C + L * K) - C
     pos = torch.from_numpy(rope_positions(C, N, K, code_positions, C - retain_tail, L)).view(1, -1)
+    copy = 0
+    if copy_token is not None:
+        copy = 1 + C
+        x = torch.cat([x, copy_token.to(dt).view(1, 1, d).expand(B, 1, d), tok_e[:, -1]], dim=1)
+        start = N * C if code_positions == "bitrev" else S0
+        pos = torch.cat([pos, start + torch.arange(copy).view(1, -1)], dim=1)
+        S0 = x.shape[1]
     cos, sin = inner.rotary_emb(x, pos)
     cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
     pl = None if prompt_len is None else np.asarray(prompt_len, dtype=np.int64)
     h = x
+    layers_out = []
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L)  # [B?, H?, S0, S0]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L, copy)  # [B?, H?, S, S]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -156,7 +166,8 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
         o = torch.matmul(w, vr).transpose(1, 2).reshape(B, S0, -1)
         h = h + attn.o_proj(o)
         h = h + layer.mlp(layer.post_attention_layernorm(h))
-    return inner.norm(h)
+        layers_out.append(h)
+    return (inner.norm(h), layers_out) if output_layers else inner.norm(h)
 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,

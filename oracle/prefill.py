@@ -11,6 +11,10 @@ compress_forward.py:20-31): pass l >= 1 reads its block's content and its pass l
 ``pause_xattn``, and later blocks read only the final pass L ("earlier_final", compress_forward.py:594-600); the
 quota counts a code row's slot within its pass ((within - C) % K, :576-577).
 
+``copy_rows`` rows after the N blocks form the copy region (copy_lambda, compress_forward.py:631-633): a copy row
+sees the last block's final-pass codes (slot < quota) and the copy rows up to itself; no other row sees it. K = 0
+(no codes) leaves causal attention within blocks of C rows (the plain forward).
+
 With a retained tail of T rows (retain_tail_kv = T) a block's codes never see its own last T content rows, and the
 last T content rows of an earlier block are visible, by ``tail_policy``
 (abridgekv/compress_forward.py:99-124, _retained_tail_visible):
@@ -49,15 +53,16 @@ XATTN = ("full", "causal", "none")
 
 
 def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-               passes=1):
-    """Boolean visibility [B?, H?, S0, S0] (leading dims only when prompt_len / head_quota are given)."""
-    S0 = N * (C + passes * K)
-    return arith_mask_block(C, K, N, np.arange(S0), np.arange(S0), prompt_len, head_quota, retain_tail, tail_policy,
-                            pause_xattn, passes)
+               passes=1, copy_rows=0):
+    """Boolean visibility [B?, H?, S, S] (leading dims only when prompt_len / head_quota are given),
+    S = N * (C + passes * K) + copy_rows."""
+    S = N * (C + passes * K) + copy_rows
+    return arith_mask_block(C, K, N, np.arange(S), np.arange(S), prompt_len, head_quota, retain_tail, tail_policy,
+                            pause_xattn, passes, copy_rows)
 
 
 def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static",
-                     pause_xattn="full", passes=1):
+                     pause_xattn="full", passes=1, copy_rows=0):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
     L = int(passes)
@@ -68,8 +73,9 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     qw, kw = q - qb * per, kv - kb * per
     k_content = kw < C
     same_blk = kb == qb
-    kp = np.where(k_content, 0, (kw - C) // K + 1)                         # pause pass of a code key (1..L)
-    qp = np.where(qw < C, 0, (qw - C) // K + 1)
+    Kd = max(K, 1)
+    kp = np.where(k_content, 0, (kw - C) // Kd + 1)                        # pause pass of a code key (1..L)
+    qp = np.where(qw < C, 0, (qw - C) // Kd + 1)
     T = int(retain_tail)
     if tail_policy not in TAIL_POLICIES:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
@@ -97,25 +103,34 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
         vis = vis & ~((qw >= C) & same_blk & k_content & (kw >= C - T))    # codes never see their own tail
     if head_quota is not None:
         hq = np.asarray(head_quota, dtype=np.int64).reshape(-1, 1, 1)
-        quota_ok = k_content | ((kw - C) % K < hq)                # [H, 1, S0]: the slot within its pass
+        quota_ok = k_content | ((kw - C) % Kd < hq)               # [H, 1, S0]: the slot within its pass
         if vis.ndim == 3:
             vis = vis[:, None] & quota_ok[None]
         else:
             vis = vis[None] & quota_ok
+    if copy_rows:
+        S0 = N * per
+        q_copy, k_copy = q >= S0, kv >= S0
+        lo = S0 - per + C + (L - 1) * K                                     # the last block's final pass
+        final = (kv >= lo) & (kv < lo + K)
+        if head_quota is not None:
+            final = final[None] & (kv - lo < hq)                            # [H, R, S]
+        vis = np.where(q_copy, (k_copy & (kv <= q)) | final, vis & ~k_copy)
     return vis
 
 
 def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-              passes=1):
-    """Same visibility from per-position role / block / content-position tables (the _dense_mask form)."""
+              passes=1, copy_rows=0):
+    """Same visibility from per-position role / block / content-position tables (the _dense_mask form); the copy
+    region as _mask_mod's ``copy`` term (compress_forward.py:627-633)."""
     L = int(passes)
     per = C + L * K
     S0 = N * per
     idx = np.arange(S0)
     within, blk = idx % per, idx // per
-    role = np.where(within < C, 0, (within - C) // K + 1)          # 0 content, 1..L pause pass (_roles)
+    role = np.where(within < C, 0, (within - C) // max(K, 1) + 1)  # 0 content, 1..L pause pass (_roles)
     content_abs = np.where(role == 0, blk * C + within, -1)
-    code_slot = np.where(role > 0, (within - C) % K, -1)
+    code_slot = np.where(role > 0, (within - C) % max(K, 1), -1)
     qr, kr = role.reshape(S0, 1), role.reshape(1, S0)
     qb, kb = blk.reshape(S0, 1), blk.reshape(1, S0)
     causal = idx.reshape(1, S0) <= idx.reshape(S0, 1)
@@ -155,6 +170,23 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_pol
             base = base[:, None] & allowed[None]
         else:
             base = base[None] & allowed
+    if copy_rows:
+        S = S0 + copy_rows
+        full = np.zeros(base.shape[:-2] + (S, S), dtype=bool)
+        full[..., :S0, :S0] = base
+        q, kv = np.arange(S).reshape(S, 1), np.arange(S).reshape(1, S)
+        in_cq, in_ck = q >= S0, kv >= S0
+        last_final_lo = (N - 1) * per + C + (L - 1) * K
+        code_kv = (kv >= last_final_lo) & (kv < last_final_lo + K) & ~in_ck
+        copy = in_cq & (code_kv | (in_ck & (kv <= q)))
+        if head_quota is not None:
+            slot = np.full(S, -1)
+            slot[:S0] = code_slot
+            copy = copy[None] & ((kv >= S0) | (slot.reshape(1, 1, S) < 0) | (slot.reshape(1, 1, S) < hq))
+            if full.ndim == 4:
+                copy = copy[None]
+        full = full | copy
+        base = full
     return base
 
 

@@ -10,6 +10,7 @@ import copy
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import model as om
 
@@ -350,3 +351,106 @@ def test_training_option_gradients_match_dense_float64():
         print(f"{n}: ours {e_ours:.3e}  eager-bf16 {e_eager:.3e}  scale {scale:.3e}")
         assert scale > 0, n
         assert e_ours <= 2 * e_eager + 1e-3 * scale, n
+
+
+def _dense_plain_hidden(model, ids_flat):
+    """Final-normed hidden states of the model's plain causal forward (eager attention), any dtype."""
+    m = copy.deepcopy(model)
+    m.config._attn_implementation = "eager"
+    with torch.no_grad():
+        return m.model(input_ids=ids_flat, use_cache=False).last_hidden_state
+
+
+@pytest.mark.parametrize("L", [1, 2])
+def test_forward_training_losses_match_dense(L):
+    """CompressLM.forward's training losses beyond the plain CE against the dense model: the reference's own
+    self-test call (distill_lambda=1, copy_lambda=1, distill_temp=2; compress_forward.py:1320-1329) with one and two
+    passes, the full-context baseline (ceiling and floor), response-masked distillation from teacher logits, the
+    chunked frozen-teacher KD, the representation loss and a prebuilt mask. Each loss within 2x the float64 error of
+    the same dense computation in bf16, plus 1e-3."""
+    from abridgekv_amd.compress_forward import CompressLM
+
+    C, N, K, B = 64, 3, 16, 2
+    base = _model(40 + L)
+    dev = torch.device("cuda")
+    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, L=L).eval()
+    torch.manual_seed(41)
+    with torch.no_grad():
+        clm.pause.normal_(0, 0.05)
+        clm.copy_token.normal_(0, 0.05)
+    ids = torch.randint(0, 257, (B, N, C))
+    resp = torch.ones((B, N, C), dtype=torch.long)
+    resp.view(B, -1)[0, :70] = 0
+    pf = torch.from_numpy(np.array([k for k in range(N * C) if k % C != C - 1]))
+    tgt = ids.view(B, -1)[:, pf + 1].reshape(-1)
+    tm = resp.view(B, -1)[:, pf + 1].reshape(-1).double()
+    teacher_hidden = torch.randn(2, B, N * C, 256) * 0.5
+    g = torch.Generator().manual_seed(42)
+    teacher_logits = torch.randn(B * (N * C - N), 257, generator=g, dtype=torch.float64)
+    teacher_head = torch.nn.Linear(256, 257, bias=False).double()
+    teacher_rows = torch.randn(B * (N * C - N), 256, generator=g, dtype=torch.float64)
+
+    def dense(dtype):
+        m = copy.deepcopy(base).to(dtype)
+        pause, ctok = clm.pause.detach().cpu().to(dtype), clm.copy_token.detach().cpu().to(dtype)
+        with torch.no_grad():
+            h, layers = om.dense_hidden(m, pause, ids, C, N, K, passes=L, copy_token=ctok, output_layers=True)
+            S0 = N * (C + L * K)
+            logits = m.lm_head(h[:, om.loss_rows(C, N, K, L)].reshape(-1, 256)).double()
+            full = m.lm_head(_dense_plain_hidden(m, ids.view(B, N * C))).double()[:, pf].reshape(-1, 257)
+            out = {"ce": F.cross_entropy(logits, tgt),
+                   "distill": F.kl_div(F.log_softmax(logits / 2, -1), F.softmax(full / 2, -1),
+                                       reduction="batchmean") * 4,
+                   "copy": F.cross_entropy(m.lm_head(h[:, S0:S0 + C]).double().reshape(-1, 257),
+                                           ids[:, -1].reshape(-1))}
+            ce_rows = F.cross_entropy(logits, tgt, reduction="none")
+            kl_rows = F.kl_div(F.log_softmax(logits, -1), F.softmax(teacher_logits, -1), reduction="none").sum(-1)
+            out["masked_ce"] = (ce_rows * tm).sum() / tm.sum()
+            out["masked_distill"] = (kl_rows * tm).sum() / tm.sum()
+            tl = teacher_head(teacher_rows)
+            kd = (F.softmax(tl, -1) * (F.log_softmax(tl, -1) - F.log_softmax(logits, -1))).sum(-1)
+            out["kd"] = (kd * tm).sum() / tm.sum()
+            # representation loss on the content rows: layer 1's output and the final (normed) hidden state
+            content = torch.from_numpy(np.array([r for r in range(S0) if r % (C + L * K) < C]))
+            rep = 0.0
+            for li, hs in enumerate([layers[0], h]):
+                hs = hs[:, content].double()
+                ht = teacher_hidden[li].double()
+                hs = hs / hs.pow(2).mean(-1, keepdim=True).clamp_min(1e-12).sqrt()
+                ht = ht / ht.pow(2).mean(-1, keepdim=True).clamp_min(1e-12).sqrt()
+                rep = rep + (hs - ht).pow(2).mean()
+            out["rep"] = rep / 2
+            for G, name in ((N, "ceiling"), (1, "floor")):
+                flat = ids.reshape(B * (N // G), G * C)
+                ar = torch.arange(G * C)
+                pos = ar[(ar % C) != C - 1]
+                hb = _dense_plain_hidden(m, flat)[:, pos].reshape(-1, 256)
+                out[name] = F.cross_entropy(m.lm_head(hb).double(), flat[:, pos + 1].reshape(-1))
+        return out
+
+    ref, eager = dense(torch.float64), dense(torch.bfloat16)
+    idd = ids.to(dev)
+    with torch.no_grad():
+        main = clm(idd, distill_lambda=1.0, copy_lambda=1.0, distill_temp=2.0)
+        masked = clm(idd, resp_mask=resp.to(dev), teacher_logits=teacher_logits.to(dev))
+        kd = clm(idd, resp_mask=resp.to(dev), teacher_rows=teacher_rows.to(dev).float(),
+                 teacher_head=copy.deepcopy(teacher_head).to(dev).float(), ce_chunk=50)
+        rep = clm(idd, teacher_hidden=teacher_hidden.to(dev))
+        ceiling = clm(idd, baseline=True)
+        floor = clm(idd, baseline=True, ctx_blocks=1)
+        prebuilt = clm(idd, blockmask=clm.compress_mask(B))
+    got = {"ce": main["ce"], "distill": main["distill"], "copy": main["copy"], "masked_ce": masked["ce"],
+           "masked_distill": masked["distill"], "kd": kd["distill"], "rep": rep["rep"], "ceiling": ceiling["ce"],
+           "floor": floor["ce"]}
+    for name, value in got.items():
+        e_ours, e_eager = abs(float(value) - float(ref[name])), abs(float(eager[name]) - float(ref[name]))
+        print(f"L={L} {name}: ours {float(value):.5f} ref {float(ref[name]):.5f} err {e_ours:.2e} eager {e_eager:.2e}")
+        assert e_ours <= 2 * e_eager + 1e-3, name
+    assert abs(float(kd["ce"]) - float(ref["masked_ce"])) <= 2 * abs(float(eager["masked_ce"] - ref["masked_ce"])) + 1e-3
+    assert float(prebuilt["ce"]) == float(rep["ce"])                       # the same mask, the same kernels
+    # the reference's self-test step: the three losses train the codes
+    clm.train()
+    losses = clm(idd, distill_lambda=1.0, copy_lambda=1.0, distill_temp=2.0)
+    (losses["ce"] + losses["distill"] + losses["copy"]).backward()
+    assert torch.isfinite(clm.pause.grad).all() and clm.pause.grad.norm() > 0
+    assert torch.isfinite(clm.copy_token.grad).all() and clm.copy_token.grad.norm() > 0

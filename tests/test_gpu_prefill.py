@@ -15,9 +15,9 @@ def _bf16(x):
 
 
 def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static", xattn="full",
-           passes=1):
+           passes=1, copy_rows=0):
     from abridgekv_amd import ops
-    S0 = N * (C + passes * K)
+    S0 = N * (C + passes * K) + copy_rows
     g = torch.Generator().manual_seed(seed)
     q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
@@ -28,14 +28,14 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
                                           lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
-                                          pause_passes=passes)
+                                          pause_passes=passes, copy_rows=copy_rows)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=passes)
+                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -141,6 +141,25 @@ def test_pause_passes(passes, shape):
         quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
         _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=22 + passes, tail=3,
                policy="rolling", xattn="causal" if passes == 3 else "none", passes=passes)
+
+
+@pytest.mark.parametrize("shape", ["aligned", "unaligned"])
+def test_copy_region(shape):
+    """A copy region of 1 + C rows after the blocks (it reads the last block's final pass and itself causally),
+    with per-head quotas, one and two passes."""
+    if shape == "aligned":
+        quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+        _check(C=128, K=64, N=3, B=2, head_quota=quota, seed=31, copy_rows=129)
+        _check(C=128, K=64, N=2, B=1, seed=32, passes=2, copy_rows=129)
+    else:
+        quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+        _check(C=8, K=4, N=5, B=2, head_quota=quota, seed=33, tail=2, policy="static", copy_rows=9)
+
+
+@pytest.mark.parametrize("C,N", [(512, 1), (256, 3), (200, 2)])
+def test_plain_causal_without_codes(C, N):
+    """codes_k = 0: causal attention within blocks of C rows (the model's plain forward), aligned and not."""
+    _check(C=C, K=0, N=N, B=2, seed=34)
 
 
 def test_strided_hf_layout():

@@ -12,7 +12,7 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1, copy_rows=0):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
@@ -24,14 +24,22 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
     block, "causal" the ones up to the query, "none" no code row of its own block.
     L = passes pause passes (compress_forward.py:594-600, "pause^l <- own pause^{l-1}", "earlier blocks' final
     codes"): a code row of pass l also reads its block's pass l - 1, the xattn rule speaks of its own pass, later
-    blocks read the final pass only, and a quota counts a row's slot within its pass."""
+    blocks read the final pass only, and a quota counts a row's slot within its pass.
+    Copy region (compress_forward.py:631, "copy region q>=S0: attend ONLY last block's K final codes + causal within
+    copy"): copy_rows rows after the blocks; the quota still hides code slots >= quota."""
     per = C + passes * K
-    S = N * per
+    S0 = N * per
+    S = S0 + copy_rows
     m = np.zeros((S, S), bool)
     for q in range(S):
+        if q >= S0:                              # a copy row
+            last_final = range(S0 - K, S0)       # the last block's final pass is the end of the blocks
+            for k in range(q + 1):
+                m[q, k] = k >= S0 or (k in last_final and (quota is None or k - (S0 - K) < quota))
+            continue
         qb, qw = divmod(q, per)
         q_pass = 0 if qw < C else (qw - C) // K + 1
-        for k in range(S):
+        for k in range(S0):
             kb, kw = divmod(k, per)
             k_content = kw < C
             k_pass = 0 if k_content else (kw - C) // K + 1
@@ -148,6 +156,30 @@ def test_pause_passes_arith_equals_role_equals_brute(C, K, N, L):
     assert not m[C, C + K] and m[C + K, C + K + K - 1]       # pass 1 does not read pass 2; pass 2 reads itself
     assert L < 3 or not m[C + 2 * K, first]                  # pass 3 does not read pass 1
     assert np.array_equal(op.arith_mask(C, K, N, passes=1), op.arith_mask(C, K, N))
+
+
+@pytest.mark.parametrize("C,K,N,L", [(4, 2, 3, 1), (4, 2, 2, 2), (6, 4, 2, 1), (3, 2, 3, 3)])
+def test_copy_region_arith_equals_role_equals_brute(C, K, N, L):
+    cr = C + 1                                               # the copy token and the last block's content
+    for T, policy, xattn in ((0, "static", "full"), (1, "static", "causal"), (2, "rolling", "full")):
+        kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L, copy_rows=cr)
+        a = op.arith_mask(C, K, N, **kw)
+        assert np.array_equal(a, op.role_mask(C, K, N, **kw))
+        assert np.array_equal(a, brute(C, K, N, tail=T, policy=policy, xattn=xattn, passes=L, copy_rows=cr))
+        S0 = N * (C + L * K)
+        assert np.array_equal(a[:S0, :S0], op.arith_mask(C, K, N, retain_tail=T, tail_policy=policy,
+                                                         pause_xattn=xattn, passes=L))
+        hq = [1, K, 2, K]
+        ah = op.arith_mask(C, K, N, head_quota=hq, **kw)
+        assert np.array_equal(ah, op.role_mask(C, K, N, head_quota=hq, **kw))
+        for h, q in enumerate(hq):
+            assert np.array_equal(ah[h], brute(C, K, N, quota=q, tail=T, policy=policy, xattn=xattn, passes=L,
+                                               copy_rows=cr))
+    # a block-local causal mask without codes
+    plain = op.arith_mask(C, 0, N)
+    blk = np.arange(N * C) // C
+    assert np.array_equal(plain, np.tril(np.ones((N * C, N * C), bool)) & (blk[:, None] == blk[None, :]))
+    assert np.array_equal(plain, op.role_mask(C, 0, N))
 
 
 def test_window_tail_spot_checks():
