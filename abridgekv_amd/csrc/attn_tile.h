@@ -250,10 +250,23 @@ __device__ __forceinline__ void tile_mask(floatx4 (&s)[2][2][H], int k0, const T
 // two 32-key halves. Lazy rescale: the running max moves only when a column's max exceeds it by more than 8 (P stays
 // below 2^8); then O and the weight sums are rescaled and t shifted. P^T k-index e < 4 of half kk is key
 // 32kk + 4j + e, e >= 4 is key 32kk + 16 + 4j + e - 4 (the order vt_operand reads V in).
+// Max of this lane's 16 scores of head u, as a chain of three-operand maxima (v_max3_f32: 8 instructions).
+template <int H>
+__device__ __forceinline__ float lane_max(const floatx4 (&s)[2][2][H], int u) {
+  float mx = fmaxf(fmaxf(s[0][0][u][0], s[0][0][u][1]), s[0][0][u][2]);
+  mx = fmaxf(fmaxf(mx, s[0][0][u][3]), s[0][1][u][0]);
+  mx = fmaxf(fmaxf(mx, s[0][1][u][1]), s[0][1][u][2]);
+  mx = fmaxf(fmaxf(mx, s[0][1][u][3]), s[1][0][u][0]);
+  mx = fmaxf(fmaxf(mx, s[1][0][u][1]), s[1][0][u][2]);
+  mx = fmaxf(fmaxf(mx, s[1][0][u][3]), s[1][1][u][0]);
+  mx = fmaxf(fmaxf(mx, s[1][1][u][1]), s[1][1][u][2]);
+  return fmaxf(mx, s[1][1][u][3]);
+}
+
 template <int H>
 __device__ __forceinline__ void tile_softmax(floatx4 (&s)[2][2][H], floatx4 (&o)[8][H], float (&m_run)[H],
                                              floatx4 (&lsum)[H], float scale_log2, bf16x8 (&pop)[2][H]) {
-  float neg_m[H], tmax[H];
+  float neg_m[H];
   bool need = false;
 #pragma unroll
   for (int u = 0; u < H; ++u) {
@@ -264,20 +277,18 @@ __device__ __forceinline__ void tile_softmax(floatx4 (&s)[2][2][H], floatx4 (&o)
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[kk][t][u][r] = fmaf(s[kk][t][u][r], scale_log2, neg_m[u]);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[kk][t][u][0], s[kk][t][u][1]), fmaxf(s[kk][t][u][2], s[kk][t][u][3])));
-    mx = max_xor16(mx);
-    tmax[u] = max_xor32(mx);
-    need |= tmax[u] - neg_m[u] > m_run[u] + 8.f;       // absolute max (log2 units) beyond the headroom
+    const float mx = lane_max(s, u);
+    // this lane's part of the column beyond the headroom: t > 8 (log2 units) once a max is set, any finite t before;
+    // some lane of a column is beyond it exactly when the column's max is, so the wave-wide vote needs no
+    // cross-lane max on the common path
+    need |= mx > (m_run[u] == -INFINITY ? -INFINITY : 8.f);
   }
   if (__any(need)) {
 #pragma unroll
     for (int u = 0; u < H; ++u) {
-      const float m_new = fmaxf(m_run[u], tmax[u] - neg_m[u]);
+      // the column's max (all four lane groups); the lane max recomputed here holds no register across the vote
+      const float tmax = max_xor32(max_xor16(lane_max(s, u)));
+      const float m_new = fmaxf(m_run[u], tmax - neg_m[u]);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[u] - m_new);
       const float d = m_new == -INFINITY ? 0.f : m_new + neg_m[u];    // new max minus the offset t was taken at
       m_run[u] = m_new;
