@@ -160,6 +160,17 @@ class _CodeRows:
         self.rows = self.slots = None
         self.S0 = -1
         self.lengths = ()           # sequence lengths of the layout: S0, and S0 + 1 + C with the copy region
+        self._copies = {}
+
+    def at(self, device):
+        """(rows, slots) on ``device`` (the module may have been moved after the layout was built); copies are kept
+        per device, the layout's own tensors stay where it built them."""
+        if self.rows.device == device:
+            return self.rows, self.slots
+        key = (str(device), self.S0)
+        if key not in self._copies:
+            self._copies[key] = (self.rows.to(device), self.slots.to(device))
+        return self._copies[key]
 
 
 class _QProjQRes(nn.Module):
@@ -179,8 +190,9 @@ class _QProjQRes(nn.Module):
         cr = self._code_rows
         if out.size(1) not in cr.lengths:
             return out
-        res = self.qres.index_select(0, cr.slots).to(out.dtype)
-        return out.index_add(1, cr.rows, res.unsqueeze(0).expand(out.size(0), -1, -1))
+        rows, slots = cr.at(out.device)
+        res = self.qres.index_select(0, slots).to(out.dtype)
+        return out.index_add(1, rows, res.unsqueeze(0).expand(out.size(0), -1, -1))
 
 
 class _QProjCode(nn.Module):
@@ -204,7 +216,8 @@ class _QProjCode(nn.Module):
         cr = self._code_rows
         if out.size(1) not in cr.lengths:
             return out
-        return out.index_copy(1, cr.rows, self.code(x.index_select(1, cr.rows)).to(out.dtype))
+        rows, _ = cr.at(out.device)
+        return out.index_copy(1, rows, self.code(x.index_select(1, rows)).to(out.dtype))
 
 
 def code_seeds(clm, tok_e: torch.Tensor, segment_mean: bool = False) -> torch.Tensor:
@@ -347,6 +360,7 @@ class CompressLM(nn.Module):
         self._code_rows.slots = code % (C + L * Ka) - C
         self._code_rows.S0 = N * (C + L * Ka)
         self._code_rows.lengths = (self._code_rows.S0, self._code_rows.S0 + 1 + C)
+        self._code_rows._copies = {}
 
     def set_N(self, N):
         """Rebuild the N-dependent layout for a new block count (compress_forward.py set_N)."""

@@ -125,3 +125,15 @@ def test_generator_projects_code_steps_like_the_forward():
         assert torch.equal(_project(attn.v_proj, x, True), attn.v_proj.code(x))
         assert torch.equal(_project(attn.v_proj, x, False), attn.v_proj.orig(x))
         assert torch.equal(_project(attn.o_proj, x.repeat(1, 1, 64), True), attn.o_proj(x.repeat(1, 1, 64)))
+
+
+def test_code_rows_follow_the_module_across_devices():
+    """Built on one device, the code-row projections index on whatever device their input is on (a module moved
+    after construction); checked here between the CPU and the meta device."""
+    from abridgekv_amd.compress_forward import CompressLM
+    clm = CompressLM(_model(), 8, 2, 4, query_residual=True)
+    cr = clm._code_rows
+    rows, slots = cr.at(torch.device("meta"))
+    assert rows.device.type == "meta" and slots.device.type == "meta" and rows.shape == (2 * 4,)
+    rows, _ = cr.at(torch.device("cpu"))
+    assert rows.device.type == "cpu" and rows.tolist() == [8, 9, 10, 11, 20, 21, 22, 23]
