@@ -39,16 +39,17 @@ SIGNATURES = {
     "abkv_prefill_masked_attn_f32": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
                                                _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
                                                C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                               C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp, _vp]),
+                                               C.c_int, C.c_int, C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp,
+                                               _vp]),
     "abkv_slot_mapping": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_long, C.c_int, _vp, _vp, _vp]),
     "abkv_prefill_masked_attn": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long, _vp, C.c_long, C.c_long, C.c_long,
                                            _vp, C.c_long, C.c_long, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
-                                           C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                           C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp, _vp]),
+                                           C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_float, _vp, C.c_long, C.c_long, C.c_long, _vp, _vp]),
     "abkv_prefill_masked_bwd_workspace_size": (C.c_size_t, [C.c_int, C.c_int]),
     "abkv_prefill_masked_attn_bwd": (C.c_int, [_vp, C.c_long, C.c_long, C.c_long] * 5
                                      + [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
-                                        C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+                                        C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
                                      + [_vp, C.c_long, C.c_long, C.c_long] * 3 + [_vp, C.c_size_t, _vp]),
     "abkv_paged_prefill_workspace_size": (C.c_size_t, [C.c_int, C.c_int]),
     "abkv_paged_prefill_attn": (C.c_int, [_vp, C.c_long, C.c_long, _vp, C.c_int, _vp, C.c_long, C.c_int, _vp, _vp,

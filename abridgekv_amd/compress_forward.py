@@ -7,19 +7,22 @@ optional raw prompt, optional fixed per-(layer, KV head) code quotas, ``active_c
 ``bitrev`` code positions and the retained tail (``retain_tail_kv`` = T: a block's codes do not see or summarize its
 last T content rows, bitrev codes spread over the first C - T; by ``retain_tail_policy`` those rows stay visible to
 every later row ("static"), to the next block's content rows ("sticky"), or to the next block's i-th content row
-from tail row i on ("rolling"), compress_forward.py:99-124); the code-seed pools (``seg_pool``,
-``gated_seg_pool``, ``pool_init``, :315-343, 1147-1178) and the code-row projections (``query_residual``,
-``code_q_heads``, ``code_kv_heads``, :181-222, 397-432). The sequence layout, RoPE positions, loss positions and
+from tail row i on ("rolling"), compress_forward.py:99-124); the replay tail (``replay_tail`` = R rows after a
+block's codes replaying its last R content tokens, seen by the next block's content as a rolling window;
+``code_exclude_replay_tail`` hides those content rows from the codes, :139-178, 594-603); the code-seed pools
+(``seg_pool``, ``gated_seg_pool``, ``pool_init``, :315-343, 1147-1178) and the code-row projections
+(``query_residual``, ``code_q_heads``, ``code_kv_heads``, :181-222, 397-432). The sequence layout, RoPE positions,
+loss positions and
 loss reductions follow the reference (compress_forward.py:20-88, 1044-1071, 957-1042, 1134-1230); the attention of
 every decoder layer runs ``abkv_prefill_masked_attn`` through a HuggingFace attention function registered as
 ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask (``_arith_mask_mod`` / ``_mask_mod`` /
 ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 566-649, 695-727, 815-894). The mask
-is never materialised: the kernel evaluates it from (C, K, L, N, prompt_len, head quota, tail, xattn); layouts off
-the 64-row tile grid, L > 1 and non-full xattn take its per-element walk.
+is never materialised: the kernel evaluates it from (C, K, L, R, N, prompt_len, head quota, tail, xattn); layouts off
+the 64-row tile grid, L > 1, replay rows and non-full xattn take its per-element walk.
 
-Replay / raw tails (legacy appended-layout checkpoints), the full-context baseline, copy and distillation losses
-and external block masks raise NotImplementedError. Gradients flow through the attention by the kernel's HIP
-backward (dq, dk, dv under the same mask), so the module trains.
+The raw tail (``raw_tail``, a training ablation the reference's serving refuses) raises NotImplementedError.
+Gradients flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module
+trains.
 """
 from __future__ import annotations
 
@@ -52,6 +55,8 @@ class CompressMask:
     pause_xattn: str = "full"
     passes: int = 1
     copy_rows: int = 0
+    replay_rows: int = 0
+    replay_exclude: bool = False
 
 
 class _MaskedPrefill(torch.autograd.Function):
@@ -71,7 +76,8 @@ class _MaskedPrefill(torch.autograd.Function):
                                               prompt_len=mask.prompt_len, head_quota=hq, scale=scale, lse=lse,
                                               retain_tail=mask.retain_tail, tail_policy=mask.tail_policy,
                                               pause_xattn=mask.pause_xattn, pause_passes=mask.passes,
-                                              copy_rows=mask.copy_rows)
+                                              copy_rows=mask.copy_rows, replay_rows=mask.replay_rows,
+                                              replay_exclude=mask.replay_exclude)
         if need_grad:
             ctx.save_for_backward(q, k, v, out, lse)
             ctx.mask, ctx.hq, ctx.scale = mask, hq, scale
@@ -86,7 +92,9 @@ class _MaskedPrefill(torch.autograd.Function):
                                                            prompt_len=m.prompt_len, head_quota=ctx.hq,
                                                            scale=ctx.scale, retain_tail=m.retain_tail,
                                                            tail_policy=m.tail_policy, pause_xattn=m.pause_xattn,
-                                                           pause_passes=m.passes, copy_rows=m.copy_rows)
+                                                           pause_passes=m.passes, copy_rows=m.copy_rows,
+                                                           replay_rows=m.replay_rows,
+                                                           replay_exclude=m.replay_exclude)
         return dq, dk, dv, None, None, None
 
 
@@ -116,32 +124,38 @@ def register_attention() -> None:
     AttentionInterface.register(ATTN_IMPLEMENTATION, masked_attention_forward)
 
 
-def roles(C: int, N: int, K: int, device=None, L: int = 1):
-    """(blk, role) per row of the layout of N blocks of [C content | L passes of K codes]: role 0 = content,
-    1..L = pause pass (compress_forward.py:20-31)."""
-    per = C + L * K
+def roles(C: int, N: int, K: int, device=None, L: int = 1, R: int = 0):
+    """(blk, role) per row of the layout of N blocks of [C content | L passes of K codes | R replay rows]: role 0 =
+    content, 1..L = pause pass, L + 1 = replay (compress_forward.py:20-31)."""
+    per = C + L * K + R
     within = torch.arange(per, device=device).repeat(N)
     blk = torch.arange(N, device=device).repeat_interleave(per)
-    return blk, torch.where(within < C, torch.zeros_like(within), torch.div(within - C, K, rounding_mode="floor") + 1)
+    code = torch.div(within - C, max(K, 1), rounding_mode="floor") + 1
+    role = torch.where(within < C, torch.zeros_like(within), torch.where(within < C + L * K, code,
+                                                                         torch.full_like(within, L + 1)))
+    return blk, role
 
 
-def content_abs_pos(C: int, N: int, K: int, device=None, L: int = 1) -> torch.Tensor:
-    """Absolute content index b*C + j of content rows; N*C for code rows (compress_forward.py:72-88, no replay)."""
-    per = C + L * K
+def content_abs_pos(C: int, N: int, K: int, device=None, L: int = 1, R: int = 0) -> torch.Tensor:
+    """Absolute content index b*C + j of content rows, of the replayed token for replay rows; N*C for code rows
+    (compress_forward.py:72-88)."""
+    per = C + L * K + R
     within = torch.arange(per, device=device).repeat(N)
     blk = torch.arange(N, device=device).repeat_interleave(per)
-    return torch.where(within < C, blk * C + within, torch.full_like(within, N * C))
+    pos = torch.where(within < C, blk * C + within, torch.full_like(within, N * C))
+    return torch.where(within >= C + L * K, blk * C + (C - R) + (within - C - L * K), pos)
 
 
 def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, device=None,
-                      code_excluded_tail: int = 0, L: int = 1) -> torch.Tensor:
-    """(1, N*(C+L*K_act)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, no replay
-    tail, no copy rows): appended code row p of a block sits at C + (p // K_act) K + p % K_act of the full layout;
-    bitrev code rows (L = 1) spread over the first C - code_excluded_tail in-block offsets."""
-    per_full, per_act = C + L * K, C + L * K_act
+                      code_excluded_tail: int = 0, L: int = 1, R: int = 0) -> torch.Tensor:
+    """(1, N*(C+L*K_act+R)) RoPE positions numbered as in the full-K layout (compress_forward.py:1044-1071, no copy
+    rows): appended code row p of a block sits at C + (p // K_act) K + p % K_act of the full layout and replay row r
+    at C + L K + r; bitrev code rows (L = 1, no replay rows) spread over the first C - code_excluded_tail in-block
+    offsets."""
+    per_full, per_act = C + L * K + R, C + L * K_act + R
     idx = torch.arange(N * per_act, device=device)
     within, blk = idx % per_act, idx // per_act
-    is_code = within >= C
+    is_code = (within >= C) & (within < C + L * K_act)
     p = (within - C).clamp_min(0)
     if code_positions == "bitrev":
         offs = torch.from_numpy(bitrev_offsets(K, C - code_excluded_tail)).to(device)
@@ -149,6 +163,8 @@ def rope_position_ids(C: int, N: int, K: int, K_act: int, code_positions: str, d
     else:
         slot = torch.div(p, K_act, rounding_mode="floor") * K + p % K_act
         pos = torch.where(is_code, blk * per_full + C + slot, blk * per_full + within)
+        replay = within >= C + L * K_act
+        pos = torch.where(replay, blk * per_full + C + L * K + (within - C - L * K_act), pos)
     return pos.view(1, -1)
 
 
@@ -252,7 +268,6 @@ def code_seeds(clm, tok_e: torch.Tensor, segment_mean: bool = False) -> torch.Te
     return pause.expand(*lead, K, d)
 
 
-_UNSUPPORTED = ("raw_tail", "replay_tail", "code_exclude_replay_tail")
 
 
 class CompressLM(nn.Module):
@@ -260,7 +275,8 @@ class CompressLM(nn.Module):
 
     ``base_model`` is a HuggingFace causal LM with 32 query heads, 8 KV heads and head size 128 in bf16 (e.g.
     Qwen3-4B or a random model of that attention shape); its attention implementation is switched to
-    ``"abridgekv_hip"``. Replay and raw tails (legacy appended-layout checkpoints) raise NotImplementedError.
+    ``"abridgekv_hip"``. The raw tail (``raw_tail``, a training ablation the reference does not serve) raises
+    NotImplementedError.
     """
 
     def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", pool_init=False, query_residual=False,
@@ -268,22 +284,27 @@ class CompressLM(nn.Module):
                  replay_tail=0, code_exclude_replay_tail=False, retain_tail_kv=0, retain_tail_policy="rolling",
                  head_code_quotas=None, active_code_rows=None, code_positions="appended"):
         super().__init__()
-        used = [name for name, value in zip(_UNSUPPORTED, (raw_tail, replay_tail, code_exclude_replay_tail)) if value]
-        if used:
-            raise NotImplementedError(f"CompressLM options {used} are not supported by the native forward")
+        if raw_tail:
+            raise NotImplementedError("CompressLM option raw_tail is not supported by the native forward")
         if int(L) != L or L < 1:
             raise ValueError(f"L must be a positive integer, got {L}")
         if pause_xattn not in ("none", "causal", "full"):
             raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {pause_xattn!r}")
+        if not 0 <= replay_tail <= C:
+            raise ValueError(f"replay_tail must be in [0, C={C}], got {replay_tail}")
         if not 0 <= retain_tail_kv < C:
             raise ValueError(f"retain_tail_kv must be in [0, C={C}), got {retain_tail_kv}")
+        if replay_tail and retain_tail_kv:
+            raise ValueError("raw_tail, replay_tail, and retain_tail_kv are mutually exclusive")
         if retain_tail_policy not in ("rolling", "sticky", "static"):
             raise ValueError(f"retain_tail_policy must be 'rolling', 'sticky' or 'static', got {retain_tail_policy!r}")
         if retain_tail_policy != "rolling" and not retain_tail_kv:
             raise ValueError(f"retain_tail_policy={retain_tail_policy!r} requires retain_tail_kv > 0")
+        if code_exclude_replay_tail and not 0 < replay_tail < C:
+            raise ValueError("code_exclude_replay_tail requires replay_tail in [1, C)")
         if code_positions not in ("appended", "bitrev"):
             raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
-        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1) or L != 1):
+        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1) or L != 1 or replay_tail):
             raise ValueError("code_positions='bitrev' needs power-of-two C and K, L=1 and no tails")
         if query_residual and code_q_heads:
             raise ValueError("query_residual and code_q_heads both replace q_proj; enable one of them")
@@ -298,8 +319,12 @@ class CompressLM(nn.Module):
         self.model.config._attn_implementation = ATTN_IMPLEMENTATION
         self.C, self.N, self.K, self.L = int(C), int(N), int(K), int(L)
         self.pause_xattn, self.code_positions = pause_xattn, code_positions
-        self.replay_tail = self.raw_tail = 0
-        self.retain_tail_kv = self.code_excluded_tail = int(retain_tail_kv)
+        self.raw_tail = 0
+        self.replay_tail = int(replay_tail)
+        self.code_exclude_replay_tail = bool(code_exclude_replay_tail)
+        self.retain_tail_kv = int(retain_tail_kv)
+        # the content rows a block's codes neither see nor summarise (compress_forward.py:298-300)
+        self.code_excluded_tail = self.replay_tail if self.code_exclude_replay_tail else self.retain_tail_kv
         self.retain_tail_policy = retain_tail_policy
         if code_positions == "bitrev" and C - self.code_excluded_tail < K:
             raise ValueError(f"bitrev code span {C - self.code_excluded_tail} < num_code_tokens {K}")
@@ -344,21 +369,21 @@ class CompressLM(nn.Module):
 
     def _set_layout(self, N):
         dev = self.pause.device
-        C, Ka, L = self.C, self.K_act, self.L
-        blk, role = roles(C, N, Ka, dev, L)
+        C, Ka, L, R = self.C, self.K_act, self.L, self.replay_tail
+        blk, role = roles(C, N, Ka, dev, L, R)
         content = role == 0
         pf = torch.tensor([k for k in range(N * C) if k % C != C - 1], device=dev, dtype=torch.long)
-        layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev, L),
+        layout = {"blk": blk, "role": role, "content_abs_pos": content_abs_pos(C, N, Ka, dev, L, R),
                   "loss_pos": content & torch.roll(content, -1), "content_pos": content.nonzero(as_tuple=True)[0],
                   "predict_flat": pf, "predict_block": pf // C,
                   "_pos_ids": rope_position_ids(C, N, self.K, Ka, self.code_positions, dev,
-                                                self.code_excluded_tail, L)}
+                                                self.code_excluded_tail, L, R)}
         for name, value in layout.items():
             self.register_buffer(name, value, persistent=False)
-        code = (role > 0).nonzero(as_tuple=True)[0]
+        code = ((role > 0) & (role <= L)).nonzero(as_tuple=True)[0]
         self._code_rows.rows = code
-        self._code_rows.slots = code % (C + L * Ka) - C
-        self._code_rows.S0 = N * (C + L * Ka)
+        self._code_rows.slots = code % (C + L * Ka + R) - C
+        self._code_rows.S0 = N * (C + L * Ka + R)
         self._code_rows.lengths = (self._code_rows.S0, self._code_rows.S0 + 1 + C)
         self._code_rows._copies = {}
 
@@ -407,7 +432,7 @@ class CompressLM(nn.Module):
                 raise ValueError("prompt_len must hold one length per sequence")
         return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
                             self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn, self.L,
-                            copy_rows)
+                            copy_rows, self.replay_tail, self.code_exclude_replay_tail)
 
     def _lm_ce(self, hid, tgt, chunk):
         if chunk <= 0:
@@ -443,20 +468,21 @@ class CompressLM(nn.Module):
             raise ValueError(f"content_ids block size {C} != C={self.C}")
         if N != self.N:
             self.set_N(N)
-        K, L = self.K_act, self.L
+        K, L, R = self.K_act, self.L, self.replay_tail
         emb = self.model.model.embed_tokens
         tok_e = emb(content_ids)
         d = tok_e.size(-1)
         pause_e = code_seeds(self, tok_e).expand(B, N, K, d)
         if L > 1:
             pause_e = pause_e.repeat(1, 1, L, 1)                      # every pass starts from the same seeds
-        x = torch.cat([tok_e, pause_e], dim=2).reshape(B, N * (C + L * K), d)
+        parts = [tok_e, pause_e] + ([tok_e[:, :, C - R:, :]] if R else [])   # the replay rows: the last R tokens
+        x = torch.cat(parts, dim=2).reshape(B, N * (C + L * K + R), d)
         pos = self._pos_ids
         if with_copy:
             copy_in = torch.cat([self.copy_token.to(tok_e.dtype).view(1, 1, d).expand(B, 1, d),
                                  emb(content_ids[:, -1, :])], dim=1)
             x = torch.cat([x, copy_in], dim=1)
-            start = N * C if self.code_positions == "bitrev" else N * (C + L * self.K)
+            start = N * C if self.code_positions == "bitrev" else N * (C + L * self.K + R)
             pos = torch.cat([pos, start + torch.arange(1 + C, device=pos.device).view(1, -1)], dim=1)
         if torch.is_autocast_enabled(x.device.type):
             x = x.to(torch.get_autocast_dtype(x.device.type))
@@ -576,7 +602,7 @@ class CompressLM(nn.Module):
         mo = self._compressed_forward(content_ids, prompt_len, with_copy, mask, need_rep)
         out = mo.last_hidden_state
         d = out.size(-1)
-        S0 = N * (C + self.L * self.K_act)
+        S0 = N * (C + self.L * self.K_act + self.replay_tail)
         if include_cross_block:
             pred_flat = torch.arange(N * C - 1, device=dev)
             hid = out[:, :S0, :][:, self.content_pos, :][:, :-1, :].reshape(-1, d)

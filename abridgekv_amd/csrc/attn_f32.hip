@@ -46,6 +46,8 @@ struct F32Args {
   int pause_xattn;             // code <-> code attention in a block (kXattn*)
   int pause_passes;            // pause passes of codes_k rows per block
   int copy_rows;               // copy-region rows at the end of the seq_len rows
+  int replay_rows;             // replay rows after each block's codes
+  int replay_exclude;          // the codes do not see the block's last replay_rows content rows
   int num_tokens;
   float scale;
   float* out;
@@ -69,8 +71,8 @@ __device__ __forceinline__ void wave_sync() {
 //   and a code key of slot s is visible to a head only if s < quota.
 __device__ __forceinline__ bool f32_visible(const F32Args& a, int qr, int kr, int plen, int quota) {
   return compress_visible(qr, kr, a.seq_len, a.copy_rows, a.block_c, a.codes_k, a.pause_passes,
-                          a.block_c + a.pause_passes * a.codes_k, plen, quota, a.retain_tail, a.tail_policy,
-                          a.pause_xattn);
+                          a.block_c + a.pause_passes * a.codes_k + a.replay_rows, plen, quota, a.retain_tail,
+                          a.tail_policy, a.pause_xattn, a.replay_rows, a.replay_exclude != 0);
 }
 
 __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(64 * kF32Waves) void attn_f32_kernel(F32Args a) {
   if (a.mode == 1) {
     b = t / a.seq_len;
     qrow = t - b * a.seq_len;
-    const int per = a.block_c + a.pause_passes * a.codes_k;
+    const int per = a.block_c + a.pause_passes * a.codes_k + a.replay_rows;
     const int s0 = a.seq_len - a.copy_rows;
     // nothing after the query's own block is visible; a copy row sees up to itself
     n_keys = qrow >= s0 ? qrow + 1 : min(s0, (qrow / per + 1) * per);
@@ -304,14 +306,17 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 int pause_passes, int copy_rows, float scale, float* out, long o_sb, long o_ss,
-                                 long o_sh, float* lse,
+                                 int pause_passes, int copy_rows, int replay_rows, int replay_exclude, float scale,
+                                 float* out, long o_sb, long o_ss, long o_sh, float* lse,
                                  hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k < 0 ||
       num_blocks <= 0 || pause_passes <= 0 || copy_rows < 0 || (codes_k == 0 && (pause_passes != 1 || copy_rows)) ||
-      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) + copy_rows || retain_tail < 0 ||
+      replay_rows < 0 || replay_rows > block_c || (replay_rows && (retain_tail || codes_k == 0)) ||
+      (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
+      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
+      retain_tail < 0 ||
       retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
       pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
@@ -339,6 +344,8 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
   a.pause_xattn = pause_xattn;
   a.pause_passes = pause_passes;
   a.copy_rows = copy_rows;
+  a.replay_rows = replay_rows;
+  a.replay_exclude = replay_exclude;
   a.num_tokens = batch * seq_len;
   a.scale = scale;
   a.out = out;

@@ -23,8 +23,10 @@ struct MaskGeom {
   int xattn;      // code rows' attention to their own pass's code rows (kXattn*)
   int K, L;       // code rows per pause pass, passes per block
   int copy;       // copy-region rows at the end of the S0 rows
+  int R;          // replay rows per block
+  bool rx;        // the codes do not see the block's last R content rows
   __device__ __forceinline__ bool visible(int kv, int u) const {
-    return compress_visible(qrow, kv, S0, copy, C, K, L, per, plen, quota[u], tail, policy, xattn);
+    return compress_visible(qrow, kv, S0, copy, C, K, L, per, plen, quota[u], tail, policy, xattn, R, rx);
   }
 };
 

@@ -41,16 +41,20 @@ __device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb
 }
 
 // Visibility of key row kv to query row q (sequence rows) under the compression mask over blocks of
-// [C content | L pause passes of K code rows] (per = C + L K; abridgekv/compress_forward.py:566-649, _mask_mod):
-//   causal & (own-block content | earlier blocks' final-pass codes | raw-prompt content (< plen) | retained tail)
+// [C content | L pause passes of K code rows | R replay rows] (per = C + L K + R; abridgekv/compress_forward.py:
+// 566-649, _mask_mod):
+//   causal & (own-block content | earlier blocks' final-pass codes | raw-prompt content (< plen) | retained tail
+//             | a replay row's own block's final pass and replay rows | for content row i, the previous block's
+//             replay rows r >= i (_replay_tail_visible))
 //   | a code row's own block's previous pass | its own pass by xattn,
-// less a code row's own block's last `tail` content rows, and less a code key whose slot (its index within its pass)
-// is >= quota. The last `copy` of the S rows are the copy region (copy_lambda, :631-633): they see the last block's
-// final pass (slot < quota) and the copy rows up to themselves, and no other row sees them. K = 0 (no codes) is
-// block-local causal attention. With L = 1 and copy = 0 (compile-time constants at most call sites) the pass and
-// copy arithmetic folds away.
+// less a code row's own block's last `tail` content rows (R of them with rx: code_exclude_replay_tail), and less a
+// code key whose slot (its index within its pass) is >= quota. The last `copy` of the S rows are the copy region
+// (copy_lambda, :631-633): they see the last block's final pass (slot < quota) and the copy rows up to themselves,
+// and no other row sees them. K = 0 (no codes) is block-local causal attention. With L = 1, R = 0 and copy = 0
+// (compile-time constants at most call sites) the pass, replay and copy arithmetic folds away.
 __device__ __forceinline__ bool compress_visible(int q, int kv, int S, int copy, int C, int K, int L, int per,
-                                                 int plen, int quota, int tail, int policy, int xattn) {
+                                                 int plen, int quota, int tail, int policy, int xattn, int R = 0,
+                                                 bool rx = false) {
   if (kv >= S || q >= S) return false;
   const int S0 = S - copy;                                  // rows of the compressed layout
   if (copy > 0 && q >= S0) {
@@ -61,18 +65,23 @@ __device__ __forceinline__ bool compress_visible(int q, int kv, int S, int copy,
   if (copy > 0 && kv >= S0) return false;
   const int qb = q / per, kb = kv / per;
   const int qw = q - qb * per, kw = kv - kb * per;
+  const int code_end = C + L * K;                           // in-block end of the code rows
   const bool kc = kw < C, qc = qw < C;
+  const bool krep = R > 0 && kw >= code_end, qrep = R > 0 && qw >= code_end;
+  const bool kcode = !kc && !krep, qcode = !qc && !qrep;
   const int kp = L == 1 ? 1 : (kw - C) / K + 1;            // pass of a code key (1..L)
   const int qp = L == 1 ? 1 : (qw - C) / K + 1;            // pass of a code query
-  const bool in_tail = kc && kw >= C - tail;
-  bool v = (kc && kb == qb) || (!kc && kp == L && kb < qb) || (kc && kb * C + kw < plen) ||
+  const int X = rx ? R : tail;                              // the own-block content rows hidden from the codes
+  bool v = (kc && kb == qb) || (kcode && kp == L && kb < qb) || (kc && kb * C + kw < plen) ||
            tail_visible(policy, tail, C, qb, qw, kb, kw);
+  if (R > 0)
+    v = v || (qrep && kb == qb && (krep || (kcode && kp == L))) || (qc && krep && kb + 1 == qb && kw - code_end >= qw);
   v = v && kv <= q;
-  const bool own_codes = !qc && !kc && kb == qb;
+  const bool own_codes = qcode && kcode && kb == qb;
   v = v || (own_codes && kp + 1 == qp);
   v = v || (own_codes && kp == qp && (xattn == kXattnFull || (xattn == kXattnCausal && kv <= q)));
-  v = v && !(!qc && kb == qb && in_tail);
-  return v && (kc || kw - C - (kp - 1) * K < quota);
+  v = v && !(qcode && kb == qb && kc && kw >= C - X);
+  return v && (!kcode || kw - C - (kp - 1) * K < quota);
 }
 
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8 a, const bf16x8 b, floatx4 c) {

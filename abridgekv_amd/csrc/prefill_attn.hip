@@ -48,7 +48,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   const int j = lane >> 4;
   const int rg = w / (4 / H);                               // row group (16 rows)
   const int hbase = H * (w % (4 / H));                      // first head of this wave inside the GQA group
-  const int per = kAligned ? a.C + a.K : a.C + a.L * a.K;
+  const int per = kAligned ? a.C + a.K : a.C + a.L * a.K + a.R;
   const int q0 = qt * kBM;
   const int qrow = q0 + 16 * rg + m16;                      // this lane's query row (MFMA column)
   const int plen = a.prompt_len ? a.prompt_len[b] : 0;
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(64 * 4 * (4 / H), 1) void prefill_masked_kernel(Pre
   // this wave's heads hbase, hbase + 1 (hbase is 0 or 2): quotas by selection, not by a computed index
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
   const MaskGeom geo{qrow, a.S0, a.C, per, plen, {wq0, wq1}, a.tail, a.policy, a.xattn, a.K, kAligned ? 1 : a.L,
-                     kAligned ? 0 : a.copy};
+                     kAligned ? 0 : a.copy, kAligned ? 0 : a.R, !kAligned && a.rx};
   const int q_last = min(q0 + kBM, a.S0) - 1;
 
   TileWalk<kAligned, kTail, kWindow> walk(q0, q_last, a.C, per, a.S0, plen, qmin, qmax, wq0, wq1, a.tail, a.policy);
@@ -123,14 +123,17 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             int tail_policy, int pause_xattn, int pause_passes, int copy_rows, float scale,
-                             void* out, long out_stride_b,
+                             int tail_policy, int pause_xattn, int pause_passes, int copy_rows, int replay_rows,
+                             int replay_exclude, float scale, void* out, long out_stride_b,
                              long out_stride_s, long out_stride_h, float* lse, hipStream_t stream) {
   using namespace abkv;
   if (batch <= 0 || seq_len <= 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || block_c <= 0 || codes_k < 0 ||
       num_blocks <= 0 || pause_passes <= 0 || copy_rows < 0 || (codes_k == 0 && (pause_passes != 1 || copy_rows)) ||
-      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) + copy_rows || retain_tail < 0 ||
+      replay_rows < 0 || replay_rows > block_c || (replay_rows && (retain_tail || codes_k == 0)) ||
+      (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
+      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
+      retain_tail < 0 ||
       retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
       pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
@@ -153,8 +156,10 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.xattn = pause_xattn;
   a.L = pause_passes;
   a.copy = copy_rows;
+  a.R = replay_rows;
+  a.rx = replay_exclude != 0;
   a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull && pause_passes == 1 &&
-              copy_rows == 0;
+              copy_rows == 0 && replay_rows == 0;
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
   // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
   const int rg = w / 2, hbase = H * (w % 2);
-  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K;
+  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K + f.R;
   const int q0 = qt * kBM;
   const int qrow = q0 + 16 * rg + m16;
   const int plen = f.prompt_len ? f.prompt_len[b] : 0;
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bwd_dq_kernel(PrefillBwdArgs a
                                  f.k_ss, f.v_ss};
   const int wq0 = hbase ? quota_all[2] : quota_all[0], wq1 = hbase ? quota_all[3] : quota_all[1];
   const MaskGeom geo{qrow, f.S0, f.C, per, plen, {wq0, wq1}, f.tail, f.policy, f.xattn, f.K, kAligned ? 1 : f.L,
-                     kAligned ? 0 : f.copy};
+                     kAligned ? 0 : f.copy, kAligned ? 0 : f.R, !kAligned && f.rx};
   const int q_last = min(q0 + kBM, f.S0) - 1;
   TileWalk<kAligned, kTail, kWindow> walk(q0, q_last, f.C, per, f.S0, plen, qmin, qmax, wq0, wq1, f.tail, f.policy);
 
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int m16 = lane & 15, j = lane >> 4;
-  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K;
+  const int per = kAligned ? f.C + f.K : f.C + f.L * f.K + f.R;
   const int k0 = kt * kBN;
   const int key = k0 + 16 * w + m16;                        // this lane's column
   const int plen = f.prompt_len ? f.prompt_len[b] : 0;
@@ -400,6 +400,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
   const int exattn = kAligned ? kXattnFull : f.xattn;
   const int epasses = kAligned ? 1 : f.L;
   const int ecopy = kAligned ? 0 : f.copy;
+  const int erep = kAligned ? 0 : f.R;
+  const bool erx = !kAligned && f.rx;
   int qt = qt_lo, h = -1, mode = 0, lim0 = 0, lim1 = 0;
   auto next_pair = [&]() -> bool {
     for (;;) {
@@ -492,7 +494,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(PrefillBwdArgs 
                                : (kWindow && cmode == 5) ? (key < clim0 || key - qrow >= clim1)
                                                          : compress_visible(qrow, key, f.S0, ecopy, f.C, f.K,
                                                                             epasses, per, plen, qh, etail, epolicy,
-                                                                            exattn);
+                                                                            exattn, erep, erx);
               const float pr = vis ? fast_exp2(fmaf(s[kk][t][0][r], f.scale_log2, -l4[r])) : 0.f;
               s[kk][t][0][r] = pr;
               dp[kk][t][0][r] = pr * (dp[kk][t][0][r] - e4[r]);
@@ -539,7 +541,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 int pause_passes, int copy_rows, float scale, void* dq,
+                                 int pause_passes, int copy_rows, int replay_rows, int replay_exclude, float scale,
+                                 void* dq,
                                  long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
                                  long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
                                  long dv_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -548,7 +551,9 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || dout == nullptr || lse == nullptr ||
       dq == nullptr || dk == nullptr || dv == nullptr || block_c <= 0 || codes_k < 0 || num_blocks <= 0 ||
       pause_passes <= 0 || copy_rows < 0 || (codes_k == 0 && (pause_passes != 1 || copy_rows)) ||
-      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k) + copy_rows ||
+      replay_rows < 0 || replay_rows > block_c || (replay_rows && (retain_tail || codes_k == 0)) ||
+      (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
+      (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
       retain_tail < 0 || retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky ||
       pause_xattn < kXattnFull || pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
@@ -573,8 +578,10 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.xattn = pause_xattn;
   f.L = pause_passes;
   f.copy = copy_rows;
+  f.R = replay_rows;
+  f.rx = replay_exclude != 0;
   f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull && pause_passes == 1 &&
-              copy_rows == 0;
+              copy_rows == 0 && replay_rows == 0;
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;

@@ -24,6 +24,8 @@ struct PrefillArgs {
                                              // serve kXattnFull, the others take the per-element walk)
   int L;                                     // pause passes of K code rows per block (the aligned walks serve 1)
   int copy;                                  // copy-region rows after the N blocks (S0 counts them; aligned: 0)
+  int R;                                     // replay rows after each block's codes (aligned: 0)
+  int rx;                                    // code_exclude_replay_tail: the codes do not see the last R content rows
 };
 
 // Workgroup -> (tile rank, KV head, sequence) for a linear grid of num_tiles x 8 x B workgroups: KV head fastest,

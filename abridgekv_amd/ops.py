@@ -396,12 +396,14 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
                              head_quota: torch.Tensor | None = None, scale: float | None = None,
                              out: torch.Tensor | None = None, lse: torch.Tensor | None = None, retain_tail: int = 0,
                              tail_policy: str = "static", pause_xattn: str = "full", pause_passes: int = 1,
-                             copy_rows: int = 0):
+                             copy_rows: int = 0, replay_rows: int = 0, replay_exclude: bool = False):
     """Teacher-forced attention under the compression mask (N blocks of [C content | L passes of K codes],
     L = ``pause_passes``: pass l reads its block's content, its pass l - 1 and its own pass by ``pause_xattn``; later
-    blocks read the final pass only; L > 1 evaluates the mask per element), then ``copy_rows`` rows of a copy region
-    that see the last block's final pass and themselves causally. ``codes_k`` = 0: causal attention within blocks of
-    C rows (the plain forward).
+    blocks read the final pass only; L > 1 evaluates the mask per element), ``replay_rows`` = R replay rows after each
+    block's codes (a block's last R content tokens again: they see their block and its final pass; content row i of
+    the next block sees them from row i on; ``replay_exclude`` hides the last R content rows from the codes), then
+    ``copy_rows`` rows of a copy region that see the last block's final pass and themselves causally. ``codes_k`` = 0:
+    causal attention within blocks of C rows (the plain forward).
 
     q [B, S0, 32, 128], k/v [B, S0, 8, 128] bf16 (any strides with contiguous dims, e.g. the [B, H, S, D]
     transposed views HF attention receives, permuted back); prompt_len [B] int32 raw-prompt content tokens;
@@ -417,11 +419,12 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     policy = tail_policy_code(tail_policy)
     xattn = xattn_code(pause_xattn)
     L, cr = _passes(pause_passes), _copy_rows(codes_k, pause_passes, copy_rows)
+    R, rx = _replay(block_c, codes_k, retain_tail, replay_rows, replay_exclude)
     if q.dtype == torch.float32:
         return _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse,
-                                   int(retain_tail), policy, xattn, L, cr)
-    _require(S0 == num_blocks * (block_c + L * codes_k) + cr,
-             "seq_len must be num_blocks * (block_c + L * codes_k) + copy_rows")
+                                   int(retain_tail), policy, xattn, L, cr, R, rx)
+    _require(S0 == num_blocks * (block_c + L * codes_k + R) + cr,
+             "seq_len must be num_blocks * (block_c + L * codes_k + replay_rows) + copy_rows")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
         _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
                  and t.stride(3) == 1, f"{name} must be cuda bf16 [B, S0, {h}, {HEAD_DIM}] with contiguous dims")
@@ -442,7 +445,8 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     rc = lib().abkv_prefill_masked_attn(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
                                         k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2), B,
                                         block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota),
-                                        int(retain_tail), policy, xattn, L, cr, scale, _ptr(out), out.stride(0),
+                                        int(retain_tail), policy, xattn, L, cr, R, rx, scale, _ptr(out),
+                                        out.stride(0),
                                         out.stride(1), out.stride(2), _ptr(lse), C.c_void_p(_stream()))
     check(rc, "abkv_prefill_masked_attn")
     return out, lse
@@ -453,7 +457,8 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
                                       num_blocks: int, prompt_len: torch.Tensor | None = None,
                                       head_quota: torch.Tensor | None = None, scale: float | None = None,
                                       retain_tail: int = 0, tail_policy: str = "static", pause_xattn: str = "full",
-                                      pause_passes: int = 1, copy_rows: int = 0):
+                                      pause_passes: int = 1, copy_rows: int = 0, replay_rows: int = 0,
+                                      replay_exclude: bool = False):
     """Gradients (dq [B, S0, 32, 128], dk, dv [B, S0, 8, 128], bf16) of sum(dout * out) for
     :func:`prefill_masked_attention` under the same mask, from its out and lse (bf16 path only)."""
     B, S0 = q.shape[0], q.shape[1]
@@ -461,8 +466,9 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
     policy = tail_policy_code(tail_policy)
     xattn = xattn_code(pause_xattn)
     L, cr = _passes(pause_passes), _copy_rows(codes_k, pause_passes, copy_rows)
-    _require(S0 == num_blocks * (block_c + L * codes_k) + cr,
-             "seq_len must be num_blocks * (block_c + L * codes_k) + copy_rows")
+    R, rx = _replay(block_c, codes_k, retain_tail, replay_rows, replay_exclude)
+    _require(S0 == num_blocks * (block_c + L * codes_k + R) + cr,
+             "seq_len must be num_blocks * (block_c + L * codes_k + replay_rows) + copy_rows")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV), ("out", out, HEADS_Q),
                        ("dout", dout, HEADS_Q)):
         _require(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
@@ -484,7 +490,7 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
     for t in (q, k, v, out, dout):
         args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
     args += [_ptr(lse), B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota), int(retain_tail),
-             policy, xattn, L, cr, scale]
+             policy, xattn, L, cr, R, rx, scale]
     for t in (dq, dk, dv):
         args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
     rc = lib().abkv_prefill_masked_attn_bwd(*args, _ptr(ws), ws.numel(), C.c_void_p(_stream()))
@@ -515,6 +521,14 @@ def _passes(pause_passes) -> int:
     return int(pause_passes)
 
 
+def _replay(block_c, codes_k, retain_tail, replay_rows, replay_exclude) -> tuple[int, int]:
+    R = int(replay_rows)
+    _require(0 <= R <= block_c and R == replay_rows, "replay_rows must be an integer in [0, block_c]")
+    _require(not (R and (retain_tail or codes_k == 0)), "replay rows need code rows and exclude a retained tail")
+    _require(not replay_exclude or 0 < R < block_c, "replay_exclude requires replay_rows in [1, block_c)")
+    return R, int(bool(replay_exclude))
+
+
 def _copy_rows(codes_k, pause_passes, copy_rows) -> int:
     _require(int(codes_k) >= 0, "codes_k must be >= 0")
     _require(int(copy_rows) == copy_rows and int(copy_rows) >= 0, "copy_rows must be an integer >= 0")
@@ -524,10 +538,10 @@ def _copy_rows(codes_k, pause_passes, copy_rows) -> int:
 
 
 def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse, retain_tail,
-                        policy, xattn, passes, copy_rows):
+                        policy, xattn, passes, copy_rows, replay_rows=0, replay_exclude=0):
     B, S0 = q.shape[0], q.shape[1]
-    _require(S0 == num_blocks * (block_c + passes * codes_k) + copy_rows,
-             "seq_len must be num_blocks * (block_c + L * codes_k) + copy_rows")
+    _require(S0 == num_blocks * (block_c + passes * codes_k + replay_rows) + copy_rows,
+             "seq_len must be num_blocks * (block_c + L * codes_k + replay_rows) + copy_rows")
     for name, t, h in (("q", q, HEADS_Q), ("k", k, HEADS_KV), ("v", v, HEADS_KV)):
         _require(t.is_cuda and t.dtype == torch.float32 and t.dim() == 4 and tuple(t.shape) == (B, S0, h, HEAD_DIM)
                  and t.stride(3) == 1 and all(x % 4 == 0 for x in t.stride()[:3]),
@@ -549,7 +563,8 @@ def _prefill_masked_f32(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_
     rc = lib().abkv_prefill_masked_attn_f32(_ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
                                             k.stride(1), k.stride(2), _ptr(v), v.stride(0), v.stride(1), v.stride(2),
                                             B, block_c, codes_k, num_blocks, S0, _ptr(prompt_len), _ptr(head_quota),
-                                            retain_tail, policy, xattn, passes, copy_rows, scale, _ptr(out),
+                                            retain_tail, policy, xattn, passes, copy_rows, replay_rows,
+                                            replay_exclude, scale, _ptr(out),
                                             out.stride(0),
                                             out.stride(1), out.stride(2), _ptr(lse), C.c_void_p(_stream()))
     check(rc, "abkv_prefill_masked_attn_f32")

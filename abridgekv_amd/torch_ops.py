@@ -202,22 +202,25 @@ def _paged_prefill_attn_fake(q, kv_cache, block_table, q_start, kv_start, kv_lim
 def prefill_masked_attn(q: Tensor, k: Tensor, v: Tensor, block_c: int, codes_k: int, num_blocks: int,
                         prompt_len: Optional[Tensor], head_quota: Optional[Tensor], scale: float, out: Tensor,
                         lse: Optional[Tensor], retain_tail: int = 0, tail_policy: int = 0,
-                        pause_xattn: int = 0, pause_passes: int = 1, copy_rows: int = 0) -> None:
+                        pause_xattn: int = 0, pause_passes: int = 1, copy_rows: int = 0, replay_rows: int = 0,
+                        replay_exclude: bool = False) -> None:
     """abkv_prefill_masked_attn: attention under the compression mask, q [B, S0, 32, 128], k / v [B, S0, 8, 128]
     (retain_tail: T of a retained tail, 0 for none; tail_policy: 0 static, 1 rolling, 2 sticky; pause_xattn: 0 full,
     1 causal, 2 none; pause_passes: L passes of codes_k code rows per block; copy_rows: a copy region after the
-    blocks)."""
+    blocks; replay_rows / replay_exclude: the replay tail)."""
     _ops.prefill_masked_attention(q, k, v, block_c, codes_k, num_blocks, prompt_len=prompt_len,
                                   head_quota=head_quota, scale=scale, out=out, lse=lse, retain_tail=retain_tail,
                                   tail_policy=_ops.TAIL_POLICIES[tail_policy], pause_xattn=_ops.XATTN[pause_xattn],
-                                  pause_passes=pause_passes, copy_rows=copy_rows)
+                                  pause_passes=pause_passes, copy_rows=copy_rows, replay_rows=replay_rows,
+                                  replay_exclude=replay_exclude)
 
 
 @prefill_masked_attn.register_fake
 def _prefill_masked_attn_fake(q, k, v, block_c, codes_k, num_blocks, prompt_len, head_quota, scale, out, lse,
-                              retain_tail=0, tail_policy=0, pause_xattn=0, pause_passes=1, copy_rows=0):
-    _need(q.shape[1] == num_blocks * (block_c + pause_passes * codes_k) + copy_rows,
-          "seq_len must be num_blocks * (block_c + L * codes_k) + copy_rows")
+                              retain_tail=0, tail_policy=0, pause_xattn=0, pause_passes=1, copy_rows=0,
+                              replay_rows=0, replay_exclude=False):
+    _need(q.shape[1] == num_blocks * (block_c + pause_passes * codes_k + replay_rows) + copy_rows,
+          "seq_len must be num_blocks * (block_c + L * codes_k + replay_rows) + copy_rows")
     _need(tuple(out.shape) == tuple(q.shape), "out must be [B, S0, 32, 128]")
 
 
@@ -226,22 +229,24 @@ def prefill_masked_attn_bwd(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: T
                             codes_k: int, num_blocks: int, prompt_len: Optional[Tensor],
                             head_quota: Optional[Tensor], scale: float,
                             retain_tail: int = 0, tail_policy: int = 0,
-                            pause_xattn: int = 0, pause_passes: int = 1,
-                            copy_rows: int = 0) -> tuple[Tensor, Tensor, Tensor]:
+                            pause_xattn: int = 0, pause_passes: int = 1, copy_rows: int = 0, replay_rows: int = 0,
+                            replay_exclude: bool = False) -> tuple[Tensor, Tensor, Tensor]:
     """abkv_prefill_masked_attn_bwd: (dq, dk, dv) of sum(dout * out) under the same mask (new tensors)."""
     return _ops.prefill_masked_attention_backward(q, k, v, out, lse, dout, block_c, codes_k, num_blocks,
                                                   prompt_len=prompt_len, head_quota=head_quota, scale=scale,
                                                   retain_tail=retain_tail,
                                                   tail_policy=_ops.TAIL_POLICIES[tail_policy],
                                                   pause_xattn=_ops.XATTN[pause_xattn], pause_passes=pause_passes,
-                                                  copy_rows=copy_rows)
+                                                  copy_rows=copy_rows, replay_rows=replay_rows,
+                                                  replay_exclude=replay_exclude)
 
 
 @prefill_masked_attn_bwd.register_fake
 def _prefill_masked_attn_bwd_fake(q, k, v, out, lse, dout, block_c, codes_k, num_blocks, prompt_len, head_quota,
-                                  scale, retain_tail=0, tail_policy=0, pause_xattn=0, pause_passes=1, copy_rows=0):
-    _need(q.shape[1] == num_blocks * (block_c + pause_passes * codes_k) + copy_rows,
-          "seq_len must be num_blocks * (block_c + L * codes_k) + copy_rows")
+                                  scale, retain_tail=0, tail_policy=0, pause_xattn=0, pause_passes=1, copy_rows=0,
+                                  replay_rows=0, replay_exclude=False):
+    _need(q.shape[1] == num_blocks * (block_c + pause_passes * codes_k + replay_rows) + copy_rows,
+          "seq_len must be num_blocks * (block_c + L * codes_k + replay_rows) + copy_rows")
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 

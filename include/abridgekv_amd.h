@@ -150,8 +150,13 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
 #define ABKV_XATTN_FULL 0
 #define ABKV_XATTN_CAUSAL 1
 #define ABKV_XATTN_NONE 2
-/* copy_rows: a copy region after the N blocks (CompressLM.forward's copy_lambda, compress_forward.py:631-633,
- * 1185-1189), seq_len = N * (block_c + pause_passes * codes_k) + copy_rows: its rows see the last block's final pass
+/* replay_rows = R (replay_tail, compress_forward.py:20-31, 594-603): after each block's codes, R rows replaying its
+ * last R content tokens (block period block_c + pause_passes * codes_k + R): a replay row sees its block's content,
+ * final pass and replay rows (causally), and content row i of the next block sees the previous block's replay rows
+ * from row i on; replay_exclude (code_exclude_replay_tail) hides a block's last R content rows from its codes.
+ * Exclusive with retain_tail.
+ * copy_rows: a copy region after the N blocks (CompressLM.forward's copy_lambda, compress_forward.py:631-633,
+ * 1185-1189), seq_len = N * (block_c + pause_passes * codes_k + replay_rows) + copy_rows: its rows see the last block's final pass
  * (slots < quota) and the copy rows up to themselves, and no other row sees them. codes_k = 0 (pause_passes 1, no
  * copy rows): plain causal attention within blocks of block_c rows (the full-context baseline and teacher,
  * compress_forward.py:952-956, 1095-1105). */
@@ -159,9 +164,9 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
                              long k_stride_b, long k_stride_s, long k_stride_h, const void* v, long v_stride_b,
                              long v_stride_s, long v_stride_h, int batch, int block_c, int codes_k, int num_blocks,
                              int seq_len, const int32_t* prompt_len, const int32_t* head_quota, int retain_tail,
-                             int tail_policy, int pause_xattn, int pause_passes, int copy_rows, float scale,
-                             void* out, long out_stride_b, long out_stride_s, long out_stride_h, float* lse,
-                             abkv_stream_t stream);
+                             int tail_policy, int pause_xattn, int pause_passes, int copy_rows, int replay_rows,
+                             int replay_exclude, float scale, void* out, long out_stride_b, long out_stride_s,
+                             long out_stride_h, float* lse, abkv_stream_t stream);
 
 /* Backward of abkv_prefill_masked_attn: the gradients dq [batch, seq_len, 32, 128] and dk, dv [batch, seq_len, 8,
  * 128] (bf16, element strides, dims contiguous; written, not accumulated) of sum(dout * out) under the same mask,
@@ -176,7 +181,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
                                  long dout_stride_s, long dout_stride_h, const float* lse, int batch, int block_c,
                                  int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 int pause_passes, int copy_rows, float scale, void* dq,
+                                 int pause_passes, int copy_rows, int replay_rows, int replay_exclude, float scale,
+                                 void* dq,
                                  long dq_stride_b, long dq_stride_s, long dq_stride_h, void* dk, long dk_stride_b,
                                  long dk_stride_s, long dk_stride_h, void* dv, long dv_stride_b, long dv_stride_s,
                                  long dv_stride_h, void* workspace, size_t workspace_bytes, abkv_stream_t stream);
@@ -289,8 +295,8 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
                                  long k_ss, long k_sh, const float* v, long v_sb, long v_ss, long v_sh, int batch,
                                  int block_c, int codes_k, int num_blocks, int seq_len, const int32_t* prompt_len,
                                  const int32_t* head_quota, int retain_tail, int tail_policy, int pause_xattn,
-                                 int pause_passes, int copy_rows, float scale, float* out, long o_sb, long o_ss,
-                                 long o_sh, float* lse,
+                                 int pause_passes, int copy_rows, int replay_rows, int replay_exclude, float scale,
+                                 float* out, long o_sb, long o_ss, long o_sh, float* lse,
                                  abkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------

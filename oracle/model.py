@@ -32,10 +32,10 @@ from . import layout as ol
 from . import prefill as op
 
 
-def rope_positions(C, N, K, code_positions, span=None, passes=1):
-    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071, no replay tail); bitrev
-    code rows (one pass) spread over in-block offsets [0, span) (span None: C); appended rows keep their index."""
-    per = C + passes * K
+def rope_positions(C, N, K, code_positions, span=None, passes=1, replay=0):
+    """RoPE position of every row of the full-K layout (compress_forward.py:1044-1071); bitrev code rows (one pass,
+    no replay rows) spread over in-block offsets [0, span) (span None: C); appended rows keep their index."""
+    per = C + passes * K + replay
     pos = np.zeros(N * per, dtype=np.int64)
     offs = ol.bitrev_code_offsets(K, C, span) if code_positions == "bitrev" else None
     for b in range(N):
@@ -47,9 +47,9 @@ def rope_positions(C, N, K, code_positions, span=None, passes=1):
     return pos
 
 
-def loss_rows(C, N, K, passes=1):
+def loss_rows(C, N, K, passes=1, replay=0):
     """Rows whose hidden state predicts the next content token of the same block (content j = 0..C-2)."""
-    per = C + passes * K
+    per = C + passes * K + replay
     return np.array([b * per + j for b in range(N) for j in range(C - 1)], dtype=np.int64)
 
 
@@ -93,26 +93,31 @@ def _rotate_half(x):
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                  layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
-                 seeds=None, code_proj=None, copy_token=None, output_layers=False):
+                 seeds=None, code_proj=None, copy_token=None, output_layers=False, replay=0, replay_exclude=False):
     """Final-normed hidden states [B, S, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
     retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own pass's codes;
     ``passes``: pause passes per block; ``seeds`` [B, N, K, d] code inputs (None: ``pause``); ``code_proj``: per
     layer a dict of the code rows' projections ("qres" [passes * K, dq]; "q" / "k" / "v": (weight, bias or None));
     ``copy_token`` [d]: append the copy region [copy_token | last block's content] (compress_forward.py:1185-1189),
-    at positions after the layout's; ``output_layers``: also return every layer's output hidden states."""
+    at positions after the layout's; ``output_layers``: also return every layer's output hidden states;
+    ``replay``: R replay rows after each block's codes, fed the block's last R content tokens (compress_forward.py:
+    1180-1183), ``replay_exclude`` hiding those content rows from the codes."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
     tok_e = inner.embed_tokens(content_ids)
     d = tok_e.shape[-1]
     L = int(passes)
+    R = int(replay)
+    per = C + L * K + R
     code_in = pause.to(dt).view(1, 1, K, d).expand(B, N, K, d) if seeds is None else seeds.to(dt)
-    x = torch.cat([tok_e] + [code_in] * L, dim=2).reshape(B, N * (C + L * K), d)
+    x = torch.cat([tok_e] + [code_in] * L + ([tok_e[:, :, C - R:]] if R else []), dim=2).reshape(B, N * per, d)
     S0 = x.shape[1]
-    code_rows = torch.from_numpy(np.array([r for r in range(S0) if r % (C + L * K) >= C], dtype=np.int64))
-    slots = code_rows % (C + L * K) - C
-    pos = torch.from_numpy(rope_positions(C, N, K, code_positions, C - retain_tail, L)).view(1, -1)
+    code_rows = torch.from_numpy(np.array([r for r in range(S0) if C <= r % per < C + L * K], dtype=np.int64))
+    slots = code_rows % per - C
+    span = C - (R if replay_exclude else retain_tail)
+    pos = torch.from_numpy(rope_positions(C, N, K, code_positions, span, L, R)).view(1, -1)
     copy = 0
     if copy_token is not None:
         copy = 1 + C
@@ -128,7 +133,8 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     for li, layer in enumerate(inner.layers):
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
-        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L, copy)  # [B?, H?, S, S]
+        vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L, copy, R,
+                            replay_exclude)                                                   # [B?, H?, S, S]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -172,9 +178,9 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                       layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
-                      seeds=None, code_proj=None):
+                      seeds=None, code_proj=None, replay=0, replay_exclude=False):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
     h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail,
-                     tail_policy, pause_xattn, passes, seeds, code_proj)
-    rows = torch.from_numpy(loss_rows(C, N, K, passes))
+                     tail_policy, pause_xattn, passes, seeds, code_proj, replay=replay, replay_exclude=replay_exclude)
+    rows = torch.from_numpy(loss_rows(C, N, K, passes, replay))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

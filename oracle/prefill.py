@@ -11,6 +11,12 @@ compress_forward.py:20-31): pass l >= 1 reads its block's content and its pass l
 ``pause_xattn``, and later blocks read only the final pass L ("earlier_final", compress_forward.py:594-600); the
 quota counts a code row's slot within its pass ((within - C) % K, :576-577).
 
+``replay`` = R rows after a block's codes replay its last R content tokens (replay_tail, compress_forward.py:20-31,
+139-178, 594-603): a replay row sees its block's content, final-pass codes and replay rows (causally) besides what
+every row sees, and content row i of the next block sees the previous block's replay rows from row i on (a rolling
+window, _replay_tail_visible); with ``replay_exclude`` (code_exclude_replay_tail) a block's codes do not see its last
+R content rows. Replay and retained tails are mutually exclusive.
+
 ``copy_rows`` rows after the N blocks form the copy region (copy_lambda, compress_forward.py:631-633): a copy row
 sees the last block's final-pass codes (slot < quota) and the copy rows up to itself; no other row sees it. K = 0
 (no codes) leaves causal attention within blocks of C rows (the plain forward).
@@ -53,33 +59,43 @@ XATTN = ("full", "causal", "none")
 
 
 def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-               passes=1, copy_rows=0):
+               passes=1, copy_rows=0, replay=0, replay_exclude=False):
     """Boolean visibility [B?, H?, S, S] (leading dims only when prompt_len / head_quota are given),
-    S = N * (C + passes * K) + copy_rows."""
-    S = N * (C + passes * K) + copy_rows
+    S = N * (C + passes * K + replay) + copy_rows."""
+    S = N * (C + passes * K + replay) + copy_rows
     return arith_mask_block(C, K, N, np.arange(S), np.arange(S), prompt_len, head_quota, retain_tail, tail_policy,
-                            pause_xattn, passes, copy_rows)
+                            pause_xattn, passes, copy_rows, replay, replay_exclude)
 
 
 def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static",
-                     pause_xattn="full", passes=1, copy_rows=0):
+                     pause_xattn="full", passes=1, copy_rows=0, replay=0, replay_exclude=False):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
-    L = int(passes)
-    per = C + L * K
+    L, R = int(passes), int(replay)
+    if R and retain_tail:
+        raise ValueError("replay and retained tails are mutually exclusive")
+    LK = L * K
+    per = C + LK + R
     q = np.asarray(rows, dtype=np.int64).reshape(-1, 1)
     kv = np.asarray(cols, dtype=np.int64).reshape(1, -1)
     qb, kb = q // per, kv // per
     qw, kw = q - qb * per, kv - kb * per
     k_content = kw < C
+    k_code = (kw >= C) & (kw < C + LK)
+    q_code = (qw >= C) & (qw < C + LK)
     same_blk = kb == qb
     Kd = max(K, 1)
-    kp = np.where(k_content, 0, (kw - C) // Kd + 1)                        # pause pass of a code key (1..L)
-    qp = np.where(qw < C, 0, (qw - C) // Kd + 1)
+    kp = np.where(k_code, (kw - C) // Kd + 1, 0)                           # pause pass of a code key (1..L)
+    qp = np.where(q_code, (qw - C) // Kd + 1, 0)
     T = int(retain_tail)
     if tail_policy not in TAIL_POLICIES:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
-    vis = (k_content & same_blk) | ((kp == L) & (kb < qb))
+    vis = (k_content & same_blk) | (k_code & (kp == L) & (kb < qb))
+    if R:
+        q_rep, k_rep = qw >= C + LK, kw >= C + LK
+        vis = vis | (q_rep & k_code & (kp == L) & same_blk)                # a replay row: its block's final codes
+        vis = vis | (q_rep & k_rep & same_blk)                              # ... and replay rows (causal below)
+        vis = vis | ((qw < C) & k_rep & (kb + 1 == qb) & (kw - C - LK >= qw))   # rolling window of the next block
     if T and tail_policy == "static":
         vis = vis | (k_content & (kb < qb) & (kw >= C - T))                 # earlier blocks' static tails
     elif T:
@@ -94,16 +110,17 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
     vis = (kv <= q) & vis
     if pause_xattn not in XATTN:
         raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
-    own = (qw >= C) & (~k_content) & same_blk                               # code query, code key, same block
+    own = q_code & k_code & same_blk                                        # code query, code key, same block
     if L > 1:
         vis = vis | (own & (kp == qp - 1))                                  # pass l reads pass l - 1
     if pause_xattn != "none":                                               # code <-> code, same pass
         vis = vis | (own & (kp == qp) & ((kv <= q) if pause_xattn == "causal" else True))
-    if T:
-        vis = vis & ~((qw >= C) & same_blk & k_content & (kw >= C - T))    # codes never see their own tail
+    X = R if (R and replay_exclude) else T
+    if X:
+        vis = vis & ~(q_code & same_blk & k_content & (kw >= C - X))       # codes never see their own tail
     if head_quota is not None:
         hq = np.asarray(head_quota, dtype=np.int64).reshape(-1, 1, 1)
-        quota_ok = k_content | ((kw - C) % Kd < hq)               # [H, 1, S0]: the slot within its pass
+        quota_ok = ~k_code | ((kw - C) % Kd < hq)                 # [H, 1, S0]: the slot within its pass
         if vis.ndim == 3:
             vis = vis[:, None] & quota_ok[None]
         else:
@@ -120,24 +137,30 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
 
 
 def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-              passes=1, copy_rows=0):
-    """Same visibility from per-position role / block / content-position tables (the _dense_mask form); the copy
-    region as _mask_mod's ``copy`` term (compress_forward.py:627-633)."""
-    L = int(passes)
-    per = C + L * K
+              passes=1, copy_rows=0, replay=0, replay_exclude=False):
+    """Same visibility from per-position role / block / content-position tables (the _dense_mask form, with its
+    replay terms); the copy region as _mask_mod's ``copy`` term (compress_forward.py:627-633)."""
+    L, R = int(passes), int(replay)
+    per = C + L * K + R
     S0 = N * per
     idx = np.arange(S0)
     within, blk = idx % per, idx // per
-    role = np.where(within < C, 0, (within - C) // max(K, 1) + 1)  # 0 content, 1..L pause pass (_roles)
-    content_abs = np.where(role == 0, blk * C + within, -1)
-    code_slot = np.where(role > 0, (within - C) % max(K, 1), -1)
+    # 0 content, 1..L pause pass, L + 1 replay (_roles)
+    role = np.where(within < C, 0, np.where(within < C + L * K, (within - C) // max(K, 1) + 1, L + 1))
+    # content_abs of a replay row: the content position it replays (_content_abs_pos)
+    content_abs = np.where(role == 0, blk * C + within,
+                           np.where(role == L + 1, blk * C + (C - R) + (within - C - L * K), -1))
+    code_slot = np.where((role > 0) & (role <= L), (within - C) % max(K, 1), -1)
     qr, kr = role.reshape(S0, 1), role.reshape(1, S0)
     qb, kb = blk.reshape(S0, 1), blk.reshape(1, S0)
     causal = idx.reshape(1, S0) <= idx.reshape(S0, 1)
     content_vis = (kr == 0) & (kb == qb)
     earlier_final = (kr == L) & (kb < qb)
-    pause_q = qr > 0
+    pause_q = (qr > 0) & (qr <= L)
     refine = pause_q & (kr == qr - 1) & (kb == qb)
+    replay_q = qr == L + 1
+    replay_own_final = replay_q & (kr == L) & (kb == qb)
+    replay_causal = replay_q & (kr == L + 1) & (kb == qb)
     samepass = pause_q & (kr == qr) & (kb == qb)
     if pause_xattn not in XATTN:
         raise ValueError(f"unknown pause_xattn {pause_xattn!r}")
@@ -154,13 +177,16 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_pol
         retained = (qr == 0) & (kr == 0) & (kb + 1 == qb) & window & (T > 0)
     else:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
-    base = (causal & (content_vis | earlier_final | refine | retained)) | samepass
+    replay_tail = (qr == 0) & (kr == L + 1) & (kb + 1 == qb) & (qa - ka <= R) & (R > 0)
+    base = (causal & (content_vis | earlier_final | refine | retained | replay_own_final | replay_causal
+                      | replay_tail)) | samepass
     if prompt_len is not None:
         pl = np.asarray(prompt_len).reshape(-1, 1, 1)
         prompt_raw = (kr == 0)[None] & (content_abs.reshape(1, 1, S0) < pl) & (content_abs.reshape(1, 1, S0) >= 0)
         base = base[None] | (causal[None] & prompt_raw)
-    if T:
-        own_tail = pause_q & (kr == 0) & (kb == qb) & (content_abs.reshape(1, S0) % C >= C - T)
+    X = R if replay_exclude else T                                 # code_excluded_tail
+    if X:
+        own_tail = pause_q & (kr == 0) & (kb == qb) & (content_abs.reshape(1, S0) % C >= C - X)
         base = base & ~own_tail
     if head_quota is not None:
         hq = np.asarray(head_quota).reshape(-1, 1, 1)

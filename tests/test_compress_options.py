@@ -59,8 +59,10 @@ def test_refusals():
         CompressLM(_model(), 8, 2, 4, L=2, code_positions="bitrev")
     with pytest.raises(ValueError, match="active_code_rows"):
         CompressLM(_model(), 8, 2, 4, seg_pool=True, active_code_rows=2)
-    with pytest.raises(NotImplementedError, match="replay_tail"):
-        CompressLM(_model(), 8, 2, 4, replay_tail=2)
+    with pytest.raises(NotImplementedError, match="raw_tail"):
+        CompressLM(_model(), 8, 2, 4, raw_tail=2)
+    with pytest.raises(ValueError, match="code_exclude_replay_tail"):
+        CompressLM(_model(), 8, 2, 4, code_exclude_replay_tail=True)
     with pytest.raises(ValueError, match="positive"):
         CompressLM(_model(), 8, 2, 4, L=0)
 
@@ -137,3 +139,27 @@ def test_code_rows_follow_the_module_across_devices():
     assert rows.device.type == "meta" and slots.device.type == "meta" and rows.shape == (2 * 4,)
     rows, _ = cr.at(torch.device("cpu"))
     assert rows.device.type == "cpu" and rows.tolist() == [8, 9, 10, 11, 20, 21, 22, 23]
+
+
+@pytest.mark.parametrize("L,R", [(1, 3), (2, 2)])
+def test_replay_layout_matches_the_oracle(L, R):
+    """Replay rows after each block's codes (compress_forward.py:20-31, 72-88, 1044-1071): roles, replayed content
+    positions, RoPE positions against the oracle's layout and the reference's closed forms."""
+    from abridgekv_amd.compress_forward import CompressLM
+    C, N, K = 8, 3, 4
+    clm = CompressLM(_model(), C, N, K, L=L, replay_tail=R, code_exclude_replay_tail=True)
+    per = C + L * K + R
+    assert clm._pos_ids.view(-1).tolist() == list(om.rope_positions(C, N, K, "appended", passes=L, replay=R))
+    assert clm.role.tolist() == [0 if j < C else (j - C) // K + 1 if j < C + L * K else L + 1
+                                 for _ in range(N) for j in range(per)]
+    cap = [b * C + j if j < C else b * C + C - R + (j - C - L * K) if j >= C + L * K else N * C
+           for b in range(N) for j in range(per)]
+    assert clm.content_abs_pos.tolist() == cap
+    assert clm._code_rows.rows.tolist() == [b * per + j for b in range(N) for j in range(C, C + L * K)]
+    assert clm.code_excluded_tail == R
+    m = clm.compress_mask(1)
+    assert (m.replay_rows, m.replay_exclude) == (R, True)
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        CompressLM(_model(), C, N, K, replay_tail=2, retain_tail_kv=2)
+    with pytest.raises(ValueError, match="L=1 and no tails"):
+        CompressLM(_model(), C, N, K, replay_tail=2, code_positions="bitrev")

@@ -83,16 +83,18 @@ def test_paged_multi_query_f32_code_step_and_chunks(tail):
                                                            ([70, 0], "mixed", 20, "causal-codes"),
                                                            ([40, 0], "mixed", 12, "two-passes"),
                                                            (None, "mixed", 0, "copy-region"),
-                                                           (None, None, 0, "no-codes")])
+                                                           (None, None, 0, "no-codes"),
+                                                           ([40, 0], "mixed", 0, "replay")])
 def test_masked_prefill_f32_matches_fp64(prompt_len, quota, tail, policy):
     from abridgekv_amd import ops
     xattn = "causal" if policy == "causal-codes" else "full"
     L = 2 if policy in ("two-passes", "copy-region") else 1
     cr = 65 if policy == "copy-region" else 0
     K = 0 if policy == "no-codes" else 16
-    policy = "static" if policy in ("causal-codes", "two-passes", "copy-region", "no-codes") else policy
+    R = 12 if policy == "replay" else 0
+    policy = "static" if policy in ("causal-codes", "two-passes", "copy-region", "no-codes", "replay") else policy
     C, N, B = 64, 4, 2
-    S0 = N * (C + L * K) + cr
+    S0 = N * (C + L * K + R) + cr
     head_quota = None if quota is None else [1 + (h * 5) % max(K, 1) for h in range(32)]
     g = torch.Generator().manual_seed(7)
     q = torch.randn((B, S0, 32, 128), generator=g, dtype=torch.float32)
@@ -104,12 +106,13 @@ def test_masked_prefill_f32_matches_fp64(prompt_len, quota, tail, policy):
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
                                           lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
-                                          pause_passes=L, copy_rows=cr)
+                                          pause_passes=L, copy_rows=cr, replay_rows=R, replay_exclude=R > 0)
     torch.cuda.synchronize()
     got_o, got_l = out.cpu().numpy(), lse.cpu().numpy()
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=L, copy_rows=cr)
+                             tail_policy=policy, pause_xattn=xattn, passes=L, copy_rows=cr, replay=R,
+                             replay_exclude=R > 0)
         if prompt_len is not None:
             mask = mask[0]
         ro, rl = op.masked_attention_fp64(q[b].numpy(), k[b].numpy(), v[b].numpy(), mask, 128 ** -0.5)

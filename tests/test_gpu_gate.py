@@ -105,7 +105,8 @@ def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="s
     pause = clm.pause.detach().cpu()
     seg_mean = (gen_options or {}).get("code_init_override") == "segment_mean"
     seeds, proj = _seeds(clm, base, ids, seg_mean), _code_options(clm)
-    kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L)
+    kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L, replay=clm.replay_tail,
+              replay_exclude=clm.code_exclude_replay_tail)
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
                                lhq, seeds=seeds, code_proj=proj, **kw)
     eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq,
@@ -193,6 +194,9 @@ OPTION_CASES = [
      dict(code_kv_heads=True, retain_tail_kv=12, retain_tail_policy="rolling"), [40, 100], [16, 4], True, None),
     ("segment-mean override of the generator", 64, 3, 16, "bitrev", {}, [40, 100], [16, 4], True,
      {"code_init_override": "segment_mean"}),
+    ("replay tail", 64, 3, 16, "appended", dict(replay_tail=16), [40, 100], None, False, None),
+    ("replay tail hidden from the codes, two passes", 64, 3, 16, "appended",
+     dict(replay_tail=12, code_exclude_replay_tail=True, L=2, seg_pool=True), [70, 0], [16, 4], False, None),
 ]
 
 

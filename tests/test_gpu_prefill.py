@@ -15,9 +15,9 @@ def _bf16(x):
 
 
 def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail=0, policy="static", xattn="full",
-           passes=1, copy_rows=0):
+           passes=1, copy_rows=0, replay=0, replay_exclude=False):
     from abridgekv_amd import ops
-    S0 = N * (C + passes * K) + copy_rows
+    S0 = N * (C + passes * K + replay) + copy_rows
     g = torch.Generator().manual_seed(seed)
     q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
@@ -28,14 +28,16 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(q.to(dev), k.to(dev), v.to(dev), C, K, N, prompt_len=pl, head_quota=hq,
                                           lse=lse, retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
-                                          pause_passes=passes, copy_rows=copy_rows)
+                                          pause_passes=passes, copy_rows=copy_rows, replay_rows=replay,
+                                          replay_exclude=replay_exclude)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows)
+                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows,
+                             replay=replay, replay_exclude=replay_exclude)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -154,6 +156,21 @@ def test_copy_region(shape):
     else:
         quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
         _check(C=8, K=4, N=5, B=2, head_quota=quota, seed=33, tail=2, policy="static", copy_rows=9)
+
+
+@pytest.mark.parametrize("shape", ["aligned", "unaligned"])
+def test_replay_rows(shape):
+    """Replay rows after each block's codes (the last R content tokens again; the next block's content reads them
+    as a rolling window), with and without hiding the replayed rows from the codes, quotas, a raw prompt, passes and
+    a copy region."""
+    if shape == "aligned":
+        quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+        _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=37, replay=16)
+        _check(C=128, K=64, N=3, B=1, seed=38, replay=64, replay_exclude=True, passes=2, copy_rows=129)
+    else:
+        quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+        _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=39, replay=3, replay_exclude=True,
+               xattn="causal")
 
 
 @pytest.mark.parametrize("C,N", [(512, 1), (256, 3), (200, 2)])

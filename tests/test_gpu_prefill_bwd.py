@@ -10,9 +10,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy="static", xattn="full", passes=1,
-           copy_rows=0):
+           copy_rows=0, replay=0, replay_exclude=False):
     from abridgekv_amd import ops
-    S0 = N * (C + passes * K) + copy_rows
+    S0 = N * (C + passes * K + replay) + copy_rows
     g = torch.Generator().manual_seed(seed)
     q = torch.randn((B, S0, 32, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((B, S0, 8, 128), generator=g).to(torch.bfloat16)
@@ -25,16 +25,19 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy=
     lse = torch.empty((B, 32, S0), dtype=torch.float32, device=dev)
     out, _ = ops.prefill_masked_attention(qd, kd, vd, C, K, N, prompt_len=pl, head_quota=hq, lse=lse,
                                           retain_tail=tail, tail_policy=policy, pause_xattn=xattn,
-                                          pause_passes=passes, copy_rows=copy_rows)
+                                          pause_passes=passes, copy_rows=copy_rows, replay_rows=replay,
+                                          replay_exclude=replay_exclude)
     dq, dk, dv = ops.prefill_masked_attention_backward(qd, kd, vd, out, lse, gd, C, K, N, prompt_len=pl,
                                                        head_quota=hq, retain_tail=tail, tail_policy=policy,
-                                                       pause_xattn=xattn, pause_passes=passes, copy_rows=copy_rows)
+                                                       pause_xattn=xattn, pause_passes=passes, copy_rows=copy_rows,
+                                                       replay_rows=replay, replay_exclude=replay_exclude)
     torch.cuda.synchronize()
     got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
     worst = 0.0
     for b in range(B):
         mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows)
+                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows,
+                             replay=replay, replay_exclude=replay_exclude)
         if prompt_len is not None:
             mask = mask[0]
         ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
@@ -113,6 +116,12 @@ def test_pause_passes(passes):
 def test_copy_region():
     quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
     _check(C=128, K=64, N=3, B=2, head_quota=quota, seed=35, passes=2, copy_rows=129)
+
+
+@pytest.mark.parametrize("exclude", [False, True])
+def test_replay_rows(exclude):
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=40, replay=16, replay_exclude=exclude)
 
 
 @pytest.mark.parametrize("C,N", [(512, 1), (200, 2)])

@@ -66,6 +66,27 @@ def test_rope_positions_with_passes():
     C, N, K = 8, 3, 4
     assert list(om.rope_positions(C, N, K, "appended", passes=3)) == list(range(N * (C + 3 * K)))
     assert list(om.loss_rows(C, N, K, passes=2)) == [b * (C + 2 * K) + j for b in range(N) for j in range(C - 1)]
+    assert list(om.rope_positions(C, N, K, "appended", passes=2, replay=3)) == list(range(N * (C + 2 * K + 3)))
+    assert list(om.loss_rows(C, N, K, 1, 3)) == [b * (C + K + 3) + j for b in range(N) for j in range(C - 1)]
+
+
+@pytest.mark.parametrize("exclude", [False, True])
+def test_replay_rows_change_later_blocks_only(exclude):
+    """Replay rows follow a block's codes: the first block's content never sees them (its logits are the model's
+    causal forward), and the next block's content does."""
+    model = tiny_model()
+    C, N, K, R = 12, 2, 4, 3
+    ids = torch.randint(0, 97, (2, N, C))
+    pause = torch.randn(K, 64, dtype=torch.float64) * 0.05
+    got = om.dense_loss_logits(model, pause, ids, C, N, K, replay=R, replay_exclude=exclude)
+    with torch.no_grad():
+        ref = model(input_ids=ids[:, 0], position_ids=torch.arange(C).view(1, C)).logits[:, : C - 1]
+    per_seq = N * (C - 1)
+    for b in range(2):
+        assert torch.allclose(got[b * per_seq: b * per_seq + C - 1], ref[b].double(), atol=1e-6)
+    plain = om.dense_loss_logits(model, pause, ids, C, N, K)
+    later = slice(C - 1, per_seq)
+    assert not torch.allclose(got[later], plain[later], atol=1e-6)
 
 
 def _code_proj(model, K, L, seed, scale=0.05):

@@ -12,7 +12,8 @@ from oracle import prefill as op
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1, copy_rows=0):
+def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1, copy_rows=0,
+          replay=0, replay_exclude=False):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
@@ -26,24 +27,37 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
     codes"): a code row of pass l also reads its block's pass l - 1, the xattn rule speaks of its own pass, later
     blocks read the final pass only, and a quota counts a row's slot within its pass.
     Copy region (compress_forward.py:631, "copy region q>=S0: attend ONLY last block's K final codes + causal within
-    copy"): copy_rows rows after the blocks; the quota still hides code slots >= quota."""
-    per = C + passes * K
+    copy"): copy_rows rows after the blocks; the quota still hides code slots >= quota.
+    Replay rows (compress_forward.py:20-31, 139-178, "post-summary tail replay", "pause^l <- own pause^{l-1}";
+    _replay_tail_visible "Whether content query q may see a post-summary replay row from the preceding block"): the
+    R rows after a block's codes replay its last R content tokens; a replay row reads its block's content, final
+    codes and replay rows up to itself; content row i of the next block reads the previous block's replay rows whose
+    replayed position is within R of its own (replay row r with r >= i); with replay_exclude the codes do not read the
+    block's last R content rows."""
+    LK = passes * K
+    per = C + LK + replay
     S0 = N * per
     S = S0 + copy_rows
     m = np.zeros((S, S), bool)
     for q in range(S):
         if q >= S0:                              # a copy row
-            last_final = range(S0 - K, S0)       # the last block's final pass is the end of the blocks
+            lo = S0 - replay - K                 # the last block's final pass (before its replay rows)
             for k in range(q + 1):
-                m[q, k] = k >= S0 or (k in last_final and (quota is None or k - (S0 - K) < quota))
+                m[q, k] = k >= S0 or (lo <= k < lo + K and (quota is None or k - lo < quota))
             continue
         qb, qw = divmod(q, per)
-        q_pass = 0 if qw < C else (qw - C) // K + 1
+        q_rep = qw >= C + LK
+        q_pass = 0 if (qw < C or q_rep) else (qw - C) // K + 1
         for k in range(S0):
             kb, kw = divmod(k, per)
             k_content = kw < C
-            k_pass = 0 if k_content else (kw - C) // K + 1
+            k_rep = kw >= C + LK
+            k_pass = 0 if (k_content or k_rep) else (kw - C) // K + 1
             vis = (k_content and kb == qb) or (k_pass == passes and kb < qb)
+            if q_rep and kb == qb and (k_pass == passes or k_rep):
+                vis = True                       # a replay row: its block's final codes and replay rows
+            if replay and qw < C and k_rep and kb == qb - 1 and kw - C - LK >= qw:
+                vis = True                       # the previous block's replay rows, a rolling window
             if prompt_len is not None and k_content and kb * C + kw < prompt_len:
                 vis = True
             if tail and policy == "static" and k_content and kb < qb and kw >= C - tail:
@@ -54,14 +68,16 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
                     vis = True
             vis = vis and k <= q
             same_pass = q_pass == k_pass
-            if qw >= C and not k_content and kb == qb and same_pass and (xattn == "full" or
-                                                                         (xattn == "causal" and k <= q)):
+            q_code, k_code = q_pass > 0, k_pass > 0
+            if q_code and k_code and kb == qb and same_pass and (xattn == "full" or (xattn == "causal" and k <= q)):
                 vis = True
-            if qw >= C and not k_content and kb == qb and k_pass == q_pass - 1:
+            if q_code and k_code and kb == qb and k_pass == q_pass - 1:
                 vis = True                       # the previous pass of the same block
-            if tail and qw >= C and k_content and kb == qb and kw >= C - tail:
+            if tail and q_code and k_content and kb == qb and kw >= C - tail:
                 vis = False                      # a code row does not summarize its own block's tail
-            if quota is not None and not k_content and (kw - C) % K >= quota:
+            if replay_exclude and q_code and k_content and kb == qb and kw >= C - replay:
+                vis = False
+            if quota is not None and k_code and (kw - C) % K >= quota:
                 vis = False
             m[q, k] = vis
     return m
@@ -180,6 +196,31 @@ def test_copy_region_arith_equals_role_equals_brute(C, K, N, L):
     blk = np.arange(N * C) // C
     assert np.array_equal(plain, np.tril(np.ones((N * C, N * C), bool)) & (blk[:, None] == blk[None, :]))
     assert np.array_equal(plain, op.role_mask(C, 0, N))
+
+
+@pytest.mark.parametrize("C,K,N,L,R", [(4, 2, 3, 1, 2), (6, 2, 3, 2, 3), (4, 3, 3, 1, 4), (3, 2, 4, 1, 1)])
+def test_replay_rows_arith_equals_role_equals_brute(C, K, N, L, R):
+    for exclude, xattn in ((False, "full"), (True, "full"), (False, "causal"), (True, "none")):
+        kw = dict(passes=L, replay=R, replay_exclude=exclude, pause_xattn=xattn)
+        a = op.arith_mask(C, K, N, **kw)
+        assert np.array_equal(a, op.role_mask(C, K, N, **kw))
+        assert np.array_equal(a, brute(C, K, N, xattn=xattn, passes=L, replay=R, replay_exclude=exclude))
+        pl, hq = [0, C + 1], [1, K, 2, K]
+        ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, copy_rows=C + 1, **kw)
+        assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, copy_rows=C + 1, **kw))
+        for b, p in enumerate(pl):
+            for h, q in enumerate(hq):
+                assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, xattn=xattn, passes=L,
+                                                      copy_rows=C + 1, replay=R, replay_exclude=exclude))
+    per = C + L * K + R
+    m = op.arith_mask(C, K, N, passes=L, replay=R)
+    rep0 = C + L * K                                          # block 0's first replay row
+    assert m[rep0, 0] and m[rep0, rep0 - 1] and not m[rep0, rep0 + 1]      # content, final codes; causal replay
+    assert m[per, rep0] and m[per + 1, rep0 + 1] and not m[per + 1, rep0]  # content row i reads replay rows >= i
+    assert not m[2 * per, rep0]                                             # two blocks later: expired
+    assert not m[rep0, per]                                                 # the next block is hidden
+    with pytest.raises(ValueError):
+        op.arith_mask(C, K, N, replay=R, retain_tail=1)
 
 
 def test_window_tail_spot_checks():
