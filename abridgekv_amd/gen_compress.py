@@ -2,7 +2,7 @@
 
 Mirrors the public surface of abridgekv/gen_compress.py:85-1052 (``CompressGen``: ``feed_content``, ``compress``,
 ``step``, ``prefill``, ``generate``, ``cache_kv_stats``) for the served configuration (L=1, raw prompt, per-layer code
-quotas, no replay / raw tail, an optional retained tail) with bidirectional, causal or no code<->code attention in a
+quotas, an optional retained or replay tail, no raw tail) with bidirectional, causal or no code<->code attention in a
 code step (``pause_xattn``; only bidirectional with per-head packed pages). The reference keeps a
 dense per-layer store and masks it; here every layer's rows live in paged caches, quotas are physical, and the block
 boundary is a compaction:
@@ -30,6 +30,11 @@ boundary is a compaction:
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
+
+A replay tail of R rows (appended code positions): after its code step a block runs its last R tokens again as a
+causal chunk (they see the prompt, the codes the quotas leave -- the code part of the block's removals runs first --
+and the block's content, which leaves after them); content token i of the next block expires replay row i, a chunk
+ending at each such token (gen_compress.py:900-916, processor.py:336-345, 594-618).
 
 Code-step inputs follow the model's seed pools (``seg_pool``, ``gated_seg_pool``, ``pool_init`` or
 ``code_init_override="segment_mean"``: gen_compress.py:867-898). A model trained with code-row projections
@@ -122,10 +127,18 @@ class CompressGen:
         self.xattn = getattr(clm, "pause_xattn", "full")
         if self.xattn not in ("full", "causal", "none"):
             raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {self.xattn!r}")
-        if any(getattr(clm, name, 0) for name in ("replay_tail", "raw_tail")):
-            raise NotImplementedError("the paged path serves no replay / raw tails")
+        if getattr(clm, "raw_tail", 0):
+            raise NotImplementedError("the paged path serves no raw tail")
         self.T = int(getattr(clm, "retain_tail_kv", 0) or 0)
         self.policy = getattr(clm, "retain_tail_policy", "rolling") if self.T else "static"
+        # replay tail (gen_compress.py:900-916): R rows after each block's codes, fed its last R content tokens; the
+        # next block's content token i expires replay row i (processor.py:336-345, 594-618)
+        self.R = int(getattr(clm, "replay_tail", 0) or 0)
+        if self.R and self.code_positions_of(clm) == "bitrev":
+            raise ValueError("a replay tail needs appended code positions")
+        # the block's last content rows its own codes do not see: the retained tail, or the replayed rows with
+        # code_exclude_replay_tail (compress_forward.py:298-300)
+        self.X = self.R if getattr(clm, "code_exclude_replay_tail", False) else self.T
         self.clm = clm
         self.inner = clm.model.model
         self.layers = self.inner.layers
@@ -203,14 +216,14 @@ class CompressGen:
     # -- positions ------------------------------------------------------------------------------------------------
     def _content_pos(self, n):
         """RoPE positions of the next n content tokens of block b (gen_compress.py:789-795)."""
-        base = self.b * self.C if self.code_positions == "bitrev" else self.b * (self.C + self.K)
+        base = self.b * self.C if self.code_positions == "bitrev" else self.b * (self.C + self.K + self.R)
         return torch.arange(base + self.f, base + self.f + n, device=self.device)
 
     def _code_pos(self):
         """RoPE positions of the K code rows of block b (gen_compress.py:797-804)."""
         if self.code_positions == "bitrev":
             return self.b * self.C + self._code_offsets
-        base = self.b * (self.C + self.K)
+        base = self.b * (self.C + self.K + self.R)
         return torch.arange(base + self.C, base + self.C + self.K, device=self.device)
 
     # -- one step over all layers ---------------------------------------------------------------------------------
@@ -229,7 +242,7 @@ class CompressGen:
             own = min(q, self.K) if self.xattn != "none" else 0
             limit = [start + own] if code_step else None
             # the block's own retained tail: its last T content rows, just before the code rows in every group
-            excluded = [[start - self.T, start]] if code_step and self.T else None
+            excluded = [[start - self.X, start]] if code_step and self.X else None
             causal = [self.xattn == "causal"] if code_step else None
             out.append(self.builder.build([0, n], [seq_len], table, code_key_limit=limit, positions=logical,
                                           compacted=comp_dev[g:g + 1], code_excluded=excluded, code_causal=causal))
@@ -279,6 +292,10 @@ class CompressGen:
         self.planner.set_num_computed_tokens(self.rid, self.logical_len)
         return hidden
 
+    @staticmethod
+    def code_positions_of(clm):
+        return getattr(clm, "code_positions", "appended")
+
     def _code_seeds(self):
         """Inputs [K, d] of the block's code rows (the content embeddings feed the seed pools)."""
         tok_e = self.inner.embed_tokens(torch.tensor([self._cur_ids], device=self.device))
@@ -286,9 +303,11 @@ class CompressGen:
 
     # -- reference surface ----------------------------------------------------------------------------------------
     def _remove(self, spans):
-        """Run span removals (logical [start, end), every group) through the planner and move the rows."""
-        for start, end in spans:
-            CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end)
+        """Run span removals (logical [start, end) in every group, or (start, end, groups)) through the planner and
+        move the rows."""
+        for span in spans:
+            start, end, groups = span if len(span) == 3 else (*span, None)
+            CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end, groups)
         _, _, fused = self.planner.take_step_outputs(as_arrays=True)
         execute_fused_moves(fused.copy(), self.caches_by_group)
 
@@ -301,7 +320,7 @@ class CompressGen:
         outs, i = [], 0
         while i < n:
             take = n - i
-            if self.policy == "rolling":
+            if self.policy == "rolling" or self.R:
                 # the chunk ends at the first content token whose tail row of the previous block expires
                 for j in range(self.f, min(self.f + take, len(self._window))):
                     if self._window[j] is not None:
@@ -310,7 +329,7 @@ class CompressGen:
             part = ids[i:i + take]
             hidden = self.inner.embed_tokens(torch.tensor([list(part)], device=self.device))
             outs.append(self._forward_rows(hidden, code_step=False))
-            if self.policy == "rolling" and self.f + take - 1 < len(self._window) and \
+            if (self.policy == "rolling" or self.R) and self.f + take - 1 < len(self._window) and \
                     self._window[self.f + take - 1] is not None:
                 row, self._window[self.f + take - 1] = self._window[self.f + take - 1], None
                 self._remove([(row, row + 1)])
@@ -348,6 +367,18 @@ class CompressGen:
             phys = code_start - self.planner.compacted_counts(self.rid)[0]
             table = self.planner.get_blocks(self.rid)[0]
             self.sidecar.capture(self.rid, physical_start=phys, physical_end=phys + K, block_ids=table)
+        if self.R:
+            # The replay rows (the block's last R tokens again, after its codes) run while the block's content is
+            # resident but must see only the code rows the quotas leave: the code part of the removals goes first
+            # (code slots >= q per group; with packed pages every paged code row, the sidecar now holding them),
+            # then the replay chunk, then the content part. The kept rows are those of the processor's order.
+            code_part = [(max(a, code_start), e, g) for a, e, g in spans if e > code_start]
+            content_part = [(a, min(e, code_start), g) for a, e, g in spans if a < code_start]
+            self._remove(code_part)
+            replay_ids = self._cur_ids[-self.R:]
+            self._forward_rows(self.inner.embed_tokens(torch.tensor([replay_ids], device=self.device)),
+                               code_step=False)
+            spans = content_part
         for start, end, groups in spans:
             CompressLMProcessor._mask_or_raise(self.planner.mask_token_span, self.rid, start, end, groups)
         _, _, fused = self.planner.take_step_outputs(as_arrays=True)
@@ -355,6 +386,9 @@ class CompressGen:
         if self.policy != "static":
             # this block's tail rows, by tail index, that the next block's content may still expire (response rows)
             self._window = [p if p >= resp_from else None for p in range(code_start - self.T, code_start)]
+        if self.R:
+            # every replay row expires, prompt blocks' too (processor.py:336-345)
+            self._window = list(range(code_start + K, code_start + K + self.R))
         self.b += 1
         self.f = 0
         self._cur_ids = []

@@ -125,8 +125,8 @@ def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="s
     rows_per_seq = N * (C - 1)
     for bi in range(2):
         p = 0 if prompt is None else prompt[bi]
-        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=hcq, max_tokens=N * (C + K) + 16,
-                        **(gen_options or {}))
+        g = CompressGen(clm, dev, raw_prompt_len=p, head_code_quotas=hcq,
+                        max_tokens=N * (C + K + clm.replay_tail) + 16, **(gen_options or {}))
         got = []
         for blk in range(N):
             toks = ids[bi, blk].tolist()
@@ -142,6 +142,8 @@ def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="s
             first = 0 if policy == "static" else blk
             tails = sum(min(T, (b + 1) * C - max(p, b * C)) for b in range(first, blk + 1) if (b + 1) * C > p) \
                 if T else 0
+            # the closed block's replay rows stay until the next block's content expires them
+            tails += clm.replay_tail
             if per_head:
                 assert g.resident_rows() == [kept_prompt + tails] * 2
                 assert g.packed_rows() == [(blk + 1) * sum(row) for row in hcq]
@@ -194,7 +196,11 @@ OPTION_CASES = [
      dict(code_kv_heads=True, retain_tail_kv=12, retain_tail_policy="rolling"), [40, 100], [16, 4], True, None),
     ("segment-mean override of the generator", 64, 3, 16, "bitrev", {}, [40, 100], [16, 4], True,
      {"code_init_override": "segment_mean"}),
-    ("replay tail", 64, 3, 16, "appended", dict(replay_tail=16), [40, 100], None, False, None),
+    ("replay tail", 64, 3, 16, "appended", dict(replay_tail=16), [40, 100], None, True, None),
+    ("replay tail hidden from the codes, per-layer quotas", 64, 4, 16, "appended",
+     dict(replay_tail=12, code_exclude_replay_tail=True), [70, 0], [16, 4], True, None),
+    ("replay tail with per-head packed pages", 64, 3, 16, "appended", dict(replay_tail=16), [40, 100],
+     [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], True, None),
     ("replay tail hidden from the codes, two passes", 64, 3, 16, "appended",
      dict(replay_tail=12, code_exclude_replay_tail=True, L=2, seg_pool=True), [70, 0], [16, 4], False, None),
 ]
