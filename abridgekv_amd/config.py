@@ -1,15 +1,17 @@
 """Serving configuration of the abridged cache (API-compatible subset of the reference's CompressLMConfig).
 
-Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309 for the configuration this path serves: one pause
-pass, raw prompt, bitrev code positions, an optional retained tail of T = retain_tail_kv original content rows
-per block (compresslm.py:22-26): "static" keeps the last T content rows of every block resident for every later
-query; the window policies keep the previous block's tail for the next block's content queries only, "rolling"
-expiring one row per next-block content token and "sticky" all of it before the next block's codes. The codes of a
-block summarize only its first C - T content rows (compresslm.py:192-206, 254-257). Optional per-layer quotas with
-physical removal, or per-head quotas in packed KV pages (packed_kv, packed_kv_k_max, packed_kv_quotas; validated as
-at compresslm.py:145-190; packed KV takes only the static tail). Options of the reference that belong to other modes
-(replay / raw tails, selective full-history evaluation) are rejected with ValueError instead of being silently
-ignored.
+Mirrors third_party/vllm_overlay/vllm/config/compresslm.py:9-309, with its defaults (appended code positions, a
+replay tail of 16), for the configurations its serving path decodes: one pause pass, raw prompt, ``appended`` or
+``bitrev`` code positions; either a replay tail of R = replay_tail rows (appended positions: after its codes a block
+runs its last R content tokens again; the next block's content token i expires replay row i; with
+code_exclude_replay_tail the codes do not see those content rows) or a retained tail of T = retain_tail_kv original
+content rows per block (compresslm.py:22-26): "static" keeps the last T content rows of every block resident for
+every later query; the window policies keep the previous block's tail for the next block's content queries only,
+"rolling" expiring one row per next-block content token and "sticky" all of it before the next block's codes. The
+codes of a block summarize only its first C - T content rows (compresslm.py:192-206, 254-257). Optional per-layer
+quotas with physical removal (bitrev positions), or per-head quotas in packed KV pages (packed_kv, packed_kv_k_max,
+packed_kv_quotas; validated as at compresslm.py:145-190; packed KV takes no window tail). The raw tail and selective
+full-history evaluation are rejected with ValueError instead of being silently ignored.
 """
 from __future__ import annotations
 
@@ -78,7 +80,7 @@ class CompressLMConfig:
     enable: bool = False
     block_size: int = 512
     num_code_tokens: int = 128
-    replay_tail: int = 0
+    replay_tail: int = 16
     retain_tail_kv: int = 0
     retain_tail_policy: str = "rolling"
     code_exclude_replay_tail: bool = False
@@ -88,7 +90,7 @@ class CompressLMConfig:
     raw_tail: int = 0
     code_token_format: str = "<|compress_code_{:03d}|>"
     debug: bool = False
-    code_positions: str = "bitrev"
+    code_positions: str = "appended"
     layer_code_quotas: tuple[int, ...] = ()
     physical_layer_quotas: bool = False
     retain_full_history_layers: tuple[int, ...] = ()
@@ -114,22 +116,28 @@ class CompressLMConfig:
             raise ValueError("block_size must be positive")
         if K <= 0:
             raise ValueError("num_code_tokens must be positive")
-        if self.code_positions != "bitrev":
-            raise ValueError("only code_positions='bitrev' is served")
-        if (C & (C - 1)) or (K & (K - 1)):
-            raise ValueError("code_positions=bitrev needs power-of-two block_size and num_code_tokens")
-        if self.replay_tail or self.raw_tail or self.code_exclude_replay_tail:
-            raise ValueError("replay / raw tails are not served")
+        if self.code_positions == "bitrev":
+            if (C & (C - 1)) or (K & (K - 1)) or self.replay_tail or self.raw_tail or self.num_passes != 1:
+                raise ValueError("code_positions=bitrev needs power-of-two block_size and num_code_tokens, "
+                                 "no replay/raw tail and num_passes=1")
+        if not 0 <= self.replay_tail <= C:
+            raise ValueError("replay_tail must be in [0, block_size]")
         if not 0 <= self.retain_tail_kv < C:
             raise ValueError("retain_tail_kv must be in [0, block_size)")
         if self.retain_tail_policy == "sticky" and not self.retain_tail_kv:
             raise ValueError("retain_tail_policy='sticky' requires retain_tail_kv > 0")
-        if C - self.retain_tail_kv < K:
-            raise ValueError(f"bitrev code span {C - self.retain_tail_kv} < num_code_tokens {K}")
+        if sum(bool(v) for v in (self.raw_tail, self.replay_tail, self.retain_tail_kv)) > 1:
+            raise ValueError("raw_tail, replay_tail, and retain_tail_kv are mutually exclusive")
+        if self.code_exclude_replay_tail and not 0 < self.replay_tail < C:
+            raise ValueError("code_exclude_replay_tail requires replay_tail in [1, block_size)")
+        if self.code_positions == "bitrev" and C - self.code_excluded_tail < K:
+            raise ValueError(f"bitrev code span {C - self.code_excluded_tail} < num_code_tokens {K}")
         if self.num_passes != 1:
             raise ValueError("CompressLM decoding supports num_passes=1 only")
         if self.pause_xattn != "full":
             raise ValueError("CompressLM decoding requires pause_xattn='full'")
+        if self.raw_tail:
+            raise ValueError("vLLM CompressLM decoding currently supports raw_tail=0 only")
         if not self.raw_prompt:
             raise ValueError("CompressLM decoding requires raw_prompt=True")
         if self.retain_full_history_layers:
@@ -137,12 +145,17 @@ class CompressLMConfig:
         for layer, q in enumerate(self.layer_code_quotas):
             if not 0 < q <= K:
                 raise ValueError(f"layer_code_quotas[{layer}]={q} must be in [1, {K}]")
+        if self.uses_layer_quotas and self.code_positions != "bitrev":
+            raise ValueError("layer_code_quotas below num_code_tokens need code_positions=bitrev (nested-prefix code "
+                             "layout)")
         if self.packed_kv and any(q < K for q in self.layer_code_quotas):
             raise ValueError("layer_code_quotas and packed KV are mutually exclusive")
         if self.packed_kv:
             if self.retain_tail_kv and self.retain_tail_policy != "static":
                 raise ValueError("packed KV supports code/replay checkpoints and the static retained tail, not window "
                                  "(rolling/sticky) or raw tails")
+            if self.code_exclude_replay_tail:
+                raise ValueError("packed KV does not yet support code_exclude_replay_tail")
             if self.packed_kv_k_max != K:
                 raise ValueError("packed_kv_k_max must equal num_code_tokens so the dense code pass computes every "
                                  "schedulable slot")
@@ -203,9 +216,10 @@ class CompressLMConfig:
     # -- positions ------------------------------------------------------------------------------------------------
     @property
     def code_excluded_tail(self) -> int:
-        """Content rows at the end of each block that the block's own codes never see and do not summarize (the
-        retained tail, whatever its policy: compresslm.py:254-257 with no replay tail)."""
-        return self.retain_tail_kv
+        """Content rows at the end of each block that the block's own codes never see and do not summarize: the
+        replayed rows with code_exclude_replay_tail, else the retained tail, whatever its policy
+        (compresslm.py:254-260)."""
+        return self.replay_tail if self.code_exclude_replay_tail else self.retain_tail_kv
 
     def bitrev_code_offsets(self) -> np.ndarray:
         """In-block RoPE offsets of the code rows (config/compresslm.py:192-206)."""

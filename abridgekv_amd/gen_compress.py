@@ -185,7 +185,8 @@ class CompressGen:
         self.planner.add_request(self.rid)
         # the block state machine's compaction rule for these groups (the serving validation of an enabled config --
         # bitrev positions, power-of-two sizes -- is the vLLM path's; the generator also runs appended positions)
-        pcfg = CompressLMConfig(block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
+        pcfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                                block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
                                 packed_kv_k_max=self.K, retain_tail_kv=self.T,
                                 retain_tail_policy=self.policy if self.T else "rolling")
         pcfg.set_code_token_ids(range(1 << 20, (1 << 20) + self.K))

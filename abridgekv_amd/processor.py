@@ -1,15 +1,21 @@
 """Scheduler-side block state machine: which tokens run when, and which spans are compacted.
 
 API-compatible with the reference's CompressLMProcessor (third_party/vllm_overlay/vllm/v1/core/compresslm/
-processor.py) for the served configuration (one pause pass, raw prompt, bitrev positions, no replay tail, an optional
-retained tail under the static, rolling or sticky policy, physical per-layer quotas or per-head packed KV pages):
+processor.py) for the served configuration (one pause pass, raw prompt, appended or bitrev positions, a replay tail or
+a retained tail under the static, rolling or sticky policy, physical per-layer quotas or per-head packed KV pages):
 prepare_request :42-105, is_code_ready / num_code_rows_pending :106-121, limit_num_new_tokens :123-151,
 should_skip_sampling :153-168, update_after_step :170-257, reset_for_preemption :259-260 (state.py:46-50),
 code_excluded_logical_range :262-274, code_physical_spans :276-316, _record_content :318-353, _stage_codes :369-400,
-_finish_block :419-465, _compact_response_content :467-557, _expire_sticky_retained_tail_at_boundary :559-592,
+_stage_replay :402-417, _finish_block :419-465, _compact_response_content :467-557,
+_expire_sticky_retained_tail_at_boundary :559-592, _expire_replay_after_content :594-618,
 _expire_retained_tail_after_content :614-646, _mask_or_raise :648-661, _check_stop :663-685; the physical exclusion
 ranges of a code step restate sched/scheduler.py:979-991. The compaction callback
 ``mask_span(request_id, start, end, groups=None)`` is KVPlanner.mask_token_span.
+
+Replay tail: after a block's code run its last R content tokens are appended again (role REPLAY) and run as
+ordinary chunks while the block's content is still resident; the block is compacted after them; the next block's
+i-th content token removes replay row i after its step (prompt blocks' too), a content chunk ending at each such
+token.
 
 Window tails: a block's last T content rows survive its compaction; under "rolling" the i-th content token of the
 next block removes the tail's i-th row (a response row; raw-prompt rows stay) after its step, and a content chunk
@@ -24,7 +30,7 @@ from dataclasses import dataclass, field
 
 from .config import CompressLMConfig
 
-CONTENT, CODE = 0, 1
+CONTENT, CODE, REPLAY = 0, 1, 2
 
 MaskSpan = Callable[..., object]
 
@@ -60,6 +66,7 @@ class CompressLMBlock:
     prompt_content_positions: list[int] = field(default_factory=list)
     response_content_positions: list[int] = field(default_factory=list)
     code_span: tuple[int, int] | None = None
+    replay_positions: list[int] = field(default_factory=list)
     retained_tail_positions: list[int] = field(default_factory=list)
     code_excluded_content_span: tuple[int, int] | None = None
 
@@ -76,6 +83,8 @@ class CompressLMState:
     compacted_block_ids: set[int] = field(default_factory=set)
     current_block_id: int = 0
     worker_token_ids_dirty: bool = False
+    content_to_expired_replay: dict[int, int] = field(default_factory=dict)
+    expired_replay_positions: set[int] = field(default_factory=set)
     content_to_expired_retained_tail: dict[int, int] = field(default_factory=dict)
     expired_retained_tail_positions: set[int] = field(default_factory=set)
     expired_sticky_retained_block_ids: set[int] = field(default_factory=set)
@@ -85,6 +94,7 @@ class CompressLMState:
         return self.blocks[self.current_block_id]
 
     def reset_compaction_progress(self) -> None:
+        self.expired_replay_positions.clear()
         self.expired_retained_tail_positions.clear()
         self.expired_sticky_retained_block_ids.clear()
         self.compacted_block_ids.clear()
@@ -143,10 +153,14 @@ class ServingRequest:
 
 def _run_end(roles: list[int], start: int, stop: int) -> int:
     """End of the run of equal roles that begins at ``start`` (scanning no further than ``stop``)."""
-    try:
-        return roles.index(CODE + CONTENT - roles[start], start + 1, stop)
-    except ValueError:
-        return max(stop, start + 1)
+    end = max(stop, start + 1)
+    for other in (CONTENT, CODE, REPLAY):
+        if other != roles[start]:
+            try:
+                end = min(end, roles.index(other, start + 1, stop))
+            except ValueError:
+                pass
+    return end
 
 
 def _no_mask(*_args, **_kwargs):
@@ -254,11 +268,12 @@ class CompressLMProcessor:
         if role == CODE:
             return remaining if proposed >= remaining else 0
         limit = min(proposed, remaining)
-        expiring = state.content_to_expired_retained_tail
-        if expiring:                                      # a rolling expiry ends the chunk
-            for pos in range(start, start + limit):
-                if pos in expiring:
-                    return pos - start + 1
+        if role == CONTENT:                               # a replay or rolling-tail expiry ends the chunk
+            replay, tail = state.content_to_expired_replay, state.content_to_expired_retained_tail
+            if replay or tail:
+                for pos in range(start, start + limit):
+                    if pos in replay or pos in tail:
+                        return pos - start + 1
         return limit
 
     def should_skip_sampling(self, request, num_scheduled_tokens: int) -> bool:
@@ -287,6 +302,8 @@ class CompressLMProcessor:
         role = state.roles[start]
         if _run_end(state.roles, start, end) != end:
             raise RuntimeError("CompressLM scheduled a mixed-role model step")
+        if role == CONTENT and state.content_to_expired_replay:
+            self._expire_replay_after_content(state, request, start, end, mask_span)
         if role == CONTENT and state.content_to_expired_retained_tail:
             self._expire_retained_tail_after_content(state, request, start, end, mask_span)
         sampled = sampled_token_ids[0] if sampled_token_ids else None
@@ -305,7 +322,7 @@ class CompressLMProcessor:
                     # the codes exist already)
                     self._expire_sticky_retained_tail_at_boundary(request, state, block, mask_span)
                 if block.code_span is None:
-                    if end + self.config.num_code_tokens >= max_model_len:
+                    if end + self.config.num_code_tokens + self.config.replay_tail >= max_model_len:
                         request.status = RequestStatus.FINISHED_LENGTH_CAPPED
                         return visible, True
                     state.held_sampled_token = sampled
@@ -313,6 +330,11 @@ class CompressLMProcessor:
             elif sampled is not None:
                 self._append_content(request, state, [sampled], is_prompt=False)
         elif role == CODE and role_end:
+            if not block.replay_positions:
+                self._stage_replay(request, state, block)
+                if not block.replay_positions:
+                    self._finish_block(request, state, block, mask_span, pack_code_span)
+        elif role == REPLAY and role_end:
             self._finish_block(request, state, block, mask_span, pack_code_span)
         return visible, False
 
@@ -320,7 +342,8 @@ class CompressLMProcessor:
         """``len(sampled_token_ids)`` consecutive one-token decode steps of one request at once, for replaying a known
         history: the same state as calling :meth:`update_after_step` once per step with ``num_scheduled_tokens=1``
         and the i-th sampled token, for a stretch in which no step computes the block's last content token (that step
-        stages the codes) and no sampled token stops the request. ``request.num_computed_tokens`` already includes
+        stages the codes), expires a replay row or a retained tail row (those steps issue removals) and no sampled
+        token stops the request. ``request.num_computed_tokens`` already includes
         the steps. Anything else (a stretch reaching the block end, a possible stop) is stepped one by one."""
         ids = list(sampled_token_ids)
         m = len(ids)
@@ -339,6 +362,8 @@ class CompressLMProcessor:
                 and len(block.content_positions) + m <= self.config.block_size
                 and block.content_positions[-1] == start and (not stops or stops.isdisjoint(ids))
                 and (not self._rolling or not block.block_id or len(block.content_positions) > self._rolling)
+                and (not block.block_id or len(block.content_positions) >
+                     len(state.blocks[block.block_id - 1].replay_positions))
                 and request.num_tokens + m < max_model_len
                 and len(state.visible_output_token_ids) + m < request.max_tokens)
         if not fast:
@@ -424,6 +449,11 @@ class CompressLMProcessor:
         (block.prompt_content_positions if is_prompt else block.response_content_positions).extend(positions)
         state.roles.extend([CONTENT] * n)
         state.position_to_block.extend([block.block_id] * n)
+        if block.block_id:
+            # the i-th content token of the block expires the previous block's i-th replay row
+            rep = state.blocks[block.block_id - 1].replay_positions
+            for i in range(within, min(within + n, len(rep))):
+                state.content_to_expired_replay[start + i - within] = rep[i]
         if self._rolling and block.block_id and within < self._rolling:
             # the i-th content token of the block expires the previous block's i-th tail row if it is a response
             # row (a block's response rows are one contiguous run after its prompt rows)
@@ -449,7 +479,9 @@ class CompressLMProcessor:
         T = self.config.retain_tail_kv
         if T:
             block.retained_tail_positions = block.content_positions[-T:]
-            tail = block.content_positions[-self.config.code_excluded_tail:]
+        X = self.config.code_excluded_tail
+        if X:
+            tail = block.content_positions[-X:]
             if tail != list(range(tail[0], tail[-1] + 1)):
                 raise RuntimeError("exact tail source positions must be contiguous")
             block.code_excluded_content_span = (tail[0], tail[-1] + 1)
@@ -457,11 +489,25 @@ class CompressLMProcessor:
         state.position_to_block.extend([block.block_id] * len(ids))
         state.worker_token_ids_dirty = True
 
+    def _stage_replay(self, request, state, block) -> None:
+        """Append the block's last R content tokens after its codes as replay tokens (processor.py:402-417)."""
+        R = self.config.replay_tail
+        if not R:
+            return
+        ids = block.content_token_ids[-R:]
+        start = request.num_tokens
+        request.append_output_token_ids(ids)
+        block.replay_positions = list(range(start, start + len(ids)))
+        state.roles.extend([REPLAY] * len(ids))
+        state.position_to_block.extend([block.block_id] * len(ids))
+        state.worker_token_ids_dirty = True
+
     def _finish_block(self, request, state, block, mask_span, pack_code_span=None) -> None:
         if self._sticky:                                      # done at the block's last content step already
             self._expire_sticky_retained_tail_at_boundary(request, state, block, mask_span)
         self._compact_response_content(request, state, block, mask_span, pack_code_span)
-        if block.code_span[1] < request.num_tokens:          # preemption replay: later tokens already exist
+        last = block.replay_positions[-1] + 1 if block.replay_positions else block.code_span[1]
+        if last < request.num_tokens:                        # preemption replay: later tokens already exist
             return
         nxt = CompressLMBlock(block_id=len(state.blocks))
         state.blocks.append(nxt)
@@ -543,6 +589,17 @@ class CompressLMProcessor:
                 raise RuntimeError("sticky retained response tail must be contiguous")
             self._mask_or_raise(mask_span, request.request_id, rows[0], rows[-1] + 1)
         state.expired_sticky_retained_block_ids.add(prev.block_id)
+
+    def _expire_replay_after_content(self, state, request, start, end, mask_span) -> None:
+        """Remove each previous-block replay row whose expiring content token ran in [start, end)
+        (processor.py:594-618)."""
+        expiring, expired = state.content_to_expired_replay, state.expired_replay_positions
+        for pos in range(start, end):
+            row = expiring.get(pos)
+            if row is None or row in expired:
+                continue
+            self._mask_or_raise(mask_span, request.request_id, row, row + 1)
+            expired.add(row)
 
     def _expire_retained_tail_after_content(self, state, request, start, end, mask_span) -> None:
         """Rolling policy: remove each previous-block tail row whose expiring content token ran in [start, end)

@@ -67,7 +67,7 @@ MAX_MODEL_LEN = 1 << 30
 
 def serving_processor(group_quotas, C=BLOCK_C, K=CODES_K_MAX) -> CompressLMProcessor:
     """The block state machine of a served model with these per-group code quotas (synthetic code token ids)."""
-    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev")
+    cfg = CompressLMConfig(replay_tail=0, enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev")
     cfg.set_code_token_ids(range(CODE_TOKEN_BASE, CODE_TOKEN_BASE + K))
     proc = CompressLMProcessor(cfg)
     proc.set_group_quotas(group_quotas)

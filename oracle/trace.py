@@ -17,6 +17,10 @@ third_party/vllm_overlay/vllm/v1/core/compresslm/processor.py:
                  expiry has a query of its own, :614-646 removes it);
     "sticky"  -- the tail's response rows go as one span after the next block's last content token has run,
                  before that block's codes (:559-592, called from :215-224 and again, as a no-op, from :427-430).
+  With a replay tail (``replay`` = R, appended positions) a block's code run is followed by R replay tokens (its last
+  R content tokens again, role REPLAY, :236-240, :402-417); the block is compacted after them (:253-259), and the
+  next block's i-th content token expires replay row i once it has run (a one-row removal of any replay row, prompt
+  blocks' too; :336-345 maps it, :123-151 ends a chunk at each, :594-618 removes it, before any tail expiry).
   Preemption (``preempt``) restarts the request at token 0 with its logical stream and block structure kept and
   its compaction progress cleared (state.py:46-50); the replay compacts every closed block again and opens no block
   that already exists (:429-431).
@@ -35,7 +39,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-CONTENT, CODE = 0, 1
+CONTENT, CODE, REPLAY = 0, 1, 2
 
 
 @dataclass
@@ -45,19 +49,25 @@ class Block:
     prompt_positions: list = field(default_factory=list)
     response_positions: list = field(default_factory=list)
     code_span: tuple | None = None
+    replay_positions: list = field(default_factory=list)
 
 
 class RequestTrace:
     """Logical token stream of one request and its block structure."""
 
-    def __init__(self, prompt_len, max_tokens, C, K, group_quotas, retain_tail=0, tail_policy="static"):
+    def __init__(self, prompt_len, max_tokens, C, K, group_quotas, retain_tail=0, tail_policy="static", replay=0):
         if prompt_len <= 0:
             raise ValueError("CompressLM decoding requires a non-empty prompt")
         if tail_policy not in ("static", "rolling", "sticky"):
             raise ValueError(f"unknown tail policy {tail_policy!r}")
         self.C, self.K = C, K
         self.T = retain_tail
+        self.R = replay
+        if replay and retain_tail:
+            raise ValueError("replay and retained tails are mutually exclusive")
         self.policy = tail_policy
+        self.replay_expire_at: dict[int, int] = {}   # content position -> previous block's replay row it expires
+        self.replay_expired: set[int] = set()
         self.expire_at: dict[int, int] = {}     # rolling: content position -> previous block's tail row it expires
         self.expired: set[int] = set()          # rolling tail rows removed so far
         self.sticky_done: set[int] = set()      # blocks whose tail the sticky policy has removed
@@ -99,6 +109,8 @@ class RequestTrace:
             (block.prompt_positions if is_prompt else block.response_positions).append(pos)
             self.roles.append(CONTENT)
             self.kind.append("prompt" if is_prompt else "response")
+            if prev is not None and within < len(prev.replay_positions):
+                self.replay_expire_at[pos] = prev.replay_positions[within]
             if self.policy == "rolling" and prev is not None and within < len(self._tail_rows(prev)):
                 row = self._tail_rows(prev)[within]
                 if self.kind[row] == "response":   # raw-prompt rows never leave
@@ -114,8 +126,8 @@ class RequestTrace:
         while end < self.num_tokens and self.roles[end] == role:
             end += 1
         if role == CONTENT:
-            for pos in range(start, end):          # a rolling expiry ends the chunk
-                if pos in self.expire_at:
+            for pos in range(start, end):          # a replay or rolling-tail expiry ends the chunk
+                if pos in self.expire_at or pos in self.replay_expire_at:
                     return pos - start + 1
         return end - start
 
@@ -125,6 +137,7 @@ class RequestTrace:
         self.compacted_block_ids.clear()
         self.expired.clear()
         self.sticky_done.clear()
+        self.replay_expired.clear()
 
     def should_skip_sampling(self, n):             # processor.py:153-168
         start = self.num_computed_tokens - n
@@ -143,6 +156,12 @@ class RequestTrace:
         role = self.roles[start]
         sampled = not self.should_skip_sampling(n)
         calls = []
+        if role == CONTENT:                            # replay expiries of the rows this step's queries saw last
+            for pos in range(start, end):
+                row = self.replay_expire_at.get(pos)
+                if row is not None and row not in self.replay_expired:
+                    calls.append((row, row + 1, None))
+                    self.replay_expired.add(row)
         if role == CONTENT:                            # rolling expiries of the rows this step's queries saw last
             for pos in range(start, end):
                 row = self.expire_at.get(pos)
@@ -168,13 +187,22 @@ class RequestTrace:
             elif sampled:
                 self._record_content(1, is_prompt=False)
         elif role == CODE and role_end:
+            if self.R and not block.replay_positions:    # _stage_replay: the block's last R tokens after its codes
+                rs = self.num_tokens
+                self.roles.extend([REPLAY] * self.R)
+                self.kind.extend(["replay"] * self.R)
+                block.replay_positions = list(range(rs, rs + self.R))
+            elif not block.replay_positions:
+                calls = self._finish_block(block)
+        elif role == REPLAY and role_end:
             calls = self._finish_block(block)
         return calls
 
     def _block_of(self, pos):
         for b in self.blocks:
             if b.content_positions and b.content_positions[0] <= pos:
-                last = b.code_span[1] if b.code_span else b.content_positions[-1] + 1
+                last = (b.replay_positions[-1] + 1 if b.replay_positions else
+                        b.code_span[1] if b.code_span else b.content_positions[-1] + 1)
                 if pos < last:
                     return b.block_id
         raise RuntimeError(f"position {pos} outside every block")
@@ -207,7 +235,8 @@ class RequestTrace:
                     continue
                 calls.append((cs + q, ce, [g for g, gq in enumerate(self.group_quotas) if gq == q]))
             self.compacted_block_ids.add(block.block_id)
-        if block.code_span[1] < self.num_tokens:       # a preemption replay: the next block exists
+        last = block.replay_positions[-1] + 1 if block.replay_positions else block.code_span[1]
+        if last < self.num_tokens:                     # a preemption replay: the next block exists
             return calls
         nxt = Block(len(self.blocks))
         self.blocks.append(nxt)
@@ -243,6 +272,9 @@ class RequestTrace:
                 for p in range(cs, min(ce, self.num_computed_tokens)):
                     if not (compacted and p - cs >= q):
                         keep.append(p)
+            for p in b.replay_positions:              # replay rows until the next block's content expires them
+                if p < self.num_computed_tokens and p not in self.replay_expired:
+                    keep.append(p)
         return sorted(keep)
 
 

@@ -46,7 +46,7 @@ def test_reference_parameter_names():
     pooled = CompressLM(_model(), 8, 2, 4, pool_init=True, code_q_heads=True)
     names = {n for n, _ in pooled.named_parameters()}
     assert {"pool_q", "pool_k.weight", "pool_v.weight", a + "q_proj.code.weight"} <= names
-    assert float(pooled.pool_v.weight.detach().abs().max()) == 0.0                 # zero value map: an exact no-op at first
+    assert float(pooled.pool_v.weight.detach().abs().max()) == 0.0        # a zero value map: an exact no-op at first
     assert torch.equal(pooled.model.model.layers[0].self_attn.q_proj.code.weight,
                        pooled.model.model.layers[0].self_attn.q_proj.orig.weight)
 

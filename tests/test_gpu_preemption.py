@@ -9,7 +9,11 @@ preemption and hold that token's bytes exactly; every replayed chunk and code st
 catch-up, must match fp64 attention under the reference's masks (2e-2, bf16). With a retained tail (rolling or sticky
 window, T=12) the code steps hide their block's tail (an excluded physical range, sched/scheduler.py:979-991) and the
 previous block's tail leaves through one-row (rolling) or one-span (sticky) removals, replayed after the preemption;
-the kept rows must then be the oracle trace's (oracle.trace.RequestTrace, stepped in lockstep)."""
+the kept rows must then be the oracle trace's (oracle.trace.RequestTrace, stepped in lockstep). With a replay tail
+(R=8 rows after each block's codes, appended code positions, one group at quota K: the reference's default layout)
+the replay chunk runs causally after the code step, the block closes after it (so "at block close" preempts in the
+replay step), the next block's content expires the replay rows one by one, and with code_exclude_replay_tail the code
+step hides the replayed content rows."""
 import numpy as np
 import pytest
 import torch
@@ -18,7 +22,7 @@ from abridgekv_amd import backend as bk
 from abridgekv_amd import worker
 from abridgekv_amd.config import CompressLMConfig
 from abridgekv_amd.planner import KVPlanner
-from abridgekv_amd.processor import CompressLMProcessor, SamplingSpec, ServingRequest
+from abridgekv_amd.processor import REPLAY, CompressLMProcessor, SamplingSpec, ServingRequest
 from oracle import masks as om
 from oracle import trace as ot
 
@@ -36,16 +40,19 @@ class Engine:
     """Scheduler + worker loop over the real state machine, native planner, attention backend and mover, one
     layer per KV-cache group."""
 
-    def __init__(self, num_pages=600, seed=0, tail=0, policy="static"):
+    def __init__(self, num_pages=600, seed=0, tail=0, policy="static", replay=0, exclude=False):
         self.dev = torch.device("cuda")
-        self.T, self.policy = tail, policy
-        cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev",
-                               layer_code_quotas=QUOTAS, physical_layer_quotas=True, retain_tail_kv=tail,
+        self.T, self.policy, self.R = tail, policy, replay
+        self.X = tail or (replay if exclude else 0)          # rows a code step hides
+        self.quotas = (K,) if replay else QUOTAS
+        cfg = CompressLMConfig(replay_tail=replay, code_exclude_replay_tail=exclude, enable=True, block_size=C,
+                               num_code_tokens=K, code_positions="appended" if replay else "bitrev",
+                               layer_code_quotas=self.quotas, physical_layer_quotas=True, retain_tail_kv=tail,
                                retain_tail_policy=policy)
         cfg.set_code_token_ids(CODES)
         self.proc = CompressLMProcessor(cfg)
-        self.proc.set_group_quotas(QUOTAS)
-        self.G = len(QUOTAS)
+        self.proc.set_group_quotas(self.quotas)
+        self.G = len(self.quotas)
         rng = np.random.default_rng(seed)
         self.planner = KVPlanner(num_pages, self.G, PAGE,
                                  free_order=rng.permutation(np.arange(1, num_pages)).astype(np.int32))
@@ -68,8 +75,8 @@ class Engine:
         req.compresslm_state = self.proc.prepare_request(req)
         self.planner.add_request(rid)
         self.reqs.append(req)
-        self.traces[rid] = ot.RequestTrace(prompt_len, 1 << 30, C, K, QUOTAS, retain_tail=self.T,
-                                           tail_policy=self.policy)
+        self.traces[rid] = ot.RequestTrace(prompt_len, 1 << 30, C, K, self.quotas, retain_tail=self.T,
+                                           tail_policy=self.policy, replay=self.R)
         return req
 
     def preempt(self, req):
@@ -97,7 +104,7 @@ class Engine:
             assert n == self.traces[req.request_id].next_chunk()
             # a code step hides its block's retained tail: the physical range in each group's layout, taken at
             # scheduling time (sched/scheduler.py:979-991)
-            excluded[req.request_id] = self.proc.code_excluded_physical_ranges(req, self.G) if code and self.T \
+            excluded[req.request_id] = self.proc.code_excluded_physical_ranges(req, self.G) if code and self.X \
                 else [(0, 0)] * self.G
             assert self.planner.allocate_slots(req.request_id, n) is not None, "pool exhausted"
             self.planner.set_num_computed_tokens(req.request_id, start + n)
@@ -112,12 +119,13 @@ class Engine:
             comp = np.array([self.planner.compacted_counts(r)[g] for r in rids], np.int64)
             seq_lens = np.array([s + n for _, s, n, _, _ in sched]) - comp
             spans = [self.proc.code_physical_spans(req, g, s + n) if code else [] for req, s, n, code, _ in sched]
-            limits = bk.code_step_key_limits(qsl, seq_lens, [sp[-1] if sp else None for sp in spans], QUOTAS[g], K)
+            limits = bk.code_step_key_limits(qsl, seq_lens, [sp[-1] if sp else None for sp in spans],
+                                             self.quotas[g], K)
             excl = np.array([excluded[req.request_id][g] for req, _, _, _, _ in sched], dtype=np.int64)
             table = self.planner.fill_block_table(rids, g, width)
             md = self.builder.build(qsl, seq_lens, torch.from_numpy(table).to(self.dev), positions=positions,
                                     compacted=torch.from_numpy(comp.astype(np.int32)).to(self.dev),
-                                    code_key_limit=limits, code_excluded=excl if self.T else None)
+                                    code_key_limit=limits, code_excluded=excl if self.X else None)
             idx = [(int(req.request_id), s, n) for req, s, n, _, _ in sched]
             q = torch.cat([self.qtab[r, s: s + n, g] for r, s, n in idx]).to(self.dev)
             k = torch.cat([self.ktab[r, s: s + n, g] for r, s, n in idx]).to(self.dev)
@@ -131,7 +139,7 @@ class Engine:
                     continue
                 sl = int(seq_lens[i])
                 ex = tuple(excl[i]) if excl[i, 1] > excl[i, 0] else None
-                mask = om.request_mask(n, sl, spans[i], ex, QUOTAS[g], K, causal=not code)
+                mask = om.request_mask(n, sl, spans[i], ex, self.quotas[g], K, causal=not code)
                 ref, _ = om.masked_paged_attention_fp64(q[qsl[i]: qsl[i + 1]].float().cpu().numpy(),
                                                         self.caches[g].float().cpu().numpy(), table[i], sl, mask,
                                                         128 ** -0.5)
@@ -169,14 +177,20 @@ def _closed_blocks(req):
     return len(req.compresslm_state.compacted_block_ids)
 
 
-CASES = [("mid_block", 0, "static"), ("at_block_close", 0, "static"), ("mid_block", 12, "rolling"),
-         ("at_block_close", 12, "rolling"), ("mid_block", 12, "sticky"), ("at_block_close", 12, "sticky")]
+CASES = [("mid_block", 0, "static", 0, False), ("at_block_close", 0, "static", 0, False),
+         ("mid_block", 12, "rolling", 0, False), ("at_block_close", 12, "rolling", 0, False),
+         ("mid_block", 12, "sticky", 0, False), ("at_block_close", 12, "sticky", 0, False),
+         ("mid_block", 0, "static", 8, False), ("at_block_close", 0, "static", 8, True)]
 
 
-@pytest.mark.parametrize("where,tail,policy", CASES, ids=[f"{w}-{p if t else 'no_tail'}" for w, t, p in CASES])
-def test_preempted_request_replays_to_the_same_layout(where, tail, policy):
-    print(f"case: {where} tail={tail} {policy}", flush=True)
-    eng = Engine(seed=3 if where == "mid_block" else 4, tail=tail, policy=policy)
+def _case_id(w, t, p, r, x):
+    return f"{w}-" + (f"replay{r}{'-excl' if x else ''}" if r else (p if t else "no_tail"))
+
+
+@pytest.mark.parametrize("where,tail,policy,replay,exclude", CASES, ids=[_case_id(*c) for c in CASES])
+def test_preempted_request_replays_to_the_same_layout(where, tail, policy, replay, exclude):
+    print(f"case: {where} tail={tail} {policy} replay={replay} exclude={exclude}", flush=True)
+    eng = Engine(seed=3 if where == "mid_block" else 4, tail=tail, policy=policy, replay=replay, exclude=exclude)
     r0 = eng.add(0, 100)                       # prompt spans block 0 and part of block 1
     r1 = eng.add(1, 30)
     # run until r0 has closed two blocks (then, mid-block: 20 more decode steps)
@@ -186,9 +200,13 @@ def test_preempted_request_replays_to_the_same_layout(where, tail, policy):
         for _ in range(20):
             eng.step()
     else:
-        # run until r0's next code step is the one scheduled, and preempt in the step that closes its block
+        # run until r0's next code step (with a replay tail: its replay step) is the one scheduled, and preempt in
+        # the step that closes its block
         while not eng.proc.is_code_ready(r0):
             eng.step()
+        if replay:
+            eng.step()
+            assert r0.compresslm_state.roles[r0.num_computed_tokens] == REPLAY
     before_closed = _closed_blocks(r0)
     if where == "at_block_close":
         eng.step(preempt_after=r0)
@@ -221,9 +239,9 @@ def test_preempted_request_replays_to_the_same_layout(where, tail, policy):
         # the kept positions are the closed-form layout: prompt rows of block 0 (raw prompt) and every closed
         # block's first QUOTAS[g] codes, then the open block's content
         closed = [b for b in r0.compresslm_state.blocks if b.block_id in r0.compresslm_state.compacted_block_ids]
-        kept_codes = {p for b in closed for p in range(b.code_span[0], b.code_span[0] + QUOTAS[g])}
+        kept_codes = {p for b in closed for p in range(b.code_span[0], b.code_span[0] + eng.quotas[g])}
         assert kept_codes <= set(logical.tolist())
-        assert not any(p in set(logical.tolist()) for b in closed for p in range(b.code_span[0] + QUOTAS[g],
+        assert not any(p in set(logical.tolist()) for b in closed for p in range(b.code_span[0] + eng.quotas[g],
                                                                                b.code_span[1]))
     # decoding resumes over the rebuilt cache (the first decode step is checked against fp64)
     for _ in range(3):

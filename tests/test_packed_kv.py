@@ -153,25 +153,31 @@ def test_oracle_code_step_without_pages_is_the_code_mask():
 
 
 def test_packed_config_validation():
-    ok = CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
+    ok = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                          enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
                           packed_kv_quotas=((1, 2),))
     assert ok.uses_packed_kv and ok.packed_layout(1, 2).quotas == ((1, 2),)
     with pytest.raises(ValueError, match="packed_kv_k_max"):
-        CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True)
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=4, num_code_tokens=2, packed_kv=True)
     with pytest.raises(ValueError, match="must be in"):
-        CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
                          packed_kv_quotas=((3,),))
     with pytest.raises(ValueError, match="must not be empty"):
-        CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
                          packed_kv_quotas=((),))
     with pytest.raises(ValueError, match="mutually exclusive"):
-        CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2,
                          layer_code_quotas=(1, 2))
 
 
 def _run_packed(prompt, generated):
     """The driving loop of scripts/test_compresslm_vllm_state.py:100-209 with packed_kv=True, K_max=2."""
-    cfg = CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2)
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=4, num_code_tokens=2, packed_kv=True, packed_kv_k_max=2)
     cfg.set_code_token_ids([900, 901])
     proc = CompressLMProcessor(cfg)
     req = ServingRequest("r", prompt, SamplingSpec(max_tokens=len(generated), bad_words_token_ids=[[900], [901]]))

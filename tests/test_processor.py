@@ -15,7 +15,7 @@ CODES = [900, 901, 902, 903]
 
 
 def make(quotas=(4, 2, 1, 2), C=4, K=4):
-    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev",
+    cfg = CompressLMConfig(replay_tail=0, enable=True, block_size=C, num_code_tokens=K, code_positions="bitrev",
                            layer_code_quotas=quotas, physical_layer_quotas=True)
     cfg.set_code_token_ids(CODES[:K] if K <= 4 else list(range(900, 900 + K)))
     proc = CompressLMProcessor(cfg)
@@ -24,8 +24,8 @@ def make(quotas=(4, 2, 1, 2), C=4, K=4):
 
 
 def test_config_positions_match_oracle_and_validate():
-    cfg = CompressLMConfig(enable=True, block_size=512, num_code_tokens=256, layer_code_quotas=ol.PERLAYER_MEAN128_QUOTAS,
-                           physical_layer_quotas=True)
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev", enable=True, block_size=512, num_code_tokens=256,
+                           layer_code_quotas=ol.PERLAYER_MEAN128_QUOTAS, physical_layer_quotas=True)
     assert np.array_equal(cfg.bitrev_code_offsets(), ol.bitrev_code_offsets(256, 512))
     logical = np.arange(5 * 768)
     assert np.array_equal(cfg.bitrev_rope_positions(logical), ol.bitrev_rope_positions(logical, 512, 256))
@@ -39,7 +39,19 @@ def test_config_positions_match_oracle_and_validate():
     for bad in (dict(layer_code_quotas=(300,)), dict(replay_tail=16), dict(num_passes=2), dict(raw_prompt=False),
                 dict(num_code_tokens=96), dict(physical_layer_quotas=True)):
         with pytest.raises(ValueError):
-            CompressLMConfig(enable=True, block_size=512, num_code_tokens=bad.pop("num_code_tokens", 256), **bad)
+            CompressLMConfig(enable=True, block_size=512, code_positions="bitrev",
+                             replay_tail=bad.pop("replay_tail", 0), num_code_tokens=bad.pop("num_code_tokens", 256),
+                             **bad)
+    # the reference's defaults: appended code positions and a replay tail of 16 (config/compresslm.py:19-44); per-layer
+    # quotas below K need the bitrev layout, and the replay tail excludes the retained one
+    default = CompressLMConfig(enable=True)
+    assert (default.code_positions, default.replay_tail, default.code_excluded_tail) == ("appended", 16, 0)
+    assert CompressLMConfig(enable=True, code_exclude_replay_tail=True).code_excluded_tail == 16
+    for bad in (dict(layer_code_quotas=(64,) * 36), dict(retain_tail_kv=8), dict(raw_tail=4),
+                dict(replay_tail=513), dict(code_exclude_replay_tail=True, replay_tail=0),
+                dict(packed_kv=True, packed_kv_k_max=128, code_exclude_replay_tail=True)):
+        with pytest.raises(ValueError):
+            CompressLMConfig(enable=True, **bad)
 
 
 def run_reference_scenario(proc, request, mask_span, generated):
@@ -173,7 +185,8 @@ def test_request_validation():
     with pytest.raises(ValueError):
         proc.prepare_request(ServingRequest("a", [], SamplingSpec(bad_words_token_ids=[[c] for c in CODES])))
     with pytest.raises(ValueError):
-        CompressLMProcessor(CompressLMConfig(enable=True, block_size=4, num_code_tokens=4))
+        CompressLMProcessor(CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                                             enable=True, block_size=4, num_code_tokens=4))
 
 
 @pytest.mark.parametrize("change,message", [
@@ -209,7 +222,8 @@ def test_request_refusals_match_the_reference(change, message):
 
 
 def test_logprobs_are_allowed_in_debug_mode():
-    cfg = CompressLMConfig(enable=True, block_size=4, num_code_tokens=2, debug=True)
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=4, num_code_tokens=2, debug=True)
     cfg.set_code_token_ids([90, 91])
     proc = CompressLMProcessor(cfg)
     req = ServingRequest("a", [1, 2], SamplingSpec(bad_words_token_ids=[[90], [91]], logprobs=1))
@@ -231,7 +245,7 @@ def test_config_json_round_trip_and_schedule_loading(tmp_path):
     assert load_layer_quotas(sched) == QWEN3_4B_LAYER_QUOTAS
     assert sum(load_layer_quotas(sched)) == 4608
 
-    cfg = CompressLMConfig(enable=True, block_size=512, num_code_tokens=256)
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev", enable=True, block_size=512, num_code_tokens=256)
     cfg.set_code_token_ids(list(range(1000, 1256)))
     path = cfg.write_json(tmp_path)
     meta = json.loads(path.read_text())

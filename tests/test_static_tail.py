@@ -14,7 +14,8 @@ def run_case(prompt, generated, T=2, packed=False, quotas=None, C=4, K=2):
     """The driving loop of scripts/test_compresslm_vllm_state.py:99-214 (block_size 4, two codes, raw prompt):
     returns (request, state, masks, pack events)."""
     codes = list(range(900, 900 + K))
-    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy="static",
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy="static",
                            packed_kv=packed, packed_kv_k_max=K if packed else 2048,
                            layer_code_quotas=quotas or (), physical_layer_quotas=bool(quotas))
     cfg.set_code_token_ids(codes)
@@ -59,24 +60,30 @@ def run_case(prompt, generated, T=2, packed=False, quotas=None, C=4, K=2):
 
 
 def test_config_static_tail():
-    cfg = CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy="static",
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy="static",
                            packed_kv=True, packed_kv_k_max=4)
     assert cfg.code_excluded_tail == 2
     offs = cfg.bitrev_code_offsets().tolist()
     assert max(offs) < 6 and len(set(offs)) == 4 and offs[0] == 0, offs       # grid over [0, C - T) = [0, 6)
-    assert CompressLMConfig(enable=True, block_size=8, num_code_tokens=4).code_excluded_tail == 0
+    assert CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                            enable=True, block_size=8, num_code_tokens=4).code_excluded_tail == 0
     with pytest.raises(ValueError, match="retain_tail_policy"):
         CompressLMConfig(retain_tail_policy="invalid")
     with pytest.raises(ValueError, match="retain_tail_kv > 0"):
-        CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_policy="sticky")
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=8, num_code_tokens=4, retain_tail_policy="sticky")
     for policy in ("rolling", "sticky"):                                     # window tails: not with packed KV
         with pytest.raises(ValueError, match="static"):
-            CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy=policy,
+            CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                             enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy=policy,
                              packed_kv=True, packed_kv_k_max=4)
     with pytest.raises(ValueError, match="block_size"):
-        CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=8, retain_tail_policy="static")
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=8, retain_tail_policy="static")
     with pytest.raises(ValueError, match="span"):
-        CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=6, retain_tail_policy="static")
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=6, retain_tail_policy="static")
     # export keeps the tail fields (compresslm_config.json)
     meta = cfg.to_metadata()
     assert meta["retain_tail_kv"] == 2 and meta["retain_tail_policy"] == "static"
@@ -117,7 +124,8 @@ def test_physical_quotas_with_static_tail_match_oracle_trace(prompt_len, gen):
     exclusion range in every group is where the block's tail lies in that group's brute-force kept stream."""
     quotas, C, K, T = (4, 2, 1, 2), 8, 4, 3
     codes = list(range(900, 900 + K))
-    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy="static",
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy="static",
                            layer_code_quotas=quotas, physical_layer_quotas=True)
     cfg.set_code_token_ids(codes)
     proc = CompressLMProcessor(cfg)

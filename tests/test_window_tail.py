@@ -16,7 +16,8 @@ from oracle import trace as ot
 
 def _proc(C=4, K=2, T=2, policy="rolling", quotas=None):
     codes = list(range(900, 900 + K))
-    cfg = CompressLMConfig(enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy=policy,
+    cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                           enable=True, block_size=C, num_code_tokens=K, retain_tail_kv=T, retain_tail_policy=policy,
                            layer_code_quotas=quotas or (), physical_layer_quotas=bool(quotas))
     cfg.set_code_token_ids(codes)
     proc = CompressLMProcessor(cfg)
@@ -70,15 +71,18 @@ def run_case(prompt, generated, T=2, policy="rolling", C=4, K=2):
 
 def test_config_accepts_the_window_tails_except_with_packed_kv():
     for policy in ("rolling", "sticky"):
-        cfg = CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2, retain_tail_policy=policy)
+        cfg = CompressLMConfig(replay_tail=0, code_positions="bitrev", enable=True, block_size=8, num_code_tokens=4,
+                               retain_tail_kv=2, retain_tail_policy=policy)
         assert cfg.code_excluded_tail == 2
         assert cfg.bitrev_code_offsets().max() < 6                          # codes spread over [0, C - T)
         with pytest.raises(ValueError, match="static"):
-            CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2,
+            CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                             enable=True, block_size=8, num_code_tokens=4, retain_tail_kv=2,
                              retain_tail_policy=policy, packed_kv=True, packed_kv_k_max=4)
     assert CompressLMConfig().retain_tail_policy == "rolling"
     with pytest.raises(ValueError, match="retain_tail_kv > 0"):
-        CompressLMConfig(enable=True, block_size=8, num_code_tokens=4, retain_tail_policy="sticky")
+        CompressLMConfig(replay_tail=0, code_positions="bitrev",
+                         enable=True, block_size=8, num_code_tokens=4, retain_tail_policy="sticky")
 
 
 def test_reference_scenario_rolling():
@@ -97,7 +101,7 @@ def test_reference_scenario_rolling():
 def test_reference_scenario_rolling_bulk_limit():
     """A re-prefill that exposes several content tokens at once still schedules one query per expiration."""
     proc, _ = _proc()
-    st = SimpleNamespace(roles=[CONTENT] * 8, content_to_expired_retained_tail={2: 0})
+    st = SimpleNamespace(roles=[CONTENT] * 8, content_to_expired_replay={}, content_to_expired_retained_tail={2: 0})
     req = SimpleNamespace(compresslm_state=st, num_computed_tokens=2, num_tokens=8)
     assert proc.limit_num_new_tokens(req, proposed=6) == 1
     st.content_to_expired_retained_tail = {3: 0}
