@@ -18,9 +18,11 @@ every decoder layer runs ``abkv_prefill_masked_attn`` through a HuggingFace atte
 ``"abridgekv_hip"`` in place of FlexAttention with a BlockMask (``_arith_mask_mod`` / ``_mask_mod`` /
 ``_mask_rawprompt_mod`` / ``_quota_key_allowed``, compress_forward.py:230-236, 566-649, 695-727, 815-894). The mask
 is never materialised: the kernel evaluates it from (C, K, L, R, N, prompt_len, head quota, tail, xattn); layouts off
-the 64-row tile grid, L > 1, replay rows and non-full xattn take its per-element walk.
+the 64-row tile grid, L > 1, replay rows, the raw tail and non-full xattn take its per-element walk.
 
-The raw tail (``raw_tail``, a training ablation the reference's serving refuses) raises NotImplementedError.
+The raw tail (``raw_tail`` = W, a training ablation the reference's serving refuses, compress_forward.py:89-96):
+content row i of the next block sees the block's last W - i content rows (the rolling window of a retained tail),
+and the block's codes see their whole block.
 Gradients flow through the attention by the kernel's HIP backward (dq, dk, dv under the same mask), so the module
 trains.
 """
@@ -44,7 +46,8 @@ class CompressMask:
     N blocks of [C content | ``passes`` passes of K code rows] and ``copy_rows`` copy-region rows (codes_k = 0: causal
     attention within blocks of C rows); ``prompt_len`` [B] int32 raw-prompt content tokens (None: no raw prompt);
     ``head_quota`` [layers, 32] int32 code rows visible per query head (None: all K); ``retain_tail`` T of a retained
-    tail (0: none) under ``tail_policy`` ("static", "rolling" or "sticky")."""
+    tail (0: none) under ``tail_policy`` ("static", "rolling", "sticky", or "raw" for the raw tail: the rolling
+    window, seen by the codes too)."""
     block_c: int
     codes_k: int
     num_blocks: int
@@ -275,8 +278,7 @@ class CompressLM(nn.Module):
 
     ``base_model`` is a HuggingFace causal LM with 32 query heads, 8 KV heads and head size 128 in bf16 (e.g.
     Qwen3-4B or a random model of that attention shape); its attention implementation is switched to
-    ``"abridgekv_hip"``. The raw tail (``raw_tail``, a training ablation the reference does not serve) raises
-    NotImplementedError.
+    ``"abridgekv_hip"``.
     """
 
     def __init__(self, base_model, C, N, K, L=1, pause_xattn="full", pool_init=False, query_residual=False,
@@ -284,17 +286,17 @@ class CompressLM(nn.Module):
                  replay_tail=0, code_exclude_replay_tail=False, retain_tail_kv=0, retain_tail_policy="rolling",
                  head_code_quotas=None, active_code_rows=None, code_positions="appended"):
         super().__init__()
-        if raw_tail:
-            raise NotImplementedError("CompressLM option raw_tail is not supported by the native forward")
         if int(L) != L or L < 1:
             raise ValueError(f"L must be a positive integer, got {L}")
         if pause_xattn not in ("none", "causal", "full"):
             raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {pause_xattn!r}")
         if not 0 <= replay_tail <= C:
             raise ValueError(f"replay_tail must be in [0, C={C}], got {replay_tail}")
+        if not 0 <= raw_tail <= C:
+            raise ValueError(f"raw_tail must be in [0, C={C}], got {raw_tail}")
         if not 0 <= retain_tail_kv < C:
             raise ValueError(f"retain_tail_kv must be in [0, C={C}), got {retain_tail_kv}")
-        if replay_tail and retain_tail_kv:
+        if sum(bool(value) for value in (raw_tail, replay_tail, retain_tail_kv)) > 1:
             raise ValueError("raw_tail, replay_tail, and retain_tail_kv are mutually exclusive")
         if retain_tail_policy not in ("rolling", "sticky", "static"):
             raise ValueError(f"retain_tail_policy must be 'rolling', 'sticky' or 'static', got {retain_tail_policy!r}")
@@ -304,7 +306,7 @@ class CompressLM(nn.Module):
             raise ValueError("code_exclude_replay_tail requires replay_tail in [1, C)")
         if code_positions not in ("appended", "bitrev"):
             raise ValueError(f"code_positions must be 'appended' or 'bitrev', got {code_positions!r}")
-        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1) or L != 1 or replay_tail):
+        if code_positions == "bitrev" and (K & (K - 1) or C & (C - 1) or L != 1 or replay_tail or raw_tail):
             raise ValueError("code_positions='bitrev' needs power-of-two C and K, L=1 and no tails")
         if query_residual and code_q_heads:
             raise ValueError("query_residual and code_q_heads both replace q_proj; enable one of them")
@@ -319,7 +321,7 @@ class CompressLM(nn.Module):
         self.model.config._attn_implementation = ATTN_IMPLEMENTATION
         self.C, self.N, self.K, self.L = int(C), int(N), int(K), int(L)
         self.pause_xattn, self.code_positions = pause_xattn, code_positions
-        self.raw_tail = 0
+        self.raw_tail = int(raw_tail)
         self.replay_tail = int(replay_tail)
         self.code_exclude_replay_tail = bool(code_exclude_replay_tail)
         self.retain_tail_kv = int(retain_tail_kv)
@@ -430,8 +432,10 @@ class CompressLM(nn.Module):
             prompt_len = prompt_len.to(device=self.pause.device, dtype=torch.int32).contiguous()
             if prompt_len.numel() != batch:
                 raise ValueError("prompt_len must hold one length per sequence")
-        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32, self.retain_tail_kv,
-                            self.retain_tail_policy if self.retain_tail_kv else "static", self.pause_xattn, self.L,
+        # the raw tail is the kernels' "raw" policy: the rolling window, not hidden from the codes
+        policy = "raw" if self.raw_tail else self.retain_tail_policy if self.retain_tail_kv else "static"
+        return CompressMask(self.C, self.K_act, N, prompt_len, self._head_quota_i32,
+                            self.raw_tail or self.retain_tail_kv, policy, self.pause_xattn, self.L,
                             copy_rows, self.replay_tail, self.code_exclude_replay_tail)
 
     def _lm_ce(self, hid, tgt, chunk):

@@ -42,7 +42,7 @@ struct F32Args {
   const int32_t* prompt_len;   // [B] or nullptr
   const int32_t* head_quota;   // [32] or nullptr
   int retain_tail;             // retained tail T (0: none)
-  int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky)
+  int tail_policy;             // its policy (kTailStatic, kTailRolling, kTailSticky, kTailRaw)
   int pause_xattn;             // code <-> code attention in a block (kXattn*)
   int pause_passes;            // pause passes of codes_k rows per block
   int copy_rows;               // copy-region rows at the end of the seq_len rows
@@ -317,7 +317,8 @@ int abkv_prefill_masked_attn_f32(const float* q, long q_sb, long q_ss, long q_sh
       (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
       (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
       retain_tail < 0 ||
-      retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
+      retain_tail > block_c || (retain_tail == block_c && tail_policy != kTailRaw) ||
+      tail_policy < kTailStatic || tail_policy > kTailRaw || pause_xattn < kXattnFull ||
       pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   F32Args a = f32_defaults();

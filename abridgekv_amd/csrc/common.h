@@ -25,6 +25,8 @@ constexpr int kPageElems = 2 * kHalfElems;                 // 32768 elements = 6
 constexpr int kTailStatic = 0;   // every later row
 constexpr int kTailRolling = 1;  // the next block's i-th content row sees the tail's rows i .. T-1
 constexpr int kTailSticky = 2;   // every content row of the next block
+constexpr int kTailRaw = 3;      // the rolling window of raw_tail (compress_forward.py:89-96): the codes see the whole
+                                 // block, their own tail included (code_excluded_tail = 0, :309-311)
 
 // pause_xattn: which code rows of its own pass and block a code row sees (compress_forward.py:313-314, 622-625).
 constexpr int kXattnFull = 0;     // all of them (bidirectional)
@@ -47,7 +49,8 @@ __device__ __forceinline__ bool tail_visible(int policy, int tail, int C, int qb
 //             | a replay row's own block's final pass and replay rows | for content row i, the previous block's
 //             replay rows r >= i (_replay_tail_visible))
 //   | a code row's own block's previous pass | its own pass by xattn,
-// less a code row's own block's last `tail` content rows (R of them with rx: code_exclude_replay_tail), and less a
+// less a code row's own block's last `tail` content rows (R of them with rx: code_exclude_replay_tail; none under
+// kTailRaw), and less a
 // code key whose slot (its index within its pass) is >= quota. The last `copy` of the S rows are the copy region
 // (copy_lambda, :631-633): they see the last block's final pass (slot < quota) and the copy rows up to themselves,
 // and no other row sees them. K = 0 (no codes) is block-local causal attention. With L = 1, R = 0 and copy = 0
@@ -71,7 +74,7 @@ __device__ __forceinline__ bool compress_visible(int q, int kv, int S, int copy,
   const bool kcode = !kc && !krep, qcode = !qc && !qrep;
   const int kp = L == 1 ? 1 : (kw - C) / K + 1;            // pass of a code key (1..L)
   const int qp = L == 1 ? 1 : (qw - C) / K + 1;            // pass of a code query
-  const int X = rx ? R : tail;                              // the own-block content rows hidden from the codes
+  const int X = rx ? R : policy == kTailRaw ? 0 : tail;    // the own-block content rows hidden from the codes
   bool v = (kc && kb == qb) || (kcode && kp == L && kb < qb) || (kc && kb * C + kw < plen) ||
            tail_visible(policy, tail, C, qb, qw, kb, kw);
   if (R > 0)

@@ -134,7 +134,8 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
       (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
       (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
       retain_tail < 0 ||
-      retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky || pause_xattn < kXattnFull ||
+      retain_tail > block_c || (retain_tail == block_c && tail_policy != kTailRaw) ||
+      tail_policy < kTailStatic || tail_policy > kTailRaw || pause_xattn < kXattnFull ||
       pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   PrefillArgs a;
@@ -159,7 +160,7 @@ int abkv_prefill_masked_attn(const void* q, long q_stride_b, long q_stride_s, lo
   a.R = replay_rows;
   a.rx = replay_exclude != 0;
   a.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull && pause_passes == 1 &&
-              copy_rows == 0 && replay_rows == 0;
+              copy_rows == 0 && replay_rows == 0 && tail_policy != kTailRaw;
   a.num_q_tiles = (seq_len + kBM - 1) / kBM;
   // 8 waves, 2 heads x 16 rows each: 216 VGPRs -> 2 waves per SIMD (the 4-head form needs 480 registers and runs
   // one wave per SIMD: 416 vs 500 TFLOP/s on the B=4, S0=10240 workload).

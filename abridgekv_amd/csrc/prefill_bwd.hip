@@ -554,7 +554,8 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
       replay_rows < 0 || replay_rows > block_c || (replay_rows && (retain_tail || codes_k == 0)) ||
       (replay_exclude && (replay_rows <= 0 || replay_rows >= block_c)) ||
       (long)seq_len != (long)num_blocks * (block_c + (long)pause_passes * codes_k + replay_rows) + copy_rows ||
-      retain_tail < 0 || retain_tail >= block_c || tail_policy < kTailStatic || tail_policy > kTailSticky ||
+      retain_tail < 0 || retain_tail > block_c || (retain_tail == block_c && tail_policy != kTailRaw) ||
+      tail_policy < kTailStatic || tail_policy > kTailRaw ||
       pause_xattn < kXattnFull || pause_xattn > kXattnNone)
     return (int)hipErrorInvalidValue;
   if (workspace == nullptr || workspace_bytes < abkv_prefill_masked_bwd_workspace_size(batch, seq_len))
@@ -581,7 +582,7 @@ int abkv_prefill_masked_attn_bwd(const void* q, long q_stride_b, long q_stride_s
   f.R = replay_rows;
   f.rx = replay_exclude != 0;
   f.aligned = (block_c % kBN == 0) && (codes_k % kBN == 0) && pause_xattn == kXattnFull && pause_passes == 1 &&
-              copy_rows == 0 && replay_rows == 0;
+              copy_rows == 0 && replay_rows == 0 && tail_policy != kTailRaw;
   f.num_q_tiles = (seq_len + kBM - 1) / kBM;
   a.o = static_cast<const __bf16*>(out);
   a.o_sb = out_stride_b; a.o_ss = out_stride_s; a.o_sh = out_stride_h;

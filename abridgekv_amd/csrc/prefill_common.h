@@ -19,7 +19,7 @@ struct PrefillArgs {
   int aligned;                               // C % 64 == 0 && K % 64 == 0 (the walk over visible tiles)
   int num_q_tiles;
   int tail;                                  // retained tail T (0: none)
-  int policy;                                // its policy: kTailStatic, kTailRolling or kTailSticky
+  int policy;                                // its policy: kTailStatic, kTailRolling, kTailSticky, kTailRaw
   int xattn;                                 // code <-> code attention in a block (kXattn*; the aligned walks
                                              // serve kXattnFull, the others take the per-element walk)
   int L;                                     // pause passes of K code rows per block (the aligned walks serve 1)

@@ -27,6 +27,9 @@ boundary is a compaction:
   (compresslm/processor.py:318-353, 559-646): "sticky" removes them all before that block's code step; "rolling"
   removes tail row i once content token i of the next block has run, and a content chunk ends at every such token
   so that each removal follows that token's query (processor.py:123-151). Raw-prompt rows never leave.
+* a raw tail of W rows (``raw_tail``, or ``raw_tail_override``; gen_compress.py:118-137, 445-470, 980-1000): the
+  rolling window over the block's last W content rows (W <= C), which the block's own codes see like the rest of
+  their block.
 
 Layers with equal quota form one KV-cache group (one page table); tensor i holds the i-th layer of every group, as
 the serving worker shares them (kv_cache_utils.py:1110-1127).
@@ -63,7 +66,7 @@ from .planner import KVPlanner
 from .processor import CompressLMBlock, CompressLMProcessor
 from .worker import execute_fused_moves
 
-_UNSUPPORTED = ("capture_hidden", "capture_attention", "raw_tail_override",
+_UNSUPPORTED = ("capture_hidden", "capture_attention",
                 "oracle_full_history", "oracle_history_layers", "preserve_full_history", "retain_full_history_layers",
                 "history_replaces_codes_layers", "capture_content_attention", "content_attention_offsets",
                 "content_head_callback", "evict_policy", "keep_per_block", "evict_seed", "skip_unused_codes")
@@ -107,7 +110,7 @@ class CompressGen:
     page pool must hold."""
 
     def __init__(self, clm, device, raw_prompt_len=0, head_code_quotas=None, code_attend_current_content=True,
-                 code_init_override=None, max_tokens: int = 1 << 15, **options):
+                 code_init_override=None, raw_tail_override=None, max_tokens: int = 1 << 15, **options):
         bad = sorted(name for name in options if name not in _UNSUPPORTED)
         if bad:
             raise TypeError(f"unexpected CompressGen options {bad}")
@@ -127,10 +130,18 @@ class CompressGen:
         self.xattn = getattr(clm, "pause_xattn", "full")
         if self.xattn not in ("full", "causal", "none"):
             raise ValueError(f"pause_xattn must be 'none', 'causal' or 'full', got {self.xattn!r}")
-        if getattr(clm, "raw_tail", 0):
-            raise NotImplementedError("the paged path serves no raw tail")
-        self.T = int(getattr(clm, "retain_tail_kv", 0) or 0)
-        self.policy = getattr(clm, "retain_tail_policy", "rolling") if self.T else "static"
+        # raw tail (gen_compress.py:118-137): the next block's i-th content row sees the block's last W - i content
+        # rows (a rolling window that its own codes also see); raw_tail_override replaces the model's W
+        retain = int(getattr(clm, "retain_tail_kv", 0) or 0)
+        if raw_tail_override is not None and retain:
+            raise ValueError("raw_tail_override cannot be combined with retain_tail_kv")
+        self.raw = int(getattr(clm, "raw_tail", 0) or 0) if raw_tail_override is None else int(raw_tail_override)
+        if not 0 <= self.raw <= int(clm.C):
+            raise ValueError(f"raw_tail must be in [0, C={clm.C}], got {self.raw}")
+        if self.raw and getattr(clm, "replay_tail", 0):
+            raise NotImplementedError("the paged path takes a raw tail or a replay tail, not both")
+        self.T = self.raw or retain
+        self.policy = "rolling" if self.raw else getattr(clm, "retain_tail_policy", "rolling") if self.T else "static"
         # replay tail (gen_compress.py:900-916): R rows after each block's codes, fed its last R content tokens; the
         # next block's content token i expires replay row i (processor.py:336-345, 594-618)
         self.R = int(getattr(clm, "replay_tail", 0) or 0)
@@ -138,7 +149,7 @@ class CompressGen:
             raise ValueError("a replay tail needs appended code positions")
         # the block's last content rows its own codes do not see: the retained tail, or the replayed rows with
         # code_exclude_replay_tail (compress_forward.py:298-300)
-        self.X = self.R if getattr(clm, "code_exclude_replay_tail", False) else self.T
+        self.X = self.R if getattr(clm, "code_exclude_replay_tail", False) else retain
         self.clm = clm
         self.inner = clm.model.model
         self.layers = self.inner.layers
@@ -185,10 +196,11 @@ class CompressGen:
         self.planner.add_request(self.rid)
         # the block state machine's compaction rule for these groups (the serving validation of an enabled config --
         # bitrev positions, power-of-two sizes -- is the vLLM path's; the generator also runs appended positions)
+        # (a raw tail is kept out of the block's response content by the generator itself, so it may span the block)
         pcfg = CompressLMConfig(replay_tail=0, code_positions="bitrev",
                                 block_size=self.C, num_code_tokens=self.K, packed_kv=self.packed,
-                                packed_kv_k_max=self.K, retain_tail_kv=self.T,
-                                retain_tail_policy=self.policy if self.T else "rolling")
+                                packed_kv_k_max=self.K, retain_tail_kv=retain,
+                                retain_tail_policy=self.policy if retain else "rolling")
         pcfg.set_code_token_ids(range(1 << 20, (1 << 20) + self.K))
         self.proc = CompressLMProcessor(pcfg)
         if not self.packed:
@@ -208,7 +220,7 @@ class CompressGen:
         self._window: list[int | None] = []
         self.logical_len = 0            # tokens in the planner's logical sequence (content + code rows)
         self._cur_ids: list[int] = []
-        self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C - self.T)).to(self.device)
+        self._code_offsets = (torch.from_numpy(bitrev_offsets(self.K, self.C - self.X)).to(self.device)
                               if self.code_positions == "bitrev" else None)
         # fp32 cos/sin of the model's rotary embedding for every position this sequence can reach (RoPE positions
         # never exceed logical positions); the fused kernel rotates q/k and appends K/V in one launch per layer
@@ -276,7 +288,7 @@ class CompressGen:
             k = k[0].to(self.dtype).contiguous()
             v = _project(attn.v_proj, normed, code_step).view(n, -1, attn.head_dim).contiguous()
             ops.rope_kv_append(q, k, v, logical, self._cos_sin, slot_mapping=md.slot_mapping, kv_cache=cache,
-                               block_c=bc, codes_k=bk, max_position=last, code_span=bc - self.T if bc else 0)
+                               block_c=bc, codes_k=bk, max_position=last, code_span=bc - self.X if bc else 0)
             o = torch.empty((n, ops.HEADS_Q, ops.HEAD_DIM), dtype=self.dtype, device=self.device)
             if self.sidecar is not None:
                 # paged rows + this layer's per-head packed pages; a code step's paged keys stop at the block's
@@ -356,11 +368,12 @@ class CompressGen:
         block_start = code_start - C
         resp_from = block_start + min(max(self.raw_prompt_len - self.b * C, 0), C)
         # the block as the state machine sees it; its removals (and their order) are the processor's
+        tail = list(range(code_start - self.T, code_start)) if self.T else []
+        response = list(range(resp_from, code_start - self.T if self.raw else code_start))
         block = CompressLMBlock(self.b, content_positions=list(range(block_start, code_start)),
                                 prompt_content_positions=list(range(block_start, resp_from)),
-                                response_content_positions=list(range(resp_from, code_start)),
-                                code_span=(code_start, code_start + K),
-                                retained_tail_positions=list(range(code_start - self.T, code_start)) if self.T else [])
+                                response_content_positions=response, code_span=(code_start, code_start + K),
+                                retained_tail_positions=[] if self.raw else tail)
         spans = self.proc.block_removal_spans(block)
         if self.sidecar is not None:
             # archive the code rows into packed pages before the span that removes them runs

@@ -409,14 +409,14 @@ def prefill_masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     transposed views HF attention receives, permuted back); prompt_len [B] int32 raw-prompt content tokens;
     head_quota [32] int32 code slots visible per query head; retain_tail = T of a retained tail (a block's last T
     content rows, hidden from its own codes) and ``tail_policy`` the later rows that see it: "static" every later row,
-    "sticky" the next block's content rows, "rolling" the next block's i-th content row from tail row i on;
+    "sticky" the next block's content rows, "rolling" the next block's i-th content row from tail row i on, "raw"
+    (CompressLM's raw_tail, T <= C) as rolling but not hidden from the codes;
     ``pause_xattn`` a code row's attention to its block's code rows ("full", "causal", "none"; the non-full ones
     evaluate the mask per element). Returns
     (out [B, S0, 32, 128] bf16, lse [B, 32, S0] fp32 natural log or None). fp32 q/k/v select the fp32 mode (out fp32).
     """
     B, S0 = q.shape[0], q.shape[1]
-    _require(0 <= int(retain_tail) < block_c, "retain_tail must be in [0, block_c)")
-    policy = tail_policy_code(tail_policy)
+    policy = _tail(block_c, retain_tail, tail_policy)
     xattn = xattn_code(pause_xattn)
     L, cr = _passes(pause_passes), _copy_rows(codes_k, pause_passes, copy_rows)
     R, rx = _replay(block_c, codes_k, retain_tail, replay_rows, replay_exclude)
@@ -462,8 +462,7 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
     """Gradients (dq [B, S0, 32, 128], dk, dv [B, S0, 8, 128], bf16) of sum(dout * out) for
     :func:`prefill_masked_attention` under the same mask, from its out and lse (bf16 path only)."""
     B, S0 = q.shape[0], q.shape[1]
-    _require(0 <= int(retain_tail) < block_c, "retain_tail must be in [0, block_c)")
-    policy = tail_policy_code(tail_policy)
+    policy = _tail(block_c, retain_tail, tail_policy)
     xattn = xattn_code(pause_xattn)
     L, cr = _passes(pause_passes), _copy_rows(codes_k, pause_passes, copy_rows)
     R, rx = _replay(block_c, codes_k, retain_tail, replay_rows, replay_exclude)
@@ -498,13 +497,25 @@ def prefill_masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch
     return dq, dk, dv
 
 
-TAIL_POLICIES = ("static", "rolling", "sticky")     # the kernels' policy codes 0, 1, 2
+TAIL_POLICIES = ("static", "rolling", "sticky", "raw")     # the kernels' policy codes 0, 1, 2, 3
 
 
 def tail_policy_code(tail_policy: str) -> int:
-    """Kernel code of a retain_tail_policy name."""
+    """Kernel code of a retain_tail_policy name ("raw": CompressLM's raw_tail, the rolling window that the codes also
+    see)."""
     _require(tail_policy in TAIL_POLICIES, f"tail_policy must be one of {TAIL_POLICIES}, got {tail_policy!r}")
     return TAIL_POLICIES.index(tail_policy)
+
+
+def _tail(block_c: int, retain_tail: int, tail_policy: str) -> int:
+    """Checks the tail size for its policy (a raw tail may span the whole block, compress_forward.py:270-271) and
+    returns the policy's kernel code."""
+    policy = tail_policy_code(tail_policy)
+    if tail_policy == "raw":
+        _require(0 <= int(retain_tail) <= block_c, "a raw tail must be in [0, block_c]")
+    else:
+        _require(0 <= int(retain_tail) < block_c, "retain_tail must be in [0, block_c)")
+    return policy
 
 
 XATTN = ("full", "causal", "none")                  # the kernels' pause_xattn codes 0, 1, 2

@@ -205,9 +205,9 @@ def prefill_masked_attn(q: Tensor, k: Tensor, v: Tensor, block_c: int, codes_k: 
                         pause_xattn: int = 0, pause_passes: int = 1, copy_rows: int = 0, replay_rows: int = 0,
                         replay_exclude: bool = False) -> None:
     """abkv_prefill_masked_attn: attention under the compression mask, q [B, S0, 32, 128], k / v [B, S0, 8, 128]
-    (retain_tail: T of a retained tail, 0 for none; tail_policy: 0 static, 1 rolling, 2 sticky; pause_xattn: 0 full,
-    1 causal, 2 none; pause_passes: L passes of codes_k code rows per block; copy_rows: a copy region after the
-    blocks; replay_rows / replay_exclude: the replay tail)."""
+    (retain_tail: T of a retained tail, 0 for none; tail_policy: 0 static, 1 rolling, 2 sticky, 3 raw; pause_xattn:
+    0 full, 1 causal, 2 none; pause_passes: L passes of codes_k code rows per block; copy_rows: a copy region after
+    the blocks; replay_rows / replay_exclude: the replay tail)."""
     _ops.prefill_masked_attention(q, k, v, block_c, codes_k, num_blocks, prompt_len=prompt_len,
                                   head_quota=head_quota, scale=scale, out=out, lse=lse, retain_tail=retain_tail,
                                   tail_policy=_ops.TAIL_POLICIES[tail_policy], pause_xattn=_ops.XATTN[pause_xattn],

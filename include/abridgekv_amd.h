@@ -138,12 +138,15 @@ int abkv_slot_mapping(const int32_t* req_idx, const int64_t* positions, int num_
  * block_c): a block's codes never see its own last T content rows (:714-715, :721-722), and tail_policy
  * (retain_tail_policy, _retained_tail_visible :99-124) names the later rows that see them: ABKV_TAIL_STATIC every
  * later row, ABKV_TAIL_STICKY every content row of the next block, ABKV_TAIL_ROLLING content row i of the next block
- * from tail row i on (key in-block offset >= block_c - T + i); lse [batch, 32, seq_len] fp32 natural log (NULL: not
- * written).
+ * from tail row i on (key in-block offset >= block_c - T + i); ABKV_TAIL_RAW is CompressLM's raw_tail = T
+ * (_raw_tail_visible, compress_forward.py:89-96; 0 <= T <= block_c): the rolling window, with the codes seeing their
+ * whole block (code_excluded_tail = 0, :309-311), on the per-element mask; lse [batch, 32, seq_len] fp32 natural log
+ * (NULL: not written).
  * ------------------------------------------------------------------------------------------------------------- */
 #define ABKV_TAIL_STATIC 0
 #define ABKV_TAIL_ROLLING 1
 #define ABKV_TAIL_STICKY 2
+#define ABKV_TAIL_RAW 3
 /* pause_xattn: a code row's attention to its own block's code rows (compress_forward.py:313-314, 622-625): all of
  * them (ABKV_XATTN_FULL, the served setting), those at or before its own row (ABKV_XATTN_CAUSAL), none
  * (ABKV_XATTN_NONE). The non-full settings run the per-element mask on every tile up to the query's block. */

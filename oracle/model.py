@@ -93,7 +93,8 @@ def _rotate_half(x):
 
 def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                  layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
-                 seeds=None, code_proj=None, copy_token=None, output_layers=False, replay=0, replay_exclude=False):
+                 seeds=None, code_proj=None, copy_token=None, output_layers=False, replay=0, replay_exclude=False,
+                 raw_tail=0):
     """Final-normed hidden states [B, S, d]. ``layer_head_quota``: [layers, Hq] code rows visible per query head
     (None: all K); ``prompt_len``: [B] raw-prompt content tokens (None: no raw prompt); ``retain_tail``: T of a
     retained tail under ``tail_policy``; ``pause_xattn``: code rows' attention to their own pass's codes;
@@ -102,7 +103,8 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
     ``copy_token`` [d]: append the copy region [copy_token | last block's content] (compress_forward.py:1185-1189),
     at positions after the layout's; ``output_layers``: also return every layer's output hidden states;
     ``replay``: R replay rows after each block's codes, fed the block's last R content tokens (compress_forward.py:
-    1180-1183), ``replay_exclude`` hiding those content rows from the codes."""
+    1180-1183), ``replay_exclude`` hiding those content rows from the codes; ``raw_tail``: W of a raw tail (the next
+    block's content rows see the block's last rows in a rolling window; the codes see their whole block)."""
     inner = model.model
     B = content_ids.shape[0]
     dt = next(model.parameters()).dtype
@@ -134,7 +136,7 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
         attn = layer.self_attn
         hq = None if layer_head_quota is None else np.asarray(layer_head_quota[li], dtype=np.int64)
         vis = op.arith_mask(C, K, N, pl, hq, retain_tail, tail_policy, pause_xattn, L, copy, R,
-                            replay_exclude)                                                   # [B?, H?, S, S]
+                            replay_exclude, raw_tail)                                                   # [B?, H?, S, S]
         vis = torch.from_numpy(np.ascontiguousarray(vis))
         if pl is None:
             vis = vis.unsqueeze(0)                              # [1, H?, S0, S0]
@@ -178,9 +180,10 @@ def dense_hidden(model, pause, content_ids, C, N, K, code_positions="appended", 
 
 def dense_loss_logits(model, pause, content_ids, C, N, K, code_positions="appended", prompt_len=None,
                       layer_head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full", passes=1,
-                      seeds=None, code_proj=None, replay=0, replay_exclude=False):
+                      seeds=None, code_proj=None, replay=0, replay_exclude=False, raw_tail=0):
     """Logits [B * N * (C-1), V] at the loss rows (block-major, within-block 0..C-2)."""
     h = dense_hidden(model, pause, content_ids, C, N, K, code_positions, prompt_len, layer_head_quota, retain_tail,
-                     tail_policy, pause_xattn, passes, seeds, code_proj, replay=replay, replay_exclude=replay_exclude)
+                     tail_policy, pause_xattn, passes, seeds, code_proj, replay=replay, replay_exclude=replay_exclude,
+                     raw_tail=raw_tail)
     rows = torch.from_numpy(loss_rows(C, N, K, passes, replay))
     return model.lm_head(h[:, rows, :].reshape(-1, h.shape[-1])).double()

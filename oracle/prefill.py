@@ -17,6 +17,10 @@ every row sees, and content row i of the next block sees the previous block's re
 window, _replay_tail_visible); with ``replay_exclude`` (code_exclude_replay_tail) a block's codes do not see its last
 R content rows. Replay and retained tails are mutually exclusive.
 
+``raw_tail`` = W (CompressLM(raw_tail=W), compress_forward.py:89-96, _raw_tail_visible): content query i of block b
+sees content row j of block b - 1 iff (b C + i) - ((b - 1) C + j) <= W; unlike a retained tail the codes still see
+their whole block (code_excluded_tail = retain_tail_kv = 0, :309-311). Exclusive with replay and retained tails.
+
 ``copy_rows`` rows after the N blocks form the copy region (copy_lambda, compress_forward.py:631-633): a copy row
 sees the last block's final-pass codes (slot < quota) and the copy rows up to itself; no other row sees it. K = 0
 (no codes) leaves causal attention within blocks of C rows (the plain forward).
@@ -59,21 +63,21 @@ XATTN = ("full", "causal", "none")
 
 
 def arith_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-               passes=1, copy_rows=0, replay=0, replay_exclude=False):
+               passes=1, copy_rows=0, replay=0, replay_exclude=False, raw_tail=0):
     """Boolean visibility [B?, H?, S, S] (leading dims only when prompt_len / head_quota are given),
     S = N * (C + passes * K + replay) + copy_rows."""
     S = N * (C + passes * K + replay) + copy_rows
     return arith_mask_block(C, K, N, np.arange(S), np.arange(S), prompt_len, head_quota, retain_tail, tail_policy,
-                            pause_xattn, passes, copy_rows, replay, replay_exclude)
+                            pause_xattn, passes, copy_rows, replay, replay_exclude, raw_tail)
 
 
 def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static",
-                     pause_xattn="full", passes=1, copy_rows=0, replay=0, replay_exclude=False):
+                     pause_xattn="full", passes=1, copy_rows=0, replay=0, replay_exclude=False, raw_tail=0):
     """The rows x cols sub-block of :func:`arith_mask` ([B?, H?, len(rows), len(cols)]) without building the whole
     S0 x S0 mask: the sampled-row / sampled-key checks at full sequence lengths use it."""
-    L, R = int(passes), int(replay)
-    if R and retain_tail:
-        raise ValueError("replay and retained tails are mutually exclusive")
+    L, R, W = int(passes), int(replay), int(raw_tail)
+    if sum(bool(x) for x in (R, retain_tail, W)) > 1:
+        raise ValueError("raw, replay and retained tails are mutually exclusive")
     LK = L * K
     per = C + LK + R
     q = np.asarray(rows, dtype=np.int64).reshape(-1, 1)
@@ -104,6 +108,8 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
             vis = vis | (nxt & (kw >= C - T))
         else:
             vis = vis | (nxt & (C + qw - kw <= T))                          # sliding window
+    if W:
+        vis = vis | ((qw < C) & k_content & (kb + 1 == qb) & (C + qw - kw <= W))   # raw tail, the codes' too
     if prompt_len is not None:
         pl = np.asarray(prompt_len, dtype=np.int64).reshape(-1, 1, 1)
         vis = vis[None] | (k_content & (kb * C + kw < pl))[...]
@@ -137,10 +143,11 @@ def arith_mask_block(C, K, N, rows, cols, prompt_len=None, head_quota=None, reta
 
 
 def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_policy="static", pause_xattn="full",
-              passes=1, copy_rows=0, replay=0, replay_exclude=False):
+              passes=1, copy_rows=0, replay=0, replay_exclude=False, raw_tail=0):
     """Same visibility from per-position role / block / content-position tables (the _dense_mask form, with its
-    replay terms); the copy region as _mask_mod's ``copy`` term (compress_forward.py:627-633)."""
-    L, R = int(passes), int(replay)
+    replay terms and _mask_mod's raw-tail term, compress_forward.py:601-603); the copy region as _mask_mod's ``copy``
+    term (compress_forward.py:627-633)."""
+    L, R, W = int(passes), int(replay), int(raw_tail)
     per = C + L * K + R
     S0 = N * per
     idx = np.arange(S0)
@@ -178,8 +185,9 @@ def role_mask(C, K, N, prompt_len=None, head_quota=None, retain_tail=0, tail_pol
     else:
         raise ValueError(f"unknown tail policy {tail_policy!r}")
     replay_tail = (qr == 0) & (kr == L + 1) & (kb + 1 == qb) & (qa - ka <= R) & (R > 0)
+    raw_tail_vis = (qr == 0) & (kr == 0) & (kb + 1 == qb) & (qa - ka <= W) & (W > 0)      # _raw_tail_visible
     base = (causal & (content_vis | earlier_final | refine | retained | replay_own_final | replay_causal
-                      | replay_tail)) | samepass
+                      | replay_tail | raw_tail_vis)) | samepass
     if prompt_len is not None:
         pl = np.asarray(prompt_len).reshape(-1, 1, 1)
         prompt_raw = (kr == 0)[None] & (content_abs.reshape(1, 1, S0) < pl) & (content_abs.reshape(1, 1, S0) >= 0)

@@ -59,8 +59,12 @@ def test_refusals():
         CompressLM(_model(), 8, 2, 4, L=2, code_positions="bitrev")
     with pytest.raises(ValueError, match="active_code_rows"):
         CompressLM(_model(), 8, 2, 4, seg_pool=True, active_code_rows=2)
-    with pytest.raises(NotImplementedError, match="raw_tail"):
-        CompressLM(_model(), 8, 2, 4, raw_tail=2)
+    with pytest.raises(ValueError, match="raw_tail must be in"):
+        CompressLM(_model(), 8, 2, 4, raw_tail=9)
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        CompressLM(_model(), 8, 2, 4, raw_tail=2, replay_tail=2)
+    with pytest.raises(ValueError, match="no tails"):
+        CompressLM(_model(), 8, 2, 4, raw_tail=2, code_positions="bitrev")
     with pytest.raises(ValueError, match="code_exclude_replay_tail"):
         CompressLM(_model(), 8, 2, 4, code_exclude_replay_tail=True)
     with pytest.raises(ValueError, match="positive"):
@@ -163,3 +167,16 @@ def test_replay_layout_matches_the_oracle(L, R):
         CompressLM(_model(), C, N, K, replay_tail=2, retain_tail_kv=2)
     with pytest.raises(ValueError, match="L=1 and no tails"):
         CompressLM(_model(), C, N, K, replay_tail=2, code_positions="bitrev")
+
+
+def test_raw_tail_is_the_kernels_raw_policy():
+    """CompressLM(raw_tail=W) hands the kernels the "raw" policy with T = W (W = C allowed) and hides nothing from
+    the codes: no excluded tail for the code seeds or the bitrev span."""
+    from abridgekv_amd.compress_forward import CompressLM
+    for W in (3, 8):
+        clm = CompressLM(_model(), 8, 2, 4, raw_tail=W)
+        m = clm.compress_mask(1)
+        assert (m.retain_tail, m.tail_policy, m.replay_rows) == (W, "raw", 0)
+        assert clm.raw_tail == W and clm.code_excluded_tail == 0
+    m = CompressLM(_model(), 8, 2, 4, retain_tail_kv=3, retain_tail_policy="sticky").compress_mask(1)
+    assert (m.retain_tail, m.tail_policy) == (3, "sticky")

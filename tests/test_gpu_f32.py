@@ -84,7 +84,9 @@ def test_paged_multi_query_f32_code_step_and_chunks(tail):
                                                            ([40, 0], "mixed", 12, "two-passes"),
                                                            (None, "mixed", 0, "copy-region"),
                                                            (None, None, 0, "no-codes"),
-                                                           ([40, 0], "mixed", 0, "replay")])
+                                                           ([40, 0], "mixed", 0, "replay"),
+                                                           ([40, 0], "mixed", 12, "raw"),
+                                                           ([40, 0], "mixed", 64, "raw")])
 def test_masked_prefill_f32_matches_fp64(prompt_len, quota, tail, policy):
     from abridgekv_amd import ops
     xattn = "causal" if policy == "causal-codes" else "full"
@@ -110,9 +112,11 @@ def test_masked_prefill_f32_matches_fp64(prompt_len, quota, tail, policy):
     torch.cuda.synchronize()
     got_o, got_l = out.cpu().numpy(), lse.cpu().numpy()
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=L, copy_rows=cr, replay=R,
-                             replay_exclude=R > 0)
+        raw = policy == "raw"                   # the kernels' raw policy is the oracle's separate raw-tail term
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota,
+                             retain_tail=0 if raw else tail, tail_policy="static" if raw else policy,
+                             pause_xattn=xattn, passes=L, copy_rows=cr, replay=R, replay_exclude=R > 0,
+                             raw_tail=tail if raw else 0)
         if prompt_len is not None:
             mask = mask[0]
         ro, rl = op.masked_attention_fp64(q[b].numpy(), k[b].numpy(), v[b].numpy(), mask, 128 ** -0.5)

@@ -105,8 +105,10 @@ def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="s
     pause = clm.pause.detach().cpu()
     seg_mean = (gen_options or {}).get("code_init_override") == "segment_mean"
     seeds, proj = _seeds(clm, base, ids, seg_mean), _code_options(clm)
+    # a raw tail: the model's, or the generator's override (then the generator alone is compared)
+    W = (gen_options or {}).get("raw_tail_override", clm.raw_tail)
     kw = dict(retain_tail=T, tail_policy=policy, pause_xattn=xattn, passes=L, replay=clm.replay_tail,
-              replay_exclude=clm.code_exclude_replay_tail)
+              replay_exclude=clm.code_exclude_replay_tail, raw_tail=W)
     ref = om.dense_loss_logits(copy.deepcopy(base).double(), pause.double(), ids, C, N, K, code_positions, prompt,
                                lhq, seeds=seeds, code_proj=proj, **kw)
     eager = om.dense_loss_logits(base, pause.to(torch.bfloat16), ids, C, N, K, code_positions, prompt, lhq,
@@ -138,10 +140,10 @@ def _gate(case, C, N, K, code_positions, prompt, quota, stepwise, T=0, policy="s
             g.compress()
             kept_prompt = min(p, (blk + 1) * C)
             # each closed block also keeps the part of its last T content rows that lies past the raw prompt (a
-            # window tail: the last closed block only)
-            first = 0 if policy == "static" else blk
-            tails = sum(min(T, (b + 1) * C - max(p, b * C)) for b in range(first, blk + 1) if (b + 1) * C > p) \
-                if T else 0
+            # window tail, the raw tail's too: the last closed block only)
+            first = 0 if policy == "static" and not W else blk
+            tails = sum(min(T or W, (b + 1) * C - max(p, b * C)) for b in range(first, blk + 1) if (b + 1) * C > p) \
+                if T or W else 0
             # the closed block's replay rows stay until the next block's content expires them
             tails += clm.replay_tail
             if per_head:
@@ -203,6 +205,12 @@ OPTION_CASES = [
      [[1, 16, 3, 5, 2, 7, 4, 16], [8, 8, 1, 1, 12, 3, 9, 2]], True, None),
     ("replay tail hidden from the codes, two passes", 64, 3, 16, "appended",
      dict(replay_tail=12, code_exclude_replay_tail=True, L=2, seg_pool=True), [70, 0], [16, 4], False, None),
+    ("raw tail", 64, 3, 16, "appended", dict(raw_tail=12, seg_pool=True), [40, 100], [16, 4], True, None),
+    ("raw tail of the whole block", 64, 3, 16, "appended", dict(raw_tail=64), [70, 0], [16, 8], True, None),
+    ("raw tail, two passes, causal codes", 64, 3, 16, "appended", dict(raw_tail=20, L=2, pause_xattn="causal"),
+     [40, 100], None, False, None),
+    ("raw-tail override of the generator", 64, 3, 16, "appended", {}, [40, 100], [16, 4], True,
+     {"raw_tail_override": 20}),
 ]
 
 
@@ -242,20 +250,23 @@ def test_forward_losses_match_dense_cross_entropy():
     assert blk["block_ce"].shape == (N,)
 
 
-@pytest.mark.parametrize("tail,policy", [(0, "static"), (12, "static"), (12, "rolling"), (12, "sticky")])
+@pytest.mark.parametrize("tail,policy", [(0, "static"), (12, "static"), (12, "rolling"), (12, "sticky"),
+                                         (12, "raw")])
 def test_training_gradients_match_dense_float64(tail, policy):
     """CompressLM trains through the kernels: the CE loss's gradients (attention and MLP weights, the pause rows)
     through the masked-prefill forward + backward kernels match the dense float64 model's autograd, within 2x the
     error of the same dense model run in bf16 autograd (plus 1e-3 of the gradient's scale); also with a retained
-    tail under each policy."""
+    tail under each policy and with a raw tail (appended code positions)."""
     from abridgekv_amd.compress_forward import CompressLM
 
     C, N, K = 64, 3, 32 if tail else 64
     quota = [[32] * 8, [32, 16, 24, 32, 8, 32, 32, 24]] if tail else [[32] * 8, [64, 16, 48, 64, 8, 32, 64, 24]]
     base = _model(11)
     dev = torch.device("cuda")
-    extra = dict(retain_tail_kv=tail, retain_tail_policy=policy) if tail else {}
-    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions="bitrev", head_code_quotas=quota,
+    raw = policy == "raw"
+    positions = "appended" if raw else "bitrev"
+    extra = dict(raw_tail=tail) if raw else dict(retain_tail_kv=tail, retain_tail_policy=policy) if tail else {}
+    clm = CompressLM(copy.deepcopy(base).to(dev), C, N, K, code_positions=positions, head_code_quotas=quota,
                      **extra).eval()
     torch.manual_seed(12)
     with torch.no_grad():
@@ -281,8 +292,9 @@ def test_training_gradients_match_dense_float64(tail, policy):
     def dense_grads(dtype):
         m = copy.deepcopy(base).to(dtype)
         pause = clm.pause.detach().cpu().to(dtype).requires_grad_()
-        logits = om.dense_loss_logits(m, pause, ids, C, N, K, "bitrev", [70, 5], lhq, retain_tail=tail,
-                                      tail_policy=policy)
+        logits = om.dense_loss_logits(m, pause, ids, C, N, K, positions, [70, 5], lhq,
+                                      retain_tail=0 if raw else tail, tail_policy="static" if raw else policy,
+                                      raw_tail=tail if raw else 0)
         ce = torch.nn.functional.cross_entropy(logits.double(), tgt, reduction="none")
         ((ce * tm).sum() / tm.sum()).backward()
         params = dict(m.named_parameters())

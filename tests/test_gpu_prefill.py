@@ -35,9 +35,11 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, rows=None, tail
     lse = lse.cpu().numpy()
     worst = 0.0
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows,
-                             replay=replay, replay_exclude=replay_exclude)
+        raw = policy == "raw"                   # the kernels' raw policy is the oracle's separate raw-tail term
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota,
+                             retain_tail=0 if raw else tail, tail_policy="static" if raw else policy,
+                             pause_xattn=xattn, passes=passes, copy_rows=copy_rows, replay=replay,
+                             replay_exclude=replay_exclude, raw_tail=tail if raw else 0)
         if prompt_len is not None:
             mask = mask[0]
         sel = slice(None) if rows is None else rows
@@ -171,6 +173,20 @@ def test_replay_rows(shape):
         quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
         _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=39, replay=3, replay_exclude=True,
                xattn="causal")
+
+
+@pytest.mark.parametrize("shape", ["aligned", "unaligned"])
+def test_raw_tail(shape):
+    """The raw tail (CompressLM(raw_tail=W)): the next block's content rows see the block's last W - i rows and the
+    block's codes see their whole block; W up to C, with quotas, a raw prompt, passes, a copy region and xattn."""
+    if shape == "aligned":
+        quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+        _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=42, tail=20, policy="raw")
+        _check(C=128, K=64, N=3, B=1, seed=43, tail=128, policy="raw", passes=2, copy_rows=129)
+    else:
+        quota = [4, 4, 4, 4, 1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3] * 2
+        _check(C=8, K=4, N=5, B=2, prompt_len=[5, 13], head_quota=quota, seed=44, tail=3, policy="raw")
+        _check(C=8, K=4, N=5, B=1, seed=45, tail=8, policy="raw", xattn="causal")
 
 
 @pytest.mark.parametrize("C,N", [(512, 1), (256, 3), (200, 2)])

@@ -35,9 +35,11 @@ def _check(C, K, N, B, prompt_len=None, head_quota=None, seed=0, tail=0, policy=
     got = [t.float().cpu().numpy() for t in (dq, dk, dv)]
     worst = 0.0
     for b in range(B):
-        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota, retain_tail=tail,
-                             tail_policy=policy, pause_xattn=xattn, passes=passes, copy_rows=copy_rows,
-                             replay=replay, replay_exclude=replay_exclude)
+        raw = policy == "raw"                   # the kernels' raw policy is the oracle's separate raw-tail term
+        mask = op.arith_mask(C, K, N, None if prompt_len is None else [prompt_len[b]], head_quota,
+                             retain_tail=0 if raw else tail, tail_policy="static" if raw else policy,
+                             pause_xattn=xattn, passes=passes, copy_rows=copy_rows, replay=replay,
+                             replay_exclude=replay_exclude, raw_tail=tail if raw else 0)
         if prompt_len is not None:
             mask = mask[0]
         ref = op.masked_attention_grads_fp64(q[b].float().numpy(), k[b].float().numpy(), v[b].float().numpy(), mask,
@@ -122,6 +124,14 @@ def test_copy_region():
 def test_replay_rows(exclude):
     quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
     _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=40, replay=16, replay_exclude=exclude)
+
+
+@pytest.mark.parametrize("W", [20, 128])
+def test_raw_tail(W):
+    """The raw tail (the rolling window that the codes also see), up to the whole block."""
+    quota = np.repeat([64, 16, 40, 64, 1, 33, 64, 8], 4).tolist()
+    print(f"case: raw W={W}", flush=True)
+    _check(C=128, K=64, N=3, B=2, prompt_len=[100, 0], head_quota=quota, seed=41, tail=W, policy="raw")
 
 
 @pytest.mark.parametrize("C,N", [(512, 1), (200, 2)])

@@ -13,7 +13,7 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
 def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="full", passes=1, copy_rows=0,
-          replay=0, replay_exclude=False):
+          replay=0, replay_exclude=False, raw=0):
     """Element-by-element rule: causal & (own-block content | earlier blocks' codes | raw-prompt content), or
     (code query & code key & same block); a code key with slot >= quota is hidden. Static retained tail (the config's
     prose, compresslm.py:22-25): "the final T content KVs of every completed block stay resident forever, visible to
@@ -33,7 +33,10 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
     R rows after a block's codes replay its last R content tokens; a replay row reads its block's content, final
     codes and replay rows up to itself; content row i of the next block reads the previous block's replay rows whose
     replayed position is within R of its own (replay row r with r >= i); with replay_exclude the codes do not read the
-    block's last R content rows."""
+    block's last R content rows.
+    Raw tail (_raw_tail_visible, compress_forward.py:90-93: "Whether content query q may see a raw token from the
+    immediately preceding block. The tail is a rolling window: at position j in a new block, only the final
+    raw_tail-j tokens from the previous block remain visible"); nothing hides it from the codes."""
     LK = passes * K
     per = C + LK + replay
     S0 = N * per
@@ -60,6 +63,8 @@ def brute(C, K, N, prompt_len=None, quota=None, tail=0, policy="static", xattn="
                 vis = True                       # the previous block's replay rows, a rolling window
             if prompt_len is not None and k_content and kb * C + kw < prompt_len:
                 vis = True
+            if raw and qw < C and k_content and kb == qb - 1 and kw >= C - (raw - qw):
+                vis = True                       # the previous block's final raw - j rows, j = the query's offset
             if tail and policy == "static" and k_content and kb < qb and kw >= C - tail:
                 vis = True                       # an earlier block's tail row: resident, seen by every later query
             if tail and policy != "static" and qw < C and k_content and kb == qb - 1:
@@ -448,3 +453,37 @@ def test_dense_reference_torch_matches_fp64_within_bf16():
     hidden_rows = ~mask[:, S - 1]
     assert torch.equal(got2[torch.from_numpy(hidden_rows)], torch.from_numpy(got)[torch.from_numpy(hidden_rows)].to(
         torch.bfloat16))
+
+
+@pytest.mark.parametrize("C,K,N,L,W", [(4, 2, 3, 1, 2), (6, 2, 3, 2, 3), (4, 3, 3, 1, 4), (3, 2, 4, 1, 1),
+                                       (8, 4, 3, 1, 5)])
+def test_raw_tail_arith_equals_role_equals_brute(C, K, N, L, W):
+    for xattn in ("full", "causal", "none"):
+        kw = dict(passes=L, raw_tail=W, pause_xattn=xattn)
+        a = op.arith_mask(C, K, N, **kw)
+        assert np.array_equal(a, op.role_mask(C, K, N, **kw))
+        assert np.array_equal(a, brute(C, K, N, xattn=xattn, passes=L, raw=W))
+        pl, hq = [0, C + 1], [1, K, 2, K]
+        ap = op.arith_mask(C, K, N, prompt_len=pl, head_quota=hq, copy_rows=C + 1, **kw)
+        assert np.array_equal(ap, op.role_mask(C, K, N, prompt_len=pl, head_quota=hq, copy_rows=C + 1, **kw))
+        for b, p in enumerate(pl):
+            for h, q in enumerate(hq):
+                assert np.array_equal(ap[b, h], brute(C, K, N, prompt_len=p, quota=q, xattn=xattn, passes=L,
+                                                      copy_rows=C + 1, raw=W))
+    per = C + L * K
+    m = op.arith_mask(C, K, N, passes=L, raw_tail=W)
+    assert m[C, C - 1] and m[C, 0]                              # a code row sees its whole block, tail included
+    assert m[per, C - W] and (W == 1 or not m[per, C - W - 1])  # content row 0 of block 1: block 0's last W rows
+    assert not m[per + W, C - 1] if W < C else True             # row W: the window has passed
+    assert not m[2 * per, C - 1]                                # two blocks later: gone
+    # the retained rolling tail is the same window with the codes kept off the block's tail
+    if W < C:
+        rolling = op.arith_mask(C, K, N, passes=L, retain_tail=W, tail_policy="rolling")
+        code = np.zeros(m.shape[0], bool)
+        code[[b * per + C + i for b in range(N) for i in range(L * K)]] = True
+        assert np.array_equal(rolling[~code], m[~code])
+        assert not np.array_equal(rolling[code], m[code])
+    with pytest.raises(ValueError):
+        op.arith_mask(C, K, N, raw_tail=W, retain_tail=1)
+    with pytest.raises(ValueError):
+        op.arith_mask(C, K, N, raw_tail=W, replay=1)
