@@ -104,9 +104,27 @@ struct Removal {
 
 struct GroupStep {
   std::vector<std::vector<Op>> batches;   // reference-format ordered op batches
-  std::vector<int32_t> blocks_before;     // page list before the step's first removal
+  // pages blocks_lo .. of the page list before the step's first removal: every row a step's moves read or write lies
+  // at or after its lowest removal start, and no removal or allocation changes a page below its own start's page, so
+  // the pages below the first removal's are copied in only when a later removal of the step starts lower
+  std::vector<int32_t> blocks_before;
+  int64_t blocks_lo = 0;
   std::vector<Removal> removals;
   bool stale = false;                     // a removal followed an allocation that followed a removal (no take)
+  // the state of a step with no removal; the vectors keep their capacity for the next step
+  void reset() {
+    batches.clear();
+    blocks_before.clear();
+    blocks_lo = 0;
+    removals.clear();
+    stale = false;
+  }
+};
+
+// One group's part of a span removal, validated before any group is changed.
+struct SpanPlan {
+  int g;
+  int64_t ps, pe, active;
 };
 
 struct Request {
@@ -132,6 +150,7 @@ struct Planner {
   bool op_rows = true;                    // build the reference-format op batches (off: fused moves only)
   // scratch of abkv_planner_mask_token_span, kept between calls
   std::vector<int> mts_targets;
+  std::vector<SpanPlan> mts_plans;
   std::vector<int32_t> mts_free;
   // scratch of abkv_planner_take_moves_packed, kept between steps
   std::vector<int64_t> mv_origin;
@@ -331,11 +350,8 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
     std::sort(targets.begin(), targets.end());
     targets.erase(std::unique(targets.begin(), targets.end()), targets.end());
   }
-  struct Plan {
-    int g;
-    int64_t ps, pe, active;
-  };
-  std::vector<Plan> plans;
+  std::vector<abkv::SpanPlan>& plans = p->mts_plans;
+  plans.clear();
   for (int g : targets) {
     if (g < 0 || g >= G) {
       p->last_error = "KV cache group " + std::to_string(g) + " out of range";
@@ -367,8 +383,17 @@ int abkv_planner_mask_token_span(void* h, int64_t rid, int64_t start, int64_t en
       return ABKV_ERR_SPAN;
     }
     if (!blocks.empty()) {
-      if (st.removals.empty()) st.blocks_before = blocks;
-      else if (r->alloc_after_removal) st.stale = true;
+      const int64_t lo_page = p->page_of(pl.ps);
+      if (st.removals.empty()) {
+        st.blocks_lo = lo_page;
+        st.blocks_before.assign(blocks.begin() + lo_page, blocks.end());
+      } else {
+        if (r->alloc_after_removal) st.stale = true;
+        if (lo_page < st.blocks_lo) {
+          st.blocks_before.insert(st.blocks_before.begin(), blocks.begin() + lo_page, blocks.begin() + st.blocks_lo);
+          st.blocks_lo = lo_page;
+        }
+      }
       st.removals.push_back({pl.ps, pl.pe, pl.active});
       const int64_t removed = pl.pe - pl.ps;
       std::vector<abkv::Op> ops;
@@ -516,9 +541,9 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
           int64_t* row = fused_rows + 6 * f;
           row[0] = rid;
           row[1] = g;
-          row[2] = st.blocks_before[p->page_of(src)];
+          row[2] = st.blocks_before[p->page_of(src) - st.blocks_lo];
           row[3] = p->off_of(src);
-          row[4] = st.blocks_before[p->page_of(dst)];
+          row[4] = st.blocks_before[p->page_of(dst) - st.blocks_lo];
           row[5] = p->off_of(dst);
         }
         ++f;
@@ -527,7 +552,7 @@ int abkv_planner_take_step_outputs(void* h, int64_t* op_rows, int64_t op_cap, in
   }
   if (n_fused) *n_fused = f;
   for (auto& kv : p->reqs) {
-    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    for (auto& st : kv.second.step) st.reset();
     kv.second.has_trunc = false;
     kv.second.alloc_after_removal = false;
   }
@@ -572,7 +597,8 @@ int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t tru
   struct RunInfo {
     int g;
     int64_t lo, n, at;                                    // at: the run's first row in the flat scratch
-    const int32_t* blocks;
+    const int32_t* blocks;                                // pages blocks_lo ..
+    int64_t blocks_lo;
     bool any;
   };
   std::vector<RunInfo> runs;
@@ -591,7 +617,7 @@ int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t tru
         removed += rm.end - rm.start;
       }
       runs.push_back({g, lo, std::max<int64_t>(st.removals.front().active - lo - removed, 0), total,
-                      st.blocks_before.data(), false});
+                      st.blocks_before.data(), st.blocks_lo, false});
       total += runs.back().n;
     }
   }
@@ -664,9 +690,9 @@ int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t tru
       const int64_t src = org[i], dst = run.lo + i;
       if (src == dst) continue;
       int32_t* d = ch[i] ? vo : vf;
-      d[0] = run.blocks[p->page_of(src)];
+      d[0] = run.blocks[p->page_of(src) - run.blocks_lo];
       d[1] = p->off_of(src);
-      d[2] = run.blocks[p->page_of(dst)];
+      d[2] = run.blocks[p->page_of(dst) - run.blocks_lo];
       d[3] = p->off_of(dst);
       if (ch[i]) vo += 4;
       else vf += 4;
@@ -676,7 +702,7 @@ int64_t abkv_planner_take_moves_packed(void* h, int64_t* trunc_rows, int64_t tru
     fre_c[(size_t)g] = vf;
   }
   for (auto& kv : p->reqs) {
-    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    for (auto& st : kv.second.step) st.reset();
     kv.second.has_trunc = false;
     kv.second.alloc_after_removal = false;
   }
@@ -812,8 +838,8 @@ int abkv_planner_take_move_runs(void* h, int64_t* trunc_rows, int64_t trunc_cap,
     int g;
     int64_t lo, n, n_ch, n_moved, t_star, a_end;
     RowMap map;
-    const std::vector<int32_t>* blocks;
-    int64_t win_lo, win_n;
+    const std::vector<int32_t>* blocks;                   // pages blocks_lo ..
+    int64_t blocks_lo, win_lo, win_n;
   };
   std::vector<RunInfo> infos;
   infos.reserve((size_t)need_runs);
@@ -846,9 +872,10 @@ int abkv_planner_take_move_runs(void* h, int64_t* trunc_rows, int64_t trunc_cap,
       const int64_t nAB = std::max<int64_t>(std::min(ri.a_end, ri.map.inv(ri.a_end)) - ri.t_star, 0);
       ri.n_ch = 2 * nA - nAB;
       ri.blocks = &st.blocks_before;
+      ri.blocks_lo = st.blocks_lo;
       ri.win_lo = p->page_of(lo);
       ri.win_n = p->page_of(std::max<int64_t>(st.removals.front().active - 1, lo)) - ri.win_lo + 1;
-      if (ri.win_lo + ri.win_n > (int64_t)st.blocks_before.size()) {
+      if (ri.win_lo < ri.blocks_lo || ri.win_lo + ri.win_n > ri.blocks_lo + (int64_t)st.blocks_before.size()) {
         p->last_error = "a run's rows lie past its page list";
         return ABKV_ERR_ARG;
       }
@@ -911,7 +938,7 @@ int abkv_planner_take_move_runs(void* h, int64_t* trunc_rows, int64_t trunc_cap,
       rec[14 + j] = j < ri.map.m ? (int32_t)ri.map.tau[j] : 0;
       rec[14 + kRunRemovalsMax + j] = j < ri.map.m ? (int32_t)ri.map.c[j] : 0;
     }
-    for (int64_t k = 0; k < ri.win_n; ++k) pages[np++] = (*ri.blocks)[(size_t)(ri.win_lo + k)];
+    for (int64_t k = 0; k < ri.win_n; ++k) pages[np++] = (*ri.blocks)[(size_t)(ri.win_lo - ri.blocks_lo + k)];
   }
   int64_t t = 0;
   if (trunc_rows) {
@@ -927,7 +954,7 @@ int abkv_planner_take_move_runs(void* h, int64_t* trunc_rows, int64_t trunc_cap,
   sizes[1] = np;
   sizes[2] = at;
   for (auto& kv : p->reqs) {
-    for (auto& st : kv.second.step) st = abkv::GroupStep();
+    for (auto& st : kv.second.step) st.reset();
     kv.second.has_trunc = false;
     kv.second.alloc_after_removal = false;
   }

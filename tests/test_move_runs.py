@@ -153,3 +153,52 @@ def test_step_move_lists_fall_back_to_host_lists(n_removals):
     got = expand(buf, layout, n_elems, 1) if kind == "runs" else buf
     assert np.array_equal(got, want) and n_elems == want.size
     assert pb.take_step_moves()[2] == []                   # the step was taken
+
+
+@pytest.mark.parametrize("order", ["descending", "scrambled"])
+def test_moves_when_a_later_removal_of_the_step_starts_lower(order):
+    """The planner keeps only the part of a step's page list at or after the step's lowest removal, and extends it
+    downward when a later removal starts below the earlier ones: the fused moves (gather-then-scatter) must leave every
+    kept row holding the row id of its logical position's slot before the step, and the same ids as the reference's
+    ordered op batches applied one after the other (oracle executor); the host-written lists and the expanded run
+    descriptors must agree. Removals in descending and scrambled order over two groups (some in one group only), with
+    pages freed by the truncations."""
+    from oracle import compaction as oc
+
+    spans = [(700, 730, None), (420, 450, [1]), (90, 100, None), (300, 305, [0]), (20, 40, None)]
+    if order == "scrambled":
+        spans = [spans[i] for i in (3, 0, 4, 1, 2)]
+    G, pages = 2, 400
+    planners = [KVPlanner(pages, G, PAGE, free_order=np.arange(1, pages, dtype=np.int32)) for _ in range(3)]
+    for p in planners:
+        p.add_request(7)
+        assert p.allocate_slots(7, 1000) is not None
+        p.set_num_computed_tokens(7, 1000)
+    before = planners[0].get_blocks(7)
+    for p in planners:
+        for s, e, groups in spans:
+            assert p.mask_token_span(7, s, e, groups).success
+    pa, pb, pc = planners
+    out = pa.take_step_outputs()
+    _, buf_b, parts_b = pb.take_step_moves()
+    _, desc, layout, parts_c, n_elems = pc.take_step_move_runs()
+    assert parts_b == parts_c and np.array_equal(expand(desc, layout, n_elems, G), buf_b)
+    fused = np.asarray(out.fused_moves, np.int64)
+    assert sum(n for _, _, n, _, _, _ in parts_b) == len(fused)
+    image = np.arange(pages * PAGE, dtype=np.int64).reshape(pages, PAGE)
+    for g in range(G):
+        rows = fused[fused[:, 1] == g]
+        mine = image.copy()
+        mine[rows[:, 4], rows[:, 5]] = image[rows[:, 2], rows[:, 3]]          # gather, then scatter
+        ref = np.stack([image, image], axis=1).copy()
+        oc.execute_kv_copy_operations({r: [b if i == g else [] for i, b in enumerate(v)]
+                                       for r, v in out.kv_copy_operations.items()},
+                                      [[ref] if i == g else [] for i in range(G)])
+        removed = {x for s, e, gs in spans if gs is None or g in gs for x in range(s, e)}
+        kept = np.array([x for x in range(1000) if x not in removed])
+        active = pa.num_computed_tokens(7) - pa.compacted_counts(7)[g]
+        assert len(kept) == active
+        slots = oc.slot_mapping(pa.get_blocks(7)[g], np.arange(active))
+        want = oc.slot_mapping(before[g], kept)                                 # each kept row's slot before the step
+        assert np.array_equal(mine[slots // PAGE, slots % PAGE], want), g
+        assert np.array_equal(ref[slots // PAGE, 0, slots % PAGE], want), g
