@@ -193,7 +193,13 @@ class ServingStress:
         self.st = plan.st
         self.dev = torch.device(device)
         self.split_pages = split_pages
-        self.code_target_blocks = code_target_blocks     # workgroups a code step's key splits aim at (None: the CUs)
+        # Workgroups a code step's key splits aim at. None: a quarter of the CUs when the code step runs beside the
+        # decode (2 key splits for one request: fewer, longer workgroups leave more of the GPU to the memory-bound
+        # decode; config 5 over 300 steps, two boxes, interleaved runs: 7369 -> 7429 and 7381 -> 7401 tokens/s
+        # against one workgroup per CU), all of them when it runs alone after the decode (serial order).
+        if code_target_blocks is None:
+            code_target_blocks = max(ops._num_cus() // 4, 1) if concurrent_code_step else ops._num_cus()
+        self.code_target_blocks = int(code_target_blocks)
         self.tag = tag
         B = self.B
         n_tensors = max(len(g) for g in self.st.groups)

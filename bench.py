@@ -74,7 +74,8 @@ def parse():
                     help="serving: run each layer's code step after its decode on one stream (for an A/B against "
                          "the default, the code step on a second stream)")
     ap.add_argument("--code-target-blocks", type=int, default=None,
-                    help="serving: workgroups a code step's key splits aim at (default: one per compute unit)")
+                    help="serving: workgroups a code step's key splits aim at (default: a quarter of the compute units "
+                         "with the code step on its own stream, every compute unit with --serial-code-step)")
     ap.add_argument("--retain-tail", type=int, default=0,
                     help="prefill / prefill_bwd: retained tail of T content rows per block (default 0)")
     ap.add_argument("--tail-policy", default="static", choices=("static", "rolling", "sticky"),
@@ -810,7 +811,7 @@ def bench_serving(args, torch):
                                f"and is compacted", "global_batch": B, "layers": s.L, "kv_groups": s.G,
                    "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)",
                    "code_step_stream": "main (serial)" if args.serial_code_step else "second stream (concurrent)",
-                   "code_target_blocks": args.code_target_blocks or "compute units"},
+                   "code_target_blocks": args.code_target_blocks or ("compute units" if args.serial_code_step else "compute units / 4")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": profiled_traffic("decode_attn_serving_b256_pmc_traffic.md"),
@@ -1055,7 +1056,7 @@ def main():
         "config": {"workload": wl, "global_batch": B, "layers": L, "kv_groups": G,
                    "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)",
                    "code_step_stream": "main (serial)" if args.serial_code_step else "second stream (concurrent)",
-                   "code_target_blocks": args.code_target_blocks or "compute units"},
+                   "code_target_blocks": args.code_target_blocks or ("compute units" if args.serial_code_step else "compute units / 4")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": (profiled_traffic(traffic_profile) if args.seed == 0 and

@@ -113,6 +113,9 @@ def test_concurrent_code_step_matches_serial(geometry):
         # every request 1..8 tokens short of a block boundary, so code steps run within the first steps
         T = 512 * rng.integers(4, 10, B) - rng.integers(1, 9, B)
         kw = dict(T=T, P=rng.integers(128, 1025, B), growth_tokens=steps + 64)
+    # the same key splits in both orders (their defaults differ: a quarter of the CUs beside the decode, all of them
+    # after it), so the outputs can be compared bit for bit
+    kw["code_target_blocks"] = 64
     a = _per_layer_stress(True, seed=5, **kw)
     b = _per_layer_stress(False, seed=5, **kw)
     code_steps = 0
