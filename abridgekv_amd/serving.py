@@ -193,6 +193,12 @@ class ServingStress:
         self.st = plan.st
         self.dev = torch.device(device)
         self.split_pages = split_pages
+        # Pages per decode split when split_pages is None: the plan's ops.auto_split_pages, capped at 40 while code
+        # steps run beside the decode. Config 5 over 300 steps, interleaved runs on two boxes, tokens/s: 40 pages
+        # 7466 / 7490 / 7440 / 7513 against 7415 / 7401 / 7414 / 7390 for the automatic choice (48 at B=256); 36
+        # pages 7282 / 7286, 44 pages 7002 / 7002, 56 pages 7305 / 7301. Alone on the GPU (the saturated decode
+        # steps) 48 pages stay faster: 7599 / 7612 against 7531 / 7488 at 40.
+        self.split_cap = 40 if concurrent_code_step else None
         # Workgroups a code step's key splits aim at. None: a quarter of the CUs when the code step runs beside the
         # decode (2 key splits for one request: fewer, longer workgroups leave more of the GPU to the memory-bound
         # decode; config 5 over 300 steps, two boxes, interleaved runs: 7369 -> 7429 and 7381 -> 7401 tokens/s
@@ -337,6 +343,13 @@ class ServingStress:
         return dict(m, view=v, n_tiles=n_tiles, n_upd=int(rows.size), moves=mv, code_split=code_split)
 
     # -- device: one step ---------------------------------------------------------------------------------------
+    def _split(self, m, g):
+        """Pages per decode split of group g in the step whose metadata is m."""
+        if self.split_pages:
+            return self.split_pages
+        sp = m["split"][g]
+        return sp if self.split_cap is None else min(sp, self.split_cap)
+
     def _layer_out(self, layer):
         """Output rows of a layer's attention (one buffer shared by every layer: the loop measures attention, and the
         next layer's queries come from the synthetic pool, not from this output)."""
@@ -385,7 +398,7 @@ class ServingStress:
                     e0.record()
                 check(L.abkv_decode_attn(_ptr(q), q.stride(0), q.stride(1), _ptr(cache), cache.shape[0],
                                          _ptr(dec_bt[g]), self.W, _ptr(v["dec_lens"][g]), nd, m["max_pages"][g],
-                                         self.split_pages or m["split"][g], C.c_float(self.scale), _ptr(out),
+                                         self._split(m, g), C.c_float(self.scale), _ptr(out),
                                          out.stride(0),
                                          out.stride(1), None, None if self.ws is None else _ptr(self.ws),
                                          C.c_size_t(self.ws_bytes), stream), "abkv_decode_attn")

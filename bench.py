@@ -809,7 +809,8 @@ def bench_serving(args, torch):
                                f"groups 256/128/64, 32q/8kv, d128, bf16, page 16), B={B}, T~U[2048,32768], "
                                f"P~U[128,1024]; a request closing a 512-token block runs its 256 code rows next step "
                                f"and is compacted", "global_batch": B, "layers": s.L, "kv_groups": s.G,
-                   "split_pages": args.split_pages or "auto", "seed": args.seed, "parallelism": "none (1 GPU)",
+                   "split_pages": args.split_pages or ("auto" if args.serial_code_step else "auto, at most 40"),
+                   "seed": args.seed, "parallelism": "none (1 GPU)",
                    "code_step_stream": "main (serial)" if args.serial_code_step else "second stream (concurrent)",
                    "code_target_blocks": args.code_target_blocks or ("compute units" if args.serial_code_step else "compute units / 4")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
