@@ -194,14 +194,14 @@ class ServingStress:
         self.dev = torch.device(device)
         self.split_pages = split_pages
         # Pages per decode split when split_pages is None: the plan's ops.auto_split_pages, capped at 40 while code
-        # steps run beside the decode. Config 5 over 300 steps, interleaved runs on two boxes, tokens/s: 40 pages
-        # 7466 / 7490 / 7440 / 7513 against 7415 / 7401 / 7414 / 7390 for the automatic choice (48 at B=256); 36
-        # pages 7282 / 7286, 44 pages 7002 / 7002, 56 pages 7305 / 7301. Alone on the GPU (the saturated decode
-        # steps) 48 pages stay faster: 7599 / 7612 against 7531 / 7488 at 40.
+        # steps run beside the decode. The B=256 stress (T ~ U[2048, 32768]) over 300 steps, interleaved runs on two
+        # boxes, tokens/s: 40 pages 7466 / 7490 / 7440 / 7513 against 7415 / 7401 / 7414 / 7390 for the automatic
+        # choice (48 at B=256); 36 pages 7282 / 7286, 44 pages 7002 / 7002, 56 pages 7305 / 7301. Alone on the GPU
+        # (the saturated decode steps) 48 pages stay faster: 7599 / 7612 against 7531 / 7488 at 40.
         self.split_cap = 40 if concurrent_code_step else None
         # Workgroups a code step's key splits aim at. None: a quarter of the CUs when the code step runs beside the
         # decode (2 key splits for one request: fewer, longer workgroups leave more of the GPU to the memory-bound
-        # decode; config 5 over 300 steps, two boxes, interleaved runs: 7369 -> 7429 and 7381 -> 7401 tokens/s
+        # decode; the B=256 stress over 300 steps, two boxes, interleaved runs: 7369 -> 7429 and 7381 -> 7401 tokens/s
         # against one workgroup per CU), all of them when it runs alone after the decode (serial order).
         if code_target_blocks is None:
             code_target_blocks = max(ops._num_cus() // 4, 1) if concurrent_code_step else ops._num_cus()
