@@ -177,7 +177,7 @@ MIN_PREFILL_WARMUP = 30
 
 
 def bench_prefill(args, torch):
-    """Config 4: teacher-forced prefill under the compression mask, B=4, N=16 blocks of [512 content | 128 codes]
+    """Teacher-forced prefill under the compression mask, B=4, N=16 blocks of [512 content | 128 codes]
     (S0 = 10240), 512-token raw prompt, 32 q / 8 kv heads, d128, bf16. FLOPs = 4 * D * visible pairs * heads * B."""
     from abridgekv_amd import ops
     from abridgekv_amd.workloads import visible_pairs_prompt_block
@@ -258,7 +258,7 @@ def prefill_cpu_baseline(torch, C, K, plen, flops_full, B_full, S0_full, N_cpu=4
 
 
 def bench_prefill_bwd(args, torch):
-    """Backward of config 4 (gradients of q, k, v through the compression mask; what training CompressLM runs per
+    """Backward of the B=4, S0=10240 masked prefill (gradients of q, k, v through the compression mask; what training CompressLM runs per
     layer after the forward). FLOPs = 10 * D * visible pairs * heads * B: the five products of the attention backward
     (S recomputed, dP, dV, dK, dQ) over the visible pairs, 2.5x the forward's; the kernels execute seven (the dQ and
     the dK/dV kernels each recompute S and dP)."""
@@ -311,7 +311,7 @@ def bench_prefill_bwd(args, torch):
 
 
 def bench_compaction(args, torch):
-    """Config 2: 64 sequences each close one 512-token block (256 code rows computed) in one step; Qwen3-4B shape,
+    """Compaction: 64 sequences each close one 512-token block (256 code rows computed) in one step; Qwen3-4B shape,
     36 layers in 6 quota groups, page 16, seeded fragmented free list. Timed: the planner step (the span removals with
     the reference's bookkeeping -- spans, page lists, truncations, free queue -- without the reference-format op
     rows the fused path does not execute), the move-list preparation (the planner writes per-run descriptors into
@@ -669,7 +669,7 @@ def code_step_cpu_baseline(torch, cache, q, tables, starts, limits, groups, K, s
 
 
 def bench_config1(args, torch):
-    """Config 1: single-layer abridged decode attention, B=1, quota K=128: 256 prompt rows at positions 0..255, 4 closed
+    """Single-layer abridged decode attention, B=1, quota K=128: 256 prompt rows at positions 0..255, 4 closed
     blocks of C=512 starting at 256 compressed to 128 code rows at in-block bitrev positions, an open block of 300 rows
     at 2304..2603 -> 1068 resident rows (812 without the prompt rows, the count the workload text gives; the reference
     never evicts prompt rows, so both are run). K/V/Q N(0,1) from the seed; the fused RoPE + append kernel rotates
@@ -744,7 +744,7 @@ def bench_config1(args, torch):
         "value": 1e6 / us, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic N(0,1) K/V/Q from the seed, RoPE theta 1e6 at the layout's positions",
-        "config": {"workload": "config 1: one layer, B=1, quota 128, prompt 256 + 4 closed blocks x 128 code rows + "
+        "config": {"workload": "single-layer decode: one layer, B=1, quota 128, prompt 256 + 4 closed blocks x 128 code rows + "
                                "open block 300 (1068 rows; the 812-row variant without prompt rows alongside)",
                    "global_batch": 1},
         "roofline": {"bound": "hbm (latency-bound at B=1: 4.4 MB per launch)", "achieved": main["gbps"],

@@ -334,7 +334,7 @@ def closed_form_pairs(C, K, N):
 
 @pytest.mark.parametrize("C,K,N", [(8, 4, 3), (16, 4, 5), (512, 128, 16)])
 def test_visible_pair_count(C, K, N):
-    """FLOP accounting of the masked prefill (config 4: N=16 blocks of [512 | 128], 512-token raw prompt)."""
+    """FLOP accounting of the masked prefill (B=4 workload: N=16 blocks of [512 | 128], 512-token raw prompt)."""
     assert op.visible_pairs(C, K, N, prompt_len=C) == closed_form_pairs(C, K, N)
 
 
