@@ -258,8 +258,8 @@ def prefill_cpu_baseline(torch, C, K, plen, flops_full, B_full, S0_full, N_cpu=4
 
 
 def bench_prefill_bwd(args, torch):
-    """Backward of the B=4, S0=10240 masked prefill (gradients of q, k, v through the compression mask; what training CompressLM runs per
-    layer after the forward). FLOPs = 10 * D * visible pairs * heads * B: the five products of the attention backward
+    """Backward of the B=4, S0=10240 masked prefill (gradients of q, k, v through the compression mask; what
+    training CompressLM runs per layer after the forward). FLOPs = 10 * D * visible pairs * heads * B: the five products of the attention backward
     (S recomputed, dP, dV, dK, dQ) over the visible pairs, 2.5x the forward's; the kernels execute seven (the dQ and
     the dK/dV kernels each recompute S and dP)."""
     from abridgekv_amd import ops
